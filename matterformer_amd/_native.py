@@ -1,0 +1,202 @@
+"""ctypes binding of libmf_hip.so (the C ABI declared in include/mf_capi.h).
+
+The library links ``libamdhip64.so.7``.  torch's ROCm build ships a HIP runtime
+with the same SONAME, so importing torch (which loads it) before ``dlopen`` of
+libmf_hip.so makes both share one runtime: torch's stream handles and device
+pointers are then valid inside the library.
+
+This module never falls back to another implementation: when the library is
+missing, every call raises ``RuntimeError`` naming what is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime the library must share)
+
+from matterformer_amd.build import LIB_PATH
+
+MF_OK = 0
+MF_ERR_INVALID_ARGUMENT = -1
+MF_ERR_UNSUPPORTED = -2
+MF_ERR_HIP = -3
+
+MF_DTYPE_F32 = 0
+MF_DTYPE_F16 = 1
+MF_DTYPE_BF16 = 2
+
+MF_PREC = {"bf16_tc": 0, "tf32": 1, "ieee_fp32": 2}
+
+# Every symbol include/mf_capi.h declares (tests check the library exports them).
+EXPORTED_SYMBOLS = (
+    "mf_abi_version",
+    "mf_last_error",
+    "mf_simplicial_fwd",
+    "mf_simplicial_fwd_supported",
+    "mf_knn",
+    "mf_radius_mask",
+    "mf_radius_attn",
+)
+
+EXPECTED_ABI_VERSION = 1
+
+_DTYPE_CODE = {
+    torch.float32: MF_DTYPE_F32,
+    torch.float16: MF_DTYPE_F16,
+    torch.bfloat16: MF_DTYPE_BF16,
+}
+
+
+class MfSimplicialFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k1", ctypes.c_void_p),
+        ("v1", ctypes.c_void_p),
+        ("k2", ctypes.c_void_p),
+        ("v2", ctypes.c_void_p),
+        ("query_valid", ctypes.c_void_p),
+        ("pair_key_valid", ctypes.c_void_p),
+        ("pair_valid", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("out_f32", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("tokens", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+    ]
+
+
+class MfKnnArgs(ctypes.Structure):
+    _fields_ = [
+        ("coords", ctypes.c_void_p),
+        ("pad_mask", ctypes.c_void_p),
+        ("idx", ctypes.c_void_p),
+        ("dist", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("atoms", ctypes.c_int32),
+        ("k", ctypes.c_int32),
+        ("exclude_self", ctypes.c_int32),
+    ]
+
+
+class MfRadiusMaskArgs(ctypes.Structure):
+    _fields_ = [
+        ("coords", ctypes.c_void_p),
+        ("gram", ctypes.c_void_p),
+        ("pad_mask", ctypes.c_void_p),
+        ("mask_bits", ctypes.c_void_p),
+        ("block_mask", ctypes.c_void_p),
+        ("cutoff", ctypes.c_float),
+        ("batch", ctypes.c_int32),
+        ("atoms", ctypes.c_int32),
+        ("block", ctypes.c_int32),
+        ("pbc_radius", ctypes.c_int32),
+    ]
+
+
+class MfRadiusAttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("mask_bits", ctypes.c_void_p),
+        ("block_mask", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("scale", ctypes.c_float),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("atoms", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("block", ctypes.c_int32),
+    ]
+
+
+_LIB: ctypes.CDLL | None = None
+_LOAD_ERROR: str | None = None
+
+
+def _load() -> ctypes.CDLL | None:
+    global _LIB, _LOAD_ERROR
+    if _LIB is not None or _LOAD_ERROR is not None:
+        return _LIB
+    path = Path(os.environ.get("MF_HIP_LIBRARY", LIB_PATH))
+    if not path.exists():
+        _LOAD_ERROR = f"{path} is not built (run `python -m matterformer_amd.build`)"
+        return None
+    try:
+        lib = ctypes.CDLL(str(path))
+    except OSError as exc:
+        _LOAD_ERROR = f"failed to load {path}: {exc}"
+        return None
+    lib.mf_abi_version.restype = ctypes.c_int
+    lib.mf_last_error.restype = ctypes.c_char_p
+    for name, argtype in (
+        ("mf_simplicial_fwd", MfSimplicialFwdArgs),
+        ("mf_knn", MfKnnArgs),
+        ("mf_radius_mask", MfRadiusMaskArgs),
+        ("mf_radius_attn", MfRadiusAttnArgs),
+    ):
+        fn = getattr(lib, name, None)
+        if fn is not None:
+            fn.argtypes = [ctypes.POINTER(argtype), ctypes.c_void_p]
+            fn.restype = ctypes.c_int
+    lib.mf_simplicial_fwd_supported.argtypes = [ctypes.c_int32] * 5
+    lib.mf_simplicial_fwd_supported.restype = ctypes.c_int
+    version = lib.mf_abi_version()
+    if version != EXPECTED_ABI_VERSION:
+        _LOAD_ERROR = f"{path} has ABI version {version}, expected {EXPECTED_ABI_VERSION}"
+        return None
+    _LIB = lib
+    return lib
+
+
+def library_path() -> Path:
+    return Path(os.environ.get("MF_HIP_LIBRARY", LIB_PATH))
+
+
+def load_error() -> str | None:
+    _load()
+    return _LOAD_ERROR
+
+
+def is_loaded() -> bool:
+    return _load() is not None
+
+
+def lib() -> ctypes.CDLL:
+    handle = _load()
+    if handle is None:
+        raise RuntimeError(f"matterformer_amd HIP library unavailable: {_LOAD_ERROR}")
+    return handle
+
+
+def last_error() -> str:
+    return lib().mf_last_error().decode("utf-8", errors="replace")
+
+
+def check(status: int, what: str) -> None:
+    if status != MF_OK:
+        raise RuntimeError(f"{what} failed (status {status}): {last_error()}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError as exc:
+        raise RuntimeError(f"unsupported dtype {dtype}; expected float16/bfloat16/float32") from exc
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def current_stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,594 @@
+// 2-simplicial attention forward for gfx950 (CDNA4).
+//
+// Math (simplicial_attention.py:161-180,304-344; triton_simplicial_attention.py:115-329):
+//   S_i[j,k] = sum_d q_i[d] k1_j[d] k2_k[d]
+//   P_i      = softmax over valid (j,k) of S_i
+//   out_i[d] = sum_{j,k} P_i[j,k] v1_j[d] v2_k[d]
+//
+// Design:
+//  * Ragged packing.  Keys (the j and k atoms) are compacted per molecule from
+//    pair_key_valid, and only valid queries are visited, so the work is
+//    n_q * n_k^2 per (molecule, head) instead of the padded N^3.
+//  * Persistent workgroups walk a balanced list of work items
+//    (molecule, head, query range).  The list is derived from the masks by
+//    every workgroup itself (a ballot-count over the masks), so there is no
+//    host synchronisation and a single launch.
+//  * Per item, the compacted K1, K2, V1 rows and V2^T are staged in LDS.
+//  * Per query i and tile of 16 j-rows, two MFMA chains:
+//      GEMM1  C1[k][j]   = sum_d K2[k][d] * (q_i (.) K1[j])[d]    -> S^T tile
+//      GEMM2  C2[d][j]  += sum_k V2^T[d][k] * P[j][k]             -> (P V2)^T
+//    The accumulator layout of GEMM1 (lane = j row, 4 consecutive keys per
+//    lane group) is exactly the B-operand layout GEMM2 needs, with the K index
+//    of GEMM2 permuted consistently on both operands, so P never leaves the
+//    registers.  Then out_i[d] += sum_j V1[j][d] * C2[d][j] in fp32.
+//  * Online softmax in the log2 domain (log2 e folded into q) with one running
+//    maximum per query, rescaled lazily: only when a tile exceeds the running
+//    maximum by more than kRescaleSlack, so exp2 arguments stay <= slack.
+#include <algorithm>
+#include <cmath>
+
+#include "mf_common.h"
+
+namespace mf {
+namespace simplicial {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 256 between rescales
+
+struct Params {
+  const void* q;
+  const void* k1;
+  const void* v1;
+  const void* k2;
+  const void* v2;
+  const uint8_t* qv;
+  const uint8_t* pkv;
+  const uint8_t* pv;
+  void* out;
+  float* out_f32;
+  float* lse;
+  int B, H, N, D;
+  int NP;           // LDS row capacity: N rounded up to 32
+  int work_target;  // target query * key^2 units per work item
+  int vec_ok;       // rows are 16-byte aligned and D*sizeof(T) % 16 == 0
+};
+
+// LDS geometry shared by host (sizing) and device (carving).
+template <typename T, int DP>
+struct Layout {
+  static constexpr int kPadK = 16 / Elem<T>::kSize;  // 16 bytes of row padding
+  static constexpr int KS = DP + kPadK;              // row stride of K1s/K2s/V1s
+  __host__ __device__ static int vs(int NP) { return NP + kPadK; }  // row stride of V2Ts
+  __host__ __device__ static size_t bytes(int NP, int B, bool has_pv) {
+    size_t s = 0;
+    s += size_t(3) * NP * KS * Elem<T>::kSize;  // K1s, K2s, V1s
+    s += size_t(DP) * vs(NP) * Elem<T>::kSize;  // V2Ts
+    s += size_t(NP) * 4 * 2;                    // kidx, qidx
+    if (has_pv) s += size_t(NP) * (NP / 32) * 4;  // pair-valid bit rows
+    s += size_t(B + 1) * 4 + size_t(B) * 4;     // item_off, nkq
+    return (s + 15) & ~size_t(15);
+  }
+};
+
+__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Queries per work item for a molecule with nk keys; a multiple of kWaves
+// once it reaches kWaves so every wave gets the same number of queries.
+__device__ __forceinline__ int queries_per_item(int nk, int work_target) {
+  const int nk2 = max(nk * nk, 1);
+  int qpi = max(1, work_target / nk2);
+  if (qpi >= kWaves) qpi -= qpi % kWaves;
+  return qpi;
+}
+
+// Copy `count` elements of a global row (elements [e0, e0+count) of a row of
+// length D) into `dst`, zero-filling past D.  count*sizeof(T) == 16.
+template <typename T>
+__device__ __forceinline__ void load_row_chunk16(T* dst, const T* row, int e0, int D, bool vec_ok) {
+  constexpr int C = 16 / sizeof(T);
+  if (vec_ok && e0 + C <= D) {
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(row + e0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < C; ++e) dst[e] = (e0 + e < D) ? row[e0 + e] : T(0.0f);
+  }
+}
+
+template <typename T, int DP>
+__global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
+  using E = Elem<T>;
+  using L = Layout<T, DP>;
+  constexpr int KS = L::KS;
+  constexpr int NMT = DP / 16;            // 16-wide d tiles of GEMM2 / outputs
+  constexpr int KPL = E::kKPerLane;       // K elements per lane per MFMA
+  constexpr int NCH = DP / E::kKPerMfma;  // MFMAs along d for GEMM1
+  constexpr int C16 = 16 / sizeof(T);     // elements per 16-byte chunk
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int NP = p.NP;
+  const int VS = L::vs(NP);
+  const int B = p.B, H = p.H, N = p.N, D = p.D;
+  const bool has_pv = p.pv != nullptr;
+  const int PW = NP / 32;  // pair-valid words per row
+
+  T* K1s = reinterpret_cast<T*>(smem);
+  T* K2s = K1s + NP * KS;
+  T* V1s = K2s + NP * KS;
+  T* V2Ts = V1s + NP * KS;
+  int* kidx = reinterpret_cast<int*>(V2Ts + DP * VS);
+  int* qidx = kidx + NP;
+  uint32_t* pvb = reinterpret_cast<uint32_t*>(qidx + NP);
+  int* item_off = reinterpret_cast<int*>(pvb + (has_pv ? NP * PW : 0));
+  int* nkq = item_off + (B + 1);
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+
+  // ---- 1. per-molecule key / query counts ----
+  for (int b = wave; b < B; b += kWaves) {
+    int ck = 0, cq = 0;
+    for (int base = 0; base < N; base += 64) {
+      const int t = base + lane;
+      const bool vk = t < N && p.pkv[size_t(b) * N + t] != 0;
+      const bool vq = t < N && p.qv[size_t(b) * N + t] != 0;
+      ck += __popcll(__ballot(vk));
+      cq += __popcll(__ballot(vq));
+    }
+    if (lane == 0) nkq[b] = (ck << 16) | cq;
+  }
+  __syncthreads();
+
+  // ---- 2. work-item offsets (exclusive scan over molecules) ----
+  if (wave == 0) {
+    int running = 0;
+    for (int base = 0; base < B; base += 64) {
+      const int b = base + lane;
+      int cnt = 0;
+      if (b < B) {
+        const int v = nkq[b];
+        const int nk = v >> 16, nq = v & 0xffff;
+        if (nq > 0) cnt = H * ceil_div(nq, queries_per_item(nk, p.work_target));
+      }
+      int x = cnt;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+      }
+      if (b < B) item_off[b] = running + x - cnt;
+      running += __shfl(x, 63, 64);
+    }
+    if (lane == 0) item_off[B] = running;
+  }
+
+  // ---- 3. zero rows of invalid queries (grid-stride) ----
+  {
+    const int CPR = ceil_div(D, 4);  // 4-element chunks per row
+    const long long rows = (long long)B * H * N;
+    const long long total = rows * CPR;
+    for (long long idx = (long long)blockIdx.x * kThreads + tid; idx < total;
+         idx += (long long)gridDim.x * kThreads) {
+      const long long row = idx / CPR;
+      const int ch = int(idx - row * CPR);
+      const int i = int(row % N);
+      const int b = int(row / ((long long)H * N));
+      if (p.qv[size_t(b) * N + i] != 0) continue;
+      const int d0 = ch * 4;
+      for (int e = 0; e < 4 && d0 + e < D; ++e) {
+        const size_t o = size_t(row) * D + d0 + e;
+        if (p.out) static_cast<T*>(p.out)[o] = T(0.0f);
+        if (p.out_f32) p.out_f32[o] = 0.0f;
+      }
+      if (ch == 0 && p.lse) p.lse[row] = 0.0f;
+    }
+  }
+  __syncthreads();
+
+  const int total_items = item_off[B];
+
+  // ---- 4. work items ----
+  for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (item_off[mid] <= item) lo = mid; else hi = mid - 1;
+    }
+    const int b = lo;
+    const int nk = nkq[b] >> 16;
+    const int nq = nkq[b] & 0xffff;
+    const int qpi = queries_per_item(nk, p.work_target);
+    const int splits = ceil_div(nq, qpi);
+    const int local = item - item_off[b];
+    const int h = local / splits;
+    const int s = local - h * splits;
+    const int q0 = s * qpi;
+    const int q1 = min(nq, q0 + qpi);
+    const int bh = b * H + h;
+
+    // compacted key list (wave 0) and query list (wave 1)
+    if (wave < 2) {
+      const uint8_t* m = (wave == 0 ? p.pkv : p.qv) + size_t(b) * N;
+      int* dst = wave == 0 ? kidx : qidx;
+      int count = 0;
+      for (int base = 0; base < N; base += 64) {
+        const int t = base + lane;
+        const bool v = t < N && m[t] != 0;
+        const unsigned long long bal = __ballot(v);
+        const int pos = count + __popcll(bal & ((1ull << lane) - 1ull));
+        if (v) dst[pos] = t;
+        count += __popcll(bal);
+      }
+    }
+    __syncthreads();
+
+    // stage K1, K2, V1 rows (row-major) and V2^T; zero-fill rows >= nk
+    const int nrow = min(NP, ceil_div(nk, 32) * 32);
+    {
+      const T* gk1 = static_cast<const T*>(p.k1) + size_t(bh) * N * D;
+      const T* gk2 = static_cast<const T*>(p.k2) + size_t(bh) * N * D;
+      const T* gv1 = static_cast<const T*>(p.v1) + size_t(bh) * N * D;
+      const T* gv2 = static_cast<const T*>(p.v2) + size_t(bh) * N * D;
+      constexpr int CPR = DP / C16;  // 16-byte chunks per padded row
+      const int units = nrow * CPR;
+      for (int u = tid; u < units; u += kThreads) {
+        const int r = u / CPR;
+        const int c = u - r * CPR;
+        const int e0 = c * C16;
+        T* d1 = K1s + r * KS + e0;
+        T* d2 = K2s + r * KS + e0;
+        T* d3 = V1s + r * KS + e0;
+        T tmp[C16];
+        if (r < nk) {
+          const size_t src = size_t(kidx[r]) * D;
+          load_row_chunk16<T>(d1, gk1 + src, e0, D, p.vec_ok);
+          load_row_chunk16<T>(d2, gk2 + src, e0, D, p.vec_ok);
+          load_row_chunk16<T>(d3, gv1 + src, e0, D, p.vec_ok);
+          load_row_chunk16<T>(tmp, gv2 + src, e0, D, p.vec_ok);
+        } else {
+#pragma unroll
+          for (int e = 0; e < C16; ++e) { d1[e] = T(0.0f); d2[e] = T(0.0f); d3[e] = T(0.0f); tmp[e] = T(0.0f); }
+        }
+#pragma unroll
+        for (int e = 0; e < C16; ++e) V2Ts[(e0 + e) * VS + r] = tmp[e];
+      }
+      if (has_pv) {
+        const uint8_t* gpv = p.pv + size_t(b) * N * N;
+        const int wpr = nrow / 32;
+        for (int u = tid; u < nrow * wpr; u += kThreads) {
+          const int j = u / wpr;
+          const int w = u - j * wpr;
+          uint32_t bits = 0;
+          if (j < nk) {
+            const uint8_t* prow = gpv + size_t(kidx[j]) * N;
+            for (int t = 0; t < 32; ++t) {
+              const int kk = w * 32 + t;
+              if (kk < nk && prow[kidx[kk]] != 0) bits |= 1u << t;
+            }
+          }
+          pvb[j * PW + w] = bits;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- per-query streaming: one wave owns one query at a time ----
+    for (int qs = q0 + wave; qs < q1; qs += kWaves) {
+      const int i = qidx[qs];
+      const size_t row_off = (size_t(bh) * N + i);
+
+      // q row in fp32, scaled by log2(e), in the GEMM1 B-operand layout:
+      // chunk c, element e  <->  d = c*kKPerMfma + g*KPL + e
+      float qf[NCH][KPL];
+      {
+        const T* gq = static_cast<const T*>(p.q) + row_off * D;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) {
+            const int d = c * E::kKPerMfma + g * KPL + e;
+            qf[c][e] = d < D ? E::to_f32(gq[d]) * kLog2e : 0.0f;
+          }
+      }
+
+      float M = -INFINITY;  // running max (log2 domain), wave-uniform
+      float lsum = 0.0f;    // per-lane partial of sum P
+      float acc[NMT][4];
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mt][r] = 0.0f;
+
+      const int njt = ceil_div(nk, 16);
+      const int nkc = ceil_div(nk, 64);
+      for (int jt = 0; jt < njt; ++jt) {
+        const int j = jt * 16 + r16;
+        const bool row_ok = j < nk;
+
+        // GEMM1 B operand: (q_i (.) k1_j) rounded to the operand type
+        typename E::Operand b1[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const T* src = K1s + j * KS + c * E::kKPerMfma + g * KPL;
+          if constexpr (KPL == 8) {
+            typename E::Operand kv = *reinterpret_cast<const typename E::Operand*>(src);
+            typename E::Operand ov;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ov[e] = E::from_f32(qf[c][e] * E::to_f32(kv[e]));
+            b1[c] = ov;
+          } else {
+            b1[c] = qf[c][0] * src[0];
+          }
+        }
+
+        mf_f32x4 tacc[NMT];
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) tacc[mt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+        for (int kc = 0; kc < nkc; ++kc) {
+          const int kbase = kc * 64;
+          const int nkt = min(4, ceil_div(nk - kbase, 16));
+
+          // GEMM1: S^T tiles, lane holds row j and keys kbase+kt*16+4g+r
+          mf_f32x4 sv[4];
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+            sv[kt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+            if (kt < nkt) {
+              const T* arow = K2s + (kbase + kt * 16 + r16) * KS + g * KPL;
+#pragma unroll
+              for (int c = 0; c < NCH; ++c) {
+                typename E::Operand a1;
+                if constexpr (KPL == 8) a1 = *reinterpret_cast<const typename E::Operand*>(arow + c * E::kKPerMfma);
+                else a1 = arow[c * E::kKPerMfma];
+                sv[kt] = E::mma(a1, b1[c], sv[kt]);
+              }
+            }
+          }
+
+          // mask + lane max
+          const bool edge = has_pv || (jt * 16 + 16 > nk) || (kbase + nkt * 16 > nk);
+          float mloc = -INFINITY;
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float sval = sv[kt][r];
+              if (kt >= nkt) {
+                sval = -INFINITY;
+              } else if (edge) {
+                const int key = kbase + kt * 16 + 4 * g + r;
+                bool ok = row_ok && key < nk;
+                if (has_pv && ok) ok = (pvb[j * PW + (key >> 5)] >> (key & 31)) & 1u;
+                sval = ok ? sval : -INFINITY;
+              }
+              sv[kt][r] = sval;
+              mloc = fmaxf(mloc, sval);
+            }
+          }
+
+          // lazy rescale of the running maximum
+          if (__any(mloc > M + kRescaleSlack)) {
+            const float mw = wave_max(mloc);
+            const float Mn = fmaxf(M, mw);
+            const float alpha = (M == -INFINITY) ? 0.0f : fast_exp2(M - Mn);
+            lsum *= alpha;
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                acc[mt][r] *= alpha;
+                tacc[mt][r] *= alpha;
+              }
+            }
+            M = Mn;
+          }
+          if (M == -INFINITY) continue;  // nothing valid seen yet
+
+          // P = exp2(S - M)
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float pe = fast_exp2(sv[kt][r] - M);
+              sv[kt][r] = pe;
+              lsum += pe;
+            }
+
+          // GEMM2: C2[d][j] += sum_k V2^T[d][k] P[j][k]
+          if constexpr (KPL == 8) {
+            using V4 = __attribute__((__vector_size__(4 * sizeof(T)))) T;
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+              if (2 * pr < nkt) {
+                typename E::Operand b2;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  b2[r] = E::from_f32(sv[2 * pr][r]);
+                  b2[4 + r] = E::from_f32(2 * pr + 1 < nkt ? sv[2 * pr + 1][r] : 0.0f);
+                }
+                const int kcol = kbase + 32 * pr + 4 * g;
+#pragma unroll
+                for (int mt = 0; mt < NMT; ++mt) {
+                  const T* vrow = V2Ts + (mt * 16 + r16) * VS + kcol;
+                  const V4 lo = *reinterpret_cast<const V4*>(vrow);
+                  const V4 hi = *reinterpret_cast<const V4*>(vrow + 16);
+                  const typename E::Operand a2 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                  tacc[mt] = E::mma(a2, b2, tacc[mt]);
+                }
+              }
+            }
+          } else {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+              if (kt < nkt) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const int kcol = kbase + kt * 16 + 4 * g + r;
+#pragma unroll
+                  for (int mt = 0; mt < NMT; ++mt) {
+                    const float a2 = V2Ts[(mt * 16 + r16) * VS + kcol];
+                    tacc[mt] = E::mma(a2, sv[kt][r], tacc[mt]);
+                  }
+                }
+              }
+            }
+          }
+        }
+
+        // out_i[d] += sum_j V1[j][d] * C2[d][j]; lane holds j = row, d = mt*16+4g+r
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) {
+          const T* vrow = V1s + j * KS + mt * 16 + 4 * g;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mt][r] += E::to_f32(vrow[r]) * tacc[mt][r];
+        }
+      }
+
+      // ---- reduce and write the query row ----
+      const float lsum_all = wave_sum(lsum);
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mt][r] = group16_sum(acc[mt][r]);
+      const bool has_mass = lsum_all > 0.0f;
+      const float inv = has_mass ? 1.0f / lsum_all : 0.0f;
+      // lane (g, r16) writes d = mt*16 + 4g + (r16&3) for mt with (mt&3) == r16>>2
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) {
+        if ((mt & 3) != (r16 >> 2)) continue;
+        float val = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((r16 & 3) == r) val = acc[mt][r];
+        const int d = mt * 16 + 4 * g + (r16 & 3);
+        if (d < D) {
+          const float o = val * inv;
+          if (p.out) static_cast<T*>(p.out)[row_off * D + d] = E::from_f32(o);
+          if (p.out_f32) p.out_f32[row_off * D + d] = o;
+        }
+      }
+      if (lane == 0 && p.lse)
+        p.lse[row_off] = has_mass ? (M + __log2f(lsum_all)) * kLn2 : 0.0f;
+    }
+    __syncthreads();
+  }
+}
+
+template <typename T, int DP>
+int launch(const Params& prm, size_t lds, int grid, hipStream_t stream) {
+  auto kern = simplicial_fwd_kernel<T, DP>;
+  static bool attr_set = false;  // per instantiation
+  if (!attr_set) {
+    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, prm);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
+
+template <typename T>
+size_t lds_bytes(int DP, int NP, int B, bool has_pv) {
+  switch (DP) {
+    case 32: return Layout<T, 32>::bytes(NP, B, has_pv);
+    case 64: return Layout<T, 64>::bytes(NP, B, has_pv);
+    default: return Layout<T, 128>::bytes(NP, B, has_pv);
+  }
+}
+
+static size_t lds_for(int dtype, int DP, int NP, int B, bool has_pv) {
+  if (dtype == MF_DTYPE_F32) return lds_bytes<float>(DP, NP, B, has_pv);
+  if (dtype == MF_DTYPE_F16) return lds_bytes<_Float16>(DP, NP, B, has_pv);
+  return lds_bytes<__bf16>(DP, NP, B, has_pv);
+}
+
+static int padded_head_dim(int D) { return D <= 32 ? 32 : (D <= 64 ? 64 : 128); }
+
+static int check_shape(int B, int H, int N, int D, int dtype, bool has_pv, size_t* lds_out) {
+  if (B <= 0 || H <= 0 || N <= 0 || D <= 0)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: batch, heads, tokens and head_dim must be positive");
+  if (D > 128)
+    return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports head_dim <= 128, got " + std::to_string(D));
+  if (N > 32767)
+    return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports tokens <= 32767");
+  if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_F16 && dtype != MF_DTYPE_BF16)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: unknown dtype " + std::to_string(dtype));
+  DeviceInfo dev;
+  int st = device_info(&dev);
+  if (st != MF_OK) return st;
+  const int NP = (N + 31) / 32 * 32;
+  const size_t lds = lds_for(dtype, padded_head_dim(D), NP, B, has_pv);
+  if (lds > size_t(dev.max_lds_per_block))
+    return fail(MF_ERR_UNSUPPORTED,
+                "mf_simplicial_fwd: tokens=" + std::to_string(N) + ", head_dim=" + std::to_string(D) +
+                    ", batch=" + std::to_string(B) + " needs " + std::to_string(lds) +
+                    " bytes of LDS per workgroup, the device offers " + std::to_string(dev.max_lds_per_block));
+  if (lds_out) *lds_out = lds;
+  return MF_OK;
+}
+
+}  // namespace simplicial
+}  // namespace mf
+
+using namespace mf;
+using namespace mf::simplicial;
+
+extern "C" int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                                           int32_t dtype) {
+  return check_shape(batch, heads, tokens, head_dim, dtype, /*has_pv=*/true, nullptr);
+}
+
+extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) {
+  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: args is NULL");
+  if (!a->q || !a->k1 || !a->v1 || !a->k2 || !a->v2)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: q, k1, v1, k2 and v2 must be non-NULL");
+  if (!a->query_valid || !a->pair_key_valid)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: query_valid and pair_key_valid must be non-NULL");
+  if (!a->out && !a->out_f32 && !a->lse)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: at least one of out, out_f32, lse must be non-NULL");
+  if (a->precision < MF_PREC_BF16_TC || a->precision > MF_PREC_IEEE_FP32)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: unknown precision " + std::to_string(a->precision));
+  const bool has_pv = a->pair_valid != nullptr;
+  size_t lds = 0;
+  int st = check_shape(a->batch, a->heads, a->tokens, a->head_dim, a->dtype, has_pv, &lds);
+  if (st != MF_OK) return st;
+  DeviceInfo dev;
+  st = device_info(&dev);
+  if (st != MF_OK) return st;
+
+  Params prm{};
+  prm.q = a->q; prm.k1 = a->k1; prm.v1 = a->v1; prm.k2 = a->k2; prm.v2 = a->v2;
+  prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
+  prm.out = a->out; prm.out_f32 = a->out_f32; prm.lse = a->lse;
+  prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
+  prm.NP = (a->tokens + 31) / 32 * 32;
+  prm.work_target = 16 * 48 * 48;
+  const size_t esize = a->dtype == MF_DTYPE_F32 ? 4 : 2;
+  bool vec = (size_t(a->head_dim) * esize) % 16 == 0;
+  for (const void* ptr : {a->q, a->k1, a->v1, a->k2, a->v2})
+    vec = vec && (reinterpret_cast<uintptr_t>(ptr) % 16 == 0);
+  prm.vec_ok = vec ? 1 : 0;
+
+  const int per_cu = std::max(1, int((160 * 1024) / std::max<size_t>(lds, 1)));
+  const int grid = dev.num_cus * std::min(per_cu, 2);
+  const int DP = padded_head_dim(a->head_dim);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->dtype == MF_DTYPE_BF16) {
+    if (DP == 32) return launch<__bf16, 32>(prm, lds, grid, s);
+    if (DP == 64) return launch<__bf16, 64>(prm, lds, grid, s);
+    return launch<__bf16, 128>(prm, lds, grid, s);
+  }
+  if (a->dtype == MF_DTYPE_F16) {
+    if (DP == 32) return launch<_Float16, 32>(prm, lds, grid, s);
+    if (DP == 64) return launch<_Float16, 64>(prm, lds, grid, s);
+    return launch<_Float16, 128>(prm, lds, grid, s);
+  }
+  if (DP == 32) return launch<float, 32>(prm, lds, grid, s);
+  if (DP == 64) return launch<float, 64>(prm, lds, grid, s);
+  return launch<float, 128>(prm, lds, grid, s);
+}

@@ -1,0 +1,257 @@
+"""HIP backend of 2-simplicial attention: host side of ``mf_simplicial_fwd``.
+
+Drop-in for ``matterformer.models.triton_simplicial_attention``
+(src/matterformer/models/triton_simplicial_attention.py).  Same names, argument
+meaning and return contract:
+
+  TRITON_AVAILABLE                  :12   -> the HIP library is loadable
+  SUPPORTED_SIMPLICIAL_PRECISIONS   :13
+  normalize_simplicial_precision    :19-25
+  triton_block_d_for_head_dim       :28-39
+  triton_simplicial_attention_forward   :790-926 -> hip_simplicial_attention_forward
+  triton_simplicial_attention_backward  :929-1204 -> hip_simplicial_attention_backward
+
+The forward is one launch of the hand-written gfx950 kernel through the C ABI
+(include/mf_capi.h).  There is no fallback inside this module: a missing
+library, a CPU tensor or an unsupported shape raises RuntimeError.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from matterformer_amd import _native
+from matterformer_amd.simplicial_types import (
+    SimplicialAttentionMask,
+    SimplicialFactorizedBias,
+    SimplicialLowRankAngleResidual,
+    SimplicialLowRankMessageResidual,
+    simplicial_attention_torch_from_projected,
+)
+
+HIP_AVAILABLE = _native.is_loaded()
+# The reference's flag name; True means the fused (here: HIP) backend is usable.
+TRITON_AVAILABLE = HIP_AVAILABLE
+SUPPORTED_SIMPLICIAL_PRECISIONS = ("bf16_tc", "tf32", "ieee_fp32")
+
+
+def normalize_simplicial_precision(precision: str) -> str:
+    normalized = str(precision).lower()
+    if normalized not in SUPPORTED_SIMPLICIAL_PRECISIONS:
+        raise ValueError(
+            f"Unsupported simplicial_precision: {precision}. Expected one of {SUPPORTED_SIMPLICIAL_PRECISIONS}."
+        )
+    return normalized
+
+
+def triton_block_d_for_head_dim(head_dim: int) -> int:
+    """Padded head dim used by the reference kernel (kept for API compatibility)."""
+    if head_dim <= 0:
+        raise ValueError("head_dim must be positive")
+    for block in (16, 32, 64, 128):
+        if head_dim <= block:
+            return block
+    raise ValueError(f"Triton simplicial attention only supports head_dim <= 128, got {head_dim}")
+
+
+def hip_block_d_for_head_dim(head_dim: int) -> int:
+    """Padded head dim of the HIP kernel's MFMA tiles (32, 64 or 128)."""
+    return max(32, triton_block_d_for_head_dim(head_dim))
+
+
+def hip_unsupported_reason(batch: int, heads: int, tokens: int, head_dim: int, dtype: torch.dtype) -> str | None:
+    """None if mf_simplicial_fwd serves this shape, else the library's reason."""
+    if not HIP_AVAILABLE:
+        return f"the HIP library is unavailable: {_native.load_error()}"
+    if dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return f"the HIP backend only supports float16/bfloat16/float32 inputs, got {dtype}"
+    lib = _native.lib()
+    status = lib.mf_simplicial_fwd_supported(batch, heads, tokens, head_dim, _native.dtype_code(dtype))
+    if status != _native.MF_OK:
+        return _native.last_error()
+    return None
+
+
+def _compute_dtype(dtype: torch.dtype, precision: str) -> torch.dtype:
+    # bf16_tc keeps 16-bit operands on 16-bit MFMA; tf32/ieee_fp32 upcast 16-bit
+    # operands to fp32 (the reference's USE_FP32_INPUT, triton...py:62-68).
+    # fp32 operands always run the fp32 MFMA path.
+    if precision == "bf16_tc" and dtype in (torch.bfloat16, torch.float16):
+        return dtype
+    return torch.float32
+
+
+def hip_simplicial_attention_forward(
+    q: torch.Tensor,
+    k1: torch.Tensor,
+    v1: torch.Tensor,
+    k2: torch.Tensor,
+    v2: torch.Tensor,
+    *,
+    query_valid: torch.Tensor,
+    pair_key_valid: torch.Tensor,
+    pair_valid: torch.Tensor | None,
+    u: torch.Tensor | None = None,
+    v_bias: torch.Tensor | None = None,
+    w: torch.Tensor | None = None,
+    gate: torch.Tensor | None = None,
+    angle_left: torch.Tensor | None = None,
+    angle_right: torch.Tensor | None = None,
+    angle_gate: torch.Tensor | None = None,
+    message_left: torch.Tensor | None = None,
+    message_right: torch.Tensor | None = None,
+    message_basis: torch.Tensor | None = None,
+    precision: str = "bf16_tc",
+    need_backward_state: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor | None, torch.Tensor | None]:
+    """Returns ``(out[q.dtype] (B,H,N,D), lse fp32 (B,H,N), out fp32 (B,H,N,D))``.
+
+    With ``need_backward_state=False`` (inference) only ``out`` is produced and
+    the other two are None, which skips the fp32 output and lse writes.
+    """
+    if not HIP_AVAILABLE:
+        raise RuntimeError(f"HIP simplicial attention is unavailable: {_native.load_error()}")
+    if q.device.type != "cuda":
+        raise RuntimeError("hip_simplicial_attention_forward requires GPU tensors")
+    if any(t is not None for t in (u, v_bias, w, gate, angle_left, angle_right, angle_gate,
+                                   message_left, message_right, message_basis)):
+        raise RuntimeError(
+            "the HIP simplicial kernel does not implement factorized bias / low-rank angle / "
+            "low-rank message terms yet"
+        )
+    precision = normalize_simplicial_precision(precision)
+    if q.dim() != 4:
+        raise ValueError(f"q must have shape (B, H, N, D), got {tuple(q.shape)}")
+    B, H, N, D = q.shape
+    for name, t in (("k1", k1), ("v1", v1), ("k2", k2), ("v2", v2)):
+        if t.shape != q.shape:
+            raise ValueError(f"{name} must have shape {tuple(q.shape)}, got {tuple(t.shape)}")
+        if t.device != q.device:
+            raise RuntimeError(f"{name} must be on {q.device}")
+    if tuple(query_valid.shape) != (B, N) or tuple(pair_key_valid.shape) != (B, N):
+        raise ValueError(f"query_valid and pair_key_valid must have shape {(B, N)}")
+    if pair_valid is not None and tuple(pair_valid.shape) != (B, N, N):
+        raise ValueError(f"pair_valid must have shape {(B, N, N)}, got {tuple(pair_valid.shape)}")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise RuntimeError(f"the HIP backend only supports float16/bfloat16/float32 inputs, got {q.dtype}")
+
+    cdt = _compute_dtype(q.dtype, precision)
+    ops = [t.to(device=q.device, dtype=cdt).contiguous() for t in (q, k1, v1, k2, v2)]
+    qv = query_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    pkv = pair_key_valid.to(device=q.device, dtype=torch.bool).contiguous()
+    pv = None if pair_valid is None else pair_valid.to(device=q.device, dtype=torch.bool).contiguous()
+
+    out_direct = q.dtype == cdt
+    out = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype) if out_direct else None
+    out_f32 = None
+    if need_backward_state or not out_direct:
+        out_f32 = torch.empty((B, H, N, D), device=q.device, dtype=torch.float32)
+    lse = torch.empty((B, H, N), device=q.device, dtype=torch.float32) if need_backward_state else None
+
+    args = _native.MfSimplicialFwdArgs(
+        q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(),
+        k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
+        query_valid=qv.data_ptr(), pair_key_valid=pkv.data_ptr(),
+        pair_valid=None if pv is None else pv.data_ptr(),
+        out=None if out is None else out.data_ptr(),
+        out_f32=None if out_f32 is None else out_f32.data_ptr(),
+        lse=None if lse is None else lse.data_ptr(),
+        batch=B, heads=H, tokens=N, head_dim=D,
+        dtype=_native.dtype_code(cdt), precision=_native.MF_PREC[precision],
+    )
+    lib = _native.lib()
+    with torch.cuda.device(q.device):
+        status = lib.mf_simplicial_fwd(args, _native.current_stream(q.device))
+    _native.check(status, "mf_simplicial_fwd")
+    if out is None:
+        out = out_f32.to(q.dtype)
+    if not need_backward_state:
+        return out, None, None
+    return out, lse, out_f32
+
+
+def hip_simplicial_attention_backward(
+    grad_out: torch.Tensor,
+    q: torch.Tensor,
+    k1: torch.Tensor,
+    v1: torch.Tensor,
+    k2: torch.Tensor,
+    v2: torch.Tensor,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    *,
+    query_valid: torch.Tensor,
+    pair_key_valid: torch.Tensor,
+    pair_valid: torch.Tensor | None,
+    u: torch.Tensor | None = None,
+    v_bias: torch.Tensor | None = None,
+    w: torch.Tensor | None = None,
+    gate: torch.Tensor | None = None,
+    angle_left: torch.Tensor | None = None,
+    angle_right: torch.Tensor | None = None,
+    angle_gate: torch.Tensor | None = None,
+    message_left: torch.Tensor | None = None,
+    message_right: torch.Tensor | None = None,
+    message_basis: torch.Tensor | None = None,
+    precision: str = "bf16_tc",
+    need_du: bool = True,
+    need_dv_bias: bool = True,
+    need_dw: bool = True,
+    need_dgate: bool = True,
+    need_dangle_left: bool = True,
+    need_dangle_right: bool = True,
+    need_dangle_gate: bool = True,
+    need_dmessage_left: bool = True,
+    need_dmessage_right: bool = True,
+    need_dmessage_basis: bool = True,
+):
+    """Gradients by recomputing the forward with the torch path on the same device.
+
+    This is the reference's own ``debug_torch_backward`` recompute
+    (simplicial_attention.py:454-552) with fp32 core; a fused HIP backward
+    kernel is not part of this library yet.  Returns the 15-tuple of
+    triton_simplicial_attention.py:963-979 (None for grads not needed/absent).
+    """
+    del out, lse, precision
+    has_bias = u is not None
+    has_angle = angle_left is not None
+    has_message = message_left is not None
+    leaves = [t.detach().requires_grad_(True) for t in (q, k1, v1, k2, v2)]
+    opt: list[torch.Tensor | None] = [None] * 10
+    if has_bias:
+        opt[0:4] = [t.detach().requires_grad_(True) for t in (u, v_bias, w, gate)]
+    if has_angle:
+        opt[4:7] = [t.detach().requires_grad_(True) for t in (angle_left, angle_right, angle_gate)]
+    if has_message:
+        opt[7:10] = [t.detach().requires_grad_(True) for t in (message_left, message_right, message_basis)]
+    with torch.enable_grad():
+        fb = SimplicialFactorizedBias(u=opt[0], v=opt[1], w=opt[2], gate=opt[3]) if has_bias else None
+        ar = SimplicialLowRankAngleResidual(left=opt[4], right=opt[5], gate=opt[6]) if has_angle else None
+        mr = SimplicialLowRankMessageResidual(left=opt[7], right=opt[8]) if has_message else None
+        mask = SimplicialAttentionMask(query_valid=query_valid, pair_key_valid=pair_key_valid, pair_valid=pair_valid)
+        ref = simplicial_attention_torch_from_projected(
+            *leaves, attention_mask=mask, factorized_bias=fb, angle_residual=ar, message_residual=mr,
+            message_basis=opt[9] if has_message else None, chunk_size=128, fp32_core=True,
+        )
+        inputs = leaves + [t for t in opt if t is not None]
+        grads = list(torch.autograd.grad(ref, inputs, grad_out.to(ref.dtype), allow_unused=True))
+    core = grads[:5]
+    rest = grads[5:]
+    flags = [need_du, need_dv_bias, need_dw, need_dgate, need_dangle_left, need_dangle_right,
+             need_dangle_gate, need_dmessage_left, need_dmessage_right, need_dmessage_basis]
+    optional: list[torch.Tensor | None] = []
+    cursor = 0
+    for present, group in ((has_bias, range(0, 4)), (has_angle, range(4, 7)), (has_message, range(7, 10))):
+        for idx in group:
+            if present:
+                g = rest[cursor]
+                cursor += 1
+                optional.append(g if flags[idx] else None)
+            else:
+                optional.append(None)
+    return (*core, *optional)
+
+
+# Reference names.
+triton_simplicial_attention_forward = hip_simplicial_attention_forward
+triton_simplicial_attention_backward = hip_simplicial_attention_backward

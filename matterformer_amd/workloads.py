@@ -1,0 +1,94 @@
+"""Seeded synthetic inputs for the BASELINE.json configurations.
+
+Generation rule (all configs): atom counts are drawn first, then tensors, from
+one CPU ``torch.Generator().manual_seed(seed)``; tensors are generated in fp32
+on the CPU and then cast and moved, so CPU and GPU see identical bits.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass
+class SimplicialWorkload:
+    name: str
+    q: torch.Tensor
+    k1: torch.Tensor
+    v1: torch.Tensor
+    k2: torch.Tensor
+    v2: torch.Tensor
+    query_valid: torch.Tensor      # (B, N) bool
+    pair_key_valid: torch.Tensor   # (B, N) bool
+    counts: torch.Tensor           # (B,) int64 valid atoms per molecule
+
+    @property
+    def shape(self) -> tuple[int, int, int, int]:
+        return tuple(self.q.shape)
+
+    def to(self, device, dtype=None) -> "SimplicialWorkload":
+        def mv(t):
+            if t.is_floating_point() and dtype is not None:
+                t = t.to(dtype)
+            return t.to(device)
+        return SimplicialWorkload(self.name, *(mv(t) for t in (self.q, self.k1, self.v1, self.k2, self.v2)),
+                                  self.query_valid.to(device), self.pair_key_valid.to(device), self.counts)
+
+    def valid_flops(self) -> int:
+        """sum_b 4*H*D*n_b^3 (logits 2 n^3 D + value path 2 n^3 D per head)."""
+        B, H, N, D = self.shape
+        n = self.counts.to(torch.int64)
+        return int(4 * H * D * int((n ** 3).sum()))
+
+
+def qm9_counts(batch: int, gen: torch.Generator) -> torch.Tensor:
+    """Config 1: atom counts uniform in [9, 29]."""
+    return torch.randint(9, 30, (batch,), generator=gen)
+
+
+def geom_counts(batch: int, gen: torch.Generator, max_atoms: int = 181) -> torch.Tensor:
+    """Config 2: round(44 + 12 z) clipped to [10, 181]."""
+    z = torch.randn(batch, generator=gen)
+    return torch.clamp(torch.round(44.0 + 12.0 * z), 10, max_atoms).to(torch.int64)
+
+
+def simplicial_workload(config: str, seed: int | None = None, *, batch: int | None = None,
+                        heads: int | None = None) -> SimplicialWorkload:
+    """fp32 CPU tensors for config "qm9" (C1) or "geom" (C2); cast/move with ``.to``."""
+    if config == "qm9":
+        B, H, N, D, seed0, std = 128, 8, 29, 32, 0, 1.0 / math.sqrt(32)
+        draw = qm9_counts
+    elif config == "geom":
+        B, H, N, D, seed0, std = 64, 8, 181, 64, 1, 1.0 / 8.0
+        draw = geom_counts
+    else:
+        raise ValueError(f"unknown simplicial config {config!r}")
+    B = batch or B
+    H = heads or H
+    gen = torch.Generator().manual_seed(seed0 if seed is None else seed)
+    counts = draw(B, gen)
+    tensors = [torch.randn(B, H, N, D, generator=gen) * std for _ in range(5)]
+    valid = torch.arange(N)[None, :] < counts[:, None]
+    return SimplicialWorkload(config, *tensors, valid.clone(), valid.clone(), counts)
+
+
+def random_simplicial(B: int, H: int, N: int, D: int, *, seed: int, counts=None, holes=None,
+                      pair_drop: float = 0.0, std: float | None = None):
+    """Small random case: returns (q,k1,v1,k2,v2, query_valid, pair_key_valid, pair_valid) fp32 CPU."""
+    gen = torch.Generator().manual_seed(seed)
+    std = (1.0 / math.sqrt(D)) if std is None else std
+    tensors = [torch.randn(B, H, N, D, generator=gen) * std for _ in range(5)]
+    key_valid = torch.ones(B, N, dtype=torch.bool)
+    if counts is not None:
+        for b, n in enumerate(counts):
+            key_valid[b, n:] = False
+    query_valid = key_valid.clone()
+    for b, i in holes or ():
+        key_valid[b, i] = False
+    pair_valid = None
+    if pair_drop > 0:
+        pair_valid = torch.rand(B, N, N, generator=gen) >= pair_drop
+    return (*tensors, query_valid, key_valid, pair_valid)

@@ -1,0 +1,153 @@
+"""Write golden input/output vectors from the stases/Matterformer reference.
+
+Run in the survey container only (the reference is not present on GPU boxes):
+
+    python tests/golden/make_golden.py [/root/reference]
+
+It imports the reference's pure-Python torch path and geometry adapters and
+stores small seeded cases as ``.npz`` fixtures next to this script.  The
+fixtures pin what the mathematical checks in ``tests/`` leave open: the exact
+rounding of the reference's bf16 torch path
+(``src/matterformer/models/simplicial_attention.py:161-180,317-329``), its
+masking conventions, and the distance / minimum-image conventions of
+``src/matterformer/geometry/adapters.py:83-125,151-212``.
+
+bf16 tensors are stored as float32 arrays holding exactly the bf16 values
+(the bf16 -> fp32 conversion is exact).
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    t = t.detach()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        t = t.float()
+    return t.cpu().numpy()
+
+
+def _simplicial_case(ref, name: str, *, seed: int, B: int, H: int, N: int, D: int, dtype: torch.dtype,
+                     fp32_core: bool, counts=None, holes=None, pair_drop=0.0, bias=False, angle_rank=0,
+                     message_rank=0, chunk_size=128) -> dict:
+    gen = torch.Generator().manual_seed(seed)
+    scale = 1.0 / math.sqrt(D)
+    shape = (B, H, N, D)
+    tensors = [(torch.randn(shape, generator=gen) * scale).to(dtype) for _ in range(5)]
+    q, k1, v1, k2, v2 = tensors
+    key_valid = torch.ones(B, N, dtype=torch.bool)
+    if counts is not None:
+        for b, n in enumerate(counts):
+            key_valid[b, n:] = False
+    query_valid = key_valid.clone()
+    if holes is not None:  # tokens that are valid queries but not pair keys (CLS-style)
+        for b, i in holes:
+            key_valid[b, i] = False
+    pair_valid = None
+    if pair_drop > 0:
+        pair_valid = torch.rand(B, N, N, generator=gen) >= pair_drop
+    mask = ref.SimplicialAttentionMask(query_valid=query_valid, pair_key_valid=key_valid, pair_valid=pair_valid)
+    fb = ar = mr = basis = None
+    extra = {}
+    if bias:
+        fb = ref.SimplicialFactorizedBias(
+            u=torch.randn(B, H, N, N, generator=gen).to(dtype),
+            v=torch.randn(B, H, N, N, generator=gen).to(dtype),
+            w=torch.randn(B, H, N, N, generator=gen).to(dtype),
+            gate=torch.randn(B, H, N, generator=gen).to(dtype),
+        )
+        extra.update(u=_np(fb.u), v_bias=_np(fb.v), w=_np(fb.w), gate=_np(fb.gate))
+    if angle_rank:
+        ar = ref.SimplicialLowRankAngleResidual(
+            left=torch.randn(B, H, N, N, angle_rank, generator=gen).to(dtype),
+            right=torch.randn(B, H, N, N, angle_rank, generator=gen).to(dtype),
+            gate=torch.randn(B, H, N, generator=gen).to(dtype),
+        )
+        extra.update(angle_left=_np(ar.left), angle_right=_np(ar.right), angle_gate=_np(ar.gate))
+    if message_rank:
+        mr = ref.SimplicialLowRankMessageResidual(
+            left=torch.randn(B, H, N, N, message_rank, generator=gen).to(dtype),
+            right=torch.randn(B, H, N, N, message_rank, generator=gen).to(dtype),
+        )
+        basis = torch.randn(H, message_rank, D, generator=gen).to(dtype)
+        extra.update(message_left=_np(mr.left), message_right=_np(mr.right), message_basis=_np(basis))
+    out = ref.simplicial_attention_torch_from_projected(
+        q, k1, v1, k2, v2, attention_mask=mask, factorized_bias=fb, angle_residual=ar,
+        message_residual=mr, message_basis=basis, chunk_size=chunk_size, fp32_core=fp32_core,
+    )
+    case = dict(
+        q=_np(q), k1=_np(k1), v1=_np(v1), k2=_np(k2), v2=_np(v2),
+        query_valid=query_valid.numpy(), pair_key_valid=key_valid.numpy(),
+        out=_np(out),
+        dtype=np.array(str(dtype).replace("torch.", "")),
+        out_dtype=np.array(str(out.dtype).replace("torch.", "")),
+        fp32_core=np.array(fp32_core), chunk_size=np.array(chunk_size),
+        **extra,
+    )
+    if pair_valid is not None:
+        case["pair_valid"] = pair_valid.numpy()
+    np.savez_compressed(HERE / f"simplicial_{name}.npz", **case)
+    return case
+
+
+def main(reference_root: str) -> None:
+    sys.path.insert(0, str(Path(reference_root) / "src"))
+    import matterformer.models.simplicial_attention as ref  # noqa: E402
+    from matterformer.geometry import NonPeriodicGeometryAdapter, PeriodicGeometryAdapter  # noqa: E402
+    from matterformer.geometry.lattice import lattice_latent_to_gram  # noqa: E402
+
+    # --- 2-simplicial attention torch path ---
+    _simplicial_case(ref, "fp32_padding", seed=10, B=2, H=4, N=5, D=8, dtype=torch.float32,
+                     fp32_core=False, counts=[4, 2], chunk_size=2)
+    _simplicial_case(ref, "fp32_holes_pairvalid", seed=11, B=3, H=2, N=9, D=16, dtype=torch.float32,
+                     fp32_core=False, counts=[9, 6, 1], holes=[(0, 3), (1, 0)], pair_drop=0.3, chunk_size=4)
+    _simplicial_case(ref, "fp32_qm9_slice", seed=12, B=4, H=8, N=29, D=32, dtype=torch.float32,
+                     fp32_core=False, counts=[29, 17, 9, 23])
+    _simplicial_case(ref, "bf16_native", seed=13, B=2, H=2, N=13, D=32, dtype=torch.bfloat16,
+                     fp32_core=False, counts=[13, 7])
+    _simplicial_case(ref, "bf16_fp32core", seed=14, B=2, H=2, N=13, D=32, dtype=torch.bfloat16,
+                     fp32_core=True, counts=[13, 7])
+    _simplicial_case(ref, "bf16_geom_slice", seed=15, B=2, H=2, N=181, D=64, dtype=torch.bfloat16,
+                     fp32_core=False, counts=[57, 33])
+    _simplicial_case(ref, "fp32_bias_angle_message", seed=16, B=1, H=2, N=7, D=8, dtype=torch.float32,
+                     fp32_core=False, counts=[5], pair_drop=0.2, bias=True, angle_rank=5, message_rank=3,
+                     chunk_size=3)
+
+    # --- geometry conventions: pairwise distances and minimum image ---
+    gen = torch.Generator().manual_seed(20)
+    coords = torch.randn(3, 37, 3, generator=gen) * math.sqrt(2.0)
+    pad = torch.zeros(3, 37, dtype=torch.bool)
+    pad[1, 30:] = True
+    feats = NonPeriodicGeometryAdapter()(coords, pad_mask=pad)
+    np.savez_compressed(
+        HERE / "geometry_nonperiodic.npz",
+        coords=coords.numpy(), pad_mask=pad.numpy(),
+        pair_dist2=feats.pair_dist2.numpy(), pair_dist=feats.pair_dist.numpy(),
+    )
+
+    gen = torch.Generator().manual_seed(21)
+    ncell, nat = 3, 40
+    frac = torch.rand(ncell, nat, 3, generator=gen)
+    lengths = 15.0 + 15.0 * torch.rand(ncell, 3, generator=gen)
+    angles = (80.0 + 20.0 * torch.rand(ncell, 3, generator=gen)) * math.pi / 180.0
+    lattice = torch.cat([lengths.log(), angles.cos()], dim=-1)
+    feats = PeriodicGeometryAdapter(pbc_radius=1, lattice_repr="y1")(frac, lattice=lattice)
+    gram = lattice_latent_to_gram(lattice, lattice_repr="y1")
+    np.savez_compressed(
+        HERE / "geometry_periodic.npz",
+        frac=frac.numpy(), lattice_y1=lattice.numpy(), gram=gram.numpy(),
+        pair_dist2=feats.pair_dist2.numpy(), pair_delta=feats.pair_delta.numpy(),
+    )
+    print("wrote fixtures to", HERE)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
