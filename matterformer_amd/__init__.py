@@ -10,13 +10,27 @@ Public modules:
   matterformer_amd.geometry_ops              kNN top-k, radius mask, radius attention
 The kernels live in libmf_hip.so (C ABI: include/mf_capi.h), built by
 ``python -m matterformer_amd.build``.
+
+The package root exports lazily, so ``matterformer_amd.build`` can be imported
+(and the library built) before anything tries to load the library.
 """
 
-from matterformer_amd.simplicial_attention import (  # noqa: F401
-    SimplicialAttention,
-    SimplicialAttentionMask,
-    SimplicialFactorizedBias,
-    SimplicialLowRankAngleResidual,
-    SimplicialLowRankMessageResidual,
-    TwoSimplicialAttention,
-)
+_LAZY = {
+    "SimplicialAttention": "matterformer_amd.simplicial_attention",
+    "SimplicialAttentionMask": "matterformer_amd.simplicial_types",
+    "SimplicialFactorizedBias": "matterformer_amd.simplicial_types",
+    "SimplicialLowRankAngleResidual": "matterformer_amd.simplicial_types",
+    "SimplicialLowRankMessageResidual": "matterformer_amd.simplicial_types",
+    "TwoSimplicialAttention": "matterformer_amd.simplicial_attention",
+}
+
+__all__ = sorted(_LAZY)
+
+
+def __getattr__(name):
+    module = _LAZY.get(name)
+    if module is None:
+        raise AttributeError(f"module 'matterformer_amd' has no attribute {name!r}")
+    import importlib
+
+    return getattr(importlib.import_module(module), name)

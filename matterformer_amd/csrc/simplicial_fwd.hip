@@ -13,7 +13,8 @@
 //    (molecule, head, query range).  The list is derived from the masks by
 //    every workgroup itself (a ballot-count over the masks), so there is no
 //    host synchronisation and a single launch.
-//  * Per item, the compacted K1, K2, V1 rows and V2^T are staged in LDS.
+//  * Per item, the compacted K1 and K2 rows and V2^T are staged in LDS; V1 is
+//    only read once per (query, j tile) in the epilogue and comes from L1/L2.
 //  * Per query i and tile of 16 j-rows, two MFMA chains:
 //      GEMM1  C1[k][j]   = sum_d K2[k][d] * (q_i (.) K1[j])[d]    -> S^T tile
 //      GEMM2  C2[d][j]  += sum_k V2^T[d][k] * P[j][k]             -> (P V2)^T
@@ -58,11 +59,11 @@ struct Params {
 template <typename T, int DP>
 struct Layout {
   static constexpr int kPadK = 16 / Elem<T>::kSize;  // 16 bytes of row padding
-  static constexpr int KS = DP + kPadK;              // row stride of K1s/K2s/V1s
+  static constexpr int KS = DP + kPadK;              // row stride of K1s/K2s
   __host__ __device__ static int vs(int NP) { return NP + kPadK; }  // row stride of V2Ts
   __host__ __device__ static size_t bytes(int NP, int B, bool has_pv) {
     size_t s = 0;
-    s += size_t(3) * NP * KS * Elem<T>::kSize;  // K1s, K2s, V1s
+    s += size_t(2) * NP * KS * Elem<T>::kSize;  // K1s, K2s
     s += size_t(DP) * vs(NP) * Elem<T>::kSize;  // V2Ts
     s += size_t(NP) * 4 * 2;                    // kidx, qidx
     if (has_pv) s += size_t(NP) * (NP / 32) * 4;  // pair-valid bit rows
@@ -114,8 +115,7 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
 
   T* K1s = reinterpret_cast<T*>(smem);
   T* K2s = K1s + NP * KS;
-  T* V1s = K2s + NP * KS;
-  T* V2Ts = V1s + NP * KS;
+  T* V2Ts = K2s + NP * KS;
   int* kidx = reinterpret_cast<int*>(V2Ts + DP * VS);
   int* qidx = kidx + NP;
   uint32_t* pvb = reinterpret_cast<uint32_t*>(qidx + NP);
@@ -230,7 +230,6 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
     {
       const T* gk1 = static_cast<const T*>(p.k1) + size_t(bh) * N * D;
       const T* gk2 = static_cast<const T*>(p.k2) + size_t(bh) * N * D;
-      const T* gv1 = static_cast<const T*>(p.v1) + size_t(bh) * N * D;
       const T* gv2 = static_cast<const T*>(p.v2) + size_t(bh) * N * D;
       constexpr int CPR = DP / C16;  // 16-byte chunks per padded row
       const int units = nrow * CPR;
@@ -240,17 +239,15 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
         const int e0 = c * C16;
         T* d1 = K1s + r * KS + e0;
         T* d2 = K2s + r * KS + e0;
-        T* d3 = V1s + r * KS + e0;
         T tmp[C16];
         if (r < nk) {
           const size_t src = size_t(kidx[r]) * D;
           load_row_chunk16<T>(d1, gk1 + src, e0, D, p.vec_ok);
           load_row_chunk16<T>(d2, gk2 + src, e0, D, p.vec_ok);
-          load_row_chunk16<T>(d3, gv1 + src, e0, D, p.vec_ok);
           load_row_chunk16<T>(tmp, gv2 + src, e0, D, p.vec_ok);
         } else {
 #pragma unroll
-          for (int e = 0; e < C16; ++e) { d1[e] = T(0.0f); d2[e] = T(0.0f); d3[e] = T(0.0f); tmp[e] = T(0.0f); }
+          for (int e = 0; e < C16; ++e) { d1[e] = T(0.0f); d2[e] = T(0.0f); tmp[e] = T(0.0f); }
         }
 #pragma unroll
         for (int e = 0; e < C16; ++e) V2Ts[(e0 + e) * VS + r] = tmp[e];
@@ -439,12 +436,17 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
           }
         }
 
-        // out_i[d] += sum_j V1[j][d] * C2[d][j]; lane holds j = row, d = mt*16+4g+r
+        // out_i[d] += sum_j V1[j][d] * C2[d][j]; lane holds j = row, d = mt*16+4g+r.
+        // V1 is read from global memory (L1/L2), rows past nk contribute 0.
+        if (row_ok) {
+          const T* vrow = static_cast<const T*>(p.v1) + (size_t(bh) * N + kidx[j]) * D;
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) {
-          const T* vrow = V1s + j * KS + mt * 16 + 4 * g;
+          for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mt][r] += E::to_f32(vrow[r]) * tacc[mt][r];
+            for (int r = 0; r < 4; ++r) {
+              const int d = mt * 16 + 4 * g + r;
+              if (d < D) acc[mt][r] += E::to_f32(vrow[d]) * tacc[mt][r];
+            }
         }
       }
 
