@@ -111,10 +111,14 @@ def main() -> int:
     B, H, N, D = wd.shape
     ops = [t.contiguous() for t in (wd.q, wd.k1, wd.v1, wd.k2, wd.v2)]
     out = torch.empty((B, H, N, D), device=dev, dtype=torch.bfloat16)
+    ws_bytes = lib.mf_simplicial_fwd_workspace_size(B, H, N, D, _native.MF_DTYPE_BF16)
+    ws = _native.workspace(ws_bytes, dev)
     args_struct = _native.MfSimplicialFwdArgs(
         q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(), k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
         query_valid=wd.query_valid.data_ptr(), pair_key_valid=wd.pair_key_valid.data_ptr(), pair_valid=None,
-        out=out.data_ptr(), out_f32=None, lse=None, batch=B, heads=H, tokens=N, head_dim=D,
+        out=out.data_ptr(), out_f32=None, lse=None,
+        workspace=None if ws is None else ws.data_ptr(), workspace_bytes=ws_bytes,
+        batch=B, heads=H, tokens=N, head_dim=D,
         dtype=_native.MF_DTYPE_BF16, precision=_native.MF_PREC["bf16_tc"],
     )
     stream = torch.cuda.current_stream(dev)

@@ -13,6 +13,10 @@
  * thread-local, human-readable description of the most recent failure on the
  * calling thread.
  *
+ * Scratch device memory an entry point needs is passed in by the caller as a
+ * workspace whose size the matching mf_*_workspace_size() reports; the
+ * workspace may be reused by later calls on the same stream.
+ *
  * Reference interfaces replaced (paths relative to stases/Matterformer):
  *   mf_simplicial_fwd   <- triton_simplicial_attention_forward
  *                          src/matterformer/models/triton_simplicial_attention.py:790-926
@@ -35,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 1
+#define MF_ABI_VERSION 2
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -93,6 +97,11 @@ typedef struct mf_simplicial_fwd_args {
   void* out;        /* [B*H, N, D] in `dtype` (the `out.to(q.dtype)` result) */
   float* out_f32;   /* [B*H, N, D] fp32 (the saved-for-backward output)      */
   float* lse;       /* [B*H, N] fp32, natural log                            */
+  /* Device scratch of at least mf_simplicial_fwd_workspace_size() bytes,
+   * 16-byte aligned (NULL when that size is 0).  Holds the per-molecule
+   * atom lists and the work items built on the device for this call. */
+  void* workspace;
+  uint64_t workspace_bytes;
   int32_t batch;
   int32_t heads;
   int32_t tokens;
@@ -107,6 +116,10 @@ int mf_simplicial_fwd(const mf_simplicial_fwd_args* args, void* stream);
  * device, MF_ERR_UNSUPPORTED (with mf_last_error set) when it cannot. */
 int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t tokens,
                                 int32_t head_dim, int32_t dtype);
+
+/* Bytes of workspace mf_simplicial_fwd needs for this shape (0 if none). */
+uint64_t mf_simplicial_fwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens,
+                                          int32_t head_dim, int32_t dtype);
 
 #ifdef __cplusplus
 }

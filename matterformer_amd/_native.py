@@ -36,12 +36,10 @@ EXPORTED_SYMBOLS = (
     "mf_last_error",
     "mf_simplicial_fwd",
     "mf_simplicial_fwd_supported",
-    "mf_knn",
-    "mf_radius_mask",
-    "mf_radius_attn",
+    "mf_simplicial_fwd_workspace_size",
 )
 
-EXPECTED_ABI_VERSION = 1
+EXPECTED_ABI_VERSION = 2
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -63,6 +61,8 @@ class MfSimplicialFwdArgs(ctypes.Structure):
         ("out", ctypes.c_void_p),
         ("out_f32", ctypes.c_void_p),
         ("lse", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_uint64),
         ("batch", ctypes.c_int32),
         ("heads", ctypes.c_int32),
         ("tokens", ctypes.c_int32),
@@ -150,6 +150,8 @@ def _load() -> ctypes.CDLL | None:
             fn.restype = ctypes.c_int
     lib.mf_simplicial_fwd_supported.argtypes = [ctypes.c_int32] * 5
     lib.mf_simplicial_fwd_supported.restype = ctypes.c_int
+    lib.mf_simplicial_fwd_workspace_size.argtypes = [ctypes.c_int32] * 5
+    lib.mf_simplicial_fwd_workspace_size.restype = ctypes.c_uint64
     version = lib.mf_abi_version()
     if version != EXPECTED_ABI_VERSION:
         _LOAD_ERROR = f"{path} has ABI version {version}, expected {EXPECTED_ABI_VERSION}"
@@ -200,3 +202,11 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 def current_stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    """Device scratch for an entry point (16-byte aligned; torch's allocator
+    hands out 512-byte aligned blocks)."""
+    if nbytes == 0:
+        return None
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)

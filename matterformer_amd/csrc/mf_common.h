@@ -24,6 +24,12 @@ struct DeviceInfo {
 };
 int device_info(DeviceInfo* out);
 
+// Register-resident simplicial kernels for 16-bit operands (simplicial_fast.hip).
+int simplicial_fast_capacity(int head_dim);
+size_t simplicial_fast_workspace_bytes(int batch, int heads, int tokens);
+int simplicial_fast_launch(const mf_simplicial_fwd_args* a, void* workspace, int num_cus, hipStream_t stream);
+constexpr int kSimplicialFastMaxBatch = 1024;  // molecules per launch slice
+
 #define MF_HIP_CHECK(expr)                                                     \
   do {                                                                         \
     hipError_t mf_err_ = (expr);                                               \

@@ -1,0 +1,1142 @@
+// 2-simplicial attention forward for 16-bit operands on gfx950 (CDNA4): the
+// kernels behind mf_simplicial_fwd for bf16/fp16 and head_dim <= 64.
+//
+// Math (simplicial_attention.py:161-180,304-344; triton_simplicial_attention.py:115-329):
+//   S_i[j,k] = sum_d q_i[d] k1_j[d] k2_k[d]
+//   P_i      = softmax over valid (j,k) of S_i
+//   out_i[d] = sum_{j,k} P_i[j,k] v1_j[d] v2_k[d],   lse_i = log sum_{j,k} exp(S_i[j,k])
+//
+// Three launches on the caller's stream, no host synchronisation:
+//   plan   one workgroup turns the byte masks into, per molecule, compacted
+//          lists of valid keys, valid queries and padded query rows, and into
+//          work items (molecule, head, range of valid queries) holding about
+//          work_target logits each, ordered by molecule cost (largest first),
+//          all written to the caller's workspace;
+//   small  a persistent grid (2 workgroups per CU) walks the items of
+//          molecules with at most CH = 16*NT keys (all of a GEOM-Drugs batch)
+//          round-robin, so every workgroup gets one item from each cost band;
+//          it also zeroes the padded query rows;
+//   large  launched only when tokens > CH: molecules with more keys, in
+//          (j chunk, k chunk) pairs and two sweeps (exact maximum, then
+//          accumulation), one query per wave.
+// Logical workgroup ids are remapped so that consecutive ids share an XCD
+// (blockIdx.x % 8 is the XCD): the items of one molecule land in one L2.
+//
+// Per item the workgroup stages the keys of (b, h) in LDS:
+//   K1s  [CH][DP+4] fp32 (bf16) / [CH][DP+8] fp16   (source of the GEMM1 B operand)
+//   V2T  [DP][CH+8]    transposed                    (GEMM2 B operand)
+//   V1T  [DP+16][CH+4] fp32, transposed, plus a row of key validity
+//   Qs   the item's query rows times log2(e), fp32 (bf16) / fp16
+// and every wave loads K2 as GEMM1 A operands and V2 as GEMM2 B operands into
+// registers, where they stay for all of the wave's queries.
+// The inner loop reads LDS only for one K1 tile and one V1 tile per
+// (query, 16-row j tile).
+//
+// Per query i and j tile (16 keys j, lane column r16 = j):
+//   B1      = bf16(q'_i (.) K1[j])           q' = q log2(e); v_mul_f32 on K1 staged
+//                                             as fp32, or v_pk_mul_f16 for fp16
+//   GEMM1   C1[k][j] = sum_d K2[k][d] B1[j][d]            (MFMA 16x16x32, k = A rows)
+//   P       = exp2(C1)                                     (= exp of the logit)
+//   GEMM2   C2[j][d] = sum_k P[j][k] V2[k][d]              (MFMA, P = A operand straight
+//                                                          from the C1 registers)
+//   out    += sum_j V1[j][d] C2[j][d]         (fp32 FMAs, V1 from LDS)
+// The softmax denominator is an extra GEMM2 column whose B operand marks the
+// valid keys, so it costs MFMA cycles instead of one VALU add per logit, and
+// padded keys need no masking: their K2/V2 rows are zero and their denominator
+// entry is 0.  Padded j rows get P = 1 but are weighted by V1 = 0 and
+// validity 0.  The code for each count of active 16-key tiles is generated
+// separately, so the inner loop is straight-line.
+//
+// No running maximum in the common case.  With m_d = max_j |K1[j][d]| and
+// n_d = max_k |K2[k][d]|, |S_i[j,k]| <= U_i = sum_d |q'_i[d]| m_d n_d.  When
+// U_i <= bound_limit (60 for bf16, 14 for fp16: P = 2^S then stays a normal
+// number of the operand type and the fp32 sums cannot overflow) P = 2^S is used
+// directly: softmax is invariant to the offset, and floating point keeps the
+// same relative precision at any scale.  Otherwise the query takes two passes:
+// pass 1 computes the exact maximum m of the valid logits (GEMM1 only), pass 2
+// uses P = 2^(S - m) with explicit masking (the accumulator starts at -m).
+#include <cmath>
+#include <type_traits>
+
+#include "mf_common.h"
+
+namespace mf {
+namespace sfast {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kPlanThreads = 1024;
+constexpr int kMaxBatch = 1024;  // molecules per launch (one plan thread each)
+constexpr int kMaxQueriesPerItem = 32;
+
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_t;
+typedef __bf16 bf16x2_e __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_e __attribute__((ext_vector_type(2)));
+
+// Workspace of one launch slice (B molecules of N tokens, H heads), in ints:
+//   hdr[4]              n_small_items, n_large_items
+//   nkq[B]              nk << 16 | nq
+//   kidx[B][N]          valid key positions, compacted
+//   qidx[B][N]          valid query positions, compacted
+//   zidx[B][N]          padded query positions (N - nq of them)
+//   small[MI][4]        items (b, h, q0 | q1 << 16, nk) of molecules with nk <= CH
+//   large[MI][4]        items of molecules with nk > CH
+// with MI = B * H * ceil(N / kWaves), a bound on the item count of either kind.
+struct Workspace {
+  int* hdr;
+  int* nkq;
+  int* kidx;
+  int* qidx;
+  int* zidx;
+  int4* small_items;
+  int4* large_items;
+};
+
+__host__ __device__ inline size_t max_items(int B, int H, int N) {
+  return size_t(B) * H * ((N + kWaves - 1) / kWaves);
+}
+
+__host__ __device__ inline Workspace carve_workspace(void* base, int B, int H, int N) {
+  Workspace w;
+  int* p = static_cast<int*>(base);
+  w.hdr = p;
+  p += 4;
+  w.nkq = p;
+  p += B;
+  w.kidx = p;
+  p += size_t(B) * N;
+  w.qidx = p;
+  p += size_t(B) * N;
+  w.zidx = p;
+  p += size_t(B) * N;
+  p += (4 - (reinterpret_cast<uintptr_t>(p) / 4) % 4) % 4;  // 16-byte alignment
+  w.small_items = reinterpret_cast<int4*>(p);
+  w.large_items = w.small_items + max_items(B, H, N);
+  return w;
+}
+
+__host__ inline size_t workspace_bytes(int B, int H, int N) {
+  return (4 + size_t(B) + 3 * size_t(B) * N + 4) * 4 + 2 * max_items(B, H, N) * sizeof(int4);
+}
+
+struct Params {
+  const void* q;
+  const void* k1;
+  const void* v1;
+  const void* k2;
+  const void* v2;
+  const uint8_t* qv;
+  const uint8_t* pkv;
+  const uint8_t* pv;
+  void* out;
+  float* out_f32;
+  float* lse;
+  Workspace ws;
+  int B, H, N, D;
+  int cap;            // keys per chunk (CH) of the kernel that serves this head dim
+  int work_target;    // logits per item
+  float bound_limit;  // largest |S| (log2 units) served without a running max
+  int vec_ok;         // rows 16-byte aligned and D*2 % 16 == 0
+};
+
+// ---------------------------------------------------------------------------
+// 16-bit element traits.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Half;
+
+typedef float f32x2_e __attribute__((ext_vector_type(2)));
+
+template <>
+struct Half<__bf16> {
+  using Op8 = mf_bf16x8;
+  using Op4 = bf16x4_t;
+  using Pair = bf16x2_e;
+  // K1 is staged in LDS as fp32 so that each product is one v_mul_f32
+  using K1T = float;
+  struct QOp {
+    float q[8];
+  };
+  __device__ static __forceinline__ mf_f32x4 mfma32(Op8 a, Op8 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_e{lo, hi}, Pair));
+  }
+  // q is staged as fp32 with log2(e) folded in, so that exp2 of the logits is
+  // the softmax numerator and each product q' k1 is rounded to bf16 once
+  using QT = float;
+  __device__ static __forceinline__ void prepare(Op8 q8, QOp& o) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o.q[e] = float(q8[e]) * kLog2e;
+  }
+  __device__ static __forceinline__ void store_q(QT* dst, Op8 v) {
+    float4* d = reinterpret_cast<float4*>(dst);
+    d[0] = float4{float(v[0]) * kLog2e, float(v[1]) * kLog2e, float(v[2]) * kLog2e, float(v[3]) * kLog2e};
+    d[1] = float4{float(v[4]) * kLog2e, float(v[5]) * kLog2e, float(v[6]) * kLog2e, float(v[7]) * kLog2e};
+  }
+  __device__ static __forceinline__ void load_q(const QT* src, QOp& o) {
+    const float4 a = *reinterpret_cast<const float4*>(src);
+    const float4 b = *reinterpret_cast<const float4*>(src + 4);
+    o.q[0] = a.x; o.q[1] = a.y; o.q[2] = a.z; o.q[3] = a.w;
+    o.q[4] = b.x; o.q[5] = b.y; o.q[6] = b.z; o.q[7] = b.w;
+  }
+  __device__ static __forceinline__ float qabs(const QOp& o, int e) { return fabsf(o.q[e]); }
+  __device__ static __forceinline__ void store_k1(K1T* dst, Op8 v) {
+    float4* d = reinterpret_cast<float4*>(dst);
+    d[0] = float4{float(v[0]), float(v[1]), float(v[2]), float(v[3])};
+    d[1] = float4{float(v[4]), float(v[5]), float(v[6]), float(v[7])};
+  }
+  // bf16(k1 (.) q) for 8 consecutive d: exact fp32 products, rounded once
+  __device__ static __forceinline__ Op8 mul(const K1T* k1, const QOp& o) {
+    const float4 a = *reinterpret_cast<const float4*>(k1);
+    const float4 b = *reinterpret_cast<const float4*>(k1 + 4);
+    const uint4 r{pack(a.x * o.q[0], a.y * o.q[1]), pack(a.z * o.q[2], a.w * o.q[3]),
+                  pack(b.x * o.q[4], b.y * o.q[5]), pack(b.z * o.q[6], b.w * o.q[7])};
+    return __builtin_bit_cast(Op8, r);
+  }
+};
+
+template <>
+struct Half<_Float16> {
+  using Op8 = mf_f16x8;
+  using Op4 = f16x4_t;
+  using Pair = f16x2_e;
+  using K1T = _Float16;
+  struct QOp {
+    f16x2_e pair[4];
+  };
+  __device__ static __forceinline__ mf_f32x4 mfma32(Op8 a, Op8 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_e{lo, hi}, Pair));
+  }
+  // q is staged as fp16(q log2 e)
+  using QT = _Float16;
+  __device__ static __forceinline__ void prepare(Op8 q8, QOp& o) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      o.pair[p] = f16x2_e{_Float16(float(q8[2 * p]) * kLog2e), _Float16(float(q8[2 * p + 1]) * kLog2e)};
+  }
+  __device__ static __forceinline__ void store_q(QT* dst, Op8 v) {
+    Op8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = _Float16(float(v[e]) * kLog2e);
+    *reinterpret_cast<Op8*>(dst) = r;
+  }
+  __device__ static __forceinline__ void load_q(const QT* src, QOp& o) {
+    const uint4 w = *reinterpret_cast<const uint4*>(src);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) o.pair[p] = __builtin_bit_cast(f16x2_e, ws[p]);
+  }
+  __device__ static __forceinline__ float qabs(const QOp& o, int e) {
+    return fabsf(float((e & 1) ? o.pair[e >> 1].y : o.pair[e >> 1].x));
+  }
+  __device__ static __forceinline__ void store_k1(K1T* dst, Op8 v) { *reinterpret_cast<Op8*>(dst) = v; }
+  // fp16(k1 (.) q) with v_pk_mul_f16 (correctly rounded products)
+  __device__ static __forceinline__ Op8 mul(const K1T* k1, const QOp& o) {
+    const uint4 w = *reinterpret_cast<const uint4*>(k1);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t r[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) r[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_e, ws[p]) * o.pair[p]);
+    return __builtin_bit_cast(Op8, uint4{r[0], r[1], r[2], r[3]});
+  }
+};
+
+
+__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// LDS geometry of the main kernels (host sizing and device carving).
+template <typename T, int DP, int NT>
+struct Layout {
+  using K1T = typename Half<T>::K1T;
+  static constexpr int CH = 16 * NT;         // keys per chunk
+  using QT = typename Half<T>::QT;
+  static constexpr int KS = DP + 16 / int(sizeof(QT));  // row stride (elements) of Qs
+  static constexpr int K1S = DP + 16 / int(sizeof(K1T));  // row stride (elements) of K1s
+  static constexpr int VS = CH + 8;          // row stride (elements) of V2T
+  static constexpr int WS = CH + 4;          // row stride (floats) of V1T
+  static constexpr int PW = (CH + 31) / 32;  // pair-valid words per row
+  static constexpr size_t kK1 = 0;
+  static constexpr size_t kV2T = kK1 + size_t(CH) * K1S * sizeof(K1T);
+  static constexpr size_t kV1T = (kV2T + size_t(DP) * VS * sizeof(T) + 15) & ~size_t(15);
+  static constexpr size_t kQs = kV1T + size_t(DP + 16) * WS * 4;
+  static constexpr size_t kPV = kQs + size_t(kMaxQueriesPerItem) * KS * sizeof(QT);
+  static constexpr size_t kAB = kPV + size_t(CH) * PW * 4;
+  static constexpr size_t kM2 = kAB + size_t(DP) * 4;
+  static constexpr size_t kRed = kM2 + size_t(DP) * 4;
+  static constexpr size_t kFixed = (kRed + size_t(kWaves) * DP * 4 + 15) & ~size_t(15);
+};
+
+// max over the valid logits of one 16-row j tile (log2 units, -inf if none);
+// NKT = number of 16-key tiles of the current key chunk.
+template <typename T, int DP, int NT, int NKT, bool HAS_PV>
+__device__ __forceinline__ float jtile_max(const typename Half<T>::K1T* K1s, const uint32_t* pvb,
+                                           const typename Half<T>::Op8 (&ka)[NT][DP / 32],
+                                           const typename Half<T>::QOp (&qo)[DP / 32], int jt, int nkj, int nkk,
+                                           int g, int r16) {
+  using Hf = Half<T>;
+  using Op8 = typename Hf::Op8;
+  using L = Layout<T, DP, NT>;
+  constexpr int NCH = DP / 32;
+  const int j = jt * 16 + r16;
+  Op8 b1[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) b1[c] = Hf::mul(K1s + j * L::K1S + c * 32 + g * 8, qo[c]);
+  uint32_t pw[L::PW];
+  if constexpr (HAS_PV) {
+#pragma unroll
+    for (int w = 0; w < L::PW; ++w) pw[w] = pvb[j * L::PW + w];
+  }
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) {
+    mf_f32x4 sv = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) sv = Hf::mfma32(ka[kt][c], b1[c], sv);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int k = kt * 16 + 4 * g + r;
+      bool ok = j < nkj && k < nkk;
+      if constexpr (HAS_PV) ok = ok && ((pw[kt >> 1] >> ((kt & 1) * 16 + 4 * g + r)) & 1u);
+      if (ok) mloc = fmaxf(mloc, sv[r]);
+    }
+  }
+  return mloc;
+}
+
+// acc[nt] += sum over this j tile of V1 (.) (P V2), with P = 2^(S - m).
+// MASKED: explicit masking of padded j/k (required whenever m != 0).  Without
+// it, padded keys get P = 1 (their K2 rows are zero) but meet zero V2 rows and
+// a zero in `ones_edge`, the denominator operand of the last key pair.
+template <typename T, int DP, int NT, int NKT, bool HAS_PV, bool MASKED>
+__device__ __forceinline__ void jtile_acc(const typename Half<T>::K1T* K1s, const float* V1T, const uint32_t* pvb,
+                                          const typename Half<T>::Op8 (&ka)[NT][DP / 32],
+                                          const typename Half<T>::Op8 (&vb)[DP / 16][(NT + 1) / 2],
+                                          typename Half<T>::Op8 ones_full, typename Half<T>::Op8 ones_edge,
+                                          const typename Half<T>::QOp (&qo)[DP / 32], int jt, int nkj, int nkk,
+                                          float m, float (&acc)[DP / 16 + 1], int g, int r16) {
+  using Hf = Half<T>;
+  using Op8 = typename Hf::Op8;
+  using L = Layout<T, DP, NT>;
+  constexpr int NCH = DP / 32;
+  constexpr int ND = DP / 16;
+  constexpr int NPU = (NKT + 1) / 2;  // 32-key GEMM2 steps in use
+  const int j = jt * 16 + r16;
+  Op8 b1[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) b1[c] = Hf::mul(K1s + j * L::K1S + c * 32 + g * 8, qo[c]);
+  uint32_t pw[L::PW];
+  if constexpr (HAS_PV) {
+#pragma unroll
+    for (int w = 0; w < L::PW; ++w) pw[w] = pvb[j * L::PW + w];
+  }
+  // GEMM1 and P = 2^(S - m), packed straight into the GEMM2 A operands
+  uint32_t pa[NPU][4];
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) {
+    mf_f32x4 sv = mf_f32x4{-m, -m, -m, -m};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) sv = Hf::mfma32(ka[kt][c], b1[c], sv);
+    float pe[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float e = fast_exp2(sv[r]);
+      if constexpr (MASKED) {
+        const int k = kt * 16 + 4 * g + r;
+        e = (j < nkj && k < nkk) ? e : 0.0f;
+      }
+      if constexpr (HAS_PV) e = ((pw[kt >> 1] >> ((kt & 1) * 16 + 4 * g + r)) & 1u) ? e : 0.0f;
+      pe[r] = e;
+    }
+    pa[kt >> 1][(kt & 1) * 2 + 0] = Hf::pack(pe[0], pe[1]);
+    pa[kt >> 1][(kt & 1) * 2 + 1] = Hf::pack(pe[2], pe[3]);
+  }
+  if constexpr (NKT % 2 == 1) {
+    pa[NPU - 1][2] = 0u;
+    pa[NPU - 1][3] = 0u;
+  }
+  // GEMM2 (C2[j][d] = sum_k P[j][k] V2[k][d]) and the V1 epilogue
+#pragma unroll
+  for (int nt = 0; nt <= ND; ++nt) {
+    mf_f32x4 c2 = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int pr = 0; pr < NPU; ++pr) {
+      const Op8 a = __builtin_bit_cast(Op8, uint4{pa[pr][0], pa[pr][1], pa[pr][2], pa[pr][3]});
+      const Op8 bop = nt < ND ? vb[nt < ND ? nt : 0][pr] : (pr == NPU - 1 ? ones_edge : ones_full);
+      c2 = Hf::mfma32(a, bop, c2);
+    }
+    const float4 v1 = *reinterpret_cast<const float4*>(V1T + (nt * 16 + r16) * L::WS + jt * 16 + 4 * g);
+    acc[nt] += v1.x * c2[0] + v1.y * c2[1] + v1.z * c2[2] + v1.w * c2[3];
+  }
+}
+
+// Calls f(std::integral_constant<int, n>) for the runtime n in [1, NT].
+template <int NT, int I = 1, typename F>
+__device__ __forceinline__ void with_tiles(int n, F&& f) {
+  if constexpr (I <= NT) {
+    if (n == I) {
+      f(std::integral_constant<int, I>{});
+    } else {
+      with_tiles<NT, I + 1>(n, static_cast<F&&>(f));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// plan: one workgroup of kPlanThreads builds the workspace.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int plan_queries_per_item(int nk, int cls, int work_target) {
+  if (cls) return kWaves;
+  int qpi = max(kWaves, min(work_target / max(nk * nk, 1), kMaxQueriesPerItem));
+  return qpi - qpi % kWaves;
+}
+
+__global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p) {
+  __shared__ int s_nkq[kMaxBatch];
+  __shared__ unsigned long long s_key[kMaxBatch];  // class, cost (descending), molecule
+  __shared__ int s_items[kMaxBatch];                // items at each sorted position
+  __shared__ int s_off[kMaxBatch + 1];              // exclusive scan of s_items
+  __shared__ int s_wsum[kPlanThreads / 64];
+  __shared__ int s_nsmall;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int B = p.B, H = p.H, N = p.N;
+  const Workspace& ws = p.ws;
+
+  // 1. compacted key / query / padded-row lists, one wave per molecule; the
+  //    first 256 positions of 4 molecules are loaded before any is used
+  constexpr int kPlanWaves = kPlanThreads / 64;
+  for (int b0 = wave; b0 < B; b0 += 4 * kPlanWaves) {
+    uint8_t kv[4][4], qv[4][4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int b = b0 + m * kPlanWaves;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = u * 64 + lane;
+        const bool in = b < B && t < N;
+        kv[m][u] = in ? p.pkv[size_t(b) * N + t] : 0;
+        qv[m][u] = in ? p.qv[size_t(b) * N + t] : 0;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int b = b0 + m * kPlanWaves;
+      if (b >= B) break;
+      int ck = 0, cq = 0, cz = 0;
+      const unsigned long long below = (1ull << lane) - 1ull;
+      for (int base = 0; base < N; base += 256) {
+        uint8_t kk[4], qq[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (base == 0) {
+            kk[u] = kv[m][u];
+            qq[u] = qv[m][u];
+          } else {
+            const int t = base + u * 64 + lane;
+            kk[u] = t < N ? p.pkv[size_t(b) * N + t] : 0;
+            qq[u] = t < N ? p.qv[size_t(b) * N + t] : 0;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int t = base + u * 64 + lane;
+          const bool in = t < N;
+          const unsigned long long bk = __ballot(in && kk[u] != 0);
+          const unsigned long long bq = __ballot(in && qq[u] != 0);
+          const unsigned long long bz = __ballot(in && qq[u] == 0);
+          if (in && kk[u] != 0) ws.kidx[size_t(b) * N + ck + __popcll(bk & below)] = t;
+          if (in && qq[u] != 0) ws.qidx[size_t(b) * N + cq + __popcll(bq & below)] = t;
+          if (in && qq[u] == 0) ws.zidx[size_t(b) * N + cz + __popcll(bz & below)] = t;
+          ck += __popcll(bk);
+          cq += __popcll(bq);
+          cz += __popcll(bz);
+        }
+      }
+      if (lane == 0) {
+        s_nkq[b] = (ck << 16) | cq;
+        ws.nkq[b] = (ck << 16) | cq;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. sort molecules by (class, cost descending, index): bitonic over the
+  //    next power of two >= B keys, in one wave's registers when B <= 64
+  {
+    unsigned long long key = ~0ull;  // padding sorts last
+    if (tid < B) {
+      const int nk = s_nkq[tid] >> 16, nq = s_nkq[tid] & 0xffff;
+      const unsigned long long cls = nk > p.cap ? 1ull : 0ull;
+      const unsigned long long cost = (unsigned long long)nq * nk * nk;  // < 2^45
+      key = (cls << 62) | (((1ull << 46) - 1ull - cost) << 10) | (unsigned long long)tid;
+    }
+    int P = 1;
+    while (P < B) P <<= 1;
+    if (P <= 64) {
+      if (wave == 0) {
+        for (int k = 2; k <= 64; k <<= 1) {
+          for (int j = k >> 1; j > 0; j >>= 1) {
+            const unsigned long long y = __shfl_xor(key, j, 64);
+            const bool up = (lane & k) == 0;
+            const bool low = (lane & j) == 0;
+            key = (low == up) ? (key < y ? key : y) : (key > y ? key : y);
+          }
+        }
+        s_key[lane] = key;
+      }
+    } else {
+      s_key[tid] = key;
+      __syncthreads();
+      for (int k = 2; k <= P; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+          const int partner = tid ^ j;
+          if (tid < P && partner > tid) {
+            const unsigned long long x = s_key[tid], y = s_key[partner];
+            const bool up = (tid & k) == 0;
+            if ((x > y) == up) {
+              s_key[tid] = y;
+              s_key[partner] = x;
+            }
+          }
+          __syncthreads();
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // 3. items per sorted position, block-wide exclusive scan
+  int items = 0;
+  if (tid < B) {
+    const int b = int(s_key[tid] & 1023ull);
+    const int cls = int(s_key[tid] >> 62);
+    const int nk = s_nkq[b] >> 16, nq = s_nkq[b] & 0xffff;
+    const int qpi = plan_queries_per_item(nk, cls, p.work_target);
+    items = nq > 0 ? H * ((nq + qpi - 1) / qpi) : 0;
+    if (cls == 0 && (tid == B - 1 || (s_key[tid + 1] >> 62) != 0)) s_nsmall = tid + 1;
+    if (cls == 1 && tid == 0) s_nsmall = 0;
+  }
+  s_items[tid] = items;
+  int x = items;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_wsum[wave] = x;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int w = 0; w < kPlanThreads / 64; ++w) {
+      const int v = s_wsum[w];
+      s_wsum[w] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  s_off[tid] = s_wsum[wave] + x - items;
+  if (tid == kPlanThreads - 1) s_off[kPlanThreads] = s_wsum[wave] + x;
+  __syncthreads();
+  const int nsmall = B > 0 ? s_nsmall : 0;
+  const int small_total = s_off[nsmall];
+  const int large_total = s_off[B] - small_total;
+  if (tid == 0) {
+    ws.hdr[0] = small_total;
+    ws.hdr[1] = large_total;
+  }
+
+  // 4. items: one molecule's items are contiguous, heads interleaved with its
+  //    query ranges; small items first (in cost order), then large ones
+  for (int u = tid; u < s_off[B]; u += kPlanThreads) {
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_off[mid] <= u) lo = mid; else hi = mid - 1;
+    }
+    const int b = int(s_key[lo] & 1023ull);
+    const int cls = int(s_key[lo] >> 62);
+    const int nk = s_nkq[b] >> 16, nq = s_nkq[b] & 0xffff;
+    const int qpi = plan_queries_per_item(nk, cls, p.work_target);
+    const int local = u - s_off[lo];
+    const int s = local / H, h = local - s * H;
+    const int4 item{b, h, (s * qpi) | (min(nq, (s + 1) * qpi) << 16), nk};
+    if (cls == 0) ws.small_items[u] = item;
+    else ws.large_items[u - small_total] = item;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// small / large kernels
+// ---------------------------------------------------------------------------
+__device__ __noinline__ void load8_slow(const void* row, int e0, int D, int esize, void* dst) {
+  const unsigned char* s = static_cast<const unsigned char*>(row);
+  unsigned char* d = static_cast<unsigned char*>(dst);
+  for (int e = 0; e < 8; ++e)
+    for (int byte = 0; byte < esize; ++byte)
+      d[e * esize + byte] = (e0 + e < D) ? s[(e0 + e) * esize + byte] : 0;
+}
+
+// Copy 8 elements [e0, e0+8) of a row of length D into registers, zero past D.
+template <typename T>
+__device__ __forceinline__ typename Half<T>::Op8 load8(const T* row, int e0, int D, bool vec) {
+  typename Half<T>::Op8 v;
+  if (vec && e0 + 8 <= D) {
+    v = *reinterpret_cast<const typename Half<T>::Op8*>(row + e0);
+  } else if (e0 >= D) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = T(0.0f);
+  } else {
+    load8_slow(row, e0, D, int(sizeof(T)), &v);
+  }
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ typename Half<T>::Op8 zero8() {
+  typename Half<T>::Op8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = T(0.0f);
+  return v;
+}
+
+template <typename T, int DP, int NT, bool HAS_PV, bool LARGE>
+__global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) {
+  using Hf = Half<T>;
+  using Op8 = typename Hf::Op8;
+  using Op4 = typename Hf::Op4;
+  using QOp = typename Hf::QOp;
+  using K1T = typename Hf::K1T;
+  using L = Layout<T, DP, NT>;
+  constexpr int CH = L::CH;
+  constexpr int KS = L::KS;
+  constexpr int VS = L::VS;
+  constexpr int WS = L::WS;
+  constexpr int PW = L::PW;
+  constexpr int NCH = DP / 32;        // 32-wide d chunks (GEMM1 K steps)
+  constexpr int ND = DP / 16;         // 16-wide d tiles of GEMM2
+  constexpr int NN = ND + 1;          // + the validity (denominator) tile
+  constexpr int NPR = (NT + 1) / 2;   // 32-key K steps of GEMM2
+  constexpr int CPR = DP / 8;         // 8-element chunks per padded row
+  constexpr int RPP = kThreads / CPR; // rows per staging pass
+  constexpr int RPT = (CH + RPP - 1) / RPP;
+  constexpr int QPT = (kMaxQueriesPerItem + RPP - 1) / RPP;
+  static_assert(kThreads % CPR == 0, "a thread's 8-column chunk must be fixed across rows");
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  K1T* K1s = reinterpret_cast<K1T*>(smem + L::kK1);
+  T* V2T = reinterpret_cast<T*>(smem + L::kV2T);
+  float* V1T = reinterpret_cast<float*>(smem + L::kV1T);
+  using QT = typename Hf::QT;
+  QT* Qs = reinterpret_cast<QT*>(smem + L::kQs);
+  uint32_t* pvb = reinterpret_cast<uint32_t*>(smem + L::kPV);
+  float* ab = reinterpret_cast<float*>(smem + L::kAB);
+  float* m2s = reinterpret_cast<float*>(smem + L::kM2);
+  float* red = reinterpret_cast<float*>(smem + L::kRed);
+  const int H = p.H, N = p.N, D = p.D;
+  const Workspace& ws = p.ws;
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+  const bool vec = p.vec_ok != 0;
+  const T* gq = static_cast<const T*>(p.q);
+  const T* gk1 = static_cast<const T*>(p.k1);
+  const T* gk2 = static_cast<const T*>(p.k2);
+  const T* gv1 = static_cast<const T*>(p.v1);
+  const T* gv2 = static_cast<const T*>(p.v2);
+
+  // XCD-aware logical workgroup id: blockIdx.x % 8 is the XCD, so give each
+  // XCD a contiguous range of logical ids (gridDim.x is a multiple of 8).
+  const int G = gridDim.x;
+  const int wg = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+
+  // Staging helpers -----------------------------------------------------------
+  // K1s rows and V1T columns for compacted keys [j0, j0 + CH) (nkj valid),
+  // V2T columns for keys [k0, k0 + CH) (nkk valid) when with_v; the column
+  // maxima of |K1| go to red[] when with_max.
+  auto stage_chunk = [&](const int* kidx, int bh, int j0, int nkj, int k0, int nkk, bool with_v, bool with_max) {
+    const int c = tid % CPR;
+    const int e0 = c * 8;
+    Op8 a[RPT], v1v[RPT], v2v[RPT];
+#pragma unroll
+    for (int t = 0; t < RPT; ++t) {
+      const int r = tid / CPR + t * RPP;
+      a[t] = zero8<T>();
+      v1v[t] = zero8<T>();
+      v2v[t] = zero8<T>();
+      if (r < nkj) {
+        const size_t src = (size_t(bh) * N + kidx[j0 + r]) * D;
+        a[t] = load8<T>(gk1 + src, e0, D, vec);
+        if (with_v) v1v[t] = load8<T>(gv1 + src, e0, D, vec);
+      }
+      if (with_v && r < nkk) v2v[t] = load8<T>(gv2 + (size_t(bh) * N + kidx[k0 + r]) * D, e0, D, vec);
+    }
+    float m1[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m1[e] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < RPT; ++t) {
+      const int r = tid / CPR + t * RPP;
+      if (r < CH) {
+        Hf::store_k1(K1s + r * L::K1S + e0, a[t]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m1[e] = fmaxf(m1[e], fabsf(float(a[t][e])));
+        if (with_v) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            V2T[(e0 + e) * VS + r] = v2v[t][e];
+            V1T[(e0 + e) * WS + r] = float(v1v[t][e]);
+          }
+        }
+      }
+    }
+    if (with_v) {
+      // validity row (DP) and zero rows DP+1 .. DP+15 of V1T
+      for (int u = tid; u < 16 * CH; u += kThreads) {
+        const int rr = u / CH, col = u - rr * CH;
+        V1T[(DP + rr) * WS + col] = (rr == 0 && col < nkj) ? 1.0f : 0.0f;
+      }
+    }
+    if (with_max) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+#pragma unroll
+        for (int off = CPR; off < 64; off <<= 1) m1[e] = fmaxf(m1[e], __shfl_xor(m1[e], off, 64));
+      }
+      if (lane < CPR) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[wave * DP + e0 + e] = m1[e];
+      }
+    }
+  };
+  // pair-valid bits of the (j chunk, k chunk) block
+  auto stage_pv = [&](const int* kidx, int b, int j0, int nkj, int k0, int nkk) {
+    if constexpr (HAS_PV) {
+      const uint8_t* gpv = p.pv + size_t(b) * N * N;
+      for (int u = tid; u < CH * PW; u += kThreads) {
+        const int jl = u / PW, w = u - jl * PW;
+        uint32_t bits = 0;
+        if (jl < nkj) {
+          const uint8_t* prow = gpv + size_t(kidx[j0 + jl]) * N;
+          for (int t = 0; t < 32; ++t) {
+            const int kl = w * 32 + t;
+            if (kl < nkk && prow[kidx[k0 + kl]] != 0) bits |= 1u << t;
+          }
+        }
+        pvb[u] = bits;
+      }
+    }
+  };
+  // K2 rows [k0, k0 + nkk) of the compacted list as GEMM1 A operands
+  auto load_ka = [&](Op8 (&ka)[NT][NCH], const int* kidx, int bh, int k0, int nkk) {
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      const int r = kt * 16 + r16;
+      const int row = r < nkk ? kidx[k0 + r] : 0;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        Op8 v = zero8<T>();
+        if (r < nkk) v = load8<T>(gk2 + (size_t(bh) * N + row) * D, c * 32 + g * 8, D, vec);
+        ka[kt][c] = v;
+      }
+    }
+  };
+  // GEMM2 B operands: V2 columns d from V2T
+  auto load_vb = [&](Op8 (&vb)[ND][NPR]) {
+#pragma unroll
+    for (int nt = 0; nt < ND; ++nt) {
+#pragma unroll
+      for (int pr = 0; pr < NPR; ++pr) {
+        const T* vr = V2T + (nt * 16 + r16) * VS + 32 * pr + 4 * g;
+        const Op4 lo4 = *reinterpret_cast<const Op4*>(vr);
+        Op4 hi4;
+        if (2 * pr + 1 < NT) {
+          hi4 = *reinterpret_cast<const Op4*>(vr + 16);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) hi4[e] = T(0.0f);
+        }
+        vb[nt][pr] = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    }
+  };
+  // GEMM2 B operands of the denominator column: 1 in column 0 for full key
+  // pairs; for the last pair of a chunk, 1 only at valid keys
+  Op8 ones_full;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones_full[e] = T(r16 == 0 ? 1.0f : 0.0f);
+  auto make_ones_edge = [&](int nkk) {
+    const int last = (ceil_div(nkk, 16) - 1) >> 1;
+    Op8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int k = 32 * last + (e < 4 ? 0 : 16) + 4 * g + (e & 3);
+      v[e] = T((r16 == 0 && k < nkk) ? 1.0f : 0.0f);
+    }
+    return v;
+  };
+  auto write_row = [&](size_t row_off, float (&acc)[NN], float m) {
+#pragma unroll
+    for (int nt = 0; nt < NN; ++nt) {
+      acc[nt] += __shfl_xor(acc[nt], 16, 64);
+      acc[nt] += __shfl_xor(acc[nt], 32, 64);
+    }
+    const float lsum = __shfl(acc[ND], 0, 64);
+    const bool has_mass = lsum > 0.0f;
+    const float inv = has_mass ? 1.0f / lsum : 0.0f;
+#pragma unroll
+    for (int nt = 0; nt < ND; ++nt) {
+      if ((nt & 3) != g) continue;
+      const int d = nt * 16 + r16;
+      if (d < D) {
+        const float o = acc[nt] * inv;
+        if (p.out) static_cast<T*>(p.out)[row_off * D + d] = T(o);
+        if (p.out_f32) p.out_f32[row_off * D + d] = o;
+      }
+    }
+    if (lane == 0 && p.lse) p.lse[row_off] = has_mass ? (m + __log2f(lsum)) * kLn2 : 0.0f;
+  };
+
+  if constexpr (!LARGE) {
+    const int n_items = ws.hdr[0];
+    int4 nxt = wg < n_items ? ws.small_items[wg] : int4{0, 0, 0, 0};
+    for (int item = wg; item < n_items; item += G) {
+      const int4 it = nxt;
+      if (item + G < n_items) nxt = ws.small_items[item + G];  // next header, one item ahead
+      const int b = it.x, h = it.y, q0 = it.z & 0xffff, q1 = it.z >> 16, nk = it.w;
+      const int bh = b * H + h;
+      const int* kidx = ws.kidx + size_t(b) * N;
+      const int* qidx = ws.qidx + size_t(b) * N;
+
+      // ---- stage: one round of index loads, then one round of data loads ----
+      const int c8 = (tid % CPR) * 8;
+      int jrow[RPT], qrow[QPT], krow[NT];
+#pragma unroll
+      for (int t = 0; t < RPT; ++t) {
+        const int r = tid / CPR + t * RPP;
+        jrow[t] = r < nk ? kidx[r] : -1;
+      }
+#pragma unroll
+      for (int t = 0; t < QPT; ++t) {
+        const int r = tid / CPR + t * RPP;
+        qrow[t] = r < q1 - q0 ? qidx[q0 + r] : -1;
+      }
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        const int r = kt * 16 + r16;
+        krow[kt] = r < nk ? kidx[r] : -1;
+      }
+      Op8 a[RPT], v1v[RPT], v2v[RPT], qv8[QPT];
+      Op8 ka[NT][NCH];
+#pragma unroll
+      for (int t = 0; t < RPT; ++t) {
+        a[t] = zero8<T>();
+        v1v[t] = zero8<T>();
+        v2v[t] = zero8<T>();
+        if (jrow[t] >= 0) {
+          const size_t src = (size_t(bh) * N + jrow[t]) * D;
+          a[t] = load8<T>(gk1 + src, c8, D, vec);
+          v1v[t] = load8<T>(gv1 + src, c8, D, vec);
+          v2v[t] = load8<T>(gv2 + src, c8, D, vec);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < QPT; ++t)
+        qv8[t] = qrow[t] >= 0 ? load8<T>(gq + (size_t(bh) * N + qrow[t]) * D, c8, D, vec) : zero8<T>();
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          ka[kt][c] = krow[kt] >= 0 ? load8<T>(gk2 + (size_t(bh) * N + krow[kt]) * D, c * 32 + g * 8, D, vec)
+                                    : zero8<T>();
+
+      // LDS: query rows, K1 (and its column maxima), V2 transposed, V1 transposed
+#pragma unroll
+      for (int t = 0; t < QPT; ++t) {
+        const int r = tid / CPR + t * RPP;
+        if (r < q1 - q0) Hf::store_q(Qs + r * KS + c8, qv8[t]);
+      }
+      {
+        float m1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m1[e] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < RPT; ++t) {
+          const int r = tid / CPR + t * RPP;
+          if (r < CH) {
+            Hf::store_k1(K1s + r * L::K1S + c8, a[t]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              m1[e] = fmaxf(m1[e], fabsf(float(a[t][e])));
+              V2T[(c8 + e) * VS + r] = v2v[t][e];
+              V1T[(c8 + e) * WS + r] = float(v1v[t][e]);
+            }
+          }
+        }
+        for (int u = tid; u < 16 * CH; u += kThreads) {
+          const int rr = u / CH, col = u - rr * CH;
+          V1T[(DP + rr) * WS + col] = (rr == 0 && col < nk) ? 1.0f : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+#pragma unroll
+          for (int off = CPR; off < 64; off <<= 1) m1[e] = fmaxf(m1[e], __shfl_xor(m1[e], off, 64));
+        }
+        if (lane < CPR) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) red[wave * DP + c8 + e] = m1[e];
+        }
+      }
+      stage_pv(kidx, b, 0, nk, 0, nk);
+      // column maxima of |K2| from the registers (every wave holds all of K2;
+      // wave w reduces the elements e with e % kWaves == w): over kt, then r16
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (e % kWaves != wave) continue;
+          float mx = 0.0f;
+#pragma unroll
+          for (int kt = 0; kt < NT; ++kt) mx = fmaxf(mx, fabsf(float(ka[kt][c][e])));
+#pragma unroll
+          for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+          if (r16 == 0) m2s[c * 32 + g * 8 + e] = mx;
+        }
+      }
+      __syncthreads();
+      if (tid < DP) {
+        float a0 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) a0 = fmaxf(a0, red[w * DP + tid]);
+        ab[tid] = a0 * m2s[tid];
+      }
+      __syncthreads();
+      Op8 vb[ND][NPR];
+      load_vb(vb);
+      const Op8 ones_edge = make_ones_edge(nk);
+      const int njt = ceil_div(nk, 16);
+
+      if (njt == 0) {
+        // valid queries of a molecule without keys: zero rows, lse 0
+        for (int qs = q0 + wave; qs < q1; qs += kWaves) {
+          float acc[NN];
+#pragma unroll
+          for (int nt = 0; nt < NN; ++nt) acc[nt] = 0.0f;
+          write_row(size_t(bh) * N + qidx[qs], acc, 0.0f);
+        }
+      }
+      with_tiles<NT>(njt, [&](auto tiles) {
+        constexpr int NKT = decltype(tiles)::value;
+        for (int qs = q0 + wave; qs < q1; qs += kWaves) {
+          const size_t row_off = size_t(bh) * N + qidx[qs];
+          QOp qo[NCH];
+          float ubound = 0.0f;
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+            Hf::load_q(Qs + (qs - q0) * KS + c * 32 + g * 8, qo[c]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ubound += Hf::qabs(qo[c], e) * ab[c * 32 + g * 8 + e];
+          }
+          ubound += __shfl_xor(ubound, 16, 64);
+          ubound += __shfl_xor(ubound, 32, 64);
+          const bool fast =
+              __builtin_amdgcn_readfirstlane(__float_as_int(ubound)) <= __float_as_int(p.bound_limit);
+          float acc[NN];
+#pragma unroll
+          for (int nt = 0; nt < NN; ++nt) acc[nt] = 0.0f;
+          float m = 0.0f;
+          if (fast) {
+#pragma unroll 1
+            for (int jt = 0; jt < NKT; ++jt)
+              jtile_acc<T, DP, NT, NKT, HAS_PV, false>(K1s, V1T, pvb, ka, vb, ones_full, ones_edge, qo, jt, nk, nk,
+                                                       0.0f, acc, g, r16);
+          } else {
+            float mloc = -INFINITY;
+#pragma unroll 1
+            for (int jt = 0; jt < NKT; ++jt)
+              mloc = fmaxf(mloc, jtile_max<T, DP, NT, NKT, HAS_PV>(K1s, pvb, ka, qo, jt, nk, nk, g, r16));
+            m = wave_max(mloc);
+            if (m != -INFINITY) {
+#pragma unroll 1
+              for (int jt = 0; jt < NKT; ++jt)
+                jtile_acc<T, DP, NT, NKT, HAS_PV, true>(K1s, V1T, pvb, ka, vb, ones_full, ones_edge, qo, jt, nk, nk,
+                                                        m, acc, g, r16);
+            }
+          }
+          write_row(row_off, acc, m);
+        }
+      });
+      __syncthreads();
+    }
+
+    // ---- zero the rows of padded queries: 16-byte chunks of the whole output,
+    //      the validity bytes of 8 chunks are loaded before any is tested ----
+    const int rowbytes = D * int(sizeof(T));
+    const bool vec_out = vec && (rowbytes % 16 == 0);
+    const int per_row = vec_out ? rowbytes / 16 : D;
+    const long long total = (long long)p.B * H * N * per_row;
+    constexpr int kZ = 8;
+    for (long long base = (long long)wg * kThreads + tid; base < total; base += (long long)G * kThreads * kZ) {
+      long long row[kZ];
+      int col[kZ];
+      uint8_t valid[kZ];
+#pragma unroll
+      for (int z = 0; z < kZ; ++z) {
+        const long long idx = base + (long long)z * G * kThreads;
+        row[z] = idx / per_row;
+        col[z] = int(idx - row[z] * per_row);
+        const long long bh = row[z] / N;
+        const int i = int(row[z] - bh * N);
+        valid[z] = idx < total ? p.qv[(bh / H) * N + i] : 1;
+      }
+#pragma unroll
+      for (int z = 0; z < kZ; ++z) {
+        if (valid[z]) continue;
+        const int c = col[z];
+        if (vec_out) {
+          if (p.out) reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row[z] * D)[c] = uint4{0u, 0u, 0u, 0u};
+          if (p.out_f32) {
+            float4* o = reinterpret_cast<float4*>(p.out_f32 + row[z] * D);
+            o[2 * c] = float4{0.f, 0.f, 0.f, 0.f};
+            o[2 * c + 1] = float4{0.f, 0.f, 0.f, 0.f};
+          }
+        } else {
+          if (p.out) static_cast<T*>(p.out)[row[z] * D + c] = T(0.0f);
+          if (p.out_f32) p.out_f32[row[z] * D + c] = 0.0f;
+        }
+        if (c == 0 && p.lse) p.lse[row[z]] = 0.0f;
+      }
+    }
+  } else {
+    // ---- molecules larger than one chunk: one query per wave, chunk pairs ----
+    const int n_items = ws.hdr[1];
+    for (int item = wg; item < n_items; item += G) {
+      const int4 it = ws.large_items[item];
+      const int b = it.x, h = it.y, q0 = it.z & 0xffff, q1 = it.z >> 16, nk = it.w;
+      const int bh = b * H + h;
+      const int* kidx = ws.kidx + size_t(b) * N;
+      const int qs = q0 + wave;
+      const bool has_q = qs < q1;
+      const size_t row_off = size_t(bh) * N + (has_q ? ws.qidx[size_t(b) * N + qs] : 0);
+      QOp qo[NCH];
+      if (has_q) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) Hf::prepare(load8<T>(gq + row_off * D, c * 32 + g * 8, D, vec), qo[c]);
+      }
+      const int nch = ceil_div(nk, CH);
+      float acc[NN];
+#pragma unroll
+      for (int nt = 0; nt < NN; ++nt) acc[nt] = 0.0f;
+      float mloc = -INFINITY;
+      float m = -INFINITY;
+      for (int sweep = 0; sweep < 2; ++sweep) {
+        for (int jc = 0; jc < nch; ++jc) {
+          const int j0 = jc * CH, nkj = min(CH, nk - j0);
+          for (int kc = 0; kc < nch; ++kc) {
+            const int k0 = kc * CH, nkk = min(CH, nk - k0);
+            stage_chunk(kidx, bh, j0, nkj, k0, nkk, sweep == 1, false);
+            stage_pv(kidx, b, j0, nkj, k0, nkk);
+            Op8 ka[NT][NCH];
+            load_ka(ka, kidx, bh, k0, nkk);
+            __syncthreads();
+            const int njt = ceil_div(nkj, 16);
+            if (sweep == 0) {
+              if (has_q)
+                for (int jt = 0; jt < njt; ++jt)
+                  mloc = fmaxf(mloc, jtile_max<T, DP, NT, NT, HAS_PV>(K1s, pvb, ka, qo, jt, nkj, nkk, g, r16));
+            } else {
+              Op8 vb[ND][NPR];
+              load_vb(vb);
+              const Op8 ones_edge = make_ones_edge(NT * 16);
+              if (has_q && m != -INFINITY)
+                for (int jt = 0; jt < njt; ++jt)
+                  jtile_acc<T, DP, NT, NT, HAS_PV, true>(K1s, V1T, pvb, ka, vb, ones_full, ones_edge, qo, jt, nkj,
+                                                         nkk, m, acc, g, r16);
+            }
+            __syncthreads();
+          }
+        }
+        if (sweep == 0) m = wave_max(mloc);
+      }
+      if (has_q) write_row(row_off, acc, m == -INFINITY ? 0.0f : m);
+    }
+  }
+}
+
+template <typename T, int DP, int NT, bool HAS_PV, bool LARGE>
+int launch_main(const Params& prm, int grid, hipStream_t stream) {
+  auto kern = simplicial_fast_kernel<T, DP, NT, HAS_PV, LARGE>;
+  const size_t lds = Layout<T, DP, NT>::kFixed;
+  static bool attr_set = false;  // per instantiation
+  if (!attr_set) {
+    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, prm);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
+
+template <typename T, int DP, int NT, bool HAS_PV>
+int launch_all(const Params& prm, int num_cus, hipStream_t stream) {
+  hipLaunchKernelGGL(simplicial_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, prm);
+  MF_HIP_CHECK(hipGetLastError());
+  const int grid = num_cus * 2;  // a multiple of 8 (the XCD count)
+  int st = launch_main<T, DP, NT, HAS_PV, false>(prm, grid, stream);
+  if (st != MF_OK || prm.N <= prm.cap) return st;
+  return launch_main<T, DP, NT, HAS_PV, true>(prm, grid, stream);
+}
+
+}  // namespace sfast
+
+// Key capacity of one chunk of the fast kernels for a head dim, or 0 when
+// they do not serve this head dim.
+int simplicial_fast_capacity(int head_dim) {
+  if (head_dim <= 32) return 16 * 6;
+  if (head_dim <= 64) return 16 * 5;
+  return 0;
+}
+
+size_t simplicial_fast_workspace_bytes(int batch, int heads, int tokens) {
+  const int b = std::min(batch, sfast::kMaxBatch);
+  return sfast::workspace_bytes(b, heads, tokens);
+}
+
+// One set of launches over a[0..batch), batch <= sfast::kMaxBatch.
+int simplicial_fast_launch(const mf_simplicial_fwd_args* a, void* workspace, int num_cus, hipStream_t stream) {
+  using namespace sfast;
+  if (a->batch > kMaxBatch) return fail(MF_ERR_INVALID_ARGUMENT, "simplicial fast launch: batch slice too large");
+  Params prm{};
+  prm.q = a->q; prm.k1 = a->k1; prm.v1 = a->v1; prm.k2 = a->k2; prm.v2 = a->v2;
+  prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
+  prm.out = a->out; prm.out_f32 = a->out_f32; prm.lse = a->lse;
+  prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
+  prm.ws = carve_workspace(workspace, a->batch, a->heads, a->tokens);
+  prm.cap = simplicial_fast_capacity(a->head_dim);
+  prm.work_target = 48 * 1024;
+  prm.bound_limit = a->dtype == MF_DTYPE_BF16 ? 60.0f : 14.0f;
+  bool vec = (a->head_dim * 2) % 16 == 0;
+  for (const void* ptr : {a->q, a->k1, a->v1, a->k2, a->v2, static_cast<const void*>(a->out)})
+    vec = vec && (reinterpret_cast<uintptr_t>(ptr) % 16 == 0);
+  if (a->out_f32) vec = vec && (reinterpret_cast<uintptr_t>(a->out_f32) % 16 == 0);
+  prm.vec_ok = vec ? 1 : 0;
+  const bool pv = a->pair_valid != nullptr;
+  const bool bf = a->dtype == MF_DTYPE_BF16;
+  if (a->head_dim <= 32) {
+    if (bf) return pv ? launch_all<__bf16, 32, 6, true>(prm, num_cus, stream) : launch_all<__bf16, 32, 6, false>(prm, num_cus, stream);
+    return pv ? launch_all<_Float16, 32, 6, true>(prm, num_cus, stream) : launch_all<_Float16, 32, 6, false>(prm, num_cus, stream);
+  }
+  if (bf) return pv ? launch_all<__bf16, 64, 5, true>(prm, num_cus, stream) : launch_all<__bf16, 64, 5, false>(prm, num_cus, stream);
+  return pv ? launch_all<_Float16, 64, 5, true>(prm, num_cus, stream) : launch_all<_Float16, 64, 5, false>(prm, num_cus, stream);
+}
+
+}  // namespace mf

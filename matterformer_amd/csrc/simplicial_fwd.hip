@@ -53,6 +53,8 @@ struct Params {
   int NP;           // LDS row capacity: N rounded up to 32
   int work_target;  // target query * key^2 units per work item
   int vec_ok;       // rows are 16-byte aligned and D*sizeof(T) % 16 == 0
+  int min_keys;     // only molecules with more keys than this are processed
+  int zero_rows;    // write the zero rows of invalid queries
 };
 
 // LDS geometry shared by host (sizing) and device (carving).
@@ -151,7 +153,7 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
       if (b < B) {
         const int v = nkq[b];
         const int nk = v >> 16, nq = v & 0xffff;
-        if (nq > 0) cnt = H * ceil_div(nq, queries_per_item(nk, p.work_target));
+        if (nq > 0 && nk > p.min_keys) cnt = H * ceil_div(nq, queries_per_item(nk, p.work_target));
       }
       int x = cnt;
 #pragma unroll
@@ -166,7 +168,7 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
   }
 
   // ---- 3. zero rows of invalid queries (grid-stride) ----
-  {
+  if (p.zero_rows) {
     const int CPR = ceil_div(D, 4);  // 4-element chunks per row
     const long long rows = (long long)B * H * N;
     const long long total = rows * CPR;
@@ -540,29 +542,27 @@ static int check_shape(int B, int H, int N, int D, int dtype, bool has_pv, size_
 using namespace mf;
 using namespace mf::simplicial;
 
+static bool uses_fast(int32_t head_dim, int32_t dtype) {
+  return dtype != MF_DTYPE_F32 && simplicial_fast_capacity(head_dim) > 0;
+}
+
 extern "C" int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
                                            int32_t dtype) {
+  if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: batch, heads, tokens and head_dim must be positive");
+  if (tokens > 32767) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports tokens <= 32767");
+  if (uses_fast(head_dim, dtype)) return MF_OK;
   return check_shape(batch, heads, tokens, head_dim, dtype, /*has_pv=*/true, nullptr);
 }
 
-extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) {
-  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: args is NULL");
-  if (!a->q || !a->k1 || !a->v1 || !a->k2 || !a->v2)
-    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: q, k1, v1, k2 and v2 must be non-NULL");
-  if (!a->query_valid || !a->pair_key_valid)
-    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: query_valid and pair_key_valid must be non-NULL");
-  if (!a->out && !a->out_f32 && !a->lse)
-    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: at least one of out, out_f32, lse must be non-NULL");
-  if (a->precision < MF_PREC_BF16_TC || a->precision > MF_PREC_IEEE_FP32)
-    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: unknown precision " + std::to_string(a->precision));
-  const bool has_pv = a->pair_valid != nullptr;
-  size_t lds = 0;
-  int st = check_shape(a->batch, a->heads, a->tokens, a->head_dim, a->dtype, has_pv, &lds);
-  if (st != MF_OK) return st;
-  DeviceInfo dev;
-  st = device_info(&dev);
-  if (st != MF_OK) return st;
+extern "C" uint64_t mf_simplicial_fwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens,
+                                                     int32_t head_dim, int32_t dtype) {
+  if (batch <= 0 || heads <= 0 || tokens <= 0 || !uses_fast(head_dim, dtype)) return 0;
+  return simplicial_fast_workspace_bytes(batch, heads, tokens);
+}
 
+static int launch_general(const mf_simplicial_fwd_args* a, size_t lds, int num_cus, int min_keys, bool zero_rows,
+                          hipStream_t s) {
   Params prm{};
   prm.q = a->q; prm.k1 = a->k1; prm.v1 = a->v1; prm.k2 = a->k2; prm.v2 = a->v2;
   prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
@@ -570,6 +570,8 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
   prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
   prm.NP = (a->tokens + 31) / 32 * 32;
   prm.work_target = 16 * 48 * 48;
+  prm.min_keys = min_keys;
+  prm.zero_rows = zero_rows ? 1 : 0;
   const size_t esize = a->dtype == MF_DTYPE_F32 ? 4 : 2;
   bool vec = (size_t(a->head_dim) * esize) % 16 == 0;
   for (const void* ptr : {a->q, a->k1, a->v1, a->k2, a->v2})
@@ -577,9 +579,8 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
   prm.vec_ok = vec ? 1 : 0;
 
   const int per_cu = std::max(1, int((160 * 1024) / std::max<size_t>(lds, 1)));
-  const int grid = dev.num_cus * std::min(per_cu, 2);
+  const int grid = num_cus * std::min(per_cu, 2);
   const int DP = padded_head_dim(a->head_dim);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (a->dtype == MF_DTYPE_BF16) {
     if (DP == 32) return launch<__bf16, 32>(prm, lds, grid, s);
     if (DP == 64) return launch<__bf16, 64>(prm, lds, grid, s);
@@ -593,4 +594,64 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
   if (DP == 32) return launch<float, 32>(prm, lds, grid, s);
   if (DP == 64) return launch<float, 64>(prm, lds, grid, s);
   return launch<float, 128>(prm, lds, grid, s);
+}
+
+extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) {
+  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: args is NULL");
+  if (!a->q || !a->k1 || !a->v1 || !a->k2 || !a->v2)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: q, k1, v1, k2 and v2 must be non-NULL");
+  if (!a->query_valid || !a->pair_key_valid)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: query_valid and pair_key_valid must be non-NULL");
+  if (!a->out && !a->out_f32 && !a->lse)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: at least one of out, out_f32, lse must be non-NULL");
+  if (a->precision < MF_PREC_BF16_TC || a->precision > MF_PREC_IEEE_FP32)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: unknown precision " + std::to_string(a->precision));
+  if (a->batch <= 0 || a->heads <= 0 || a->tokens <= 0 || a->head_dim <= 0)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: batch, heads, tokens and head_dim must be positive");
+  if (a->dtype != MF_DTYPE_F32 && a->dtype != MF_DTYPE_F16 && a->dtype != MF_DTYPE_BF16)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: unknown dtype " + std::to_string(a->dtype));
+  const bool has_pv = a->pair_valid != nullptr;
+  DeviceInfo dev;
+  int st = device_info(&dev);
+  if (st != MF_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  // 16-bit operands with head_dim <= 64: the register-resident kernels, one
+  // set of launches per slice of at most kSimplicialFastMaxBatch molecules
+  // (the slices reuse the workspace in stream order).
+  size_t lds = 0;
+  if (uses_fast(a->head_dim, a->dtype)) {
+    if (a->tokens > 32767) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports tokens <= 32767");
+    const uint64_t need = simplicial_fast_workspace_bytes(a->batch, a->heads, a->tokens);
+    if (a->workspace == nullptr || a->workspace_bytes < need)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: workspace of " + std::to_string(need) +
+                                               " bytes required (mf_simplicial_fwd_workspace_size), got " +
+                                               std::to_string(a->workspace_bytes));
+    if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: workspace must be 16-byte aligned");
+    const size_t esize = 2;
+    for (int b0 = 0; b0 < a->batch; b0 += kSimplicialFastMaxBatch) {
+      mf_simplicial_fwd_args sub = *a;
+      const size_t row = size_t(a->heads) * a->tokens;
+      const size_t elem = row * a->head_dim * esize;
+      sub.batch = std::min(kSimplicialFastMaxBatch, a->batch - b0);
+      sub.q = static_cast<const char*>(a->q) + b0 * elem;
+      sub.k1 = static_cast<const char*>(a->k1) + b0 * elem;
+      sub.v1 = static_cast<const char*>(a->v1) + b0 * elem;
+      sub.k2 = static_cast<const char*>(a->k2) + b0 * elem;
+      sub.v2 = static_cast<const char*>(a->v2) + b0 * elem;
+      sub.query_valid = a->query_valid + size_t(b0) * a->tokens;
+      sub.pair_key_valid = a->pair_key_valid + size_t(b0) * a->tokens;
+      if (a->pair_valid) sub.pair_valid = a->pair_valid + size_t(b0) * a->tokens * a->tokens;
+      if (a->out) sub.out = static_cast<char*>(a->out) + b0 * elem;
+      if (a->out_f32) sub.out_f32 = a->out_f32 + b0 * row * a->head_dim;
+      if (a->lse) sub.lse = a->lse + b0 * row;
+      st = simplicial_fast_launch(&sub, a->workspace, dev.num_cus, s);
+      if (st != MF_OK) return st;
+    }
+    return MF_OK;
+  }
+  st = check_shape(a->batch, a->heads, a->tokens, a->head_dim, a->dtype, has_pv, &lds);
+  if (st != MF_OK) return st;
+  return launch_general(a, lds, dev.num_cus, 0, /*zero_rows=*/true, s);
 }

@@ -148,6 +148,9 @@ def hip_simplicial_attention_forward(
         out_f32 = torch.empty((B, H, N, D), device=q.device, dtype=torch.float32)
     lse = torch.empty((B, H, N), device=q.device, dtype=torch.float32) if need_backward_state else None
 
+    lib = _native.lib()
+    ws_bytes = lib.mf_simplicial_fwd_workspace_size(B, H, N, D, _native.dtype_code(cdt))
+    ws = _native.workspace(ws_bytes, q.device)
     args = _native.MfSimplicialFwdArgs(
         q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(),
         k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
@@ -156,10 +159,10 @@ def hip_simplicial_attention_forward(
         out=None if out is None else out.data_ptr(),
         out_f32=None if out_f32 is None else out_f32.data_ptr(),
         lse=None if lse is None else lse.data_ptr(),
+        workspace=None if ws is None else ws.data_ptr(), workspace_bytes=ws_bytes,
         batch=B, heads=H, tokens=N, head_dim=D,
         dtype=_native.dtype_code(cdt), precision=_native.MF_PREC[precision],
     )
-    lib = _native.lib()
     with torch.cuda.device(q.device):
         status = lib.mf_simplicial_fwd(args, _native.current_stream(q.device))
     _native.check(status, "mf_simplicial_fwd")
