@@ -549,6 +549,8 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p)
   if (tid == 0) {
     ws.hdr[0] = small_total;
     ws.hdr[1] = large_total;
+    ws.hdr[2] = 0;  // next small item to hand out
+    ws.hdr[3] = 0;  // next large item to hand out
   }
 
   // 4. items: one molecule's items are contiguous, heads interleaved with its
@@ -574,25 +576,17 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p)
 // ---------------------------------------------------------------------------
 // small / large kernels
 // ---------------------------------------------------------------------------
-__device__ __noinline__ void load8_slow(const void* row, int e0, int D, int esize, void* dst) {
-  const unsigned char* s = static_cast<const unsigned char*>(row);
-  unsigned char* d = static_cast<unsigned char*>(dst);
-  for (int e = 0; e < 8; ++e)
-    for (int byte = 0; byte < esize; ++byte)
-      d[e * esize + byte] = (e0 + e < D) ? s[(e0 + e) * esize + byte] : 0;
-}
-
-// Copy 8 elements [e0, e0+8) of a row of length D into registers, zero past D.
+// Copy 8 elements [e0, e0+8) of a row into registers.  These kernels run only
+// with head_dim % 8 == 0 and 16-byte aligned rows, so a chunk lies either
+// inside the row or entirely past its end (then it reads as zero).
 template <typename T>
-__device__ __forceinline__ typename Half<T>::Op8 load8(const T* row, int e0, int D, bool vec) {
+__device__ __forceinline__ typename Half<T>::Op8 load8(const T* row, int e0, int D) {
   typename Half<T>::Op8 v;
-  if (vec && e0 + 8 <= D) {
+  if (e0 < D) {
     v = *reinterpret_cast<const typename Half<T>::Op8*>(row + e0);
-  } else if (e0 >= D) {
+  } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = T(0.0f);
-  } else {
-    load8_slow(row, e0, D, int(sizeof(T)), &v);
   }
   return v;
 }
@@ -674,10 +668,10 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       v2v[t] = zero8<T>();
       if (r < nkj) {
         const size_t src = (size_t(bh) * N + kidx[j0 + r]) * D;
-        a[t] = load8<T>(gk1 + src, e0, D, vec);
-        if (with_v) v1v[t] = load8<T>(gv1 + src, e0, D, vec);
+        a[t] = load8<T>(gk1 + src, e0, D);
+        if (with_v) v1v[t] = load8<T>(gv1 + src, e0, D);
       }
-      if (with_v && r < nkk) v2v[t] = load8<T>(gv2 + (size_t(bh) * N + kidx[k0 + r]) * D, e0, D, vec);
+      if (with_v && r < nkk) v2v[t] = load8<T>(gv2 + (size_t(bh) * N + kidx[k0 + r]) * D, e0, D);
     }
     float m1[8];
 #pragma unroll
@@ -744,7 +738,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         Op8 v = zero8<T>();
-        if (r < nkk) v = load8<T>(gk2 + (size_t(bh) * N + row) * D, c * 32 + g * 8, D, vec);
+        if (r < nkk) v = load8<T>(gk2 + (size_t(bh) * N + row) * D, c * 32 + g * 8, D);
         ka[kt][c] = v;
       }
     }
@@ -843,19 +837,19 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
         v2v[t] = zero8<T>();
         if (jrow[t] >= 0) {
           const size_t src = (size_t(bh) * N + jrow[t]) * D;
-          a[t] = load8<T>(gk1 + src, c8, D, vec);
-          v1v[t] = load8<T>(gv1 + src, c8, D, vec);
-          v2v[t] = load8<T>(gv2 + src, c8, D, vec);
+          a[t] = load8<T>(gk1 + src, c8, D);
+          v1v[t] = load8<T>(gv1 + src, c8, D);
+          v2v[t] = load8<T>(gv2 + src, c8, D);
         }
       }
 #pragma unroll
       for (int t = 0; t < QPT; ++t)
-        qv8[t] = qrow[t] >= 0 ? load8<T>(gq + (size_t(bh) * N + qrow[t]) * D, c8, D, vec) : zero8<T>();
+        qv8[t] = qrow[t] >= 0 ? load8<T>(gq + (size_t(bh) * N + qrow[t]) * D, c8, D) : zero8<T>();
 #pragma unroll
       for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
         for (int c = 0; c < NCH; ++c)
-          ka[kt][c] = krow[kt] >= 0 ? load8<T>(gk2 + (size_t(bh) * N + krow[kt]) * D, c * 32 + g * 8, D, vec)
+          ka[kt][c] = krow[kt] >= 0 ? load8<T>(gk2 + (size_t(bh) * N + krow[kt]) * D, c * 32 + g * 8, D)
                                     : zero8<T>();
 
       // LDS: query rows, K1 (and its column maxima), V2 transposed, V1 transposed
@@ -1029,7 +1023,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       QOp qo[NCH];
       if (has_q) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) Hf::prepare(load8<T>(gq + row_off * D, c * 32 + g * 8, D, vec), qo[c]);
+        for (int c = 0; c < NCH; ++c) Hf::prepare(load8<T>(gq + row_off * D, c * 32 + g * 8, D), qo[c]);
       }
       const int nch = ceil_div(nk, CH);
       float acc[NN];
@@ -1078,7 +1072,7 @@ int launch_main(const Params& prm, int grid, hipStream_t stream) {
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
     MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, prm);

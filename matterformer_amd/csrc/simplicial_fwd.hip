@@ -542,8 +542,17 @@ static int check_shape(int B, int H, int N, int D, int dtype, bool has_pv, size_
 using namespace mf;
 using namespace mf::simplicial;
 
+// The register-resident kernels take 16-bit operands with head_dim <= 64 and a
+// multiple of 8 (whole 16-byte row chunks); everything else, and operands
+// that are not 16-byte aligned, runs on the general kernel.
 static bool uses_fast(int32_t head_dim, int32_t dtype) {
-  return dtype != MF_DTYPE_F32 && simplicial_fast_capacity(head_dim) > 0;
+  return dtype != MF_DTYPE_F32 && head_dim % 8 == 0 && simplicial_fast_capacity(head_dim) > 0;
+}
+
+static bool operands_aligned(const mf_simplicial_fwd_args* a) {
+  for (const void* ptr : {a->q, a->k1, a->v1, a->k2, a->v2})
+    if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0) return false;
+  return true;
 }
 
 extern "C" int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
@@ -620,7 +629,7 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
   // set of launches per slice of at most kSimplicialFastMaxBatch molecules
   // (the slices reuse the workspace in stream order).
   size_t lds = 0;
-  if (uses_fast(a->head_dim, a->dtype)) {
+  if (uses_fast(a->head_dim, a->dtype) && operands_aligned(a)) {
     if (a->tokens > 32767) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports tokens <= 32767");
     const uint64_t need = simplicial_fast_workspace_bytes(a->batch, a->heads, a->tokens);
     if (a->workspace == nullptr || a->workspace_bytes < need)
