@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 2
+#define MF_ABI_VERSION 3
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -120,6 +120,94 @@ int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t tokens,
 /* Bytes of workspace mf_simplicial_fwd needs for this shape (0 if none). */
 uint64_t mf_simplicial_fwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens,
                                           int32_t head_dim, int32_t dtype);
+
+/* ------------------------------------------------------------------------ */
+/* k nearest neighbours of every atom of a batch of molecules.               */
+/*                                                                           */
+/* Distance convention of NonPeriodicGeometryAdapter.forward                 */
+/* (geometry/adapters.py:98-100): delta = x_i - x_j,                         */
+/* d2 = (dx*dx + dy*dy) + dz*dz in fp32, each operation rounded (no FMA).    */
+/* For every valid atom i the k valid atoms j (j != i when exclude_self)     */
+/* with the smallest (d2, j) -- ties go to the lower index -- in ascending   */
+/* order; dist = sqrt(d2) correctly rounded.  Slots beyond the number of     */
+/* candidates, and every slot of a padded atom, get idx -1 and dist +inf.    */
+/* Replaces the legacy knn / knn_graph (cdist + topk, unspecified tie order) */
+/* of legacy/rapidash_v5/models/rapidash_utils.py:139-193.                   */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_knn_args {
+  const float* coords;     /* [B, N, 3] fp32, finite                         */
+  const uint8_t* pad_mask; /* [B, N] bytes, nonzero = padding, or NULL       */
+  int32_t* idx;            /* [B, N, k] out                                  */
+  float* dist;             /* [B, N, k] out, or NULL                         */
+  int32_t batch;
+  int32_t atoms;           /* N >= 1                                         */
+  int32_t k;               /* 1 <= k <= 64                                   */
+  int32_t exclude_self;    /* nonzero: j == i is not a candidate             */
+} mf_knn_args;
+
+int mf_knn(const mf_knn_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Cutoff (radius) neighbour mask, minimum image for periodic cells.         */
+/*                                                                           */
+/* periodic (gram != NULL): coords are fractional; for the integer image     */
+/*   offsets o in {-r..r}^3 (r = pbc_radius, PeriodicGeometryAdapter,        */
+/*   adapters.py:141-149,176-190), e = (f_i - f_j) + o and                   */
+/*   t_c = (G[c][0]*e0 + G[c][1]*e1) + G[c][2]*e2,                          */
+/*   d2  = (e0*t0 + e1*t1) + e2*t2, minimised over the images;               */
+/* non-periodic (gram == NULL): d2 = (dx*dx + dy*dy) + dz*dz (adapters.py:98-99). */
+/* fp32, each operation rounded.  mask[i,j] = d2 <= cutoff*cutoff for valid  */
+/* i and j (i == j included).                                                */
+/*   mask_bits  [B, N, ceil(N/32)] uint32: bit t of word w is column 32w+t;  */
+/*              bits of columns >= N are 0.                                  */
+/*   block_mask [B, NB, NB] bytes (NB = ceil(N/block)), or NULL: 1 iff any   */
+/*              bit of the (block x block) tile is set.                      */
+/* block is 32, 64 or 128.                                                   */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_radius_mask_args {
+  const float* coords;     /* [B, N, 3] fp32 (fractional when periodic)      */
+  const float* gram;       /* [B, 3, 3] fp32 metric G = cell cell^T, or NULL */
+  const uint8_t* pad_mask; /* [B, N] bytes, nonzero = padding, or NULL       */
+  uint32_t* mask_bits;     /* out                                            */
+  uint8_t* block_mask;     /* out, or NULL                                   */
+  float cutoff;            /* > 0                                            */
+  int32_t batch;
+  int32_t atoms;
+  int32_t block;
+  int32_t pbc_radius;      /* 1 or 2 (ignored when gram == NULL)             */
+} mf_radius_mask_args;
+
+int mf_radius_mask(const mf_radius_mask_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Local (radius) attention over a neighbour bit mask.                        */
+/*                                                                           */
+/* out[b,h,i] = sum_j softmax_j(scale * q_i . k_j over j with mask[b,i,j]) v_j */
+/* lse[b,h,i] = log sum_j exp(scale * q_i . k_j) over the same j; rows with  */
+/* no allowed key get out = 0 and lse = 0.  This is the dense masked softmax */
+/* that an additive attn_mask (0 / -inf) gives in nn.MultiheadAttention and  */
+/* scaled_dot_product_attention (transformer.py:256-268,                     */
+/* regular_attention.py:262-268,303-308), skipping 64x64 tiles whose         */
+/* block_mask entry is 0.                                                    */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_radius_attn_args {
+  const void* q;               /* [B, H, N, D], dtype bf16 or fp16           */
+  const void* k;
+  const void* v;
+  const uint32_t* mask_bits;   /* [B, N, ceil(N/32)] as mf_radius_mask writes */
+  const uint8_t* block_mask;   /* [B, NB, NB] for block 64, or NULL (all tiles) */
+  void* out;                   /* [B, H, N, D] dtype, or NULL                */
+  float* out_f32;              /* [B, H, N, D] fp32, or NULL                 */
+  float* lse;                  /* [B, H, N] fp32 (natural log), or NULL      */
+  float scale;                 /* logit scale, e.g. head_dim^-1/2            */
+  int32_t batch;
+  int32_t heads;
+  int32_t atoms;
+  int32_t head_dim;            /* 32, 64 or 128                              */
+  int32_t dtype;               /* MF_DTYPE_BF16 or MF_DTYPE_F16              */
+} mf_radius_attn_args;
+
+int mf_radius_attn(const mf_radius_attn_args* args, void* stream);
 
 #ifdef __cplusplus
 }

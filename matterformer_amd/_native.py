@@ -37,9 +37,12 @@ EXPORTED_SYMBOLS = (
     "mf_simplicial_fwd",
     "mf_simplicial_fwd_supported",
     "mf_simplicial_fwd_workspace_size",
+    "mf_knn",
+    "mf_radius_mask",
+    "mf_radius_attn",
 )
 
-EXPECTED_ABI_VERSION = 2
+EXPECTED_ABI_VERSION = 3
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -108,6 +111,7 @@ class MfRadiusAttnArgs(ctypes.Structure):
         ("mask_bits", ctypes.c_void_p),
         ("block_mask", ctypes.c_void_p),
         ("out", ctypes.c_void_p),
+        ("out_f32", ctypes.c_void_p),
         ("lse", ctypes.c_void_p),
         ("scale", ctypes.c_float),
         ("batch", ctypes.c_int32),
@@ -115,7 +119,6 @@ class MfRadiusAttnArgs(ctypes.Structure):
         ("atoms", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
-        ("block", ctypes.c_int32),
     ]
 
 

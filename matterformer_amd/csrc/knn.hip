@@ -1,0 +1,189 @@
+// k nearest neighbours of every atom of a batch of molecules (mf_knn) on
+// gfx950.
+//
+// Distances follow NonPeriodicGeometryAdapter.forward
+// (src/matterformer/geometry/adapters.py:98-100): delta = x_i - x_j,
+// d2 = (dx*dx + dy*dy) + dz*dz in fp32 with every operation rounded (this file
+// is built with -ffp-contract=off, so no FMA is formed).  The order is the
+// stable one, (d2, j) ascending, which the legacy torch_cluster / topk path
+// (legacy/rapidash_v5/models/rapidash_utils.py:139-193) leaves unspecified.
+//
+// Layout: one workgroup of 256 threads serves 256/L queries of one molecule;
+// the L lanes of a query split the candidates j (lane s takes j = s mod L),
+// reading the molecule's coordinates from LDS tiles of kTile atoms (every lane
+// of a wave reads the same few words per step: broadcast, no bank conflicts).
+// Each lane keeps the KMAX smallest keys it has seen, sorted, in registers:
+//   key = float_bits(d2) << 32 | j
+// (d2 >= 0, so the float bit pattern orders like the value and the low word
+// breaks ties by index).  A candidate below the current KMAX-th key is merged
+// in by one compare-exchange chain.  The L lists are then merged in log2(L)
+// butterfly rounds: partners exchange lists, take min(a[s], b[KMAX-1-s])
+// (a bitonic sequence holding the KMAX smallest of both) and sort it with a
+// bitonic network, so both partners end with the same list.
+#include <cmath>
+
+#include "mf_common.h"
+
+namespace mf {
+namespace knn {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 2048;  // atoms staged in LDS per pass (24 KB + 2 KB)
+constexpr uint64_t kEmpty = ~0ull;
+
+struct Params {
+  const float* coords;
+  const uint8_t* pad;
+  int32_t* idx;
+  float* dist;
+  int B, N, K, exclude_self;
+};
+
+__device__ __forceinline__ void cmp_swap(uint64_t& lo, uint64_t& hi) {
+  const uint64_t a = lo, b = hi;
+  lo = a < b ? a : b;
+  hi = a < b ? b : a;
+}
+
+template <int KMAX>
+__device__ __forceinline__ void insert(uint64_t (&list)[KMAX], uint64_t key) {
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) cmp_swap(list[s], key);
+}
+
+// Sort a bitonic sequence ascending.
+template <int KMAX>
+__device__ __forceinline__ void bitonic_sort(uint64_t (&list)[KMAX]) {
+#pragma unroll
+  for (int stride = KMAX / 2; stride >= 1; stride >>= 1) {
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s)
+      if ((s & stride) == 0) cmp_swap(list[s], list[s + stride]);
+  }
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
+  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), mask, 64);
+  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), mask, 64);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+template <int KMAX, int L>
+__global__ void __launch_bounds__(kThreads) knn_kernel(Params p) {
+  __shared__ float sx[kTile], sy[kTile], sz[kTile];
+  __shared__ uint8_t spad[kTile];
+
+  constexpr int kQueries = kThreads / L;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int sub = tid % L;
+  const int i = blockIdx.x * kQueries + tid / L;
+  const int N = p.N;
+  const float* x = p.coords + size_t(b) * N * 3;
+  const uint8_t* pad = p.pad ? p.pad + size_t(b) * N : nullptr;
+  const bool valid_i = i < N && !(pad && pad[i]);
+  float xi = 0.0f, yi = 0.0f, zi = 0.0f;
+  if (valid_i) {
+    xi = x[3 * i + 0];
+    yi = x[3 * i + 1];
+    zi = x[3 * i + 2];
+  }
+
+  uint64_t list[KMAX];
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) list[s] = kEmpty;
+
+  for (int t0 = 0; t0 < N; t0 += kTile) {
+    const int n = min(kTile, N - t0);
+    __syncthreads();
+    for (int u = tid; u < n; u += kThreads) {
+      sx[u] = x[3 * (t0 + u) + 0];
+      sy[u] = x[3 * (t0 + u) + 1];
+      sz[u] = x[3 * (t0 + u) + 2];
+      spad[u] = pad ? pad[t0 + u] : 0;
+    }
+    __syncthreads();
+    if (!valid_i) continue;
+    for (int u = sub; u < n; u += L) {
+      const int j = t0 + u;
+      if (spad[u] || (p.exclude_self && j == i)) continue;
+      const float dx = xi - sx[u];
+      const float dy = yi - sy[u];
+      const float dz = zi - sz[u];
+      const float xx = dx * dx;
+      const float yy = dy * dy;
+      const float zz = dz * dz;
+      const float s = xx + yy;
+      const float d2 = s + zz;
+      const uint64_t key = (static_cast<uint64_t>(__float_as_uint(d2)) << 32) | static_cast<uint32_t>(j);
+      if (key < list[KMAX - 1]) insert(list, key);
+    }
+  }
+
+  // butterfly merge of the L lane lists of a query
+#pragma unroll
+  for (int mask = 1; mask < L; mask <<= 1) {
+#pragma unroll
+    for (int s = 0; s < KMAX / 2; ++s) {
+      const uint64_t other_hi = shfl_xor_u64(list[KMAX - 1 - s], mask);
+      const uint64_t other_lo = shfl_xor_u64(list[s], mask);
+      list[s] = list[s] < other_hi ? list[s] : other_hi;
+      list[KMAX - 1 - s] = list[KMAX - 1 - s] < other_lo ? list[KMAX - 1 - s] : other_lo;
+    }
+    bitonic_sort(list);
+  }
+
+  if (i >= N) return;
+  int32_t* oi = p.idx + (size_t(b) * N + i) * p.K;
+  float* od = p.dist ? p.dist + (size_t(b) * N + i) * p.K : nullptr;
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    if (s % L != sub || s >= p.K) continue;
+    const uint64_t key = list[s];
+    const bool empty = key == kEmpty;
+    oi[s] = empty ? -1 : static_cast<int32_t>(static_cast<uint32_t>(key));
+    if (od) od[s] = empty ? INFINITY : sqrtf(__uint_as_float(static_cast<uint32_t>(key >> 32)));
+  }
+}
+
+template <int KMAX, int L>
+int launch(const Params& p, hipStream_t stream) {
+  constexpr int kQueries = kThreads / L;
+  const dim3 grid((p.N + kQueries - 1) / kQueries, p.B);
+  hipLaunchKernelGGL((knn_kernel<KMAX, L>), grid, dim3(kThreads), 0, stream, p);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
+
+// Lanes per query: enough queries in flight to fill the GPU at small batch
+// sizes, fewer lanes (less merging) when there are many queries.
+template <int KMAX>
+int dispatch_lanes(const Params& p, int num_cus, hipStream_t stream) {
+  const long long queries = (long long)p.B * p.N;
+  if (queries * 16 <= (long long)num_cus * 2048) return launch<KMAX, 16>(p, stream);
+  if (queries * 8 <= (long long)num_cus * 4096) return launch<KMAX, 8>(p, stream);
+  return launch<KMAX, 4>(p, stream);
+}
+
+}  // namespace knn
+}  // namespace mf
+
+extern "C" int mf_knn(const mf_knn_args* a, void* stream) {
+  using namespace mf;
+  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_knn: args is NULL");
+  if (!a->coords || !a->idx) return fail(MF_ERR_INVALID_ARGUMENT, "mf_knn: coords and idx must be non-NULL");
+  if (a->batch < 0 || a->atoms < 0)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_knn: batch and atoms must be non-negative");
+  if (a->k < 1 || a->k > 64) return fail(MF_ERR_INVALID_ARGUMENT, "mf_knn: k must be in [1, 64]");
+  if (a->batch > 65535) return fail(MF_ERR_UNSUPPORTED, "mf_knn: batch must be <= 65535");
+  if (a->batch == 0 || a->atoms == 0) return MF_OK;
+  DeviceInfo dev;
+  int st = device_info(&dev);
+  if (st != MF_OK) return st;
+  knn::Params p{a->coords, a->pad_mask, a->idx, a->dist, a->batch, a->atoms, a->k, a->exclude_self != 0};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->k <= 8) return knn::dispatch_lanes<8>(p, dev.num_cus, s);
+  if (a->k <= 16) return knn::dispatch_lanes<16>(p, dev.num_cus, s);
+  if (a->k <= 32) return knn::dispatch_lanes<32>(p, dev.num_cus, s);
+  return knn::launch<64, 4>(p, s);
+}

@@ -1,0 +1,303 @@
+// Local (radius) attention over a neighbour bit mask (mf_radius_attn) on
+// gfx950.
+//
+// out_i = sum_j softmax_j(scale q_i . k_j over j with mask[i,j]) v_j, the dense
+// masked softmax an additive 0/-inf attn_mask gives in nn.MultiheadAttention /
+// scaled_dot_product_attention (src/matterformer/models/transformer.py:256-268,
+// src/matterformer/models/regular_attention.py:262-268,303-308).  Rows without
+// an allowed key give out = 0, lse = 0.
+//
+// One workgroup (4 waves) per (cell, head, 64-query tile); wave w owns the 16
+// queries 16w..16w+15 of the tile.  Key tiles of 64 whose block-mask entry is
+// set are staged in LDS (K row-major, V transposed), the next one prefetched
+// into registers during the current one's compute.  Per key tile and wave:
+//   S^T[key][q] = K Q^T        (MFMA 16x16x32, K rows = A operand from LDS,
+//                               Q^T = B operand held in registers)
+//   masked online softmax per query column (base 2, scale*log2 e folded in)
+//   O^T[d][q]  += V^T P^T      (P^T straight from the S^T accumulators as
+//                               the B operand, keys of a 32-key step taken in
+//                               the order {4g+r, 16+4g+r}; V^T rows read from
+//                               LDS in the same key order)
+#include <cmath>
+
+#include "mf_common.h"
+
+namespace mf {
+namespace rattn {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 64;          // queries per workgroup, keys per tile
+constexpr int kMaxTiles = 1024;    // key tiles per row (atoms <= 65536)
+
+struct Params {
+  const void* q;
+  const void* k;
+  const void* v;
+  const uint32_t* bits;
+  const uint8_t* block_mask;
+  void* out;
+  float* out_f32;
+  float* lse;
+  float scale_log2;  // scale * log2(e)
+  int B, H, N, W, NB;
+};
+
+template <typename T>
+struct Ops;
+template <>
+struct Ops<__bf16> {
+  using Op8 = mf_bf16x8;
+  __device__ static __forceinline__ mf_f32x4 mma(Op8 a, Op8 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Ops<_Float16> {
+  using Op8 = mf_f16x8;
+  __device__ static __forceinline__ mf_f32x4 mma(Op8 a, Op8 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
+  using Op8 = typename Ops<T>::Op8;
+  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T Op4;
+  constexpr int KS = D + 8;         // K row stride in LDS (elements)
+  constexpr int VS = kTile + 8;     // V^T row stride in LDS (elements)
+  constexpr int DK = D / 32;        // K steps of S^T
+  constexpr int ND = D / 16;        // d tiles of O^T
+  constexpr int CPR = D / 8;        // 16-byte chunks per row
+  constexpr int CPT = kTile * CPR / kThreads;  // chunks per thread per tile
+  static_assert(CPT >= 1 && (kTile * CPR) % kThreads == 0, "staging shape");
+
+  __shared__ __attribute__((aligned(16))) T Ks[kTile * KS];
+  __shared__ __attribute__((aligned(16))) T VT[D * VS];
+  __shared__ int s_tiles[kMaxTiles];
+  __shared__ int s_ntiles;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int N = p.N;
+  const size_t bh = size_t(b) * p.H + h;
+  const T* gq = static_cast<const T*>(p.q) + bh * N * D;
+  const T* gk = static_cast<const T*>(p.k) + bh * N * D;
+  const T* gv = static_cast<const T*>(p.v) + bh * N * D;
+
+  // active key tiles of this query tile, in order (ballot compaction by wave 0)
+  if (wave == 0) {
+    const uint8_t* brow = p.block_mask ? p.block_mask + (size_t(b) * p.NB + qt) * p.NB : nullptr;
+    int n = 0;
+    for (int base = 0; base < p.NB; base += 64) {
+      const int jt = base + lane;
+      const bool on = jt < p.NB && (!brow || brow[jt] != 0);
+      const uint64_t bal = __ballot(on);
+      if (on) s_tiles[n + __popcll(bal & ((1ull << lane) - 1))] = jt;
+      n += __popcll(bal);
+    }
+    if (lane == 0) s_ntiles = n;
+  }
+
+  // Q^T as B operands: lane holds q = q0 + r16, d = 32 kk + 8 g .. + 7
+  const int qi = qt * kTile + wave * 16 + r16;
+  const bool q_in = qi < N;
+  Op8 qb[DK];
+#pragma unroll
+  for (int kk = 0; kk < DK; ++kk) {
+    if (q_in) {
+      qb[kk] = *reinterpret_cast<const Op8*>(gq + size_t(qi) * D + 32 * kk + 8 * g);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qb[kk][e] = T(0.0f);
+    }
+  }
+  const uint32_t* qbits = p.bits + size_t(b) * N * p.W + size_t(q_in ? qi : 0) * p.W;
+
+  mf_f32x4 acc[ND];
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) acc[nd] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+
+  __syncthreads();
+  const int ntiles = s_ntiles;
+
+  // register staging of one key tile: chunk c = tid + t*kThreads -> (key c / CPR, d 8*(c % CPR))
+  Op8 kr[CPT], vr[CPT];
+  auto load_tile = [&](int jt) {
+#pragma unroll
+    for (int t = 0; t < CPT; ++t) {
+      const int c = tid + t * kThreads;
+      const int key = jt * kTile + c / CPR;
+      const int d0 = (c % CPR) * 8;
+      if (key < N) {
+        kr[t] = *reinterpret_cast<const Op8*>(gk + size_t(key) * D + d0);
+        vr[t] = *reinterpret_cast<const Op8*>(gv + size_t(key) * D + d0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          kr[t][e] = T(0.0f);
+          vr[t][e] = T(0.0f);
+        }
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int t = 0; t < CPT; ++t) {
+      const int c = tid + t * kThreads;
+      const int key = c / CPR;
+      const int d0 = (c % CPR) * 8;
+      *reinterpret_cast<Op8*>(Ks + key * KS + d0) = kr[t];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) VT[(d0 + e) * VS + key] = vr[t][e];
+    }
+  };
+
+  if (ntiles > 0) load_tile(s_tiles[0]);
+  for (int it = 0; it < ntiles; ++it) {
+    const int jt = s_tiles[it];
+    store_tile();
+    __syncthreads();
+    if (it + 1 < ntiles) load_tile(s_tiles[it + 1]);
+
+    // mask words of this key tile for the lane's query
+    const int w0 = 2 * jt;
+    const uint32_t mw0 = (q_in && w0 < p.W) ? qbits[w0] : 0u;
+    const uint32_t mw1 = (q_in && w0 + 1 < p.W) ? qbits[w0 + 1] : 0u;
+
+    // S^T tiles: keys 16 kt + 4 g + r, query r16
+    float s[4][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      mf_f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < DK; ++kk) {
+        const Op8 a = *reinterpret_cast<const Op8*>(Ks + (16 * kt + r16) * KS + 32 * kk + 8 * g);
+        c = Ops<T>::mma(a, qb[kk], c);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[kt][r] = c[r];
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = 16 * kt + 4 * g + r;
+        const uint32_t word = key < 32 ? mw0 : mw1;
+        const bool allowed = (word >> (key & 31)) & 1u;
+        s[kt][r] = allowed ? s[kt][r] * p.scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, s[kt][r]);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    // Branch-free (the MFMAs below need the whole wave): while a query has
+    // seen no allowed key its maximum stays -inf and the exponent offset is
+    // 0, so alpha = exp2(-inf) = 0 and every p = exp2(-inf) = 0.
+    const float m_new = fmaxf(m, tmax);
+    const float m_off = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = fast_exp2(m - m_off);
+    m = m_new;
+    float psum = 0.0f;
+    Op8 pb[2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = fast_exp2(s[kt][r] - m_off);  // masked keys: exp2(-inf) = 0
+        psum += pv;
+        pb[kt >> 1][(kt & 1) * 4 + r] = T(pv);
+      }
+    }
+    l = l * alpha + psum;
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[nd][r] *= alpha;
+    }
+    // O^T[d][q] += sum_keys V^T[d][key] P^T[key][q]
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd) {
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const T* vrow = VT + (16 * nd + r16) * VS + 32 * pr + 4 * g;
+        const Op4 lo = *reinterpret_cast<const Op4*>(vrow);
+        const Op4 hi = *reinterpret_cast<const Op4*>(vrow + 16);
+        const Op8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[nd] = Ops<T>::mma(a, pb[pr], acc[nd]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // finish: l summed over the 4 key groups g; lane (g, r16) holds d = 16 nd + 4 g + r of query r16
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (!q_in) return;
+  const bool has = l > 0.0f;
+  const float inv = has ? 1.0f / l : 0.0f;
+  const size_t row = bh * N + qi;
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) {
+    const int d0 = 16 * nd + 4 * g;
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = acc[nd][r] * inv;
+    if (p.out) {
+      Op4 ov;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ov[r] = T(o[r]);
+      *reinterpret_cast<Op4*>(static_cast<T*>(p.out) + row * D + d0) = ov;
+    }
+    if (p.out_f32) *reinterpret_cast<float4*>(p.out_f32 + row * D + d0) = float4{o[0], o[1], o[2], o[3]};
+  }
+  if (p.lse && g == 0) p.lse[row] = has ? (m + __log2f(l)) * kLn2 : 0.0f;
+}
+
+template <typename T, int D>
+int launch(const Params& p, hipStream_t stream) {
+  const dim3 grid((p.N + kTile - 1) / kTile, p.H, p.B);
+  hipLaunchKernelGGL((radius_attn_kernel<T, D>), grid, dim3(kThreads), 0, stream, p);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
+
+template <typename T>
+int dispatch_dim(const Params& p, int D, hipStream_t stream) {
+  if (D == 32) return launch<T, 32>(p, stream);
+  if (D == 64) return launch<T, 64>(p, stream);
+  return launch<T, 128>(p, stream);
+}
+
+}  // namespace rattn
+}  // namespace mf
+
+extern "C" int mf_radius_attn(const mf_radius_attn_args* a, void* stream) {
+  using namespace mf;
+  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_radius_attn: args is NULL");
+  if (!a->q || !a->k || !a->v || !a->mask_bits)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_radius_attn: q, k, v and mask_bits must be non-NULL");
+  if (!a->out && !a->out_f32 && !a->lse)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_radius_attn: at least one of out, out_f32, lse must be non-NULL");
+  if (a->batch < 0 || a->heads < 0 || a->atoms < 0)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_radius_attn: batch, heads and atoms must be non-negative");
+  if (a->dtype != MF_DTYPE_BF16 && a->dtype != MF_DTYPE_F16)
+    return fail(MF_ERR_UNSUPPORTED, "mf_radius_attn: only supports float16/bfloat16 operands");
+  if (a->head_dim != 32 && a->head_dim != 64 && a->head_dim != 128)
+    return fail(MF_ERR_UNSUPPORTED, "mf_radius_attn: head_dim must be 32, 64 or 128");
+  if (!std::isfinite(a->scale)) return fail(MF_ERR_INVALID_ARGUMENT, "mf_radius_attn: scale must be finite");
+  for (const void* ptr : {a->q, a->k, a->v, static_cast<const void*>(a->out), static_cast<const void*>(a->out_f32)})
+    if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_radius_attn: q, k, v, out and out_f32 must be 16-byte aligned");
+  if (a->batch == 0 || a->heads == 0 || a->atoms == 0) return MF_OK;
+  const int nb = (a->atoms + rattn::kTile - 1) / rattn::kTile;
+  if (nb > rattn::kMaxTiles || a->batch > 65535 || a->heads > 65535)
+    return fail(MF_ERR_UNSUPPORTED, "mf_radius_attn: atoms must be <= 65536 and batch, heads <= 65535");
+  rattn::Params p{a->q, a->k, a->v, a->mask_bits, a->block_mask, a->out, a->out_f32, a->lse,
+                  a->scale * kLog2e, a->batch, a->heads, a->atoms, (a->atoms + 31) / 32, nb};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->dtype == MF_DTYPE_BF16) return rattn::dispatch_dim<__bf16>(p, a->head_dim, s);
+  return rattn::dispatch_dim<_Float16>(p, a->head_dim, s);
+}

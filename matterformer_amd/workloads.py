@@ -92,3 +92,44 @@ def random_simplicial(B: int, H: int, N: int, D: int, *, seed: int, counts=None,
     if pair_drop > 0:
         pair_valid = torch.rand(B, N, N, generator=gen) >= pair_drop
     return (*tensors, query_valid, key_valid, pair_valid)
+
+
+@dataclass
+class KnnWorkload:
+    coords: torch.Tensor            # (B, N, 3) fp32
+    pad_mask: torch.Tensor | None   # (B, N) bool, True = padding
+    k: int
+
+
+def knn_workload(seed: int = 2, *, batch: int = 32, atoms: int = 181, k: int = 16) -> KnnWorkload:
+    """Config 3: coordinates ~ N(0, 2 A^2) per component, every atom valid."""
+    gen = torch.Generator().manual_seed(seed)
+    coords = torch.randn(batch, atoms, 3, generator=gen) * math.sqrt(2.0)
+    return KnnWorkload(coords, None, k)
+
+
+@dataclass
+class RadiusWorkload:
+    frac: torch.Tensor        # (B, N, 3) fp32 fractional coordinates
+    lattice: torch.Tensor     # (B, 6) y1 latent [log a, log b, log c, cos alpha, cos beta, cos gamma]
+    q: torch.Tensor           # (B, H, N, D) fp32 (cast to the compute dtype)
+    k: torch.Tensor
+    v: torch.Tensor
+    cutoff: float
+
+    def attention_flops(self, n_pairs: int) -> int:
+        """4 H D flops per allowed (i, j) pair (q.k and p.v)."""
+        B, H, N, D = self.q.shape
+        return 4 * H * D * int(n_pairs)
+
+
+def radius_workload(seed: int = 3, *, cells: int = 8, atoms: int = 512, heads: int = 8, head_dim: int = 64,
+                    cutoff: float = 6.0) -> RadiusWorkload:
+    """Config 4: frac ~ U[0,1)^3, lengths ~ U[15,30] A, angles ~ U[80,100] deg, q,k,v ~ N(0,1)/8."""
+    gen = torch.Generator().manual_seed(seed)
+    frac = torch.rand(cells, atoms, 3, generator=gen)
+    lengths = 15.0 + 15.0 * torch.rand(cells, 3, generator=gen)
+    angles = (80.0 + 20.0 * torch.rand(cells, 3, generator=gen)) * math.pi / 180.0
+    lattice = torch.cat([lengths.log(), angles.cos()], dim=-1)
+    q, k, v = (torch.randn(cells, heads, atoms, head_dim, generator=gen) / 8.0 for _ in range(3))
+    return RadiusWorkload(frac, lattice, q, k, v, cutoff)

@@ -94,8 +94,8 @@ def pair_d2(coords: np.ndarray, gram: np.ndarray | None = None, pbc_radius: int 
 
 
 def unpack_bits(bits: np.ndarray, N: int) -> np.ndarray:
-    """(B,N,W) uint32 -> (B,N,N) bool."""
-    B, _, W = bits.shape
+    """(B,R,W) uint32 -> (B,R,N) bool (bit t of word w is column 32 w + t)."""
+    B, R, W = bits.shape
     shifts = np.arange(32, dtype=np.uint32)
-    full = ((bits[..., None] >> shifts) & 1).astype(bool).reshape(B, N, W * 32)
+    full = ((bits[..., None] >> shifts) & 1).astype(bool).reshape(B, R, W * 32)
     return full[..., :N]

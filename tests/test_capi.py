@@ -57,3 +57,32 @@ def test_check_raises_runtime_error_with_library_message():
     _native.lib().mf_simplicial_fwd(None, None)
     with pytest.raises(RuntimeError, match="args is NULL"):
         _native.check(_native.MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd")
+
+
+@pytest.mark.parametrize("name,argtype", [("mf_knn", _native.MfKnnArgs), ("mf_radius_mask", _native.MfRadiusMaskArgs),
+                                          ("mf_radius_attn", _native.MfRadiusAttnArgs)])
+def test_geometry_entry_points_reject_null_and_missing_pointers(name, argtype):
+    fn = getattr(_native.lib(), name)
+    assert fn(None, None) == _native.MF_ERR_INVALID_ARGUMENT
+    assert "args is NULL" in _native.last_error()
+    assert fn(argtype(), None) == _native.MF_ERR_INVALID_ARGUMENT
+    assert "must be non-NULL" in _native.last_error()
+
+
+def test_geometry_entry_points_validate_sizes_before_any_device_call():
+    lib = _native.lib()
+    fake = 1 << 20  # never dereferenced: every call below fails validation first
+    a = _native.MfKnnArgs(coords=fake, idx=fake, batch=1, atoms=4, k=65)
+    assert lib.mf_knn(a, None) == _native.MF_ERR_INVALID_ARGUMENT and "k must be in [1, 64]" in _native.last_error()
+    r = _native.MfRadiusMaskArgs(coords=fake, mask_bits=fake, batch=1, atoms=4, block=48, cutoff=1.0, pbc_radius=1)
+    assert lib.mf_radius_mask(r, None) == _native.MF_ERR_INVALID_ARGUMENT and "block" in _native.last_error()
+    r.block, r.cutoff = 64, -1.0
+    assert lib.mf_radius_mask(r, None) == _native.MF_ERR_INVALID_ARGUMENT and "cutoff" in _native.last_error()
+    r.cutoff, r.gram, r.pbc_radius = 1.0, fake, 3
+    assert lib.mf_radius_mask(r, None) == _native.MF_ERR_INVALID_ARGUMENT and "pbc_radius" in _native.last_error()
+    t = _native.MfRadiusAttnArgs(q=fake, k=fake, v=fake, mask_bits=fake, out=fake, scale=0.125, batch=1, heads=1,
+                                 atoms=4, head_dim=64, dtype=_native.MF_DTYPE_F32)
+    assert lib.mf_radius_attn(t, None) == _native.MF_ERR_UNSUPPORTED
+    assert "float16/bfloat16" in _native.last_error()
+    t.dtype, t.head_dim = _native.MF_DTYPE_BF16, 48
+    assert lib.mf_radius_attn(t, None) == _native.MF_ERR_UNSUPPORTED and "head_dim" in _native.last_error()

@@ -1,0 +1,295 @@
+"""GPU parity of the geometry kernels (mf_knn, mf_radius_mask, mf_radius_attn)
+against the CPU oracle, through the C ABI.
+
+Bars: kNN indices and distances bit for bit; radius bit masks and block
+masks bit for bit; radius attention within 2e-2 (bf16) / 5e-3 (fp16) of the
+float64 masked softmax, normwise, and lse within 3e-2 absolute.
+"""
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from matterformer_amd.geometry_ops import knn_graph, lattice_to_gram, radius_attention, radius_mask
+from matterformer_amd.workloads import knn_workload, radius_workload
+from oracle.native import knn as oracle_knn
+from oracle.native import radius_mask as oracle_radius_mask
+from oracle.native import unpack_bits
+from oracle.radius import lattice_y1_to_gram, masked_attention_fp64
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _bits_u32(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint32)
+
+
+# ----------------------------------------------------------------------------- kNN
+
+KNN_CASES = [
+    # B, N, k, pad pattern, exclude_self
+    (1, 1, 1, None, True),
+    (2, 5, 4, None, True),
+    (3, 37, 16, "tail", True),
+    (2, 45, 5, "holes", False),
+    (4, 181, 16, None, True),
+    (2, 181, 32, "holes", True),
+    (2, 130, 64, "tail", True),
+    (1, 2100, 16, "holes", True),   # more atoms than one LDS tile
+    (3, 70, 8, None, False),
+]
+
+
+@pytest.mark.parametrize("B,N,k,pad_kind,excl", KNN_CASES)
+def test_knn_matches_oracle_bitwise(cuda, B, N, k, pad_kind, excl):
+    print(f"knn B={B} N={N} k={k} pad={pad_kind} exclude_self={excl}", flush=True)
+    gen = torch.Generator().manual_seed(1000 + N + k)
+    coords = torch.randn(B, N, 3, generator=gen) * math.sqrt(2.0)
+    pad = None
+    if pad_kind == "tail":
+        pad = torch.zeros(B, N, dtype=torch.bool)
+        pad[-1, N // 2:] = True
+    elif pad_kind == "holes":
+        pad = torch.rand(B, N, generator=gen) < 0.2
+    idx, dist = knn_graph(coords.to(cuda), k, None if pad is None else pad.to(cuda), exclude_self=excl)
+    torch.cuda.synchronize()
+    ridx, rdist = oracle_knn(coords.numpy(), k, None if pad is None else pad.numpy(), exclude_self=excl)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(dist.cpu().numpy().view(np.uint32), rdist.view(np.uint32))
+
+
+def test_knn_golden_distances_and_order(cuda):
+    z = np.load(GOLDEN / "geometry_nonperiodic.npz")
+    coords, pad, d2 = z["coords"], z["pad_mask"], z["pair_dist2"]
+    B, N, _ = coords.shape
+    idx, dist = knn_graph(torch.from_numpy(coords).to(cuda), 20, torch.from_numpy(pad).to(cuda))
+    idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
+    for b in range(B):
+        for i in np.flatnonzero(~pad[b]):
+            cand = np.array([j for j in range(N) if j != i and not pad[b, j]])
+            expect = cand[np.lexsort((cand, d2[b, i, cand]))][:20]
+            np.testing.assert_array_equal(idx[b, i, : len(expect)], expect)
+            np.testing.assert_array_equal(dist[b, i, : len(expect)], np.sqrt(d2[b, i, expect]))
+
+
+def test_knn_ties_and_duplicates(cuda):
+    pts = torch.tensor([[[0, 0, 0], [0, 0, -1], [1, 0, 0], [0, 1, 0], [-1, 0, 0], [0, -1, 0], [0, 0, 1],
+                         [2, 0, 0]]], dtype=torch.float32)
+    idx, dist = knn_graph(pts.to(cuda), 7)
+    assert idx[0, 0].tolist() == [1, 2, 3, 4, 5, 6, 7]
+    dup = torch.zeros(1, 70, 3)
+    idx, dist = knn_graph(dup.to(cuda), 16)
+    for i in (0, 17, 69):
+        assert idx[0, i].tolist() == [j for j in range(70) if j != i][:16]
+        assert (dist[0, i] == 0).all()
+
+
+def test_knn_config3_full_size(cuda):
+    w = knn_workload()
+    idx, dist = knn_graph(w.coords.to(cuda), w.k)
+    ridx, rdist = oracle_knn(w.coords.numpy(), w.k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(dist.cpu().numpy(), rdist)
+
+
+def test_knn_scaled_batch_properties(cuda):
+    """Config 3 scaled 64x: sorted rows, valid indices, no self, distances
+    consistent with the coordinates, and a sampled subset equal to the oracle."""
+    w = knn_workload(batch=32 * 64)
+    c = w.coords.to(cuda)
+    idx, dist = knn_graph(c, w.k)
+    B, N, k = idx.shape
+    assert (idx >= 0).all() and (idx < N).all()
+    assert (idx != torch.arange(N, device=cuda)[None, :, None]).all()
+    assert (dist[..., 1:] >= dist[..., :-1]).all()
+    nb = torch.gather(c, 1, idx.long().reshape(B, N * k, 1).expand(-1, -1, 3)).reshape(B, N, k, 3)
+    d = nb - c[:, :, None, :]
+    d2 = (d[..., 0] * d[..., 0] + d[..., 1] * d[..., 1]) + d[..., 2] * d[..., 2]
+    torch.testing.assert_close(dist, torch.sqrt(d2), rtol=1e-6, atol=0)
+    sample = slice(0, 2048, 97)
+    ridx, rdist = oracle_knn(w.coords[sample].numpy(), w.k)
+    np.testing.assert_array_equal(idx[sample].cpu().numpy(), ridx)
+    np.testing.assert_array_equal(dist[sample].cpu().numpy(), rdist)
+
+
+# ----------------------------------------------------------------------------- radius mask
+
+def _cells(B, seed, lo=8.0, hi=12.0, amin=80.0, amax=100.0):
+    rng = np.random.default_rng(seed)
+    y1 = np.concatenate([np.log(rng.uniform(lo, hi, (B, 3))), np.cos(np.deg2rad(rng.uniform(amin, amax, (B, 3))))],
+                        axis=1).astype(np.float32)
+    return y1
+
+
+MASK_CASES = [
+    # B, N, block, periodic, pbc_radius, pad
+    (1, 1, 64, False, 1, False),
+    (2, 31, 32, False, 1, True),
+    (2, 33, 64, True, 1, False),
+    (3, 150, 64, True, 1, True),
+    (2, 150, 128, True, 2, True),
+    (2, 257, 32, False, 1, True),
+    (1, 700, 64, True, 1, False),
+]
+
+
+@pytest.mark.parametrize("B,N,block,periodic,R,with_pad", MASK_CASES)
+def test_radius_mask_matches_oracle_bitwise(cuda, B, N, block, periodic, R, with_pad):
+    print(f"radius_mask B={B} N={N} block={block} periodic={periodic} R={R} pad={with_pad}", flush=True)
+    rng = np.random.default_rng(N + block)
+    if periodic:
+        coords = rng.random((B, N, 3)).astype(np.float32)
+        gram = lattice_y1_to_gram(_cells(B, N))
+        cutoff = 4.0
+    else:
+        coords = (rng.standard_normal((B, N, 3)) * 3).astype(np.float32)
+        gram = None
+        cutoff = 3.0
+    pad = (rng.random((B, N)) < 0.15) if with_pad else None
+    bits, blocks = radius_mask(torch.from_numpy(coords).to(cuda), cutoff,
+                               gram=None if gram is None else torch.from_numpy(gram).to(cuda),
+                               pad_mask=None if pad is None else torch.from_numpy(pad).to(cuda), pbc_radius=R,
+                               block=block)
+    rbits, rblocks = oracle_radius_mask(coords, cutoff, gram=gram, pad_mask=pad, pbc_radius=R, block=block)
+    np.testing.assert_array_equal(_bits_u32(bits), rbits)
+    np.testing.assert_array_equal(blocks.cpu().numpy(), rblocks)
+
+
+def test_radius_mask_skewed_cell_without_pruning(cuda):
+    """A cell too skewed for the image bound: every image is evaluated."""
+    B, N = 2, 120
+    rng = np.random.default_rng(11)
+    coords = rng.random((B, N, 3)).astype(np.float32)
+    y1 = np.array([[np.log(6.0), np.log(7.0), np.log(8.0), np.cos(np.deg2rad(25.0)), np.cos(np.deg2rad(30.0)),
+                    np.cos(np.deg2rad(40.0))]] * B, np.float32)
+    gram = lattice_y1_to_gram(y1)
+    bits, blocks = radius_mask(torch.from_numpy(coords).to(cuda), 5.0, gram=torch.from_numpy(gram).to(cuda))
+    rbits, rblocks = oracle_radius_mask(coords, 5.0, gram=gram)
+    np.testing.assert_array_equal(_bits_u32(bits), rbits)
+    np.testing.assert_array_equal(blocks.cpu().numpy(), rblocks)
+
+
+def test_radius_mask_minimum_image_kat(cuda):
+    # tests/test_geometry.py:30-39 of the reference: identity cell, distance 0.2
+    frac = torch.tensor([[[0.1, 0.0, 0.0], [0.9, 0.0, 0.0]]])
+    lattice = torch.zeros(1, 6)
+    bits, _ = radius_mask(frac.to(cuda), 0.25, lattice=lattice.to(cuda))
+    assert _bits_u32(bits)[0, :, 0].tolist() == [3, 3]
+    bits, _ = radius_mask(frac.to(cuda), 0.15, lattice=lattice.to(cuda))
+    assert _bits_u32(bits)[0, :, 0].tolist() == [1, 2]
+
+
+def test_lattice_to_gram_matches_reference_golden(cuda):
+    z = np.load(GOLDEN / "geometry_periodic.npz")
+    g = lattice_to_gram(torch.from_numpy(z["lattice_y1"]).to(cuda))
+    np.testing.assert_allclose(g.cpu().numpy(), z["gram"], rtol=2e-6, atol=1e-4)
+
+
+def test_radius_mask_config4_full_size(cuda):
+    w = radius_workload()
+    gram = lattice_y1_to_gram(w.lattice.numpy())
+    bits, blocks = radius_mask(w.frac.to(cuda), w.cutoff, gram=torch.from_numpy(gram).to(cuda))
+    rbits, rblocks = oracle_radius_mask(w.frac.numpy(), w.cutoff, gram=gram)
+    np.testing.assert_array_equal(_bits_u32(bits), rbits)
+    np.testing.assert_array_equal(blocks.cpu().numpy(), rblocks)
+    density = unpack_bits(rbits, 512).mean()
+    assert 0.05 < density < 0.2, density
+
+
+# ----------------------------------------------------------------------------- radius attention
+
+def _attn_case(B, H, N, D, seed, density=0.15, empty_rows=0):
+    gen = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, H, N, D, generator=gen) for _ in range(3))
+    mask = torch.rand(B, N, N, generator=gen) < density
+    mask |= torch.eye(N, dtype=torch.bool)[None]
+    if empty_rows:
+        mask[0, -empty_rows:, :] = False
+    return q, k, v, mask
+
+
+def _pack(mask: torch.Tensor, block: int = 64):
+    B, N, _ = mask.shape
+    W = (N + 31) // 32
+    padded = torch.zeros(B, N, W * 32, dtype=torch.bool)
+    padded[..., :N] = mask
+    weights = (1 << torch.arange(32, dtype=torch.int64))
+    words = (padded.reshape(B, N, W, 32).to(torch.int64) * weights).sum(-1)
+    bits = words.to(torch.uint32).view(torch.int32) if hasattr(torch, "uint32") else None
+    if bits is None:
+        bits = torch.from_numpy(words.numpy().astype(np.uint32).view(np.int32))
+    NB = (N + block - 1) // block
+    blocks = torch.zeros(B, NB, NB, dtype=torch.uint8)
+    for bi in range(NB):
+        for bj in range(NB):
+            blocks[:, bi, bj] = mask[:, bi * block:(bi + 1) * block, bj * block:(bj + 1) * block].flatten(1).any(1)
+    return bits, blocks
+
+
+ATTN_CASES = [
+    # B, H, N, D, dtype, use_block_mask, empty_rows
+    (1, 1, 5, 32, torch.bfloat16, True, 0),
+    (2, 3, 70, 64, torch.bfloat16, True, 3),
+    (2, 2, 130, 64, torch.float16, False, 0),
+    (1, 4, 200, 128, torch.bfloat16, True, 5),
+    (2, 2, 64, 32, torch.float16, True, 0),
+]
+
+
+@pytest.mark.parametrize("B,H,N,D,dtype,use_blocks,empty", ATTN_CASES)
+def test_radius_attention_matches_fp64_masked_softmax(cuda, B, H, N, D, dtype, use_blocks, empty):
+    print(f"radius_attn B={B} H={H} N={N} D={D} {dtype} blocks={use_blocks} empty={empty}", flush=True)
+    q, k, v, mask = _attn_case(B, H, N, D, seed=N + D, empty_rows=empty)
+    bits, blocks = _pack(mask)
+    ops = [t.to(dtype) for t in (q, k, v)]
+    scale = D ** -0.5
+    out, lse, out32 = radius_attention(*(t.to(cuda) for t in ops), bits.to(cuda),
+                                       blocks.to(cuda) if use_blocks else None, scale=scale, return_lse=True,
+                                       return_fp32=True)
+    ref, ref_lse = masked_attention_fp64(*(t.double().numpy() for t in ops), mask.numpy(), scale)
+    tol = 2e-2 if dtype == torch.bfloat16 else 5e-3
+    got = out32.cpu().double().numpy()
+    err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert err <= tol, err
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=3e-2, rtol=0)
+    torch.testing.assert_close(out.cpu().float(), out32.cpu().to(dtype).float(), rtol=0, atol=0)
+    if empty:
+        assert (out32[0, :, -empty:] == 0).all() and (lse[0, :, -empty:] == 0).all()
+    # torch fp32 reference of the same op
+    tq, tk, tv = (t.float() for t in ops)
+    t_ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask[:, None], scale=scale)
+    t_ref = torch.where(mask.any(-1)[:, None, :, None], t_ref, torch.zeros(()))
+    terr = (out32.cpu() - t_ref).norm() / t_ref.norm()
+    assert terr <= tol, terr
+
+
+def test_radius_attention_block_skipping_is_exact(cuda):
+    q, k, v, _ = _attn_case(1, 2, 256, 64, seed=5)
+    # a banded mask: only tiles near the diagonal are active
+    i = torch.arange(256)
+    mask = ((i[:, None] - i[None, :]).abs() <= 20)[None]
+    bits, blocks = _pack(mask)
+    assert blocks.float().mean() < 0.7
+    ops = [t.to(torch.bfloat16).to(cuda) for t in (q, k, v)]
+    a = radius_attention(*ops, bits.to(cuda), blocks.to(cuda), return_fp32=True)[1]
+    b = radius_attention(*ops, bits.to(cuda), None, return_fp32=True)[1]
+    assert torch.equal(a, b)
+
+
+def test_radius_attention_config4_full_size(cuda):
+    w = radius_workload()
+    gram = lattice_to_gram(w.lattice.to(cuda))
+    bits, blocks = radius_mask(w.frac.to(cuda), w.cutoff, gram=gram)
+    ops = [t.to(torch.bfloat16).to(cuda) for t in (w.q, w.k, w.v)]
+    out, lse, out32 = radius_attention(*ops, bits, blocks, return_lse=True, return_fp32=True)
+    torch.cuda.synchronize()
+    mask = torch.from_numpy(unpack_bits(_bits_u32(bits), 512))
+    tq, tk, tv = (t.float().cpu() for t in ops)
+    ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask[:, None])
+    err = (out32.cpu() - ref).norm() / ref.norm()
+    assert err <= 2e-2, err
+    assert torch.isfinite(lse).all()
