@@ -11,11 +11,22 @@ already resident in HBM.
 value = valid FLOPs (sum_b 4 H D n_b^3) / step time, in TFLOP/s.
 
 Prints ONE JSON line.  Also reports:
-  roofline      the kernel's achieved TFLOP/s against the bf16 dense MFMA peak,
-                timed with HIP events on the launch stream; `traffic` comes from
-                the committed rocprofv3 --pmc summary when present;
+  roofline      the entry point's achieved TFLOP/s against the bf16 dense MFMA
+                peak: valid FLOPs over the average duration of one
+                mf_simplicial_fwd launch sequence (plan kernel + main kernel +
+                the pass for molecules above one key chunk), timed with HIP
+                events on the launch stream; `traffic` is the HBM bytes of one
+                such sequence from the committed rocprofv3 --pmc summary
+                (profiles/simplicial_fwd_geom_traffic.json) when present;
   cpu_baseline  the oracle's torch-CPU restatement of the reference path
-                (padded N, chunk 128, bf16 as configured) on a bounded sample.
+                (padded N, chunk 128, bf16 as configured) on the whole batch.
+
+Other workloads (one JSON line each, not the headline):
+  --workload knn          kNN top-16 at B=32 and scaled to
+                          B=32*1024 for the HBM roofline;
+  --workload radius       radius mask + radius attention (configs[3]);
+  --copy-calibration      a plain device copy of known size, run under
+                          rocprofv3 --pmc to scale FETCH_SIZE / WRITE_SIZE.
 """
 
 from __future__ import annotations
@@ -40,8 +51,11 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-sample", type=int, default=32, help="molecules in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--cpu-sample", type=int, default=64, help="molecules in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0 = min(16, cores))")
+    ap.add_argument("--workload", choices=("simplicial", "knn", "radius"), default="simplicial")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a plain 512 MiB device copy (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -86,13 +100,170 @@ def cpu_baseline(workload, sample: int, threads: int):
     }
 
 
+def event_times(stream, fn, launches: int):
+    """Median and mean duration (ms) of single launches of fn, one HIP event pair
+    each, recorded on the stream the kernels run on."""
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(launches)]
+    for a, b in evs:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in evs)
+    return t[len(t) // 2], sum(t) / len(t)
+
+
+def timed_loop(stream, fn, steps: int, warmup: int):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps, time.perf_counter() - t0
+
+
+def copy_calibration() -> int:
+    """512 MiB device-to-device copy, 5 launches: FETCH_SIZE and WRITE_SIZE of
+    one dispatch should each read 524288 KiB on an exact counter."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    n = 512 * 1024 * 1024 // 4
+    src = torch.arange(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    assert torch.equal(dst[-4:], src[-4:])
+    print(json.dumps({"copy_bytes": n * 4, "launches": 5}), flush=True)
+    return 0
+
+
+def bench_knn(args) -> int:
+    import torch
+
+    from matterformer_amd.geometry_ops import knn_graph
+    from matterformer_amd.workloads import knn_workload
+
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    small = knn_workload()
+    scaled = knn_workload(batch=32 * 1024)
+    res = {}
+    for name, w in (("c3", small), ("scaled", scaled)):
+        c = w.coords.to(dev)
+        B, N, _ = c.shape
+        step = lambda: knn_graph(c, w.k)  # noqa: E731
+        ms, _ = timed_loop(stream, step, args.steps, args.warmup)
+        med, _ = event_times(stream, step, 50)
+        nbytes = B * N * 3 * 4 + B * N * w.k * 8
+        res[name] = {"B": B, "ms": ms, "kernel_ms": med, "bytes": nbytes, "queries": B * N}
+    cpu = None
+    if args.cpu_sample > 0:
+        from oracle.native import knn as oracle_knn
+
+        n_cpu = min(args.cpu_sample * 128, scaled.coords.shape[0])
+        sample = scaled.coords[:n_cpu].numpy()
+        t0 = time.perf_counter()
+        oracle_knn(sample, scaled.k)
+        el = time.perf_counter() - t0
+        cpu = {"value": n_cpu * 181 / el, "unit": "queries/s", "cores": 1, "kind": "port",
+               "sample": f"oracle/knn.c (gcc -O2, 1 thread) on {n_cpu} molecules x 181 atoms, k=16; {el:.2f} s"}
+    sc = res["scaled"]
+    achieved = sc["bytes"] / (sc["kernel_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "kNN top-16 queries/s (configs[2] scaled to 32768 molecules)",
+        "value": round(sc["queries"] / (sc["ms"] * 1e-3), 1),
+        "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(sc["ms"], 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded, BASELINE.json configs[2])",
+        "config": {"workload": "kNN top-16, 181 atoms/molecule, coords N(0, 2 A^2)", "batch": sc["B"], "atoms": 181,
+                   "k": 16, "c3_batch32_ms": round(res["c3"]["ms"], 5)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("knn_c3_scaled"),
+                     "kernel": "mf::knn::knn_kernel<16, 4>", "kernel_ms": round(sc["kernel_ms"], 5)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_radius(args) -> int:
+    import torch
+
+    from matterformer_amd.geometry_ops import lattice_to_gram, radius_attention, radius_mask
+    from matterformer_amd.workloads import radius_workload
+
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    w = radius_workload()
+    frac = w.frac.to(dev)
+    gram = lattice_to_gram(w.lattice.to(dev))
+    q, k, v = (t.to(torch.bfloat16).to(dev) for t in (w.q, w.k, w.v))
+    bits, blocks = radius_mask(frac, w.cutoff, gram=gram)
+    pairs = 0
+    words = bits.cpu().numpy().view("uint32")
+    import numpy as np
+
+    pairs = int(np.unpackbits(words.view(np.uint8)).sum())
+    B, H, N, D = q.shape
+    mask_step = lambda: radius_mask(frac, w.cutoff, gram=gram)  # noqa: E731
+    attn_step = lambda: radius_attention(q, k, v, bits, blocks)  # noqa: E731
+    both = lambda: radius_attention(q, k, v, *radius_mask(frac, w.cutoff, gram=gram))  # noqa: E731
+    ms, _ = timed_loop(stream, both, args.steps, args.warmup)
+    mask_ms, _ = event_times(stream, mask_step, 50)
+    attn_ms, _ = event_times(stream, attn_step, 50)
+    flops = w.attention_flops(pairs)
+    attn_bytes = 4 * B * H * N * D * 2 + bits.numel() * 4 + blocks.numel()
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_sample > 0:
+        from oracle.native import radius_mask as oracle_radius_mask
+        from oracle.native import unpack_bits
+        from oracle.radius import masked_attention_fp64
+
+        g = gram.cpu().numpy()
+        t0 = time.perf_counter()
+        rb, _ = oracle_radius_mask(w.frac.numpy(), w.cutoff, gram=g)
+        masked_attention_fp64(*(t.float().cpu().numpy() for t in (q, k, v)), unpack_bits(rb, N), D ** -0.5)
+        el = time.perf_counter() - t0
+        cpu = {"value": B / el, "unit": "cells/s", "cores": 1, "kind": "port",
+               "sample": f"oracle radius mask (C, 1 thread) + float64 numpy masked softmax, all 8 cells; {el:.2f} s"}
+    line = {
+        "metric": "radius mask + radius attention cells/s (configs[3])",
+        "value": round(B / (ms * 1e-3), 1), "unit": "cells/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded, BASELINE.json configs[3])",
+        "config": {"workload": "periodic MOF cells, 6 A cutoff, minimum image, 64-atom tiles", "cells": B,
+                   "atoms": N, "heads": H, "head_dim": D, "allowed_pairs": pairs,
+                   "mask_ms": round(mask_ms, 5), "attn_ms": round(attn_ms, 5),
+                   "attn_valid_gflop": round(flops / 1e9, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("radius_attn_c4"),
+                     "kernel": "mf::rattn::radius_attn_kernel<bf16, 64>", "kernel_ms": round(attn_ms, 5)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "the simplicial forward has no cross-GPU exchange, see DESIGN.md for how it shards.",
-              file=sys.stderr)
+              "every kernel here works per molecule or per cell with no cross-GPU exchange, "
+              "see DESIGN.md for how the path would shard.", file=sys.stderr)
         return 2
 
     import torch
@@ -103,6 +274,12 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        return copy_calibration()
+    if args.workload == "knn":
+        return bench_knn(args)
+    if args.workload == "radius":
+        return bench_radius(args)
     dev = torch.device("cuda", 0)
     lib = _native.lib()
 
@@ -130,35 +307,15 @@ def main() -> int:
         if st != 0:
             raise RuntimeError(f"mf_simplicial_fwd failed: {_native.last_error()}")
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        step()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = start.elapsed_time(stop)
-    ms_per_step = gpu_ms / args.steps
+    ms_per_step, wall = timed_loop(stream, step, args.steps, args.warmup)
 
     flops = w.valid_flops()
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     atoms = int(w.counts.sum())
 
-    # Per-launch kernel time: one event pair per launch, averaged (same stream).
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(50)]
-    for a, b in evs:
-        a.record(stream)
-        step()
-        b.record(stream)
-    torch.cuda.synchronize()
-    kernel_ms = sorted(a.elapsed_time(b) for a, b in evs)[len(evs) // 2]
+    # Per-launch duration of the launch sequence: one event pair per launch on
+    # the launch stream (median and mean of 100 launches).
+    kernel_ms, kernel_mean_ms = event_times(stream, step, 100)
     achieved = flops / (kernel_ms * 1e-3) / 1e12
 
     cpu = cpu_baseline(w, args.cpu_sample, args.cpu_threads) if args.cpu_sample > 0 else None
@@ -192,8 +349,10 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / BF16_DENSE_PEAK_TFLOPS, 5),
             "traffic": committed_traffic("simplicial_fwd_geom"),
-            "kernel": "mf::simplicial::simplicial_fwd_kernel<__bf16, 64>",
+            "kernel": ("mf_simplicial_fwd launch sequence: simplicial_plan_kernel + "
+                       "simplicial_fast_kernel<bf16,64,5,small> + simplicial_fast_kernel<bf16,64,5,large>"),
             "kernel_ms": round(kernel_ms, 5),
+            "kernel_mean_ms": round(kernel_mean_ms, 5),
         },
         "cpu_baseline": cpu,
     }
