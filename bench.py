@@ -80,22 +80,27 @@ def cpu_baseline(workload, sample: int, threads: int):
     torch.set_num_threads(threads)
     bf = [t[:sample].to(torch.bfloat16) for t in (workload.q, workload.k1, workload.v1, workload.k2, workload.v2)]
     group = 8
+    passes = 0
     t0 = time.perf_counter()
-    for s in range(0, sample, group):
-        e = min(sample, s + group)
-        reference_path(*(t[s:e] for t in bf), workload.query_valid[s:e], workload.pair_key_valid[s:e],
-                       chunk_size=128)
+    # whole passes over the sample until about 10 s of CPU work (at most 5)
+    while passes < 5 and (passes == 0 or time.perf_counter() - t0 < 10.0):
+        for s in range(0, sample, group):
+            e = min(sample, s + group)
+            reference_path(*(t[s:e] for t in bf), workload.query_valid[s:e], workload.pair_key_valid[s:e],
+                           chunk_size=128)
+        passes += 1
     elapsed = time.perf_counter() - t0
     n = workload.counts[:sample].to(torch.int64)
-    flops = 4 * workload.q.shape[1] * workload.q.shape[3] * int((n ** 3).sum())
+    flops = passes * 4 * workload.q.shape[1] * workload.q.shape[3] * int((n ** 3).sum())
     return {
         "value": flops / elapsed / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"first {sample} of the 64 GEOM molecules, bf16, padded N=181, chunk_size 128, "
-                   f"torch CPU restatement of simplicial_attention_torch_from_projected; {elapsed:.2f} s"),
-        "molecules_per_s": sample / elapsed,
+        "sample": (f"{passes} pass(es) over the first {sample} of the 64 GEOM molecules, bf16, padded N=181, "
+                   f"chunk_size 128, torch CPU restatement of simplicial_attention_torch_from_projected; "
+                   f"{elapsed:.2f} s"),
+        "molecules_per_s": passes * sample / elapsed,
         "seconds": elapsed,
     }
 
