@@ -76,11 +76,11 @@ typedef _Float16 f16x2_e __attribute__((ext_vector_type(2)));
 
 // Workspace of one launch slice (B molecules of N tokens, H heads), in ints:
 //   hdr[4]              n_small_items, n_large_items
-//   nkq[B]              nk << 16 | nq
-//   kidx[B][N]          valid key positions, compacted
-//   qidx[B][N]          valid query positions, compacted
-//   zidx[B][N]          padded query positions (N - nq of them)
-//   small[MI][4]        items (b, h, q0 | q1 << 16, nk) of molecules with nk <= CH
+//   nkq[B]              molecule info word (see info_*)
+//   kidx[B][N]          valid key positions, compacted (only for molecules
+//                       whose valid keys are not the prefix 0..nk-1)
+//   qidx[B][N]          valid query positions, compacted (likewise)
+//   small[MI][4]        items (b, h, q0 | q1 << 16, info) of molecules with nk <= CH
 //   large[MI][4]        items of molecules with nk > CH
 // with MI = B * H * ceil(N / kWaves), a bound on the item count of either kind.
 struct Workspace {
@@ -88,7 +88,6 @@ struct Workspace {
   int* nkq;
   int* kidx;
   int* qidx;
-  int* zidx;
   int4* small_items;
   int4* large_items;
 };
@@ -108,8 +107,6 @@ __host__ __device__ inline Workspace carve_workspace(void* base, int B, int H, i
   p += size_t(B) * N;
   w.qidx = p;
   p += size_t(B) * N;
-  w.zidx = p;
-  p += size_t(B) * N;
   p += (4 - (reinterpret_cast<uintptr_t>(p) / 4) % 4) % 4;  // 16-byte alignment
   w.small_items = reinterpret_cast<int4*>(p);
   w.large_items = w.small_items + max_items(B, H, N);
@@ -117,7 +114,7 @@ __host__ __device__ inline Workspace carve_workspace(void* base, int B, int H, i
 }
 
 __host__ inline size_t workspace_bytes(int B, int H, int N) {
-  return (4 + size_t(B) + 3 * size_t(B) * N + 4) * 4 + 2 * max_items(B, H, N) * sizeof(int4);
+  return (4 + size_t(B) + 2 * size_t(B) * N + 4) * 4 + 2 * max_items(B, H, N) * sizeof(int4);
 }
 
 struct Params {
@@ -390,185 +387,201 @@ __device__ __forceinline__ void with_tiles(int n, F&& f) {
 // ---------------------------------------------------------------------------
 // plan: one workgroup of kPlanThreads builds the workspace.
 // ---------------------------------------------------------------------------
+// Molecule info word: nk | kpre << 30 | qpre << 31 in item.w, and
+// nq | nk << 15 | kpre << 30 | qpre << 31 in nkq[b]; kpre / qpre: the valid
+// keys / queries are exactly the prefix 0..n-1 (no index list needed).
+__device__ __forceinline__ int info_nq(uint32_t w) { return int(w & 0x7fffu); }
+__device__ __forceinline__ int info_nk(uint32_t w) { return int((w >> 15) & 0x7fffu); }
+constexpr uint32_t kKPre = 1u << 30;
+constexpr uint32_t kQPre = 1u << 31;
+
 __device__ __forceinline__ int plan_queries_per_item(int nk, int cls, int work_target) {
   if (cls) return kWaves;
   int qpi = max(kWaves, min(work_target / max(nk * nk, 1), kMaxQueriesPerItem));
   return qpi - qpi % kWaves;
 }
 
+// One aligned dword of a mask row per lane: bytes of lane l are atoms
+// t = boff + e - off (e = 0..3).  Adds the valid bytes to `count` and notes a
+// "rise" (a valid atom right after an invalid one) in `rise`; `carry` is the
+// validity of the atom before the window (1 before the row).  Ballots and
+// scalar mask arithmetic only.
+__device__ __forceinline__ void scan_word(uint32_t w, int boff, int off, int N, int& carry, int& count, bool& rise) {
+  bool cb[4], pb[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = boff + e - off;
+    const bool in = t >= 0 && t < N;
+    cb[e] = in && ((w >> (8 * e)) & 0xffu) != 0;
+    pb[e] = t < 0 || cb[e];  // bytes before the row count as valid predecessors
+  }
+  const bool inner = (cb[1] && !pb[0]) || (cb[2] && !pb[1]) || (cb[3] && !pb[2]);
+  const unsigned long long b0 = __ballot(cb[0]);
+  const unsigned long long p3 = __ballot(pb[3]);
+  // byte 0 of lane l follows byte 3 of lane l - 1 (lane 0: the carry)
+  const unsigned long long pred = (p3 << 1) | (unsigned long long)(carry & 1);
+  rise = rise || __ballot(inner) != 0ull || (b0 & ~pred) != 0ull;
+  count += __popcll(b0) + __popcll(__ballot(cb[1])) + __popcll(__ballot(cb[2])) + __popcll(__ballot(cb[3]));
+  carry = int(p3 >> 63);
+}
+
+// The aligned dword at window offset base + 4 lane of a mask row (0 past the
+// row).  A dword that starts inside [row - off, row + N) stays on the row's
+// pages.
+__device__ __forceinline__ uint32_t load_window(const uint8_t* row, int N, int base, int lane, int& off) {
+  const uintptr_t start = reinterpret_cast<uintptr_t>(row);
+  const uintptr_t astart = start & ~uintptr_t(3);
+  off = int(start - astart);
+  const int boff = base + 4 * lane;
+  return boff < off + N ? *reinterpret_cast<const uint32_t*>(astart + boff) : 0u;
+}
+
+// dst[r] = the atom of valid rank r in a mask row (one wave).
+__device__ void write_ranks(const uint8_t* row, int N, int* dst, int lane) {
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int run = 0;
+  for (int base = 0; base < N; base += 256) {
+    uint8_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = base + 64 * u + lane;
+      v[u] = t < N ? row[t] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = base + 64 * u + lane;
+      const bool ok = t < N && v[u] != 0;
+      const unsigned long long bal = __ballot(ok);
+      if (ok) dst[run + __popcll(bal & below)] = t;
+      run += __popcll(bal);
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p) {
-  __shared__ int s_nkq[kMaxBatch];
+  constexpr int kPlanWaves = kPlanThreads / 64;
+  constexpr int kRound = 4;  // molecule rows a wave loads at once
+  __shared__ uint32_t s_info[kMaxBatch];
   __shared__ unsigned long long s_key[kMaxBatch];  // class, cost (descending), molecule
-  __shared__ int s_items[kMaxBatch];                // items at each sorted position
-  __shared__ int s_off[kMaxBatch + 1];              // exclusive scan of s_items
-  __shared__ int s_wsum[kPlanThreads / 64];
-  __shared__ int s_nsmall;
+  __shared__ int s_items[kMaxBatch];               // items of each molecule
+  __shared__ int s_order[kMaxBatch];               // molecule (| class << 16) at each sorted position
+  __shared__ int s_off[kMaxBatch + 1];             // first item of each sorted position
+  __shared__ int s_small;                          // items of the small class
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int B = p.B, H = p.H, N = p.N;
   const Workspace& ws = p.ws;
 
-  // 1. compacted key / query / padded-row lists, one wave per molecule; the
-  //    first 256 positions of 4 molecules are loaded before any is used
-  constexpr int kPlanWaves = kPlanThreads / 64;
-  for (int b0 = wave; b0 < B; b0 += 4 * kPlanWaves) {
-    uint8_t kv[4][4], qv[4][4];
+  // 1. valid keys / queries per molecule and whether they form a prefix
+  if (N <= 252) {
+    // one aligned 256-byte window covers a row
+    for (int b0 = wave; b0 < B; b0 += kPlanWaves * kRound) {
+      uint32_t wk[kRound], wq[kRound];
+      int offk[kRound], offq[kRound];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int b = b0 + m * kPlanWaves;
+      for (int m = 0; m < kRound; ++m) {
+        const int b = b0 + m * kPlanWaves;
+        wk[m] = wq[m] = 0u;
+        offk[m] = offq[m] = 0;
+        if (b < B) {
+          wk[m] = load_window(p.pkv + size_t(b) * N, N, 0, lane, offk[m]);
+          wq[m] = load_window(p.qv + size_t(b) * N, N, 0, lane, offq[m]);
+        }
+      }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int t = u * 64 + lane;
-        const bool in = b < B && t < N;
-        kv[m][u] = in ? p.pkv[size_t(b) * N + t] : 0;
-        qv[m][u] = in ? p.qv[size_t(b) * N + t] : 0;
+      for (int m = 0; m < kRound; ++m) {
+        const int b = b0 + m * kPlanWaves;
+        if (b >= B) break;
+        int ck = 0, cq = 0, carry_k = 1, carry_q = 1;
+        bool rk = false, rq = false;
+        scan_word(wk[m], 4 * lane, offk[m], N, carry_k, ck, rk);
+        scan_word(wq[m], 4 * lane, offq[m], N, carry_q, cq, rq);
+        if (lane == 0) s_info[b] = uint32_t(cq) | (uint32_t(ck) << 15) | (rk ? 0u : kKPre) | (rq ? 0u : kQPre);
       }
     }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int b = b0 + m * kPlanWaves;
-      if (b >= B) break;
-      int ck = 0, cq = 0, cz = 0;
-      const unsigned long long below = (1ull << lane) - 1ull;
-      for (int base = 0; base < N; base += 256) {
-        uint8_t kk[4], qq[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (base == 0) {
-            kk[u] = kv[m][u];
-            qq[u] = qv[m][u];
-          } else {
-            const int t = base + u * 64 + lane;
-            kk[u] = t < N ? p.pkv[size_t(b) * N + t] : 0;
-            qq[u] = t < N ? p.qv[size_t(b) * N + t] : 0;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int t = base + u * 64 + lane;
-          const bool in = t < N;
-          const unsigned long long bk = __ballot(in && kk[u] != 0);
-          const unsigned long long bq = __ballot(in && qq[u] != 0);
-          const unsigned long long bz = __ballot(in && qq[u] == 0);
-          if (in && kk[u] != 0) ws.kidx[size_t(b) * N + ck + __popcll(bk & below)] = t;
-          if (in && qq[u] != 0) ws.qidx[size_t(b) * N + cq + __popcll(bq & below)] = t;
-          if (in && qq[u] == 0) ws.zidx[size_t(b) * N + cz + __popcll(bz & below)] = t;
-          ck += __popcll(bk);
-          cq += __popcll(bq);
-          cz += __popcll(bz);
-        }
+  } else {
+    for (int b = wave; b < B; b += kPlanWaves) {
+      int ck = 0, cq = 0, carry_k = 1, carry_q = 1;
+      bool rk = false, rq = false;
+      for (int base = 0; base < N + 3; base += 256) {
+        int offk, offq;
+        const uint32_t wk = load_window(p.pkv + size_t(b) * N, N, base, lane, offk);
+        const uint32_t wq = load_window(p.qv + size_t(b) * N, N, base, lane, offq);
+        scan_word(wk, base + 4 * lane, offk, N, carry_k, ck, rk);
+        scan_word(wq, base + 4 * lane, offq, N, carry_q, cq, rq);
       }
-      if (lane == 0) {
-        s_nkq[b] = (ck << 16) | cq;
-        ws.nkq[b] = (ck << 16) | cq;
-      }
+      if (lane == 0) s_info[b] = uint32_t(cq) | (uint32_t(ck) << 15) | (rk ? 0u : kKPre) | (rq ? 0u : kQPre);
     }
   }
   __syncthreads();
 
-  // 2. sort molecules by (class, cost descending, index): bitonic over the
-  //    next power of two >= B keys, in one wave's registers when B <= 64
-  {
-    unsigned long long key = ~0ull;  // padding sorts last
-    if (tid < B) {
-      const int nk = s_nkq[tid] >> 16, nq = s_nkq[tid] & 0xffff;
-      const unsigned long long cls = nk > p.cap ? 1ull : 0ull;
-      const unsigned long long cost = (unsigned long long)nq * nk * nk;  // < 2^45
-      key = (cls << 62) | (((1ull << 46) - 1ull - cost) << 10) | (unsigned long long)tid;
-    }
-    int P = 1;
-    while (P < B) P <<= 1;
-    if (P <= 64) {
-      if (wave == 0) {
-        for (int k = 2; k <= 64; k <<= 1) {
-          for (int j = k >> 1; j > 0; j >>= 1) {
-            const unsigned long long y = __shfl_xor(key, j, 64);
-            const bool up = (lane & k) == 0;
-            const bool low = (lane & j) == 0;
-            key = (low == up) ? (key < y ? key : y) : (key > y ? key : y);
-          }
-        }
-        s_key[lane] = key;
-      }
-    } else {
-      s_key[tid] = key;
-      __syncthreads();
-      for (int k = 2; k <= P; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-          const int partner = tid ^ j;
-          if (tid < P && partner > tid) {
-            const unsigned long long x = s_key[tid], y = s_key[partner];
-            const bool up = (tid & k) == 0;
-            if ((x > y) == up) {
-              s_key[tid] = y;
-              s_key[partner] = x;
-            }
-          }
-          __syncthreads();
-        }
-      }
-    }
-    __syncthreads();
+  // 2. index lists of the molecules that need them
+  for (int b = wave; b < B; b += kPlanWaves) {
+    const uint32_t w = s_info[b];
+    if (!(w & kKPre)) write_ranks(p.pkv + size_t(b) * N, N, ws.kidx + size_t(b) * N, lane);
+    if (!(w & kQPre)) write_ranks(p.qv + size_t(b) * N, N, ws.qidx + size_t(b) * N, lane);
   }
-  // 3. items per sorted position, block-wide exclusive scan
-  int items = 0;
+
+  // 3. molecules in (class, cost descending, index) order and the first item
+  //    of each: every thread ranks its molecule against all others
+  unsigned long long key = ~0ull;
+  int cls = 0;
   if (tid < B) {
-    const int b = int(s_key[tid] & 1023ull);
-    const int cls = int(s_key[tid] >> 62);
-    const int nk = s_nkq[b] >> 16, nq = s_nkq[b] & 0xffff;
+    const uint32_t w = s_info[tid];
+    const int nk = info_nk(w), nq = info_nq(w);
+    cls = nk > p.cap ? 1 : 0;
+    const unsigned long long cost = (unsigned long long)nq * nk * nk;  // < 2^45
+    key = ((unsigned long long)cls << 62) | (((1ull << 46) - 1ull - cost) << 10) | (unsigned long long)tid;
     const int qpi = plan_queries_per_item(nk, cls, p.work_target);
-    items = nq > 0 ? H * ((nq + qpi - 1) / qpi) : 0;
-    if (cls == 0 && (tid == B - 1 || (s_key[tid + 1] >> 62) != 0)) s_nsmall = tid + 1;
-    if (cls == 1 && tid == 0) s_nsmall = 0;
+    s_items[tid] = nq > 0 ? H * ((nq + qpi - 1) / qpi) : 0;
+    s_key[tid] = key;
   }
-  s_items[tid] = items;
-  int x = items;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
-  if (lane == 63) s_wsum[wave] = x;
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < kPlanThreads / 64; ++w) {
-      const int v = s_wsum[w];
-      s_wsum[w] = run;
-      run += v;
+  int rank = 0, off = 0, total = 0, total_small = 0;
+  if (wave * 64 < B) {  // only the waves that hold molecules
+#pragma unroll 4
+    for (int u = 0; u < B; ++u) {
+      const unsigned long long ku = s_key[u];
+      const int iu = s_items[u];
+      const bool before = ku < key;
+      rank += before ? 1 : 0;
+      off += before ? iu : 0;
+      total += iu;
+      total_small += (ku >> 62) == 0ull ? iu : 0;
     }
   }
-  __syncthreads();
-  s_off[tid] = s_wsum[wave] + x - items;
-  if (tid == kPlanThreads - 1) s_off[kPlanThreads] = s_wsum[wave] + x;
-  __syncthreads();
-  const int nsmall = B > 0 ? s_nsmall : 0;
-  const int small_total = s_off[nsmall];
-  const int large_total = s_off[B] - small_total;
-  if (tid == 0) {
-    ws.hdr[0] = small_total;
-    ws.hdr[1] = large_total;
-    ws.hdr[2] = 0;  // next small item to hand out
-    ws.hdr[3] = 0;  // next large item to hand out
+  if (tid < B) {
+    s_order[rank] = tid | (cls << 16);
+    s_off[rank] = off;
   }
+  if (tid == 0) {
+    s_off[B] = total;
+    s_small = total_small;
+    ws.hdr[0] = total_small;
+    ws.hdr[1] = total - total_small;
+  }
+  __syncthreads();
 
   // 4. items: one molecule's items are contiguous, heads interleaved with its
   //    query ranges; small items first (in cost order), then large ones
+  const int small_total = s_small;
   for (int u = tid; u < s_off[B]; u += kPlanThreads) {
     int lo = 0, hi = B - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (s_off[mid] <= u) lo = mid; else hi = mid - 1;
     }
-    const int b = int(s_key[lo] & 1023ull);
-    const int cls = int(s_key[lo] >> 62);
-    const int nk = s_nkq[b] >> 16, nq = s_nkq[b] & 0xffff;
-    const int qpi = plan_queries_per_item(nk, cls, p.work_target);
+    const int ord = s_order[lo];
+    const int b = ord & 0xffff;
+    const int c = ord >> 16;
+    const uint32_t w = s_info[b];
+    const int nk = info_nk(w), nq = info_nq(w);
+    const int qpi = plan_queries_per_item(nk, c, p.work_target);
     const int local = u - s_off[lo];
     const int s = local / H, h = local - s * H;
-    const int4 item{b, h, (s * qpi) | (min(nq, (s + 1) * qpi) << 16), nk};
-    if (cls == 0) ws.small_items[u] = item;
+    const int4 item{b, h, (s * qpi) | (min(nq, (s + 1) * qpi) << 16), int(uint32_t(nk) | (w & (kKPre | kQPre)))};
+    if (c == 0) ws.small_items[u] = item;
     else ws.large_items[u - small_total] = item;
   }
 }
@@ -591,6 +604,10 @@ __device__ __forceinline__ typename Half<T>::Op8 load8(const T* row, int e0, int
   return v;
 }
 
+// Position of the valid atom of rank r: the identity when the valid atoms are
+// a prefix (idx == nullptr), else the plan's compacted list.
+__device__ __forceinline__ int atom_at(const int* idx, int r) { return idx ? idx[r] : r; }
+
 template <typename T>
 __device__ __forceinline__ typename Half<T>::Op8 zero8() {
   typename Half<T>::Op8 v;
@@ -599,7 +616,9 @@ __device__ __forceinline__ typename Half<T>::Op8 zero8() {
   return v;
 }
 
-template <typename T, int DP, int NT, bool HAS_PV, bool LARGE>
+// MODE 0: molecules of at most one key chunk (small items) and the padded
+// rows; MODE 1: small items, padded rows, then the larger molecules.
+template <typename T, int DP, int NT, bool HAS_PV, int MODE>
 __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) {
   using Hf = Half<T>;
   using Op8 = typename Hf::Op8;
@@ -667,11 +686,11 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       v1v[t] = zero8<T>();
       v2v[t] = zero8<T>();
       if (r < nkj) {
-        const size_t src = (size_t(bh) * N + kidx[j0 + r]) * D;
+        const size_t src = (size_t(bh) * N + atom_at(kidx, j0 + r)) * D;
         a[t] = load8<T>(gk1 + src, e0, D);
         if (with_v) v1v[t] = load8<T>(gv1 + src, e0, D);
       }
-      if (with_v && r < nkk) v2v[t] = load8<T>(gv2 + (size_t(bh) * N + kidx[k0 + r]) * D, e0, D);
+      if (with_v && r < nkk) v2v[t] = load8<T>(gv2 + (size_t(bh) * N + atom_at(kidx, k0 + r)) * D, e0, D);
     }
     float m1[8];
 #pragma unroll
@@ -719,10 +738,10 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
         const int jl = u / PW, w = u - jl * PW;
         uint32_t bits = 0;
         if (jl < nkj) {
-          const uint8_t* prow = gpv + size_t(kidx[j0 + jl]) * N;
+          const uint8_t* prow = gpv + size_t(atom_at(kidx, j0 + jl)) * N;
           for (int t = 0; t < 32; ++t) {
             const int kl = w * 32 + t;
-            if (kl < nkk && prow[kidx[k0 + kl]] != 0) bits |= 1u << t;
+            if (kl < nkk && prow[atom_at(kidx, k0 + kl)] != 0) bits |= 1u << t;
           }
         }
         pvb[u] = bits;
@@ -734,7 +753,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       const int r = kt * 16 + r16;
-      const int row = r < nkk ? kidx[k0 + r] : 0;
+      const int row = r < nkk ? atom_at(kidx, k0 + r) : 0;
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         Op8 v = zero8<T>();
@@ -799,16 +818,16 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
     if (lane == 0 && p.lse) p.lse[row_off] = has_mass ? (m + __log2f(lsum)) * kLn2 : 0.0f;
   };
 
-  if constexpr (!LARGE) {
+  {
     const int n_items = ws.hdr[0];
     int4 nxt = wg < n_items ? ws.small_items[wg] : int4{0, 0, 0, 0};
     for (int item = wg; item < n_items; item += G) {
       const int4 it = nxt;
       if (item + G < n_items) nxt = ws.small_items[item + G];  // next header, one item ahead
-      const int b = it.x, h = it.y, q0 = it.z & 0xffff, q1 = it.z >> 16, nk = it.w;
+      const int b = it.x, h = it.y, q0 = it.z & 0xffff, q1 = it.z >> 16, nk = it.w & 0xffff;
       const int bh = b * H + h;
-      const int* kidx = ws.kidx + size_t(b) * N;
-      const int* qidx = ws.qidx + size_t(b) * N;
+      const int* kidx = (uint32_t(it.w) & kKPre) ? nullptr : ws.kidx + size_t(b) * N;
+      const int* qidx = (uint32_t(it.w) & kQPre) ? nullptr : ws.qidx + size_t(b) * N;
 
       // ---- stage: one round of index loads, then one round of data loads ----
       const int c8 = (tid % CPR) * 8;
@@ -816,17 +835,17 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
 #pragma unroll
       for (int t = 0; t < RPT; ++t) {
         const int r = tid / CPR + t * RPP;
-        jrow[t] = r < nk ? kidx[r] : -1;
+        jrow[t] = r < nk ? atom_at(kidx, r) : -1;
       }
 #pragma unroll
       for (int t = 0; t < QPT; ++t) {
         const int r = tid / CPR + t * RPP;
-        qrow[t] = r < q1 - q0 ? qidx[q0 + r] : -1;
+        qrow[t] = r < q1 - q0 ? atom_at(qidx, q0 + r) : -1;
       }
 #pragma unroll
       for (int kt = 0; kt < NT; ++kt) {
         const int r = kt * 16 + r16;
-        krow[kt] = r < nk ? kidx[r] : -1;
+        krow[kt] = r < nk ? atom_at(kidx, r) : -1;
       }
       Op8 a[RPT], v1v[RPT], v2v[RPT], qv8[QPT];
       Op8 ka[NT][NCH];
@@ -924,13 +943,13 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
           float acc[NN];
 #pragma unroll
           for (int nt = 0; nt < NN; ++nt) acc[nt] = 0.0f;
-          write_row(size_t(bh) * N + qidx[qs], acc, 0.0f);
+          write_row(size_t(bh) * N + atom_at(qidx, qs), acc, 0.0f);
         }
       }
       with_tiles<NT>(njt, [&](auto tiles) {
         constexpr int NKT = decltype(tiles)::value;
         for (int qs = q0 + wave; qs < q1; qs += kWaves) {
-          const size_t row_off = size_t(bh) * N + qidx[qs];
+          const size_t row_off = size_t(bh) * N + atom_at(qidx, qs);
           QOp qo[NCH];
           float ubound = 0.0f;
 #pragma unroll
@@ -1009,17 +1028,20 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
         if (c == 0 && p.lse) p.lse[row[z]] = 0.0f;
       }
     }
-  } else {
+  }
+  if constexpr (MODE == 1) {
     // ---- molecules larger than one chunk: one query per wave, chunk pairs ----
     const int n_items = ws.hdr[1];
+    if (n_items > 0) __syncthreads();  // LDS of the last small item
     for (int item = wg; item < n_items; item += G) {
       const int4 it = ws.large_items[item];
-      const int b = it.x, h = it.y, q0 = it.z & 0xffff, q1 = it.z >> 16, nk = it.w;
+      const int b = it.x, h = it.y, q0 = it.z & 0xffff, q1 = it.z >> 16, nk = it.w & 0xffff;
       const int bh = b * H + h;
-      const int* kidx = ws.kidx + size_t(b) * N;
+      const int* kidx = (uint32_t(it.w) & kKPre) ? nullptr : ws.kidx + size_t(b) * N;
+      const int* qidx = (uint32_t(it.w) & kQPre) ? nullptr : ws.qidx + size_t(b) * N;
       const int qs = q0 + wave;
       const bool has_q = qs < q1;
-      const size_t row_off = size_t(bh) * N + (has_q ? ws.qidx[size_t(b) * N + qs] : 0);
+      const size_t row_off = size_t(bh) * N + (has_q ? atom_at(qidx, qs) : 0);
       QOp qo[NCH];
       if (has_q) {
 #pragma unroll
@@ -1065,9 +1087,9 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
   }
 }
 
-template <typename T, int DP, int NT, bool HAS_PV, bool LARGE>
+template <typename T, int DP, int NT, bool HAS_PV, int MODE>
 int launch_main(const Params& prm, int grid, hipStream_t stream) {
-  auto kern = simplicial_fast_kernel<T, DP, NT, HAS_PV, LARGE>;
+  auto kern = simplicial_fast_kernel<T, DP, NT, HAS_PV, MODE>;
   const size_t lds = Layout<T, DP, NT>::kFixed;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
@@ -1085,9 +1107,8 @@ int launch_all(const Params& prm, int num_cus, hipStream_t stream) {
   hipLaunchKernelGGL(simplicial_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, prm);
   MF_HIP_CHECK(hipGetLastError());
   const int grid = num_cus * 2;  // a multiple of 8 (the XCD count)
-  int st = launch_main<T, DP, NT, HAS_PV, false>(prm, grid, stream);
-  if (st != MF_OK || prm.N <= prm.cap) return st;
-  return launch_main<T, DP, NT, HAS_PV, true>(prm, grid, stream);
+  if (prm.N <= prm.cap) return launch_main<T, DP, NT, HAS_PV, 0>(prm, grid, stream);
+  return launch_main<T, DP, NT, HAS_PV, 1>(prm, grid, stream);
 }
 
 }  // namespace sfast
