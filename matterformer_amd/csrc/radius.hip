@@ -129,6 +129,35 @@ __device__ __forceinline__ bool periodic_hit(float fi0, float fi1, float fi2, fl
   return hit;
 }
 
+// All image bounds below 1/2: of the offsets o_c, only the one nearest to
+// -d_c can leave |d_c + o_c| <= bound_c, so at most one image can be inside
+// the cutoff: o = -rint(d).  It is evaluated with the same operations (and
+// order) as the full search, so the decision is identical.
+__device__ __forceinline__ bool nearest_image_hit(float fi0, float fi1, float fi2, float fj0, float fj1, float fj2,
+                                                  const float* G, const float* bound, float rc2) {
+  const float d0 = fi0 - fj0;
+  const float d1 = fi1 - fj1;
+  const float d2v = fi2 - fj2;
+  const float e0 = d0 + (-rintf(d0));
+  const float e1 = d1 + (-rintf(d1));
+  const float e2 = d2v + (-rintf(d2v));
+  if (fabsf(e0) > bound[0] || fabsf(e1) > bound[1] || fabsf(e2) > bound[2]) return false;
+  float t[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const float p0 = G[3 * c + 0] * e0;
+    const float p1 = G[3 * c + 1] * e1;
+    const float s01 = p0 + p1;
+    const float p2 = G[3 * c + 2] * e2;
+    t[c] = s01 + p2;
+  }
+  const float q0 = e0 * t[0];
+  const float q1 = e1 * t[1];
+  const float q2 = e2 * t[2];
+  const float s = q0 + q1;
+  return s + q2 <= rc2;
+}
+
 __device__ __forceinline__ bool plain_hit(float xi, float yi, float zi, float xj, float yj, float zj, float rc2) {
   const float dx = xi - xj;
   const float dy = yi - yj;
@@ -184,15 +213,25 @@ __global__ void __launch_bounds__(BLOCK * (BLOCK / 32)) radius_mask_kernel(Param
 #pragma unroll
       for (int c = 0; c < 3; ++c) bound[c] = sbound[c];
     }
-    for (int t = 0; t < 32; ++t) {
-      const int u = ww * 32 + t;
-      if (spj[u]) continue;
-      bool hit;
-      if constexpr (MODE == 0)
-        hit = plain_hit(xi, yi, zi, sj[0][u], sj[1][u], sj[2][u], p.rc2);
-      else
-        hit = periodic_hit<MODE>(xi, yi, zi, sj[0][u], sj[1][u], sj[2][u], G, bound, p.rc2);
-      if (hit) word |= 1u << t;
+    bool nearest = false;
+    if constexpr (MODE != 0) nearest = bound[0] < 0.5f && bound[1] < 0.5f && bound[2] < 0.5f;  // per cell
+    if (nearest) {
+      for (int t = 0; t < 32; ++t) {
+        const int u = ww * 32 + t;
+        if (!spj[u] && nearest_image_hit(xi, yi, zi, sj[0][u], sj[1][u], sj[2][u], G, bound, p.rc2))
+          word |= 1u << t;
+      }
+    } else {
+      for (int t = 0; t < 32; ++t) {
+        const int u = ww * 32 + t;
+        if (spj[u]) continue;
+        bool hit;
+        if constexpr (MODE == 0)
+          hit = plain_hit(xi, yi, zi, sj[0][u], sj[1][u], sj[2][u], p.rc2);
+        else
+          hit = periodic_hit<MODE>(xi, yi, zi, sj[0][u], sj[1][u], sj[2][u], G, bound, p.rc2);
+        if (hit) word |= 1u << t;
+      }
     }
   }
   const int w = jb * WPB + ww;

@@ -40,6 +40,7 @@ struct Params {
   float* lse;
   float scale_log2;  // scale * log2(e)
   int B, H, N, W, NB;
+  int units;         // B * H * query tiles (the grid is rounded up to a multiple of 8)
 };
 
 template <typename T>
@@ -71,14 +72,23 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
   constexpr int CPT = kTile * CPR / kThreads;  // chunks per thread per tile
   static_assert(CPT >= 1 && (kTile * CPR) % kThreads == 0, "staging shape");
 
-  __shared__ __attribute__((aligned(16))) T Ks[kTile * KS];
-  __shared__ __attribute__((aligned(16))) T VT[D * VS];
+  __shared__ __attribute__((aligned(16))) T Ks[2][kTile * KS];  // double-buffered key tiles
+  __shared__ __attribute__((aligned(16))) T VT[2][D * VS];
   __shared__ int s_tiles[kMaxTiles];
   __shared__ int s_ntiles;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // XCD-aware unit order: blockIdx.x % 8 is the XCD, so consecutive logical
+  // units -- the query tiles of one (cell, head), which share K and V -- run
+  // on one XCD and its L2.
+  const int G = gridDim.x;
+  const int unit = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  if (unit >= p.units) return;  // grid padding (whole workgroup)
+  const int NQT = p.NB;         // query tiles per (cell, head) = key tiles
+  const int qt = unit % NQT;
+  const int h = (unit / NQT) % p.H;
+  const int b = unit / (NQT * p.H);
   const int N = p.N;
   const size_t bh = size_t(b) * p.H + h;
   const T* gq = static_cast<const T*>(p.q) + bh * N * D;
@@ -122,50 +132,72 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
   __syncthreads();
   const int ntiles = s_ntiles;
 
-  // register staging of one key tile: chunk c = tid + t*kThreads -> (key c / CPR, d 8*(c % CPR))
-  Op8 kr[CPT], vr[CPT];
-  auto load_tile = [&](int jt) {
+  // register staging of one key tile: chunk c = tid + t*kThreads -> (key c / CPR, d 8*(c % CPR)),
+  // and the lane's two mask words of that tile
+  struct Stage {
+    Op8 k[CPT], v[CPT];
+    uint32_t m0, m1;
+  };
+  auto load_tile = [&](int jt, Stage& st) {
+    const int w0 = 2 * jt;
+    st.m0 = (q_in && w0 < p.W) ? qbits[w0] : 0u;
+    st.m1 = (q_in && w0 + 1 < p.W) ? qbits[w0 + 1] : 0u;
 #pragma unroll
     for (int t = 0; t < CPT; ++t) {
+      // K: 8 lanes per key row (coalesced); V: 64 consecutive keys per wave
+      // and 8-column chunk, so the transposed V^T stores of a wave fill one
+      // contiguous row segment
       const int c = tid + t * kThreads;
       const int key = jt * kTile + c / CPR;
       const int d0 = (c % CPR) * 8;
+      const int vkey = jt * kTile + c % kTile;
+      const int vd0 = (c / kTile) * 8;
       if (key < N) {
-        kr[t] = *reinterpret_cast<const Op8*>(gk + size_t(key) * D + d0);
-        vr[t] = *reinterpret_cast<const Op8*>(gv + size_t(key) * D + d0);
+        st.k[t] = *reinterpret_cast<const Op8*>(gk + size_t(key) * D + d0);
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          kr[t][e] = T(0.0f);
-          vr[t][e] = T(0.0f);
-        }
+        for (int e = 0; e < 8; ++e) st.k[t][e] = T(0.0f);
+      }
+      if (vkey < N) {
+        st.v[t] = *reinterpret_cast<const Op8*>(gv + size_t(vkey) * D + vd0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st.v[t][e] = T(0.0f);
       }
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](const Stage& st, int buf) {
 #pragma unroll
     for (int t = 0; t < CPT; ++t) {
       const int c = tid + t * kThreads;
       const int key = c / CPR;
       const int d0 = (c % CPR) * 8;
-      *reinterpret_cast<Op8*>(Ks + key * KS + d0) = kr[t];
+      *reinterpret_cast<Op8*>(Ks[buf] + key * KS + d0) = st.k[t];
+      const int vkey = c % kTile;
+      const int vd0 = (c / kTile) * 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) VT[(d0 + e) * VS + key] = vr[t][e];
+      for (int e = 0; e < 8; ++e) VT[buf][(vd0 + e) * VS + vkey] = st.v[t][e];
     }
   };
 
-  if (ntiles > 0) load_tile(s_tiles[0]);
-  for (int it = 0; it < ntiles; ++it) {
-    const int jt = s_tiles[it];
-    store_tile();
+  // Tile it is computed from LDS buffer it & 1; tile it + 1 waits in
+  // registers and goes to the other buffer at the end of the step; tile it + 2
+  // is loaded meanwhile (two tiles of loads in flight, one barrier per tile).
+  uint32_t mw0 = 0u, mw1 = 0u;
+  Stage sa, sb;
+  if (ntiles > 0) {
+    load_tile(s_tiles[0], sa);
+    if (ntiles > 1) load_tile(s_tiles[1], sb);
+    store_tile(sa, 0);
+    mw0 = sa.m0;
+    mw1 = sa.m1;
     __syncthreads();
-    if (it + 1 < ntiles) load_tile(s_tiles[it + 1]);
-
-    // mask words of this key tile for the lane's query
-    const int w0 = 2 * jt;
-    const uint32_t mw0 = (q_in && w0 < p.W) ? qbits[w0] : 0u;
-    const uint32_t mw1 = (q_in && w0 + 1 < p.W) ? qbits[w0 + 1] : 0u;
-
+  }
+  auto step = [&](int it, Stage& freed, const Stage& next) {
+    const int buf = it & 1;
+    if (it + 2 < ntiles) load_tile(s_tiles[it + 2], freed);
+    const T* Kt = Ks[buf];
+    const T* VTt = VT[buf];
     // S^T tiles: keys 16 kt + 4 g + r, query r16
     float s[4][4];
 #pragma unroll
@@ -173,7 +205,7 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
       mf_f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < DK; ++kk) {
-        const Op8 a = *reinterpret_cast<const Op8*>(Ks + (16 * kt + r16) * KS + 32 * kk + 8 * g);
+        const Op8 a = *reinterpret_cast<const Op8*>(Kt + (16 * kt + r16) * KS + 32 * kk + 8 * g);
         c = Ops<T>::mma(a, qb[kk], c);
       }
 #pragma unroll
@@ -193,13 +225,25 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    // Branch-free (the MFMAs below need the whole wave): while a query has
-    // seen no allowed key its maximum stays -inf and the exponent offset is
-    // 0, so alpha = exp2(-inf) = 0 and every p = exp2(-inf) = 0.
-    const float m_new = fmaxf(m, tmax);
-    const float m_off = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = fast_exp2(m - m_off);
-    m = m_new;
+    // The exponent offset m follows the running maximum lazily: it moves
+    // only when a logit exceeds it by more than 8 (log2 units), so every
+    // p <= 2^8, and the rescaling of the accumulators (MFMA registers) runs
+    // only in the rare tiles where some query's offset moves (a wave-uniform
+    // branch; the MFMAs need the whole wave).  While a query has seen no
+    // allowed key its m stays -inf and its p = exp2(-inf) = 0.
+    const bool grow = tmax > m + 8.0f;  // false while tmax is -inf
+    if (__ballot(grow) != 0ull) {
+      const float m_set = grow ? tmax : m;
+      const float alpha = grow ? fast_exp2(m - m_set) : 1.0f;  // 0 when m was -inf
+      l *= alpha;
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[nd][r] *= alpha;
+      }
+      m = m_set;
+    }
+    const float m_off = m == -INFINITY ? 0.0f : m;
     float psum = 0.0f;
     Op8 pb[2];
 #pragma unroll
@@ -211,25 +255,27 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
         pb[kt >> 1][(kt & 1) * 4 + r] = T(pv);
       }
     }
-    l = l * alpha + psum;
-#pragma unroll
-    for (int nd = 0; nd < ND; ++nd) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[nd][r] *= alpha;
-    }
+    l += psum;
     // O^T[d][q] += sum_keys V^T[d][key] P^T[key][q]
 #pragma unroll
     for (int nd = 0; nd < ND; ++nd) {
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) {
-        const T* vrow = VT + (16 * nd + r16) * VS + 32 * pr + 4 * g;
+        const T* vrow = VTt + (16 * nd + r16) * VS + 32 * pr + 4 * g;
         const Op4 lo = *reinterpret_cast<const Op4*>(vrow);
         const Op4 hi = *reinterpret_cast<const Op4*>(vrow + 16);
         const Op8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         acc[nd] = Ops<T>::mma(a, pb[pr], acc[nd]);
       }
     }
+    if (it + 1 < ntiles) store_tile(next, buf ^ 1);
     __syncthreads();
+    mw0 = next.m0;
+    mw1 = next.m1;
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    step(it, sa, sb);
+    if (it + 1 < ntiles) step(it + 1, sb, sa);
   }
 
   // finish: l summed over the 4 key groups g; lane (g, r16) holds d = 16 nd + 4 g + r of query r16
@@ -258,7 +304,7 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
 
 template <typename T, int D>
 int launch(const Params& p, hipStream_t stream) {
-  const dim3 grid((p.N + kTile - 1) / kTile, p.H, p.B);
+  const dim3 grid((p.units + 7) / 8 * 8);
   hipLaunchKernelGGL((radius_attn_kernel<T, D>), grid, dim3(kThreads), 0, stream, p);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
@@ -293,10 +339,11 @@ extern "C" int mf_radius_attn(const mf_radius_attn_args* a, void* stream) {
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_radius_attn: q, k, v, out and out_f32 must be 16-byte aligned");
   if (a->batch == 0 || a->heads == 0 || a->atoms == 0) return MF_OK;
   const int nb = (a->atoms + rattn::kTile - 1) / rattn::kTile;
-  if (nb > rattn::kMaxTiles || a->batch > 65535 || a->heads > 65535)
-    return fail(MF_ERR_UNSUPPORTED, "mf_radius_attn: atoms must be <= 65536 and batch, heads <= 65535");
+  if (nb > rattn::kMaxTiles) return fail(MF_ERR_UNSUPPORTED, "mf_radius_attn: atoms must be <= 65536");
+  const long long units = (long long)a->batch * a->heads * nb;
+  if (units > 0x7fffffffLL - 8) return fail(MF_ERR_UNSUPPORTED, "mf_radius_attn: batch * heads * tiles too large");
   rattn::Params p{a->q, a->k, a->v, a->mask_bits, a->block_mask, a->out, a->out_f32, a->lse,
-                  a->scale * kLog2e, a->batch, a->heads, a->atoms, (a->atoms + 31) / 32, nb};
+                  a->scale * kLog2e, a->batch, a->heads, a->atoms, (a->atoms + 31) / 32, nb, int(units)};
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a->dtype == MF_DTYPE_BF16) return rattn::dispatch_dim<__bf16>(p, a->head_dim, s);
   return rattn::dispatch_dim<_Float16>(p, a->head_dim, s);
