@@ -266,7 +266,8 @@ struct Layout {
   static constexpr size_t kAB = kPV + size_t(CH) * PW * 4;
   static constexpr size_t kM2 = kAB + size_t(DP) * 4;
   static constexpr size_t kRed = kM2 + size_t(DP) * 4;
-  static constexpr size_t kFixed = (kRed + size_t(kWaves) * DP * 4 + 15) & ~size_t(15);
+  static constexpr size_t kQn = kRed + size_t(kWaves) * DP * 4;  // |q'|_1 of the item's queries
+  static constexpr size_t kFixed = (kQn + size_t(kMaxQueriesPerItem) * 4 + 15) & ~size_t(15);
 };
 
 // max over the valid logits of one 16-row j tile (log2 units, -inf if none);
@@ -458,7 +459,48 @@ __device__ void write_ranks(const uint8_t* row, int N, int* dst, int lane) {
   }
 }
 
+// Rows of padded queries are zeroed by workgroups 1.. of the plan launch,
+// concurrently with the plan itself (workgroup 0): 16-byte chunks of the
+// whole 16-bit output, the validity bytes of kZ chunks loaded before any is
+// tested.
+__device__ void zero_padded_rows(const Params& p, int worker, int workers) {
+  const int per_row = p.D / 8;  // head_dim % 8 == 0 on this path
+  const long long total = (long long)p.B * p.H * p.N * per_row;
+  const long long stride = (long long)workers * kPlanThreads;
+  constexpr int kZ = 8;
+  for (long long base = (long long)worker * kPlanThreads + threadIdx.x; base < total; base += stride * kZ) {
+    long long row[kZ];
+    int col[kZ];
+    uint8_t valid[kZ];
+#pragma unroll
+    for (int z = 0; z < kZ; ++z) {
+      const long long idx = base + (long long)z * stride;
+      row[z] = idx / per_row;
+      col[z] = int(idx - row[z] * per_row);
+      const long long bh = row[z] / p.N;
+      const int i = int(row[z] - bh * p.N);
+      valid[z] = idx < total ? p.qv[(bh / p.H) * p.N + i] : 1;
+    }
+#pragma unroll
+    for (int z = 0; z < kZ; ++z) {
+      if (valid[z]) continue;
+      const int c = col[z];
+      if (p.out) reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + row[z] * p.D)[c] = uint4{0u, 0u, 0u, 0u};
+      if (p.out_f32) {
+        float4* o = reinterpret_cast<float4*>(p.out_f32 + row[z] * p.D);
+        o[2 * c] = float4{0.f, 0.f, 0.f, 0.f};
+        o[2 * c + 1] = float4{0.f, 0.f, 0.f, 0.f};
+      }
+      if (c == 0 && p.lse) p.lse[row[z]] = 0.0f;
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p) {
+  if (blockIdx.x > 0) {
+    zero_padded_rows(p, blockIdx.x - 1, gridDim.x - 1);
+    return;
+  }
   constexpr int kPlanWaves = kPlanThreads / 64;
   constexpr int kRound = 4;  // molecule rows a wave loads at once
   __shared__ uint32_t s_info[kMaxBatch];
@@ -651,6 +693,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
   float* ab = reinterpret_cast<float*>(smem + L::kAB);
   float* m2s = reinterpret_cast<float*>(smem + L::kM2);
   float* red = reinterpret_cast<float*>(smem + L::kRed);
+  float* qns = reinterpret_cast<float*>(smem + L::kQn);
   const int H = p.H, N = p.N, D = p.D;
   const Workspace& ws = p.ws;
 
@@ -796,24 +839,41 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
     }
     return v;
   };
+  // Row of a query: lane (g, r16) holds partial sums over its row group g of
+  // the MFMA layout.  A reduce-scatter over the 4 groups (3 shuffles) leaves
+  // lane (g, r16) with the full sum of d tile g (ND <= 4 tiles), and the
+  // denominator partials of lanes (g, 0) are summed from 4 lane reads.
   auto write_row = [&](size_t row_off, float (&acc)[NN], float m) {
-#pragma unroll
-    for (int nt = 0; nt < NN; ++nt) {
-      acc[nt] += __shfl_xor(acc[nt], 16, 64);
-      acc[nt] += __shfl_xor(acc[nt], 32, 64);
+    static_assert(ND == 2 || ND == 4, "reduce-scatter shape");
+    float x0, x1;
+    {
+      // groups {g, g ^ 2}: groups 0, 1 keep d tiles 0, 1; groups 2, 3 keep 2, 3
+      const bool lo = g < 2;
+      const float s0 = ND == 4 ? (lo ? acc[2 % ND] : acc[0]) : acc[0];
+      const float s1 = ND == 4 ? (lo ? acc[3 % ND] : acc[1]) : acc[1];
+      const float r0 = __shfl_xor(s0, 32, 64);
+      const float r1 = __shfl_xor(s1, 32, 64);
+      if constexpr (ND == 4) {
+        x0 = (lo ? acc[0] : acc[2 % ND]) + r0;
+        x1 = (lo ? acc[1] : acc[3 % ND]) + r1;
+      } else {
+        x0 = acc[0] + r0;
+        x1 = acc[1] + r1;
+      }
     }
-    const float lsum = __shfl(acc[ND], 0, 64);
+    // groups {g, g ^ 1}: even groups keep x0, odd groups keep x1
+    const bool odd = (g & 1) != 0;
+    const float y = (odd ? x1 : x0) + __shfl_xor(odd ? x0 : x1, 16, 64);
+    auto lane_val = [&](int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc[ND]), l)); };
+    const float lsum = (lane_val(0) + lane_val(16)) + (lane_val(32) + lane_val(48));
     const bool has_mass = lsum > 0.0f;
     const float inv = has_mass ? 1.0f / lsum : 0.0f;
-#pragma unroll
-    for (int nt = 0; nt < ND; ++nt) {
-      if ((nt & 3) != g) continue;
-      const int d = nt * 16 + r16;
-      if (d < D) {
-        const float o = acc[nt] * inv;
-        if (p.out) static_cast<T*>(p.out)[row_off * D + d] = T(o);
-        if (p.out_f32) p.out_f32[row_off * D + d] = o;
-      }
+    const int nt = ND == 4 ? g : (g & 1);
+    const int d = nt * 16 + r16;
+    if ((ND == 4 || g < 2) && d < D) {
+      const float o = y * inv;
+      if (p.out) static_cast<T*>(p.out)[row_off * D + d] = T(o);
+      if (p.out_f32) p.out_f32[row_off * D + d] = o;
     }
     if (lane == 0 && p.lse) p.lse[row_off] = has_mass ? (m + __log2f(lsum)) * kLn2 : 0.0f;
   };
@@ -876,6 +936,13 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       for (int t = 0; t < QPT; ++t) {
         const int r = tid / CPR + t * RPP;
         if (r < q1 - q0) Hf::store_q(Qs + r * KS + c8, qv8[t]);
+        // |q'|_1 of the row (q' = q log2 e), reduced over its CPR chunk lanes
+        float qn = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qn += fabsf(float(qv8[t][e]));
+#pragma unroll
+        for (int off = 1; off < CPR; off <<= 1) qn += __shfl_xor(qn, off, 64);
+        if (c8 == 0 && r < q1 - q0) qns[r] = qn * kLog2e;
       }
       {
         float m1[8];
@@ -932,6 +999,8 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
         ab[tid] = a0 * m2s[tid];
       }
       __syncthreads();
+      // sum_d |q'_d| m1_d m2_d <= |q'|_1 max_d (m1_d m2_d) = |q'|_1 M bounds |S| of a query
+      const float mab = wave_max(lane < DP ? ab[lane] : 0.0f);
       Op8 vb[ND][NPR];
       load_vb(vb);
       const Op8 ones_edge = make_ones_edge(nk);
@@ -951,17 +1020,10 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
         for (int qs = q0 + wave; qs < q1; qs += kWaves) {
           const size_t row_off = size_t(bh) * N + atom_at(qidx, qs);
           QOp qo[NCH];
-          float ubound = 0.0f;
 #pragma unroll
-          for (int c = 0; c < NCH; ++c) {
-            Hf::load_q(Qs + (qs - q0) * KS + c * 32 + g * 8, qo[c]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ubound += Hf::qabs(qo[c], e) * ab[c * 32 + g * 8 + e];
-          }
-          ubound += __shfl_xor(ubound, 16, 64);
-          ubound += __shfl_xor(ubound, 32, 64);
-          const bool fast =
-              __builtin_amdgcn_readfirstlane(__float_as_int(ubound)) <= __float_as_int(p.bound_limit);
+          for (int c = 0; c < NCH; ++c) Hf::load_q(Qs + (qs - q0) * KS + c * 32 + g * 8, qo[c]);
+          const float ubound = qns[qs - q0] * mab;
+          const bool fast = __builtin_amdgcn_readfirstlane(ubound <= p.bound_limit ? 1 : 0) != 0;
           float acc[NN];
 #pragma unroll
           for (int nt = 0; nt < NN; ++nt) acc[nt] = 0.0f;
@@ -990,44 +1052,6 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       __syncthreads();
     }
 
-    // ---- zero the rows of padded queries: 16-byte chunks of the whole output,
-    //      the validity bytes of 8 chunks are loaded before any is tested ----
-    const int rowbytes = D * int(sizeof(T));
-    const bool vec_out = vec && (rowbytes % 16 == 0);
-    const int per_row = vec_out ? rowbytes / 16 : D;
-    const long long total = (long long)p.B * H * N * per_row;
-    constexpr int kZ = 8;
-    for (long long base = (long long)wg * kThreads + tid; base < total; base += (long long)G * kThreads * kZ) {
-      long long row[kZ];
-      int col[kZ];
-      uint8_t valid[kZ];
-#pragma unroll
-      for (int z = 0; z < kZ; ++z) {
-        const long long idx = base + (long long)z * G * kThreads;
-        row[z] = idx / per_row;
-        col[z] = int(idx - row[z] * per_row);
-        const long long bh = row[z] / N;
-        const int i = int(row[z] - bh * N);
-        valid[z] = idx < total ? p.qv[(bh / H) * N + i] : 1;
-      }
-#pragma unroll
-      for (int z = 0; z < kZ; ++z) {
-        if (valid[z]) continue;
-        const int c = col[z];
-        if (vec_out) {
-          if (p.out) reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row[z] * D)[c] = uint4{0u, 0u, 0u, 0u};
-          if (p.out_f32) {
-            float4* o = reinterpret_cast<float4*>(p.out_f32 + row[z] * D);
-            o[2 * c] = float4{0.f, 0.f, 0.f, 0.f};
-            o[2 * c + 1] = float4{0.f, 0.f, 0.f, 0.f};
-          }
-        } else {
-          if (p.out) static_cast<T*>(p.out)[row[z] * D + c] = T(0.0f);
-          if (p.out_f32) p.out_f32[row[z] * D + c] = 0.0f;
-        }
-        if (c == 0 && p.lse) p.lse[row[z]] = 0.0f;
-      }
-    }
   }
   if constexpr (MODE == 1) {
     // ---- molecules larger than one chunk: one query per wave, chunk pairs ----
@@ -1104,7 +1128,8 @@ int launch_main(const Params& prm, int grid, hipStream_t stream) {
 
 template <typename T, int DP, int NT, bool HAS_PV>
 int launch_all(const Params& prm, int num_cus, hipStream_t stream) {
-  hipLaunchKernelGGL(simplicial_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, prm);
+  // workgroup 0 plans, the others zero the rows of padded queries
+  hipLaunchKernelGGL(simplicial_plan_kernel, dim3(std::max(2, num_cus)), dim3(kPlanThreads), 0, stream, prm);
   MF_HIP_CHECK(hipGetLastError());
   const int grid = num_cus * 2;  // a multiple of 8 (the XCD count)
   if (prm.N <= prm.cap) return launch_main<T, DP, NT, HAS_PV, 0>(prm, grid, stream);
