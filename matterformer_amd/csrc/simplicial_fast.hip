@@ -185,14 +185,20 @@ struct Half<__bf16> {
     d[0] = float4{float(v[0]), float(v[1]), float(v[2]), float(v[3])};
     d[1] = float4{float(v[4]), float(v[5]), float(v[6]), float(v[7])};
   }
+  // 8 consecutive d of a K1 row
+  struct K1V {
+    float4 a, b;
+  };
+  __device__ static __forceinline__ K1V load_k1(const K1T* k1) {
+    return K1V{*reinterpret_cast<const float4*>(k1), *reinterpret_cast<const float4*>(k1 + 4)};
+  }
   // bf16(k1 (.) q) for 8 consecutive d: exact fp32 products, rounded once
-  __device__ static __forceinline__ Op8 mul(const K1T* k1, const QOp& o) {
-    const float4 a = *reinterpret_cast<const float4*>(k1);
-    const float4 b = *reinterpret_cast<const float4*>(k1 + 4);
-    const uint4 r{pack(a.x * o.q[0], a.y * o.q[1]), pack(a.z * o.q[2], a.w * o.q[3]),
-                  pack(b.x * o.q[4], b.y * o.q[5]), pack(b.z * o.q[6], b.w * o.q[7])};
+  __device__ static __forceinline__ Op8 mul_v(const K1V& k, const QOp& o) {
+    const uint4 r{pack(k.a.x * o.q[0], k.a.y * o.q[1]), pack(k.a.z * o.q[2], k.a.w * o.q[3]),
+                  pack(k.b.x * o.q[4], k.b.y * o.q[5]), pack(k.b.z * o.q[6], k.b.w * o.q[7])};
     return __builtin_bit_cast(Op8, r);
   }
+  __device__ static __forceinline__ Op8 mul(const K1T* k1, const QOp& o) { return mul_v(load_k1(k1), o); }
 };
 
 template <>
@@ -233,15 +239,19 @@ struct Half<_Float16> {
     return fabsf(float((e & 1) ? o.pair[e >> 1].y : o.pair[e >> 1].x));
   }
   __device__ static __forceinline__ void store_k1(K1T* dst, Op8 v) { *reinterpret_cast<Op8*>(dst) = v; }
+  struct K1V {
+    uint4 w;
+  };
+  __device__ static __forceinline__ K1V load_k1(const K1T* k1) { return K1V{*reinterpret_cast<const uint4*>(k1)}; }
   // fp16(k1 (.) q) with v_pk_mul_f16 (correctly rounded products)
-  __device__ static __forceinline__ Op8 mul(const K1T* k1, const QOp& o) {
-    const uint4 w = *reinterpret_cast<const uint4*>(k1);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  __device__ static __forceinline__ Op8 mul_v(const K1V& k, const QOp& o) {
+    const uint32_t ws[4] = {k.w.x, k.w.y, k.w.z, k.w.w};
     uint32_t r[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) r[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_e, ws[p]) * o.pair[p]);
     return __builtin_bit_cast(Op8, uint4{r[0], r[1], r[2], r[3]});
   }
+  __device__ static __forceinline__ Op8 mul(const K1T* k1, const QOp& o) { return mul_v(load_k1(k1), o); }
 };
 
 
@@ -260,7 +270,11 @@ struct Layout {
   static constexpr int PW = (CH + 31) / 32;  // pair-valid words per row
   static constexpr size_t kK1 = 0;
   static constexpr size_t kV2T = kK1 + size_t(CH) * K1S * sizeof(K1T);
-  static constexpr size_t kV1T = (kV2T + size_t(DP) * VS * sizeof(T) + 15) & ~size_t(15);
+  // the small items keep the GEMM2 B operands (DP/16 x NPR operands of 16
+  // bytes per lane) where the larger molecules keep V2T
+  static constexpr size_t kVBBytes = size_t(DP / 16) * ((NT + 1) / 2) * 64 * 16;
+  static constexpr size_t kV2TBytes = size_t(DP) * VS * sizeof(T);
+  static constexpr size_t kV1T = (kV2T + (kVBBytes > kV2TBytes ? kVBBytes : kV2TBytes) + 15) & ~size_t(15);
   static constexpr size_t kQs = kV1T + size_t(DP + 16) * WS * 4;
   static constexpr size_t kPV = kQs + size_t(kMaxQueriesPerItem) * KS * sizeof(QT);
   static constexpr size_t kAB = kPV + size_t(CH) * PW * 4;
@@ -370,6 +384,119 @@ __device__ __forceinline__ void jtile_acc(const typename Half<T>::K1T* K1s, cons
     }
     const float4 v1 = *reinterpret_cast<const float4*>(V1T + (nt * 16 + r16) * L::WS + jt * 16 + 4 * g);
     acc[nt] += v1.x * c2[0] + v1.y * c2[1] + v1.z * c2[2] + v1.w * c2[3];
+  }
+}
+
+// acc += the contributions of j tiles 0 .. NKT-1 of one query (all of a small
+// item's keys): jtile_acc with the LDS reads software-pipelined.  The K1 rows
+// of tile jt + 1 are read while tile jt runs its GEMMs, and the V1 columns of
+// tile jt are read at its start, so that no LDS read waits in the middle of
+// the MFMA chain.
+template <typename T, int DP, int NT, int NKT, bool HAS_PV, bool MASKED>
+__device__ __forceinline__ void query_acc(const typename Half<T>::K1T* K1s, const float* V1T, const uint32_t* pvb,
+                                          const typename Half<T>::Op8 (&ka)[NT][DP / 32],
+                                          const typename Half<T>::Op8 (&vb)[DP / 16][(NT + 1) / 2],
+                                          typename Half<T>::Op8 ones_full, typename Half<T>::Op8 ones_edge,
+                                          const typename Half<T>::QOp (&qo)[DP / 32], int nk, float m,
+                                          float (&acc)[DP / 16 + 1], int g, int r16) {
+  using Hf = Half<T>;
+  using Op8 = typename Hf::Op8;
+  using L = Layout<T, DP, NT>;
+  constexpr int NCH = DP / 32;
+  constexpr int ND = DP / 16;
+  constexpr int NPU = (NKT + 1) / 2;
+  typename Hf::K1V k1[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) k1[c] = Hf::load_k1(K1s + r16 * L::K1S + c * 32 + g * 8);
+#pragma unroll 1
+  for (int jt = 0; jt < NKT; ++jt) {
+    const int j = jt * 16 + r16;
+    float4 v1[ND + 1];
+#pragma unroll
+    for (int nt = 0; nt <= ND; ++nt)
+      v1[nt] = *reinterpret_cast<const float4*>(V1T + (nt * 16 + r16) * L::WS + jt * 16 + 4 * g);
+    Op8 b1[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) b1[c] = Hf::mul_v(k1[c], qo[c]);
+    // next tile's K1 rows (the last tile re-reads its own rows)
+    const int jn = jt + 1 < NKT ? j + 16 : j;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) k1[c] = Hf::load_k1(K1s + jn * L::K1S + c * 32 + g * 8);
+    // keep the reads above ahead of the MFMA chain (the scheduler would sink
+    // them next to their uses)
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t pw[L::PW];
+    if constexpr (HAS_PV) {
+#pragma unroll
+      for (int w = 0; w < L::PW; ++w) pw[w] = pvb[j * L::PW + w];
+    }
+    uint32_t pa[NPU][4];
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      mf_f32x4 sv = mf_f32x4{-m, -m, -m, -m};
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) sv = Hf::mfma32(ka[kt][c], b1[c], sv);
+      float pe[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float e = fast_exp2(sv[r]);
+        if constexpr (MASKED) {
+          const int k = kt * 16 + 4 * g + r;
+          e = (j < nk && k < nk) ? e : 0.0f;
+        }
+        if constexpr (HAS_PV) e = ((pw[kt >> 1] >> ((kt & 1) * 16 + 4 * g + r)) & 1u) ? e : 0.0f;
+        pe[r] = e;
+      }
+      pa[kt >> 1][(kt & 1) * 2 + 0] = Hf::pack(pe[0], pe[1]);
+      pa[kt >> 1][(kt & 1) * 2 + 1] = Hf::pack(pe[2], pe[3]);
+    }
+    if constexpr (NKT % 2 == 1) {
+      pa[NPU - 1][2] = 0u;
+      pa[NPU - 1][3] = 0u;
+    }
+    mf_f32x4 c2[ND + 1];
+#pragma unroll
+    for (int nt = 0; nt <= ND; ++nt) {
+      c2[nt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int pr = 0; pr < NPU; ++pr) {
+        const Op8 a = __builtin_bit_cast(Op8, uint4{pa[pr][0], pa[pr][1], pa[pr][2], pa[pr][3]});
+        const Op8 bop = nt < ND ? vb[nt < ND ? nt : 0][pr] : (pr == NPU - 1 ? ones_edge : ones_full);
+        c2[nt] = Hf::mfma32(a, bop, c2[nt]);
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt <= ND; ++nt) {
+      acc[nt] = fmaf(v1[nt].x, c2[nt][0], acc[nt]);
+      acc[nt] = fmaf(v1[nt].y, c2[nt][1], acc[nt]);
+      acc[nt] = fmaf(v1[nt].z, c2[nt][2], acc[nt]);
+      acc[nt] = fmaf(v1[nt].w, c2[nt][3], acc[nt]);
+    }
+  }
+}
+
+// Maximum over the lanes l ^ OFF, l ^ OFF/2, ... (log2 NV steps) of NV
+// values per lane, scattered: each step keeps half of the values, so the
+// lane ends with the maximum of value idx (NV - 1 shuffles instead of
+// NV log2 NV).
+template <int NV, int OFF>
+__device__ __forceinline__ float reduce_scatter_max(const float (&v)[NV], int lane, int& idx) {
+  if constexpr (NV == 1) {
+    idx = 0;
+    return v[0];
+  } else {
+    const bool up = (lane & OFF) != 0;
+    float k[NV / 2];
+#pragma unroll
+    for (int i = 0; i < NV / 2; ++i) {
+      const float send = up ? v[i] : v[i + NV / 2];
+      const float keep = up ? v[i + NV / 2] : v[i];
+      k[i] = fmaxf(keep, __shfl_xor(send, OFF, 64));
+    }
+    int sub;
+    const float r = reduce_scatter_max<NV / 2, OFF / 2>(k, lane, sub);
+    idx = (up ? NV / 2 : 0) + sub;
+    return r;
   }
 }
 
@@ -658,10 +785,10 @@ __device__ __forceinline__ typename Half<T>::Op8 zero8() {
   return v;
 }
 
-// MODE 0: molecules of at most one key chunk (small items) and the padded
-// rows; MODE 1: small items, padded rows, then the larger molecules.
-template <typename T, int DP, int NT, bool HAS_PV, int MODE>
-__global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) {
+// PART 0: the items of molecules with at most one key chunk (small items);
+// PART 1: the items of larger molecules.
+template <typename T, int DP, int NT, bool HAS_PV, int PART>
+__device__ __forceinline__ void fast_body(const Params& p) {
   using Hf = Half<T>;
   using Op8 = typename Hf::Op8;
   using Op4 = typename Hf::Op4;
@@ -681,11 +808,13 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
   constexpr int RPP = kThreads / CPR; // rows per staging pass
   constexpr int RPT = (CH + RPP - 1) / RPP;
   constexpr int QPT = (kMaxQueriesPerItem + RPP - 1) / RPP;
+  constexpr int NU = (NT * NCH + kWaves - 1) / kWaves;  // V1 tiles (16 keys x 32 columns) per wave
   static_assert(kThreads % CPR == 0, "a thread's 8-column chunk must be fixed across rows");
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   K1T* K1s = reinterpret_cast<K1T*>(smem + L::kK1);
   T* V2T = reinterpret_cast<T*>(smem + L::kV2T);
+  unsigned char* VB = smem + L::kV2T;  // small items: GEMM2 B operands, 16 bytes per lane
   float* V1T = reinterpret_cast<float*>(smem + L::kV1T);
   using QT = typename Hf::QT;
   QT* Qs = reinterpret_cast<QT*>(smem + L::kQs);
@@ -824,6 +953,13 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       }
     }
   };
+  // 0/1 selector B operands: sel[sh] picks columns 16 sh .. 16 sh + 15 of a
+  // 32-column A tile (B[kk][n] = 1 iff kk == n + 16 sh)
+  Op8 sel[2];
+#pragma unroll
+  for (int sh = 0; sh < 2; ++sh)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sel[sh][e] = T(8 * g + e == r16 + 16 * sh ? 1.0f : 0.0f);
   // GEMM2 B operands of the denominator column: 1 in column 0 for full key
   // pairs; for the last pair of a chunk, 1 only at valid keys
   Op8 ones_full;
@@ -878,7 +1014,16 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
     if (lane == 0 && p.lse) p.lse[row_off] = has_mass ? (m + __log2f(lsum)) * kLn2 : 0.0f;
   };
 
-  {
+  if constexpr (PART == 0) {
+    // rows DP + 1 .. DP + 15 of V1T (the denominator tile's unused columns)
+    // stay zero for the whole launch
+    for (int u = tid; u < 15 * WS; u += kThreads) V1T[(DP + 1) * WS + u] = 0.0f;
+    // with an odd tile count the upper half of the last B operand (keys
+    // 16 NT .. 16 NT + 15) is never written: zero
+    if constexpr (NT % 2 == 1) {
+      for (int u = tid; u < ND * 64; u += kThreads)
+        *reinterpret_cast<uint2*>(VB + (((u / 64) * NPR + NPR - 1) * 64 + u % 64) * 16 + 8) = uint2{0u, 0u};
+    }
     const int n_items = ws.hdr[0];
     int4 nxt = wg < n_items ? ws.small_items[wg] : int4{0, 0, 0, 0};
     for (int item = wg; item < n_items; item += G) {
@@ -890,6 +1035,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       const int* qidx = (uint32_t(it.w) & kQPre) ? nullptr : ws.qidx + size_t(b) * N;
 
       // ---- stage: one round of index loads, then one round of data loads ----
+      const int njt = ceil_div(nk, 16);
       const int c8 = (tid % CPR) * 8;
       int jrow[RPT], qrow[QPT], krow[NT];
 #pragma unroll
@@ -907,31 +1053,36 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
         const int r = kt * 16 + r16;
         krow[kt] = r < nk ? atom_at(kidx, r) : -1;
       }
-      Op8 a[RPT], v1v[RPT], v2v[RPT], qv8[QPT];
-      Op8 ka[NT][NCH];
+      // K1 and query rows (one thread per 8 columns of a row); K2 and V2 in
+      // the MFMA A layout (every wave holds all of them); this wave's share of
+      // the V1 tiles (16 keys x 32 columns, tile u = wave + kWaves i), also in
+      // the A layout
+      Op8 a[RPT], qv8[QPT];
+      Op8 ka[NT][NCH], va[NU], v1a[NU];
 #pragma unroll
-      for (int t = 0; t < RPT; ++t) {
-        a[t] = zero8<T>();
-        v1v[t] = zero8<T>();
-        v2v[t] = zero8<T>();
-        if (jrow[t] >= 0) {
-          const size_t src = (size_t(bh) * N + jrow[t]) * D;
-          a[t] = load8<T>(gk1 + src, c8, D);
-          v1v[t] = load8<T>(gv1 + src, c8, D);
-          v2v[t] = load8<T>(gv2 + src, c8, D);
-        }
-      }
+      for (int t = 0; t < RPT; ++t)
+        a[t] = jrow[t] >= 0 ? load8<T>(gk1 + (size_t(bh) * N + jrow[t]) * D, c8, D) : zero8<T>();
 #pragma unroll
       for (int t = 0; t < QPT; ++t)
         qv8[t] = qrow[t] >= 0 ? load8<T>(gq + (size_t(bh) * N + qrow[t]) * D, c8, D) : zero8<T>();
 #pragma unroll
-      for (int kt = 0; kt < NT; ++kt)
+      for (int kt = 0; kt < NT; ++kt) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c)
           ka[kt][c] = krow[kt] >= 0 ? load8<T>(gk2 + (size_t(bh) * N + krow[kt]) * D, c * 32 + g * 8, D)
                                     : zero8<T>();
+      }
+#pragma unroll
+      for (int i = 0; i < NU; ++i) {
+        const int u = wave + kWaves * i, jt = u / NCH, c = u % NCH;
+        const int key = jt * 16 + r16;
+        const int row = jt < NT && key < nk ? atom_at(kidx, key) : -1;
+        const size_t src = (size_t(bh) * N + row) * D;
+        v1a[i] = row >= 0 ? load8<T>(gv1 + src, c * 32 + g * 8, D) : zero8<T>();
+        va[i] = row >= 0 ? load8<T>(gv2 + src, c * 32 + g * 8, D) : zero8<T>();
+      }
 
-      // LDS: query rows, K1 (and its column maxima), V2 transposed, V1 transposed
+      // LDS: query rows, K1 (and its column maxima), V1 transposed
 #pragma unroll
       for (int t = 0; t < QPT; ++t) {
         const int r = tid / CPR + t * RPP;
@@ -954,44 +1105,73 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
           if (r < CH) {
             Hf::store_k1(K1s + r * L::K1S + c8, a[t]);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              m1[e] = fmaxf(m1[e], fabsf(float(a[t][e])));
-              V2T[(c8 + e) * VS + r] = v2v[t][e];
-              V1T[(c8 + e) * WS + r] = float(v1v[t][e]);
-            }
+            for (int e = 0; e < 8; ++e) m1[e] = fmaxf(m1[e], fabsf(float(a[t][e])));
           }
         }
-        for (int u = tid; u < 16 * CH; u += kThreads) {
-          const int rr = u / CH, col = u - rr * CH;
-          V1T[(DP + rr) * WS + col] = (rr == 0 && col < nk) ? 1.0f : 0.0f;
-        }
+        // the 8 lanes of a column chunk (lanes l ^ 8, l ^ 16, l ^ 32; 16 lanes
+        // when CPR == 4) scatter the 8 column maxima among themselves
+        int e1;
+        float mx = reduce_scatter_max<8, 32>(m1, lane, e1);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int off = 4; off >= CPR; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        red[wave * DP + c8 + e1] = mx;
+      }
+      if (tid < CH) V1T[DP * WS + tid] = tid < nk ? 1.0f : 0.0f;  // key validity row
+      // V1T[d][j] and the GEMM2 B operands of V2: an MFMA with a 0/1
+      // selector B operand (exact) turns a 16-key x 32-column A tile into the
+      // 16 x 16 C layout, lane (g, r16) holding keys 4g..4g+3 of column r16.
+      // V1: one 16-byte store per lane into V1T.  V2: the bf16 keys
+      // 4g..4g+3 of 16-key tile kt are half kt & 1 of operand (nt, kt / 2),
+      // which holds keys 32 pr + 4g + 0..3 and 32 pr + 16 + 4g + 0..3
 #pragma unroll
-          for (int off = CPR; off < 64; off <<= 1) m1[e] = fmaxf(m1[e], __shfl_xor(m1[e], off, 64));
-        }
-        if (lane < CPR) {
+      for (int i = 0; i < NU; ++i) {
+        const int u = wave + kWaves * i, jt = u / NCH, c = u % NCH;
+        if (jt < NT) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) red[wave * DP + c8 + e] = m1[e];
+          for (int sh = 0; sh < 2; ++sh) {
+            const int nt = 2 * c + sh;
+            if (jt < njt) {
+              const mf_f32x4 t4 = Hf::mfma32(v1a[i], sel[sh], mf_f32x4{0.f, 0.f, 0.f, 0.f});
+              *reinterpret_cast<float4*>(V1T + (nt * 16 + r16) * WS + jt * 16 + 4 * g) =
+                  float4{t4[0], t4[1], t4[2], t4[3]};
+            }
+            const mf_f32x4 w4 = Hf::mfma32(va[i], sel[sh], mf_f32x4{0.f, 0.f, 0.f, 0.f});
+            *reinterpret_cast<uint2*>(VB + ((nt * NPR + jt / 2) * 64 + lane) * 16 + (jt & 1) * 8) =
+                uint2{Hf::pack(w4[0], w4[1]), Hf::pack(w4[2], w4[3])};
+          }
         }
       }
       stage_pv(kidx, b, 0, nk, 0, nk);
-      // column maxima of |K2| from the registers (every wave holds all of K2;
-      // wave w reduces the elements e with e % kWaves == w): over kt, then r16
+      {
+        // column maxima of |K2| from the registers: over kt, then a reduce-
+        // scatter over the 16 key lanes; wave w takes the values v = w + kWaves i
+        // (column (v / 8) * 32 + 8 g + v % 8)
+        constexpr int NV = NCH * 8 / kWaves;
+        float mk[NV];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
+        for (int i = 0; i < NV; ++i) {
+          mk[i] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (e % kWaves != wave) continue;
-          float mx = 0.0f;
+          for (int vv = 0; vv < NCH * 8; ++vv) {
+            if (vv % kWaves != wave || vv / kWaves != i) continue;
 #pragma unroll
-          for (int kt = 0; kt < NT; ++kt) mx = fmaxf(mx, fabsf(float(ka[kt][c][e])));
-#pragma unroll
-          for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-          if (r16 == 0) m2s[c * 32 + g * 8 + e] = mx;
+            for (int kt = 0; kt < NT; ++kt) mk[i] = fmaxf(mk[i], fabsf(float(ka[kt][vv / 8][vv % 8])));
+          }
         }
+        int i2;
+        float m2 = reduce_scatter_max<NV, 8>(mk, lane, i2);
+#pragma unroll
+        for (int off = 8 / NV; off >= 1; off >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, off, 64));
+        const int v = wave + kWaves * i2;
+        m2s[(v / 8) * 32 + g * 8 + v % 8] = m2;
       }
       __syncthreads();
+      Op8 vb[ND][NPR];
+#pragma unroll
+      for (int nt = 0; nt < ND; ++nt)
+#pragma unroll
+        for (int pr = 0; pr < NPR; ++pr)
+          vb[nt][pr] = *reinterpret_cast<const Op8*>(VB + ((nt * NPR + pr) * 64 + lane) * 16);
       if (tid < DP) {
         float a0 = 0.0f;
 #pragma unroll
@@ -1001,10 +1181,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       __syncthreads();
       // sum_d |q'_d| m1_d m2_d <= |q'|_1 max_d (m1_d m2_d) = |q'|_1 M bounds |S| of a query
       const float mab = wave_max(lane < DP ? ab[lane] : 0.0f);
-      Op8 vb[ND][NPR];
-      load_vb(vb);
       const Op8 ones_edge = make_ones_edge(nk);
-      const int njt = ceil_div(nk, 16);
 
       if (njt == 0) {
         // valid queries of a molecule without keys: zero rows, lse 0
@@ -1029,22 +1206,17 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
           for (int nt = 0; nt < NN; ++nt) acc[nt] = 0.0f;
           float m = 0.0f;
           if (fast) {
-#pragma unroll 1
-            for (int jt = 0; jt < NKT; ++jt)
-              jtile_acc<T, DP, NT, NKT, HAS_PV, false>(K1s, V1T, pvb, ka, vb, ones_full, ones_edge, qo, jt, nk, nk,
-                                                       0.0f, acc, g, r16);
+            query_acc<T, DP, NT, NKT, HAS_PV, false>(K1s, V1T, pvb, ka, vb, ones_full, ones_edge, qo, nk, 0.0f, acc,
+                                                     g, r16);
           } else {
             float mloc = -INFINITY;
 #pragma unroll 1
             for (int jt = 0; jt < NKT; ++jt)
               mloc = fmaxf(mloc, jtile_max<T, DP, NT, NKT, HAS_PV>(K1s, pvb, ka, qo, jt, nk, nk, g, r16));
             m = wave_max(mloc);
-            if (m != -INFINITY) {
-#pragma unroll 1
-              for (int jt = 0; jt < NKT; ++jt)
-                jtile_acc<T, DP, NT, NKT, HAS_PV, true>(K1s, V1T, pvb, ka, vb, ones_full, ones_edge, qo, jt, nk, nk,
-                                                        m, acc, g, r16);
-            }
+            if (m != -INFINITY)
+              query_acc<T, DP, NT, NKT, HAS_PV, true>(K1s, V1T, pvb, ka, vb, ones_full, ones_edge, qo, nk, m, acc, g,
+                                                      r16);
           }
           write_row(row_off, acc, m);
         }
@@ -1053,7 +1225,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
     }
 
   }
-  if constexpr (MODE == 1) {
+  if constexpr (PART == 1) {
     // ---- molecules larger than one chunk: one query per wave, chunk pairs ----
     const int n_items = ws.hdr[1];
     if (n_items > 0) __syncthreads();  // LDS of the last small item
@@ -1109,6 +1281,14 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) 
       if (has_q) write_row(row_off, acc, m == -INFINITY ? 0.0f : m);
     }
   }
+}
+
+// MODE 0: small items only (every molecule fits one key chunk); MODE 1:
+// small items, then the larger molecules.
+template <typename T, int DP, int NT, bool HAS_PV, int MODE>
+__global__ void __launch_bounds__(kThreads, 2) simplicial_fast_kernel(Params p) {
+  fast_body<T, DP, NT, HAS_PV, 0>(p);
+  if constexpr (MODE == 1) fast_body<T, DP, NT, HAS_PV, 1>(p);
 }
 
 template <typename T, int DP, int NT, bool HAS_PV, int MODE>
