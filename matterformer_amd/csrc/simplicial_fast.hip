@@ -275,13 +275,15 @@ struct Layout {
   static constexpr size_t kVBBytes = size_t(DP / 16) * ((NT + 1) / 2) * 64 * 16;
   static constexpr size_t kV2TBytes = size_t(DP) * VS * sizeof(T);
   static constexpr size_t kV1T = (kV2T + (kVBBytes > kV2TBytes ? kVBBytes : kV2TBytes) + 15) & ~size_t(15);
-  static constexpr size_t kQs = kV1T + size_t(DP + 16) * WS * 4;
+  static constexpr size_t kQs = kV1T + size_t(DP + 1) * WS * 4;  // V1T rows: DP columns + key validity
   static constexpr size_t kPV = kQs + size_t(kMaxQueriesPerItem) * KS * sizeof(QT);
   static constexpr size_t kAB = kPV + size_t(CH) * PW * 4;
-  static constexpr size_t kM2 = kAB + size_t(DP) * 4;
-  static constexpr size_t kRed = kM2 + size_t(DP) * 4;
-  static constexpr size_t kQn = kRed + size_t(kWaves) * DP * 4;  // |q'|_1 of the item's queries
-  static constexpr size_t kFixed = (kQn + size_t(kMaxQueriesPerItem) * 4 + 15) & ~size_t(15);
+  static constexpr size_t kRed2 = kAB + size_t(DP) * 4;              // per-wave column maxima of |K2|
+  static constexpr size_t kRed = kRed2 + size_t(kWaves) * DP * 4;    // per-wave column maxima of |K1|
+  static constexpr size_t kQn = kRed + size_t(kWaves) * DP * 4;      // |q'|_1 of the item's queries
+  static constexpr size_t kKA = (kQn + size_t(kMaxQueriesPerItem) * 4 + 15) & ~size_t(15);
+  // small items: the K2 GEMM1 A operands (NT x DP/32 operands of 16 bytes per lane)
+  static constexpr size_t kFixed = kKA + size_t(NT) * (DP / 32) * 64 * 16;
 };
 
 // max over the valid logits of one 16-row j tile (log2 units, -inf if none);
@@ -382,7 +384,7 @@ __device__ __forceinline__ void jtile_acc(const typename Half<T>::K1T* K1s, cons
       const Op8 bop = nt < ND ? vb[nt < ND ? nt : 0][pr] : (pr == NPU - 1 ? ones_edge : ones_full);
       c2 = Hf::mfma32(a, bop, c2);
     }
-    const float4 v1 = *reinterpret_cast<const float4*>(V1T + (nt * 16 + r16) * L::WS + jt * 16 + 4 * g);
+    const float4 v1 = *reinterpret_cast<const float4*>(V1T + (nt < ND ? nt * 16 + r16 : DP) * L::WS + jt * 16 + 4 * g);
     acc[nt] += v1.x * c2[0] + v1.y * c2[1] + v1.z * c2[2] + v1.w * c2[3];
   }
 }
@@ -414,7 +416,7 @@ __device__ __forceinline__ void query_acc(const typename Half<T>::K1T* K1s, cons
     float4 v1[ND + 1];
 #pragma unroll
     for (int nt = 0; nt <= ND; ++nt)
-      v1[nt] = *reinterpret_cast<const float4*>(V1T + (nt * 16 + r16) * L::WS + jt * 16 + 4 * g);
+      v1[nt] = *reinterpret_cast<const float4*>(V1T + (nt < ND ? nt * 16 + r16 : DP) * L::WS + jt * 16 + 4 * g);
     Op8 b1[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) b1[c] = Hf::mul_v(k1[c], qo[c]);
@@ -773,6 +775,17 @@ __device__ __forceinline__ typename Half<T>::Op8 load8(const T* row, int e0, int
   return v;
 }
 
+// A work item, read through the scalar cache (constant address space): the
+// plan kernel wrote the list before this launch and nothing writes it during
+// the launch.  A scalar load is waited for at the first use of the header,
+// one item later, where a vector load would be waited for at once (its
+// uniform value moves to scalar registers).
+typedef __attribute__((address_space(4))) const int const_int;
+__device__ __forceinline__ int4 load_item(const int4* items, int i) {
+  const const_int* c = (const const_int*)items + 4 * i;
+  return int4{c[0], c[1], c[2], c[3]};
+}
+
 // Position of the valid atom of rank r: the identity when the valid atoms are
 // a prefix (idx == nullptr), else the plan's compacted list.
 __device__ __forceinline__ int atom_at(const int* idx, int r) { return idx ? idx[r] : r; }
@@ -820,7 +833,8 @@ __device__ __forceinline__ void fast_body(const Params& p) {
   QT* Qs = reinterpret_cast<QT*>(smem + L::kQs);
   uint32_t* pvb = reinterpret_cast<uint32_t*>(smem + L::kPV);
   float* ab = reinterpret_cast<float*>(smem + L::kAB);
-  float* m2s = reinterpret_cast<float*>(smem + L::kM2);
+  float* red2 = reinterpret_cast<float*>(smem + L::kRed2);
+  uint4* KA = reinterpret_cast<uint4*>(smem + L::kKA);
   float* red = reinterpret_cast<float*>(smem + L::kRed);
   float* qns = reinterpret_cast<float*>(smem + L::kQn);
   const int H = p.H, N = p.N, D = p.D;
@@ -884,11 +898,8 @@ __device__ __forceinline__ void fast_body(const Params& p) {
       }
     }
     if (with_v) {
-      // validity row (DP) and zero rows DP+1 .. DP+15 of V1T
-      for (int u = tid; u < 16 * CH; u += kThreads) {
-        const int rr = u / CH, col = u - rr * CH;
-        V1T[(DP + rr) * WS + col] = (rr == 0 && col < nkj) ? 1.0f : 0.0f;
-      }
+      // key validity row (DP) of V1T
+      for (int u = tid; u < CH; u += kThreads) V1T[DP * WS + u] = u < nkj ? 1.0f : 0.0f;
     }
     if (with_max) {
 #pragma unroll
@@ -954,12 +965,17 @@ __device__ __forceinline__ void fast_body(const Params& p) {
     }
   };
   // 0/1 selector B operands: sel[sh] picks columns 16 sh .. 16 sh + 15 of a
-  // 32-column A tile (B[kk][n] = 1 iff kk == n + 16 sh)
-  Op8 sel[2];
+  // 32-column A tile (B[kk][n] = 1 iff kk == n + 16 sh).  Built per item
+  // from an opaque zero so that they are not kept live through the query
+  // loops.
+  auto make_sel = [&](Op8 (&sel)[2]) {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
 #pragma unroll
-  for (int sh = 0; sh < 2; ++sh)
+    for (int sh = 0; sh < 2; ++sh)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sel[sh][e] = T(8 * g + e == r16 + 16 * sh ? 1.0f : 0.0f);
+      for (int e = 0; e < 8; ++e) sel[sh][e] = T(8 * g + e + z == r16 + 16 * sh ? 1.0f : 0.0f);
+  };
   // GEMM2 B operands of the denominator column: 1 in column 0 for full key
   // pairs; for the last pair of a chunk, 1 only at valid keys
   Op8 ones_full;
@@ -1015,9 +1031,6 @@ __device__ __forceinline__ void fast_body(const Params& p) {
   };
 
   if constexpr (PART == 0) {
-    // rows DP + 1 .. DP + 15 of V1T (the denominator tile's unused columns)
-    // stay zero for the whole launch
-    for (int u = tid; u < 15 * WS; u += kThreads) V1T[(DP + 1) * WS + u] = 0.0f;
     // with an odd tile count the upper half of the last B operand (keys
     // 16 NT .. 16 NT + 15) is never written: zero
     if constexpr (NT % 2 == 1) {
@@ -1025,10 +1038,10 @@ __device__ __forceinline__ void fast_body(const Params& p) {
         *reinterpret_cast<uint2*>(VB + (((u / 64) * NPR + NPR - 1) * 64 + u % 64) * 16 + 8) = uint2{0u, 0u};
     }
     const int n_items = ws.hdr[0];
-    int4 nxt = wg < n_items ? ws.small_items[wg] : int4{0, 0, 0, 0};
+    int4 nxt = wg < n_items ? load_item(ws.small_items, wg) : int4{0, 0, 0, 0};
     for (int item = wg; item < n_items; item += G) {
       const int4 it = nxt;
-      if (item + G < n_items) nxt = ws.small_items[item + G];  // next header, one item ahead
+      if (item + G < n_items) nxt = load_item(ws.small_items, item + G);  // next header, one item ahead
       const int b = it.x, h = it.y, q0 = it.z & 0xffff, q1 = it.z >> 16, nk = it.w & 0xffff;
       const int bh = b * H + h;
       const int* kidx = (uint32_t(it.w) & kKPre) ? nullptr : ws.kidx + size_t(b) * N;
@@ -1053,12 +1066,11 @@ __device__ __forceinline__ void fast_body(const Params& p) {
         const int r = kt * 16 + r16;
         krow[kt] = r < nk ? atom_at(kidx, r) : -1;
       }
-      // K1 and query rows (one thread per 8 columns of a row); K2 and V2 in
-      // the MFMA A layout (every wave holds all of them); this wave's share of
-      // the V1 tiles (16 keys x 32 columns, tile u = wave + kWaves i), also in
-      // the A layout
+      // K1 and query rows (one thread per 8 columns of a row); this wave's
+      // share of the K2, V1 and V2 tiles (16 keys x 32 columns, tile
+      // u = wave + kWaves i) in the MFMA A layout
       Op8 a[RPT], qv8[QPT];
-      Op8 ka[NT][NCH], va[NU], v1a[NU];
+      Op8 kaa[NU], va[NU], v1a[NU];
 #pragma unroll
       for (int t = 0; t < RPT; ++t)
         a[t] = jrow[t] >= 0 ? load8<T>(gk1 + (size_t(bh) * N + jrow[t]) * D, c8, D) : zero8<T>();
@@ -1066,18 +1078,12 @@ __device__ __forceinline__ void fast_body(const Params& p) {
       for (int t = 0; t < QPT; ++t)
         qv8[t] = qrow[t] >= 0 ? load8<T>(gq + (size_t(bh) * N + qrow[t]) * D, c8, D) : zero8<T>();
 #pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-          ka[kt][c] = krow[kt] >= 0 ? load8<T>(gk2 + (size_t(bh) * N + krow[kt]) * D, c * 32 + g * 8, D)
-                                    : zero8<T>();
-      }
-#pragma unroll
       for (int i = 0; i < NU; ++i) {
         const int u = wave + kWaves * i, jt = u / NCH, c = u % NCH;
         const int key = jt * 16 + r16;
         const int row = jt < NT && key < nk ? atom_at(kidx, key) : -1;
         const size_t src = (size_t(bh) * N + row) * D;
+        kaa[i] = row >= 0 ? load8<T>(gk2 + src, c * 32 + g * 8, D) : zero8<T>();
         v1a[i] = row >= 0 ? load8<T>(gv1 + src, c * 32 + g * 8, D) : zero8<T>();
         va[i] = row >= 0 ? load8<T>(gv2 + src, c * 32 + g * 8, D) : zero8<T>();
       }
@@ -1117,6 +1123,8 @@ __device__ __forceinline__ void fast_body(const Params& p) {
         red[wave * DP + c8 + e1] = mx;
       }
       if (tid < CH) V1T[DP * WS + tid] = tid < nk ? 1.0f : 0.0f;  // key validity row
+      Op8 sel[2];
+      make_sel(sel);
       // V1T[d][j] and the GEMM2 B operands of V2: an MFMA with a 0/1
       // selector B operand (exact) turns a 16-key x 32-column A tile into the
       // 16 x 16 C layout, lane (g, r16) holding keys 4g..4g+3 of column r16.
@@ -1143,27 +1151,31 @@ __device__ __forceinline__ void fast_body(const Params& p) {
       }
       stage_pv(kidx, b, 0, nk, 0, nk);
       {
-        // column maxima of |K2| from the registers: over kt, then a reduce-
-        // scatter over the 16 key lanes; wave w takes the values v = w + kWaves i
-        // (column (v / 8) * 32 + 8 g + v % 8)
-        constexpr int NV = NCH * 8 / kWaves;
-        float mk[NV];
+        // K2 operands to LDS, and this wave's column maxima of |K2|: per
+        // column chunk over the wave's tiles, then a reduce-scatter over the
+        // 16 key lanes (value v: column (v / 8) * 32 + 8 g + v % 8)
+        constexpr int NV2 = NCH * 8;
+        float mk[NV2];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          mk[i] = 0.0f;
+        for (int v = 0; v < NV2; ++v) mk[v] = 0.0f;
 #pragma unroll
-          for (int vv = 0; vv < NCH * 8; ++vv) {
-            if (vv % kWaves != wave || vv / kWaves != i) continue;
+        for (int i = 0; i < NU; ++i) {
+          const int u = wave + kWaves * i, c = u % NCH;
+          if (u < NT * NCH) {
+            KA[u * 64 + lane] = __builtin_bit_cast(uint4, kaa[i]);
 #pragma unroll
-            for (int kt = 0; kt < NT; ++kt) mk[i] = fmaxf(mk[i], fabsf(float(ka[kt][vv / 8][vv % 8])));
+            for (int cc = 0; cc < NCH; ++cc) {
+              if (cc != c) continue;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) mk[cc * 8 + e] = fmaxf(mk[cc * 8 + e], fabsf(float(kaa[i][e])));
+            }
           }
         }
         int i2;
-        float m2 = reduce_scatter_max<NV, 8>(mk, lane, i2);
+        float m2 = reduce_scatter_max<NV2, 8>(mk, lane, i2);
 #pragma unroll
-        for (int off = 8 / NV; off >= 1; off >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, off, 64));
-        const int v = wave + kWaves * i2;
-        m2s[(v / 8) * 32 + g * 8 + v % 8] = m2;
+        for (int off = 16 / NV2 / 2; off >= 1; off >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, off, 64));
+        red2[wave * DP + (i2 / 8) * 32 + g * 8 + i2 % 8] = m2;
       }
       __syncthreads();
       Op8 vb[ND][NPR];
@@ -1172,11 +1184,19 @@ __device__ __forceinline__ void fast_body(const Params& p) {
 #pragma unroll
         for (int pr = 0; pr < NPR; ++pr)
           vb[nt][pr] = *reinterpret_cast<const Op8*>(VB + ((nt * NPR + pr) * 64 + lane) * 16);
-      if (tid < DP) {
-        float a0 = 0.0f;
+      Op8 ka[NT][NCH];
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) a0 = fmaxf(a0, red[w * DP + tid]);
-        ab[tid] = a0 * m2s[tid];
+      for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) ka[kt][c] = __builtin_bit_cast(Op8, KA[(kt * NCH + c) * 64 + lane]);
+      if (tid < DP) {
+        float a0 = 0.0f, b0 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          a0 = fmaxf(a0, red[w * DP + tid]);
+          b0 = fmaxf(b0, red2[w * DP + tid]);
+        }
+        ab[tid] = a0 * b0;
       }
       __syncthreads();
       // sum_d |q'_d| m1_d m2_d <= |q'|_1 max_d (m1_d m2_d) = |q'|_1 M bounds |S| of a query
