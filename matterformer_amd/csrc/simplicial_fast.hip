@@ -6,31 +6,34 @@
 //   P_i      = softmax over valid (j,k) of S_i
 //   out_i[d] = sum_{j,k} P_i[j,k] v1_j[d] v2_k[d],   lse_i = log sum_{j,k} exp(S_i[j,k])
 //
-// Three launches on the caller's stream, no host synchronisation:
-//   plan   one workgroup turns the byte masks into, per molecule, compacted
-//          lists of valid keys, valid queries and padded query rows, and into
-//          work items (molecule, head, range of valid queries) holding about
-//          work_target logits each, ordered by molecule cost (largest first),
-//          all written to the caller's workspace;
-//   small  a persistent grid (2 workgroups per CU) walks the items of
-//          molecules with at most CH = 16*NT keys (all of a GEOM-Drugs batch)
-//          round-robin, so every workgroup gets one item from each cost band;
-//          it also zeroes the padded query rows;
-//   large  launched only when tokens > CH: molecules with more keys, in
-//          (j chunk, k chunk) pairs and two sweeps (exact maximum, then
-//          accumulation), one query per wave.
+// Two launches on the caller's stream, no host synchronisation:
+//   plan   workgroup 0 turns the byte masks into, per molecule, counts of
+//          valid keys and queries (and compacted index lists when the valid
+//          atoms are not a prefix), and into work items (molecule, head,
+//          range of at most 32 valid queries, about work_target logits); the
+//          items of molecules with at most CH = 16*NT keys ("small", all of a
+//          GEOM-Drugs batch) are listed by estimated time, longest first.
+//          The other workgroups of the launch zero the padded query rows.
+//   main   a persistent grid (2 workgroups per CU): round r gives small item
+//          r G + w to workgroup w for even r and r G + G - 1 - w for odd r,
+//          pairing long and short items; then, when tokens > CH, the larger
+//          molecules in (j chunk, k chunk) pairs with two sweeps (exact
+//          maximum, then accumulation), one query per wave.
 // Logical workgroup ids are remapped so that consecutive ids share an XCD
-// (blockIdx.x % 8 is the XCD): the items of one molecule land in one L2.
+// (blockIdx.x % 8 is the XCD): neighbouring items land in one L2.
 //
-// Per item the workgroup stages the keys of (b, h) in LDS:
-//   K1s  [CH][DP+4] fp32 (bf16) / [CH][DP+8] fp16   (source of the GEMM1 B operand)
-//   V2T  [DP][CH+8]    transposed                    (GEMM2 B operand)
-//   V1T  [DP+16][CH+4] fp32, transposed, plus a row of key validity
-//   Qs   the item's query rows times log2(e), fp32 (bf16) / fp16
-// and every wave loads K2 as GEMM1 A operands and V2 as GEMM2 B operands into
-// registers, where they stay for all of the wave's queries.
-// The inner loop reads LDS only for one K1 tile and one V1 tile per
-// (query, 16-row j tile).
+// Per small item the workgroup stages the keys of (b, h):
+//   K1s  [CH][DP+4] fp32 (bf16) / [CH][DP+8] fp16 in LDS (GEMM1 B operand source)
+//   V1T  [DP+1][CH+4] fp32 in LDS, transposed, plus a row of key validity
+//   Qs   the item's query rows times log2(e), fp32 (bf16) / fp16, in LDS
+//   K2 (GEMM1 A operands) and V2 (GEMM2 B operands) in every wave's registers
+//        for all of the wave's queries
+// Each of the four waves loads a quarter of the 16-key x 32-column tiles of
+// K2, V1 and V2 in the MFMA A layout.  V1 and V2 are transposed by an MFMA
+// against a 0/1 selector matrix (exact), which leaves each lane with 4
+// consecutive keys of one column: one 16-byte LDS store per lane for V1T, and
+// the GEMM2 B operand halves for V2.  The K2 and V2 operands go through LDS
+// once to reach the other waves.
 //
 // Per query i and j tile (16 keys j, lane column r16 = j):
 //   B1      = bf16(q'_i (.) K1[j])           q' = q log2(e); v_mul_f32 on K1 staged
@@ -45,16 +48,18 @@
 // padded keys need no masking: their K2/V2 rows are zero and their denominator
 // entry is 0.  Padded j rows get P = 1 but are weighted by V1 = 0 and
 // validity 0.  The code for each count of active 16-key tiles is generated
-// separately, so the inner loop is straight-line.
+// separately, so the inner loop is straight-line; the LDS reads of tile j + 1
+// are issued before the MFMAs of tile j.
 //
 // No running maximum in the common case.  With m_d = max_j |K1[j][d]| and
-// n_d = max_k |K2[k][d]|, |S_i[j,k]| <= U_i = sum_d |q'_i[d]| m_d n_d.  When
-// U_i <= bound_limit (60 for bf16, 14 for fp16: P = 2^S then stays a normal
-// number of the operand type and the fp32 sums cannot overflow) P = 2^S is used
-// directly: softmax is invariant to the offset, and floating point keeps the
-// same relative precision at any scale.  Otherwise the query takes two passes:
-// pass 1 computes the exact maximum m of the valid logits (GEMM1 only), pass 2
-// uses P = 2^(S - m) with explicit masking (the accumulator starts at -m).
+// n_d = max_k |K2[k][d]|, |S_i[j,k]| <= sum_d |q'_i[d]| m_d n_d
+// <= |q'_i|_1 max_d (m_d n_d) = U_i.  When U_i <= bound_limit (60 for bf16, 14
+// for fp16: P = 2^S then stays a normal number of the operand type and the
+// fp32 sums cannot overflow) P = 2^S is used directly: softmax is invariant to
+// the offset, and floating point keeps the same relative precision at any
+// scale.  Otherwise the query takes two passes: pass 1 computes the exact
+// maximum m of the valid logits (GEMM1 only), pass 2 uses P = 2^(S - m) with
+// explicit masking (the accumulator starts at -m).
 #include <cmath>
 #include <type_traits>
 
@@ -734,10 +739,18 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p)
   }
   __syncthreads();
 
-  // 4. items: one molecule's items are contiguous, heads interleaved with its
-  //    query ranges; small items first (in cost order), then large ones
+  // 4. items: a molecule's items are its query ranges, heads interleaved.
+  //    Large items are listed in molecule order.  Small items are listed by
+  //    estimated time, longest first: a counting sort on the query loop's
+  //    steps per wave, ceil(queries / kWaves) x key tiles (the main kernel
+  //    pairs long and short items from this order).
+  constexpr int kCostKeys = 64;
+  __shared__ int s_cnt[kCostKeys];
+  if (tid < kCostKeys) s_cnt[tid] = 0;
+  __syncthreads();
   const int small_total = s_small;
-  for (int u = tid; u < s_off[B]; u += kPlanThreads) {
+  const int n_all = s_off[B];
+  auto item_at = [&](int u, int4& item, int& key) {
     int lo = 0, hi = B - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -751,8 +764,33 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p)
     const int qpi = plan_queries_per_item(nk, c, p.work_target);
     const int local = u - s_off[lo];
     const int s = local / H, h = local - s * H;
-    const int4 item{b, h, (s * qpi) | (min(nq, (s + 1) * qpi) << 16), int(uint32_t(nk) | (w & (kKPre | kQPre)))};
-    if (c == 0) ws.small_items[u] = item;
+    const int qa = s * qpi, qb = min(nq, (s + 1) * qpi);
+    item = int4{b, h, qa | (qb << 16), int(uint32_t(nk) | (w & (kKPre | kQPre)))};
+    key = min(kCostKeys - 1, ((qb - qa + kWaves - 1) / kWaves) * ((nk + 15) / 16));
+    return c == 0;
+  };
+  for (int u = tid; u < n_all; u += kPlanThreads) {
+    int4 item;
+    int key;
+    if (item_at(u, item, key)) atomicAdd(&s_cnt[key], 1);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // first position of each key, keys in descending order (lane l: key 63 - l)
+    const int v = s_cnt[kCostKeys - 1 - tid];
+    int incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (tid >= off) incl += t;
+    }
+    s_cnt[kCostKeys - 1 - tid] = incl - v;
+  }
+  __syncthreads();
+  for (int u = tid; u < n_all; u += kPlanThreads) {
+    int4 item;
+    int key;
+    if (item_at(u, item, key)) ws.small_items[atomicAdd(&s_cnt[key], 1)] = item;
     else ws.large_items[u - small_total] = item;
   }
 }
@@ -1037,11 +1075,16 @@ __device__ __forceinline__ void fast_body(const Params& p) {
       for (int u = tid; u < ND * 64; u += kThreads)
         *reinterpret_cast<uint2*>(VB + (((u / 64) * NPR + NPR - 1) * 64 + u % 64) * 16 + 8) = uint2{0u, 0u};
     }
+    // The plan lists the items by estimated time, longest first.  Round r
+    // gives item r G + w to workgroup w for even r and item r G + G - 1 - w
+    // for odd r, so that each workgroup's long and short items pair up.
     const int n_items = ws.hdr[0];
+    auto pos_of = [&](int r) { return r * G + ((r & 1) ? G - 1 - wg : wg); };
     int4 nxt = wg < n_items ? load_item(ws.small_items, wg) : int4{0, 0, 0, 0};
-    for (int item = wg; item < n_items; item += G) {
+    for (int r = 0, item = wg; item < n_items; item = pos_of(++r)) {
       const int4 it = nxt;
-      if (item + G < n_items) nxt = load_item(ws.small_items, item + G);  // next header, one item ahead
+      const int inext = pos_of(r + 1);
+      if (inext < n_items) nxt = load_item(ws.small_items, inext);  // next header, one item ahead
       const int b = it.x, h = it.y, q0 = it.z & 0xffff, q1 = it.z >> 16, nk = it.w & 0xffff;
       const int bh = b * H + h;
       const int* kidx = (uint32_t(it.w) & kKPre) ? nullptr : ws.kidx + size_t(b) * N;
@@ -1362,7 +1405,7 @@ int simplicial_fast_launch(const mf_simplicial_fwd_args* a, void* workspace, int
   prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
   prm.ws = carve_workspace(workspace, a->batch, a->heads, a->tokens);
   prm.cap = simplicial_fast_capacity(a->head_dim);
-  prm.work_target = 48 * 1024;
+  prm.work_target = 128 * 1024;
   prm.bound_limit = a->dtype == MF_DTYPE_BF16 ? 60.0f : 14.0f;
   bool vec = (a->head_dim * 2) % 16 == 0;
   for (const void* ptr : {a->q, a->k1, a->v1, a->k2, a->v2, static_cast<const void*>(a->out)})
