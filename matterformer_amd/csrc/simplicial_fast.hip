@@ -536,30 +536,6 @@ __device__ __forceinline__ int plan_queries_per_item(int nk, int cls, int work_t
   return qpi - qpi % kWaves;
 }
 
-// One aligned dword of a mask row per lane: bytes of lane l are atoms
-// t = boff + e - off (e = 0..3).  Adds the valid bytes to `count` and notes a
-// "rise" (a valid atom right after an invalid one) in `rise`; `carry` is the
-// validity of the atom before the window (1 before the row).  Ballots and
-// scalar mask arithmetic only.
-__device__ __forceinline__ void scan_word(uint32_t w, int boff, int off, int N, int& carry, int& count, bool& rise) {
-  bool cb[4], pb[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int t = boff + e - off;
-    const bool in = t >= 0 && t < N;
-    cb[e] = in && ((w >> (8 * e)) & 0xffu) != 0;
-    pb[e] = t < 0 || cb[e];  // bytes before the row count as valid predecessors
-  }
-  const bool inner = (cb[1] && !pb[0]) || (cb[2] && !pb[1]) || (cb[3] && !pb[2]);
-  const unsigned long long b0 = __ballot(cb[0]);
-  const unsigned long long p3 = __ballot(pb[3]);
-  // byte 0 of lane l follows byte 3 of lane l - 1 (lane 0: the carry)
-  const unsigned long long pred = (p3 << 1) | (unsigned long long)(carry & 1);
-  rise = rise || __ballot(inner) != 0ull || (b0 & ~pred) != 0ull;
-  count += __popcll(b0) + __popcll(__ballot(cb[1])) + __popcll(__ballot(cb[2])) + __popcll(__ballot(cb[3]));
-  carry = int(p3 >> 63);
-}
-
 // The aligned dword at window offset base + 4 lane of a mask row (0 past the
 // row).  A dword that starts inside [row - off, row + N) stays on the row's
 // pages.
@@ -571,63 +547,79 @@ __device__ __forceinline__ uint32_t load_window(const uint8_t* row, int N, int b
   return boff < off + N ? *reinterpret_cast<const uint32_t*>(astart + boff) : 0u;
 }
 
+// Valid bytes of one window (the dword w of each lane, bytes of lane l at
+// atoms t = boff + e - off) added to `count`, and the last valid atom so far
+// in `last`.  The valid atoms are a prefix exactly when last + 1 == count.
+__device__ __forceinline__ void scan_window(uint32_t w, int boff, int off, int N, int& count, int& last) {
+  int ll = -1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = boff + e - off;
+    const bool v = t >= 0 && t < N && ((w >> (8 * e)) & 0xffu) != 0u;
+    count += __popcll(__ballot(v));
+    ll = v ? t : ll;
+  }
+  const unsigned long long any = __ballot(ll >= 0);
+  if (any) last = __builtin_amdgcn_readlane(ll, 63 - __builtin_clzll(any));
+}
+
 // dst[r] = the atom of valid rank r in a mask row (one wave).
 __device__ void write_ranks(const uint8_t* row, int N, int* dst, int lane) {
   const unsigned long long below = (1ull << lane) - 1ull;
   int run = 0;
-  for (int base = 0; base < N; base += 256) {
-    uint8_t v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = base + 64 * u + lane;
-      v[u] = t < N ? row[t] : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = base + 64 * u + lane;
-      const bool ok = t < N && v[u] != 0;
-      const unsigned long long bal = __ballot(ok);
-      if (ok) dst[run + __popcll(bal & below)] = t;
-      run += __popcll(bal);
-    }
+#pragma unroll 1
+  for (int t0 = 0; t0 < N; t0 += 64) {
+    const int t = t0 + lane;
+    const bool ok = t < N && row[t] != 0;
+    const unsigned long long bal = __ballot(ok);
+    if (ok) dst[run + __popcll(bal & below)] = t;
+    run += __popcll(bal);
   }
 }
 
 // Rows of padded queries are zeroed by workgroups 1.. of the plan launch,
-// concurrently with the plan itself (workgroup 0): 16-byte chunks of the
-// whole 16-bit output, the validity bytes of kZ chunks loaded before any is
-// tested.
+// concurrently with the plan itself (workgroup 0): one 16-byte chunk of the
+// 16-bit output per thread and step, rows (b, h, i) in b-major order.
 __device__ void zero_padded_rows(const Params& p, int worker, int workers) {
   const int per_row = p.D / 8;  // head_dim % 8 == 0 on this path
-  const long long total = (long long)p.B * p.H * p.N * per_row;
-  const long long stride = (long long)workers * kPlanThreads;
-  constexpr int kZ = 8;
-  for (long long base = (long long)worker * kPlanThreads + threadIdx.x; base < total; base += stride * kZ) {
-    long long row[kZ];
-    int col[kZ];
-    uint8_t valid[kZ];
-#pragma unroll
-    for (int z = 0; z < kZ; ++z) {
-      const long long idx = base + (long long)z * stride;
-      row[z] = idx / per_row;
-      col[z] = int(idx - row[z] * per_row);
-      const long long bh = row[z] / p.N;
-      const int i = int(row[z] - bh * p.N);
-      valid[z] = idx < total ? p.qv[(bh / p.H) * p.N + i] : 1;
+  const int rows_per_step = kPlanThreads / per_row;
+  const long long rows = (long long)p.B * p.H * p.N;
+  const int rr = threadIdx.x / per_row, c = threadIdx.x - rr * per_row;
+  if (rr >= rows_per_step) return;
+#pragma unroll 1
+  for (long long row = (long long)worker * rows_per_step + rr; row < rows; row += (long long)workers * rows_per_step) {
+    const long long bh = row / p.N;
+    const int i = int(row - bh * p.N);
+    if (p.qv[(bh / p.H) * p.N + i]) continue;
+    if (p.out) reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + row * p.D)[c] = uint4{0u, 0u, 0u, 0u};
+    if (p.out_f32) {
+      float4* o = reinterpret_cast<float4*>(p.out_f32 + row * p.D);
+      o[2 * c] = float4{0.f, 0.f, 0.f, 0.f};
+      o[2 * c + 1] = float4{0.f, 0.f, 0.f, 0.f};
     }
-#pragma unroll
-    for (int z = 0; z < kZ; ++z) {
-      if (valid[z]) continue;
-      const int c = col[z];
-      if (p.out) reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + row[z] * p.D)[c] = uint4{0u, 0u, 0u, 0u};
-      if (p.out_f32) {
-        float4* o = reinterpret_cast<float4*>(p.out_f32 + row[z] * p.D);
-        o[2 * c] = float4{0.f, 0.f, 0.f, 0.f};
-        o[2 * c + 1] = float4{0.f, 0.f, 0.f, 0.f};
-      }
-      if (c == 0 && p.lse) p.lse[row[z]] = 0.0f;
-    }
+    if (c == 0 && p.lse) p.lse[row] = 0.0f;
   }
+}
+
+// Items of one molecule: queries per item, item count and, for small
+// molecules, the cost keys of its full items and of its last item (the query
+// loop's steps per wave, ceil(queries / kWaves) x key tiles).
+constexpr int kCostKeys = 64;
+struct MolItems {
+  int cls, qpi, splits, n, key_full, key_last;
+};
+__device__ __forceinline__ MolItems mol_items(uint32_t w, int H, int cap, int work_target) {
+  MolItems m;
+  const int nk = info_nk(w), nq = info_nq(w);
+  m.cls = nk > cap ? 1 : 0;
+  m.qpi = plan_queries_per_item(nk, m.cls, work_target);
+  m.splits = (nq + m.qpi - 1) / m.qpi;
+  m.n = H * m.splits;
+  const int nkt = (nk + 15) / 16;
+  const int q_last = nq - (m.splits - 1) * m.qpi;
+  m.key_full = min(kCostKeys - 1, ((m.qpi + kWaves - 1) / kWaves) * nkt);
+  m.key_last = min(kCostKeys - 1, ((q_last + kWaves - 1) / kWaves) * nkt);
+  return m;
 }
 
 __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p) {
@@ -636,143 +628,56 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p)
     return;
   }
   constexpr int kPlanWaves = kPlanThreads / 64;
-  constexpr int kRound = 4;  // molecule rows a wave loads at once
   __shared__ uint32_t s_info[kMaxBatch];
-  __shared__ unsigned long long s_key[kMaxBatch];  // class, cost (descending), molecule
-  __shared__ int s_items[kMaxBatch];               // items of each molecule
-  __shared__ int s_order[kMaxBatch];               // molecule (| class << 16) at each sorted position
-  __shared__ int s_off[kMaxBatch + 1];             // first item of each sorted position
-  __shared__ int s_small;                          // items of the small class
+  __shared__ int s_cnt[kCostKeys];  // small items per cost key, then the next position of each key
+  __shared__ int s_small, s_large, s_large_next;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int B = p.B, H = p.H, N = p.N;
   const Workspace& ws = p.ws;
+  if (tid < kCostKeys) s_cnt[tid] = 0;
+  if (tid == 0) s_small = s_large = s_large_next = 0;
 
-  // 1. valid keys / queries per molecule and whether they form a prefix
-  if (N <= 252) {
-    // one aligned 256-byte window covers a row
-    for (int b0 = wave; b0 < B; b0 += kPlanWaves * kRound) {
-      uint32_t wk[kRound], wq[kRound];
-      int offk[kRound], offq[kRound];
-#pragma unroll
-      for (int m = 0; m < kRound; ++m) {
-        const int b = b0 + m * kPlanWaves;
-        wk[m] = wq[m] = 0u;
-        offk[m] = offq[m] = 0;
-        if (b < B) {
-          wk[m] = load_window(p.pkv + size_t(b) * N, N, 0, lane, offk[m]);
-          wq[m] = load_window(p.qv + size_t(b) * N, N, 0, lane, offq[m]);
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < kRound; ++m) {
-        const int b = b0 + m * kPlanWaves;
-        if (b >= B) break;
-        int ck = 0, cq = 0, carry_k = 1, carry_q = 1;
-        bool rk = false, rq = false;
-        scan_word(wk[m], 4 * lane, offk[m], N, carry_k, ck, rk);
-        scan_word(wq[m], 4 * lane, offq[m], N, carry_q, cq, rq);
-        if (lane == 0) s_info[b] = uint32_t(cq) | (uint32_t(ck) << 15) | (rk ? 0u : kKPre) | (rq ? 0u : kQPre);
-      }
+  // 1. valid keys / queries per molecule and whether they form a prefix (one
+  //    wave per molecule; both rows' windows are loaded before either is
+  //    scanned)
+#pragma unroll 1
+  for (int b = wave; b < B; b += kPlanWaves) {
+    int ck = 0, cq = 0, lk = -1, lq = -1;
+#pragma unroll 1
+    for (int base = 0; base < N + 3; base += 256) {
+      int offk, offq;
+      const uint32_t wk = load_window(p.pkv + size_t(b) * N, N, base, lane, offk);
+      const uint32_t wq = load_window(p.qv + size_t(b) * N, N, base, lane, offq);
+      scan_window(wk, base + 4 * lane, offk, N, ck, lk);
+      scan_window(wq, base + 4 * lane, offq, N, cq, lq);
     }
-  } else {
-    for (int b = wave; b < B; b += kPlanWaves) {
-      int ck = 0, cq = 0, carry_k = 1, carry_q = 1;
-      bool rk = false, rq = false;
-      for (int base = 0; base < N + 3; base += 256) {
-        int offk, offq;
-        const uint32_t wk = load_window(p.pkv + size_t(b) * N, N, base, lane, offk);
-        const uint32_t wq = load_window(p.qv + size_t(b) * N, N, base, lane, offq);
-        scan_word(wk, base + 4 * lane, offk, N, carry_k, ck, rk);
-        scan_word(wq, base + 4 * lane, offq, N, carry_q, cq, rq);
-      }
-      if (lane == 0) s_info[b] = uint32_t(cq) | (uint32_t(ck) << 15) | (rk ? 0u : kKPre) | (rq ? 0u : kQPre);
-    }
+    if (lane == 0)
+      s_info[b] = uint32_t(cq) | (uint32_t(ck) << 15) | (lk + 1 == ck ? kKPre : 0u) | (lq + 1 == cq ? kQPre : 0u);
   }
   __syncthreads();
 
   // 2. index lists of the molecules that need them
+#pragma unroll 1
   for (int b = wave; b < B; b += kPlanWaves) {
     const uint32_t w = s_info[b];
     if (!(w & kKPre)) write_ranks(p.pkv + size_t(b) * N, N, ws.kidx + size_t(b) * N, lane);
     if (!(w & kQPre)) write_ranks(p.qv + size_t(b) * N, N, ws.qidx + size_t(b) * N, lane);
   }
 
-  // 3. molecules in (class, cost descending, index) order and the first item
-  //    of each: every thread ranks its molecule against all others
-  unsigned long long key = ~0ull;
-  int cls = 0;
+  // 3. item counts: small items per cost key, large items in total
   if (tid < B) {
-    const uint32_t w = s_info[tid];
-    const int nk = info_nk(w), nq = info_nq(w);
-    cls = nk > p.cap ? 1 : 0;
-    const unsigned long long cost = (unsigned long long)nq * nk * nk;  // < 2^45
-    key = ((unsigned long long)cls << 62) | (((1ull << 46) - 1ull - cost) << 10) | (unsigned long long)tid;
-    const int qpi = plan_queries_per_item(nk, cls, p.work_target);
-    s_items[tid] = nq > 0 ? H * ((nq + qpi - 1) / qpi) : 0;
-    s_key[tid] = key;
-  }
-  __syncthreads();
-  int rank = 0, off = 0, total = 0, total_small = 0;
-  if (wave * 64 < B) {  // only the waves that hold molecules
-#pragma unroll 4
-    for (int u = 0; u < B; ++u) {
-      const unsigned long long ku = s_key[u];
-      const int iu = s_items[u];
-      const bool before = ku < key;
-      rank += before ? 1 : 0;
-      off += before ? iu : 0;
-      total += iu;
-      total_small += (ku >> 62) == 0ull ? iu : 0;
+    const MolItems m = mol_items(s_info[tid], H, p.cap, p.work_target);
+    if (m.n > 0) {
+      if (m.cls == 0) {
+        if (m.splits > 1) atomicAdd(&s_cnt[m.key_full], H * (m.splits - 1));
+        atomicAdd(&s_cnt[m.key_last], H);
+        atomicAdd(&s_small, m.n);
+      } else {
+        atomicAdd(&s_large, m.n);
+      }
     }
-  }
-  if (tid < B) {
-    s_order[rank] = tid | (cls << 16);
-    s_off[rank] = off;
-  }
-  if (tid == 0) {
-    s_off[B] = total;
-    s_small = total_small;
-    ws.hdr[0] = total_small;
-    ws.hdr[1] = total - total_small;
-  }
-  __syncthreads();
-
-  // 4. items: a molecule's items are its query ranges, heads interleaved.
-  //    Large items are listed in molecule order.  Small items are listed by
-  //    estimated time, longest first: a counting sort on the query loop's
-  //    steps per wave, ceil(queries / kWaves) x key tiles (the main kernel
-  //    pairs long and short items from this order).
-  constexpr int kCostKeys = 64;
-  __shared__ int s_cnt[kCostKeys];
-  if (tid < kCostKeys) s_cnt[tid] = 0;
-  __syncthreads();
-  const int small_total = s_small;
-  const int n_all = s_off[B];
-  auto item_at = [&](int u, int4& item, int& key) {
-    int lo = 0, hi = B - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_off[mid] <= u) lo = mid; else hi = mid - 1;
-    }
-    const int ord = s_order[lo];
-    const int b = ord & 0xffff;
-    const int c = ord >> 16;
-    const uint32_t w = s_info[b];
-    const int nk = info_nk(w), nq = info_nq(w);
-    const int qpi = plan_queries_per_item(nk, c, p.work_target);
-    const int local = u - s_off[lo];
-    const int s = local / H, h = local - s * H;
-    const int qa = s * qpi, qb = min(nq, (s + 1) * qpi);
-    item = int4{b, h, qa | (qb << 16), int(uint32_t(nk) | (w & (kKPre | kQPre)))};
-    key = min(kCostKeys - 1, ((qb - qa + kWaves - 1) / kWaves) * ((nk + 15) / 16));
-    return c == 0;
-  };
-  for (int u = tid; u < n_all; u += kPlanThreads) {
-    int4 item;
-    int key;
-    if (item_at(u, item, key)) atomicAdd(&s_cnt[key], 1);
   }
   __syncthreads();
   if (tid < 64) {
@@ -785,13 +690,43 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p)
       if (tid >= off) incl += t;
     }
     s_cnt[kCostKeys - 1 - tid] = incl - v;
+    if (tid == 0) {
+      ws.hdr[0] = s_small;
+      ws.hdr[1] = s_large;
+    }
   }
   __syncthreads();
-  for (int u = tid; u < n_all; u += kPlanThreads) {
-    int4 item;
-    int key;
-    if (item_at(u, item, key)) ws.small_items[atomicAdd(&s_cnt[key], 1)] = item;
-    else ws.large_items[u - small_total] = item;
+
+  // 4. items (one wave per molecule): a molecule's items are its query
+  //    ranges, heads interleaved; small items go to the positions of their
+  //    cost keys (longest first), large ones follow each other
+#pragma unroll 1
+  for (int b = wave; b < B; b += kPlanWaves) {
+    const uint32_t w = s_info[b];
+    const MolItems m = mol_items(w, H, p.cap, p.work_target);
+    if (m.n == 0) continue;
+    const int n_full = H * (m.splits - 1);
+    int base_full = 0, base_last = 0;
+    if (lane == 0) {
+      if (m.cls == 0) {
+        if (n_full > 0) base_full = atomicAdd(&s_cnt[m.key_full], n_full);
+        base_last = atomicAdd(&s_cnt[m.key_last], H) - n_full;
+      } else {
+        base_full = base_last = atomicAdd(&s_large_next, m.n);
+      }
+    }
+    base_full = __shfl(base_full, 0, 64);
+    base_last = __shfl(base_last, 0, 64);
+    const int nk = info_nk(w), nq = info_nq(w);
+#pragma unroll 1
+    for (int l = lane; l < m.n; l += 64) {
+      const int sp = l / H, h = l - sp * H;
+      const int4 item{b, h, (sp * m.qpi) | (min(nq, (sp + 1) * m.qpi) << 16),
+                      int(uint32_t(nk) | (w & (kKPre | kQPre)))};
+      const int pos = (l < n_full ? base_full : base_last) + l;
+      if (m.cls == 0) ws.small_items[pos] = item;
+      else ws.large_items[pos] = item;
+    }
   }
 }
 
