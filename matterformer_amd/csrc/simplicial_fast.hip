@@ -640,21 +640,46 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p)
   if (tid == 0) s_small = s_large = s_large_next = 0;
 
   // 1. valid keys / queries per molecule and whether they form a prefix (one
-  //    wave per molecule; both rows' windows are loaded before either is
-  //    scanned)
-#pragma unroll 1
-  for (int b = wave; b < B; b += kPlanWaves) {
-    int ck = 0, cq = 0, lk = -1, lq = -1;
-#pragma unroll 1
-    for (int base = 0; base < N + 3; base += 256) {
-      int offk, offq;
-      const uint32_t wk = load_window(p.pkv + size_t(b) * N, N, base, lane, offk);
-      const uint32_t wq = load_window(p.qv + size_t(b) * N, N, base, lane, offq);
-      scan_window(wk, base + 4 * lane, offk, N, ck, lk);
-      scan_window(wq, base + 4 * lane, offq, N, cq, lq);
-    }
+  //    wave per molecule).  Rows of up to 252 bytes are one window: the
+  //    windows of kRound molecules are loaded before any is scanned.
+  constexpr int kRound = 4;
+  auto put_info = [&](int b, int ck, int lk, int cq, int lq) {
     if (lane == 0)
       s_info[b] = uint32_t(cq) | (uint32_t(ck) << 15) | (lk + 1 == ck ? kKPre : 0u) | (lq + 1 == cq ? kQPre : 0u);
+  };
+  if (N <= 252) {
+#pragma unroll 1
+    for (int b0 = wave; b0 < B; b0 += kPlanWaves * kRound) {
+      uint32_t wk[kRound], wq[kRound];
+      int offk[kRound], offq[kRound];
+#pragma unroll
+      for (int r = 0; r < kRound; ++r) {
+        const int b = min(b0 + r * kPlanWaves, B - 1);
+        wk[r] = load_window(p.pkv + size_t(b) * N, N, 0, lane, offk[r]);
+        wq[r] = load_window(p.qv + size_t(b) * N, N, 0, lane, offq[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < kRound; ++r) {
+        int ck = 0, cq = 0, lk = -1, lq = -1;
+        scan_window(wk[r], 4 * lane, offk[r], N, ck, lk);
+        scan_window(wq[r], 4 * lane, offq[r], N, cq, lq);
+        if (b0 + r * kPlanWaves < B) put_info(b0 + r * kPlanWaves, ck, lk, cq, lq);
+      }
+    }
+  } else {
+#pragma unroll 1
+    for (int b = wave; b < B; b += kPlanWaves) {
+      int ck = 0, cq = 0, lk = -1, lq = -1;
+#pragma unroll 1
+      for (int base = 0; base < N + 3; base += 256) {
+        int offk, offq;
+        const uint32_t wk = load_window(p.pkv + size_t(b) * N, N, base, lane, offk);
+        const uint32_t wq = load_window(p.qv + size_t(b) * N, N, base, lane, offq);
+        scan_window(wk, base + 4 * lane, offk, N, ck, lk);
+        scan_window(wq, base + 4 * lane, offq, N, cq, lq);
+      }
+      put_info(b, ck, lk, cq, lq);
+    }
   }
   __syncthreads();
 
@@ -699,33 +724,45 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_plan_kernel(Params p)
 
   // 4. items (one wave per molecule): a molecule's items are its query
   //    ranges, heads interleaved; small items go to the positions of their
-  //    cost keys (longest first), large ones follow each other
+  //    cost keys (longest first), large ones follow each other.  Lane r
+  //    claims the positions of the wave's molecule of round r (64 rounds at
+  //    a time), so one LDS atomic instruction serves them all.
 #pragma unroll 1
-  for (int b = wave; b < B; b += kPlanWaves) {
-    const uint32_t w = s_info[b];
-    const MolItems m = mol_items(w, H, p.cap, p.work_target);
-    if (m.n == 0) continue;
-    const int n_full = H * (m.splits - 1);
-    int base_full = 0, base_last = 0;
-    if (lane == 0) {
-      if (m.cls == 0) {
-        if (n_full > 0) base_full = atomicAdd(&s_cnt[m.key_full], n_full);
-        base_last = atomicAdd(&s_cnt[m.key_last], H) - n_full;
-      } else {
-        base_full = base_last = atomicAdd(&s_large_next, m.n);
+  for (int b0 = wave; b0 < B; b0 += kPlanWaves * 64) {
+    int bf = 0, bl = 0;
+    {
+      const int b = b0 + lane * kPlanWaves;
+      if (b < B) {
+        const MolItems m = mol_items(s_info[b], H, p.cap, p.work_target);
+        const int n_full = H * (m.splits - 1);
+        if (m.n > 0) {
+          if (m.cls == 0) {
+            if (n_full > 0) bf = atomicAdd(&s_cnt[m.key_full], n_full);
+            bl = atomicAdd(&s_cnt[m.key_last], H) - n_full;
+          } else {
+            bf = bl = atomicAdd(&s_large_next, m.n);
+          }
+        }
       }
     }
-    base_full = __shfl(base_full, 0, 64);
-    base_last = __shfl(base_last, 0, 64);
-    const int nk = info_nk(w), nq = info_nq(w);
 #pragma unroll 1
-    for (int l = lane; l < m.n; l += 64) {
-      const int sp = l / H, h = l - sp * H;
-      const int4 item{b, h, (sp * m.qpi) | (min(nq, (sp + 1) * m.qpi) << 16),
-                      int(uint32_t(nk) | (w & (kKPre | kQPre)))};
-      const int pos = (l < n_full ? base_full : base_last) + l;
-      if (m.cls == 0) ws.small_items[pos] = item;
-      else ws.large_items[pos] = item;
+    for (int r = 0; r < 64 && b0 + r * kPlanWaves < B; ++r) {
+      const int b = b0 + r * kPlanWaves;
+      const uint32_t w = s_info[b];
+      const MolItems m = mol_items(w, H, p.cap, p.work_target);
+      const int n_full = H * (m.splits - 1);
+      const int base_full = __shfl(bf, r, 64);
+      const int base_last = __shfl(bl, r, 64);
+      const int nk = info_nk(w), nq = info_nq(w);
+#pragma unroll 1
+      for (int l = lane; l < m.n; l += 64) {
+        const int sp = l / H, h = l - sp * H;
+        const int4 item{b, h, (sp * m.qpi) | (min(nq, (sp + 1) * m.qpi) << 16),
+                        int(uint32_t(nk) | (w & (kKPre | kQPre)))};
+        const int pos = (l < n_full ? base_full : base_last) + l;
+        if (m.cls == 0) ws.small_items[pos] = item;
+        else ws.large_items[pos] = item;
+      }
     }
   }
 }
