@@ -567,7 +567,10 @@ extern "C" int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t
 extern "C" uint64_t mf_simplicial_fwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens,
                                                      int32_t head_dim, int32_t dtype) {
   if (batch <= 0 || heads <= 0 || tokens <= 0 || !uses_fast(head_dim, dtype)) return 0;
-  return simplicial_fast_workspace_bytes(batch, heads, tokens);
+  // enough for either 16-bit path (unaligned operands take the other one)
+  const uint64_t fast = simplicial_fast_workspace_bytes(batch, heads, tokens);
+  if (!simplicial_pair_serves(tokens, head_dim, dtype)) return fast;
+  return std::max<uint64_t>(fast, simplicial_pair_workspace_bytes(batch, tokens));
 }
 
 static int launch_general(const mf_simplicial_fwd_args* a, size_t lds, int num_cus, int min_keys, bool zero_rows,
@@ -629,6 +632,41 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
   // set of launches per slice of at most kSimplicialFastMaxBatch molecules
   // (the slices reuse the workspace in stream order).
   size_t lds = 0;
+  const bool outputs_aligned = reinterpret_cast<uintptr_t>(a->out) % 16 == 0 &&
+                               reinterpret_cast<uintptr_t>(a->out_f32) % 16 == 0;
+  if (uses_fast(a->head_dim, a->dtype) && operands_aligned(a) && outputs_aligned &&
+      simplicial_pair_serves(a->tokens, a->head_dim, a->dtype)) {
+    // the pair-flash kernels: plan + main launch per slice of molecules (the
+    // slices reuse the schedule workspace in stream order)
+    const uint64_t need = simplicial_pair_workspace_bytes(a->batch, a->tokens);
+    if (a->workspace == nullptr || a->workspace_bytes < need)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: workspace of " + std::to_string(need) +
+                                               " bytes required (mf_simplicial_fwd_workspace_size), got " +
+                                               std::to_string(a->workspace_bytes));
+    if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: workspace must be 16-byte aligned");
+    const int slice = simplicial_pair_max_batch(a->tokens);
+    const size_t row = size_t(a->heads) * a->tokens;
+    const size_t elem = row * a->head_dim * 2;
+    for (int b0 = 0; b0 < a->batch; b0 += slice) {
+      mf_simplicial_fwd_args sub = *a;
+      sub.batch = std::min(slice, a->batch - b0);
+      sub.q = static_cast<const char*>(a->q) + b0 * elem;
+      sub.k1 = static_cast<const char*>(a->k1) + b0 * elem;
+      sub.v1 = static_cast<const char*>(a->v1) + b0 * elem;
+      sub.k2 = static_cast<const char*>(a->k2) + b0 * elem;
+      sub.v2 = static_cast<const char*>(a->v2) + b0 * elem;
+      sub.query_valid = a->query_valid + size_t(b0) * a->tokens;
+      sub.pair_key_valid = a->pair_key_valid + size_t(b0) * a->tokens;
+      if (a->pair_valid) sub.pair_valid = a->pair_valid + size_t(b0) * a->tokens * a->tokens;
+      if (a->out) sub.out = static_cast<char*>(a->out) + b0 * elem;
+      if (a->out_f32) sub.out_f32 = a->out_f32 + b0 * row * a->head_dim;
+      if (a->lse) sub.lse = a->lse + b0 * row;
+      st = simplicial_pair_launch(&sub, a->workspace, dev.num_cus, s);
+      if (st != MF_OK) return st;
+    }
+    return MF_OK;
+  }
   if (uses_fast(a->head_dim, a->dtype) && operands_aligned(a)) {
     if (a->tokens > 32767) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports tokens <= 32767");
     const uint64_t need = simplicial_fast_workspace_bytes(a->batch, a->heads, a->tokens);

@@ -1,0 +1,1236 @@
+// 2-simplicial attention forward for 16-bit operands on gfx950 (CDNA4),
+// written as flash attention over key PAIRS: the kernel behind
+// mf_simplicial_fwd for bf16/fp16, head_dim <= 64 (a multiple of 8) and
+// tokens <= kMaxN.
+//
+// Math (simplicial_attention.py:161-180,304-344; triton_simplicial_attention.py:115-329):
+//   S_i[j,k] = sum_d q_i[d] k1_j[d] k2_k[d]
+//   P_i      = softmax over valid (j,k) of S_i
+//   out_i[d] = sum_{j,k} P_i[j,k] v1_j[d] v2_k[d],   lse_i = log sum_{j,k} exp(S_i[j,k])
+// Read the valid pairs p = (j,k) as keys with key vector W_p = k1_j (.) k2_k
+// and value vector Z_p = v1_j (.) v2_k: then S = Q W^T and out = softmax(S) Z,
+// plain attention over nk^2 keys whose tiles are formed on the fly.
+//
+// One launch, no workspace.  A persistent grid of 2 workgroups per CU; each
+// workgroup first reads every molecule's two byte masks (valid keys, valid
+// queries), ranks the molecules by cost and enumerates the units
+// (molecule b, head h, query group g) in that order -- every workgroup
+// derives the same list -- and takes units r G + w (even rounds) and
+// r G + G - 1 - w (odd rounds) of it, so that long and short units pair up.
+// A query group is at most 48 valid queries (3 tiles of 16); molecules with
+// more than 48 queries use groups of 32.  The rows of padded queries are
+// zeroed by a static share of (b, h) per workgroup.
+//
+// Per unit the workgroup stages the unit's valid key rows (compacted) into
+// LDS as fp16 scaled by powers of two: K1s, K2s row-major, V1s, V2s as
+// [row][r16][dt] (the ND = DP/16 halves of columns r16, 16+r16, ... side by
+// side), and the group's query rows Qs = q log2(e) 2^sq.  The scales
+// normalise max|K1|, max|K2|, max|V1|, max|V2| into [1, 2), so every pair
+// product is a normal fp16 number and one v_pk_mul_f16 forms two of them;
+// sq = -(s1 + s2) keeps S in log2 units.  Keys beyond kCap are taken in
+// (j block, k block) pairs of kCap keys.
+//
+// The four waves split the iterations (16-key tile kt of k, pair of rows
+// j0, j0+1) of the unit.  Per iteration and wave (QT query tiles):
+//   W      = K1s[j] (.) K2s[k0 + r16]            (A operand: pair = row, d = K)
+//   GEMM1  S^T[pair][i] = W Q^T                   (MFMA 16x16x32 f16, 2 QT per j)
+//   P      = fp16(2^S)                            (B operand of GEMM2 straight from
+//                                                  the accumulators: keys 4g+r of j0
+//                                                  and of j0+1 are K 8g..8g+7)
+//   Z      = V1s[j] (.) V2s[k0 + 4g + r]          (A operand: d = row, pair = K)
+//   GEMM2  O^T[d][i] += Z^T P                     (MFMA, ND QT per iteration)
+//   L[i]  += 1^T P                                (one MFMA per query tile, A = 1
+//                                                  at the valid keys)
+// Padded keys (k >= nk) and the padding row j0+1 = nk have zero K and V rows:
+// their P is finite, Z = 0 removes them from O and the ones operand from L.
+// pair_valid clears P bit by bit.
+//
+// No running maximum in the common case.  With m_d = max_j |k1_j[d]| and
+// n_d = max_k |k2_k[d]|, |S_i[j,k]| <= U_i = sum_d |q'_i[d]| m_d n_d.  When
+// U_i <= kBoundLimit for every query of the unit (and the query scale is
+// representable), P = 2^S lies in [2^-U, 2^U], inside the normal fp16 range,
+// and softmax is invariant to the missing offset.  Otherwise the unit takes
+// two passes: the exact maximum m_i of the valid logits (GEMM1 only), then
+// P = 2^(S - m_i) with S rescaled to log2 units (the query scale is then
+// normalised on its own: sq = 1 - exponent(max|q'|)).
+#include <cmath>
+#include <type_traits>
+
+#include "mf_common.h"
+
+namespace mf {
+namespace spair {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kCap = 128;             // keys per staged block (one row per 2 threads)
+constexpr int kMaxQ = 48;             // queries per unit
+constexpr int kMaxBatch = 256;        // molecules per launch
+constexpr int kMaxN = 512;            // tokens
+constexpr float kBoundLimit = 13.5f;  // fast path bound on |S| (log2 units)
+constexpr float kQLimit = 8192.0f;    // fast path bound on max |Qs|
+
+enum Mode { kFast = 0, kSlow = 1, kMax = 2 };
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+
+struct Params {
+  const void* q;
+  const void* k1;
+  const void* v1;
+  const void* k2;
+  const void* v2;
+  const uint8_t* qv;
+  const uint8_t* pkv;
+  const uint8_t* pv;
+  void* out;
+  float* out_f32;
+  float* lse;
+  int* ws;  // the schedule (see Schedule)
+  int B, H, N, D;
+};
+
+// The schedule the plan kernel writes for the main kernel (int words):
+//   total               units of the launch
+//   info[B]             molecule info word (see info_*)
+//   order[B]            molecule of each cost rank, longest first
+//   pre[B + 1]          first unit position of each rank (pre[B] = total)
+//   kidx[B][N], qidx[B][N]  u16 valid key / query atoms of the molecules whose
+//                       valid atoms are not a prefix (others are not written)
+struct Schedule {
+  int* total;
+  uint32_t* info;
+  int* order;
+  int* pre;
+  uint16_t* kidx;
+  uint16_t* qidx;
+};
+__host__ __device__ inline Schedule carve_schedule(int* ws, int B, int N) {
+  Schedule sc;
+  sc.total = ws;
+  sc.info = reinterpret_cast<uint32_t*>(ws + 4);
+  sc.order = ws + 4 + B;
+  sc.pre = ws + 4 + 2 * B;
+  int* tail = ws + 4 + 3 * B + 4;
+  sc.kidx = reinterpret_cast<uint16_t*>(tail);
+  sc.qidx = sc.kidx + size_t(B) * N;
+  return sc;
+}
+__host__ inline size_t schedule_bytes(int B, int N) {
+  return (4 + 3 * size_t(B) + 4) * 4 + 2 * size_t(B) * N * 2;
+}
+
+// LDS layout (bytes) for padded head dim DP.
+template <int DP>
+struct Lay {
+  static constexpr int RB = DP * 2;  // bytes per staged fp16 row
+  static constexpr int kK1 = 0;
+  static constexpr int kK2 = kK1 + kCap * RB;
+  static constexpr int kV1 = kK2 + kCap * RB;
+  static constexpr int kV2 = kV1 + kCap * RB;
+  static constexpr int kQ = kV2 + kCap * RB;
+  static constexpr int kPV = kQ + kMaxQ * RB;             // u32 [kCap][kCap / 32] pair-valid bits
+  static constexpr int kInfo = kPV + kCap * (kCap / 32) * 4;  // u32 [kMaxBatch] molecule info
+  static constexpr int kPre = kInfo + kMaxBatch * 4;     // int [kMaxBatch + 4] unit prefix by rank
+  static constexpr int kOrder = kPre + (kMaxBatch + 4) * 4;  // u16 [kMaxBatch] molecule of each rank
+  static constexpr int kKidx = kOrder + kMaxBatch * 2;   // u16 [kMaxN] valid key atoms
+  static constexpr int kQidx = kKidx + kMaxN * 2;        // u16 [kMaxN] valid query atoms
+  // column maxima float [kWaves][2][DP]; aliased by the molecule costs
+  // (schedule) and by the per-wave query maxima (two-pass mode)
+  static constexpr int kColBytes = kWaves * 2 * DP * 4 > kMaxBatch * 4 ? kWaves * 2 * DP * 4 : kMaxBatch * 4;
+  static constexpr int kCol = kQidx + kMaxN * 2;
+  static constexpr int kMn = kCol + (kColBytes > kWaves * kMaxQ * 4 ? kColBytes : kWaves * kMaxQ * 4);
+  static constexpr int kG = kMn + DP * 4;       // float [kWaves][4] |V1|, |V2|, |q| maxima
+  static constexpr int kScal = kG + kWaves * 4 * 4;  // int [8] scale exponents, slow flag
+  static constexpr int kM = kScal + 8 * 4;      // float [kMaxQ] two-pass maxima (log2 units)
+  static constexpr int kTotal = kM + kMaxQ * 4;
+  // after the pair loop: per-wave partial outputs float [kWaves][kMaxQ][RS]
+  // and denominators float [kWaves][kMaxQ], over K1s .. V2s
+  static constexpr int RS = DP + 4;
+  static constexpr int kRed = 0;
+  static constexpr int kRedL = kRed + kWaves * kMaxQ * RS * 4;
+  static_assert(kRedL + kWaves * kMaxQ * 4 <= kQ, "reduction area must fit in the K/V staging area");
+};
+
+// ---------------------------------------------------------------------------
+// small helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pkmul(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, a) * __builtin_bit_cast(h2_t, b));
+}
+__device__ __forceinline__ uint4 pkmul4(uint4 a, uint4 b) {
+  return uint4{pkmul(a.x, b.x), pkmul(a.y, b.y), pkmul(a.z, b.z), pkmul(a.w, b.w)};
+}
+// (a.lo * w.h, a.hi * w.h) with w.h the half HI of w
+template <int HI>
+__device__ __forceinline__ uint32_t pkmul_splat(uint32_t a, uint32_t w) {
+  const h2_t x = __builtin_bit_cast(h2_t, w);
+  const h2_t s = HI ? h2_t{x.y, x.y} : h2_t{x.x, x.x};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, a) * s);
+}
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{lo, hi}, h2_t));
+}
+__device__ __forceinline__ mf_f32x4 mfma(uint4 a, uint4 b, mf_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf_f16x8, a), __builtin_bit_cast(mf_f16x8, b), c,
+                                                0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ float elem_lo(uint32_t w) {
+  if constexpr (std::is_same<T, __bf16>::value) return __uint_as_float(w << 16);
+  else return float(__builtin_bit_cast(h2_t, w).x);
+}
+template <typename T>
+__device__ __forceinline__ float elem_hi(uint32_t w) {
+  if constexpr (std::is_same<T, __bf16>::value) return __uint_as_float(w & 0xffff0000u);
+  else return float(__builtin_bit_cast(h2_t, w).y);
+}
+// the 8 elements of a 16-byte chunk as floats
+template <typename T>
+__device__ __forceinline__ void unpack8(uint4 u, float (&f)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    f[2 * p] = elem_lo<T>(w[p]);
+    f[2 * p + 1] = elem_hi<T>(w[p]);
+  }
+}
+
+// Maximum over the lanes l ^ OFF, l ^ OFF/2, ..., l ^ LAST (log2 NV steps)
+// of NV values per lane, scattered: each step keeps half of the values, so
+// the lane ends with the maximum of value idx.
+template <int NV, int OFF, int LAST>
+__device__ __forceinline__ float reduce_scatter_max(const float (&v)[NV], int lane, int& idx) {
+  if constexpr (NV == 1) {
+    // remaining steps reduce the single value
+    float r = v[0];
+#pragma unroll
+    for (int off = OFF; off >= LAST; off >>= 1) r = fmaxf(r, __shfl_xor(r, off, 64));
+    idx = 0;
+    return r;
+  } else if constexpr (OFF < LAST) {
+    // no lanes left: reduce locally
+    float r = v[0];
+#pragma unroll
+    for (int i = 1; i < NV; ++i) r = fmaxf(r, v[i]);
+    idx = -1;
+    return r;
+  } else {
+    const bool up = (lane & OFF) != 0;
+    float k[NV / 2];
+#pragma unroll
+    for (int i = 0; i < NV / 2; ++i) {
+      const float send = up ? v[i] : v[i + NV / 2];
+      const float keep = up ? v[i + NV / 2] : v[i];
+      k[i] = fmaxf(keep, __shfl_xor(send, OFF, 64));
+    }
+    int sub;
+    const float r = reduce_scatter_max<NV / 2, OFF / 2, LAST>(k, lane, sub);
+    idx = (up ? NV / 2 : 0) + sub;
+    return r;
+  }
+}
+
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a),
+                                                                __builtin_bit_cast(u16x2_t, b)));
+}
+// |x| from the 16-bit pattern of x with the sign cleared
+template <typename T>
+__device__ __forceinline__ float mag_to_float(uint32_t m) {
+  if constexpr (std::is_same<T, __bf16>::value) return __uint_as_float(m << 16);
+  else return float(__builtin_bit_cast(_Float16, uint16_t(m)));
+}
+
+// Exponent s with x 2^s in [1, 2) (0 for x == 0 or not finite).
+__device__ __forceinline__ int norm_exp(float x) {
+  if (!(x > 0.0f) || !(x < INFINITY)) return 0;
+  int e;
+  (void)frexpf(x, &e);
+  return 1 - e;
+}
+
+// Molecule info word: nk | nq << 11 | kpre << 30 | qpre << 31 (kpre / qpre:
+// the valid keys / queries are exactly the prefix 0..n-1).
+constexpr uint32_t kKPre = 1u << 30;
+constexpr uint32_t kQPre = 1u << 31;
+__device__ __forceinline__ int info_nk(uint32_t w) { return int(w & 0x7ffu); }
+__device__ __forceinline__ int info_nq(uint32_t w) { return int((w >> 11) & 0x7ffu); }
+
+// Query groups of a molecule with nk valid keys and nq valid queries: one
+// group of up to 48, else groups of 32; molecules with more than kCap keys
+// (taken in key blocks) use groups of 16, one query tile.
+__device__ __forceinline__ int group_size(int nk, int nq) {
+  if (nk > kCap) return 16;
+  return nq <= kMaxQ ? kMaxQ : 32;
+}
+__device__ __forceinline__ int num_groups(int nk, int nq) {
+  if (nq <= 0) return 0;
+  const int gs = group_size(nk, nq);
+  return (nq + gs - 1) / gs;
+}
+
+// The aligned dword at window offset base + 4 lane of a mask row (0 past the
+// row).  A dword that starts inside [row - off, row + N) stays on the row's
+// pages.
+__device__ __forceinline__ uint32_t load_window(const uint8_t* row, int N, int base, int lane, int& off) {
+  off = int(reinterpret_cast<uintptr_t>(row) & 3u);
+  const uint8_t* astart = row - off;  // pointer arithmetic keeps the global address space
+  const int boff = base + 4 * lane;
+  return boff < off + N ? *reinterpret_cast<const uint32_t*>(astart + boff) : 0u;
+}
+
+// Bytes of a window dword that belong to the row: lane l holds atoms
+// 4 l + e - off (e = 0..3) of window `base`; keep those in [0, N).
+__device__ __forceinline__ uint32_t window_keep(int base, int off, int N, int lane) {
+  const int t0 = base + 4 * lane - off;  // atom of byte 0
+  const int lo = min(max(-t0, 0), 4), hi = min(max(t0 + 4 - N, 0), 4);
+  if (lo + hi >= 4) return 0u;
+  return (0xffffffffu << (8 * lo)) & (0xffffffffu >> (8 * hi));
+}
+
+// Valid (nonzero) bytes of one window added to `count`; the last valid atom
+// so far in `last` (t0 = atom of byte 0 of lane 0).
+__device__ __forceinline__ void scan_window(uint32_t w, int t0, int& count, int& last) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const unsigned long long bal = __ballot(((w >> (8 * e)) & 0xffu) != 0u);
+    count += __popcll(bal);
+    if (bal) last = max(last, t0 + 4 * (63 - __builtin_clzll(bal)) + e);
+  }
+}
+
+// dst[r] = the atom of valid rank r in a mask row (one wave).
+__device__ __forceinline__ void write_ranks(const uint8_t* row, int N, uint16_t* dst, int lane) {
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int run = 0;
+  for (int t0 = 0; t0 < N; t0 += 64) {
+    const int t = t0 + lane;
+    const bool ok = t < N && row[t] != 0;
+    const unsigned long long bal = __ballot(ok);
+    if (ok) dst[run + __popcll(bal & below)] = uint16_t(t);
+    run += __popcll(bal);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// pair loop of one wave over its share of a staged block
+// ---------------------------------------------------------------------------
+template <int DP>
+struct Shape {
+  static constexpr int NCH = DP / 32;  // 32-wide d chunks (GEMM1 K steps)
+  static constexpr int ND = DP / 16;   // 16-wide d tiles (GEMM2 M tiles)
+};
+
+// Pair-valid mask (0xffff per valid half) of keys k0 + 4g + {2 s, 2 s + 1}
+// of row j.
+__device__ __forceinline__ uint32_t pv_mask(uint32_t bits4, int s) {
+  return ((bits4 >> (2 * s)) & 1u ? 0x0000ffffu : 0u) | ((bits4 >> (2 * s + 1)) & 1u ? 0xffff0000u : 0u);
+}
+
+// The first QT of the MQ query tiles held in registers are in use.
+template <int DP, int QT, int MODE, bool HAS_PV, int MQ>
+__device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, int nkk,
+                                          const uint4 (&qop)[MQ][DP / 32], const float (&negm)[MQ], float sc,
+                                          mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
+                                          int g, int r16) {
+  using Ly = Lay<DP>;
+  constexpr int RB = Ly::RB;
+  constexpr int NCH = Shape<DP>::NCH;
+  constexpr int ND = Shape<DP>::ND;
+  const unsigned char* K1s = smem + Ly::kK1;
+  const unsigned char* K2s = smem + Ly::kK2;
+  const unsigned char* V1s = smem + Ly::kV1;
+  const unsigned char* V2s = smem + Ly::kV2;
+  const uint32_t* pvb = reinterpret_cast<const uint32_t*>(smem + Ly::kPV);
+  const int nkt = (nkk + 15) >> 4;
+  const int njp = (nkj + 1) >> 1;
+  const int total = nkt * njp;
+  int it = (wave * total) >> 2;
+  const int it1 = ((wave + 1) * total) >> 2;
+  const bool odd = (nkj & 1) != 0;
+  constexpr uint32_t kOne2 = 0x3c003c00u;  // fp16 (1, 1)
+  const mf_f32x4 zero4 = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  while (it < it1) {
+    const int kt = it / njp;
+    int jp = it - kt * njp;
+    const int jend = min(njp, jp + (it1 - it));
+    it += jend - jp;
+    const int k0 = kt * 16;
+    // per key tile: K2 rows as the GEMM1 A operand multiplicands, the V2
+    // halves of keys k0 + 4g + r as pairs (r = 0,1), (r = 2,3) per d tile,
+    // and the denominator operand (1 at the valid keys)
+    uint4 k2op[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      k2op[c] = *reinterpret_cast<const uint4*>(K2s + (k0 + r16) * RB + c * 64 + g * 16);
+    uint32_t v2p[ND][2];
+    {
+      uint32_t rv[4][(ND + 1) / 2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const unsigned char* src = V2s + (k0 + 4 * g + r) * RB + r16 * ND * 2;
+        if constexpr (ND == 4) {
+          const uint2 t = *reinterpret_cast<const uint2*>(src);
+          rv[r][0] = t.x;
+          rv[r][1] = t.y;
+        } else {
+          rv[r][0] = *reinterpret_cast<const uint32_t*>(src);
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
+        v2p[dt][0] = __builtin_amdgcn_perm(rv[1][dt >> 1], rv[0][dt >> 1], sel);
+        v2p[dt][1] = __builtin_amdgcn_perm(rv[3][dt >> 1], rv[2][dt >> 1], sel);
+      }
+    }
+    const int kvalid = nkk - (k0 + 4 * g);  // keys 4g + r valid for r < kvalid
+    const uint32_t o01 = kvalid >= 2 ? kOne2 : (kvalid == 1 ? 0x00003c00u : 0u);
+    const uint32_t o23 = kvalid >= 4 ? kOne2 : (kvalid == 3 ? 0x00003c00u : 0u);
+    const uint4 ones_kt{o01, o23, o01, o23};
+    const uint4 ones_half{o01, o23, 0u, 0u};
+    const uint32_t kmask = kvalid >= 4 ? 0xfu : (kvalid <= 0 ? 0u : ((1u << kvalid) - 1u));
+    int pvshift = 0, pvword = 0;
+    if constexpr (HAS_PV) {
+      pvword = k0 >> 5;
+      pvshift = (k0 & 31) + 4 * g;
+    }
+    for (; jp < jend; ++jp) {
+      const int j0 = 2 * jp;
+      const bool last_odd = odd && jp == njp - 1;
+      uint4 ka[NCH], kb[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        ka[c] = *reinterpret_cast<const uint4*>(K1s + j0 * RB + c * 64 + g * 16);
+        kb[c] = *reinterpret_cast<const uint4*>(K1s + (j0 + 1) * RB + c * 64 + g * 16);
+      }
+      uint32_t va[(ND + 1) / 2], vb[(ND + 1) / 2];
+      if constexpr (MODE != kMax) {
+        if constexpr (ND == 4) {
+          const uint2 ta = *reinterpret_cast<const uint2*>(V1s + j0 * RB + r16 * 8);
+          const uint2 tb = *reinterpret_cast<const uint2*>(V1s + (j0 + 1) * RB + r16 * 8);
+          va[0] = ta.x; va[1] = ta.y;
+          vb[0] = tb.x; vb[1] = tb.y;
+        } else {
+          va[0] = *reinterpret_cast<const uint32_t*>(V1s + j0 * RB + r16 * 4);
+          vb[0] = *reinterpret_cast<const uint32_t*>(V1s + (j0 + 1) * RB + r16 * 4);
+        }
+      }
+      // valid keys 4g + r of rows j0 (bits_a) and j0 + 1 (bits_b)
+      uint32_t bits_a = kmask, bits_b = last_odd ? 0u : kmask;
+      if constexpr (HAS_PV) {
+        bits_a &= pvb[j0 * (kCap / 32) + pvword] >> pvshift;
+        bits_b &= pvb[(j0 + 1) * (kCap / 32) + pvword] >> pvshift;
+      }
+      // GEMM1 for rows j0 and j0 + 1
+      uint4 wa[NCH], wb[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        wa[c] = pkmul4(ka[c], k2op[c]);
+        wb[c] = pkmul4(kb[c], k2op[c]);
+      }
+      mf_f32x4 sa[QT], sb[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        sa[qt] = mfma(wa[0], qop[qt][0], zero4);
+        sb[qt] = mfma(wb[0], qop[qt][0], zero4);
+#pragma unroll
+        for (int c = 1; c < NCH; ++c) {
+          sa[qt] = mfma(wa[c], qop[qt][c], sa[qt]);
+          sb[qt] = mfma(wb[c], qop[qt][c], sb[qt]);
+        }
+      }
+      if constexpr (MODE == kMax) {
+        // maxima of the valid logits (padded keys and rows have S = 0 and
+        // must not count)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const bool ka_ok = (bits_a >> r) & 1u;
+            const bool kb_ok = (bits_b >> r) & 1u;
+            mloc[qt] = fmaxf(mloc[qt], ka_ok ? sa[qt][r] : -INFINITY);
+            mloc[qt] = fmaxf(mloc[qt], kb_ok ? sb[qt][r] : -INFINITY);
+          }
+        }
+      } else {
+        // Z^T operands: d = 16 dt + r16, keys 4g + r of row j0 (halves
+        // 0..3) and of row j0 + 1 (halves 4..7)
+        uint4 z[ND];
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+          const uint32_t wa1 = va[dt >> 1], wb1 = vb[dt >> 1];
+          if (dt & 1) {
+            z[dt] = uint4{pkmul_splat<1>(v2p[dt][0], wa1), pkmul_splat<1>(v2p[dt][1], wa1),
+                          pkmul_splat<1>(v2p[dt][0], wb1), pkmul_splat<1>(v2p[dt][1], wb1)};
+          } else {
+            z[dt] = uint4{pkmul_splat<0>(v2p[dt][0], wa1), pkmul_splat<0>(v2p[dt][1], wa1),
+                          pkmul_splat<0>(v2p[dt][0], wb1), pkmul_splat<0>(v2p[dt][1], wb1)};
+          }
+        }
+        uint4 pop[QT];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          float ea[4], eb[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if constexpr (MODE == kFast) {
+              ea[r] = __builtin_amdgcn_exp2f(sa[qt][r]);
+              eb[r] = __builtin_amdgcn_exp2f(sb[qt][r]);
+            } else {
+              ea[r] = __builtin_amdgcn_exp2f(fmaf(sa[qt][r], sc, negm[qt]));
+              eb[r] = __builtin_amdgcn_exp2f(fmaf(sb[qt][r], sc, negm[qt]));
+            }
+          }
+          pop[qt] = uint4{pack_h2(ea[0], ea[1]), pack_h2(ea[2], ea[3]), pack_h2(eb[0], eb[1]), pack_h2(eb[2], eb[3])};
+          // two-pass mode: padded pairs have S = 0, so 2^(0 - m) may exceed
+          // the fp16 range; they and the pairs pair_valid clears get P = 0
+          if constexpr (HAS_PV || MODE == kSlow) {
+            pop[qt].x &= pv_mask(bits_a, 0);
+            pop[qt].y &= pv_mask(bits_a, 1);
+            pop[qt].z &= pv_mask(bits_b, 0);
+            pop[qt].w &= pv_mask(bits_b, 1);
+          }
+        }
+        const uint4 ones = last_odd ? ones_half : ones_kt;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt) O[dt][qt] = mfma(z[dt], pop[qt], O[dt][qt]);
+          L[qt] = mfma(ones, pop[qt], L[qt]);
+        }
+      }
+    }
+  }
+}
+
+// pair_loop for the runtime tile count nqt (1 .. MQ)
+template <int DP, int MODE, bool HAS_PV, int MQ>
+__device__ __forceinline__ void pair_loop_n(int nqt, const unsigned char* smem, int nkj, int nkk,
+                                            const uint4 (&qop)[MQ][DP / 32], const float (&negm)[MQ], float sc,
+                                            mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
+                                            int g, int r16) {
+  static_assert(MQ == 3, "three query tiles");
+  if (nqt == 1) pair_loop<DP, 1, MODE, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+  else if (nqt == 2) pair_loop<DP, 2, MODE, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+  else pair_loop<DP, 3, MODE, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+}
+
+// ---------------------------------------------------------------------------
+// one unit (molecule b, head h, queries q0 .. q0 + nqg - 1 of its valid ones)
+// ---------------------------------------------------------------------------
+// MULTI: the unit has more than kCap keys and is taken in (j block, k block)
+// pairs, with one query tile (its accumulators stay live across the block
+// loop, so the group is kept small).
+template <typename T, int DP, bool HAS_PV, bool MULTI>
+__device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, int b, int h, int nk, int q0, int nqg,
+                                          bool kpre, bool qpre) {
+  constexpr int QT = kMaxQ / 16;       // query tiles held in registers
+  const int nqt = (nqg + 15) >> 4;     // query tiles in use
+  using Ly = Lay<DP>;
+  constexpr int RB = Ly::RB;
+  constexpr int NCH = Shape<DP>::NCH;
+  constexpr int ND = Shape<DP>::ND;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+  const int H = p.H, N = p.N, D = p.D;
+  const int bh = b * H + h;
+  const uint16_t* kidx = reinterpret_cast<const uint16_t*>(smem + Ly::kKidx);
+  const uint16_t* qidx = reinterpret_cast<const uint16_t*>(smem + Ly::kQidx);
+  float* colmax = reinterpret_cast<float*>(smem + Ly::kCol);
+  float* mn = reinterpret_cast<float*>(smem + Ly::kMn);
+  float* gmax = reinterpret_cast<float*>(smem + Ly::kG);
+  int* scal = reinterpret_cast<int*>(smem + Ly::kScal);
+  float* s_m = reinterpret_cast<float*>(smem + Ly::kM);
+  const T* gq = static_cast<const T*>(p.q) + size_t(bh) * N * D;
+  const T* gk1 = static_cast<const T*>(p.k1) + size_t(bh) * N * D;
+  const T* gk2 = static_cast<const T*>(p.k2) + size_t(bh) * N * D;
+  const T* gv1 = static_cast<const T*>(p.v1) + size_t(bh) * N * D;
+  const T* gv2 = static_cast<const T*>(p.v2) + size_t(bh) * N * D;
+
+  // staging map: 16-byte chunk u = tid + kThreads i of a row set is row
+  // u / CPR, columns 8 cc .. 8 cc + 7 with cc = tid % CPR for every i; only
+  // the rows the pair loop reads (the valid ones rounded up to 16) are staged
+  constexpr int CPR = DP / 8;                        // chunks per row
+  constexpr int MAXC = kCap * CPR / kThreads;        // chunks per thread and block
+  constexpr int MAXQC = (kMaxQ * CPR + kThreads - 1) / kThreads;
+  const int cc = tid % CPR;
+  const int e0 = 8 * cc;
+  const bool col_ok = e0 < D;
+  const int nch = (nk + kCap - 1) / kCap;
+  auto key_atom = [&](int rank) { return kpre ? rank : int(kidx[rank]); };
+  auto round16 = [](int n) { return (n + 15) & ~15; };
+  // rows [row0, row0 + nrows) of the compacted keys; rows up to the next
+  // multiple of 16 read as zero
+  auto load_set = [&](const T* base, int row0, int nrows, uint4 (&arr)[MAXC]) {
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      const int row = (tid + kThreads * i) / CPR;
+      arr[i] = (row < nrows && col_ok)
+                   ? *reinterpret_cast<const uint4*>(base + size_t(key_atom(row0 + row)) * D + e0)
+                   : uint4{0u, 0u, 0u, 0u};
+    }
+  };
+  uint4 rk1[MAXC], rk2[MAXC], rv1[MAXC], rv2[MAXC], rq[MAXQC];
+  auto load_block = [&](int jc, int kc) {
+    const int j0 = jc * kCap, k0 = kc * kCap;
+    const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
+    load_set(gk1, j0, nkj, rk1);
+    load_set(gv1, j0, nkj, rv1);
+    load_set(gk2, k0, nkk, rk2);
+    load_set(gv2, k0, nkk, rv2);
+  };
+
+  // ---- phase A: maxima -> scale exponents -------------------------------
+  // magnitudes as 16-bit patterns (|x| of bf16 / fp16 orders like its bits
+  // with the sign cleared), two per dword, reduced with v_pk_max_u16
+  uint32_t c1[4], c2[4];  // column maxima of |K1|, |K2| for columns e0 .. e0 + 7
+  uint32_t gv = 0u, gqm = 0u;  // |V1| (low half) and |V2| (high half) maxima; |q| maxima
+#pragma unroll
+  for (int e = 0; e < 4; ++e) c1[e] = c2[e] = 0u;
+  auto acc_max = [&]() {
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      const uint32_t a1[4] = {rk1[i].x, rk1[i].y, rk1[i].z, rk1[i].w};
+      const uint32_t a2[4] = {rk2[i].x, rk2[i].y, rk2[i].z, rk2[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        c1[e] = pk_max_u16(c1[e], a1[e] & 0x7fff7fffu);
+        c2[e] = pk_max_u16(c2[e], a2[e] & 0x7fff7fffu);
+      }
+      const uint32_t m1 = pk_max_u16(pk_max_u16(rv1[i].x, rv1[i].y), pk_max_u16(rv1[i].z, rv1[i].w)) & 0x7fff7fffu;
+      const uint32_t m2 = pk_max_u16(pk_max_u16(rv2[i].x, rv2[i].y), pk_max_u16(rv2[i].z, rv2[i].w)) & 0x7fff7fffu;
+      // low half: |V1|, high half: |V2|
+      gv = pk_max_u16(gv, __builtin_amdgcn_perm(m2, m1, 0x07060302u));
+      gv = pk_max_u16(gv, __builtin_amdgcn_perm(m2, m1, 0x05040100u));
+    }
+  };
+  {
+    // query rows of the group (rows >= nqg read as zero)
+#pragma unroll
+    for (int i = 0; i < MAXQC; ++i) {
+      const int row = (tid + kThreads * i) / CPR;
+      rq[i] = (row < nqg && col_ok)
+                  ? *reinterpret_cast<const uint4*>(gq + size_t(qpre ? q0 + row : int(qidx[q0 + row])) * D + e0)
+                  : uint4{0u, 0u, 0u, 0u};
+    }
+  }
+  if constexpr (!MULTI) {
+    load_block(0, 0);
+    acc_max();
+  } else {
+    for (int rc = 0; rc < nch; ++rc) {
+      load_block(rc, rc);
+      acc_max();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MAXQC; ++i)
+    gqm = pk_max_u16(gqm, pk_max_u16(pk_max_u16(rq[i].x, rq[i].y), pk_max_u16(rq[i].z, rq[i].w)) & 0x7fff7fffu);
+  {
+    // column maxima over the lanes that share cc, then per wave to LDS
+#pragma unroll
+    for (int off = CPR; off < 64; off <<= 1) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        c1[e] = pk_max_u16(c1[e], uint32_t(__shfl_xor(int(c1[e]), off, 64)));
+        c2[e] = pk_max_u16(c2[e], uint32_t(__shfl_xor(int(c2[e]), off, 64)));
+      }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      gv = pk_max_u16(gv, uint32_t(__shfl_xor(int(gv), off, 64)));
+      gqm = pk_max_u16(gqm, uint32_t(__shfl_xor(int(gqm), off, 64)));
+    }
+    uint32_t* colw = reinterpret_cast<uint32_t*>(colmax);  // [kWaves][2][DP / 2] packed pairs
+    if (lane < CPR) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        colw[(wave * 2 + 0) * (DP / 2) + 4 * lane + e] = c1[e];
+        colw[(wave * 2 + 1) * (DP / 2) + 4 * lane + e] = c2[e];
+      }
+    }
+    if (lane == 0) {
+      uint32_t* gw = reinterpret_cast<uint32_t*>(gmax);
+      gw[wave * 4 + 0] = gv;
+      gw[wave * 4 + 1] = gqm;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const uint32_t* colw = reinterpret_cast<const uint32_t*>(colmax);
+    float m1 = 0.0f, m2 = 0.0f;
+    if (lane < DP) {
+      uint32_t w1 = 0u, w2 = 0u;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        w1 = max(w1, (colw[(w * 2 + 0) * (DP / 2) + lane / 2] >> (16 * (lane & 1))) & 0xffffu);
+        w2 = max(w2, (colw[(w * 2 + 1) * (DP / 2) + lane / 2] >> (16 * (lane & 1))) & 0xffffu);
+      }
+      m1 = mag_to_float<T>(w1);
+      m2 = mag_to_float<T>(w2);
+      mn[lane] = m1 * m2;
+    }
+    const float a1 = wave_max(m1), a2 = wave_max(m2);
+    if (lane == 0) {
+      const uint32_t* gw = reinterpret_cast<const uint32_t*>(gmax);
+      uint32_t v = 0u, qm = 0u;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        v = pk_max_u16(v, gw[w * 4 + 0]);
+        qm = pk_max_u16(qm, gw[w * 4 + 1]);
+      }
+      const float b1 = mag_to_float<T>(v & 0xffffu), b2 = mag_to_float<T>(v >> 16);
+      const float bq = fmaxf(mag_to_float<T>(qm & 0xffffu), mag_to_float<T>(qm >> 16));
+      const int s1 = norm_exp(a1), s2 = norm_exp(a2);
+      const int t1 = norm_exp(b1), t2 = norm_exp(b2);
+      const float cq = bq * kLog2e;
+      int sq = -(s1 + s2);
+      int E = 0;
+      if (!(ldexpf(cq, sq) < kQLimit)) {
+        sq = norm_exp(cq);
+        E = s1 + s2 + sq;
+      }
+      scal[0] = s1;
+      scal[1] = s2;
+      scal[2] = t1;
+      scal[3] = t2;
+      scal[4] = sq;
+      scal[5] = E;
+      scal[6] = E != 0 ? 1 : 0;  // two-pass flag (queries add theirs)
+    }
+  }
+  __syncthreads();
+  const int s1 = scal[0], s2 = scal[1], t1 = scal[2], t2 = scal[3], sq = scal[4], E = scal[5];
+
+  // ---- phase B: query rows, bounds ---------------------------------------
+  {
+    unsigned char* Qs = smem + Ly::kQ;
+    const float4 mlo = *reinterpret_cast<const float4*>(mn + e0);
+    const float4 mhi = *reinterpret_cast<const float4*>(mn + e0 + 4);
+    const float mm[8] = {mlo.x, mlo.y, mlo.z, mlo.w, mhi.x, mhi.y, mhi.z, mhi.w};
+#pragma unroll
+    for (int i = 0; i < MAXQC; ++i) {
+      const int row = (tid + kThreads * i) / CPR;
+      float f[8];
+      unpack8<T>(rq[i], f);
+      float ub = 0.0f;
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float qq = f[e] * kLog2e;
+        ub = fmaf(fabsf(qq), mm[e], ub);
+        f[e] = ldexpf(qq, sq);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = pack_h2(f[2 * e], f[2 * e + 1]);
+      if (row < 16 * QT) *reinterpret_cast<uint4*>(Qs + row * RB + e0 * 2) = uint4{w[0], w[1], w[2], w[3]};
+      // |S| bound of the row: the CPR lanes of a row are consecutive
+#pragma unroll
+      for (int off = 1; off < CPR; off <<= 1) ub += __shfl_xor(ub, off, 64);
+      if (row < nqg && cc == 0 && !(ub <= kBoundLimit)) atomicOr(&scal[6], 1);
+    }
+  }
+
+  // ---- staging of one (j block, k block) ----------------------------------
+  auto store_block = [&](int jc, int kc) {
+    unsigned char* K1s = smem + Ly::kK1;
+    unsigned char* K2s = smem + Ly::kK2;
+    unsigned char* V1s = smem + Ly::kV1;
+    unsigned char* V2s = smem + Ly::kV2;
+    const int nkj = min(kCap, nk - jc * kCap), nkk = min(kCap, nk - kc * kCap);
+    const int rj = round16(nkj), rk = round16(nkk);
+    // K rows: row-major fp16
+    auto store_k = [&](unsigned char* dst, const uint4& v, int row, int sc_exp) {
+      float f[8];
+      uint32_t w[4];
+      unpack8<T>(v, f);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = pack_h2(ldexpf(f[2 * e], sc_exp), ldexpf(f[2 * e + 1], sc_exp));
+      *reinterpret_cast<uint4*>(dst + row * RB + e0 * 2) = uint4{w[0], w[1], w[2], w[3]};
+    };
+    // V rows: [row][r16][dt]: column d = 16 dt + r16 at half r16 ND + dt
+    auto store_v = [&](unsigned char* dst, const uint4& v, int row, int sc_exp) {
+      float f[8];
+      unpack8<T>(v, f);
+      unsigned char* a = dst + row * RB + ((8 * (cc & 1)) * ND + (cc >> 1)) * 2;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<_Float16*>(a + e * ND * 2) = _Float16(ldexpf(f[e], sc_exp));
+    };
+    if constexpr (!MULTI) {
+      // the rows loaded in phase A
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i) {
+        const int row = (tid + kThreads * i) / CPR;
+        if (row < rj) {
+          store_k(K1s, rk1[i], row, s1);
+          store_v(V1s, rv1[i], row, t1);
+        }
+        if (row < rk) {
+          store_k(K2s, rk2[i], row, s2);
+          store_v(V2s, rv2[i], row, t2);
+        }
+      }
+    } else {
+      // larger molecules: one tensor at a time, so that few registers are
+      // live next to the accumulators
+      const int j0 = jc * kCap, k0 = kc * kCap;
+      uint4 t[MAXC];
+      load_set(gk1, j0, nkj, t);
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i)
+        if ((tid + kThreads * i) / CPR < rj) store_k(K1s, t[i], (tid + kThreads * i) / CPR, s1);
+      load_set(gv1, j0, nkj, t);
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i)
+        if ((tid + kThreads * i) / CPR < rj) store_v(V1s, t[i], (tid + kThreads * i) / CPR, t1);
+      load_set(gk2, k0, nkk, t);
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i)
+        if ((tid + kThreads * i) / CPR < rk) store_k(K2s, t[i], (tid + kThreads * i) / CPR, s2);
+      load_set(gv2, k0, nkk, t);
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i)
+        if ((tid + kThreads * i) / CPR < rk) store_v(V2s, t[i], (tid + kThreads * i) / CPR, t2);
+    }
+    if constexpr (HAS_PV) {
+      // bits of pair_valid for rows j of the j block and keys k of the k block
+      uint32_t* pvb = reinterpret_cast<uint32_t*>(smem + Ly::kPV);
+      const uint8_t* gpv = p.pv + size_t(b) * N * N;
+      const int j0 = jc * kCap, k0 = kc * kCap;
+      for (int u = tid; u < kCap * (kCap / 32); u += kThreads) {
+        const int jl = u / (kCap / 32), wd = u % (kCap / 32);
+        uint32_t bits = 0;
+        if (jl < nkj) {
+          const uint8_t* prow = gpv + size_t(key_atom(j0 + jl)) * N;
+          for (int t = 0; t < 32; ++t) {
+            const int kl = wd * 32 + t;
+            if (kl < nkk && prow[key_atom(k0 + kl)] != 0) bits |= 1u << t;
+          }
+        }
+        pvb[u] = bits;
+      }
+    }
+  };
+
+  // ---- phase C: pair loop -------------------------------------------------
+  uint4 qop[QT][NCH];
+  mf_f32x4 O[ND][QT], L[QT];
+  float mloc[QT], negm[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    L[qt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+    mloc[qt] = -INFINITY;
+    negm[qt] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) O[dt][qt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float sc = ldexpf(1.0f, -E);
+  auto load_qop = [&]() {
+    const unsigned char* Qs = smem + Ly::kQ;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int cc = 0; cc < NCH; ++cc)
+        if (qt < nqt)
+        qop[qt][cc] = *reinterpret_cast<const uint4*>(Qs + (16 * qt + r16) * RB + cc * 64 + g * 16);
+  };
+  // per-query maxima of the two-pass mode: reduce the waves' partial maxima
+  auto finish_max = [&]() {
+    float* redm = colmax;  // [kWaves][kMaxQ]
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float m = mloc[qt];
+      m = fmaxf(m, __shfl_xor(m, 16, 64));
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      if (g == 0) redm[wave * kMaxQ + 16 * qt + r16] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) m = fmaxf(m, redm[w * kMaxQ + 16 * qt + r16]);
+      m = m == -INFINITY ? 0.0f : m * sc;  // log2 units
+      negm[qt] = -m;
+      if (wave == 0 && g == 0) s_m[16 * qt + r16] = m;
+    }
+  };
+  bool slow = false;
+  if (!MULTI && nch == 1) {
+    store_block(0, 0);
+    __syncthreads();
+    slow = scal[6] != 0;
+    load_qop();
+    if (!slow) {
+      pair_loop_n<DP, kFast, HAS_PV>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+    } else {
+      pair_loop_n<DP, kMax, HAS_PV>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+      finish_max();
+      pair_loop_n<DP, kSlow, HAS_PV>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+    }
+  } else if (MULTI && nch > 1) {
+    __syncthreads();
+    slow = scal[6] != 0;
+    load_qop();
+    for (int pass = slow ? 0 : 1; pass < 2; ++pass) {
+      for (int jc = 0; jc < nch; ++jc) {
+        for (int kc = 0; kc < nch; ++kc) {
+          store_block(jc, kc);
+          __syncthreads();
+          const int nkj = min(kCap, nk - jc * kCap), nkk = min(kCap, nk - kc * kCap);
+          if (pass == 0)
+            pair_loop<DP, 1, kMax, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+          else if (slow)
+            pair_loop<DP, 1, kSlow, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+          else
+            pair_loop<DP, 1, kFast, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+          __syncthreads();
+        }
+      }
+      if (pass == 0) finish_max();
+    }
+  }
+
+  // ---- phase D: reduce the waves' partials, normalise, write ---------------
+  __syncthreads();  // every wave is done with K/V (the reduction area aliases them)
+  float* red = reinterpret_cast<float*>(smem + Ly::kRed);
+  float* redl = reinterpret_cast<float*>(smem + Ly::kRedL);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    if (qt >= nqt) continue;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+      *reinterpret_cast<mf_f32x4*>(red + (wave * kMaxQ + 16 * qt + r16) * Ly::RS + 16 * dt + 4 * g) = O[dt][qt];
+    if (g == 0) redl[wave * kMaxQ + 16 * qt + r16] = L[qt][0];
+  }
+  __syncthreads();
+  constexpr int CPQ = DP / 8;  // 8-column chunks per query
+  const float oscale = ldexpf(1.0f, -(t1 + t2));
+  for (int idx = tid; idx < nqg * CPQ; idx += kThreads) {
+    const int i = idx / CPQ;
+    const int c8 = (idx - i * CPQ) * 8;
+    if (c8 >= D) continue;
+    float l = 0.0f;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      l += redl[w * kMaxQ + i];
+      const float4 lo = *reinterpret_cast<const float4*>(red + (w * kMaxQ + i) * Ly::RS + c8);
+      const float4 hi = *reinterpret_cast<const float4*>(red + (w * kMaxQ + i) * Ly::RS + c8 + 4);
+      o[0] += lo.x; o[1] += lo.y; o[2] += lo.z; o[3] += lo.w;
+      o[4] += hi.x; o[5] += hi.y; o[6] += hi.z; o[7] += hi.w;
+    }
+    const bool mass = l > 0.0f;
+    const float inv = mass ? oscale / l : 0.0f;
+    const int atom = qpre ? q0 + i : int(qidx[q0 + i]);
+    const size_t row = size_t(bh) * N + atom;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= inv;
+    if (p.out) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const T lo = T(o[2 * e]), hi = T(o[2 * e + 1]);
+        w[e] = uint32_t(__builtin_bit_cast(uint16_t, lo)) | (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
+      }
+      *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row * D + c8) = uint4{w[0], w[1], w[2], w[3]};
+    }
+    if (p.out_f32) {
+      float4* dst = reinterpret_cast<float4*>(p.out_f32 + row * D + c8);
+      dst[0] = float4{o[0], o[1], o[2], o[3]};
+      dst[1] = float4{o[4], o[5], o[6], o[7]};
+    }
+    if (c8 == 0 && p.lse) p.lse[row] = mass ? ((slow ? s_m[i] : 0.0f) + __log2f(l)) * kLn2 : 0.0f;
+  }
+  __syncthreads();  // the next unit rewrites the index lists and LDS
+}
+
+// ---------------------------------------------------------------------------
+// plan kernel: workgroup 0 writes the schedule, the others zero the rows of
+// padded queries
+// ---------------------------------------------------------------------------
+constexpr int kPlanThreads = 1024;
+
+template <typename T>
+__global__ void __launch_bounds__(kPlanThreads) simplicial_pair_plan(Params p) {
+  constexpr int kPW = kPlanThreads / 64;  // waves
+  __shared__ uint32_t s_info[kMaxBatch];
+  __shared__ uint32_t s_cost[kMaxBatch];
+  __shared__ int s_order[kMaxBatch];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int B = p.B, H = p.H, N = p.N, D = p.D;
+  const Schedule sc = carve_schedule(p.ws, B, N);
+
+  if (blockIdx.x > 0) {
+    // zero the rows of padded queries, (b, h) pairs strided over the workgroups
+    const int cpr = D / 8;  // 16-byte chunks of a 16-bit output row
+    for (int bh = blockIdx.x - 1; bh < B * H; bh += gridDim.x - 1) {
+      const int b = bh / H;
+      const uint8_t* qrow = p.qv + size_t(b) * N;
+      // validity bytes of this thread's rows first (one round of loads)
+      constexpr int kMaxIt = (kMaxN * 8 + kPlanThreads - 1) / kPlanThreads;
+      uint8_t valid[kMaxIt];
+#pragma unroll
+      for (int it = 0; it < kMaxIt; ++it) {
+        const int u = tid + it * kPlanThreads;
+        valid[it] = u < N * cpr ? qrow[u / cpr] : 1;
+      }
+#pragma unroll
+      for (int it = 0; it < kMaxIt; ++it) {
+        const int u = tid + it * kPlanThreads;
+        const int i = u / cpr, cc = u - i * cpr;
+        if (valid[it]) continue;
+        const size_t row = size_t(bh) * N + i;
+        if (p.out) reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row * D)[cc] = uint4{0u, 0u, 0u, 0u};
+        if (p.out_f32) {
+          float4* o = reinterpret_cast<float4*>(p.out_f32 + row * D + cc * 8);
+          o[0] = float4{0.f, 0.f, 0.f, 0.f};
+          o[1] = float4{0.f, 0.f, 0.f, 0.f};
+        }
+        if (cc == 0 && p.lse) p.lse[row] = 0.0f;
+      }
+    }
+    return;
+  }
+
+  // 1. valid keys / queries of every molecule (one wave per molecule; rows
+  //    of up to 252 bytes are one window, the windows of up to 8 molecules
+  //    per wave are loaded before any is scanned)
+  auto put_info = [&](int b, int ck, int lk, int cq, int lq) {
+    if (lane == 0)
+      s_info[b] = uint32_t(ck) | (uint32_t(cq) << 11) | (lk + 1 == ck ? kKPre : 0u) | (lq + 1 == cq ? kQPre : 0u);
+  };
+  if (N <= 252) {
+    constexpr int kRound = 8;
+    for (int b0 = wave; b0 < B; b0 += kPW * kRound) {
+      uint32_t wk[kRound], wq[kRound];
+      int off[kRound];
+#pragma unroll
+      for (int rr = 0; rr < kRound; ++rr) {
+        const int b = min(b0 + rr * kPW, B - 1);
+        int o2;
+        wk[rr] = load_window(p.pkv + size_t(b) * N, N, 0, lane, off[rr]);
+        wq[rr] = load_window(p.qv + size_t(b) * N, N, 0, lane, o2);
+      }
+#pragma unroll
+      for (int rr = 0; rr < kRound; ++rr) {
+        if (b0 + rr * kPW < B) {
+          const uint32_t keep = window_keep(0, off[rr], N, lane);
+          int ck = 0, cq = 0, lk = -1, lq = -1;
+          scan_window(wk[rr] & keep, -off[rr], ck, lk);
+          scan_window(wq[rr] & keep, -off[rr], cq, lq);
+          put_info(b0 + rr * kPW, ck, lk, cq, lq);
+        }
+      }
+    }
+  } else {
+    for (int b = wave; b < B; b += kPW) {
+      int ck = 0, cq = 0, lk = -1, lq = -1;
+      for (int base = 0; base < N + 3; base += 256) {
+        int off, o2;
+        const uint32_t wk = load_window(p.pkv + size_t(b) * N, N, base, lane, off);
+        const uint32_t wq = load_window(p.qv + size_t(b) * N, N, base, lane, o2);
+        const uint32_t keep = window_keep(base, off, N, lane);
+        scan_window(wk & keep, base - off, ck, lk);
+        scan_window(wq & keep, base - off, cq, lq);
+      }
+      put_info(b, ck, lk, cq, lq);
+    }
+  }
+  __syncthreads();
+
+  // 2. index lists of the molecules that need them (one wave per list)
+  for (int t = wave; t < 2 * B; t += kPW) {
+    const int b = t >> 1;
+    const uint32_t w = s_info[b];
+    if ((t & 1) == 0 && !(w & kKPre)) write_ranks(p.pkv + size_t(b) * N, N, sc.kidx + size_t(b) * N, lane);
+    if ((t & 1) == 1 && !(w & kQPre)) write_ranks(p.qv + size_t(b) * N, N, sc.qidx + size_t(b) * N, lane);
+  }
+
+  // 3. molecules ranked by cost (nk^2 x query tiles, longest first, ties by
+  //    index) and the unit prefix over ranks
+  for (int b = tid; b < B; b += kPlanThreads) {
+    const uint32_t w = s_info[b];
+    const int nk = info_nk(w), nq = info_nq(w);
+    s_cost[b] = uint32_t(nk * nk) * uint32_t((nq + 15) / 16);
+    sc.info[b] = w;
+  }
+  __syncthreads();
+  for (int u0 = 0; u0 < 4 * B; u0 += kPlanThreads) {
+    const int u = u0 + tid;
+    const int b = min(u >> 2, B - 1), part = u & 3;
+    const uint32_t cb = s_cost[b];
+    int rank = 0;
+#pragma unroll 4
+    for (int o = part; o < B; o += 4) {
+      const uint32_t co = s_cost[o];
+      rank += (co > cb || (co == cb && o < b)) ? 1 : 0;
+    }
+    rank += __shfl_xor(rank, 1, 64);
+    rank += __shfl_xor(rank, 2, 64);
+    if (part == 0 && u < 4 * B) {
+      s_order[rank] = b;
+      sc.order[rank] = b;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // exclusive prefix of H x groups over ranks, 4 ranks per lane (B <= 256)
+    int v[4], sum = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rk = 4 * lane + e;
+      v[e] = rk < B ? H * num_groups(info_nk(s_info[s_order[rk]]), info_nq(s_info[s_order[rk]])) : 0;
+      sum += v[e];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rk = 4 * lane + e;
+      if (rk < B) sc.pre[rk] = run;
+      run += v[e];
+    }
+    if (lane == 63) {
+      sc.pre[B] = incl;
+      *sc.total = incl;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// main kernel: the units of the schedule
+// ---------------------------------------------------------------------------
+template <typename T, int DP, bool HAS_PV>
+__global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) {
+  using Ly = Lay<DP>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + Ly::kInfo);
+  int* s_pre = reinterpret_cast<int*>(smem + Ly::kPre);
+  uint16_t* s_order = reinterpret_cast<uint16_t*>(smem + Ly::kOrder);
+  uint16_t* kidx = reinterpret_cast<uint16_t*>(smem + Ly::kKidx);
+  uint16_t* qidx = reinterpret_cast<uint16_t*>(smem + Ly::kQidx);
+  const int tid = threadIdx.x;
+  const int B = p.B, N = p.N;
+  const int G = gridDim.x;
+  // XCD-aware logical id: blockIdx.x % 8 is the XCD (G is a multiple of 8)
+  const int wg = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  const Schedule sc = carve_schedule(p.ws, B, N);
+  for (int b = tid; b <= B; b += kThreads) {
+    if (b < B) {
+      s_info[b] = sc.info[b];
+      s_order[b] = uint16_t(sc.order[b]);
+    }
+    s_pre[b] = sc.pre[b];
+  }
+  __syncthreads();
+  const int total = s_pre[B];
+
+  // units: round rr takes position rr G + w (even) or rr G + G - 1 - w (odd)
+  for (int rr = 0;; ++rr) {
+    const int pos = rr * G + ((rr & 1) ? G - 1 - wg : wg);
+    if (pos >= total) break;
+    // rank of the molecule: the last rank whose prefix is <= pos
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_pre[mid] <= pos) lo = mid;
+      else hi = mid - 1;
+    }
+    const int b = s_order[lo];
+    const uint32_t info = s_info[b];
+    const int nk = info_nk(info), nq = info_nq(info);
+    const int ng = num_groups(nk, nq);
+    const int gs = group_size(nk, nq);
+    const int u = pos - s_pre[lo];
+    const int h = u / ng, gi = u - h * ng;
+    const int q0 = gs * gi;
+    const int nqg = min(gs, nq - q0);
+    const bool kpre = (info & kKPre) != 0, qpre = (info & kQPre) != 0;
+    if (!kpre)
+      for (int t = tid; t < nk; t += kThreads) kidx[t] = sc.kidx[size_t(b) * N + t];
+    if (!qpre)
+      for (int t = tid; t < nq; t += kThreads) qidx[t] = sc.qidx[size_t(b) * N + t];
+    __syncthreads();
+    if (nk > kCap) unit_body<T, DP, HAS_PV, true>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
+    else unit_body<T, DP, HAS_PV, false>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
+  }
+}
+
+template <typename T, int DP, bool HAS_PV>
+int launch(const Params& prm, int num_cus, hipStream_t stream) {
+  // plan: workgroup 0 plus workgroups that zero the padded query rows
+  hipLaunchKernelGGL(simplicial_pair_plan<T>, dim3(std::max(2, num_cus)), dim3(kPlanThreads), 0, stream, prm);
+  MF_HIP_CHECK(hipGetLastError());
+  const int grid = std::max(8, (2 * num_cus) & ~7);  // a multiple of 8 (the XCD count)
+  auto kern = simplicial_pair_kernel<T, DP, HAS_PV>;
+  const size_t lds = Lay<DP>::kTotal;
+  static bool attr_set = false;  // per instantiation
+  if (!attr_set) {
+    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, prm);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
+
+}  // namespace spair
+
+bool simplicial_pair_serves(int tokens, int head_dim, int dtype) {
+  return dtype != MF_DTYPE_F32 && head_dim % 8 == 0 && head_dim <= 64 && tokens <= spair::kMaxN;
+}
+
+int simplicial_pair_max_batch(int tokens) {
+  (void)tokens;
+  return spair::kMaxBatch;
+}
+
+size_t simplicial_pair_workspace_bytes(int batch, int tokens) {
+  return spair::schedule_bytes(std::min(batch, spair::kMaxBatch), tokens);
+}
+
+// One plan + main launch over a[0..batch), batch <= simplicial_pair_max_batch(tokens).
+int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* workspace, int num_cus, hipStream_t stream) {
+  using namespace spair;
+  if (a->batch > simplicial_pair_max_batch(a->tokens))
+    return fail(MF_ERR_INVALID_ARGUMENT, "simplicial pair launch: batch slice too large");
+  if (!simplicial_pair_serves(a->tokens, a->head_dim, a->dtype))
+    return fail(MF_ERR_UNSUPPORTED, "simplicial pair launch: unsupported shape");
+  Params prm{};
+  prm.q = a->q; prm.k1 = a->k1; prm.v1 = a->v1; prm.k2 = a->k2; prm.v2 = a->v2;
+  prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
+  prm.out = a->out; prm.out_f32 = a->out_f32; prm.lse = a->lse;
+  prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
+  prm.ws = static_cast<int*>(workspace);
+  const int g = num_cus;
+  const bool pv = a->pair_valid != nullptr;
+  const bool bf = a->dtype == MF_DTYPE_BF16;
+  if (a->head_dim <= 32) {
+    if (bf) return pv ? launch<__bf16, 32, true>(prm, g, stream) : launch<__bf16, 32, false>(prm, g, stream);
+    return pv ? launch<_Float16, 32, true>(prm, g, stream) : launch<_Float16, 32, false>(prm, g, stream);
+  }
+  if (bf) return pv ? launch<__bf16, 64, true>(prm, g, stream) : launch<__bf16, 64, false>(prm, g, stream);
+  return pv ? launch<_Float16, 64, true>(prm, g, stream) : launch<_Float16, 64, false>(prm, g, stream);
+}
+
+}  // namespace mf
