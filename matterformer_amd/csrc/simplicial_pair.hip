@@ -966,7 +966,6 @@ template <typename T>
 __global__ void __launch_bounds__(kPlanThreads) simplicial_pair_plan(Params p) {
   constexpr int kPW = kPlanThreads / 64;  // waves
   __shared__ uint32_t s_info[kMaxBatch];
-  __shared__ uint32_t s_cost[kMaxBatch];
   __shared__ int s_order[kMaxBatch];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1009,9 +1008,14 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_pair_plan(Params p) {
   // 1. valid keys / queries of every molecule (one wave per molecule; rows
   //    of up to 252 bytes are one window, the windows of up to 8 molecules
   //    per wave are loaded before any is scanned)
+  __shared__ int s_lists;  // some molecule's valid atoms are not a prefix
+  if (tid == 0) s_lists = 0;
+  __syncthreads();
   auto put_info = [&](int b, int ck, int lk, int cq, int lq) {
-    if (lane == 0)
+    if (lane == 0) {
       s_info[b] = uint32_t(ck) | (uint32_t(cq) << 11) | (lk + 1 == ck ? kKPre : 0u) | (lq + 1 == cq ? kQPre : 0u);
+      if (lk + 1 != ck || lq + 1 != cq) s_lists = 1;
+    }
   };
   if (N <= 252) {
     constexpr int kRound = 8;
@@ -1053,30 +1057,31 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_pair_plan(Params p) {
   __syncthreads();
 
   // 2. index lists of the molecules that need them (one wave per list)
-  for (int t = wave; t < 2 * B; t += kPW) {
-    const int b = t >> 1;
-    const uint32_t w = s_info[b];
-    if ((t & 1) == 0 && !(w & kKPre)) write_ranks(p.pkv + size_t(b) * N, N, sc.kidx + size_t(b) * N, lane);
-    if ((t & 1) == 1 && !(w & kQPre)) write_ranks(p.qv + size_t(b) * N, N, sc.qidx + size_t(b) * N, lane);
+  if (s_lists) {
+    for (int t = wave; t < 2 * B; t += kPW) {
+      const int b = t >> 1;
+      const uint32_t w = s_info[b];
+      if ((t & 1) == 0 && !(w & kKPre)) write_ranks(p.pkv + size_t(b) * N, N, sc.kidx + size_t(b) * N, lane);
+      if ((t & 1) == 1 && !(w & kQPre)) write_ranks(p.qv + size_t(b) * N, N, sc.qidx + size_t(b) * N, lane);
+    }
   }
 
   // 3. molecules ranked by cost (nk^2 x query tiles, longest first, ties by
   //    index) and the unit prefix over ranks
-  for (int b = tid; b < B; b += kPlanThreads) {
+  auto cost_of = [&](int b) {
     const uint32_t w = s_info[b];
     const int nk = info_nk(w), nq = info_nq(w);
-    s_cost[b] = uint32_t(nk * nk) * uint32_t((nq + 15) / 16);
-    sc.info[b] = w;
-  }
-  __syncthreads();
+    return uint32_t(nk * nk) * uint32_t((nq + 15) / 16);
+  };
+  for (int b = tid; b < B; b += kPlanThreads) sc.info[b] = s_info[b];
   for (int u0 = 0; u0 < 4 * B; u0 += kPlanThreads) {
     const int u = u0 + tid;
     const int b = min(u >> 2, B - 1), part = u & 3;
-    const uint32_t cb = s_cost[b];
+    const uint32_t cb = cost_of(b);
     int rank = 0;
 #pragma unroll 4
     for (int o = part; o < B; o += 4) {
-      const uint32_t co = s_cost[o];
+      const uint32_t co = cost_of(o);
       rank += (co > cb || (co == cb && o < b)) ? 1 : 0;
     }
     rank += __shfl_xor(rank, 1, 64);
