@@ -13,9 +13,9 @@ value = valid FLOPs (sum_b 4 H D n_b^3) / step time, in TFLOP/s.
 Prints ONE JSON line.  Also reports:
   roofline      the entry point's achieved TFLOP/s against the bf16 dense MFMA
                 peak: valid FLOPs over the average duration of one
-                mf_simplicial_fwd launch sequence (plan kernel + main kernel +
-                the pass for molecules above one key chunk), timed with HIP
-                events on the launch stream; `traffic` is the HBM bytes of one
+                mf_simplicial_fwd launch sequence (the plan kernel and the
+                pair kernel), timed with HIP events on the launch stream;
+                `traffic` is the HBM bytes of one
                 such sequence from the committed rocprofv3 --pmc summary
                 (profiles/simplicial_fwd_geom_traffic.json) when present;
   cpu_baseline  the oracle's torch-CPU restatement of the reference path
@@ -354,8 +354,8 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / BF16_DENSE_PEAK_TFLOPS, 5),
             "traffic": committed_traffic("simplicial_fwd_geom"),
-            "kernel": ("mf_simplicial_fwd launch sequence: simplicial_plan_kernel + "
-                       "simplicial_fast_kernel<bf16,64,5,small> + simplicial_fast_kernel<bf16,64,5,large>"),
+            "kernel": ("mf_simplicial_fwd launch sequence: simplicial_pair_plan<bf16> + "
+                       "simplicial_pair_kernel<bf16, 64, pair_valid=0>"),
             "kernel_ms": round(kernel_ms, 5),
             "kernel_mean_ms": round(kernel_mean_ms, 5),
         },
