@@ -1,12 +1,15 @@
-"""GPU parity of the register-resident fast path of mf_simplicial_fwd (16-bit operands, head_dim <= 64).
+"""GPU parity of the 16-bit pair kernel behind mf_simplicial_fwd (bf16/fp16, head_dim <= 64).
 
-The fast kernel picks, per query, between P = 2^S directly (when an a-priori
-bound on |S| is small) and a two-pass exact-maximum mode; inputs are scaled
-here so that each mode is exercised: std 0.05 keeps every logit bound small,
-std 1.3 pushes the bound past the limit.  Molecules with more than 80 keys
-(96 for head_dim <= 32) are served by the general kernel in a second launch,
-which the mixed-size cases cover.  Tolerance: normwise relative error <= 2e-2
-against the float64 oracle on the same 16-bit-rounded inputs.
+The kernel stages each (molecule, head) as fp16 scaled by powers of two and
+picks, per unit, between P = 2^S directly (when the a-priori bound on |S| is
+at most 13.5 and the query scale needs no rescaling) and a two-pass
+exact-maximum mode; inputs are scaled here so that each mode is exercised:
+std 0.05 keeps every logit bound small, std 1.3 pushes the bound past the
+limit, and the extreme-scale case forces the rescaled two-pass mode.
+Molecules with more than 128 keys are taken in key blocks (the mixed-size
+cases), molecules with more than 48 queries in several query groups.
+Tolerance: normwise relative error <= 2e-2 against the float64 oracle on the
+same 16-bit-rounded inputs.
 """
 
 import numpy as np
@@ -66,7 +69,7 @@ def test_fast_path_matches_oracle(cuda, shape, dtype, std):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 def test_mixed_sizes_fast_and_general(cuda, dtype):
-    # molecules on both sides of the fast kernel's 80-key capacity in one call
+    # molecules on both sides of the 128-key block in one call
     B, H, N, D = 4, 2, 150, 64
     case = random_simplicial(B, H, N, D, seed=5, counts=[150, 80, 81, 12], holes=[(0, 7)], std=0.08)
     out, lse, out32, ref, ref_lse = run(case, cuda, dtype)
@@ -76,7 +79,7 @@ def test_mixed_sizes_fast_and_general(cuda, dtype):
 
 
 def test_large_batch_is_chunked(cuda):
-    # more molecules than one fast launch's item table holds (1024)
+    # more molecules than one launch takes (256 per launch)
     B, H, N, D = 1100, 1, 8, 8
     gen = torch.Generator().manual_seed(3)
     counts = torch.randint(1, N + 1, (B,), generator=gen).tolist()
@@ -99,3 +102,21 @@ def test_scaled_inputs_give_same_softmax(cuda):
         out, lse, out32, ref, ref_lse = run(tuple(c), cuda, torch.bfloat16)
         assert rel(out32.cpu().numpy(), ref) <= 2e-2, scale
         np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_extreme_scale_rescaled_two_pass(cuda, dtype):
+    # Large components in different head dimensions of q (d = 0), k1 (d = 1)
+    # and k2 (d = 2): max|q log2 e| max|k1| max|k2| is far beyond what the
+    # fp16 query operand can carry at the scale that keeps S in log2 units,
+    # so the unit rescales S in the two-pass mode, while every product
+    # q_d k1_d k2_d, and so every logit, stays moderate
+    B, H, N, D = 2, 2, 33, 64
+    case = list(random_simplicial(B, H, N, D, seed=11, counts=[33, 20], std=0.1))
+    case[0][..., 0] += 100.0
+    case[1][..., 1] += 50.0
+    case[3][..., 2] += 50.0
+    out, lse, out32, ref, ref_lse = run(tuple(case), cuda, dtype)
+    assert torch.isfinite(out32).all()
+    assert rel(out32.cpu().numpy(), ref) <= 2e-2
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
