@@ -93,6 +93,7 @@ struct Params {
 
 // The schedule the plan kernel writes for the main kernel (int words):
 //   total               units of the launch
+//   claimed             units claimed so far after the first round
 //   info[B]             molecule info word (see info_*)
 //   order[B]            molecule of each cost rank, longest first
 //   pre[B + 1]          first unit position of each rank (pre[B] = total)
@@ -100,6 +101,7 @@ struct Params {
 //                       valid atoms are not a prefix (others are not written)
 struct Schedule {
   int* total;
+  int* claimed;  // units claimed after the first round (the plan sets it to 0)
   uint32_t* info;
   int* order;
   int* pre;
@@ -109,6 +111,7 @@ struct Schedule {
 __host__ __device__ inline Schedule carve_schedule(int* ws, int B, int N) {
   Schedule sc;
   sc.total = ws;
+  sc.claimed = ws + 1;
   sc.info = reinterpret_cast<uint32_t*>(ws + 4);
   sc.order = ws + 4 + B;
   sc.pre = ws + 4 + 2 * B;
@@ -1117,6 +1120,7 @@ __global__ void __launch_bounds__(kPlanThreads) simplicial_pair_plan(Params p) {
     if (lane == 63) {
       sc.pre[B] = incl;
       *sc.total = incl;
+      *sc.claimed = 0;
     }
   }
 }
@@ -1149,10 +1153,12 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
   __syncthreads();
   const int total = s_pre[B];
 
-  // units: round rr takes position rr G + w (even) or rr G + G - 1 - w (odd)
-  for (int rr = 0;; ++rr) {
-    const int pos = rr * G + ((rr & 1) ? G - 1 - wg : wg);
-    if (pos >= total) break;
+  // units: the first round gives position w to workgroup w (positions are
+  // ordered longest first); after that a workgroup that finishes a unit
+  // claims the next position with one device-scope atomic, so the workgroups
+  // that finish first take the longest remaining units
+  __shared__ int s_next;
+  for (int pos = wg; pos < total;) {
     // rank of the molecule: the last rank whose prefix is <= pos
     int lo = 0, hi = B - 1;
     while (lo < hi) {
@@ -1177,6 +1183,9 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
     __syncthreads();
     if (nk > kCap) unit_body<T, DP, HAS_PV, true>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
     else unit_body<T, DP, HAS_PV, false>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
+    if (tid == 0) s_next = G + atomicAdd(sc.claimed, 1);
+    __syncthreads();
+    pos = s_next;  // rewritten only after the next unit's barriers
   }
 }
 
