@@ -1140,8 +1140,10 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
   const int tid = threadIdx.x;
   const int B = p.B, N = p.N;
   const int G = gridDim.x;
-  // XCD-aware logical id: blockIdx.x % 8 is the XCD (G is a multiple of 8)
-  const int wg = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  // first-round position = block index: consecutive blocks are dispatched
+  // round-robin over the 8 XCDs and then over the CUs of each XCD, so the
+  // longest units (the first positions) land on different CUs of every XCD
+  const int wg = blockIdx.x;
   const Schedule sc = carve_schedule(p.ws, B, N);
   for (int b = tid; b <= B; b += kThreads) {
     if (b < B) {
