@@ -13,10 +13,9 @@ value = valid FLOPs (sum_b 4 H D n_b^3) / step time, in TFLOP/s.
 Prints ONE JSON line.  Also reports:
   roofline      the entry point's achieved TFLOP/s against the bf16 dense MFMA
                 peak: valid FLOPs over the average duration of one
-                mf_simplicial_fwd launch sequence (the plan kernel and the
-                pair kernel), timed with HIP events on the launch stream;
-                `traffic` is the HBM bytes of one
-                such sequence from the committed rocprofv3 --pmc summary
+                mf_simplicial_fwd launch (the pair kernel), timed with HIP
+                events on the launch stream; `traffic` is the HBM bytes of
+                one such launch from the committed rocprofv3 --pmc summary
                 (profiles/simplicial_fwd_geom_traffic.json) when present;
   cpu_baseline  the oracle's torch-CPU restatement of the reference path
                 (padded N, chunk 128, bf16 as configured) on the whole batch.
@@ -354,8 +353,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / BF16_DENSE_PEAK_TFLOPS, 5),
             "traffic": committed_traffic("simplicial_fwd_geom"),
-            "kernel": ("mf_simplicial_fwd launch sequence: simplicial_pair_plan<bf16> + "
-                       "simplicial_pair_kernel<bf16, 64, pair_valid=0>"),
+            "kernel": "mf_simplicial_fwd launch: simplicial_pair_kernel<bf16, 64, pair_valid=0>",
             "kernel_ms": round(kernel_ms, 5),
             "kernel_mean_ms": round(kernel_mean_ms, 5),
         },

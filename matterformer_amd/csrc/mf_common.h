@@ -30,9 +30,9 @@ size_t simplicial_fast_workspace_bytes(int batch, int heads, int tokens);
 int simplicial_fast_launch(const mf_simplicial_fwd_args* a, void* workspace, int num_cus, hipStream_t stream);
 constexpr int kSimplicialFastMaxBatch = 1024;  // molecules per launch slice
 
-// Pair-flash simplicial kernels for 16-bit operands (simplicial_pair.hip):
-// a plan launch and a main launch per slice of simplicial_pair_max_batch
-// molecules, with a schedule workspace of simplicial_pair_workspace_bytes.
+// Pair-flash simplicial kernel for 16-bit operands (simplicial_pair.hip):
+// one launch per slice of simplicial_pair_max_batch molecules; the
+// workspace (simplicial_pair_workspace_bytes) holds the unit-claim counter.
 bool simplicial_pair_serves(int tokens, int head_dim, int dtype);
 int simplicial_pair_max_batch(int tokens);
 size_t simplicial_pair_workspace_bytes(int batch, int tokens);

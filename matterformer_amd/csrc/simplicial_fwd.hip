@@ -636,8 +636,8 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
                                reinterpret_cast<uintptr_t>(a->out_f32) % 16 == 0;
   if (uses_fast(a->head_dim, a->dtype) && operands_aligned(a) && outputs_aligned &&
       simplicial_pair_serves(a->tokens, a->head_dim, a->dtype)) {
-    // the pair-flash kernels: plan + main launch per slice of molecules (the
-    // slices reuse the schedule workspace in stream order)
+    // the pair-flash kernel: one launch per slice of molecules (the slices
+    // share the claim counter in the workspace, in stream order)
     const uint64_t need = simplicial_pair_workspace_bytes(a->batch, a->tokens);
     if (a->workspace == nullptr || a->workspace_bytes < need)
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: workspace of " + std::to_string(need) +

@@ -11,15 +11,18 @@
 // and value vector Z_p = v1_j (.) v2_k: then S = Q W^T and out = softmax(S) Z,
 // plain attention over nk^2 keys whose tiles are formed on the fly.
 //
-// One launch, no workspace.  A persistent grid of 2 workgroups per CU; each
-// workgroup first reads every molecule's two byte masks (valid keys, valid
-// queries), ranks the molecules by cost and enumerates the units
-// (molecule b, head h, query group g) in that order -- every workgroup
-// derives the same list -- and takes units r G + w (even rounds) and
-// r G + G - 1 - w (odd rounds) of it, so that long and short units pair up.
-// A query group is at most 48 valid queries (3 tiles of 16); molecules with
-// more than 48 queries use groups of 32.  The rows of padded queries are
-// zeroed by a static share of (b, h) per workgroup.
+// One launch.  A persistent grid of 2 workgroups per CU; each workgroup
+// first copies every molecule's two byte masks (valid keys, valid queries)
+// into LDS and scans them, ranks the molecules by cost and enumerates the
+// units (molecule b, head h, query group g) in that order, longest first --
+// every workgroup derives the same list.  Workgroup w takes position w;
+// after that a workgroup that finishes a unit claims the next position with
+// one device-scope atomic on a counter in the caller's workspace (block 0
+// publishes the counter's value at launch start as the launch's base, tagged
+// with a per-launch epoch, so the counter is never reset).  A query group is
+// at most 48 valid queries (3 tiles of 16); molecules with more than 48
+// queries use groups of 32.  Each workgroup zeroes the rows of padded
+// queries of a static share of (b, h) after its first unit.
 //
 // Per unit the workgroup stages the unit's valid key rows (compacted) into
 // LDS as fp16 scaled by powers of two: K1s, K2s row-major, V1s, V2s as
@@ -53,6 +56,8 @@
 // two passes: the exact maximum m_i of the valid logits (GEMM1 only), then
 // P = 2^(S - m_i) with S rescaled to log2 units (the query scale is then
 // normalised on its own: sq = 1 - exponent(max|q'|)).
+#include <atomic>
+#include <chrono>
 #include <cmath>
 #include <type_traits>
 
@@ -87,42 +92,22 @@ struct Params {
   void* out;
   float* out_f32;
   float* lse;
-  int* ws;  // the schedule (see Schedule)
+  unsigned long long* sync;  // claim words (kFlag, kBase, kCounter)
+  unsigned long long epoch;  // unique per launch, nonzero
   int B, H, N, D;
 };
 
-// The schedule the plan kernel writes for the main kernel (int words):
-//   total               units of the launch
-//   claimed             units claimed so far after the first round
-//   info[B]             molecule info word (see info_*)
-//   order[B]            molecule of each cost rank, longest first
-//   pre[B + 1]          first unit position of each rank (pre[B] = total)
-//   kidx[B][N], qidx[B][N]  u16 valid key / query atoms of the molecules whose
-//                       valid atoms are not a prefix (others are not written)
-struct Schedule {
-  int* total;
-  int* claimed;  // units claimed after the first round (the plan sets it to 0)
-  uint32_t* info;
-  int* order;
-  int* pre;
-  uint16_t* kidx;
-  uint16_t* qidx;
-};
-__host__ __device__ inline Schedule carve_schedule(int* ws, int B, int N) {
-  Schedule sc;
-  sc.total = ws;
-  sc.claimed = ws + 1;
-  sc.info = reinterpret_cast<uint32_t*>(ws + 4);
-  sc.order = ws + 4 + B;
-  sc.pre = ws + 4 + 2 * B;
-  int* tail = ws + 4 + 3 * B + 4;
-  sc.kidx = reinterpret_cast<uint16_t*>(tail);
-  sc.qidx = sc.kidx + size_t(B) * N;
-  return sc;
-}
-__host__ inline size_t schedule_bytes(int B, int N) {
-  return (4 + 3 * size_t(B) + 4) * 4 + 2 * size_t(B) * N * 2;
-}
+// Claim words in the caller's workspace (u64 slots).  Block 0 reads the
+// counter when the launch starts and publishes it as the launch's base with
+// the epoch as the flag; a workgroup's list position is then
+// (counter value it claims) - base.  The counter is never reset, so the
+// workspace needs no initialisation and two launches that share it must run
+// in stream order.
+constexpr int kFlag = 0;
+constexpr int kBase = 1;
+constexpr int kCounter = 16;  // its own 128-byte line
+constexpr size_t kSyncBytes = 256;
+constexpr int kSpinLimit = 1 << 16;  // flag polls before the static fallback
 
 // LDS layout (bytes) for padded head dim DP.
 template <int DP>
@@ -960,174 +945,221 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 }
 
 // ---------------------------------------------------------------------------
-// plan kernel: workgroup 0 writes the schedule, the others zero the rows of
-// padded queries
+// schedule: every workgroup derives the same unit list from the masks
 // ---------------------------------------------------------------------------
-constexpr int kPlanThreads = 1024;
+// 16-byte chunks of the global byte range [src, src + nbytes) into LDS at
+// dst, starting from the chunk that holds src (returns src's offset in it).
+// A 16-byte aligned chunk that starts inside the range stays on the range's
+// pages.
+__device__ __forceinline__ int copy_bytes_to_lds(const uint8_t* src, int nbytes, unsigned char* dst, int wave,
+                                                 int lane) {
+  const int off = int(reinterpret_cast<uintptr_t>(src) & 15u);
+  const uint8_t* a0 = src - off;
+  const int nchunks = (off + nbytes + 15) >> 4;
+  for (int c0 = wave * 64; c0 < nchunks; c0 += kWaves * 64) {
+    if (c0 + lane < nchunks)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(a0 + 16 * (c0 + lane)),
+                                       (__attribute__((address_space(3))) void*)(dst + 16 * c0), 16, 0, 0);
+  }
+  return off;
+}
 
-template <typename T>
-__global__ void __launch_bounds__(kPlanThreads) simplicial_pair_plan(Params p) {
-  constexpr int kPW = kPlanThreads / 64;  // waves
-  __shared__ uint32_t s_info[kMaxBatch];
-  __shared__ int s_order[kMaxBatch];
+// Bytes [lo, hi) of a 16-byte mask chunk folded into a row's valid count
+// and last valid index (base = row index of the chunk's byte 0).  A byte is
+// valid when nonzero: bit 7 of ((x & 0x7f) + 0x7f) | x.
+template <bool PARTIAL>
+__device__ __forceinline__ void fold_chunk(uint4 v, int lo, int hi, int base, int& count, int& last) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t nz = (((w[j] & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w[j]) & 0x80808080u;
+    if constexpr (PARTIAL) {
+      const int l = min(max(lo - 4 * j, 0), 4), h = min(max(4 * j + 4 - hi, 0), 4);
+      nz = (l + h >= 4) ? 0u : nz & (0xffffffffu << (8 * l)) & (0xffffffffu >> (8 * h));
+    }
+    count += __popc(nz);
+    if (nz) last = base + 4 * j + ((31 - __clz(nz)) >> 3);
+  }
+}
+
+// Valid count and last valid index of bytes [a, b) of the mask row that
+// starts at LDS byte s of buf (16-byte chunks; the first and last are
+// partial).
+__device__ __forceinline__ void scan_segment(const unsigned char* buf, int s, int a, int b, int& count, int& last) {
+  if (a >= b) return;
+  int c = (s + a) & ~15;
+  const int end = s + b;
+  fold_chunk<true>(*reinterpret_cast<const uint4*>(buf + c), s + a - c, min(end - c, 16), c - s, count, last);
+#pragma unroll 2
+  for (c += 16; c + 16 <= end; c += 16)
+    fold_chunk<false>(*reinterpret_cast<const uint4*>(buf + c), 0, 16, c - s, count, last);
+  if (c < end) fold_chunk<true>(*reinterpret_cast<const uint4*>(buf + c), 0, end - c, c - s, count, last);
+}
+
+// Valid key / query counts and prefix flags of every molecule into s_info.
+// The masks of a chunk of molecules are copied into the staging area (two
+// halves of SB bytes, global -> LDS loads that need no registers); then TPR
+// adjacent threads scan one row (key rows 0..cb-1, query rows cb..2cb-1),
+// each a segment of it, and the segment counts meet over lanes.
+template <int DP>
+__device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem, uint32_t* s_info, int wave,
+                                           int lane) {
+  constexpr int SB = Lay<DP>::kQ / 2;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int B = p.B, H = p.H, N = p.N, D = p.D;
-  const Schedule sc = carve_schedule(p.ws, B, N);
-
-  if (blockIdx.x > 0) {
-    // zero the rows of padded queries, (b, h) pairs strided over the workgroups
-    const int cpr = D / 8;  // 16-byte chunks of a 16-bit output row
-    for (int bh = blockIdx.x - 1; bh < B * H; bh += gridDim.x - 1) {
-      const int b = bh / H;
-      const uint8_t* qrow = p.qv + size_t(b) * N;
-      // validity bytes of this thread's rows first (one round of loads)
-      constexpr int kMaxIt = (kMaxN * 8 + kPlanThreads - 1) / kPlanThreads;
-      uint8_t valid[kMaxIt];
-#pragma unroll
-      for (int it = 0; it < kMaxIt; ++it) {
-        const int u = tid + it * kPlanThreads;
-        valid[it] = u < N * cpr ? qrow[u / cpr] : 1;
-      }
-#pragma unroll
-      for (int it = 0; it < kMaxIt; ++it) {
-        const int u = tid + it * kPlanThreads;
-        const int i = u / cpr, cc = u - i * cpr;
-        if (valid[it]) continue;
-        const size_t row = size_t(bh) * N + i;
-        if (p.out) reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row * D)[cc] = uint4{0u, 0u, 0u, 0u};
-        if (p.out_f32) {
-          float4* o = reinterpret_cast<float4*>(p.out_f32 + row * D + cc * 8);
-          o[0] = float4{0.f, 0.f, 0.f, 0.f};
-          o[1] = float4{0.f, 0.f, 0.f, 0.f};
-        }
-        if (cc == 0 && p.lse) p.lse[row] = 0.0f;
-      }
+  const int B = p.B, N = p.N;
+  const int cmax = min((SB - 32) / N, kThreads / 2);  // molecules per chunk (slack: alignment)
+  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP>::kQ);  // [2 cmax] counts, then last indices
+  static_assert(kMaxQ * Lay<DP>::RB >= kThreads * 2 * 4, "row results must fit in the query staging area");
+  for (int b0 = 0; b0 < B; b0 += cmax) {
+    const int cb = min(cmax, B - b0);
+    const int ok = copy_bytes_to_lds(p.pkv + size_t(b0) * N, cb * N, smem, wave, lane);
+    const int oq = copy_bytes_to_lds(p.qv + size_t(b0) * N, cb * N, smem + SB, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies have landed
+    __syncthreads();
+    const int rows = 2 * cb;
+    // threads per row: a power of two, <= 8, tpr * rows <= kThreads (rows <= 2 cmax <= kThreads)
+    const int tpr = rows > kThreads / 2 ? 1 : rows > kThreads / 4 ? 2 : rows > kThreads / 8 ? 4 : 8;
+    const int r = tid / tpr, sg = tid & (tpr - 1);
+    int cnt = 0, last = -1;
+    if (r < rows) {
+      const bool key = r < cb;
+      const int m = key ? r : r - cb;
+      const int seg = (N + tpr - 1) / tpr;
+      const int a = sg * seg;
+      scan_segment(key ? smem : smem + SB, (key ? ok : oq) + m * N, a, min(N, a + seg), cnt, last);
     }
-    return;
+    // the tpr threads of a row are adjacent lanes of one wave
+    for (int o = 1; o < tpr; o <<= 1) {
+      cnt += __shfl_xor(cnt, o, 64);
+      last = max(last, __shfl_xor(last, o, 64));
+    }
+    if (r < rows && sg == 0) {
+      s_cnt[r] = cnt;
+      s_cnt[2 * cmax + r] = last;
+    }
+    __syncthreads();
+    for (int m = tid; m < cb; m += kThreads) {
+      const int ck = min(s_cnt[m], N), cq = min(s_cnt[cb + m], N);
+      const int lk = s_cnt[2 * cmax + m], lq = s_cnt[2 * cmax + cb + m];
+      s_info[b0 + m] =
+          uint32_t(ck) | (uint32_t(cq) << 11) | (lk + 1 == ck ? kKPre : 0u) | (lq + 1 == cq ? kQPre : 0u);
+    }
+    __syncthreads();
   }
+}
 
-  // 1. valid keys / queries of every molecule (one wave per molecule; rows
-  //    of up to 252 bytes are one window, the windows of up to 8 molecules
-  //    per wave are loaded before any is scanned)
-  __shared__ int s_lists;  // some molecule's valid atoms are not a prefix
-  if (tid == 0) s_lists = 0;
-  __syncthreads();
-  auto put_info = [&](int b, int ck, int lk, int cq, int lq) {
-    if (lane == 0) {
-      s_info[b] = uint32_t(ck) | (uint32_t(cq) << 11) | (lk + 1 == ck ? kKPre : 0u) | (lq + 1 == cq ? kQPre : 0u);
-      if (lk + 1 != ck || lq + 1 != cq) s_lists = 1;
-    }
-  };
-  if (N <= 252) {
-    constexpr int kRound = 8;
-    for (int b0 = wave; b0 < B; b0 += kPW * kRound) {
-      uint32_t wk[kRound], wq[kRound];
-      int off[kRound];
-#pragma unroll
-      for (int rr = 0; rr < kRound; ++rr) {
-        const int b = min(b0 + rr * kPW, B - 1);
-        int o2;
-        wk[rr] = load_window(p.pkv + size_t(b) * N, N, 0, lane, off[rr]);
-        wq[rr] = load_window(p.qv + size_t(b) * N, N, 0, lane, o2);
-      }
-#pragma unroll
-      for (int rr = 0; rr < kRound; ++rr) {
-        if (b0 + rr * kPW < B) {
-          const uint32_t keep = window_keep(0, off[rr], N, lane);
-          int ck = 0, cq = 0, lk = -1, lq = -1;
-          scan_window(wk[rr] & keep, -off[rr], ck, lk);
-          scan_window(wq[rr] & keep, -off[rr], cq, lq);
-          put_info(b0 + rr * kPW, ck, lk, cq, lq);
-        }
-      }
-    }
-  } else {
-    for (int b = wave; b < B; b += kPW) {
-      int ck = 0, cq = 0, lk = -1, lq = -1;
-      for (int base = 0; base < N + 3; base += 256) {
-        int off, o2;
-        const uint32_t wk = load_window(p.pkv + size_t(b) * N, N, base, lane, off);
-        const uint32_t wq = load_window(p.qv + size_t(b) * N, N, base, lane, o2);
-        const uint32_t keep = window_keep(base, off, N, lane);
-        scan_window(wk & keep, base - off, ck, lk);
-        scan_window(wq & keep, base - off, cq, lq);
-      }
-      put_info(b, ck, lk, cq, lq);
-    }
-  }
-  __syncthreads();
 
-  // 2. index lists of the molecules that need them (one wave per list)
-  if (s_lists) {
-    for (int t = wave; t < 2 * B; t += kPW) {
-      const int b = t >> 1;
+// s_order[rank] = molecule, s_pre[rank] = its first list position
+// (s_pre[B] = attention units in the list), molecules longest first (cost
+// nk^2 x query tiles, ties by index).  A molecule's position is the sum of
+// the units of the molecules ranked before it, so rank and position come
+// from one pass over (cost, units) pairs: 4 threads per molecule, each over
+// every 4th pair.  s_cu holds the pairs (over the staging area).
+__device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* s_info, uint16_t* s_order, int* s_pre,
+                                               uint2* s_cu) {
+  const int tid = threadIdx.x;
+  const int B = p.B, H = p.H;
+  const int B4 = (B + 3) & ~3;
+  for (int b = tid; b < B4; b += kThreads) {
+    uint2 cu{0u, 0u};  // padding: cost 0 and index >= B never rank before a molecule
+    if (b < B) {
       const uint32_t w = s_info[b];
-      if ((t & 1) == 0 && !(w & kKPre)) write_ranks(p.pkv + size_t(b) * N, N, sc.kidx + size_t(b) * N, lane);
-      if ((t & 1) == 1 && !(w & kQPre)) write_ranks(p.qv + size_t(b) * N, N, sc.qidx + size_t(b) * N, lane);
+      const int nk = info_nk(w), nq = info_nq(w);
+      cu.x = uint32_t(nk * nk) * uint32_t((nq + 15) / 16);
+      cu.y = uint32_t(H * num_groups(nk, nq));
     }
+    s_cu[b] = cu;
   }
-
-  // 3. molecules ranked by cost (nk^2 x query tiles, longest first, ties by
-  //    index) and the unit prefix over ranks
-  auto cost_of = [&](int b) {
-    const uint32_t w = s_info[b];
-    const int nk = info_nk(w), nq = info_nq(w);
-    return uint32_t(nk * nk) * uint32_t((nq + 15) / 16);
-  };
-  for (int b = tid; b < B; b += kPlanThreads) sc.info[b] = s_info[b];
-  for (int u0 = 0; u0 < 4 * B; u0 += kPlanThreads) {
-    const int u = u0 + tid;
-    const int b = min(u >> 2, B - 1), part = u & 3;
-    const uint32_t cb = cost_of(b);
-    int rank = 0;
-#pragma unroll 4
-    for (int o = part; o < B; o += 4) {
-      const uint32_t co = cost_of(o);
-      rank += (co > cb || (co == cb && o < b)) ? 1 : 0;
+  __syncthreads();
+  for (int t = tid; t < 4 * B; t += kThreads) {
+    const int b = t >> 2, part = t & 3;
+    const uint32_t cb = s_cu[b].x;
+    int rank = 0, pre = 0;
+    // pairs part, part + 4, ...: two per 16-byte read
+    const uint4* c4 = reinterpret_cast<const uint4*>(s_cu);
+    for (int o = 2 * part; o < B4; o += 8) {
+      const uint4 v = c4[o >> 1];  // pairs o, o + 1
+      const bool f0 = v.x > cb || (v.x == cb && o < b);
+      const bool f1 = v.z > cb || (v.z == cb && o + 1 < b);
+      rank += int(f0) + int(f1);
+      pre += (f0 ? int(v.y) : 0) + (f1 ? int(v.w) : 0);
     }
     rank += __shfl_xor(rank, 1, 64);
+    pre += __shfl_xor(pre, 1, 64);
     rank += __shfl_xor(rank, 2, 64);
-    if (part == 0 && u < 4 * B) {
-      s_order[rank] = b;
-      sc.order[rank] = b;
+    pre += __shfl_xor(pre, 2, 64);
+    if (part == 0) {
+      s_order[rank] = uint16_t(b);
+      s_pre[rank] = pre;
+      if (rank == B - 1) s_pre[B] = pre + int(s_cu[b].y);
     }
   }
   __syncthreads();
-  if (wave == 0) {
-    // exclusive prefix of H x groups over ranks, 4 ranks per lane (B <= 256)
-    int v[4], sum = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int rk = 4 * lane + e;
-      v[e] = rk < B ? H * num_groups(info_nk(s_info[s_order[rk]]), info_nq(s_info[s_order[rk]])) : 0;
-      sum += v[e];
-    }
-    int incl = sum;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += t;
-    }
-    int run = incl - sum;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int rk = 4 * lane + e;
-      if (rk < B) sc.pre[rk] = run;
-      run += v[e];
-    }
-    if (lane == 63) {
-      sc.pre[B] = incl;
-      *sc.total = incl;
-      *sc.claimed = 0;
+}
+
+// Zero the output rows of the padded queries of the (b, h) pairs w, w + G,
+// ... (a workgroup's share; rows of CPR 16-byte chunks, DP / 8 of them).
+template <typename T, int DP>
+__device__ __forceinline__ void zero_padded_share(const Params& p, const uint32_t* s_info, int w, int G) {
+  constexpr int CPR = DP / 8;
+  const int N = p.N, D = p.D, H = p.H;
+  const int cpr = D / 8;
+  for (int bh = w; bh < p.B * H; bh += G) {
+    const int b = bh / H;
+    const uint32_t info = s_info[b];
+    const bool qpre = (info & kQPre) != 0;
+    const int i0 = qpre ? info_nq(info) : 0;  // rows below are valid
+    const uint8_t* qrow = p.qv + size_t(b) * N;
+    for (int u = int(threadIdx.x); u < (N - i0) * CPR; u += kThreads) {
+      const int i = i0 + u / CPR, cc = u % CPR;
+      if (cc >= cpr || (!qpre && qrow[i] != 0)) continue;
+      const size_t row = size_t(bh) * N + i;
+      if (p.out) reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row * D)[cc] = uint4{0u, 0u, 0u, 0u};
+      if (p.out_f32) {
+        float4* o = reinterpret_cast<float4*>(p.out_f32 + row * D + cc * 8);
+        o[0] = float4{0.f, 0.f, 0.f, 0.f};
+        o[1] = float4{0.f, 0.f, 0.f, 0.f};
+      }
+      if (cc == 0 && p.lse) p.lse[row] = 0.0f;
     }
   }
 }
 
+// One unit (molecule b, head h, query group g): index lists of non-prefix
+// masks and the attention of the group's queries.  Ends with a barrier.
+template <typename T, int DP, bool HAS_PV>
+__device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, int b, int h, int g) {
+  using Ly = Lay<DP>;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const uint32_t info = reinterpret_cast<const uint32_t*>(smem + Ly::kInfo)[b];
+  const int nk = info_nk(info), nq = info_nq(info);
+  const bool kpre = (info & kKPre) != 0, qpre = (info & kQPre) != 0;
+  const int gs = group_size(nk, nq);
+  const int q0 = gs * g;
+  const int nqg = min(gs, nq - q0);
+  if (nqg > 0) {
+    if (!kpre || !qpre) {
+      uint16_t* kidx = reinterpret_cast<uint16_t*>(smem + Ly::kKidx);
+      uint16_t* qidx = reinterpret_cast<uint16_t*>(smem + Ly::kQidx);
+      if (wave == 0 && !kpre) write_ranks(p.pkv + size_t(b) * p.N, p.N, kidx, lane);
+      if (wave == 1 && !qpre) write_ranks(p.qv + size_t(b) * p.N, p.N, qidx, lane);
+      __syncthreads();
+    }
+    if (nk > kCap) unit_body<T, DP, HAS_PV, true>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
+    else unit_body<T, DP, HAS_PV, false>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
+  }
+  __syncthreads();
+}
+
 // ---------------------------------------------------------------------------
-// main kernel: the units of the schedule
+// the kernel: persistent workgroups over the units
 // ---------------------------------------------------------------------------
+// The list: the attention units (molecule, head, query group) of the
+// molecules in cost order (longest first).  Workgroup w takes position w
+// first; after that a workgroup that
+// finishes a unit claims the next position with one device-scope atomic, so
+// the workgroups that finish first take the longest remaining units.
 template <typename T, int DP, bool HAS_PV>
 __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) {
   using Ly = Lay<DP>;
@@ -1135,31 +1167,31 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
   uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + Ly::kInfo);
   int* s_pre = reinterpret_cast<int*>(smem + Ly::kPre);
   uint16_t* s_order = reinterpret_cast<uint16_t*>(smem + Ly::kOrder);
-  uint16_t* kidx = reinterpret_cast<uint16_t*>(smem + Ly::kKidx);
-  uint16_t* qidx = reinterpret_cast<uint16_t*>(smem + Ly::kQidx);
+  __shared__ int s_next;
+  __shared__ unsigned long long s_base;
+  __shared__ int s_dynamic;
   const int tid = threadIdx.x;
-  const int B = p.B, N = p.N;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int B = p.B, H = p.H;
   const int G = gridDim.x;
-  // first-round position = block index: consecutive blocks are dispatched
-  // round-robin over the 8 XCDs and then over the CUs of each XCD, so the
-  // longest units (the first positions) land on different CUs of every XCD
   const int wg = blockIdx.x;
-  const Schedule sc = carve_schedule(p.ws, B, N);
-  for (int b = tid; b <= B; b += kThreads) {
-    if (b < B) {
-      s_info[b] = sc.info[b];
-      s_order[b] = uint16_t(sc.order[b]);
-    }
-    s_pre[b] = sc.pre[b];
+
+  if (wg == 0 && tid == 0) {
+    // the launch's base: every claim of earlier launches has completed, and
+    // no claim of this one happens before the flag
+    const unsigned long long base =
+        __hip_atomic_fetch_add(p.sync + kCounter, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.sync + kBase, base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.sync + kFlag, p.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
+  if (tid == 0) s_dynamic = -1;  // the base is not read yet
+  scan_masks<DP>(p, smem, s_info, wave, lane);  // ends with a barrier
+  rank_molecules(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem));
   const int total = s_pre[B];
 
-  // units: the first round gives position w to workgroup w (positions are
-  // ordered longest first); after that a workgroup that finishes a unit
-  // claims the next position with one device-scope atomic, so the workgroups
-  // that finish first take the longest remaining units
-  __shared__ int s_next;
+  // the rows of padded queries: a static share of (b, h) pairs per
+  // workgroup, written after its first unit (or at once without one)
+  if (wg >= total) zero_padded_share<T, DP>(p, s_info, wg, G);
   for (int pos = wg; pos < total;) {
     // rank of the molecule: the last rank whose prefix is <= pos
     int lo = 0, hi = B - 1;
@@ -1170,22 +1202,32 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
     }
     const int b = s_order[lo];
     const uint32_t info = s_info[b];
-    const int nk = info_nk(info), nq = info_nq(info);
-    const int ng = num_groups(nk, nq);
-    const int gs = group_size(nk, nq);
-    const int u = pos - s_pre[lo];
-    const int h = u / ng, gi = u - h * ng;
-    const int q0 = gs * gi;
-    const int nqg = min(gs, nq - q0);
-    const bool kpre = (info & kKPre) != 0, qpre = (info & kQPre) != 0;
-    if (!kpre)
-      for (int t = tid; t < nk; t += kThreads) kidx[t] = sc.kidx[size_t(b) * N + t];
-    if (!qpre)
-      for (int t = tid; t < nq; t += kThreads) qidx[t] = sc.qidx[size_t(b) * N + t];
-    __syncthreads();
-    if (nk > kCap) unit_body<T, DP, HAS_PV, true>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
-    else unit_body<T, DP, HAS_PV, false>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
-    if (tid == 0) s_next = G + atomicAdd(sc.claimed, 1);
+    const int ng = num_groups(info_nk(info), info_nq(info));
+    const int i = pos - s_pre[lo];
+    const int h = i / ng;
+    run_unit<T, DP, HAS_PV>(p, smem, b, h, i - h * ng);  // ends with a barrier: s_next is read
+    if (tid == 0) {
+      if (s_dynamic < 0) {
+        // the base of this launch; a workgroup that never sees the flag
+        // takes the static positions w + G, w + 2 G, ... (a unit done twice
+        // writes the same bytes, and the claimed positions still cover the
+        // list)
+        int dyn = 0;
+        unsigned long long base = 0ull;
+        for (int it = 0; it < kSpinLimit; ++it) {
+          if (__hip_atomic_load(p.sync + kFlag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == p.epoch) {
+            base = __hip_atomic_load(p.sync + kBase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            dyn = 1;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(8);
+        }
+        s_base = base;
+        s_dynamic = dyn;
+      }
+      s_next = s_dynamic ? G + int(atomicAdd(p.sync + kCounter, 1ull) - s_base) : pos + G;
+    }
+    if (pos == wg) zero_padded_share<T, DP>(p, s_info, wg, G);
     __syncthreads();
     pos = s_next;  // rewritten only after the next unit's barriers
   }
@@ -1193,10 +1235,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
 
 template <typename T, int DP, bool HAS_PV>
 int launch(const Params& prm, int num_cus, hipStream_t stream) {
-  // plan: workgroup 0 plus workgroups that zero the padded query rows
-  hipLaunchKernelGGL(simplicial_pair_plan<T>, dim3(std::max(2, num_cus)), dim3(kPlanThreads), 0, stream, prm);
-  MF_HIP_CHECK(hipGetLastError());
-  const int grid = std::max(8, (2 * num_cus) & ~7);  // a multiple of 8 (the XCD count)
+  const int grid = std::max(8, 2 * num_cus);  // 2 workgroups per CU
   auto kern = simplicial_pair_kernel<T, DP, HAS_PV>;
   const size_t lds = Lay<DP>::kTotal;
   static bool attr_set = false;  // per instantiation
@@ -1222,10 +1261,24 @@ int simplicial_pair_max_batch(int tokens) {
 }
 
 size_t simplicial_pair_workspace_bytes(int batch, int tokens) {
-  return spair::schedule_bytes(std::min(batch, spair::kMaxBatch), tokens);
+  (void)batch;
+  (void)tokens;
+  return spair::kSyncBytes;
 }
 
-// One plan + main launch over a[0..batch), batch <= simplicial_pair_max_batch(tokens).
+// A value no earlier launch in this process used, never 0: a process-wide
+// counter mixed with a per-process salt from the clock.
+static unsigned long long next_epoch() {
+  static const unsigned long long salt =
+      (static_cast<unsigned long long>(std::chrono::steady_clock::now().time_since_epoch().count()) *
+       0x9E3779B97F4A7C15ull) | 1ull;
+  static std::atomic<unsigned long long> counter{0};
+  unsigned long long e = salt ^ (counter.fetch_add(1, std::memory_order_relaxed) + 1);
+  return e != 0 ? e : 1;
+}
+
+// One launch over a[0..batch), batch <= simplicial_pair_max_batch(tokens);
+// the workspace holds the claim words (kSyncBytes, 8-byte aligned).
 int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* workspace, int num_cus, hipStream_t stream) {
   using namespace spair;
   if (a->batch > simplicial_pair_max_batch(a->tokens))
@@ -1237,7 +1290,8 @@ int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* workspace, int
   prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
   prm.out = a->out; prm.out_f32 = a->out_f32; prm.lse = a->lse;
   prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
-  prm.ws = static_cast<int*>(workspace);
+  prm.sync = static_cast<unsigned long long*>(workspace);
+  prm.epoch = next_epoch();
   const int g = num_cus;
   const bool pv = a->pair_valid != nullptr;
   const bool bf = a->dtype == MF_DTYPE_BF16;

@@ -120,3 +120,40 @@ def test_extreme_scale_rescaled_two_pass(cuda, dtype):
     assert torch.isfinite(out32).all()
     assert rel(out32.cpu().numpy(), ref) <= 2e-2
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_long_rows_empty_molecule_and_mask_holes(cuda, dtype):
+    # mask rows longer than 252 bytes (several 16-byte chunks per scanned
+    # segment), a molecule without valid atoms, a hole in the key mask and one
+    # in the query mask (neither mask of molecule 2 is a prefix)
+    B, H, N, D = 3, 2, 270, 32
+    case = list(random_simplicial(B, H, N, D, seed=21, counts=[200, 0, 75], holes=[(2, 10)], std=0.05))
+    case[5] = case[5].clone()
+    case[5][2, 30] = False
+    out, lse, out32, ref, ref_lse = run(tuple(case), cuda, dtype)
+    assert torch.isfinite(out32).all()
+    for b in range(B):
+        assert rel(out32[b].cpu().numpy(), ref[b]) <= 2e-2, b
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+    qv = case[5]
+    assert torch.count_nonzero(out32.cpu().permute(0, 2, 1, 3)[~qv]) == 0
+    assert torch.count_nonzero(out.float().cpu().permute(0, 2, 1, 3)[~qv]) == 0
+
+
+def test_more_units_than_workgroups(cuda):
+    # 256 molecules x 4 heads: more (molecule, head) pairs than the persistent
+    # grid has workgroups, molecules of 0 .. 12 atoms, some with holes
+    B, H, N, D = 256, 4, 12, 16
+    gen = torch.Generator().manual_seed(6)
+    counts = torch.randint(0, N + 1, (B,), generator=gen).tolist()
+    holes = [(b, 1) for b in range(0, B, 7) if counts[b] > 2]
+    case = random_simplicial(B, H, N, D, seed=9, counts=counts, holes=holes, std=0.3)
+    out, lse, out32, ref, ref_lse = run(case, cuda, torch.bfloat16)
+    assert rel(out32.cpu().numpy(), ref) <= 2e-2
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+    qv = case[5]
+    assert torch.count_nonzero(out32.cpu().permute(0, 2, 1, 3)[~qv]) == 0
+    # a second call reuses the workspace counter from where the first ended
+    out2 = run(case, cuda, torch.bfloat16)[2]
+    assert torch.equal(out2, out32)
