@@ -98,9 +98,11 @@ struct Params {
 };
 
 // Claim words in the caller's workspace (u64 slots).  Block 0 reads the
-// counter when the launch starts and publishes it as the launch's base with
-// the epoch as the flag; a workgroup's list position is then
-// (counter value it claims) - base.  The counter is never reset, so the
+// counter when the launch starts and publishes it as the launch's base, with
+// flag = epoch ^ mix(base) beside it; a reader that loads both words (in any
+// order, no fences) accepts them only when they match, so it never takes a
+// stale or half-written pair.  A workgroup's list position is then
+// G + (counter value it claims) - base.  The counter is never reset, so the
 // workspace needs no initialisation and two launches that share it must run
 // in stream order.
 constexpr int kFlag = 0;
@@ -108,6 +110,21 @@ constexpr int kBase = 1;
 constexpr int kCounter = 16;  // its own 128-byte line
 constexpr size_t kSyncBytes = 256;
 constexpr int kSpinLimit = 1 << 16;  // flag polls before the static fallback
+
+__host__ __device__ inline unsigned long long claim_flag(unsigned long long epoch, unsigned long long base) {
+  return epoch ^ (base * 0x9E3779B97F4A7C15ull);  // odd multiplier: a bijection of base
+}
+
+// Claim state of a workgroup (LDS): base of the launch, dynamic = -1 (flag
+// not seen yet), 0 (never seen: static positions) or 1; next = the position
+// claimed during the last unit when claimed != 0.
+struct ClaimState {
+  unsigned long long base;
+  int dynamic;
+  int claimed;
+  int next;
+  int pad;
+};
 
 // LDS layout (bytes) for padded head dim DP.
 template <int DP>
@@ -132,7 +149,8 @@ struct Lay {
   static constexpr int kG = kMn + DP * 4;       // float [kWaves][4] |V1|, |V2|, |q| maxima
   static constexpr int kScal = kG + kWaves * 4 * 4;  // int [8] scale exponents, slow flag
   static constexpr int kM = kScal + 8 * 4;      // float [kMaxQ] two-pass maxima (log2 units)
-  static constexpr int kTotal = kM + kMaxQ * 4;
+  static constexpr int kClaim = (kM + kMaxQ * 4 + 7) & ~7;  // ClaimState
+  static constexpr int kTotal = kClaim + int(sizeof(ClaimState));
   // after the pair loop: per-wave partial outputs float [kWaves][kMaxQ][RS]
   // and denominators float [kWaves][kMaxQ], over K1s .. V2s
   static constexpr int RS = DP + 4;
@@ -226,6 +244,67 @@ __device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a),
                                                                 __builtin_bit_cast(u16x2_t, b)));
 }
+// Cross-lane reductions on VALU (DPP and v_permlane*_swap) instead of
+// ds_bpermute.  group_reduce<G>: every lane gets op over its aligned group of
+// G consecutive lanes (quad permutes; then the half-row and row mirrors,
+// which pair a lane with the other half of its group once each half holds
+// its own total; then the 16- and 32-lane swaps, whose two results are the
+// lane's value and its partner's, in some order).  stride_reduce<S>: op over
+// the lanes l' = l mod S (row rotations by 4 and 8 within rows of 16, then
+// the swaps).  Every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_peer(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), CTRL, 0xf, 0xf, false));
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t swap16_op(uint32_t v, Op op) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return op(uint32_t(r[0]), uint32_t(r[1]));
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t swap32_op(uint32_t v, Op op) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return op(uint32_t(r[0]), uint32_t(r[1]));
+}
+template <int G, typename Op>
+__device__ __forceinline__ uint32_t group_reduce(uint32_t v, Op op) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group size");
+  if constexpr (G >= 2) v = op(v, dpp_peer<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  if constexpr (G >= 4) v = op(v, dpp_peer<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  if constexpr (G >= 8) v = op(v, dpp_peer<0x141>(v));  // row_half_mirror
+  if constexpr (G >= 16) v = op(v, dpp_peer<0x140>(v)); // row_mirror
+  if constexpr (G >= 32) v = swap16_op(v, op);
+  if constexpr (G >= 64) v = swap32_op(v, op);
+  return v;
+}
+template <int S, typename Op>
+__device__ __forceinline__ uint32_t stride_reduce(uint32_t v, Op op) {
+  static_assert(S == 4 || S == 8, "stride");
+  if constexpr (S == 4) v = op(v, dpp_peer<0x124>(v));  // row_ror:4
+  v = op(v, dpp_peer<0x128>(v));                        // row_ror:8
+  v = swap16_op(v, op);
+  return swap32_op(v, op);
+}
+struct PkMaxU16 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return pk_max_u16(a, b); }
+};
+struct MaxF32 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }
+};
+struct AddF32 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }
+};
+struct AddI32 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; }
+};
+struct MaxI32 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return uint32_t(max(int(a), int(b))); }
+};
+
 // |x| from the 16-bit pattern of x with the sign cleared
 template <typename T>
 __device__ __forceinline__ float mag_to_float(uint32_t m) {
@@ -257,8 +336,14 @@ __device__ __forceinline__ int group_size(int nk, int nq) {
 }
 __device__ __forceinline__ int num_groups(int nk, int nq) {
   if (nq <= 0) return 0;
-  const int gs = group_size(nk, nq);
-  return (nq + gs - 1) / gs;
+  if (nk > kCap) return (nq + 15) >> 4;
+  return nq <= kMaxQ ? 1 : (nq + 31) >> 5;
+}
+
+// i / d for 0 <= i, d and i + d < 2^21: (i + 1/2) / d is at least 1/(2d)
+// away from an integer, more than the error of the float reciprocal.
+__device__ __forceinline__ int div_small(int i, int d) {
+  return int((float(i) + 0.5f) * __builtin_amdgcn_rcpf(float(d)));
 }
 
 // The aligned dword at window offset base + 4 lane of a mask row (0 past the
@@ -514,9 +599,37 @@ __device__ __forceinline__ void pair_loop_n(int nqt, const unsigned char* smem, 
 // MULTI: the unit has more than kCap keys and is taken in (j block, k block)
 // pairs, with one query tile (its accumulators stay live across the block
 // loop, so the group is kept small).
+// Zero the output rows of the padded queries of the (b, h) pairs w, w + G,
+// ... (a workgroup's share; rows of CPR 16-byte chunks, DP / 8 of them).
+template <typename T, int DP>
+__device__ __forceinline__ void zero_padded_share(const Params& p, const uint32_t* s_info, int w, int G) {
+  constexpr int CPR = DP / 8;
+  const int N = p.N, D = p.D, H = p.H;
+  const int cpr = D / 8;
+  for (int bh = w; bh < p.B * H; bh += G) {
+    const int b = bh / H;
+    const uint32_t info = s_info[b];
+    const bool qpre = (info & kQPre) != 0;
+    const int i0 = qpre ? info_nq(info) : 0;  // rows below are valid
+    const uint8_t* qrow = p.qv + size_t(b) * N;
+    for (int u = int(threadIdx.x); u < (N - i0) * CPR; u += kThreads) {
+      const int i = i0 + u / CPR, cc = u % CPR;
+      if (cc >= cpr || (!qpre && qrow[i] != 0)) continue;
+      const size_t row = size_t(bh) * N + i;
+      if (p.out) reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row * D)[cc] = uint4{0u, 0u, 0u, 0u};
+      if (p.out_f32) {
+        float4* o = reinterpret_cast<float4*>(p.out_f32 + row * D + cc * 8);
+        o[0] = float4{0.f, 0.f, 0.f, 0.f};
+        o[1] = float4{0.f, 0.f, 0.f, 0.f};
+      }
+      if (cc == 0 && p.lse) p.lse[row] = 0.0f;
+    }
+  }
+}
+
 template <typename T, int DP, bool HAS_PV, bool MULTI>
 __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, int b, int h, int nk, int q0, int nqg,
-                                          bool kpre, bool qpre) {
+                                          bool kpre, bool qpre, bool zero_share) {
   constexpr int QT = kMaxQ / 16;       // query tiles held in registers
   const int nqt = (nqg + 15) >> 4;     // query tiles in use
   using Ly = Lay<DP>;
@@ -610,10 +723,22 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
                   : uint4{0u, 0u, 0u, 0u};
     }
   }
+  // the launch's claim base, loaded with the unit's rows while not known yet
+  ClaimState* cl = reinterpret_cast<ClaimState*>(smem + Ly::kClaim);
+  const bool want_base = tid == 0 && cl->dynamic < 0;
+  unsigned long long f_flag = 0ull, f_base = 0ull;
+  if (want_base) {
+    f_flag = __hip_atomic_load(p.sync + kFlag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    f_base = __hip_atomic_load(p.sync + kBase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   if constexpr (!MULTI) {
     load_block(0, 0);
+    // the workgroup's share of padded query rows, stored while the loads are
+    // in flight (first unit only)
+    if (zero_share) zero_padded_share<T, DP>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
     acc_max();
   } else {
+    if (zero_share) zero_padded_share<T, DP>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
     for (int rc = 0; rc < nch; ++rc) {
       load_block(rc, rc);
       acc_max();
@@ -625,18 +750,12 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   {
     // column maxima over the lanes that share cc, then per wave to LDS
 #pragma unroll
-    for (int off = CPR; off < 64; off <<= 1) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        c1[e] = pk_max_u16(c1[e], uint32_t(__shfl_xor(int(c1[e]), off, 64)));
-        c2[e] = pk_max_u16(c2[e], uint32_t(__shfl_xor(int(c2[e]), off, 64)));
-      }
+    for (int e = 0; e < 4; ++e) {
+      c1[e] = stride_reduce<CPR>(c1[e], PkMaxU16{});
+      c2[e] = stride_reduce<CPR>(c2[e], PkMaxU16{});
     }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      gv = pk_max_u16(gv, uint32_t(__shfl_xor(int(gv), off, 64)));
-      gqm = pk_max_u16(gqm, uint32_t(__shfl_xor(int(gqm), off, 64)));
-    }
+    gv = group_reduce<64>(gv, PkMaxU16{});
+    gqm = group_reduce<64>(gqm, PkMaxU16{});
     uint32_t* colw = reinterpret_cast<uint32_t*>(colmax);  // [kWaves][2][DP / 2] packed pairs
     if (lane < CPR) {
 #pragma unroll
@@ -666,7 +785,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       m2 = mag_to_float<T>(w2);
       mn[lane] = m1 * m2;
     }
-    const float a1 = wave_max(m1), a2 = wave_max(m2);
+    const float a1 = __uint_as_float(group_reduce<64>(__float_as_uint(m1), MaxF32{}));
+    const float a2 = __uint_as_float(group_reduce<64>(__float_as_uint(m2), MaxF32{}));
     if (lane == 0) {
       const uint32_t* gw = reinterpret_cast<const uint32_t*>(gmax);
       uint32_t v = 0u, qm = 0u;
@@ -693,6 +813,10 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       scal[4] = sq;
       scal[5] = E;
       scal[6] = E != 0 ? 1 : 0;  // two-pass flag (queries add theirs)
+      if (want_base && f_flag == claim_flag(p.epoch, f_base)) {
+        cl->base = f_base;
+        cl->dynamic = 1;
+      }
     }
   }
   __syncthreads();
@@ -721,8 +845,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       for (int e = 0; e < 4; ++e) w[e] = pack_h2(f[2 * e], f[2 * e + 1]);
       if (row < 16 * QT) *reinterpret_cast<uint4*>(Qs + row * RB + e0 * 2) = uint4{w[0], w[1], w[2], w[3]};
       // |S| bound of the row: the CPR lanes of a row are consecutive
-#pragma unroll
-      for (int off = 1; off < CPR; off <<= 1) ub += __shfl_xor(ub, off, 64);
+      ub = __uint_as_float(group_reduce<CPR>(__float_as_uint(ub), AddF32{}));
       if (row < nqg && cc == 0 && !(ub <= kBoundLimit)) atomicOr(&scal[6], 1);
     }
   }
@@ -836,9 +959,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     float* redm = colmax;  // [kWaves][kMaxQ]
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      float m = mloc[qt];
-      m = fmaxf(m, __shfl_xor(m, 16, 64));
-      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      const float m = __uint_as_float(swap32_op(swap16_op(__float_as_uint(mloc[qt]), MaxF32{}), MaxF32{}));
       if (g == 0) redm[wave * kMaxQ + 16 * qt + r16] = m;
     }
     __syncthreads();
@@ -887,6 +1008,12 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       if (pass == 0) finish_max();
     }
   }
+
+  // the next position, claimed now: the atomic's round trip overlaps the
+  // output of this unit
+  const bool claiming = tid == 0 && cl->dynamic > 0;
+  unsigned long long ticket = 0ull;
+  if (claiming) ticket = atomicAdd(p.sync + kCounter, 1ull);
 
   // ---- phase D: reduce the waves' partials, normalise, write ---------------
   __syncthreads();  // every wave is done with K/V (the reduction area aliases them)
@@ -941,6 +1068,10 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     }
     if (c8 == 0 && p.lse) p.lse[row] = mass ? ((slow ? s_m[i] : 0.0f) + __log2f(l)) * kLn2 : 0.0f;
   }
+  if (claiming) {
+    cl->next = int(gridDim.x) + int(ticket - cl->base);
+    cl->claimed = 1;
+  }
   __syncthreads();  // the next unit rewrites the index lists and LDS
 }
 
@@ -964,36 +1095,56 @@ __device__ __forceinline__ int copy_bytes_to_lds(const uint8_t* src, int nbytes,
   return off;
 }
 
-// Bytes [lo, hi) of a 16-byte mask chunk folded into a row's valid count
-// and last valid index (base = row index of the chunk's byte 0).  A byte is
-// valid when nonzero: bit 7 of ((x & 0x7f) + 0x7f) | x.
+// Nonzero bytes of a dword as bit 7 of each byte: ((x & 0x7f) + 0x7f) | x.
+__device__ __forceinline__ uint32_t nz_bytes(uint32_t x) { return (((x & 0x7f7f7f7fu) + 0x7f7f7f7fu) | x) & 0x80808080u; }
+
+// Those of bytes [lo, hi) of a 16-byte chunk (dword j covers bytes 4j..4j+3).
 template <bool PARTIAL>
-__device__ __forceinline__ void fold_chunk(uint4 v, int lo, int hi, int base, int& count, int& last) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t nz = (((w[j] & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w[j]) & 0x80808080u;
-    if constexpr (PARTIAL) {
-      const int l = min(max(lo - 4 * j, 0), 4), h = min(max(4 * j + 4 - hi, 0), 4);
-      nz = (l + h >= 4) ? 0u : nz & (0xffffffffu << (8 * l)) & (0xffffffffu >> (8 * h));
-    }
-    count += __popc(nz);
-    if (nz) last = base + 4 * j + ((31 - __clz(nz)) >> 3);
+__device__ __forceinline__ uint32_t nz_chunk_word(uint32_t x, int j, int lo, int hi) {
+  uint32_t nz = nz_bytes(x);
+  if constexpr (PARTIAL) {
+    const int l = min(max(lo - 4 * j, 0), 4), h = min(max(4 * j + 4 - hi, 0), 4);
+    nz = (l + h >= 4) ? 0u : nz & (0xffffffffu << (8 * l)) & (0xffffffffu >> (8 * h));
   }
+  return nz;
+}
+
+// Valid bytes [lo, hi) of the 16-byte chunk at LDS byte c folded into a
+// count; lastc = c when the chunk has one (the last such chunk wins).
+template <bool PARTIAL>
+__device__ __forceinline__ void fold_chunk(const unsigned char* buf, int c, int lo, int hi, int& count, int& lastc) {
+  const uint4 v = *reinterpret_cast<const uint4*>(buf + c);
+  const uint32_t n0 = nz_chunk_word<PARTIAL>(v.x, 0, lo, hi), n1 = nz_chunk_word<PARTIAL>(v.y, 1, lo, hi);
+  const uint32_t n2 = nz_chunk_word<PARTIAL>(v.z, 2, lo, hi), n3 = nz_chunk_word<PARTIAL>(v.w, 3, lo, hi);
+  count += __popc(n0) + __popc(n1) + __popc(n2) + __popc(n3);
+  if ((n0 | n1 | n2 | n3) != 0u) lastc = c;
 }
 
 // Valid count and last valid index of bytes [a, b) of the mask row that
 // starts at LDS byte s of buf (16-byte chunks; the first and last are
-// partial).
+// partial).  The last valid byte is found once, in the last chunk that has
+// one.
 __device__ __forceinline__ void scan_segment(const unsigned char* buf, int s, int a, int b, int& count, int& last) {
   if (a >= b) return;
-  int c = (s + a) & ~15;
-  const int end = s + b;
-  fold_chunk<true>(*reinterpret_cast<const uint4*>(buf + c), s + a - c, min(end - c, 16), c - s, count, last);
+  const int begin = s + a, end = s + b;
+  int c = begin & ~15;
+  int lastc = -1;
+  fold_chunk<true>(buf, c, begin - c, end - c, count, lastc);
 #pragma unroll 2
-  for (c += 16; c + 16 <= end; c += 16)
-    fold_chunk<false>(*reinterpret_cast<const uint4*>(buf + c), 0, 16, c - s, count, last);
-  if (c < end) fold_chunk<true>(*reinterpret_cast<const uint4*>(buf + c), 0, end - c, c - s, count, last);
+  for (c += 16; c + 16 <= end; c += 16) fold_chunk<false>(buf, c, 0, 16, count, lastc);
+  if (c < end) fold_chunk<true>(buf, c, 0, end - c, count, lastc);
+  if (lastc >= 0) {
+    const uint4 v = *reinterpret_cast<const uint4*>(buf + lastc);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const int lo = begin - lastc, hi = end - lastc;
+    int l = -1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t nz = nz_chunk_word<true>(w[j], j, lo, hi);
+      if (nz) l = 4 * j + ((31 - __clz(nz)) >> 3);
+    }
+    last = lastc - s + l;
+  }
 }
 
 // Valid key / query counts and prefix flags of every molecule into s_info.
@@ -1028,10 +1179,18 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
       const int a = sg * seg;
       scan_segment(key ? smem : smem + SB, (key ? ok : oq) + m * N, a, min(N, a + seg), cnt, last);
     }
-    // the tpr threads of a row are adjacent lanes of one wave
-    for (int o = 1; o < tpr; o <<= 1) {
-      cnt += __shfl_xor(cnt, o, 64);
-      last = max(last, __shfl_xor(last, o, 64));
+    // the tpr threads of a row are adjacent lanes of one wave (all active)
+    if (tpr >= 2) {
+      cnt = int(AddI32{}(uint32_t(cnt), dpp_peer<0xB1>(uint32_t(cnt))));
+      last = int(MaxI32{}(uint32_t(last), dpp_peer<0xB1>(uint32_t(last))));
+    }
+    if (tpr >= 4) {
+      cnt = int(AddI32{}(uint32_t(cnt), dpp_peer<0x4E>(uint32_t(cnt))));
+      last = int(MaxI32{}(uint32_t(last), dpp_peer<0x4E>(uint32_t(last))));
+    }
+    if (tpr >= 8) {
+      cnt = int(AddI32{}(uint32_t(cnt), dpp_peer<0x141>(uint32_t(cnt))));
+      last = int(MaxI32{}(uint32_t(last), dpp_peer<0x141>(uint32_t(last))));
     }
     if (r < rows && sg == 0) {
       s_cnt[r] = cnt;
@@ -1054,9 +1213,11 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
 // nk^2 x query tiles, ties by index).  A molecule's position is the sum of
 // the units of the molecules ranked before it, so rank and position come
 // from one pass over (cost, units) pairs: 4 threads per molecule, each over
-// every 4th pair.  s_cu holds the pairs (over the staging area).
+// every 4th pair.  s_cu holds the pairs (over the staging area).  The
+// molecule whose positions hold position w (when w < s_pre[B]) writes
+// *s_first = b | (w - its first position) << 16.
 __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* s_info, uint16_t* s_order, int* s_pre,
-                                               uint2* s_cu) {
+                                               uint2* s_cu, int w, int* s_first) {
   const int tid = threadIdx.x;
   const int B = p.B, H = p.H;
   const int B4 = (B + 3) & ~3;
@@ -1084,51 +1245,24 @@ __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* 
       rank += int(f0) + int(f1);
       pre += (f0 ? int(v.y) : 0) + (f1 ? int(v.w) : 0);
     }
-    rank += __shfl_xor(rank, 1, 64);
-    pre += __shfl_xor(pre, 1, 64);
-    rank += __shfl_xor(rank, 2, 64);
-    pre += __shfl_xor(pre, 2, 64);
+    // the 4 threads of a molecule are one quad (whole quads are active)
+    rank = int(group_reduce<4>(uint32_t(rank), AddI32{}));
+    pre = int(group_reduce<4>(uint32_t(pre), AddI32{}));
     if (part == 0) {
+      const int units = int(s_cu[b].y);
       s_order[rank] = uint16_t(b);
       s_pre[rank] = pre;
-      if (rank == B - 1) s_pre[B] = pre + int(s_cu[b].y);
+      if (rank == B - 1) s_pre[B] = pre + units;
+      if (w >= pre && w < pre + units) *s_first = b | ((w - pre) << 16);
     }
   }
   __syncthreads();
 }
 
-// Zero the output rows of the padded queries of the (b, h) pairs w, w + G,
-// ... (a workgroup's share; rows of CPR 16-byte chunks, DP / 8 of them).
-template <typename T, int DP>
-__device__ __forceinline__ void zero_padded_share(const Params& p, const uint32_t* s_info, int w, int G) {
-  constexpr int CPR = DP / 8;
-  const int N = p.N, D = p.D, H = p.H;
-  const int cpr = D / 8;
-  for (int bh = w; bh < p.B * H; bh += G) {
-    const int b = bh / H;
-    const uint32_t info = s_info[b];
-    const bool qpre = (info & kQPre) != 0;
-    const int i0 = qpre ? info_nq(info) : 0;  // rows below are valid
-    const uint8_t* qrow = p.qv + size_t(b) * N;
-    for (int u = int(threadIdx.x); u < (N - i0) * CPR; u += kThreads) {
-      const int i = i0 + u / CPR, cc = u % CPR;
-      if (cc >= cpr || (!qpre && qrow[i] != 0)) continue;
-      const size_t row = size_t(bh) * N + i;
-      if (p.out) reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row * D)[cc] = uint4{0u, 0u, 0u, 0u};
-      if (p.out_f32) {
-        float4* o = reinterpret_cast<float4*>(p.out_f32 + row * D + cc * 8);
-        o[0] = float4{0.f, 0.f, 0.f, 0.f};
-        o[1] = float4{0.f, 0.f, 0.f, 0.f};
-      }
-      if (cc == 0 && p.lse) p.lse[row] = 0.0f;
-    }
-  }
-}
-
 // One unit (molecule b, head h, query group g): index lists of non-prefix
 // masks and the attention of the group's queries.  Ends with a barrier.
 template <typename T, int DP, bool HAS_PV>
-__device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, int b, int h, int g) {
+__device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, int b, int h, int g, bool zero_share) {
   using Ly = Lay<DP>;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -1146,8 +1280,8 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
       if (wave == 1 && !qpre) write_ranks(p.qv + size_t(b) * p.N, p.N, qidx, lane);
       __syncthreads();
     }
-    if (nk > kCap) unit_body<T, DP, HAS_PV, true>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
-    else unit_body<T, DP, HAS_PV, false>(p, smem, b, h, nk, q0, nqg, kpre, qpre);
+    if (nk > kCap) unit_body<T, DP, HAS_PV, true>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
+    else unit_body<T, DP, HAS_PV, false>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
   }
   __syncthreads();
 }
@@ -1167,9 +1301,8 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
   uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + Ly::kInfo);
   int* s_pre = reinterpret_cast<int*>(smem + Ly::kPre);
   uint16_t* s_order = reinterpret_cast<uint16_t*>(smem + Ly::kOrder);
-  __shared__ int s_next;
-  __shared__ unsigned long long s_base;
-  __shared__ int s_dynamic;
+  ClaimState* cl = reinterpret_cast<ClaimState*>(smem + Ly::kClaim);
+  __shared__ int s_first;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int B = p.B, H = p.H;
@@ -1178,58 +1311,70 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
 
   if (wg == 0 && tid == 0) {
     // the launch's base: every claim of earlier launches has completed, and
-    // no claim of this one happens before the flag
+    // no claim of this one happens before a workgroup has read the base
     const unsigned long long base =
         __hip_atomic_fetch_add(p.sync + kCounter, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(p.sync + kBase, base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.sync + kFlag, p.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.sync + kFlag, claim_flag(p.epoch, base), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (tid == 0) s_dynamic = -1;  // the base is not read yet
+  if (tid == 0) {
+    cl->dynamic = -1;  // the base is not read yet
+    cl->claimed = 0;
+  }
   scan_masks<DP>(p, smem, s_info, wave, lane);  // ends with a barrier
-  rank_molecules(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem));
+  rank_molecules(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
   const int total = s_pre[B];
 
   // the rows of padded queries: a static share of (b, h) pairs per
-  // workgroup, written after its first unit (or at once without one)
+  // workgroup, written during its first unit (or at once without one)
   if (wg >= total) zero_padded_share<T, DP>(p, s_info, wg, G);
   for (int pos = wg; pos < total;) {
-    // rank of the molecule: the last rank whose prefix is <= pos
-    int lo = 0, hi = B - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_pre[mid] <= pos) lo = mid;
-      else hi = mid - 1;
+    int b, i;  // molecule, unit within it
+    if (pos == wg) {
+      b = s_first & 0xffff;
+      i = s_first >> 16;
+    } else {
+      // rank of the molecule: the last rank whose prefix is <= pos (the
+      // prefixes do not decrease), counted over all ranks at once: lane l
+      // compares ranks 4 l .. 4 l + 3 (B <= 256)
+      const int4 v = reinterpret_cast<const int4*>(s_pre)[lane];
+      const int r0 = 4 * lane;
+      const int lo = __popcll(__ballot(r0 < B && v.x <= pos)) + __popcll(__ballot(r0 + 1 < B && v.y <= pos)) +
+                     __popcll(__ballot(r0 + 2 < B && v.z <= pos)) + __popcll(__ballot(r0 + 3 < B && v.w <= pos)) - 1;
+      b = s_order[lo];
+      i = pos - s_pre[lo];
     }
-    const int b = s_order[lo];
     const uint32_t info = s_info[b];
     const int ng = num_groups(info_nk(info), info_nq(info));
-    const int i = pos - s_pre[lo];
-    const int h = i / ng;
-    run_unit<T, DP, HAS_PV>(p, smem, b, h, i - h * ng);  // ends with a barrier: s_next is read
+    const int h = div_small(i, ng);
+    run_unit<T, DP, HAS_PV>(p, smem, b, h, i - h * ng, pos == wg);  // ends with a barrier: cl->next is read
     if (tid == 0) {
-      if (s_dynamic < 0) {
-        // the base of this launch; a workgroup that never sees the flag
-        // takes the static positions w + G, w + 2 G, ... (a unit done twice
-        // writes the same bytes, and the claimed positions still cover the
-        // list)
-        int dyn = 0;
-        unsigned long long base = 0ull;
-        for (int it = 0; it < kSpinLimit; ++it) {
-          if (__hip_atomic_load(p.sync + kFlag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == p.epoch) {
-            base = __hip_atomic_load(p.sync + kBase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            dyn = 1;
-            break;
+      if (cl->claimed) {
+        cl->claimed = 0;  // the unit claimed the next position
+      } else {
+        if (cl->dynamic < 0) {
+          // the base of this launch; a workgroup that never sees it takes
+          // the static positions w + G, w + 2 G, ... (a unit done twice
+          // writes the same bytes, and the claimed positions still cover
+          // the list)
+          int dyn = 0;
+          for (int it = 0; it < kSpinLimit; ++it) {
+            const unsigned long long f = __hip_atomic_load(p.sync + kFlag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned long long bb = __hip_atomic_load(p.sync + kBase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (f == claim_flag(p.epoch, bb)) {
+              cl->base = bb;
+              dyn = 1;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(8);
           }
-          __builtin_amdgcn_s_sleep(8);
+          cl->dynamic = dyn;
         }
-        s_base = base;
-        s_dynamic = dyn;
+        cl->next = cl->dynamic > 0 ? G + int(atomicAdd(p.sync + kCounter, 1ull) - cl->base) : pos + G;
       }
-      s_next = s_dynamic ? G + int(atomicAdd(p.sync + kCounter, 1ull) - s_base) : pos + G;
     }
-    if (pos == wg) zero_padded_share<T, DP>(p, s_info, wg, G);
     __syncthreads();
-    pos = s_next;  // rewritten only after the next unit's barriers
+    pos = cl->next;  // rewritten only after the next unit's barriers
   }
 }
 
