@@ -195,7 +195,7 @@ def bench_knn(args) -> int:
                    "k": 16, "c3_batch32_ms": round(res["c3"]["ms"], 5)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("knn_c3_scaled"),
-                     "kernel": "mf::knn::knn_kernel<16, 4>", "kernel_ms": round(sc["kernel_ms"], 5)},
+                     "kernel": "mf::knn::knn_block_kernel<16, 1>", "kernel_ms": round(sc["kernel_ms"], 5)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -15,10 +15,19 @@
 // Each lane keeps the KMAX smallest keys it has seen, sorted, in registers:
 //   key = float_bits(d2) << 32 | j
 // (d2 >= 0, so the float bit pattern orders like the value and the low word
-// breaks ties by index).  A candidate below the current KMAX-th key is merged
-// in by one compare-exchange chain.  The L lists are then merged in log2(L)
-// butterfly rounds: partners exchange lists, take min(a[s], b[KMAX-1-s])
-// (a bitonic sequence holding the KMAX smallest of both) and sort it with a
+// breaks ties by index).
+//   k <= 16 (knn_block_kernel): a lane takes its candidates KMAX at a time:
+//     the block's keys are sorted by a bitonic network and merged into the
+//     list as min(list[s], block[KMAX-1-s]) (a bitonic sequence holding the
+//     KMAX smallest of both) followed by a bitonic clean-up; a block none of
+//     whose keys is below the wave's current KMAX-th keys is skipped.  No
+//     step depends on the data, so the 64 lanes of a wave never diverge (an
+//     insertion chain runs for the wave whenever one lane inserts, which is
+//     nearly every candidate).
+//   k > 16 (knn_kernel): a candidate below the current KMAX-th key is merged
+//     in by one compare-exchange chain.
+// The L lists of a query are then merged in log2(L) butterfly rounds:
+// partners exchange lists, take min(a[s], b[KMAX-1-s]) and clean up with the
 // bitonic network, so both partners end with the same list.
 #include <cmath>
 
@@ -66,6 +75,134 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
   const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), mask, 64);
   const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), mask, 64);
   return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Sort KMAX keys ascending (bitonic sorting network).
+template <int KMAX>
+__device__ __forceinline__ void sort_network(uint64_t (&v)[KMAX]) {
+#pragma unroll
+  for (int k = 2; k <= KMAX; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) {
+        const int l = i ^ j;
+        if (l > i) {
+          if ((i & k) == 0) cmp_swap(v[i], v[l]);
+          else cmp_swap(v[l], v[i]);
+        }
+      }
+    }
+  }
+}
+
+// The 64-bit value of the partner lane in a butterfly merge over groups of
+// consecutive lanes: quad permutes for masks 1 and 2, then the half-row and
+// row mirrors (lane l of an 8 / 16 group meets the lane at the mirrored
+// position of the other half; after the earlier rounds every lane of a half
+// holds the same list, so any cross pairing merges the two halves).
+template <int MASK>
+__device__ __forceinline__ uint64_t partner_u64(uint64_t v) {
+  constexpr int ctrl = MASK == 1 ? 0xB1 : MASK == 2 ? 0x4E : MASK == 4 ? 0x141 : 0x140;
+  static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "lanes per query <= 16");
+  const uint32_t lo = uint32_t(__builtin_amdgcn_update_dpp(int(uint32_t(v)), int(uint32_t(v)), ctrl, 0xf, 0xf, false));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_update_dpp(int(uint32_t(v >> 32)), int(uint32_t(v >> 32)), ctrl, 0xf, 0xf, false));
+  return (uint64_t(hi) << 32) | lo;
+}
+
+template <int KMAX, int L, int MASK>
+__device__ __forceinline__ void merge_round(uint64_t (&list)[KMAX]) {
+  if constexpr (MASK < L) {
+    uint64_t other[KMAX];
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) other[s] = partner_u64<MASK>(list[KMAX - 1 - s]);
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) list[s] = list[s] < other[s] ? list[s] : other[s];
+    bitonic_sort(list);
+    merge_round<KMAX, L, MASK * 2>(list);
+  }
+}
+
+template <int KMAX, int L>
+__global__ void __launch_bounds__(kThreads) knn_block_kernel(Params p) {
+  __shared__ float sx[kTile], sy[kTile], sz[kTile];
+  __shared__ uint8_t spad[kTile];
+
+  constexpr int kQueries = kThreads / L;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int sub = tid % L;
+  const int i = blockIdx.x * kQueries + tid / L;
+  const int N = p.N;
+  const float* x = p.coords + size_t(b) * N * 3;
+  const uint8_t* pad = p.pad ? p.pad + size_t(b) * N : nullptr;
+  const bool valid_i = i < N && !(pad && pad[i]);
+  float xi = 0.0f, yi = 0.0f, zi = 0.0f;
+  if (valid_i) {
+    xi = x[3 * i + 0];
+    yi = x[3 * i + 1];
+    zi = x[3 * i + 2];
+  }
+
+  uint64_t list[KMAX];
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) list[s] = kEmpty;
+
+  for (int t0 = 0; t0 < N; t0 += kTile) {
+    const int n = min(kTile, N - t0);
+    __syncthreads();
+    for (int u = tid; u < n; u += kThreads) {
+      sx[u] = x[3 * (t0 + u) + 0];
+      sy[u] = x[3 * (t0 + u) + 1];
+      sz[u] = x[3 * (t0 + u) + 2];
+      spad[u] = pad ? pad[t0 + u] : 0;
+    }
+    __syncthreads();
+    // every lane runs the same number of blocks (invalid queries see only
+    // empty keys), so the whole wave stays converged
+    for (int u0 = sub; u0 - sub < n; u0 += L * KMAX) {
+      uint64_t blk[KMAX];
+      bool below = false;
+#pragma unroll
+      for (int t = 0; t < KMAX; ++t) {
+        const int u = u0 + L * t;
+        const int j = t0 + u;
+        uint64_t key = kEmpty;
+        if (valid_i && u < n && !spad[u] && !(p.exclude_self && j == i)) {
+          const float dx = xi - sx[u];
+          const float dy = yi - sy[u];
+          const float dz = zi - sz[u];
+          const float xx = dx * dx;
+          const float yy = dy * dy;
+          const float zz = dz * dz;
+          const float s2 = xx + yy;
+          const float d2 = s2 + zz;
+          key = (static_cast<uint64_t>(__float_as_uint(d2)) << 32) | static_cast<uint32_t>(j);
+        }
+        blk[t] = key;
+        below |= key < list[KMAX - 1];
+      }
+      if (!__any(below)) continue;  // no lane of the wave keeps any of these
+      sort_network(blk);
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s) list[s] = list[s] < blk[KMAX - 1 - s] ? list[s] : blk[KMAX - 1 - s];
+      bitonic_sort(list);
+    }
+  }
+
+  merge_round<KMAX, L, 1>(list);
+
+  if (i >= N) return;
+  int32_t* oi = p.idx + (size_t(b) * N + i) * p.K;
+  float* od = p.dist ? p.dist + (size_t(b) * N + i) * p.K : nullptr;
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    if (s % L != sub || s >= p.K) continue;
+    const uint64_t key = list[s];
+    const bool empty = key == kEmpty;
+    oi[s] = empty ? -1 : static_cast<int32_t>(static_cast<uint32_t>(key));
+    if (od) od[s] = empty ? INFINITY : sqrtf(__uint_as_float(static_cast<uint32_t>(key >> 32)));
+  }
 }
 
 template <int KMAX, int L>
@@ -150,19 +287,31 @@ template <int KMAX, int L>
 int launch(const Params& p, hipStream_t stream) {
   constexpr int kQueries = kThreads / L;
   const dim3 grid((p.N + kQueries - 1) / kQueries, p.B);
-  hipLaunchKernelGGL((knn_kernel<KMAX, L>), grid, dim3(kThreads), 0, stream, p);
+  if constexpr (KMAX <= 16) hipLaunchKernelGGL((knn_block_kernel<KMAX, L>), grid, dim3(kThreads), 0, stream, p);
+  else hipLaunchKernelGGL((knn_kernel<KMAX, L>), grid, dim3(kThreads), 0, stream, p);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
 }
 
 // Lanes per query: enough queries in flight to fill the GPU at small batch
-// sizes, fewer lanes (less merging) when there are many queries.
+// sizes, fewer lanes (less merging) when there are many queries.  The block
+// kernel (k <= 16) goes down to one lane per query once the queries alone
+// give every SIMD four waves.
 template <int KMAX>
 int dispatch_lanes(const Params& p, int num_cus, hipStream_t stream) {
   const long long queries = (long long)p.B * p.N;
-  if (queries * 16 <= (long long)num_cus * 2048) return launch<KMAX, 16>(p, stream);
-  if (queries * 8 <= (long long)num_cus * 4096) return launch<KMAX, 8>(p, stream);
-  return launch<KMAX, 4>(p, stream);
+  if constexpr (KMAX <= 16) {
+    const long long lanes = (long long)num_cus * 4 * 4 * 64;
+    if (queries >= lanes) return launch<KMAX, 1>(p, stream);
+    if (queries * 2 >= lanes) return launch<KMAX, 2>(p, stream);
+    if (queries * 4 >= lanes) return launch<KMAX, 4>(p, stream);
+    if (queries * 8 >= lanes) return launch<KMAX, 8>(p, stream);
+    return launch<KMAX, 16>(p, stream);
+  } else {
+    if (queries * 16 <= (long long)num_cus * 2048) return launch<KMAX, 16>(p, stream);
+    if (queries * 8 <= (long long)num_cus * 4096) return launch<KMAX, 8>(p, stream);
+    return launch<KMAX, 4>(p, stream);
+  }
 }
 
 }  // namespace knn
