@@ -98,8 +98,11 @@ typedef struct mf_simplicial_fwd_args {
   float* out_f32;   /* [B*H, N, D] fp32 (the saved-for-backward output)      */
   float* lse;       /* [B*H, N] fp32, natural log                            */
   /* Device scratch of at least mf_simplicial_fwd_workspace_size() bytes,
-   * 16-byte aligned (NULL when that size is 0).  Holds the per-molecule
-   * atom lists and the work items built on the device for this call. */
+   * 16-byte aligned (NULL when that size is 0).  The 16-bit kernels keep
+   * their device-side state there: the pair kernel a unit-claim counter
+   * that needs no initialisation (it is never reset), the other 16-bit
+   * kernel the per-molecule atom lists and work items of the call.  Calls
+   * that share a workspace must be ordered on one stream. */
   void* workspace;
   uint64_t workspace_bytes;
   int32_t batch;
