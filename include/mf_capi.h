@@ -98,11 +98,11 @@ typedef struct mf_simplicial_fwd_args {
   float* out_f32;   /* [B*H, N, D] fp32 (the saved-for-backward output)      */
   float* lse;       /* [B*H, N] fp32, natural log                            */
   /* Device scratch of at least mf_simplicial_fwd_workspace_size() bytes,
-   * 16-byte aligned (NULL when that size is 0).  The 16-bit kernels keep
-   * their device-side state there: the pair kernel a unit-claim counter
-   * that needs no initialisation (it is never reset), the other 16-bit
-   * kernel the per-molecule atom lists and work items of the call.  Calls
-   * that share a workspace must be ordered on one stream. */
+   * 16-byte aligned (NULL when that size is 0).  ZERO IT ONCE before its
+   * first use: its first 256 bytes hold the pair kernel's unit-claim
+   * counter, which every call leaves at 0 again (graph replays included);
+   * the rest holds the other 16-bit kernel's per-call atom lists and work
+   * items.  Calls that share a workspace must be ordered on one stream. */
   void* workspace;
   uint64_t workspace_bytes;
   int32_t batch;

@@ -207,9 +207,24 @@ def current_stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_WORKSPACES: dict = {}
+
+
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
     """Device scratch for an entry point (16-byte aligned; torch's allocator
-    hands out 512-byte aligned blocks)."""
+    hands out 512-byte aligned blocks).
+
+    mf_simplicial_fwd's workspace holds a claim counter that must be zero
+    before the first call and that every call leaves zero, so one buffer is
+    kept per (device, stream) -- calls on one stream are ordered -- and
+    zero-filled whenever it is allocated or grown."""
     if nbytes == 0:
         return None
-    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+    dev = torch.device(device)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(dev).cuda_stream)
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(int(nbytes), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = buf
+    return buf

@@ -31,12 +31,13 @@ int simplicial_fast_launch(const mf_simplicial_fwd_args* a, void* workspace, int
 constexpr int kSimplicialFastMaxBatch = 1024;  // molecules per launch slice
 
 // Pair-flash simplicial kernel for 16-bit operands (simplicial_pair.hip):
-// one launch per slice of simplicial_pair_max_batch molecules; the
-// workspace (simplicial_pair_workspace_bytes) holds the unit-claim counter.
+// one launch per slice of simplicial_pair_max_batch molecules; its claim
+// region (simplicial_pair_workspace_bytes) holds the unit-claim counter,
+// 0 before the first launch and left 0 by every launch.
 bool simplicial_pair_serves(int tokens, int head_dim, int dtype);
 int simplicial_pair_max_batch(int tokens);
 size_t simplicial_pair_workspace_bytes(int batch, int tokens);
-int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* workspace, int num_cus, hipStream_t stream);
+int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* claims, int num_cus, hipStream_t stream);
 
 #define MF_HIP_CHECK(expr)                                                     \
   do {                                                                         \

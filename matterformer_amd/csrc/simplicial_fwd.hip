@@ -567,10 +567,11 @@ extern "C" int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t
 extern "C" uint64_t mf_simplicial_fwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens,
                                                      int32_t head_dim, int32_t dtype) {
   if (batch <= 0 || heads <= 0 || tokens <= 0 || !uses_fast(head_dim, dtype)) return 0;
-  // enough for either 16-bit path (unaligned operands take the other one)
-  const uint64_t fast = simplicial_fast_workspace_bytes(batch, heads, tokens);
-  if (!simplicial_pair_serves(tokens, head_dim, dtype)) return fast;
-  return std::max<uint64_t>(fast, simplicial_pair_workspace_bytes(batch, tokens));
+  // either 16-bit path (unaligned operands take the other one): the pair
+  // kernel's claim region first, at the same offset for every shape (its
+  // counter stays 0 between calls, so nothing else may write there), then
+  // the other kernel's region
+  return simplicial_pair_workspace_bytes(batch, tokens) + simplicial_fast_workspace_bytes(batch, heads, tokens);
 }
 
 static int launch_general(const mf_simplicial_fwd_args* a, size_t lds, int num_cus, int min_keys, bool zero_rows,
@@ -637,8 +638,9 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
   if (uses_fast(a->head_dim, a->dtype) && operands_aligned(a) && outputs_aligned &&
       simplicial_pair_serves(a->tokens, a->head_dim, a->dtype)) {
     // the pair-flash kernel: one launch per slice of molecules (the slices
-    // share the claim counter in the workspace, in stream order)
-    const uint64_t need = simplicial_pair_workspace_bytes(a->batch, a->tokens);
+    // share the claim counter at the start of the workspace, in stream order)
+    const uint64_t need = simplicial_pair_workspace_bytes(a->batch, a->tokens) +
+                          simplicial_fast_workspace_bytes(a->batch, a->heads, a->tokens);
     if (a->workspace == nullptr || a->workspace_bytes < need)
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: workspace of " + std::to_string(need) +
                                                " bytes required (mf_simplicial_fwd_workspace_size), got " +
@@ -669,7 +671,9 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
   }
   if (uses_fast(a->head_dim, a->dtype) && operands_aligned(a)) {
     if (a->tokens > 32767) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports tokens <= 32767");
-    const uint64_t need = simplicial_fast_workspace_bytes(a->batch, a->heads, a->tokens);
+    // its region follows the pair kernel's claim region
+    const uint64_t claims = simplicial_pair_workspace_bytes(a->batch, a->tokens);
+    const uint64_t need = claims + simplicial_fast_workspace_bytes(a->batch, a->heads, a->tokens);
     if (a->workspace == nullptr || a->workspace_bytes < need)
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: workspace of " + std::to_string(need) +
                                                " bytes required (mf_simplicial_fwd_workspace_size), got " +
@@ -693,7 +697,7 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
       if (a->out) sub.out = static_cast<char*>(a->out) + b0 * elem;
       if (a->out_f32) sub.out_f32 = a->out_f32 + b0 * row * a->head_dim;
       if (a->lse) sub.lse = a->lse + b0 * row;
-      st = simplicial_fast_launch(&sub, a->workspace, dev.num_cus, s);
+      st = simplicial_fast_launch(&sub, static_cast<char*>(a->workspace) + claims, dev.num_cus, s);
       if (st != MF_OK) return st;
     }
     return MF_OK;

@@ -17,9 +17,10 @@
 // units (molecule b, head h, query group g) in that order, longest first --
 // every workgroup derives the same list.  Workgroup w takes position w;
 // after that a workgroup that finishes a unit claims the next position with
-// one device-scope atomic on a counter in the caller's workspace (block 0
-// publishes the counter's value at launch start as the launch's base, tagged
-// with a per-launch epoch, so the counter is never reset).  A query group is
+// one device-scope atomic on a counter in the caller's workspace (each unit
+// makes one claim, so the claim that returns the unit count minus one is the
+// launch's last, and its workgroup puts the counter back to 0: every launch,
+// graph replays included, starts from 0).  A query group is
 // at most 48 valid queries (3 tiles of 16); molecules with more than 48
 // queries use groups of 32.  Each workgroup zeroes the rows of padded
 // queries of a static share of (b, h) after its first unit.
@@ -56,8 +57,6 @@
 // two passes: the exact maximum m_i of the valid logits (GEMM1 only), then
 // P = 2^(S - m_i) with S rescaled to log2 units (the query scale is then
 // normalised on its own: sq = 1 - exponent(max|q'|)).
-#include <atomic>
-#include <chrono>
 #include <cmath>
 #include <type_traits>
 
@@ -92,39 +91,29 @@ struct Params {
   void* out;
   float* out_f32;
   float* lse;
-  unsigned long long* sync;  // claim words (kFlag, kBase, kCounter)
-  unsigned long long epoch;  // unique per launch, nonzero
+  unsigned int* counter;  // claims of this launch (0 at launch start and end)
   int B, H, N, D;
 };
 
-// Claim words in the caller's workspace (u64 slots).  Block 0 reads the
-// counter when the launch starts and publishes it as the launch's base, with
-// flag = epoch ^ mix(base) beside it; a reader that loads both words (in any
-// order, no fences) accepts them only when they match, so it never takes a
-// stale or half-written pair.  A workgroup's list position is then
-// G + (counter value it claims) - base.  The counter is never reset, so the
-// workspace needs no initialisation and two launches that share it must run
-// in stream order.
-constexpr int kFlag = 0;
-constexpr int kBase = 1;
-constexpr int kCounter = 16;  // its own 128-byte line
+// The claim counter in the caller's workspace (its own 128-byte line).  It
+// must be 0 before the first launch; every launch leaves it 0.
 constexpr size_t kSyncBytes = 256;
-constexpr int kSpinLimit = 1 << 16;  // flag polls before the static fallback
 
-__host__ __device__ inline unsigned long long claim_flag(unsigned long long epoch, unsigned long long base) {
-  return epoch ^ (base * 0x9E3779B97F4A7C15ull);  // odd multiplier: a bijection of base
-}
-
-// Claim state of a workgroup (LDS): base of the launch, dynamic = -1 (flag
-// not seen yet), 0 (never seen: static positions) or 1; next = the position
-// claimed during the last unit when claimed != 0.
+// Claim state of a workgroup (LDS): claimed != 0 when the unit just run
+// claimed the next position, next = that position.
 struct ClaimState {
-  unsigned long long base;
-  int dynamic;
   int claimed;
   int next;
-  int pad;
 };
+
+// Thread 0's claim: position G + ticket.  A launch of `total` units makes
+// exactly `total` claims (one per unit run, the last of each workgroup's
+// failing), which return 0 .. total - 1; the one that returns total - 1 is
+// the last, so no claim of this launch can follow its reset of the counter.
+__device__ __forceinline__ int claimed_position(unsigned int* counter, unsigned int ticket, int total) {
+  if (int(ticket) == total - 1) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return int(gridDim.x) + int(ticket);
+}
 
 // LDS layout (bytes) for padded head dim DP.
 template <int DP>
@@ -149,7 +138,7 @@ struct Lay {
   static constexpr int kG = kMn + DP * 4;       // float [kWaves][4] |V1|, |V2|, |q| maxima
   static constexpr int kScal = kG + kWaves * 4 * 4;  // int [8] scale exponents, slow flag
   static constexpr int kM = kScal + 8 * 4;      // float [kMaxQ] two-pass maxima (log2 units)
-  static constexpr int kClaim = (kM + kMaxQ * 4 + 7) & ~7;  // ClaimState
+  static constexpr int kClaim = kM + kMaxQ * 4;  // ClaimState
   static constexpr int kTotal = kClaim + int(sizeof(ClaimState));
   // after the pair loop: per-wave partial outputs float [kWaves][kMaxQ][RS]
   // and denominators float [kWaves][kMaxQ], over K1s .. V2s
@@ -723,14 +712,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
                   : uint4{0u, 0u, 0u, 0u};
     }
   }
-  // the launch's claim base, loaded with the unit's rows while not known yet
   ClaimState* cl = reinterpret_cast<ClaimState*>(smem + Ly::kClaim);
-  const bool want_base = tid == 0 && cl->dynamic < 0;
-  unsigned long long f_flag = 0ull, f_base = 0ull;
-  if (want_base) {
-    f_flag = __hip_atomic_load(p.sync + kFlag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    f_base = __hip_atomic_load(p.sync + kBase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
   if constexpr (!MULTI) {
     load_block(0, 0);
     // the workgroup's share of padded query rows, stored while the loads are
@@ -813,10 +795,6 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       scal[4] = sq;
       scal[5] = E;
       scal[6] = E != 0 ? 1 : 0;  // two-pass flag (queries add theirs)
-      if (want_base && f_flag == claim_flag(p.epoch, f_base)) {
-        cl->base = f_base;
-        cl->dynamic = 1;
-      }
     }
   }
   __syncthreads();
@@ -1011,9 +989,9 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 
   // the next position, claimed now: the atomic's round trip overlaps the
   // output of this unit
-  const bool claiming = tid == 0 && cl->dynamic > 0;
-  unsigned long long ticket = 0ull;
-  if (claiming) ticket = atomicAdd(p.sync + kCounter, 1ull);
+  const bool claiming = tid == 0;
+  unsigned int ticket = 0u;
+  if (claiming) ticket = atomicAdd(p.counter, 1u);
 
   // ---- phase D: reduce the waves' partials, normalise, write ---------------
   __syncthreads();  // every wave is done with K/V (the reduction area aliases them)
@@ -1069,7 +1047,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     if (c8 == 0 && p.lse) p.lse[row] = mass ? ((slow ? s_m[i] : 0.0f) + __log2f(l)) * kLn2 : 0.0f;
   }
   if (claiming) {
-    cl->next = int(gridDim.x) + int(ticket - cl->base);
+    cl->next = claimed_position(p.counter, ticket, reinterpret_cast<const int*>(smem + Ly::kPre)[p.B]);
     cl->claimed = 1;
   }
   __syncthreads();  // the next unit rewrites the index lists and LDS
@@ -1309,18 +1287,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
   const int G = gridDim.x;
   const int wg = blockIdx.x;
 
-  if (wg == 0 && tid == 0) {
-    // the launch's base: every claim of earlier launches has completed, and
-    // no claim of this one happens before a workgroup has read the base
-    const unsigned long long base =
-        __hip_atomic_fetch_add(p.sync + kCounter, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.sync + kBase, base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.sync + kFlag, claim_flag(p.epoch, base), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (tid == 0) {
-    cl->dynamic = -1;  // the base is not read yet
-    cl->claimed = 0;
-  }
+  if (tid == 0) cl->claimed = 0;
   scan_masks<DP>(p, smem, s_info, wave, lane);  // ends with a barrier
   rank_molecules(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
   const int total = s_pre[B];
@@ -1352,25 +1319,9 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
       if (cl->claimed) {
         cl->claimed = 0;  // the unit claimed the next position
       } else {
-        if (cl->dynamic < 0) {
-          // the base of this launch; a workgroup that never sees it takes
-          // the static positions w + G, w + 2 G, ... (a unit done twice
-          // writes the same bytes, and the claimed positions still cover
-          // the list)
-          int dyn = 0;
-          for (int it = 0; it < kSpinLimit; ++it) {
-            const unsigned long long f = __hip_atomic_load(p.sync + kFlag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned long long bb = __hip_atomic_load(p.sync + kBase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (f == claim_flag(p.epoch, bb)) {
-              cl->base = bb;
-              dyn = 1;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-          }
-          cl->dynamic = dyn;
-        }
-        cl->next = cl->dynamic > 0 ? G + int(atomicAdd(p.sync + kCounter, 1ull) - cl->base) : pos + G;
+        // every unit run makes exactly one claim (unit_body claims for all
+        // units the list holds; this covers a unit without valid queries)
+        cl->next = claimed_position(p.counter, atomicAdd(p.counter, 1u), total);
       }
     }
     __syncthreads();
@@ -1411,20 +1362,10 @@ size_t simplicial_pair_workspace_bytes(int batch, int tokens) {
   return spair::kSyncBytes;
 }
 
-// A value no earlier launch in this process used, never 0: a process-wide
-// counter mixed with a per-process salt from the clock.
-static unsigned long long next_epoch() {
-  static const unsigned long long salt =
-      (static_cast<unsigned long long>(std::chrono::steady_clock::now().time_since_epoch().count()) *
-       0x9E3779B97F4A7C15ull) | 1ull;
-  static std::atomic<unsigned long long> counter{0};
-  unsigned long long e = salt ^ (counter.fetch_add(1, std::memory_order_relaxed) + 1);
-  return e != 0 ? e : 1;
-}
-
 // One launch over a[0..batch), batch <= simplicial_pair_max_batch(tokens);
-// the workspace holds the claim words (kSyncBytes, 8-byte aligned).
-int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* workspace, int num_cus, hipStream_t stream) {
+// `claims` is the kSyncBytes claim region of the workspace (4-byte aligned,
+// 0 before the first launch, left 0 by every launch).
+int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* claims, int num_cus, hipStream_t stream) {
   using namespace spair;
   if (a->batch > simplicial_pair_max_batch(a->tokens))
     return fail(MF_ERR_INVALID_ARGUMENT, "simplicial pair launch: batch slice too large");
@@ -1435,8 +1376,7 @@ int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* workspace, int
   prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
   prm.out = a->out; prm.out_f32 = a->out_f32; prm.lse = a->lse;
   prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
-  prm.sync = static_cast<unsigned long long*>(workspace);
-  prm.epoch = next_epoch();
+  prm.counter = static_cast<unsigned int*>(claims);
   const int g = num_cus;
   const bool pv = a->pair_valid != nullptr;
   const bool bf = a->dtype == MF_DTYPE_BF16;

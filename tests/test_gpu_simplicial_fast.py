@@ -157,3 +157,33 @@ def test_more_units_than_workgroups(cuda):
     # a second call reuses the workspace counter from where the first ended
     out2 = run(case, cuda, torch.bfloat16)[2]
     assert torch.equal(out2, out32)
+
+
+def test_graph_replays_match_eager(cuda):
+    # A captured call replays with the same kernel arguments; the unit-claim
+    # counter in the workspace is put back to 0 by each launch's last claim,
+    # so every replay schedules like a fresh call.  Eager calls run between
+    # the replays, and every replay is checked against the eager result.
+    B, H, N, D = 6, 2, 40, 64
+    q, k1, v1, k2, v2, qv, pkv, _ = random_simplicial(B, H, N, D, seed=31, counts=[40, 33, 17, 2, 25, 39],
+                                                      std=0.1)
+    ops = [t.to(torch.bfloat16).to(cuda) for t in (q, k1, v1, k2, v2)]
+    masks = dict(query_valid=qv.to(cuda), pair_key_valid=pkv.to(cuda), pair_valid=None, precision="bf16_tc")
+    eager = hip_simplicial_attention_forward(*ops, **masks)[2].clone()
+    side = torch.cuda.Stream(cuda)
+    side.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(side):
+        warm = hip_simplicial_attention_forward(*ops, **masks)[2]  # workspace of this stream, zeroed, outside capture
+    torch.cuda.current_stream(cuda).wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(warm, eager)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        captured = hip_simplicial_attention_forward(*ops, **masks)[2]
+    for rep in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), rep
+        again = hip_simplicial_attention_forward(*ops, **masks)[2]
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager), rep
