@@ -134,14 +134,21 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
 
   // register staging of one key tile: chunk c = tid + t*kThreads -> (key c / CPR, d 8*(c % CPR)),
   // and the lane's two mask words of that tile
+  // Loads are branch-free (rows past N read row N - 1, mask words past W
+  // read word W - 1, and both are zeroed where they are used), so the wait
+  // for a tile's loads counts only the loads issued after them.
   struct Stage {
     Op8 k[CPT], v[CPT];
     uint32_t m0, m1;
+    uint32_t valid;  // bit t: K chunk t is a real key; bit CPT + t: V chunk t
   };
   auto load_tile = [&](int jt, Stage& st) {
     const int w0 = 2 * jt;
-    st.m0 = (q_in && w0 < p.W) ? qbits[w0] : 0u;
-    st.m1 = (q_in && w0 + 1 < p.W) ? qbits[w0 + 1] : 0u;
+    st.m0 = qbits[min(w0, p.W - 1)];
+    st.m1 = qbits[min(w0 + 1, p.W - 1)];
+    st.m0 = (q_in && w0 < p.W) ? st.m0 : 0u;
+    st.m1 = (q_in && w0 + 1 < p.W) ? st.m1 : 0u;
+    st.valid = 0u;
 #pragma unroll
     for (int t = 0; t < CPT; ++t) {
       // K: 8 lanes per key row (coalesced); V: 64 consecutive keys per wave
@@ -152,18 +159,9 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
       const int d0 = (c % CPR) * 8;
       const int vkey = jt * kTile + c % kTile;
       const int vd0 = (c / kTile) * 8;
-      if (key < N) {
-        st.k[t] = *reinterpret_cast<const Op8*>(gk + size_t(key) * D + d0);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) st.k[t][e] = T(0.0f);
-      }
-      if (vkey < N) {
-        st.v[t] = *reinterpret_cast<const Op8*>(gv + size_t(vkey) * D + vd0);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) st.v[t][e] = T(0.0f);
-      }
+      st.k[t] = *reinterpret_cast<const Op8*>(gk + size_t(min(key, N - 1)) * D + d0);
+      st.v[t] = *reinterpret_cast<const Op8*>(gv + size_t(min(vkey, N - 1)) * D + vd0);
+      st.valid |= (key < N ? 1u << t : 0u) | (vkey < N ? 1u << (CPT + t) : 0u);
     }
   };
   auto store_tile = [&](const Stage& st, int buf) {
@@ -172,11 +170,17 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
       const int c = tid + t * kThreads;
       const int key = c / CPR;
       const int d0 = (c % CPR) * 8;
-      *reinterpret_cast<Op8*>(Ks[buf] + key * KS + d0) = st.k[t];
+      Op8 kz = st.k[t];
+      if (!((st.valid >> t) & 1u)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kz[e] = T(0.0f);
+      }
+      *reinterpret_cast<Op8*>(Ks[buf] + key * KS + d0) = kz;
       const int vkey = c % kTile;
       const int vd0 = (c / kTile) * 8;
+      const bool vok = (st.valid >> (CPT + t)) & 1u;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) VT[buf][(vd0 + e) * VS + vkey] = st.v[t][e];
+      for (int e = 0; e < 8; ++e) VT[buf][(vd0 + e) * VS + vkey] = vok ? st.v[t][e] : T(0.0f);
     }
   };
 
@@ -223,8 +227,13 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
         tmax = fmaxf(tmax, s[kt][r]);
       }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    // over the 4 key groups g (lanes l ^ 16, l ^ 32): VALU lane swaps
+    {
+      const auto r16s = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+      tmax = fmaxf(__uint_as_float(r16s[0]), __uint_as_float(r16s[1]));
+      const auto r32s = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+      tmax = fmaxf(__uint_as_float(r32s[0]), __uint_as_float(r32s[1]));
+    }
     // The exponent offset m follows the running maximum lazily: it moves
     // only when a logit exceeds it by more than 8 (log2 units), so every
     // p <= 2^8, and the rescaling of the accumulators (MFMA registers) runs
