@@ -119,6 +119,33 @@ def event_times(stream, fn, launches: int):
     return t[len(t) // 2], sum(t) / len(t)
 
 
+def graph_times(stream, fn, per_graph: int = 20, replays: int = 10):
+    """Mean duration (ms) of one call of fn when calls run back to back: fn is
+    captured per_graph times into one HIP graph, and one event pair on the
+    launch stream brackets `replays` replays.  For kernels of a few
+    microseconds a per-launch event pair mostly measures the host's launch
+    latency; this figure is the device time of the kernels."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        g.replay()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(replays):
+            g.replay()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / (replays * per_graph)
+
+
 def timed_loop(stream, fn, steps: int, warmup: int):
     import torch
 
@@ -225,8 +252,11 @@ def bench_radius(args) -> int:
     attn_step = lambda: radius_attention(q, k, v, bits, blocks)  # noqa: E731
     both = lambda: radius_attention(q, k, v, *radius_mask(frac, w.cutoff, gram=gram))  # noqa: E731
     ms, _ = timed_loop(stream, both, args.steps, args.warmup)
-    mask_ms, _ = event_times(stream, mask_step, 50)
-    attn_ms, _ = event_times(stream, attn_step, 50)
+    mask_launch_ms, _ = event_times(stream, mask_step, 50)
+    attn_launch_ms, _ = event_times(stream, attn_step, 50)
+    mask_ms = graph_times(stream, mask_step)
+    attn_ms = graph_times(stream, attn_step)
+    graph_step_ms = graph_times(stream, both)
     flops = w.attention_flops(pairs)
     attn_bytes = 4 * B * H * N * D * 2 + bits.numel() * 4 + blocks.numel()
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
@@ -251,6 +281,9 @@ def bench_radius(args) -> int:
         "config": {"workload": "periodic MOF cells, 6 A cutoff, minimum image, 64-atom tiles", "cells": B,
                    "atoms": N, "heads": H, "head_dim": D, "allowed_pairs": pairs,
                    "mask_ms": round(mask_ms, 5), "attn_ms": round(attn_ms, 5),
+                   "mask_single_launch_ms": round(mask_launch_ms, 5),
+                   "attn_single_launch_ms": round(attn_launch_ms, 5),
+                   "graph_replay_ms_per_step": round(graph_step_ms, 5),
                    "attn_valid_gflop": round(flops / 1e9, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("radius_attn_c4"),

@@ -173,6 +173,25 @@ def test_radius_mask_skewed_cell_without_pruning(cuda):
     np.testing.assert_array_equal(blocks.cpu().numpy(), rblocks)
 
 
+@pytest.mark.parametrize("R,block", [(1, 64), (2, 32), (1, 128)])
+def test_radius_mask_unwrapped_fractional_coords(cuda, R, block):
+    """Fractional coordinates outside [0, 1) with cells whose image bounds
+    are all below 1/2 (the kernel's one-image path): only the offsets
+    {-R..R} are images, as in the reference's search."""
+    print(f"radius_mask unwrapped R={R} block={block}", flush=True)
+    rng = np.random.default_rng(20 + R)
+    B, N, cutoff = 2, 200, 6.0
+    coords = rng.uniform(-2.5, 3.5, (B, N, 3)).astype(np.float32)
+    gram = lattice_y1_to_gram(_cells(B, 7, lo=15.0, hi=30.0))
+    pad = rng.random((B, N)) < 0.1
+    bits, blocks = radius_mask(torch.from_numpy(coords).to(cuda), cutoff, gram=torch.from_numpy(gram).to(cuda),
+                               pad_mask=torch.from_numpy(pad).to(cuda), pbc_radius=R, block=block)
+    rbits, rblocks = oracle_radius_mask(coords, cutoff, gram=gram, pad_mask=pad, pbc_radius=R, block=block)
+    np.testing.assert_array_equal(_bits_u32(bits), rbits)
+    np.testing.assert_array_equal(blocks.cpu().numpy(), rblocks)
+    assert 0.003 < unpack_bits(rbits, N).mean() < 0.2
+
+
 def test_radius_mask_minimum_image_kat(cuda):
     # tests/test_geometry.py:30-39 of the reference: identity cell, distance 0.2
     frac = torch.tensor([[[0.1, 0.0, 0.0], [0.9, 0.0, 0.0]]])

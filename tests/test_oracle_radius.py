@@ -79,6 +79,45 @@ def test_27_images_equal_the_5x5x5_shell_and_are_symmetric():
     np.testing.assert_array_equal(d1, d1.transpose(0, 2, 1))
 
 
+def _nearest_image_mask(frac, gram, cutoff, R, clamp):
+    """The GPU kernel's one-image shortcut, restated in float32 numpy: offset
+    o = -rint(d), clamped to {-R..R} when ``clamp``, evaluated in the oracle's
+    operation order."""
+    f32 = np.float32
+    d = (frac[:, :, None, :] - frac[:, None, :, :]).astype(f32)
+    o = -np.rint(d)
+    if clamp:
+        o = np.clip(o, -R, R)
+    e = (d + o.astype(f32)).astype(f32)
+    G = gram[:, None, None].astype(f32)
+    t = [((G[..., c, 0] * e[..., 0]).astype(f32) + (G[..., c, 1] * e[..., 1]).astype(f32)).astype(f32)
+         + (G[..., c, 2] * e[..., 2]).astype(f32) for c in range(3)]
+    t = [x.astype(f32) for x in t]
+    s = ((e[..., 0] * t[0]).astype(f32) + (e[..., 1] * t[1]).astype(f32)).astype(f32)
+    s = (s + (e[..., 2] * t[2]).astype(f32)).astype(f32)
+    return s <= f32(cutoff) * f32(cutoff)
+
+
+@pytest.mark.parametrize("R", [1, 2])
+def test_nearest_image_shortcut_needs_the_offset_clamp(R):
+    """For cells whose image bounds are all below 1/2 the kernel evaluates one
+    image per pair.  The reference searches only offsets {-R..R}
+    (adapters.py:141-149) and does not wrap fractional coordinates, so the
+    shortcut equals the full search only with the offset clamped to that
+    range; unwrapped coordinates tell the two apart."""
+    rng = np.random.default_rng(20 + R)
+    B, N, cutoff = 2, 200, 6.0
+    frac = rng.uniform(-2.5, 3.5, (B, N, 3)).astype(np.float32)
+    y1 = np.concatenate([np.log(rng.uniform(15, 30, (B, 3))), np.cos(np.deg2rad(rng.uniform(80, 100, (B, 3))))],
+                        axis=1).astype(np.float32)
+    gram = lattice_y1_to_gram(y1)
+    bits, _ = radius_mask(frac, cutoff, gram=gram, pbc_radius=R)
+    full = unpack_bits(bits, N)
+    assert 0.003 < full.mean() < 0.2
+    np.testing.assert_array_equal(_nearest_image_mask(frac, gram, cutoff, R, clamp=True), full)
+    assert (_nearest_image_mask(frac, gram, cutoff, R, clamp=False) != full).sum() > 100
+
+
 @pytest.mark.parametrize("periodic", [False, True])
 def test_bit_mask_and_block_mask_follow_their_definition(periodic):
     rng = np.random.default_rng(3 + periodic)
