@@ -287,7 +287,7 @@ def bench_radius(args) -> int:
                    "attn_valid_gflop": round(flops / 1e9, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("radius_attn_c4"),
-                     "kernel": "mf::rattn::radius_attn_kernel<bf16, 64>", "kernel_ms": round(attn_ms, 5)},
+                     "kernel": "mf::rattn::radius_attn_pair_kernel<bf16, 64, true>", "kernel_ms": round(attn_ms, 5)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

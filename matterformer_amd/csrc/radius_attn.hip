@@ -311,6 +311,304 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
   if (p.lse && g == 0) p.lse[row] = has ? (m + __log2f(l)) * kLn2 : 0.0f;
 }
 
+// ---------------------------------------------------------------------------
+// Two key-tile streams (head_dim 32 and 64): 8 waves per (cell, head,
+// 64-query tile).  Waves w and w + 4 own the 16 queries 16 (w & 3) .. +15;
+// stream e (waves 4e .. 4e + 3) takes the active key tiles of parity e, one
+// per step, each staged in LDS by the 256 threads of its stream.  (The
+// parity, not the position in the active list, picks the stream, so the
+// sums are the same whether or not empty tiles are skipped.)  Per step and wave the work is that of the kernel
+// above; with twice the waves per workgroup and half the steps per wave,
+// four waves share each SIMD.  At the end the two streams' (O, m, l) of a
+// query meet in LDS:
+//   out = (2^(m0 - M) O0 + 2^(m1 - M) O1) / (2^(m0 - M) l0 + 2^(m1 - M) l1).
+// ---------------------------------------------------------------------------
+constexpr int kThreads2 = 512;
+
+// POS: scale > 0.  The running maximum is then taken over the unscaled
+// masked logits (scaling preserves the order) and p = exp2(s scale - m) is
+// one fma per logit.
+template <typename T, int D, bool POS>
+__global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p) {
+  using Op8 = typename Ops<T>::Op8;
+  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T Op4;
+  constexpr int KS = D + 8;         // K row stride in LDS (elements)
+  constexpr int VS = kTile + 8;     // V^T row stride in LDS (elements)
+  constexpr int DK = D / 32;        // K steps of S^T
+  constexpr int ND = D / 16;        // d tiles of O^T
+  constexpr int CPR = D / 8;        // 16-byte chunks per row
+  constexpr int CPT = kTile * CPR / 256;  // chunks per thread per tile (256 threads per stream)
+  static_assert(CPT >= 1 && (kTile * CPR) % 256 == 0, "staging shape");
+  constexpr int CW = ND * 4 + 2;    // floats per lane in the combine: O^T, m, l
+  static_assert(4 * 64 * CW * 4 <= int(sizeof(T)) * 2 * 2 * kTile * KS, "combine area");
+
+  __shared__ __attribute__((aligned(16))) T Ks[2][2][kTile * KS];  // [buffer][stream]
+  __shared__ __attribute__((aligned(16))) T VT[2][2][D * VS];
+  __shared__ int s_tiles[2][kMaxTiles / 2];  // active tiles of each parity, in order
+  __shared__ int s_ntiles[2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int kh = wave >> 2, qw = wave & 3;  // key stream, query group
+  const int ht = tid & 255;                 // thread index within the stream
+  const int G = gridDim.x;
+  const int unit = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);  // XCD-aware order
+  if (unit >= p.units) return;  // grid padding (whole workgroup)
+  const int NQT = p.NB;
+  const int qt = unit % NQT;
+  const int h = (unit / NQT) % p.H;
+  const int b = unit / (NQT * p.H);
+  const int N = p.N;
+  const size_t bh = size_t(b) * p.H + h;
+  const T* gq = static_cast<const T*>(p.q) + bh * N * D;
+  const T* gk = static_cast<const T*>(p.k) + bh * N * D;
+  const T* gv = static_cast<const T*>(p.v) + bh * N * D;
+
+  if (wave < 2) {
+    // wave e lists the active tiles of parity e: lane l looks at tile 2 (base + l) + e
+    const uint8_t* brow = p.block_mask ? p.block_mask + (size_t(b) * p.NB + qt) * p.NB : nullptr;
+    int n = 0;
+    for (int base = 0; 2 * base < p.NB; base += 64) {
+      const int jt = 2 * (base + lane) + wave;
+      const bool on = jt < p.NB && (!brow || brow[jt] != 0);
+      const uint64_t bal = __ballot(on);
+      if (on) s_tiles[wave][n + __popcll(bal & ((1ull << lane) - 1))] = jt;
+      n += __popcll(bal);
+    }
+    if (lane == 0) s_ntiles[wave] = n;
+  }
+
+  const int qi = qt * kTile + qw * 16 + r16;
+  const bool q_in = qi < N;
+  Op8 qb[DK];
+#pragma unroll
+  for (int kk = 0; kk < DK; ++kk)
+    qb[kk] = *reinterpret_cast<const Op8*>(gq + size_t(min(qi, N - 1)) * D + 32 * kk + 8 * g);
+  const uint32_t* qbits = p.bits + size_t(b) * N * p.W + size_t(q_in ? qi : 0) * p.W;
+
+  mf_f32x4 acc[ND];
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) acc[nd] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+
+  __syncthreads();
+  const int ntiles = s_ntiles[kh];  // this stream's
+  const int nsteps = max(s_ntiles[0], s_ntiles[1]);
+  const int* tiles = s_tiles[kh];
+
+  // register staging of this stream's tile of a step (as in the kernel above;
+  // branch-free loads, rows past N zeroed where stored)
+  // chunk t of a thread: K row c / CPR, columns 8 (c % CPR); V row c % 64,
+  // columns 8 (c / 64) (c = ht + 256 t); offsets within a tile, once
+  int krow[CPT], kgo[CPT], vrow_[CPT], vgo[CPT], kso[CPT], vso[CPT];
+#pragma unroll
+  for (int t = 0; t < CPT; ++t) {
+    const int c = ht + t * 256;
+    krow[t] = c / CPR;
+    kgo[t] = krow[t] * D + (c % CPR) * 8;
+    vrow_[t] = c % kTile;
+    vgo[t] = vrow_[t] * D + (c / kTile) * 8;
+    kso[t] = krow[t] * KS + (c % CPR) * 8;
+    vso[t] = (c / kTile) * 8 * VS + vrow_[t];
+  }
+  struct Stage {
+    Op8 k[CPT], v[CPT];
+    uint32_t m0, m1;
+    int key0;   // first key of the tile
+    bool full;  // every key of the tile is < N (uniform)
+  };
+  auto load_tile = [&](int jt, Stage& st) {
+    const int w0 = 2 * jt;
+    st.m0 = qbits[min(w0, p.W - 1)];
+    st.m1 = qbits[min(w0 + 1, p.W - 1)];
+    st.m0 = (q_in && w0 < p.W) ? st.m0 : 0u;
+    st.m1 = (q_in && w0 + 1 < p.W) ? st.m1 : 0u;
+    const int key0 = jt * kTile;
+    st.key0 = key0;
+    st.full = key0 + kTile <= N;
+    const T* kb = gk + size_t(key0) * D;
+    const T* vb = gv + size_t(key0) * D;
+    if (st.full) {
+#pragma unroll
+      for (int t = 0; t < CPT; ++t) {
+        st.k[t] = *reinterpret_cast<const Op8*>(kb + kgo[t]);
+        st.v[t] = *reinterpret_cast<const Op8*>(vb + vgo[t]);
+      }
+    } else {
+      // rows past N read row N - 1 (zeroed when stored)
+#pragma unroll
+      for (int t = 0; t < CPT; ++t) {
+        st.k[t] = *reinterpret_cast<const Op8*>(gk + size_t(min(key0 + krow[t], N - 1)) * D + (kgo[t] - krow[t] * D));
+        st.v[t] = *reinterpret_cast<const Op8*>(gv + size_t(min(key0 + vrow_[t], N - 1)) * D + (vgo[t] - vrow_[t] * D));
+      }
+    }
+  };
+  auto store_tile = [&](const Stage& st, int buf) {
+    T* kd = Ks[buf][kh];
+    T* vd = VT[buf][kh];
+    if (st.full) {
+#pragma unroll
+      for (int t = 0; t < CPT; ++t) {
+        *reinterpret_cast<Op8*>(kd + kso[t]) = st.k[t];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vd[vso[t] + e * VS] = st.v[t][e];
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < CPT; ++t) {
+        Op8 kz = st.k[t];
+        if (st.key0 + krow[t] >= N) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kz[e] = T(0.0f);
+        }
+        *reinterpret_cast<Op8*>(kd + kso[t]) = kz;
+        const bool vok = st.key0 + vrow_[t] < N;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vd[vso[t] + e * VS] = vok ? st.v[t][e] : T(0.0f);
+      }
+    }
+  };
+
+  // Step s computes the stream's tile s from buffer s & 1.  The stage holds
+  // the loads of step s + 1 (issued after the previous step's store) and
+  // goes to the other buffer at the end of the step.
+  Stage st;
+  uint32_t mw0 = 0u, mw1 = 0u;
+  if (nsteps > 0) {
+    if (0 < ntiles) {
+      load_tile(tiles[0], st);
+      store_tile(st, 0);
+      mw0 = st.m0;
+      mw1 = st.m1;
+    }
+    if (1 < ntiles) load_tile(tiles[1], st);
+    __syncthreads();
+  }
+  for (int s = 0; s < nsteps; ++s) {
+    const int buf = s & 1;
+    if (s < ntiles) {
+      const T* Kt = Ks[buf][kh];
+      const T* VTt = VT[buf][kh];
+      float sv[4][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        mf_f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < DK; ++kk) {
+          const Op8 a = *reinterpret_cast<const Op8*>(Kt + (16 * kt + r16) * KS + 32 * kk + 8 * g);
+          c = Ops<T>::mma(a, qb[kk], c);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sv[kt][r] = c[r];
+      }
+      const float sc = p.scale_log2;
+      float tmax = -INFINITY;
+      // key 16 kt + 4 g + r is bit 16 (kt & 1) + r of (word kt / 2) >> 4 g
+      const uint32_t wa = mw0 >> (4 * g), wb = mw1 >> (4 * g);
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool allowed = (((kt < 2 ? wa : wb) >> (16 * (kt & 1) + r)) & 1u) != 0u;
+          if constexpr (POS) sv[kt][r] = allowed ? sv[kt][r] : -INFINITY;
+          else sv[kt][r] = allowed ? sv[kt][r] * sc : -INFINITY;
+          tmax = fmaxf(tmax, sv[kt][r]);
+        }
+      }
+      {
+        const auto r16s = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+        tmax = fmaxf(__uint_as_float(r16s[0]), __uint_as_float(r16s[1]));
+        const auto r32s = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+        tmax = fmaxf(__uint_as_float(r32s[0]), __uint_as_float(r32s[1]));
+      }
+      if constexpr (POS) tmax *= sc;  // -inf stays -inf
+      // lazy offset, as in the kernel above
+      const bool grow = tmax > m + 8.0f;
+      if (__ballot(grow) != 0ull) {
+        const float m_set = grow ? tmax : m;
+        const float alpha = grow ? fast_exp2(m - m_set) : 1.0f;
+        l *= alpha;
+#pragma unroll
+        for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[nd][r] *= alpha;
+        m = m_set;
+      }
+      const float m_off = m == -INFINITY ? 0.0f : m;
+      float psum = 0.0f;
+      Op8 pb[2];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = POS ? fast_exp2(fmaf(sv[kt][r], sc, -m_off)) : fast_exp2(sv[kt][r] - m_off);
+          psum += pv;
+          pb[kt >> 1][(kt & 1) * 4 + r] = T(pv);
+        }
+      }
+      l += psum;
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          const T* vrow = VTt + (16 * nd + r16) * VS + 32 * pr + 4 * g;
+          const Op4 lo = *reinterpret_cast<const Op4*>(vrow);
+          const Op4 hi = *reinterpret_cast<const Op4*>(vrow + 16);
+          const Op8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[nd] = Ops<T>::mma(a, pb[pr], acc[nd]);
+        }
+      }
+    }
+    if (s + 1 < ntiles) {
+      store_tile(st, buf ^ 1);
+      mw0 = st.m0;
+      mw1 = st.m1;
+    }
+    __syncthreads();
+    if (s + 2 < ntiles) load_tile(tiles[s + 2], st);
+  }
+
+  // combine the streams: l summed over the 4 key groups g first
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  float* cmb = reinterpret_cast<float*>(&Ks[0][0][0]);  // [query group][lane][CW] (after the last barrier)
+  if (kh == 1) {
+    float* c = cmb + (qw * 64 + lane) * CW;
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) c[nd * 4 + r] = acc[nd][r];
+    c[ND * 4] = m;
+    c[ND * 4 + 1] = l;
+  }
+  __syncthreads();
+  if (kh == 1 || !q_in) return;
+  const float* c = cmb + (qw * 64 + lane) * CW;
+  const float m1 = c[ND * 4], l1 = c[ND * 4 + 1];
+  const float M = fmaxf(m, m1);
+  const float a0 = M == -INFINITY ? 0.0f : fast_exp2(m - M);  // 0 for a stream without allowed keys
+  const float a1 = M == -INFINITY ? 0.0f : fast_exp2(m1 - M);
+  const float L = a0 * l + a1 * l1;
+  const bool has = L > 0.0f;
+  const float inv = has ? 1.0f / L : 0.0f;
+  const size_t row = bh * N + qi;
+#pragma unroll
+  for (int nd = 0; nd < ND; ++nd) {
+    const int d0 = 16 * nd + 4 * g;
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = (a0 * acc[nd][r] + a1 * c[nd * 4 + r]) * inv;
+    if (p.out) {
+      Op4 ov;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ov[r] = T(o[r]);
+      *reinterpret_cast<Op4*>(static_cast<T*>(p.out) + row * D + d0) = ov;
+    }
+    if (p.out_f32) *reinterpret_cast<float4*>(p.out_f32 + row * D + d0) = float4{o[0], o[1], o[2], o[3]};
+  }
+  if (p.lse && g == 0) p.lse[row] = has ? (M + __log2f(L)) * kLn2 : 0.0f;
+}
+
 template <typename T, int D>
 int launch(const Params& p, hipStream_t stream) {
   const dim3 grid((p.units + 7) / 8 * 8);
@@ -319,10 +617,21 @@ int launch(const Params& p, hipStream_t stream) {
   return MF_OK;
 }
 
+template <typename T, int D>
+int launch_pair(const Params& p, hipStream_t stream) {
+  const dim3 grid((p.units + 7) / 8 * 8);
+  if (p.scale_log2 > 0.0f)
+    hipLaunchKernelGGL((radius_attn_pair_kernel<T, D, true>), grid, dim3(kThreads2), 0, stream, p);
+  else
+    hipLaunchKernelGGL((radius_attn_pair_kernel<T, D, false>), grid, dim3(kThreads2), 0, stream, p);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
+
 template <typename T>
 int dispatch_dim(const Params& p, int D, hipStream_t stream) {
-  if (D == 32) return launch<T, 32>(p, stream);
-  if (D == 64) return launch<T, 64>(p, stream);
+  if (D == 32) return launch_pair<T, 32>(p, stream);
+  if (D == 64) return launch_pair<T, 64>(p, stream);
   return launch<T, 128>(p, stream);
 }
 

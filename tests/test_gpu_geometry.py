@@ -256,6 +256,7 @@ ATTN_CASES = [
     (2, 2, 130, 64, torch.float16, False, 0),
     (1, 4, 200, 128, torch.bfloat16, True, 5),
     (2, 2, 64, 32, torch.float16, True, 0),
+    (3, 2, 97, 32, torch.float16, True, 2),
 ]
 
 
