@@ -139,15 +139,17 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
   // for a tile's loads counts only the loads issued after them.
   struct Stage {
     Op8 k[CPT], v[CPT];
-    uint32_t m0, m1;
-    uint32_t valid;  // bit t: K chunk t is a real key; bit CPT + t: V chunk t
+    uint32_t m0, m1;  // mask words as loaded
+    uint32_t mok;     // bit 0 / 1: m0 / m1 are real words of a real query
+    uint32_t valid;   // bit t: K chunk t is a real key; bit CPT + t: V chunk t
   };
   auto load_tile = [&](int jt, Stage& st) {
+    // the words are selected when used (a step later), so that nothing
+    // waits for these loads now
     const int w0 = 2 * jt;
     st.m0 = qbits[min(w0, p.W - 1)];
     st.m1 = qbits[min(w0 + 1, p.W - 1)];
-    st.m0 = (q_in && w0 < p.W) ? st.m0 : 0u;
-    st.m1 = (q_in && w0 + 1 < p.W) ? st.m1 : 0u;
+    st.mok = (q_in && w0 < p.W ? 1u : 0u) | (q_in && w0 + 1 < p.W ? 2u : 0u);
     st.valid = 0u;
 #pragma unroll
     for (int t = 0; t < CPT; ++t) {
@@ -193,8 +195,8 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
     load_tile(s_tiles[0], sa);
     if (ntiles > 1) load_tile(s_tiles[1], sb);
     store_tile(sa, 0);
-    mw0 = sa.m0;
-    mw1 = sa.m1;
+    mw0 = (sa.mok & 1u) ? sa.m0 : 0u;
+    mw1 = (sa.mok & 2u) ? sa.m1 : 0u;
     __syncthreads();
   }
   auto step = [&](int it, Stage& freed, const Stage& next) {
@@ -279,8 +281,8 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
     }
     if (it + 1 < ntiles) store_tile(next, buf ^ 1);
     __syncthreads();
-    mw0 = next.m0;
-    mw1 = next.m1;
+    mw0 = (next.mok & 1u) ? next.m0 : 0u;
+    mw1 = (next.mok & 2u) ? next.m1 : 0u;
   };
   for (int it = 0; it < ntiles; it += 2) {
     step(it, sa, sb);
@@ -413,16 +415,18 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
   }
   struct Stage {
     Op8 k[CPT], v[CPT];
-    uint32_t m0, m1;
-    int key0;   // first key of the tile
-    bool full;  // every key of the tile is < N (uniform)
+    uint32_t m0, m1;  // mask words as loaded
+    uint32_t mok;     // bit 0 / 1: m0 / m1 are real words of a real query
+    int key0;         // first key of the tile
+    bool full;        // every key of the tile is < N (uniform)
   };
   auto load_tile = [&](int jt, Stage& st) {
+    // the words are selected when used (a step later), so that nothing
+    // waits for these loads now
     const int w0 = 2 * jt;
     st.m0 = qbits[min(w0, p.W - 1)];
     st.m1 = qbits[min(w0 + 1, p.W - 1)];
-    st.m0 = (q_in && w0 < p.W) ? st.m0 : 0u;
-    st.m1 = (q_in && w0 + 1 < p.W) ? st.m1 : 0u;
+    st.mok = (q_in && w0 < p.W ? 1u : 0u) | (q_in && w0 + 1 < p.W ? 2u : 0u);
     const int key0 = jt * kTile;
     st.key0 = key0;
     st.full = key0 + kTile <= N;
@@ -478,8 +482,8 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
     if (0 < ntiles) {
       load_tile(tiles[0], st);
       store_tile(st, 0);
-      mw0 = st.m0;
-      mw1 = st.m1;
+      mw0 = (st.mok & 1u) ? st.m0 : 0u;
+      mw1 = (st.mok & 2u) ? st.m1 : 0u;
     }
     if (1 < ntiles) load_tile(tiles[1], st);
     __syncthreads();
@@ -561,8 +565,8 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
     }
     if (s + 1 < ntiles) {
       store_tile(st, buf ^ 1);
-      mw0 = st.m0;
-      mw1 = st.m1;
+      mw0 = (st.mok & 1u) ? st.m0 : 0u;
+      mw1 = (st.mok & 2u) ? st.m1 : 0u;
     }
     __syncthreads();
     if (s + 2 < ntiles) load_tile(tiles[s + 2], st);
