@@ -48,10 +48,17 @@ struct Params {
   int B, N, K, exclude_self;
 };
 
+// One 64-bit compare per comparator: the maximum is the other key,
+// a ^ b ^ min(a, b) (exact for equal keys too), so the compiler does not
+// expand a separate umax with a second compare.
 __device__ __forceinline__ void cmp_swap(uint64_t& lo, uint64_t& hi) {
   const uint64_t a = lo, b = hi;
-  lo = a < b ? a : b;
-  hi = a < b ? b : a;
+  const uint64_t mn = a < b ? a : b;
+  // v_bitop3_b32 with truth table 0x96 is the 3-input XOR
+  const uint32_t h0 = __builtin_amdgcn_bitop3_b32(uint32_t(a), uint32_t(b), uint32_t(mn), 0x96);
+  const uint32_t h1 = __builtin_amdgcn_bitop3_b32(uint32_t(a >> 32), uint32_t(b >> 32), uint32_t(mn >> 32), 0x96);
+  hi = (uint64_t(h1) << 32) | h0;
+  lo = mn;
 }
 
 template <int KMAX>
