@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 3
+#define MF_ABI_VERSION 4
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -111,6 +111,30 @@ typedef struct mf_simplicial_fwd_args {
   int32_t head_dim; /* 1..128 */
   int32_t dtype;     /* mf_dtype */
   int32_t precision; /* mf_precision */
+  /* Optional logit and message terms; each group is absent when its first
+   * pointer is NULL.  Semantics of SimplicialFactorizedBias,
+   * SimplicialLowRankAngleResidual and SimplicialLowRankMessageResidual
+   * (simplicial_attention.py:18-104,330-337; triton_simplicial_attention.py:
+   * 244-279,305-326), with (j,k) valid as above:
+   *   factorized bias:  S[j,k] += gate_i * ((u[i,j] + v[i,k]) + w[j,k])
+   *   low-rank angle:   S[j,k] += angle_gate_i * Ra^-1/2 * sum_r AL[i,j,r] AR[i,k,r]
+   *   low-rank message: out_i  += sum_r c_r basis[h,r,:],
+   *                     c_r = Rm^-1/2 * sum_{j,k} P[j,k] ML[i,j,r] MR[i,k,r]
+   * (P the normalised softmax weights).  Calls with any of them run the
+   * general kernel. */
+  const void* bias_u;     /* [B*H, N, N] in bias_dtype                     */
+  const void* bias_v;     /* [B*H, N, N]                                   */
+  const void* bias_w;     /* [B*H, N, N]                                   */
+  const void* bias_gate;  /* [B*H, N]                                      */
+  int32_t bias_dtype;     /* mf_dtype of the four bias tensors             */
+  int32_t angle_rank;     /* Ra, 1..64 when angle_left != NULL            */
+  const float* angle_left;   /* [B*H, N, N, Ra] fp32                       */
+  const float* angle_right;  /* [B*H, N, N, Ra] fp32                       */
+  const float* angle_gate;   /* [B*H, N] fp32                              */
+  const float* message_left;   /* [B*H, N, N, Rm] fp32                     */
+  const float* message_right;  /* [B*H, N, N, Rm] fp32                     */
+  const float* message_basis;  /* [H, Rm, D] fp32                          */
+  int32_t message_rank;        /* Rm, 1..64 when message_left != NULL     */
 } mf_simplicial_fwd_args;
 
 int mf_simplicial_fwd(const mf_simplicial_fwd_args* args, void* stream);

@@ -42,7 +42,7 @@ EXPORTED_SYMBOLS = (
     "mf_radius_attn",
 )
 
-EXPECTED_ABI_VERSION = 3
+EXPECTED_ABI_VERSION = 4
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -72,6 +72,19 @@ class MfSimplicialFwdArgs(ctypes.Structure):
         ("head_dim", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
         ("precision", ctypes.c_int32),
+        ("bias_u", ctypes.c_void_p),
+        ("bias_v", ctypes.c_void_p),
+        ("bias_w", ctypes.c_void_p),
+        ("bias_gate", ctypes.c_void_p),
+        ("bias_dtype", ctypes.c_int32),
+        ("angle_rank", ctypes.c_int32),
+        ("angle_left", ctypes.c_void_p),
+        ("angle_right", ctypes.c_void_p),
+        ("angle_gate", ctypes.c_void_p),
+        ("message_left", ctypes.c_void_p),
+        ("message_right", ctypes.c_void_p),
+        ("message_basis", ctypes.c_void_p),
+        ("message_rank", ctypes.c_int32),
     ]
 
 
@@ -208,6 +221,11 @@ def current_stream(device: torch.device) -> int:
 
 
 _WORKSPACES: dict = {}
+# Workspaces of calls recorded into HIP graphs.  A captured kernel keeps the
+# address it was recorded with, so each captured call gets a buffer of its
+# own that must outlive every replay: they are kept here until the process
+# ends (a few hundred bytes per captured call on the pair-kernel path).
+_CAPTURED_WORKSPACES: list = []
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
@@ -215,12 +233,23 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
     hands out 512-byte aligned blocks).
 
     mf_simplicial_fwd's workspace holds a claim counter that must be zero
-    before the first call and that every call leaves zero, so one buffer is
-    kept per (device, stream) -- calls on one stream are ordered -- and
-    zero-filled whenever it is allocated or grown."""
+    before the first call and that every call leaves zero.  Eager calls keep
+    one buffer per (device, stream) -- calls on one stream are ordered -- and
+    zero-fill it whenever it is allocated or grown.
+
+    A call made while the current stream is capturing a HIP graph gets a
+    fresh buffer instead, zeroed by a fill kernel recorded into the same
+    graph (so every replay starts from zero), which no eager call and no
+    other captured call shares.  One graph replayed concurrently with itself
+    on two streams would still share its own buffer; replays of one graph
+    must be ordered."""
     if nbytes == 0:
         return None
     dev = torch.device(device)
+    if torch.cuda.is_current_stream_capturing():
+        buf = torch.zeros(int(nbytes), dtype=torch.uint8, device=dev)
+        _CAPTURED_WORKSPACES.append(buf)
+        return buf
     key = (dev.index if dev.index is not None else torch.cuda.current_device(),
            torch.cuda.current_stream(dev).cuda_stream)
     buf = _WORKSPACES.get(key)

@@ -591,11 +591,20 @@ __device__ void zero_padded_rows(const Params& p, int worker, int workers) {
     const long long bh = row / p.N;
     const int i = int(row - bh * p.N);
     if (p.qv[(bh / p.H) * p.N + i]) continue;
-    if (p.out) reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + row * p.D)[c] = uint4{0u, 0u, 0u, 0u};
-    if (p.out_f32) {
-      float4* o = reinterpret_cast<float4*>(p.out_f32 + row * p.D);
-      o[2 * c] = float4{0.f, 0.f, 0.f, 0.f};
-      o[2 * c + 1] = float4{0.f, 0.f, 0.f, 0.f};
+    if (p.vec_ok) {
+      if (p.out) reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + row * p.D)[c] = uint4{0u, 0u, 0u, 0u};
+      if (p.out_f32) {
+        float4* o = reinterpret_cast<float4*>(p.out_f32 + row * p.D);
+        o[2 * c] = float4{0.f, 0.f, 0.f, 0.f};
+        o[2 * c + 1] = float4{0.f, 0.f, 0.f, 0.f};
+      }
+    } else {
+      // outputs not 16-byte aligned (operands are, on this path): element stores
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (p.out) static_cast<uint16_t*>(p.out)[row * p.D + 8 * c + e] = 0;
+        if (p.out_f32) p.out_f32[row * p.D + 8 * c + e] = 0.0f;
+      }
     }
     if (c == 0 && p.lse) p.lse[row] = 0.0f;
   }

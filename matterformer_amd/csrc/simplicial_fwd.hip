@@ -36,6 +36,35 @@ namespace simplicial {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 256 between rescales
+constexpr int kMaxRank = 64;           // low-rank angle / message terms
+constexpr int kRankTiles = kMaxRank / 16;
+constexpr int kRankSteps = kMaxRank / 4;
+
+// Optional logit / message terms (any pointer group may be absent).
+// Row indices: tensors indexed [.., i, j] use (bh*N + i)*N + j.
+struct Extras {
+  const void* u;     // [BH, N, N] factorized bias, element type bias_dtype
+  const void* v;
+  const void* w;
+  const void* gate;  // [BH, N]
+  int bias_dtype;
+  const float* al;   // [BH, N, N, Ra] angle left / right, [BH, N] gate
+  const float* ar;
+  const float* ag;
+  int a_rank;
+  float a_scale;     // Ra^-1/2
+  const float* ml;   // [BH, N, N, Rm] message left / right, [H, Rm, D] basis
+  const float* mr;
+  const float* mb;
+  int m_rank;
+  float m_scale;     // Rm^-1/2
+};
+
+__device__ __forceinline__ float load_any(const void* p, size_t idx, int dtype) {
+  if (dtype == MF_DTYPE_F32) return static_cast<const float*>(p)[idx];
+  if (dtype == MF_DTYPE_BF16) return static_cast<float>(static_cast<const __bf16*>(p)[idx]);
+  return static_cast<float>(static_cast<const _Float16*>(p)[idx]);
+}
 
 struct Params {
   const void* q;
@@ -55,6 +84,7 @@ struct Params {
   int vec_ok;       // rows are 16-byte aligned and D*sizeof(T) % 16 == 0
   int min_keys;     // only molecules with more keys than this are processed
   int zero_rows;    // write the zero rows of invalid queries
+  Extras x;         // used by the EXT instantiations only
 };
 
 // LDS geometry shared by host (sizing) and device (carving).
@@ -98,9 +128,30 @@ __device__ __forceinline__ void load_row_chunk16(T* dst, const T* row, int e0, i
   }
 }
 
-template <typename T, int DP>
-__global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
+// EXT instantiations add the optional terms of Params::x:
+//  * factorized bias and low-rank angle are added to each S^T tile right
+//    after GEMM1 (u per lane row, v and w per key; the angle tile is its own
+//    fp32 MFMA chain C[k][j] = sum_r AR[k][r] AL[j][r], the layout of S^T);
+//  * the message term runs a third MFMA chain beside GEMM2,
+//    CM[r][j] += sum_k MR^T[r][k] P[j][k], folded as c_r += ML[j][r] CM[r][j]
+//    like the value path, rescaled with it, and added as c @ basis at the end.
+// All of them read their tensors from global memory (L2): they are per query
+// (u, v, the rank factors) or per (b, h) (w), not shared across work items.
+// EXT: 0 = no optional terms, 1 = bias / angle, 2 = bias / angle / message.
+// The message term holds a rank-tile accumulator per lane beside the value
+// path; EXT == 2 runs 4 waves per workgroup so that each wave may use the
+// whole register file (architectural + accumulation registers).
+template <int EXT>
+struct Waves {
+  static constexpr int kCount = EXT == 2 ? 4 : kWaves;
+  static constexpr int kThreadCount = kCount * 64;
+};
+
+template <typename T, int DP, int EXT>
+__global__ void __launch_bounds__(Waves<EXT>::kThreadCount) simplicial_fwd_kernel(Params p) {
   using E = Elem<T>;
+  constexpr int kWaves = Waves<EXT>::kCount;
+  constexpr int kThreads = Waves<EXT>::kThreadCount;
   using L = Layout<T, DP>;
   constexpr int KS = L::KS;
   constexpr int NMT = DP / 16;            // 16-wide d tiles of GEMM2 / outputs
@@ -301,11 +352,42 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[mt][r] = 0.0f;
 
+      // optional terms: gates in log2 units, message accumulators
+      const bool has_bias = EXT && p.x.u != nullptr;
+      const bool has_angle = EXT && p.x.al != nullptr;
+      const bool has_msg = EXT == 2 && p.x.ml != nullptr;
+      const int a_rank = has_angle ? p.x.a_rank : 0;
+      const int m_rank = has_msg ? p.x.m_rank : 0;
+      const int a_steps = (a_rank + 3) >> 2;   // 4-wide K steps of the angle MFMA
+      const int m_tiles = (m_rank + 15) >> 4;  // 16-row tiles of the message MFMA
+      float gq = 0.0f, ga = 0.0f;
+      if (has_bias) gq = load_any(p.x.gate, row_off, p.x.bias_dtype) * kLog2e;
+      if (has_angle) ga = p.x.ag[row_off] * p.x.a_scale * kLog2e;
+      float macc[EXT == 2 ? kRankTiles : 1][4];
+#pragma unroll
+      for (int rt = 0; rt < (EXT == 2 ? kRankTiles : 1); ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) macc[rt][r] = 0.0f;
+
       const int njt = ceil_div(nk, 16);
       const int nkc = ceil_div(nk, 64);
       for (int jt = 0; jt < njt; ++jt) {
         const int j = jt * 16 + r16;
         const bool row_ok = j < nk;
+        const int jo = row_ok ? kidx[j] : 0;  // original token index of row j
+
+        // per-row terms of this lane's row j
+        float uj = 0.0f;
+        mf_f32x4 mtacc[EXT == 2 ? kRankTiles : 1];
+        if constexpr (EXT) {
+          if (has_bias && row_ok) uj = load_any(p.x.u, row_off * N + jo, p.x.bias_dtype);
+        }
+        if constexpr (EXT == 2) {
+#pragma unroll
+          for (int rt = 0; rt < kRankTiles; ++rt) mtacc[rt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        // angle B operand source: AL[i][jo][4c + g] (read per use, from L1)
+        const float* alrow = EXT && has_angle ? p.x.al + (row_off * N + jo) * a_rank : nullptr;
 
         // GEMM1 B operand: (q_i (.) k1_j) rounded to the operand type
         typename E::Operand b1[NCH];
@@ -348,6 +430,43 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
             }
           }
 
+          if constexpr (EXT) {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+              if (kt >= nkt) continue;
+              if (has_angle) {
+                // C[k][j] = sum_r AR[i][k][r] AL[i][j][r]: lane supplies A[k = r16][r = 4c + g]
+                const int keyA = kbase + kt * 16 + r16;
+                const int koA = keyA < nk ? kidx[keyA] : 0;
+                const float* arow = p.x.ar + (row_off * N + koA) * a_rank;
+                mf_f32x4 at = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < kRankSteps; ++c) {
+                  if (c < a_steps) {
+                    const int rr = 4 * c + g;
+                    const float a = (keyA < nk && rr < a_rank) ? arow[rr] : 0.0f;
+                    const float b = (row_ok && rr < a_rank) ? alrow[rr] : 0.0f;
+                    at = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, at, 0, 0, 0);
+                  }
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sv[kt][r] = fmaf(ga, at[r], sv[kt][r]);
+              }
+              if (has_bias && row_ok) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const int key = kbase + kt * 16 + 4 * g + r;
+                  if (key < nk) {
+                    const int ko = kidx[key];
+                    const float vk = load_any(p.x.v, row_off * N + ko, p.x.bias_dtype);
+                    const float wk = load_any(p.x.w, (size_t(bh) * N + jo) * N + ko, p.x.bias_dtype);
+                    sv[kt][r] = fmaf(gq, (uj + vk) + wk, sv[kt][r]);
+                  }
+                }
+              }
+            }
+          }
+
           // mask + lane max
           const bool edge = has_pv || (jt * 16 + 16 > nk) || (kbase + nkt * 16 > nk);
           float mloc = -INFINITY;
@@ -383,6 +502,17 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
                 tacc[mt][r] *= alpha;
               }
             }
+            if constexpr (EXT == 2) {
+              if (has_msg) {
+#pragma unroll
+                for (int rt = 0; rt < kRankTiles; ++rt)
+#pragma unroll
+                  for (int r = 0; r < 4; ++r) {
+                    macc[rt][r] *= alpha;
+                    mtacc[rt][r] *= alpha;
+                  }
+              }
+            }
             M = Mn;
           }
           if (M == -INFINITY) continue;  // nothing valid seen yet
@@ -396,6 +526,30 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
               sv[kt][r] = pe;
               lsum += pe;
             }
+
+          // message: CM[r][j] += sum_k MR[i][k][r] P[j][k] (fp32 MFMA; lane
+          // supplies A[r = 16 rt + r16][k] for key 4g + rs of tile kt)
+          if constexpr (EXT == 2) {
+            if (has_msg) {
+#pragma unroll
+              for (int rt = 0; rt < kRankTiles; ++rt) {
+                if (rt >= m_tiles) continue;
+                const int rr = 16 * rt + r16;
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt) {
+                  if (kt >= nkt) continue;
+#pragma unroll
+                  for (int rs = 0; rs < 4; ++rs) {
+                    const int key = kbase + kt * 16 + 4 * g + rs;
+                    const float a = (key < nk && rr < m_rank) ? p.x.mr[(row_off * N + kidx[key]) * m_rank + rr] : 0.0f;
+                    mtacc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, sv[kt][rs], mtacc[rt], 0, 0, 0);
+                  }
+                }
+                // one rank tile's 16 loads in flight at a time (keeps them out of spill range)
+                __builtin_amdgcn_sched_barrier(0);
+              }
+            }
+          }
 
           // GEMM2: C2[d][j] += sum_k V2^T[d][k] P[j][k]
           if constexpr (KPL == 8) {
@@ -450,6 +604,19 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
               if (d < D) acc[mt][r] += E::to_f32(vrow[d]) * tacc[mt][r];
             }
         }
+        // message: c_r += ML[i][j][r] CM[r][j]; lane holds r = 16 rt + 4g + rr of row j
+        if constexpr (EXT == 2) {
+          if (has_msg && row_ok) {
+            const float* lrow = p.x.ml + (row_off * N + jo) * m_rank;
+#pragma unroll
+            for (int rt = 0; rt < kRankTiles; ++rt)
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) {
+                const int rank = 16 * rt + 4 * g + rr;
+                if (rt < m_tiles && rank < m_rank) macc[rt][rr] += lrow[rank] * mtacc[rt][rr];
+              }
+          }
+        }
       }
 
       // ---- reduce and write the query row ----
@@ -460,6 +627,40 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
         for (int r = 0; r < 4; ++r) acc[mt][r] = group16_sum(acc[mt][r]);
       const bool has_mass = lsum_all > 0.0f;
       const float inv = has_mass ? 1.0f / lsum_all : 0.0f;
+      // message term out[d] += sum_r c_r basis[h][r][d], c_r = Rm^-1/2 * (sum_j CM) / l:
+      // after the row-group sum, every lane of group (r & 15) >> 2 holds c_r's sum
+      float msg_out[NMT];
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) msg_out[mt] = 0.0f;
+      if constexpr (EXT == 2) {
+        if (has_msg) {
+#pragma unroll
+          for (int rt = 0; rt < kRankTiles; ++rt)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) macc[rt][rr] = group16_sum(macc[rt][rr]);
+          const float* basis = p.x.mb + size_t(bh % H) * m_rank * D;
+          const float cs = p.x.m_scale * inv;
+#pragma unroll
+          for (int rt = 0; rt < kRankTiles; ++rt) {
+            if (rt >= m_tiles) continue;
+#pragma unroll
+            for (int gs = 0; gs < 4; ++gs)
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) {
+                const int r = 16 * rt + 4 * gs + rr;
+                const float c = __shfl(macc[rt][rr], 16 * gs, 64) * cs;
+                if (r < m_rank) {
+#pragma unroll
+                  for (int mt = 0; mt < NMT; ++mt) {
+                    const int d = mt * 16 + 4 * g + (r16 & 3);
+                    if ((mt & 3) == (r16 >> 2) && d < D)
+                      msg_out[mt] = fmaf(c, basis[size_t(r) * D + d], msg_out[mt]);
+                  }
+                }
+              }
+          }
+        }
+      }
       // lane (g, r16) writes d = mt*16 + 4g + (r16&3) for mt with (mt&3) == r16>>2
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) {
@@ -470,7 +671,7 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
           if ((r16 & 3) == r) val = acc[mt][r];
         const int d = mt * 16 + 4 * g + (r16 & 3);
         if (d < D) {
-          const float o = val * inv;
+          const float o = val * inv + msg_out[mt];
           if (p.out) static_cast<T*>(p.out)[row_off * D + d] = E::from_f32(o);
           if (p.out_f32) p.out_f32[row_off * D + d] = o;
         }
@@ -482,9 +683,10 @@ __global__ void __launch_bounds__(kThreads) simplicial_fwd_kernel(Params p) {
   }
 }
 
-template <typename T, int DP>
+template <typename T, int DP, int EXT>
 int launch(const Params& prm, size_t lds, int grid, hipStream_t stream) {
-  auto kern = simplicial_fwd_kernel<T, DP>;
+  auto kern = simplicial_fwd_kernel<T, DP, EXT>;
+  constexpr int kThreads = Waves<EXT>::kThreadCount;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
     MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -574,6 +776,54 @@ extern "C" uint64_t mf_simplicial_fwd_workspace_size(int32_t batch, int32_t head
   return simplicial_pair_workspace_bytes(batch, tokens) + simplicial_fast_workspace_bytes(batch, heads, tokens);
 }
 
+template <int EXT>
+static int dispatch(int dtype, int DP, const Params& prm, size_t lds, int grid, hipStream_t s) {
+  if (dtype == MF_DTYPE_BF16) {
+    if (DP == 32) return launch<__bf16, 32, EXT>(prm, lds, grid, s);
+    if (DP == 64) return launch<__bf16, 64, EXT>(prm, lds, grid, s);
+    return launch<__bf16, 128, EXT>(prm, lds, grid, s);
+  }
+  if (dtype == MF_DTYPE_F16) {
+    if (DP == 32) return launch<_Float16, 32, EXT>(prm, lds, grid, s);
+    if (DP == 64) return launch<_Float16, 64, EXT>(prm, lds, grid, s);
+    return launch<_Float16, 128, EXT>(prm, lds, grid, s);
+  }
+  if (DP == 32) return launch<float, 32, EXT>(prm, lds, grid, s);
+  if (DP == 64) return launch<float, 64, EXT>(prm, lds, grid, s);
+  return launch<float, 128, EXT>(prm, lds, grid, s);
+}
+
+static bool has_extras(const mf_simplicial_fwd_args* a) {
+  return a->bias_u != nullptr || a->angle_left != nullptr || a->message_left != nullptr;
+}
+
+// Validation of the optional terms (the reference's launcher checks at
+// triton_simplicial_attention.py:838-869 and the rank limit of :50-59).
+static int check_extras(const mf_simplicial_fwd_args* a) {
+  if (a->bias_u || a->bias_v || a->bias_w || a->bias_gate) {
+    if (!a->bias_u || !a->bias_v || !a->bias_w || !a->bias_gate)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: bias_u, bias_v, bias_w and bias_gate go together");
+    if (a->bias_dtype != MF_DTYPE_F32 && a->bias_dtype != MF_DTYPE_F16 && a->bias_dtype != MF_DTYPE_BF16)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: unknown bias_dtype " + std::to_string(a->bias_dtype));
+  }
+  if (a->angle_left || a->angle_right || a->angle_gate) {
+    if (!a->angle_left || !a->angle_right || !a->angle_gate)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: angle_left, angle_right and angle_gate go together");
+    if (a->angle_rank < 1 || a->angle_rank > kMaxRank)
+      return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports low-rank features <= 64, got angle rank " +
+                                          std::to_string(a->angle_rank));
+  }
+  if (a->message_left || a->message_right || a->message_basis) {
+    if (!a->message_left || !a->message_right || !a->message_basis)
+      return fail(MF_ERR_INVALID_ARGUMENT,
+                  "mf_simplicial_fwd: message_left, message_right and message_basis go together");
+    if (a->message_rank < 1 || a->message_rank > kMaxRank)
+      return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd only supports low-rank features <= 64, got message rank " +
+                                          std::to_string(a->message_rank));
+  }
+  return MF_OK;
+}
+
 static int launch_general(const mf_simplicial_fwd_args* a, size_t lds, int num_cus, int min_keys, bool zero_rows,
                           hipStream_t s) {
   Params prm{};
@@ -594,19 +844,24 @@ static int launch_general(const mf_simplicial_fwd_args* a, size_t lds, int num_c
   const int per_cu = std::max(1, int((160 * 1024) / std::max<size_t>(lds, 1)));
   const int grid = num_cus * std::min(per_cu, 2);
   const int DP = padded_head_dim(a->head_dim);
-  if (a->dtype == MF_DTYPE_BF16) {
-    if (DP == 32) return launch<__bf16, 32>(prm, lds, grid, s);
-    if (DP == 64) return launch<__bf16, 64>(prm, lds, grid, s);
-    return launch<__bf16, 128>(prm, lds, grid, s);
+  if (has_extras(a)) {
+    Extras& x = prm.x;
+    if (a->bias_u) {
+      x.u = a->bias_u; x.v = a->bias_v; x.w = a->bias_w; x.gate = a->bias_gate;
+      x.bias_dtype = a->bias_dtype;
+    }
+    if (a->angle_left) {
+      x.al = a->angle_left; x.ar = a->angle_right; x.ag = a->angle_gate;
+      x.a_rank = a->angle_rank; x.a_scale = 1.0f / std::sqrt(float(a->angle_rank));
+    }
+    if (a->message_left) {
+      x.ml = a->message_left; x.mr = a->message_right; x.mb = a->message_basis;
+      x.m_rank = a->message_rank; x.m_scale = 1.0f / std::sqrt(float(a->message_rank));
+    }
+    return a->message_left ? dispatch<2>(a->dtype, DP, prm, lds, grid, s)
+                           : dispatch<1>(a->dtype, DP, prm, lds, grid, s);
   }
-  if (a->dtype == MF_DTYPE_F16) {
-    if (DP == 32) return launch<_Float16, 32>(prm, lds, grid, s);
-    if (DP == 64) return launch<_Float16, 64>(prm, lds, grid, s);
-    return launch<_Float16, 128>(prm, lds, grid, s);
-  }
-  if (DP == 32) return launch<float, 32>(prm, lds, grid, s);
-  if (DP == 64) return launch<float, 64>(prm, lds, grid, s);
-  return launch<float, 128>(prm, lds, grid, s);
+  return dispatch<0>(a->dtype, DP, prm, lds, grid, s);
 }
 
 extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) {
@@ -632,7 +887,15 @@ extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) 
   // 16-bit operands with head_dim <= 64: the register-resident kernels, one
   // set of launches per slice of at most kSimplicialFastMaxBatch molecules
   // (the slices reuse the workspace in stream order).
+  st = check_extras(a);
+  if (st != MF_OK) return st;
   size_t lds = 0;
+  if (has_extras(a)) {
+    // the optional terms run on the general kernel
+    st = check_shape(a->batch, a->heads, a->tokens, a->head_dim, a->dtype, has_pv, &lds);
+    if (st != MF_OK) return st;
+    return launch_general(a, lds, dev.num_cus, 0, /*zero_rows=*/true, s);
+  }
   const bool outputs_aligned = reinterpret_cast<uintptr_t>(a->out) % 16 == 0 &&
                                reinterpret_cast<uintptr_t>(a->out_f32) % 16 == 0;
   if (uses_fast(a->head_dim, a->dtype) && operands_aligned(a) && outputs_aligned &&

@@ -81,6 +81,84 @@ def _compute_dtype(dtype: torch.dtype, precision: str) -> torch.dtype:
     return torch.float32
 
 
+class _Extras:
+    """Device tensors of the optional terms, laid out as mf_simplicial_fwd reads them."""
+
+    def __init__(self):
+        self.bias = None      # (u, v, w, gate) [B*H,N,N] x3, [B*H,N]; one dtype
+        self.angle = None     # (left, right, gate) fp32
+        self.message = None   # (left, right, basis) fp32
+
+    @property
+    def present(self) -> bool:
+        return self.bias is not None or self.angle is not None or self.message is not None
+
+    def fields(self) -> dict:
+        f = {}
+        if self.bias is not None:
+            u, v, w, g = self.bias
+            f.update(bias_u=u.data_ptr(), bias_v=v.data_ptr(), bias_w=w.data_ptr(), bias_gate=g.data_ptr(),
+                     bias_dtype=_native.dtype_code(u.dtype))
+        if self.angle is not None:
+            left, right, g = self.angle
+            f.update(angle_left=left.data_ptr(), angle_right=right.data_ptr(), angle_gate=g.data_ptr(),
+                     angle_rank=int(left.shape[-1]))
+        if self.message is not None:
+            left, right, basis = self.message
+            f.update(message_left=left.data_ptr(), message_right=right.data_ptr(),
+                     message_basis=basis.data_ptr(), message_rank=int(left.shape[-1]))
+        return f
+
+
+def _on_device(name: str, t: torch.Tensor, device: torch.device, shape: tuple) -> torch.Tensor:
+    if t.device != device:
+        raise RuntimeError(f"{name} must be on {device}, got {t.device}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    return t
+
+
+def _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, angle_left, angle_right, angle_gate,
+                    message_left, message_right, message_basis) -> _Extras:
+    """Presence rules and checks of the reference launcher (triton_simplicial_attention.py:827-871):
+    a group is used only when all its tensors are given; the bias keeps its dtype (fp32 if it is
+    none of fp16/bf16/fp32), the rank factors are read as fp32."""
+    ext = _Extras()
+    dev = q.device
+    if u is not None and v_bias is not None and w is not None and gate is not None:
+        tensors = [_on_device(n, t, dev, s) for n, t, s in (
+            ("u", u, (B, H, N, N)), ("v_bias", v_bias, (B, H, N, N)), ("w", w, (B, H, N, N)),
+            ("gate", gate, (B, H, N)))]
+        dt = tensors[0].dtype
+        if dt not in (torch.float32, torch.float16, torch.bfloat16) or any(t.dtype != dt for t in tensors):
+            dt = torch.float32
+        ext.bias = tuple(t.to(dt).contiguous() for t in tensors)
+    if angle_left is not None and angle_right is not None and angle_gate is not None:
+        if angle_left.shape != angle_right.shape:
+            raise ValueError(
+                f"angle_left and angle_right must have the same shape, got {angle_left.shape} and {angle_right.shape}")
+        rank = int(angle_left.shape[-1])
+        if rank > 64:
+            raise ValueError(f"the HIP kernel only supports low-rank features <= 64, got {rank}")
+        ext.angle = tuple(_on_device(n, t, dev, s).float().contiguous() for n, t, s in (
+            ("angle_left", angle_left, (B, H, N, N, rank)), ("angle_right", angle_right, (B, H, N, N, rank)),
+            ("angle_gate", angle_gate, (B, H, N))))
+    if message_left is not None and message_right is not None and message_basis is not None:
+        if message_left.shape != message_right.shape:
+            raise ValueError(
+                f"message_left and message_right must have the same shape, got {message_left.shape} and "
+                f"{message_right.shape}")
+        rank = int(message_left.shape[-1])
+        if tuple(message_basis.shape) != (H, rank, D):
+            raise ValueError(f"message_basis must have shape {(H, rank, D)}, got {tuple(message_basis.shape)}")
+        if rank > 64:
+            raise ValueError(f"the HIP kernel only supports low-rank features <= 64, got {rank}")
+        ext.message = tuple(_on_device(n, t, dev, s).float().contiguous() for n, t, s in (
+            ("message_left", message_left, (B, H, N, N, rank)), ("message_right", message_right, (B, H, N, N, rank)),
+            ("message_basis", message_basis, (H, rank, D))))
+    return ext
+
+
 def hip_simplicial_attention_forward(
     q: torch.Tensor,
     k1: torch.Tensor,
@@ -113,12 +191,6 @@ def hip_simplicial_attention_forward(
         raise RuntimeError(f"HIP simplicial attention is unavailable: {_native.load_error()}")
     if q.device.type != "cuda":
         raise RuntimeError("hip_simplicial_attention_forward requires GPU tensors")
-    if any(t is not None for t in (u, v_bias, w, gate, angle_left, angle_right, angle_gate,
-                                   message_left, message_right, message_basis)):
-        raise RuntimeError(
-            "the HIP simplicial kernel does not implement factorized bias / low-rank angle / "
-            "low-rank message terms yet"
-        )
     precision = normalize_simplicial_precision(precision)
     if q.dim() != 4:
         raise ValueError(f"q must have shape (B, H, N, D), got {tuple(q.shape)}")
@@ -148,8 +220,11 @@ def hip_simplicial_attention_forward(
         out_f32 = torch.empty((B, H, N, D), device=q.device, dtype=torch.float32)
     lse = torch.empty((B, H, N), device=q.device, dtype=torch.float32) if need_backward_state else None
 
+    ext = _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, angle_left, angle_right, angle_gate,
+                          message_left, message_right, message_basis)
+
     lib = _native.lib()
-    ws_bytes = lib.mf_simplicial_fwd_workspace_size(B, H, N, D, _native.dtype_code(cdt))
+    ws_bytes = 0 if ext.present else lib.mf_simplicial_fwd_workspace_size(B, H, N, D, _native.dtype_code(cdt))
     ws = _native.workspace(ws_bytes, q.device)
     args = _native.MfSimplicialFwdArgs(
         q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(),
@@ -162,6 +237,7 @@ def hip_simplicial_attention_forward(
         workspace=None if ws is None else ws.data_ptr(), workspace_bytes=ws_bytes,
         batch=B, heads=H, tokens=N, head_dim=D,
         dtype=_native.dtype_code(cdt), precision=_native.MF_PREC[precision],
+        **ext.fields(),
     )
     with torch.cuda.device(q.device):
         status = lib.mf_simplicial_fwd(args, _native.current_stream(q.device))

@@ -303,9 +303,29 @@ class SimplicialAttention(nn.Module):
             return "the HIP backend does not support arbitrary Python logit_bias_fn callbacks"
         if self.head_dim > 128:
             return f"the HIP backend only supports head_dim <= 128, got {self.head_dim}"
-        if factorized_bias is not None or angle_residual is not None or message_residual is not None:
-            return "the HIP kernel does not implement factorized bias / low-rank angle / message terms yet"
-        if message_basis is not None:
+        if factorized_bias is not None:
+            for name, tensor in (("u", factorized_bias.u), ("v", factorized_bias.v), ("w", factorized_bias.w),
+                                 ("gate", factorized_bias.gate)):
+                if tensor.device != x.device:
+                    return f"factorized bias tensor {name} must be on the same GPU device as the attention input"
+        if angle_residual is not None:
+            if any(t.device != x.device for t in (angle_residual.left, angle_residual.right, angle_residual.gate)):
+                return "angle residual tensors must be on the same GPU device as the attention input"
+            if angle_residual.rank > 64:
+                return f"the HIP backend only supports low-rank angle residual rank <= 64, got {angle_residual.rank}"
+        if message_residual is not None:
+            if message_basis is None:
+                return "message residual tensors require a message_basis"
+            if message_residual.left.device != x.device or message_residual.right.device != x.device:
+                return "message residual tensors must be on the same GPU device as the attention input"
+            if message_basis.device != x.device:
+                return "message basis tensor must be on the same GPU device as the attention input"
+            expected = (self.num_heads, message_residual.rank, self.head_dim)
+            if tuple(message_basis.shape) != expected:
+                return f"message basis tensor must have shape {expected}, got {tuple(message_basis.shape)}"
+            if message_residual.rank > 64:
+                return f"the HIP backend only supports low-rank message residual rank <= 64, got {message_residual.rank}"
+        elif message_basis is not None:
             return "message_basis must be None when message_residual is None"
         return hip_unsupported_reason(x.shape[0], self.num_heads, x.shape[1], self.head_dim,
                                       self._triton_compute_dtype())
@@ -381,8 +401,11 @@ class SimplicialAttention(nn.Module):
                 )
         message_basis = self.message_basis if message_residual is not None else None
 
-        q, k1, v1, k2, v2 = self._project_inputs(x)
-        q_content = self._content_query(q)
+        # The dispatch decision depends only on x and the module, so it is taken
+        # before the projection: an explicit impl="triton" call with an
+        # unsupported input dtype then fails with the backend's own message
+        # (the behaviour tests/test_simplicial_attention.py:819-824 expects)
+        # rather than inside in_proj.
         reason = self._triton_unavailable_reason(
             x=x, factorized_bias=factorized_bias, angle_residual=angle_residual, message_residual=message_residual,
             message_basis=message_basis, logit_bias_fn=logit_bias_fn, return_attn=return_attn,
@@ -398,6 +421,9 @@ class SimplicialAttention(nn.Module):
         else:
             impl_used = "torch"
         self._last_impl_used = impl_used
+
+        q, k1, v1, k2, v2 = self._project_inputs(x)
+        q_content = self._content_query(q)
 
         if impl_used == "triton":
             out = self._forward_triton(

@@ -116,9 +116,23 @@ def brute_force_fp64(
     query_valid: np.ndarray,
     pair_key_valid: np.ndarray,
     pair_valid: np.ndarray | None = None,
+    *,
+    bias: tuple | None = None,
+    angle: tuple | None = None,
+    message: tuple | None = None,
 ) -> tuple[np.ndarray, np.ndarray]:
-    """float64 reference over valid atoms; returns (out [B,H,N,D], lse [B,H,N])."""
+    """float64 reference over valid atoms; returns (out [B,H,N,D], lse [B,H,N]).
+
+    Optional terms (simplicial_attention.py:41-47,76-81,330-337), float64 arrays:
+      bias    = (u, v, w, gate): S[j,k] += gate_i (u_ij + v_ik + w_jk)        u,v,w [B,H,N,N], gate [B,H,N]
+      angle   = (left, right, gate): S[j,k] += gate_i R^-1/2 sum_r L_ijr R_ikr   [B,H,N,N,R], gate [B,H,N]
+      message = (left, right, basis): out_i += sum_r c_r basis[h,r],
+                c_r = R^-1/2 sum_jk P_jk L_ijr R_ikr                             basis [H,R,D]
+    """
     q, k1, v1, k2, v2 = (np.asarray(a, dtype=np.float64) for a in (q, k1, v1, k2, v2))
+    bias = None if bias is None else tuple(np.asarray(a, dtype=np.float64) for a in bias)
+    angle = None if angle is None else tuple(np.asarray(a, dtype=np.float64) for a in angle)
+    message = None if message is None else tuple(np.asarray(a, dtype=np.float64) for a in message)
     B, H, N, D = q.shape
     out = np.zeros((B, H, N, D))
     lse = np.zeros((B, H, N))
@@ -136,12 +150,25 @@ def brute_force_fp64(
             K1, V1, K2, V2 = k1[b, h, keys], v1[b, h, keys], k2[b, h, keys], v2[b, h, keys]
             for i in queries:
                 S = np.einsum("d,jd,kd->jk", q[b, h, i], K1, K2)
+                if bias is not None:
+                    u, v, w, gate = bias
+                    S = S + gate[b, h, i] * (u[b, h, i, keys][:, None] + v[b, h, i, keys][None, :]
+                                             + w[b, h][np.ix_(keys, keys)])
+                if angle is not None:
+                    left, right, gate = angle
+                    L, R = left[b, h, i, keys], right[b, h, i, keys]
+                    S = S + gate[b, h, i] * (L @ R.T) / math.sqrt(L.shape[-1])
                 S = np.where(pm, S, -np.inf)
                 m = S.max()
                 P = np.exp(S - m)
                 tot = P.sum()
                 P /= tot
                 out[b, h, i] = np.einsum("jk,jd,kd->d", P, V1, V2)
+                if message is not None:
+                    left, right, basis = message
+                    L, R = left[b, h, i, keys], right[b, h, i, keys]
+                    c = np.einsum("jk,jr,kr->r", P, L, R) / math.sqrt(L.shape[-1])
+                    out[b, h, i] += c @ basis[h]
                 lse[b, h, i] = m + math.log(tot)
     return out, lse
 

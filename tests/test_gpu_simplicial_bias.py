@@ -1,0 +1,275 @@
+"""GPU parity of the fused optional terms of mf_simplicial_fwd: factorized bias, low-rank angle, low-rank message.
+
+Reference semantics: triton_simplicial_attention.py:244-279,305-326 and
+simplicial_attention.py:18-104,330-337 (stases/Matterformer).  The checker is
+the float64 brute force of oracle/simplicial.py, itself pinned to the
+reference's bias + angle + message fixture (tests/test_oracle_simplicial.py).
+
+Tolerances as for the plain forward: fp32 operands with ieee_fp32 precision
+1e-4 (the reference's own parity bar, tests/test_simplicial_attention.py:1017),
+16-bit operands normwise relative error <= 2e-2 against float64 on the same
+16-bit-rounded inputs, and additionally every valid query row within 6e-2 of
+its own norm, so a few wrong rows cannot hide in the normwise figure.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from matterformer_amd.hip_simplicial_attention import hip_simplicial_attention_forward
+from matterformer_amd.simplicial_attention import SimplicialAttention
+from matterformer_amd.simplicial_types import (
+    SimplicialAttentionMask,
+    SimplicialFactorizedBias,
+    SimplicialLowRankAngleResidual,
+    SimplicialLowRankMessageResidual,
+    simplicial_attention_torch_from_projected,
+)
+from matterformer_amd.workloads import random_simplicial, simplicial_workload
+from oracle.simplicial import brute_force_fp64
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    return float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+
+
+def row_errors(got, ref, qv):
+    """Per valid (b, h, i) row: |got - ref| / max(|ref|, 1e-3 * typical row norm)."""
+    got = np.asarray(got, dtype=np.float64)
+    rows = qv.numpy().astype(bool)[:, None, :].repeat(got.shape[1], 1)  # [B, H, N]
+    diff = np.linalg.norm(got - ref, axis=-1)[rows]
+    norm = np.linalg.norm(ref, axis=-1)[rows]
+    floor = 1e-3 * max(float(np.median(norm)), 1e-30)
+    return diff / np.maximum(norm, floor)
+
+
+def make_terms(B, H, N, D, seed, *, bias=True, angle_rank=0, message_rank=0, scale=0.5):
+    gen = torch.Generator().manual_seed(seed)
+    terms = {}
+    if bias:
+        terms["bias"] = [torch.randn(B, H, N, N, generator=gen) * scale for _ in range(3)] + \
+                        [torch.randn(B, H, N, generator=gen)]
+    if angle_rank:
+        terms["angle"] = [torch.randn(B, H, N, N, angle_rank, generator=gen) * scale for _ in range(2)] + \
+                         [torch.randn(B, H, N, generator=gen)]
+    if message_rank:
+        terms["message"] = [torch.randn(B, H, N, N, message_rank, generator=gen) for _ in range(2)] + \
+                           [torch.randn(H, message_rank, D, generator=gen) * D ** -0.5]
+    return terms
+
+
+def run(case, terms, device, dtype, precision, bias_dtype=None):
+    q, k1, v1, k2, v2, qv, pkv, pv = case
+    ops = [t.to(dtype).to(device) for t in (q, k1, v1, k2, v2)]
+    kw = {}
+    if "bias" in terms:
+        bdt = bias_dtype or dtype
+        u, v, w, gate = (t.to(bdt).to(device) for t in terms["bias"])
+        kw.update(u=u, v_bias=v, w=w, gate=gate)
+    if "angle" in terms:
+        left, right, gate = (t.to(device) for t in terms["angle"])
+        kw.update(angle_left=left, angle_right=right, angle_gate=gate)
+    if "message" in terms:
+        left, right, basis = (t.to(device) for t in terms["message"])
+        kw.update(message_left=left, message_right=right, message_basis=basis)
+    out, lse, out32 = hip_simplicial_attention_forward(
+        *ops, query_valid=qv.to(device), pair_key_valid=pkv.to(device),
+        pair_valid=None if pv is None else pv.to(device), precision=precision, **kw)
+    torch.cuda.synchronize()
+    return out, lse, out32
+
+
+def oracle(case, terms, dtype, bias_dtype=None):
+    q, k1, v1, k2, v2, qv, pkv, pv = case
+    ops = [t.to(dtype).double().numpy() for t in (q, k1, v1, k2, v2)]
+    kw = {}
+    if "bias" in terms:
+        bdt = bias_dtype or dtype
+        kw["bias"] = tuple(t.to(bdt).double().numpy() for t in terms["bias"])
+    if "angle" in terms:
+        kw["angle"] = tuple(t.double().numpy() for t in terms["angle"])
+    if "message" in terms:
+        kw["message"] = tuple(t.double().numpy() for t in terms["message"])
+    return brute_force_fp64(*ops, qv.numpy(), pkv.numpy(), None if pv is None else pv.numpy(), **kw)
+
+
+def logit_std(D):
+    return (4.0 / D) ** (1.0 / 6.0)
+
+
+def test_reference_golden_bias_angle_message(cuda):
+    z = np.load(GOLDEN / "simplicial_fp32_bias_angle_message.npz")
+    t = {k: torch.from_numpy(z[k]).to(cuda) for k in z.files if z[k].ndim > 0}
+    out, lse, out32 = hip_simplicial_attention_forward(
+        t["q"], t["k1"], t["v1"], t["k2"], t["v2"], query_valid=t["query_valid"],
+        pair_key_valid=t["pair_key_valid"], pair_valid=t["pair_valid"],
+        u=t["u"], v_bias=t["v_bias"], w=t["w"], gate=t["gate"],
+        angle_left=t["angle_left"], angle_right=t["angle_right"], angle_gate=t["angle_gate"],
+        message_left=t["message_left"], message_right=t["message_right"], message_basis=t["message_basis"],
+        precision="ieee_fp32")
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out32.cpu().numpy(), z["out"], rtol=1e-4, atol=1e-4)
+
+
+SHAPES = [
+    # (B, H, N, D, counts, holes, pair_drop)
+    (1, 2, 7, 8, [5], None, 0.2),
+    (3, 2, 29, 32, [29, 17, 9], [(0, 3)], 0.0),
+    (2, 2, 70, 64, [70, 41], None, 0.1),      # two key chunks
+    (2, 1, 130, 64, [130, 64], [(1, 5)], 0.0),  # three key chunks
+    (2, 2, 33, 128, [33, 16], None, 0.0),
+    (2, 2, 24, 20, [24, 11], [(1, 5)], 0.0),  # head_dim not a multiple of 8
+]
+TERMS = [
+    ("bias", dict(bias=True)),
+    ("angle5", dict(bias=False, angle_rank=5)),
+    ("message3", dict(bias=False, message_rank=3)),
+    ("all16", dict(bias=True, angle_rank=16, message_rank=16)),
+    ("all_r33_r64", dict(bias=True, angle_rank=33, message_rank=64)),
+]
+
+
+@pytest.mark.parametrize("terms", TERMS, ids=[t[0] for t in TERMS])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"B{s[0]}H{s[1]}N{s[2]}D{s[3]}")
+def test_fp32_terms_match_fp64(cuda, shape, terms):
+    B, H, N, D, counts, holes, drop = shape
+    case = random_simplicial(B, H, N, D, seed=N + D + 7, counts=counts, holes=holes, pair_drop=drop,
+                            std=logit_std(D))
+    tm = make_terms(B, H, N, D, seed=N * 3 + D, **terms[1])
+    out, lse, out32 = run(case, tm, cuda, torch.float32, "ieee_fp32")
+    ref, ref_lse = oracle(case, tm, torch.float32)
+    np.testing.assert_allclose(out32.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("terms", TERMS, ids=[t[0] for t in TERMS])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"B{s[0]}H{s[1]}N{s[2]}D{s[3]}")
+def test_16bit_terms_match_fp64(cuda, shape, terms, dtype):
+    B, H, N, D, counts, holes, drop = shape
+    case = random_simplicial(B, H, N, D, seed=N + D + 8, counts=counts, holes=holes, pair_drop=drop,
+                            std=logit_std(D))
+    tm = make_terms(B, H, N, D, seed=N * 5 + D, **terms[1])
+    out, lse, out32 = run(case, tm, cuda, dtype, "bf16_tc")
+    ref, ref_lse = oracle(case, tm, dtype)
+    assert out.dtype == dtype
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-2
+    assert row_errors(out32.cpu().numpy(), ref, case[5]).max() <= 6e-2
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
+def test_fp32_bias_with_bf16_operands(cuda):
+    """The module passes the bias in its own dtype: fp32 bias with bf16 operands."""
+    case = random_simplicial(2, 2, 40, 64, seed=3, counts=[40, 21], std=logit_std(64))
+    tm = make_terms(2, 2, 40, 64, seed=4)
+    out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc", bias_dtype=torch.float32)
+    ref, ref_lse = oracle(case, tm, torch.bfloat16, bias_dtype=torch.float32)
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+
+
+def test_zero_gate_bias_equals_no_bias(cuda):
+    """gate = 0 removes the bias exactly (u, v, w enter only through gate * (.))."""
+    case = random_simplicial(2, 2, 37, 64, seed=5, counts=[37, 20], std=logit_std(64))
+    tm = make_terms(2, 2, 37, 64, seed=6)
+    tm["bias"][3] = torch.zeros_like(tm["bias"][3])
+    with_bias = run(case, tm, cuda, torch.float32, "ieee_fp32")[2]
+    plain = run(case, {}, cuda, torch.float32, "ieee_fp32")[2]
+    np.testing.assert_allclose(with_bias.cpu().numpy(), plain.cpu().numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_qm9_config_with_bias_whole_batch(cuda):
+    """Config 1 (fp32, 128 molecules) with a factorized bias, every molecule against float64."""
+    w = simplicial_workload("qm9")
+    B, H, N, D = w.shape
+    case = (w.q, w.k1, w.v1, w.k2, w.v2, w.query_valid, w.pair_key_valid, None)
+    tm = make_terms(B, H, N, D, seed=101)
+    out, lse, out32 = run(case, tm, cuda, torch.float32, "ieee_fp32")
+    ref, ref_lse = oracle(case, tm, torch.float32)
+    np.testing.assert_allclose(out32.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=1e-4, atol=1e-4)
+
+
+def test_geom_config_with_bias_whole_batch(cuda):
+    """Config 2 (bf16, 64 molecules up to 181 atoms) with a factorized bias, every molecule against float64."""
+    w = simplicial_workload("geom")
+    B, H, N, D = w.shape
+    case = (w.q, w.k1, w.v1, w.k2, w.v2, w.query_valid, w.pair_key_valid, None)
+    tm = make_terms(B, H, N, D, seed=102)
+    out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc")
+    ref, ref_lse = oracle(case, tm, torch.bfloat16)
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+    assert row_errors(out32.cpu().numpy(), ref, w.query_valid).max() <= 6e-2
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
+def test_module_auto_dispatch_serves_factorized_bias_on_gpu(cuda):
+    """The default trunk's call (factorized bias, bf16_tc) runs the HIP kernel under impl="auto" and
+    agrees with the torch path of the same module."""
+    torch.manual_seed(0)
+    attn = SimplicialAttention(dim=64, num_heads=4, impl="auto", precision="bf16_tc").to(cuda)
+    x = torch.randn(3, 19, 64, device=cuda)
+    kpm = torch.zeros(3, 19, dtype=torch.bool, device=cuda)
+    kpm[1, 12:] = True
+    kpm[2, 5:] = True
+    fb = SimplicialFactorizedBias(*(torch.randn(3, 4, 19, 19, device=cuda) * 0.5 for _ in range(3)),
+                                  gate=torch.randn(3, 4, 19, device=cuda))
+    got = attn(x, key_padding_mask=kpm, factorized_bias=fb)
+    assert attn._last_impl_used == "triton"
+    attn.impl = "torch"
+    ref = attn(x, key_padding_mask=kpm, factorized_bias=fb)
+    assert attn._last_impl_used == "torch"
+    assert rel_err(got.detach().cpu().numpy(), ref.detach().cpu().double().numpy()) <= 2e-2
+
+
+def test_module_all_terms_fp32_matches_torch_path(cuda):
+    """impl="triton" with every optional term (angle and message cast to fp32 as the reference does)."""
+    torch.manual_seed(1)
+    attn = SimplicialAttention(dim=32, num_heads=2, impl="triton", precision="ieee_fp32", message_mode="low_rank",
+                               message_rank=4).to(cuda)
+    B, T = 2, 9
+    x = torch.randn(B, T, 32, device=cuda)
+    mask = SimplicialAttentionMask(query_valid=torch.ones(B, T, dtype=torch.bool, device=cuda),
+                                   pair_key_valid=torch.ones(B, T, dtype=torch.bool, device=cuda),
+                                   pair_valid=torch.rand(B, T, T, device=cuda) > 0.2)
+    fb = SimplicialFactorizedBias(*(torch.randn(B, 2, T, T, device=cuda) for _ in range(3)),
+                                  gate=torch.randn(B, 2, T, device=cuda))
+    ar = SimplicialLowRankAngleResidual(left=torch.randn(B, 2, T, T, 3, device=cuda),
+                                        right=torch.randn(B, 2, T, T, 3, device=cuda),
+                                        gate=torch.randn(B, 2, T, device=cuda))
+    mr = SimplicialLowRankMessageResidual(left=torch.randn(B, 2, T, T, 4, device=cuda),
+                                          right=torch.randn(B, 2, T, T, 4, device=cuda))
+    got = attn(x, attention_mask=mask, factorized_bias=fb, angle_residual=ar, message_residual=mr)
+    assert attn._last_impl_used == "triton"
+    q, k1, v1, k2, v2 = attn._project_inputs(x)
+    heads = simplicial_attention_torch_from_projected(
+        q, k1, v1, k2, v2, attention_mask=mask, factorized_bias=fb, angle_residual=ar, message_residual=mr,
+        message_basis=attn.message_basis, fp32_core=True)
+    ref = attn.out_proj(attn._merge_heads(heads))
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_launcher_rejects_mismatched_terms(cuda):
+    case = random_simplicial(1, 2, 8, 16, seed=1)
+    q, k1, v1, k2, v2, qv, pkv = (t.to(cuda) for t in case[:7])
+    bad = torch.randn(1, 2, 8, 7, device=cuda)
+    with pytest.raises(ValueError, match="must have shape"):
+        hip_simplicial_attention_forward(q, k1, v1, k2, v2, query_valid=qv, pair_key_valid=pkv, pair_valid=None,
+                                         u=bad, v_bias=bad, w=bad, gate=torch.randn(1, 2, 8, device=cuda))
+    left = torch.randn(1, 2, 8, 8, 3, device=cuda)
+    with pytest.raises(ValueError, match="same shape"):
+        hip_simplicial_attention_forward(q, k1, v1, k2, v2, query_valid=qv, pair_key_valid=pkv, pair_valid=None,
+                                         angle_left=left, angle_right=left[..., :2],
+                                         angle_gate=torch.randn(1, 2, 8, device=cuda))
+    with pytest.raises(ValueError, match="message_basis must have shape"):
+        hip_simplicial_attention_forward(q, k1, v1, k2, v2, query_valid=qv, pair_key_valid=pkv, pair_valid=None,
+                                         message_left=left, message_right=left,
+                                         message_basis=torch.randn(2, 4, 16, device=cuda))

@@ -55,6 +55,26 @@ def test_golden_vectors_agree_with_fp64_brute_force(name):
     assert err <= tol, err
 
 
+def test_brute_force_optional_terms_match_reference_golden():
+    """The reference's own bias + angle + message fixture pins each optional term of the brute force;
+    dropping any one of them (or transposing u and v) moves the result far outside the tolerance."""
+    z, ops, qv, pkv, pv, opt = load_case("simplicial_fp32_bias_angle_message")
+    args = [o.numpy() for o in ops] + [qv.numpy(), pkv.numpy(), pv.numpy()]
+    terms = dict(bias=tuple(a.numpy() for a in opt["factorized_bias"]),
+                 angle=tuple(a.numpy() for a in opt["angle_residual"]),
+                 message=tuple(a.numpy() for a in opt["message_residual"]))
+    expected = z["out"].astype(np.float64)
+    ref, _ = brute_force_fp64(*args, **terms)
+    np.testing.assert_allclose(ref, expected, rtol=1e-5, atol=1e-5)
+    for drop in terms:
+        partial = {k: v for k, v in terms.items() if k != drop}
+        bad, _ = brute_force_fp64(*args, **partial)
+        assert np.abs(bad - expected).max() > 1e-2, drop
+    u, v, w, g = terms["bias"]
+    bad, _ = brute_force_fp64(*args, **{**terms, "bias": (v, u, w, g)})
+    assert np.abs(bad - expected).max() > 1e-2
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_reference_path_matches_brute_force_fp32(seed):
     q, k1, v1, k2, v2, qv, pkv, pv = random_simplicial(3, 2, 11, 8, seed=seed, counts=[11, 7, 3],
