@@ -139,6 +139,63 @@ typedef struct mf_simplicial_fwd_args {
 
 int mf_simplicial_fwd(const mf_simplicial_fwd_args* args, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* 2-simplicial attention backward (deterministic).                          */
+/*                                                                           */
+/* With P[i,j,k] = exp(S[i,j,k] - lse[i]) on valid pairs (S including the    */
+/* factorized bias when given), go = grad_out and                            */
+/* dS[i,j,k] = P[i,j,k] (sum_d go[i,d] v1[j,d] v2[k,d] - go[i] . out[i]):    */
+/*   dq[i]  = sum_jk dS k1[j] (.) k2[k]    dk1[j] = sum_ik dS q[i] (.) k2[k]  */
+/*   dk2[k] = sum_ij dS q[i] (.) k1[j]     dv1[j] = sum_ik P go[i] (.) v2[k]  */
+/*   dv2[k] = sum_ij P go[i] (.) v1[j]                                        */
+/*   du[i,j] = gate_i sum_k dS   dv_bias[i,k] = gate_i sum_j dS              */
+/*   dw[j,k] = sum_i gate_i dS   dgate[i] = sum_jk dS (u_ij + v_ik + w_jk)   */
+/* (the quantities of triton_simplicial_attention.py:332-782 and             */
+/* :929-1204, which accumulates them with atomics).  Every output element is */
+/* written by one wave after sums in a fixed order: two calls on the same    */
+/* inputs give bitwise identical gradients.  Outputs are fp32, written only  */
+/* at valid entries: the caller zero-fills them.  Low-rank angle and message */
+/* terms are not part of this entry point.                                   */
+/* Replaces triton_simplicial_attention_backward,                            */
+/* triton_simplicial_attention.py:929-1204.                                  */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_simplicial_bwd_args {
+  const void* q;            /* [B*H, N, D] element type `dtype`              */
+  const void* k1;
+  const void* v1;
+  const void* k2;
+  const void* v2;
+  const void* grad_out;     /* [B*H, N, D] element type `grad_dtype`         */
+  const float* out;         /* [B*H, N, D] fp32 forward output (out_f32)     */
+  const float* lse;         /* [B*H, N] fp32 forward lse                     */
+  const uint8_t* query_valid;     /* [B, N]                                  */
+  const uint8_t* pair_key_valid;  /* [B, N]                                  */
+  const uint8_t* pair_valid;      /* [B, N, N] or NULL                       */
+  const void* bias_u;       /* factorized bias as in mf_simplicial_fwd, or NULL */
+  const void* bias_v;
+  const void* bias_w;
+  const void* bias_gate;
+  int32_t bias_dtype;
+  int32_t grad_dtype;       /* mf_dtype of grad_out                          */
+  float* dq;                /* [B*H, N, D] fp32 each; NULL = not wanted      */
+  float* dk1;
+  float* dv1;
+  float* dk2;
+  float* dv2;
+  float* du;                /* [B*H, N, N] fp32 each (bias only); NULL = not wanted */
+  float* dv_bias;
+  float* dw;
+  float* dgate;             /* [B*H, N] fp32                                  */
+  int32_t batch;
+  int32_t heads;
+  int32_t tokens;
+  int32_t head_dim;         /* 1..128                                        */
+  int32_t dtype;            /* mf_dtype of q, k1, v1, k2, v2                 */
+  int32_t reserved;
+} mf_simplicial_bwd_args;
+
+int mf_simplicial_bwd(const mf_simplicial_bwd_args* args, void* stream);
+
 /* Returns MF_OK when mf_simplicial_fwd can serve this shape on the current
  * device, MF_ERR_UNSUPPORTED (with mf_last_error set) when it cannot. */
 int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t tokens,

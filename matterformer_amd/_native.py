@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "mf_simplicial_fwd",
     "mf_simplicial_fwd_supported",
     "mf_simplicial_fwd_workspace_size",
+    "mf_simplicial_bwd",
     "mf_knn",
     "mf_radius_mask",
     "mf_radius_attn",
@@ -86,6 +87,15 @@ class MfSimplicialFwdArgs(ctypes.Structure):
         ("message_basis", ctypes.c_void_p),
         ("message_rank", ctypes.c_int32),
     ]
+
+
+class MfSimplicialBwdArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "q", "k1", "v1", "k2", "v2", "grad_out", "out", "lse", "query_valid", "pair_key_valid", "pair_valid",
+        "bias_u", "bias_v", "bias_w", "bias_gate")] + \
+        [("bias_dtype", ctypes.c_int32), ("grad_dtype", ctypes.c_int32)] + \
+        [(n, ctypes.c_void_p) for n in ("dq", "dk1", "dv1", "dk2", "dv2", "du", "dv_bias", "dw", "dgate")] + \
+        [(n, ctypes.c_int32) for n in ("batch", "heads", "tokens", "head_dim", "dtype", "reserved")]
 
 
 class MfKnnArgs(ctypes.Structure):
@@ -156,6 +166,7 @@ def _load() -> ctypes.CDLL | None:
     lib.mf_last_error.restype = ctypes.c_char_p
     for name, argtype in (
         ("mf_simplicial_fwd", MfSimplicialFwdArgs),
+        ("mf_simplicial_bwd", MfSimplicialBwdArgs),
         ("mf_knn", MfKnnArgs),
         ("mf_radius_mask", MfRadiusMaskArgs),
         ("mf_radius_attn", MfRadiusAttnArgs),

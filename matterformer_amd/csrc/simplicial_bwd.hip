@@ -1,0 +1,610 @@
+// 2-simplicial attention backward for gfx950 (CDNA4), deterministic.
+//
+// Math (the gradient of simplicial_attention.py:206-344; the same quantities
+// as triton_simplicial_attention.py:332-782, which sums them with atomics):
+//   P_ijk  = exp(S_ijk - lse_i) on valid pairs, S_ijk = sum_d q_id k1_jd k2_kd
+//            (+ gate_i (u_ij + v_ik + w_jk))
+//   dP_ijk = sum_d go_id v1_jd v2_kd,   dS_ijk = P_ijk (dP_ijk - go_i . out_i)
+//   dq_i   = sum_jk dS k1_j (.) k2_k     dk1_j = sum_i q_i (.) sum_k dS k2_k
+//   dk2_k  = sum_i q_i (.) sum_j dS k1_j dv1_j = sum_i go_i (.) sum_k P v2_k
+//   dv2_k  = sum_i go_i (.) sum_j P v1_j
+//   du_ij  = gate_i sum_k dS   dv_ik = gate_i sum_j dS   dw_jk = sum_i gate_i dS
+//   dgate_i = sum_jk dS (u_ij + v_ik + w_jk)
+//
+// Ownership instead of atomics.  Every gradient row belongs to one index:
+// dq, du, dv, dgate to the query i; dk1, dv1, dw to the key j; dk2, dv2 to
+// the key k.  The three "roles" are one trilinear pattern with the operands
+// permuted (S_ijk is symmetric under q <-> k1 <-> k2 with the masks moved):
+//
+//   role outer o rows r cols c  S = C_S . (oS (.) R_S)      dP = C_P . (oP (.) R_P)   value paths
+//   Q    i       j      k       K2 . (q_i (.) K1[j])       V2 . (go_i (.) V1[j])    dS: K1[j] (.) K2 -> dq_i
+//   J    j       i      k       K2 . (k1_j (.) Q[i])       V2 . (v1_j (.) GO[i])    dS: Q (.) K2 -> dk1_j, P: GO (.) V2 -> dv1_j
+//   K    k       i      j       K1 . (k2_k (.) Q[i])       V1 . (v2_k (.) GO[i])    dS: Q (.) K1 -> dk2_k, P: GO (.) V1 -> dv2_k
+//
+// One workgroup per (b, h, block of outer indices, role); each wave owns one
+// outer index for the whole launch, so every gradient element is written by
+// one wave after sums in a fixed order: no atomics, bitwise reproducible.
+//
+// Per wave: for each 64-column block (keys, staged fp32 in LDS as C_S and
+// C_P, shared by the waves) and each 16-row tile (rows read from L2, 4
+// consecutive d per lane):
+//   GEMM1   S^T[c][r]  = sum_d C_S[c][d] (oS (.) R_S[r])[d]   fp32 MFMA 16x16x4
+//   GEMM1'  dP^T[c][r] = sum_d C_P[c][d] (oP (.) R_P[r])[d]
+//   P = exp2(S2 - lse2) (log2 e folded into oS), dS = P (dP - delta)
+//   GEMM2   C2a[d][r] += sum_c C_S[c][d] dS[r][c]  (and C2b with C_P and P)
+//   out_o[d] += R[r][d] C2[d][r]   (fp32, the row values already in registers)
+// The accumulator layout of GEMM1 (lane = row r, 4 consecutive columns per
+// lane group) is the B-operand layout GEMM2 needs, as in the forward.  The
+// K index of the fp32 MFMA is mapped to d = 16 t + 4 g + e so that each lane
+// reads 4 consecutive d of a row (one 16-byte load) for 4 MFMA steps.
+// 16-bit inputs are widened to fp32 on load; all products and sums are fp32.
+#include <algorithm>
+#include <cmath>
+
+#include "mf_common.h"
+
+namespace mf {
+namespace sbwd {
+
+constexpr int kRoleQ = 0;
+constexpr int kRoleJ = 1;
+constexpr int kRoleK = 2;
+constexpr int kCols = 64;  // staged key columns per block
+
+template <int DP>
+struct Shape {
+  static constexpr int kWaves = DP >= 128 ? 4 : 8;  // D = 128 needs the whole register file per wave
+  static constexpr int kThreads = kWaves * 64;
+  static constexpr int NT = DP / 16;   // 16-wide d tiles
+  static constexpr int D4 = DP + 4;    // LDS row stride (floats) of the staged columns
+};
+
+struct Params {
+  const void* q;
+  const void* k1;
+  const void* v1;
+  const void* k2;
+  const void* v2;
+  const void* go;
+  const float* out;
+  const float* lse;
+  const uint8_t* qv;
+  const uint8_t* pkv;
+  const uint8_t* pv;
+  const void* u;
+  const void* vb;
+  const void* w;
+  const void* gate;
+  int bias_dtype;
+  float* dq;
+  float* dk1;
+  float* dv1;
+  float* dk2;
+  float* dv2;
+  float* du;
+  float* dvb;
+  float* dw;
+  float* dgate;
+  int B, H, N, D;
+  int dtype, gdtype;
+  int NP;       // N rounded up to 64: LDS list capacity
+  int OB;       // outer blocks per (b, h): ceil(N / waves)
+  int vec;      // q/k/v/go rows 4-element loads are aligned (D % 4 == 0, aligned bases)
+};
+
+// LDS layout (bytes), shared by host sizing and device carving.
+template <int DP>
+struct Lay {
+  static size_t __host__ __device__ cols() { return size_t(2) * kCols * Shape<DP>::D4 * 4; }
+  static size_t __host__ __device__ bytes(int NP, bool has_pv, bool has_bias) {
+    size_t s = cols();
+    s += size_t(NP) * 4 * 3;                                  // kidx, qidx, delta
+    if (has_pv) s += size_t(NP) * 2 * 4;                      // 64 column bits per row
+    if (has_bias) s += size_t(Shape<DP>::kWaves) * (NP + kCols) * 4;  // per-wave row / column sums
+    s += 16;                                                  // counts
+    return s;
+  }
+};
+
+__device__ __forceinline__ float ld1(const void* p, size_t i, int dt) {
+  if (dt == MF_DTYPE_F32) return static_cast<const float*>(p)[i];
+  if (dt == MF_DTYPE_BF16) return static_cast<float>(static_cast<const __bf16*>(p)[i]);
+  return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+}
+
+// Elements d0..d0+3 of row `row` (length D) of a [.., D] tensor, 0 past D.
+__device__ __forceinline__ float4 ld4(const void* p, size_t row, int d0, int D, int dt, bool vec) {
+  const size_t base = row * size_t(D) + d0;
+  if (vec && d0 + 3 < D) {
+    if (dt == MF_DTYPE_F32) return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + base);
+    const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + base);
+    float4 r;
+    if (dt == MF_DTYPE_BF16) {
+      r.x = __uint_as_float(raw.x << 16);
+      r.y = __uint_as_float(raw.x & 0xffff0000u);
+      r.z = __uint_as_float(raw.y << 16);
+      r.w = __uint_as_float(raw.y & 0xffff0000u);
+    } else {
+      const _Float16* h = reinterpret_cast<const _Float16*>(&raw);
+      r.x = float(h[0]); r.y = float(h[1]); r.z = float(h[2]); r.w = float(h[3]);
+    }
+    return r;
+  }
+  float4 r;
+  r.x = d0 < D ? ld1(p, base, dt) : 0.0f;
+  r.y = d0 + 1 < D ? ld1(p, base + 1, dt) : 0.0f;
+  r.z = d0 + 2 < D ? ld1(p, base + 2, dt) : 0.0f;
+  r.w = d0 + 3 < D ? ld1(p, base + 3, dt) : 0.0f;
+  return r;
+}
+
+__device__ __forceinline__ float f4(const float4& v, int e) {
+  return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+}
+
+// Compact the valid positions of a byte mask row into dst; returns the count.
+__device__ __forceinline__ int compact(const uint8_t* m, int N, int* dst, int lane) {
+  int count = 0;
+  for (int base = 0; base < N; base += 64) {
+    const int t = base + lane;
+    const bool v = t < N && m[t] != 0;
+    const unsigned long long bal = __ballot(v);
+    if (v) dst[count + __popcll(bal & ((1ull << lane) - 1ull))] = t;
+    count += __popcll(bal);
+  }
+  return count;
+}
+
+template <int DP, int ROLE>
+__device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, int bh, int ob) {
+  using S = Shape<DP>;
+  constexpr int kWaves = S::kWaves;
+  constexpr int kThreads = S::kThreads;
+  constexpr int NT = S::NT;
+  constexpr int D4 = S::D4;
+  const int N = p.N, D = p.D, NP = p.NP;
+  const int b = bh / p.H;
+  const bool has_pv = p.pv != nullptr;
+  const bool has_bias = p.u != nullptr;
+  const bool vec = p.vec != 0;
+
+  float* CS = reinterpret_cast<float*>(smem);
+  float* CP = CS + kCols * D4;
+  int* kidx = reinterpret_cast<int*>(CP + kCols * D4);
+  int* qidx = kidx + NP;
+  float* delta = reinterpret_cast<float*>(qidx + NP);
+  uint32_t* pvb = reinterpret_cast<uint32_t*>(delta + NP);
+  float* wrow = reinterpret_cast<float*>(pvb + (has_pv ? 2 * NP : 0));
+  float* wcol = wrow + (has_bias ? kWaves * NP : 0);
+  int* counts = reinterpret_cast<int*>(wcol + (has_bias ? kWaves * kCols : 0));
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+
+  // ---- compacted key and query lists of molecule b ----
+  if (wave == 0) {
+    const int nk = compact(p.pkv + size_t(b) * N, N, kidx, lane);
+    if (lane == 0) counts[0] = nk;
+  } else if (wave == 1) {
+    const int nq = compact(p.qv + size_t(b) * N, N, qidx, lane);
+    if (lane == 0) counts[1] = nq;
+  }
+  __syncthreads();
+  const int nk = counts[0], nq = counts[1];
+  const int n_outer = ROLE == kRoleQ ? nq : nk;
+  const int n_rows = ROLE == kRoleQ ? nk : nq;
+  if (ob * kWaves >= n_outer || nk == 0 || nq == 0) return;  // uniform over the workgroup
+  const int* outer_list = ROLE == kRoleQ ? qidx : kidx;
+  const int* row_list = ROLE == kRoleQ ? kidx : qidx;
+
+  // tensors of each role (rows of [B*H, N, D])
+  const void* t_os = ROLE == kRoleQ ? p.q : (ROLE == kRoleJ ? p.k1 : p.k2);   // outer, S side
+  const void* t_op = ROLE == kRoleQ ? p.go : (ROLE == kRoleJ ? p.v1 : p.v2);  // outer, dP side
+  const int dt_op = ROLE == kRoleQ ? p.gdtype : p.dtype;
+  const void* t_rs = ROLE == kRoleQ ? p.k1 : p.q;    // rows, S side
+  const void* t_rp = ROLE == kRoleQ ? p.v1 : p.go;   // rows, dP side
+  const int dt_rp = ROLE == kRoleQ ? p.dtype : p.gdtype;
+  const void* t_cs = ROLE == kRoleK ? p.k1 : p.k2;   // columns, S side
+  const void* t_cp = ROLE == kRoleK ? p.v1 : p.v2;   // columns, dP side
+  const size_t rbase = size_t(bh) * N;               // first row of (b, h)
+
+  // ---- delta_i = go_i . out_i of every valid query (rows of roles J / K) ----
+  if constexpr (ROLE != kRoleQ) {
+    for (int r = wave; r < nq; r += kWaves) {
+      const size_t row = rbase + qidx[r];
+      float s = 0.0f;
+      for (int d = lane; d < D; d += 64) s += ld1(p.go, row * D + d, p.gdtype) * p.out[row * D + d];
+      s = wave_sum(s);
+      if (lane == 0) delta[r] = s;
+    }
+  }
+
+  // ---- this wave's outer index ----
+  const int ol = ob * kWaves + wave;
+  const bool active = ol < n_outer;
+  const int oo = active ? outer_list[ol] : 0;
+  const size_t orow = rbase + oo;
+  float4 oS[NT], oP[NT];  // outer vectors at d = 16 t + 4 g + e (oS carries log2 e)
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    oS[t] = float4{0.f, 0.f, 0.f, 0.f};
+    oP[t] = float4{0.f, 0.f, 0.f, 0.f};
+    if (active) {
+      const float4 a = ld4(t_os, orow, 16 * t + 4 * g, D, p.dtype, vec);
+      oS[t] = float4{a.x * kLog2e, a.y * kLog2e, a.z * kLog2e, a.w * kLog2e};
+      oP[t] = ld4(t_op, orow, 16 * t + 4 * g, D, dt_op, vec);
+    }
+  }
+  float lse2_o = 0.0f, delta_o = 0.0f, gate_o = 0.0f;
+  if constexpr (ROLE == kRoleQ) {
+    if (active) {
+      lse2_o = p.lse[orow] * kLog2e;
+      float s = 0.0f;
+      for (int d = lane; d < D; d += 64) s += ld1(p.go, orow * D + d, p.gdtype) * p.out[orow * D + d];
+      delta_o = wave_sum(s);
+      if (has_bias) gate_o = ld1(p.gate, orow, p.bias_dtype);
+    }
+  }
+
+  float acc_a[NT][4], acc_b[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc_a[t][r] = 0.0f;
+      acc_b[t][r] = 0.0f;
+    }
+  float gacc = 0.0f;  // role Q: dgate partial
+
+  const int n_rt = (n_rows + 15) / 16;
+  for (int cb0 = 0; cb0 < nk; cb0 += kCols) {
+    __syncthreads();  // the previous block's LDS reads are done
+    // stage the column block (fp32, zero past nk and past D)
+    constexpr int CPR = DP / 4;  // float4 chunks per row
+    for (int u = tid; u < kCols * CPR; u += kThreads) {
+      const int c = u / CPR;
+      const int d0 = (u - c * CPR) * 4;
+      float4 a = float4{0.f, 0.f, 0.f, 0.f}, bb = a;
+      if (cb0 + c < nk) {
+        const size_t row = rbase + kidx[cb0 + c];
+        a = ld4(t_cs, row, d0, D, p.dtype, vec);
+        bb = ld4(t_cp, row, d0, D, p.dtype, vec);
+      }
+      *reinterpret_cast<float4*>(CS + c * D4 + d0) = a;
+      *reinterpret_cast<float4*>(CP + c * D4 + d0) = bb;
+    }
+    if (has_pv) {
+      // bits of the block's 64 columns for every compacted key x:
+      //   roles Q, J: pair_valid[x][column]; role K: pair_valid[column][x]
+      const uint8_t* pvm = p.pv + size_t(b) * N * N;
+      for (int u = tid; u < nk * 2; u += kThreads) {
+        const int x = u >> 1;
+        const int wd = u & 1;
+        uint32_t bits = 0;
+        for (int t = 0; t < 32; ++t) {
+          const int c = cb0 + 32 * wd + t;
+          if (c < nk) {
+            const size_t idx = ROLE == kRoleK ? size_t(kidx[c]) * N + kidx[x] : size_t(kidx[x]) * N + kidx[c];
+            if (pvm[idx]) bits |= 1u << t;
+          }
+        }
+        pvb[2 * x + wd] = bits;
+      }
+    }
+    if (has_bias) {
+      for (int u = lane; u < kCols; u += 64) wcol[wave * kCols + u] = 0.0f;
+      if (cb0 == 0)
+        for (int u = lane; u < NP; u += 64) wrow[wave * NP + u] = 0.0f;
+    }
+    __syncthreads();
+    if (!active) continue;
+
+    // column-tile validity of this block
+    const int ncols = min(kCols, nk - cb0);
+    const int nkt = (ncols + 15) / 16;
+    uint32_t pv_outer[2] = {0xffffffffu, 0xffffffffu};
+    if constexpr (ROLE != kRoleQ) {
+      if (has_pv) {
+        pv_outer[0] = pvb[2 * ol];
+        pv_outer[1] = pvb[2 * ol + 1];
+      }
+    }
+    const float gq_o = gate_o * kLog2e;
+
+    for (int rt = 0; rt < n_rt; ++rt) {
+      const int row = rt * 16 + r16;
+      const bool row_ok = row < n_rows;
+      const size_t rrow = rbase + (row_ok ? row_list[row] : 0);
+      const int ro = row_ok ? row_list[row] : 0;
+      float4 rs[NT], rp[NT];  // raw row values at d = 16 t + 4 g + e
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        rs[t] = row_ok ? ld4(t_rs, rrow, 16 * t + 4 * g, D, p.dtype, vec) : float4{0.f, 0.f, 0.f, 0.f};
+        rp[t] = row_ok ? ld4(t_rp, rrow, 16 * t + 4 * g, D, dt_rp, vec) : float4{0.f, 0.f, 0.f, 0.f};
+      }
+      // per-row softmax state: the query's lse (log2) and delta
+      float lse2_r = lse2_o, delta_r = delta_o, gate_r = gate_o, gq_r = gq_o;
+      if constexpr (ROLE != kRoleQ) {
+        lse2_r = row_ok ? p.lse[rrow] * kLog2e : 0.0f;
+        delta_r = row_ok ? delta[row] : 0.0f;
+        if (has_bias) {
+          gate_r = row_ok ? ld1(p.gate, rrow, p.bias_dtype) : 0.0f;
+          gq_r = gate_r * kLog2e;
+        }
+      }
+      uint32_t pv_row[2] = {pv_outer[0], pv_outer[1]};
+      if constexpr (ROLE == kRoleQ) {
+        if (has_pv) {
+          pv_row[0] = row_ok ? pvb[2 * row] : 0u;
+          pv_row[1] = row_ok ? pvb[2 * row + 1] : 0u;
+        }
+      }
+      // bias term that depends on (outer, row) only
+      float bias_row = 0.0f;
+      if (has_bias && row_ok) {
+        if constexpr (ROLE == kRoleQ) bias_row = ld1(p.u, orow * N + ro, p.bias_dtype);   // u[i=o][j=r]
+        if constexpr (ROLE == kRoleJ) bias_row = ld1(p.u, rrow * N + oo, p.bias_dtype);   // u[i=r][j=o]
+        if constexpr (ROLE == kRoleK) bias_row = ld1(p.vb, rrow * N + oo, p.bias_dtype);  // v[i=r][k=o]
+      }
+
+      // GEMM1 (S^T) and GEMM1' (dP^T): lane holds row r16 and columns 16 kt + 4 g + r
+      mf_f32x4 sv[4], dv[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        sv[kt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+        dv[kt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+        if (kt < nkt) {
+          const float* cs = CS + (kt * 16 + r16) * D4 + 4 * g;
+          const float* cp = CP + (kt * 16 + r16) * D4 + 4 * g;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const float4 as = *reinterpret_cast<const float4*>(cs + 16 * t);
+            const float4 ap = *reinterpret_cast<const float4*>(cp + 16 * t);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              sv[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4(as, e), f4(rs[t], e) * f4(oS[t], e), sv[kt], 0, 0, 0);
+              dv[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4(ap, e), f4(rp[t], e) * f4(oP[t], e), dv[kt], 0, 0, 0);
+            }
+          }
+        }
+      }
+
+      // P, dS (sv <- dS, dv <- P) and the bias sums
+      float rowsum = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = kt * 16 + 4 * g + r;  // column within the block
+          const bool col_ok = kt < nkt && cb0 + c < nk;
+          const bool ok = row_ok && col_ok && ((pv_row[c >> 5] >> (c & 31)) & 1u);
+          float s2 = sv[kt][r];
+          float base = 0.0f;
+          if (has_bias && ok) {
+            const int co = kidx[cb0 + c];
+            float be = 0.0f, bc = 0.0f;  // terms of (row, col) and of (outer, col)
+            if constexpr (ROLE == kRoleQ) {
+              bc = ld1(p.vb, orow * N + co, p.bias_dtype);            // v[i=o][k=c]
+              be = ld1(p.w, (rbase + ro) * N + co, p.bias_dtype);     // w[j=r][k=c]
+            } else if constexpr (ROLE == kRoleJ) {
+              be = ld1(p.vb, rrow * N + co, p.bias_dtype);            // v[i=r][k=c]
+              bc = ld1(p.w, orow * N + co, p.bias_dtype);             // w[j=o][k=c]
+            } else {
+              be = ld1(p.u, rrow * N + co, p.bias_dtype);             // u[i=r][j=c]
+              bc = ld1(p.w, (rbase + co) * N + oo, p.bias_dtype);     // w[j=c][k=o]
+            }
+            base = (bias_row + be) + bc;
+            s2 = fmaf(gq_r, base, s2);
+          }
+          const float pe = ok ? fast_exp2(s2 - lse2_r) : 0.0f;
+          const float ds = pe * (dv[kt][r] - delta_r);
+          sv[kt][r] = ds;
+          dv[kt][r] = pe;
+          if constexpr (ROLE == kRoleQ) {
+            rowsum += ds;
+            gacc = fmaf(ds, base, gacc);
+          }
+        }
+      }
+
+      // bias sums: role Q du (row sums) and dv (column sums), role J dw (column sums of gate_r dS)
+      if (has_bias) {
+        if constexpr (ROLE == kRoleQ) {
+          rowsum += __shfl_xor(rowsum, 16, 64);
+          rowsum += __shfl_xor(rowsum, 32, 64);
+          if (g == 0 && row_ok) wrow[wave * NP + row] += rowsum;
+        }
+        if constexpr (ROLE != kRoleK) {
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float x = ROLE == kRoleQ ? sv[kt][r] : gate_r * sv[kt][r];
+              x += __shfl_xor(x, 1, 64);
+              x += __shfl_xor(x, 2, 64);
+              x += __shfl_xor(x, 4, 64);
+              x += __shfl_xor(x, 8, 64);
+              if (r16 == 0) wcol[wave * kCols + kt * 16 + 4 * g + r] += x;
+            }
+        }
+      }
+
+      // GEMM2: C2a[d][r] = sum_c C_S[c][d] dS[r][c];  C2b[d][r] = sum_c C_P[c][d] P[r][c] (roles J, K)
+      mf_f32x4 c2a[NT], c2b[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        c2a[t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+        c2b[t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        if (kt >= nkt) continue;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int c = kt * 16 + 4 * g + rr;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            c2a[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(CS[c * D4 + 16 * t + r16], sv[kt][rr], c2a[t], 0, 0, 0);
+            if constexpr (ROLE != kRoleQ)
+              c2b[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(CP[c * D4 + 16 * t + r16], dv[kt][rr], c2b[t], 0, 0, 0);
+          }
+        }
+      }
+      // out_o[d] += R[r][d] C2[d][r]: lane holds d = 16 t + 4 g + r of row r16, which is rs[t] / rp[t]
+      if (row_ok) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc_a[t][r] = fmaf(f4(rs[t], r), c2a[t][r], acc_a[t][r]);
+            if constexpr (ROLE != kRoleQ) acc_b[t][r] = fmaf(f4(rp[t], r), c2b[t][r], acc_b[t][r]);
+          }
+      }
+    }
+
+    // column sums of this block are complete: dv_bias (role Q) and dw (role J)
+    if constexpr (ROLE != kRoleK) {
+      if (has_bias) {
+        for (int c = lane; c < ncols; c += 64) {
+          const size_t dst = orow * N + kidx[cb0 + c];
+          if constexpr (ROLE == kRoleQ) {
+            if (p.dvb) p.dvb[dst] = gate_o * wcol[wave * kCols + c];
+          } else {
+            if (p.dw) p.dw[dst] = wcol[wave * kCols + c];
+          }
+        }
+      }
+    }
+  }
+  if (!active) return;
+
+  // ---- write the outer index's rows: sum over the 16 row lanes of each group ----
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc_a[t][r] = group16_sum(acc_a[t][r]);
+      if constexpr (ROLE != kRoleQ) acc_b[t][r] = group16_sum(acc_b[t][r]);
+    }
+  float* out_a = ROLE == kRoleQ ? p.dq : (ROLE == kRoleJ ? p.dk1 : p.dk2);
+  float* out_b = ROLE == kRoleQ ? nullptr : (ROLE == kRoleJ ? p.dv1 : p.dv2);
+  // lane (g, r16) writes d = 16 t + 4 g + (r16 & 3) for the tiles t with (t & 3) == r16 >> 2
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if ((t & 3) != (r16 >> 2)) continue;
+    const int d = 16 * t + 4 * g + (r16 & 3);
+    if (d >= D) continue;
+    float va = 0.0f, vb = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if ((r16 & 3) == r) {
+        va = acc_a[t][r];
+        vb = acc_b[t][r];
+      }
+    if (out_a) out_a[orow * D + d] = va;
+    if (out_b) out_b[orow * D + d] = vb;
+  }
+  if constexpr (ROLE == kRoleQ) {
+    if (has_bias) {
+      const float dg = wave_sum(gacc);
+      if (lane == 0 && p.dgate) p.dgate[orow] = dg;
+      if (p.du)
+        for (int row = lane; row < nk; row += 64) p.du[orow * N + kidx[row]] = gate_o * wrow[wave * NP + row];
+    }
+  }
+}
+
+template <int DP>
+__global__ void __launch_bounds__(Shape<DP>::kThreads) simplicial_bwd_kernel(Params p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int bh = blockIdx.x / p.OB;
+  const int ob = blockIdx.x - bh * p.OB;
+  if (blockIdx.y == kRoleQ) run_role<DP, kRoleQ>(p, smem, bh, ob);
+  else if (blockIdx.y == kRoleJ) run_role<DP, kRoleJ>(p, smem, bh, ob);
+  else run_role<DP, kRoleK>(p, smem, bh, ob);
+}
+
+template <int DP>
+int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
+  const size_t lds = Lay<DP>::bytes(prm.NP, has_pv, has_bias);
+  DeviceInfo dev;
+  int st = device_info(&dev);
+  if (st != MF_OK) return st;
+  if (lds > size_t(dev.max_lds_per_block))
+    return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: tokens=" + std::to_string(prm.N) + " needs " +
+                                        std::to_string(lds) + " bytes of LDS per workgroup, the device offers " +
+                                        std::to_string(dev.max_lds_per_block));
+  auto kern = simplicial_bwd_kernel<DP>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set = true;
+  }
+  prm.OB = (prm.N + Shape<DP>::kWaves - 1) / Shape<DP>::kWaves;
+  const long long blocks = (long long)prm.B * prm.H * prm.OB;
+  if (blocks > 0x7fffffffLL) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: grid too large");
+  hipLaunchKernelGGL(kern, dim3(unsigned(blocks), 3), dim3(Shape<DP>::kThreads), lds, stream, prm);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
+
+}  // namespace sbwd
+}  // namespace mf
+
+using namespace mf;
+
+extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) {
+  using namespace mf::sbwd;
+  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: args is NULL");
+  if (!a->q || !a->k1 || !a->v1 || !a->k2 || !a->v2 || !a->grad_out || !a->out || !a->lse)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: q, k1, v1, k2, v2, grad_out, out and lse must be non-NULL");
+  if (!a->query_valid || !a->pair_key_valid)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: query_valid and pair_key_valid must be non-NULL");
+  if (a->batch <= 0 || a->heads <= 0 || a->tokens <= 0 || a->head_dim <= 0)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: batch, heads, tokens and head_dim must be positive");
+  if (a->head_dim > 128)
+    return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd only supports head_dim <= 128, got " + std::to_string(a->head_dim));
+  for (int dt : {a->dtype, a->grad_dtype})
+    if (dt != MF_DTYPE_F32 && dt != MF_DTYPE_F16 && dt != MF_DTYPE_BF16)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: unknown dtype " + std::to_string(dt));
+  const bool has_bias = a->bias_u != nullptr;
+  if (has_bias) {
+    if (!a->bias_v || !a->bias_w || !a->bias_gate)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: bias_u, bias_v, bias_w and bias_gate go together");
+    if (a->bias_dtype != MF_DTYPE_F32 && a->bias_dtype != MF_DTYPE_F16 && a->bias_dtype != MF_DTYPE_BF16)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: unknown bias_dtype " + std::to_string(a->bias_dtype));
+  } else if (a->du || a->dv_bias || a->dw || a->dgate) {
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: bias gradients requested without a bias");
+  }
+  Params prm{};
+  prm.q = a->q; prm.k1 = a->k1; prm.v1 = a->v1; prm.k2 = a->k2; prm.v2 = a->v2; prm.go = a->grad_out;
+  prm.out = a->out; prm.lse = a->lse;
+  prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
+  if (has_bias) {
+    prm.u = a->bias_u; prm.vb = a->bias_v; prm.w = a->bias_w; prm.gate = a->bias_gate;
+    prm.bias_dtype = a->bias_dtype;
+  }
+  prm.dq = a->dq; prm.dk1 = a->dk1; prm.dv1 = a->dv1; prm.dk2 = a->dk2; prm.dv2 = a->dv2;
+  prm.du = a->du; prm.dvb = a->dv_bias; prm.dw = a->dw; prm.dgate = a->dgate;
+  prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
+  prm.dtype = a->dtype; prm.gdtype = a->grad_dtype;
+  prm.NP = (a->tokens + 63) / 64 * 64;
+  // 4-element row loads need D % 4 == 0 and bases aligned to 4 elements
+  bool vec = a->head_dim % 4 == 0;
+  const size_t esz = a->dtype == MF_DTYPE_F32 ? 16 : 8;
+  for (const void* ptr : {a->q, a->k1, a->v1, a->k2, a->v2})
+    vec = vec && reinterpret_cast<uintptr_t>(ptr) % esz == 0;
+  vec = vec && reinterpret_cast<uintptr_t>(a->grad_out) % (a->grad_dtype == MF_DTYPE_F32 ? 16 : 8) == 0;
+  prm.vec = vec ? 1 : 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool has_pv = a->pair_valid != nullptr;
+  const int D = a->head_dim;
+  if (D <= 16) return launch<16>(prm, has_pv, has_bias, s);
+  if (D <= 32) return launch<32>(prm, has_pv, has_bias, s);
+  if (D <= 64) return launch<64>(prm, has_pv, has_bias, s);
+  return launch<128>(prm, has_pv, has_bias, s);
+}

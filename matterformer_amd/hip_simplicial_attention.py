@@ -11,9 +11,14 @@ meaning and return contract:
   triton_simplicial_attention_forward   :790-926 -> hip_simplicial_attention_forward
   triton_simplicial_attention_backward  :929-1204 -> hip_simplicial_attention_backward
 
-The forward is one launch of the hand-written gfx950 kernel through the C ABI
-(include/mf_capi.h).  There is no fallback inside this module: a missing
-library, a CPU tensor or an unsupported shape raises RuntimeError.
+The forward is one launch of the hand-written gfx950 kernels through the C ABI
+(include/mf_capi.h), factorized bias, low-rank angle and message terms
+included; a missing library, a CPU tensor or an unsupported shape raises
+RuntimeError.  The backward is one launch of the deterministic HIP backward
+kernel, except for calls with low-rank angle / message terms (and shapes
+beyond that kernel's LDS capacity), whose gradients come from the reference's
+own fp32-core recompute on the same device; ``last_backward_impl`` says which
+ran.
 """
 
 from __future__ import annotations
@@ -284,14 +289,104 @@ def hip_simplicial_attention_backward(
     need_dmessage_right: bool = True,
     need_dmessage_basis: bool = True,
 ):
-    """Gradients by recomputing the forward with the torch path on the same device.
+    """Returns the 15-tuple of triton_simplicial_attention.py:963-979 (None for grads not needed or absent).
 
-    This is the reference's own ``debug_torch_backward`` recompute
-    (simplicial_attention.py:454-552) with fp32 core; a fused HIP backward
-    kernel is not part of this library yet.  Returns the 15-tuple of
-    triton_simplicial_attention.py:963-979 (None for grads not needed/absent).
+    Without low-rank angle / message terms the gradients come from one launch
+    of the deterministic HIP kernel ``mf_simplicial_bwd`` (fp32 arithmetic,
+    bitwise reproducible).  Calls with angle or message terms, and shapes
+    beyond that kernel's LDS capacity (the library reports them), recompute
+    the forward with the fp32-core torch path on the same device and take its
+    autograd gradients -- the reference's own ``debug_torch_backward`` route
+    (simplicial_attention.py:454-552).  ``last_backward_impl`` records which
+    of the two ran ("hip" or "torch_recompute").
     """
-    del out, lse, precision
+    global last_backward_impl
+    flags = dict(need_du=need_du, need_dv_bias=need_dv_bias, need_dw=need_dw, need_dgate=need_dgate,
+                 need_dangle_left=need_dangle_left, need_dangle_right=need_dangle_right,
+                 need_dangle_gate=need_dangle_gate, need_dmessage_left=need_dmessage_left,
+                 need_dmessage_right=need_dmessage_right, need_dmessage_basis=need_dmessage_basis)
+    has_low_rank = angle_left is not None or message_left is not None
+    if not has_low_rank:
+        result = _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_key_valid, pair_valid,
+                                  u, v_bias, w, gate, flags)
+        if result is not None:
+            last_backward_impl = "hip"
+            return result
+    last_backward_impl = "torch_recompute"
+    return _recompute_backward(grad_out, q, k1, v1, k2, v2, query_valid=query_valid,
+                               pair_key_valid=pair_key_valid, pair_valid=pair_valid, u=u, v_bias=v_bias, w=w,
+                               gate=gate, angle_left=angle_left, angle_right=angle_right, angle_gate=angle_gate,
+                               message_left=message_left, message_right=message_right,
+                               message_basis=message_basis, **flags)
+
+
+last_backward_impl: str | None = None
+
+
+def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_key_valid, pair_valid,
+                     u, v_bias, w, gate, flags):
+    """mf_simplicial_bwd; None when the library reports the shape as beyond its capacity."""
+    if not HIP_AVAILABLE:
+        raise RuntimeError(f"HIP simplicial attention is unavailable: {_native.load_error()}")
+    if q.device.type != "cuda":
+        raise RuntimeError("hip_simplicial_attention_backward requires GPU tensors")
+    B, H, N, D = q.shape
+    dev = q.device
+    dt = q.dtype if q.dtype in (torch.float16, torch.bfloat16, torch.float32) else torch.float32
+    ops = [t.to(device=dev, dtype=dt).contiguous() for t in (q, k1, v1, k2, v2)]
+    gdt = grad_out.dtype if grad_out.dtype in (torch.float16, torch.bfloat16, torch.float32) else torch.float32
+    go = grad_out.to(device=dev, dtype=gdt).contiguous()
+    out32 = out.to(device=dev, dtype=torch.float32).contiguous()
+    lse32 = lse.to(device=dev, dtype=torch.float32).contiguous()
+    for name, t, shape in (("grad_out", go, (B, H, N, D)), ("out", out32, (B, H, N, D)), ("lse", lse32, (B, H, N))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
+    qv = query_valid.to(device=dev, dtype=torch.bool).contiguous()
+    pkv = pair_key_valid.to(device=dev, dtype=torch.bool).contiguous()
+    pv = None if pair_valid is None else pair_valid.to(device=dev, dtype=torch.bool).contiguous()
+    if tuple(qv.shape) != (B, N) or tuple(pkv.shape) != (B, N) or (pv is not None and tuple(pv.shape) != (B, N, N)):
+        raise ValueError("query_valid / pair_key_valid must be (B, N) and pair_valid (B, N, N)")
+    ext = _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, None, None, None, None, None, None)
+    grads = [torch.zeros(B, H, N, D, device=dev, dtype=torch.float32) for _ in range(5)]
+    bias_grads = [None] * 4
+    if ext.bias is not None:
+        for idx, (name, shape) in enumerate((("need_du", (B, H, N, N)), ("need_dv_bias", (B, H, N, N)),
+                                             ("need_dw", (B, H, N, N)), ("need_dgate", (B, H, N)))):
+            if flags[name]:
+                bias_grads[idx] = torch.zeros(shape, device=dev, dtype=torch.float32)
+    f = ext.fields()
+    args = _native.MfSimplicialBwdArgs(
+        q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(), k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
+        grad_out=go.data_ptr(), out=out32.data_ptr(), lse=lse32.data_ptr(), query_valid=qv.data_ptr(),
+        pair_key_valid=pkv.data_ptr(), pair_valid=None if pv is None else pv.data_ptr(),
+        bias_u=f.get("bias_u"), bias_v=f.get("bias_v"), bias_w=f.get("bias_w"), bias_gate=f.get("bias_gate"),
+        bias_dtype=f.get("bias_dtype", 0), grad_dtype=_native.dtype_code(gdt),
+        dq=grads[0].data_ptr(), dk1=grads[1].data_ptr(), dv1=grads[2].data_ptr(), dk2=grads[3].data_ptr(),
+        dv2=grads[4].data_ptr(), du=_native.ptr(bias_grads[0]), dv_bias=_native.ptr(bias_grads[1]),
+        dw=_native.ptr(bias_grads[2]), dgate=_native.ptr(bias_grads[3]),
+        batch=B, heads=H, tokens=N, head_dim=D, dtype=_native.dtype_code(dt), reserved=0)
+    lib = _native.lib()
+    with torch.cuda.device(dev):
+        status = lib.mf_simplicial_bwd(args, _native.current_stream(dev))
+    if status == _native.MF_ERR_UNSUPPORTED:
+        return None
+    _native.check(status, "mf_simplicial_bwd")
+    core = [g.to(t.dtype) for g, t in zip(grads, (q, k1, v1, k2, v2))]
+    optional = [None] * 10
+    if ext.bias is not None:
+        for idx, src in enumerate((u, v_bias, w, gate)):
+            if bias_grads[idx] is not None:
+                optional[idx] = bias_grads[idx].to(src.dtype)
+    return (*core, *optional)
+
+
+def _recompute_backward(
+    grad_out, q, k1, v1, k2, v2, *, query_valid, pair_key_valid, pair_valid, u, v_bias, w, gate,
+    angle_left, angle_right, angle_gate, message_left, message_right, message_basis,
+    need_du, need_dv_bias, need_dw, need_dgate, need_dangle_left, need_dangle_right, need_dangle_gate,
+    need_dmessage_left, need_dmessage_right, need_dmessage_basis,
+):
+    """fp32-core torch recompute + autograd on the inputs' device (simplicial_attention.py:454-552)."""
     has_bias = u is not None
     has_angle = angle_left is not None
     has_message = message_left is not None
