@@ -205,6 +205,18 @@ int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t tokens,
 uint64_t mf_simplicial_fwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens,
                                           int32_t head_dim, int32_t dtype);
 
+/* Allocation-free variant of mf_simplicial_fwd.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, validation and results as mf_simplicial_fwd, except that
+ * `workspace` and `workspace_bytes` are ignored: the scratch lives in a static
+ * 8 MiB device array, one per GPU, held until the process ends.  A shape whose
+ * mf_simplicial_fwd_workspace_size() exceeds 8 MiB returns MF_ERR_UNSUPPORTED.
+ * The call allocates nothing (no hipMalloc/hipFree, no allocating library
+ * routine).  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (two streams, concurrent graph replays) race. */
+int mf_simplicial_fwd_noalloc(const mf_simplicial_fwd_args* args, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* k nearest neighbours of every atom of a batch of molecules.               */
 /*                                                                           */

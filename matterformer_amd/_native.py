@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "mf_simplicial_fwd",
     "mf_simplicial_fwd_supported",
     "mf_simplicial_fwd_workspace_size",
+    "mf_simplicial_fwd_noalloc",
     "mf_simplicial_bwd",
     "mf_knn",
     "mf_radius_mask",
@@ -166,6 +167,7 @@ def _load() -> ctypes.CDLL | None:
     lib.mf_last_error.restype = ctypes.c_char_p
     for name, argtype in (
         ("mf_simplicial_fwd", MfSimplicialFwdArgs),
+        ("mf_simplicial_fwd_noalloc", MfSimplicialFwdArgs),
         ("mf_simplicial_bwd", MfSimplicialBwdArgs),
         ("mf_knn", MfKnnArgs),
         ("mf_radius_mask", MfRadiusMaskArgs),

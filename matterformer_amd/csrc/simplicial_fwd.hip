@@ -27,6 +27,8 @@
 //    maximum by more than kRescaleSlack, so exp2 arguments stay <= slack.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
+#include <vector>
 
 #include "mf_common.h"
 
@@ -864,7 +866,75 @@ static int launch_general(const mf_simplicial_fwd_args* a, size_t lds, int num_c
   return dispatch<0>(a->dtype, DP, prm, lds, grid, s);
 }
 
+static int simplicial_fwd_impl(const mf_simplicial_fwd_args* a, void* stream);
+
 extern "C" int mf_simplicial_fwd(const mf_simplicial_fwd_args* a, void* stream) {
+  return simplicial_fwd_impl(a, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant (for callers that cannot allocate: code under HIP
+// graph capture, serving loops).  The scratch the 16-bit kernels need lives
+// in this file-scope device array, one copy per GPU, instead of a caller
+// workspace.  Host code must not use the array's name as a device address:
+// its per-device address comes from hipGetSymbolAddress, taken once per
+// device on that device's first call.  Every call on a GPU shares that GPU's
+// array, so calls that overlap on one GPU race; each call clears the claim
+// counter (the only part that must start at zero) with a fill kernel, which
+// stays valid inside captured graphs.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;  // 8 MiB per GPU
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+__global__ void clear_words_kernel(uint32_t* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+static int scratch_address(void** out) {
+  static std::mutex mu;
+  static std::vector<void*> ptrs;
+  int dev = 0;
+  MF_HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= static_cast<int>(ptrs.size())) ptrs.resize(dev + 1, nullptr);
+  if (ptrs[dev] == nullptr) {
+    void* ptr = nullptr;
+    MF_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (ptr == nullptr) return fail(MF_ERR_HIP, "mf_simplicial_fwd_noalloc: hipGetSymbolAddress returned NULL");
+    ptrs[dev] = ptr;
+  }
+  *out = ptrs[dev];
+  return MF_OK;
+}
+
+extern "C" int mf_simplicial_fwd_noalloc(const mf_simplicial_fwd_args* a, void* stream) {
+  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd_noalloc: args is NULL");
+  const uint64_t need =
+      mf_simplicial_fwd_workspace_size(a->batch, a->heads, a->tokens, a->head_dim, a->dtype);
+  if (need > kNoAllocScratchBytes)
+    return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_fwd_noalloc: batch=" + std::to_string(a->batch) +
+                                        ", heads=" + std::to_string(a->heads) + ", tokens=" +
+                                        std::to_string(a->tokens) + " needs " + std::to_string(need) +
+                                        " bytes of scratch, the static scratch holds " +
+                                        std::to_string(kNoAllocScratchBytes) + " (use mf_simplicial_fwd)");
+  mf_simplicial_fwd_args sub = *a;
+  sub.workspace = nullptr;
+  sub.workspace_bytes = 0;
+  if (need > 0) {
+    void* ptr = nullptr;
+    int st = scratch_address(&ptr);
+    if (st != MF_OK) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int words = int(simplicial_pair_workspace_bytes(a->batch, a->tokens) / 4);
+    hipLaunchKernelGGL(clear_words_kernel, dim3(1), dim3(64), 0, s, static_cast<uint32_t*>(ptr), words);
+    MF_HIP_CHECK(hipGetLastError());
+    sub.workspace = ptr;
+    sub.workspace_bytes = kNoAllocScratchBytes;
+  }
+  return simplicial_fwd_impl(&sub, stream);
+}
+
+static int simplicial_fwd_impl(const mf_simplicial_fwd_args* a, void* stream) {
   if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: args is NULL");
   if (!a->q || !a->k1 || !a->v1 || !a->k2 || !a->v2)
     return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: q, k1, v1, k2 and v2 must be non-NULL");
