@@ -244,6 +244,30 @@ typedef struct mf_knn_args {
 int mf_knn(const mf_knn_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* kNN lists -> local-attention masks in the layout mf_radius_attn reads.    */
+/*                                                                           */
+/*   mask[b,i,j] = valid_i && (j in idx[b,i,:] || (include_self && j == i))  */
+/* mask_bits [B, N, ceil(N/32)] (bit t of word w is column 32w+t, columns    */
+/* >= N are 0) and block_mask [B, NB, NB] for 64-atom tiles (NB = ceil(N/64)) */
+/* as mf_radius_mask writes them.  The reference has no kNN attention; its   */
+/* trunk expresses one only as MHA with a 0/-inf attn_head_bias              */
+/* (src/matterformer/models/transformer.py:256-268), whose allowed entries   */
+/* are these bits.                                                           */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_knn_mask_args {
+  const int32_t* idx;      /* [B, N, k] as mf_knn writes it (-1 = none)     */
+  const uint8_t* pad_mask; /* [B, N] bytes, nonzero = padding, or NULL       */
+  uint32_t* mask_bits;     /* out                                            */
+  uint8_t* block_mask;     /* out, or NULL                                   */
+  int32_t batch;
+  int32_t atoms;
+  int32_t k;
+  int32_t include_self;    /* nonzero: every valid atom is its own neighbour */
+} mf_knn_mask_args;
+
+int mf_knn_mask(const mf_knn_mask_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Cutoff (radius) neighbour mask, minimum image for periodic cells.         */
 /*                                                                           */
 /* periodic (gram != NULL): coords are fractional; for the integer image     */

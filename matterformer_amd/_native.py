@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "mf_simplicial_fwd_noalloc",
     "mf_simplicial_bwd",
     "mf_knn",
+    "mf_knn_mask",
     "mf_radius_mask",
     "mf_radius_attn",
 )
@@ -112,6 +113,19 @@ class MfKnnArgs(ctypes.Structure):
     ]
 
 
+class MfKnnMaskArgs(ctypes.Structure):
+    _fields_ = [
+        ("idx", ctypes.c_void_p),
+        ("pad_mask", ctypes.c_void_p),
+        ("mask_bits", ctypes.c_void_p),
+        ("block_mask", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("atoms", ctypes.c_int32),
+        ("k", ctypes.c_int32),
+        ("include_self", ctypes.c_int32),
+    ]
+
+
 class MfRadiusMaskArgs(ctypes.Structure):
     _fields_ = [
         ("coords", ctypes.c_void_p),
@@ -170,6 +184,7 @@ def _load() -> ctypes.CDLL | None:
         ("mf_simplicial_fwd_noalloc", MfSimplicialFwdArgs),
         ("mf_simplicial_bwd", MfSimplicialBwdArgs),
         ("mf_knn", MfKnnArgs),
+        ("mf_knn_mask", MfKnnMaskArgs),
         ("mf_radius_mask", MfRadiusMaskArgs),
         ("mf_radius_attn", MfRadiusAttnArgs),
     ):

@@ -80,6 +80,33 @@ def knn_graph(coords: torch.Tensor, k: int, pad_mask: torch.Tensor | None = None
     return (idx, dist) if return_dist else idx
 
 
+def knn_mask(idx: torch.Tensor, pad_mask: torch.Tensor | None = None, *, include_self: bool = True,
+             with_block_mask: bool = True):
+    """Local-attention masks from kNN lists: mask[b, i, j] = valid_i and (j in idx[b, i] or j == i).
+
+    idx (B, N, k) int32 as knn_graph returns it (-1 = none); pad_mask (B, N) bool, True = padding.
+    Returns mask_bits int32 (B, N, ceil(N/32)) and, with with_block_mask, block_mask uint8
+    (B, ceil(N/64), ceil(N/64)) -- the layout radius_attention reads.  The reference's trunk can only
+    express such a mask as a 0 / -inf attn_head_bias (transformer.py:256-268); these are its allowed entries.
+    """
+    if idx.ndim != 3 or idx.dtype != torch.int32:
+        raise ValueError(f"idx must be int32 of shape (B, N, k), got {idx.dtype} {tuple(idx.shape)}")
+    dev = _require_device(idx, pad_mask)
+    B, N, K = idx.shape
+    pad = _pad_bytes(pad_mask, B, N)
+    W = (N + 31) // 32
+    NB = (N + MASK_BLOCK - 1) // MASK_BLOCK
+    bits = torch.empty(B, N, W, dtype=torch.int32, device=dev)
+    blocks = torch.empty(B, NB, NB, dtype=torch.uint8, device=dev) if with_block_mask else None
+    ic = idx.contiguous()
+    args = _native.MfKnnMaskArgs(idx=ic.data_ptr(), pad_mask=_native.ptr(pad), mask_bits=bits.data_ptr(),
+                                 block_mask=_native.ptr(blocks), batch=B, atoms=N, k=K,
+                                 include_self=int(bool(include_self)))
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().mf_knn_mask(args, _native.current_stream(dev)), "mf_knn_mask")
+    return (bits, blocks) if with_block_mask else bits
+
+
 def lattice_to_gram(lattice: torch.Tensor, lattice_repr: str = "y1") -> torch.Tensor:
     """Metric G = cell cell^T of a lattice latent (B, 6), as lattice_latent_to_gram
     (src/matterformer/geometry/lattice.py:12-59,94-100): lower-triangular cell

@@ -98,8 +98,77 @@ def _simplicial_case(ref, name: str, *, seed: int, B: int, H: int, N: int, D: in
     return case
 
 
+# Trunk case (configs[4] at a reduced batch): ada_ln's zero-initialised last layer is replaced by
+# N(0, TRUNK_ADA_STD^2) draws from torch.Generator().manual_seed(TRUNK_SEED + 100), block by block,
+# weight then bias, so that the gates are non-zero (at zero they hide the attention entirely).
+TRUNK_SEED = 4
+TRUNK_ADA_STD = 0.05
+TRUNK_SHAPE = dict(batch=4, d_model=512, heads=8, layers=12, knn_k=32)
+
+
+def trunk_case(transformer, geometry) -> None:
+    """12 reference AdaLNBlocks, simplicial on even and MHA with a kNN 0/-inf attn_head_bias on odd layers
+    (transformer.py:154-316, :256-268), fp32 on the CPU.  The kNN uses the reference's own pair distances
+    (NonPeriodicGeometryAdapter, adapters.py:98-100): the k nearest valid j != i by (d2, j), plus i itself."""
+    B, d, H, L, k = (TRUNK_SHAPE[n] for n in ("batch", "d_model", "heads", "layers", "knn_k"))
+    gen = torch.Generator().manual_seed(TRUNK_SEED)
+    z = torch.randn(B, generator=gen)
+    counts = torch.clamp(torch.round(44.0 + 12.0 * z), 10, 181).to(torch.int64)
+    N = int(counts.max())
+    pad = torch.arange(N)[None, :] >= counts[:, None]
+    x = torch.randn(B, N, d, generator=gen)
+    cond = torch.randn(B, d, generator=gen)
+    coords = torch.randn(B, N, 3, generator=gen) * math.sqrt(2.0)
+
+    torch.manual_seed(TRUNK_SEED)
+    blocks = [transformer.AdaLNBlock(d, H, attn_type="simplicial" if layer % 2 == 0 else "mha",
+                                     simplicial_impl="torch", simplicial_precision="ieee_fp32")
+              for layer in range(L)]
+    ada = torch.Generator().manual_seed(TRUNK_SEED + 100)
+    for blk in blocks:
+        lin = blk.ada_ln[-1]
+        lin.weight.data.copy_(torch.randn(lin.weight.shape, generator=ada) * TRUNK_ADA_STD)
+        lin.bias.data.copy_(torch.randn(lin.bias.shape, generator=ada) * TRUNK_ADA_STD)
+
+    d2 = geometry.NonPeriodicGeometryAdapter()(coords, pad_mask=pad).pair_dist2.clone()
+    eye = torch.eye(N, dtype=torch.bool)[None]
+    d2 = d2.masked_fill(eye | pad[:, None, :] | pad[:, :, None], float("inf"))
+    order = torch.sort(d2, dim=-1, stable=True)
+    take = torch.zeros(B, N, N, dtype=torch.bool)
+    ranks = torch.arange(N)[None, None, :]
+    take.scatter_(2, order.indices, (ranks < k) & torch.isfinite(order.values))
+    allowed = take | eye
+    bias = torch.zeros(B, N, N).masked_fill(~allowed, float("-inf"))[:, None].expand(B, H, N, N).contiguous()
+
+    with torch.no_grad():
+        h = x
+        for layer, blk in enumerate(blocks):
+            h = blk(h, cond, pad_mask=pad, attn_head_bias=bias if layer % 2 else None)
+    def checks(blk):  # per state-dict entry: float64 sum and sum of squares
+        return np.array([[float(t.double().sum()), float(t.double().square().sum())]
+                         for t in blk.state_dict().values()])
+
+    np.savez_compressed(
+        HERE / "trunk_alternating_b4.npz",
+        x=x.numpy(), cond=cond.numpy(), coords=coords.numpy(), counts=counts.numpy(), pad_mask=pad.numpy(),
+        allowed=allowed.numpy(), out=h.numpy(),
+        param_checks_even=np.stack([checks(b) for b in blocks[0::2]]),
+        param_checks_odd=np.stack([checks(b) for b in blocks[1::2]]),
+        param_names_even=np.array(list(blocks[0].state_dict().keys())),
+        param_names_odd=np.array(list(blocks[1].state_dict().keys())),
+        seed=np.array(TRUNK_SEED), ada_std=np.array(TRUNK_ADA_STD), shape=np.array([B, d, H, L, k]),
+    )
+
+
 def main(reference_root: str) -> None:
     sys.path.insert(0, str(Path(reference_root) / "src"))
+    if len(sys.argv) > 2 and sys.argv[2] == "trunk":
+        import matterformer.geometry.adapters as geometry  # noqa: E402
+        import matterformer.models.transformer as transformer  # noqa: E402
+
+        trunk_case(transformer, geometry)
+        print("wrote the trunk fixture to", HERE)
+        return
     import matterformer.models.simplicial_attention as ref  # noqa: E402
     from matterformer.geometry import NonPeriodicGeometryAdapter, PeriodicGeometryAdapter  # noqa: E402
     from matterformer.geometry.lattice import lattice_latent_to_gram  # noqa: E402
