@@ -11,19 +11,28 @@ already resident in HBM.
 value = valid FLOPs (sum_b 4 H D n_b^3) / step time, in TFLOP/s.
 
 Prints ONE JSON line.  Also reports:
-  roofline      the entry point's achieved TFLOP/s against the bf16 dense MFMA
-                peak: valid FLOPs over the average duration of one
-                mf_simplicial_fwd launch (the pair kernel), timed with HIP
-                events on the launch stream; `traffic` is the HBM bytes of
-                one such launch from the committed rocprofv3 --pmc summary
-                (profiles/simplicial_fwd_geom_traffic.json) when present;
+  roofline      the pair kernel's achieved TFLOP/s against the bf16 dense MFMA
+                peak: valid FLOPs over the kernel's duration, taken from HIP
+                events on the launch stream around replays of a graph of 20
+                back-to-back launches (so launch latency is not counted);
+                `traffic` is the HBM bytes of one launch from the committed
+                rocprofv3 --pmc summary (profiles/simplicial_fwd_geom_traffic.json);
   cpu_baseline  the oracle's torch-CPU restatement of the reference path
-                (padded N, chunk 128, bf16 as configured) on the whole batch.
+                (padded N, chunk 128, bf16 as configured) on the host's physical
+                cores (bounded by the box's share), plus a single-thread figure,
+                the CPU model and the peak RSS;
+  extra         the other configurations and calls, each timed the same way
+                (graph replays) with its own roofline where one applies:
+                the training-state forward (fp32 out + lse), forward + backward
+                (mf_simplicial_bwd), C2 with a factorized bias, C1 (fp32),
+                C3 kNN (and its HBM-sized scaled batch), C4 radius mask +
+                attention, and the configs[4] trunk forward (molecules/s).
 
-Other workloads (one JSON line each, not the headline):
+Other entry modes (one JSON line each, not the headline):
   --workload knn          kNN top-16 at B=32 and scaled to
                           B=32*1024 for the HBM roofline;
   --workload radius       radius mask + radius attention (configs[3]);
+  --workload trunk        the configs[4] trunk forward;
   --copy-calibration      a plain device copy of known size, run under
                           rocprofv3 --pmc to scale FETCH_SIZE / WRITE_SIZE.
 """
@@ -41,6 +50,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 BF16_DENSE_PEAK_TFLOPS = 2516.6
+FP32_MFMA_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
 PROFILES = ROOT / "profiles"
 
@@ -51,8 +61,10 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-sample", type=int, default=64, help="molecules in the CPU-baseline sample (0 = skip)")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0 = min(16, cores))")
-    ap.add_argument("--workload", choices=("simplicial", "knn", "radius"), default="simplicial")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU-baseline threads (0 = physical cores, capped by OMP_NUM_THREADS when set)")
+    ap.add_argument("--workload", choices=("simplicial", "knn", "radius", "trunk"), default="simplicial")
+    ap.add_argument("--no-extra", action="store_true", help="headline only (skip the extra configurations)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 512 MiB device copy (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -69,38 +81,82 @@ def committed_traffic(name: str):
         return None
 
 
-def cpu_baseline(workload, sample: int, threads: int):
+def host_cpu() -> dict:
+    """Physical cores (distinct (socket, core) pairs of lscpu -p) and the CPU model."""
+    import subprocess
+
+    info = {"physical_cores": os.cpu_count() or 1, "model": "unknown"}
+    try:
+        out = subprocess.run(["lscpu", "-p=SOCKET,CORE"], capture_output=True, text=True, timeout=10).stdout
+        cores = {line for line in out.splitlines() if line and not line.startswith("#")}
+        if cores:
+            info["physical_cores"] = len(cores)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                info["model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return info
+
+
+def _cpu_passes(workload, sample: int, seconds: float, max_passes: int = 5):
     import torch
 
     from oracle.simplicial import reference_path
 
-    sample = min(sample, workload.q.shape[0])
-    threads = threads or min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
     bf = [t[:sample].to(torch.bfloat16) for t in (workload.q, workload.k1, workload.v1, workload.k2, workload.v2)]
     group = 8
     passes = 0
     t0 = time.perf_counter()
-    # whole passes over the sample until about 10 s of CPU work (at most 5)
-    while passes < 5 and (passes == 0 or time.perf_counter() - t0 < 10.0):
+    while passes < max_passes and (passes == 0 or time.perf_counter() - t0 < seconds):
         for s in range(0, sample, group):
             e = min(sample, s + group)
             reference_path(*(t[s:e] for t in bf), workload.query_valid[s:e], workload.pair_key_valid[s:e],
                            chunk_size=128)
         passes += 1
-    elapsed = time.perf_counter() - t0
-    n = workload.counts[:sample].to(torch.int64)
-    flops = passes * 4 * workload.q.shape[1] * workload.q.shape[3] * int((n ** 3).sum())
+    return passes, time.perf_counter() - t0
+
+
+def cpu_baseline(workload, sample: int, threads: int):
+    import resource
+
+    import torch
+
+    host = host_cpu()
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = threads or (min(host["physical_cores"], share) if share > 0 else host["physical_cores"])
+    sample = min(sample, workload.q.shape[0])
+    n = workload.counts.to(torch.int64)
+    H, D = workload.q.shape[1], workload.q.shape[3]
+    torch.set_num_threads(threads)
+    passes, elapsed = _cpu_passes(workload, sample, 10.0)
+    flops = passes * 4 * H * D * int((n[:sample] ** 3).sum())
+    # single thread on the first 8 molecules
+    torch.set_num_threads(1)
+    single_sample = min(8, sample)
+    p1, e1 = _cpu_passes(workload, single_sample, 5.0, max_passes=3)
+    f1 = p1 * 4 * H * D * int((n[:single_sample] ** 3).sum())
+    torch.set_num_threads(threads)
+    rss_gb = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 1e6
     return {
         "value": flops / elapsed / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
         "sample": (f"{passes} pass(es) over the first {sample} of the 64 GEOM molecules, bf16, padded N=181, "
-                   f"chunk_size 128, torch CPU restatement of simplicial_attention_torch_from_projected; "
-                   f"{elapsed:.2f} s"),
+                   f"chunk_size 128, torch CPU restatement of simplicial_attention_torch_from_projected, "
+                   f"{threads} threads; {elapsed:.2f} s"),
         "molecules_per_s": passes * sample / elapsed,
         "seconds": elapsed,
+        "cpu_model": host["model"],
+        "physical_cores": host["physical_cores"],
+        "single_thread": {"value": f1 / e1 / 1e12, "unit": "TFLOP/s", "molecules_per_s": p1 * single_sample / e1,
+                          "sample": f"{p1} pass(es) over the first {single_sample} molecules; {e1:.2f} s"},
+        "peak_rss_gb": round(rss_gb, 3),
     }
 
 
@@ -180,88 +236,73 @@ def copy_calibration() -> int:
     return 0
 
 
-def bench_knn(args) -> int:
+def _graph_ms(fn, per_graph: int = 20, replays: int = 10) -> float:
+    import torch
+
+    return graph_times(torch.cuda.current_stream(), fn, per_graph=per_graph, replays=replays)
+
+
+def measure_knn(cpu_sample: int) -> dict:
+    """C3 (B=32) and the HBM-sized scaled batch (B=32*1024): graph-replayed times and the HBM roofline."""
     import torch
 
     from matterformer_amd.geometry_ops import knn_graph
     from matterformer_amd.workloads import knn_workload
 
     dev = torch.device("cuda", 0)
-    stream = torch.cuda.current_stream(dev)
-    small = knn_workload()
-    scaled = knn_workload(batch=32 * 1024)
     res = {}
-    for name, w in (("c3", small), ("scaled", scaled)):
+    for name, w, per_graph in (("c3", knn_workload(), 20), ("scaled", knn_workload(batch=32 * 1024), 2)):
         c = w.coords.to(dev)
         B, N, _ = c.shape
-        step = lambda: knn_graph(c, w.k)  # noqa: E731
-        ms, _ = timed_loop(stream, step, args.steps, args.warmup)
-        med, _ = event_times(stream, step, 50)
+        ms = _graph_ms(lambda: knn_graph(c, w.k), per_graph=per_graph, replays=5)  # noqa: B023
         nbytes = B * N * 3 * 4 + B * N * w.k * 8
-        res[name] = {"B": B, "ms": ms, "kernel_ms": med, "bytes": nbytes, "queries": B * N}
+        res[name] = {"batch": B, "ms": ms, "bytes": nbytes, "queries": B * N}
+    sc = res["scaled"]
+    achieved = sc["bytes"] / (sc["ms"] * 1e-3) / 1e9
     cpu = None
-    if args.cpu_sample > 0:
+    if cpu_sample > 0:
         from oracle.native import knn as oracle_knn
 
-        n_cpu = min(args.cpu_sample * 128, scaled.coords.shape[0])
-        sample = scaled.coords[:n_cpu].numpy()
+        w = knn_workload(batch=32 * 1024)
+        n_cpu = min(cpu_sample * 128, w.coords.shape[0])
         t0 = time.perf_counter()
-        oracle_knn(sample, scaled.k)
+        oracle_knn(w.coords[:n_cpu].numpy(), w.k)
         el = time.perf_counter() - t0
         cpu = {"value": n_cpu * 181 / el, "unit": "queries/s", "cores": 1, "kind": "port",
                "sample": f"oracle/knn.c (gcc -O2, 1 thread) on {n_cpu} molecules x 181 atoms, k=16; {el:.2f} s"}
-    sc = res["scaled"]
-    achieved = sc["bytes"] / (sc["kernel_ms"] * 1e-3) / 1e9
-    line = {
-        "metric": "kNN top-16 queries/s (configs[2] scaled to 32768 molecules)",
-        "value": round(sc["queries"] / (sc["ms"] * 1e-3), 1),
-        "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(sc["ms"], 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic (seeded, BASELINE.json configs[2])",
-        "config": {"workload": "kNN top-16, 181 atoms/molecule, coords N(0, 2 A^2)", "batch": sc["B"], "atoms": 181,
-                   "k": 16, "c3_batch32_ms": round(res["c3"]["ms"], 5)},
+    return {
+        "c3_ms": round(res["c3"]["ms"], 5), "scaled_batch": sc["batch"], "scaled_ms": round(sc["ms"], 5),
+        "queries_per_s": round(sc["queries"] / (sc["ms"] * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("knn_c3_scaled"),
-                     "kernel": "mf::knn::knn_block_kernel<16, 1>", "kernel_ms": round(sc["kernel_ms"], 5)},
+                     "kernel": "mf::knn::knn_block_kernel<16, 1>", "kernel_ms": round(sc["ms"], 5),
+                     "algorithmic_bytes": sc["bytes"]},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
-    return 0
 
 
-def bench_radius(args) -> int:
+def measure_radius(cpu_sample: int) -> dict:
+    import numpy as np
     import torch
 
     from matterformer_amd.geometry_ops import lattice_to_gram, radius_attention, radius_mask
     from matterformer_amd.workloads import radius_workload
 
     dev = torch.device("cuda", 0)
-    stream = torch.cuda.current_stream(dev)
     w = radius_workload()
     frac = w.frac.to(dev)
     gram = lattice_to_gram(w.lattice.to(dev))
     q, k, v = (t.to(torch.bfloat16).to(dev) for t in (w.q, w.k, w.v))
     bits, blocks = radius_mask(frac, w.cutoff, gram=gram)
-    pairs = 0
-    words = bits.cpu().numpy().view("uint32")
-    import numpy as np
-
-    pairs = int(np.unpackbits(words.view(np.uint8)).sum())
+    pairs = int(np.unpackbits(bits.cpu().numpy().view(np.uint32).view(np.uint8)).sum())
     B, H, N, D = q.shape
-    mask_step = lambda: radius_mask(frac, w.cutoff, gram=gram)  # noqa: E731
-    attn_step = lambda: radius_attention(q, k, v, bits, blocks)  # noqa: E731
-    both = lambda: radius_attention(q, k, v, *radius_mask(frac, w.cutoff, gram=gram))  # noqa: E731
-    ms, _ = timed_loop(stream, both, args.steps, args.warmup)
-    mask_launch_ms, _ = event_times(stream, mask_step, 50)
-    attn_launch_ms, _ = event_times(stream, attn_step, 50)
-    mask_ms = graph_times(stream, mask_step)
-    attn_ms = graph_times(stream, attn_step)
-    graph_step_ms = graph_times(stream, both)
-    flops = w.attention_flops(pairs)
+    mask_ms = _graph_ms(lambda: radius_mask(frac, w.cutoff, gram=gram))
+    attn_ms = _graph_ms(lambda: radius_attention(q, k, v, bits, blocks))
+    step_ms = _graph_ms(lambda: radius_attention(q, k, v, *radius_mask(frac, w.cutoff, gram=gram)))
     attn_bytes = 4 * B * H * N * D * 2 + bits.numel() * 4 + blocks.numel()
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
     cpu = None
-    if args.cpu_sample > 0:
+    if cpu_sample > 0:
         from oracle.native import radius_mask as oracle_radius_mask
         from oracle.native import unpack_bits
         from oracle.radius import masked_attention_fp64
@@ -273,25 +314,189 @@ def bench_radius(args) -> int:
         el = time.perf_counter() - t0
         cpu = {"value": B / el, "unit": "cells/s", "cores": 1, "kind": "port",
                "sample": f"oracle radius mask (C, 1 thread) + float64 numpy masked softmax, all 8 cells; {el:.2f} s"}
-    line = {
-        "metric": "radius mask + radius attention cells/s (configs[3])",
-        "value": round(B / (ms * 1e-3), 1), "unit": "cells/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded, BASELINE.json configs[3])",
-        "config": {"workload": "periodic MOF cells, 6 A cutoff, minimum image, 64-atom tiles", "cells": B,
-                   "atoms": N, "heads": H, "head_dim": D, "allowed_pairs": pairs,
-                   "mask_ms": round(mask_ms, 5), "attn_ms": round(attn_ms, 5),
-                   "mask_single_launch_ms": round(mask_launch_ms, 5),
-                   "attn_single_launch_ms": round(attn_launch_ms, 5),
-                   "graph_replay_ms_per_step": round(graph_step_ms, 5),
-                   "attn_valid_gflop": round(flops / 1e9, 4)},
+    return {
+        "cells": B, "atoms": N, "allowed_pairs": pairs, "mask_ms": round(mask_ms, 5), "attn_ms": round(attn_ms, 5),
+        "step_ms": round(step_ms, 5), "cells_per_s": round(B / (step_ms * 1e-3), 1),
+        "attn_valid_gflop": round(w.attention_flops(pairs) / 1e9, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("radius_attn_c4"),
-                     "kernel": "mf::rattn::radius_attn_pair_kernel<bf16, 64, true>", "kernel_ms": round(attn_ms, 5)},
+                     "kernel": "mf::rattn::radius_attn_pair_kernel<bf16, 64, true>", "kernel_ms": round(attn_ms, 5),
+                     "algorithmic_bytes": attn_bytes},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+
+
+def measure_trunk() -> dict:
+    """12-layer alternating trunk forward, bf16 weights and activations, 64 GEOM molecules."""
+    import torch
+
+    from matterformer_amd.trunk import AlternatingTrunk
+    from matterformer_amd.workloads import trunk_workload
+
+    dev = torch.device("cuda", 0)
+    w = trunk_workload()
+    torch.manual_seed(4)
+    trunk = AlternatingTrunk(w.d_model, w.heads, w.layers, knn_k=w.knn_k).to(dev).to(torch.bfloat16).eval()
+    gen = torch.Generator().manual_seed(104)
+    for blk in trunk.blocks:  # non-zero adaLN gates (the reference zero-initialises them)
+        lin = blk.ada_ln[-1]
+        lin.weight.data.copy_((torch.randn(lin.weight.shape, generator=gen) * 0.05).to(lin.weight.dtype))
+        lin.bias.data.copy_((torch.randn(lin.bias.shape, generator=gen) * 0.05).to(lin.bias.dtype))
+    x, cond = w.x.to(dev, torch.bfloat16), w.cond.to(dev, torch.bfloat16)
+    coords, pad = w.coords.to(dev), w.pad_mask.to(dev)
+
+    def step():
+        with torch.no_grad():
+            trunk(x, cond, coords, pad)
+
+    for _ in range(3):
+        step()
+    ms, _ = timed_loop(torch.cuda.current_stream(), step, 10, 2)
+    flops = w.valid_flops()
+    atoms = int(w.counts.sum())
+    return {"ms": round(ms, 4), "molecules_per_s": round(w.x.shape[0] / (ms * 1e-3), 1),
+            "atoms_per_s": round(atoms / (ms * 1e-3), 1), "valid_gflop": round(flops["total"] / 1e9, 3),
+            "valid_tflops": round(flops["total"] / (ms * 1e-3) / 1e12, 3),
+            "gflop_split": {k: round(v / 1e9, 3) for k, v in flops.items() if k != "total"},
+            "config": "12 layers d=512 H=8 MLP 4x, even simplicial (bf16_tc) / odd kNN-local k=32, bf16, "
+                      "64 GEOM molecules padded to 181, seed 4, eager forward"}
+
+
+def _line(metric, value, unit, ms, args, dtype, data, config, **more):
+    line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": dtype, "data": data, "config": config}
+    line.update(more)
+    return line
+
+
+def bench_knn(args) -> int:
+    m = measure_knn(args.cpu_sample)
+    print(json.dumps(_line("kNN top-16 queries/s (configs[2] scaled to 32768 molecules)", m["queries_per_s"],
+                           "queries/s", m["scaled_ms"], args, "f32", "synthetic (seeded, BASELINE.json configs[2])",
+                           {"workload": "kNN top-16, 181 atoms/molecule, coords N(0, 2 A^2)",
+                            "batch": m["scaled_batch"], "atoms": 181, "k": 16, "c3_batch32_ms": m["c3_ms"]},
+                           roofline=m["roofline"], cpu_baseline=m["cpu_baseline"])), flush=True)
     return 0
+
+
+def bench_radius(args) -> int:
+    m = measure_radius(args.cpu_sample)
+    print(json.dumps(_line("radius mask + radius attention cells/s (configs[3])", m["cells_per_s"], "cells/s",
+                           m["step_ms"], args, "bf16", "synthetic (seeded, BASELINE.json configs[3])",
+                           {"workload": "periodic MOF cells, 6 A cutoff, minimum image, 64-atom tiles",
+                            "cells": m["cells"], "atoms": m["atoms"], "allowed_pairs": m["allowed_pairs"],
+                            "mask_ms": m["mask_ms"], "attn_ms": m["attn_ms"]},
+                           roofline=m["roofline"], cpu_baseline=m["cpu_baseline"])), flush=True)
+    return 0
+
+
+def bench_trunk(args) -> int:
+    m = measure_trunk()
+    print(json.dumps(_line("configs[4] trunk forward molecules/s", m["molecules_per_s"], "molecules/s", m["ms"], args,
+                           "bf16", "synthetic (seeded, BASELINE.json configs[4]); random-init weights",
+                           {"workload": m["config"]}, atoms_per_s=m["atoms_per_s"],
+                           valid_tflops=m["valid_tflops"], gflop_split=m["gflop_split"])), flush=True)
+    return 0
+
+
+def _simplicial_call(lib, ops, qv, pkv, dtype_code, precision, out=None, out_f32=None, lse=None, bias=None):
+    """A step closure calling mf_simplicial_fwd on torch's current stream (so graph capture records it)."""
+    import torch
+
+    from matterformer_amd import _native
+
+    B, H, N, D = ops[0].shape
+    ws_bytes = lib.mf_simplicial_fwd_workspace_size(B, H, N, D, dtype_code)
+    ws = torch.zeros(max(int(ws_bytes), 16), dtype=torch.uint8, device=ops[0].device)
+    extra = {}
+    if bias is not None:
+        extra = dict(bias_u=bias[0].data_ptr(), bias_v=bias[1].data_ptr(), bias_w=bias[2].data_ptr(),
+                     bias_gate=bias[3].data_ptr(), bias_dtype=_native.dtype_code(bias[0].dtype))
+    a = _native.MfSimplicialFwdArgs(
+        q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(), k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
+        query_valid=qv.data_ptr(), pair_key_valid=pkv.data_ptr(), pair_valid=None,
+        out=_native.ptr(out), out_f32=_native.ptr(out_f32), lse=_native.ptr(lse),
+        workspace=ws.data_ptr(), workspace_bytes=ws.numel(), batch=B, heads=H, tokens=N, head_dim=D,
+        dtype=dtype_code, precision=_native.MF_PREC[precision], **extra)
+    fwd = lib.mf_simplicial_fwd
+
+    def step():
+        st = fwd(a, torch.cuda.current_stream().cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"mf_simplicial_fwd failed: {_native.last_error()}")
+
+    step.keepalive = (a, ws, ops, out, out_f32, lse, bias)
+    return step
+
+
+def measure_simplicial_extras(lib, w, wd) -> dict:
+    """Training-state forward, forward + backward, factorized bias (C2), and C1 fp32."""
+    import torch
+
+    from matterformer_amd import _native
+    from matterformer_amd.hip_simplicial_attention import hip_simplicial_attention_backward
+    from matterformer_amd.workloads import simplicial_workload
+
+    dev = wd.q.device
+    B, H, N, D = wd.shape
+    ops = [t.contiguous() for t in (wd.q, wd.k1, wd.v1, wd.k2, wd.v2)]
+    fwd_flops = w.valid_flops()
+    out = torch.empty(B, H, N, D, dtype=torch.bfloat16, device=dev)
+    out32 = torch.empty(B, H, N, D, dtype=torch.float32, device=dev)
+    lse = torch.empty(B, H, N, dtype=torch.float32, device=dev)
+    train_step = _simplicial_call(lib, ops, wd.query_valid, wd.pair_key_valid, _native.MF_DTYPE_BF16, "bf16_tc",
+                                  out=out, out_f32=out32, lse=lse)
+    train_ms = _graph_ms(train_step)
+    res = {"train_state_fwd": {"ms": round(train_ms, 5), "tflops": round(fwd_flops / (train_ms * 1e-3) / 1e12, 3),
+                               "outputs": "bf16 out + fp32 out + fp32 lse (the reference launcher's contract)"}}
+
+    # backward: mf_simplicial_bwd on the training-state outputs
+    gen = torch.Generator().manual_seed(11)
+    go = torch.randn(B, H, N, D, generator=gen).to(dev, torch.bfloat16)
+    train_step()
+    torch.cuda.synchronize()
+
+    def bwd_step():
+        hip_simplicial_attention_backward(go, *ops, out32, lse, query_valid=wd.query_valid,
+                                          pair_key_valid=wd.pair_key_valid, pair_valid=None, precision="bf16_tc")
+
+    bwd_step()
+    bwd_ms, _ = timed_loop(torch.cuda.current_stream(), bwd_step, 10, 2)
+    bwd_flops = 3 * fwd_flops  # dP, dq, dk1, dk2, dv1, dv2: 12 D n^3 per head against the forward's 4 D n^3
+    res["fwd_bwd"] = {
+        "fwd_ms": round(train_ms, 5), "bwd_ms": round(bwd_ms, 5), "ms": round(train_ms + bwd_ms, 5),
+        "molecules_per_s": round(B / ((train_ms + bwd_ms) * 1e-3), 1),
+        "valid_gflop": round(4 * fwd_flops / 1e9, 3),
+        "bwd_roofline": {"bound": "mfma", "achieved": round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 3),
+                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 5),
+                         "kernel": "mf::sbwd::simplicial_bwd_kernel<64> (fp32 MFMA, deterministic)",
+                         "kernel_ms": round(bwd_ms, 5), "note": "eager call incl. zero-fills and casts"},
+    }
+
+    # factorized bias (bf16), the default trunk's call: general kernel
+    bias = [(torch.randn(B, H, N, N, generator=gen) * 0.5).to(dev, torch.bfloat16) for _ in range(3)] + \
+           [torch.randn(B, H, N, generator=gen).to(dev, torch.bfloat16)]
+    bias_step = _simplicial_call(lib, ops, wd.query_valid, wd.pair_key_valid, _native.MF_DTYPE_BF16, "bf16_tc",
+                                 out=out, bias=bias)
+    bias_ms = _graph_ms(bias_step)
+    res["bias_fwd"] = {"ms": round(bias_ms, 5), "tflops": round(fwd_flops / (bias_ms * 1e-3) / 1e12, 3),
+                       "kernel": "mf::simplicial::simplicial_fwd_kernel<bf16, 64, 1> (factorized bias, bf16)"}
+
+    # C1: QM9 fp32
+    c1 = simplicial_workload("qm9").to(dev)
+    c1_ops = [t.contiguous() for t in (c1.q, c1.k1, c1.v1, c1.k2, c1.v2)]
+    c1_out = torch.empty_like(c1_ops[0])
+    c1_step = _simplicial_call(lib, c1_ops, c1.query_valid, c1.pair_key_valid, _native.MF_DTYPE_F32, "ieee_fp32",
+                               out=c1_out)
+    c1_ms = _graph_ms(c1_step)
+    c1_flops = c1.valid_flops()
+    res["c1_qm9_fp32"] = {"ms": round(c1_ms, 5), "tflops": round(c1_flops / (c1_ms * 1e-3) / 1e12, 3),
+                          "molecules_per_s": round(c1.q.shape[0] / (c1_ms * 1e-3), 1),
+                          "roofline": {"bound": "mfma", "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(c1_flops / (c1_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 5)}}
+    return res
 
 
 def main() -> int:
@@ -317,6 +522,8 @@ def main() -> int:
         return bench_knn(args)
     if args.workload == "radius":
         return bench_radius(args)
+    if args.workload == "trunk":
+        return bench_trunk(args)
     dev = torch.device("cuda", 0)
     lib = _native.lib()
 
@@ -325,24 +532,8 @@ def main() -> int:
     B, H, N, D = wd.shape
     ops = [t.contiguous() for t in (wd.q, wd.k1, wd.v1, wd.k2, wd.v2)]
     out = torch.empty((B, H, N, D), device=dev, dtype=torch.bfloat16)
-    ws_bytes = lib.mf_simplicial_fwd_workspace_size(B, H, N, D, _native.MF_DTYPE_BF16)
-    ws = _native.workspace(ws_bytes, dev)
-    args_struct = _native.MfSimplicialFwdArgs(
-        q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(), k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
-        query_valid=wd.query_valid.data_ptr(), pair_key_valid=wd.pair_key_valid.data_ptr(), pair_valid=None,
-        out=out.data_ptr(), out_f32=None, lse=None,
-        workspace=None if ws is None else ws.data_ptr(), workspace_bytes=ws_bytes,
-        batch=B, heads=H, tokens=N, head_dim=D,
-        dtype=_native.MF_DTYPE_BF16, precision=_native.MF_PREC["bf16_tc"],
-    )
+    step = _simplicial_call(lib, ops, wd.query_valid, wd.pair_key_valid, _native.MF_DTYPE_BF16, "bf16_tc", out=out)
     stream = torch.cuda.current_stream(dev)
-    handle = stream.cuda_stream
-    fwd = lib.mf_simplicial_fwd
-
-    def step():
-        st = fwd(args_struct, handle)
-        if st != 0:
-            raise RuntimeError(f"mf_simplicial_fwd failed: {_native.last_error()}")
 
     ms_per_step, wall = timed_loop(stream, step, args.steps, args.warmup)
 
@@ -350,48 +541,39 @@ def main() -> int:
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     atoms = int(w.counts.sum())
 
-    # Per-launch duration of the launch sequence: one event pair per launch on
-    # the launch stream (median and mean of 100 launches).
-    kernel_ms, kernel_mean_ms = event_times(stream, step, 100)
+    # kernel duration: graph of 20 back-to-back launches, replayed; plus single-launch events for reference
+    kernel_ms = graph_times(stream, step)
+    single_ms, _ = event_times(stream, step, 100)
     achieved = flops / (kernel_ms * 1e-3) / 1e12
+
+    extra = None
+    if not args.no_extra:
+        extra = measure_simplicial_extras(lib, w, wd)
+        extra["knn"] = measure_knn(args.cpu_sample)
+        extra["radius"] = measure_radius(args.cpu_sample)
+        extra["c5_trunk"] = measure_trunk()
 
     cpu = cpu_baseline(w, args.cpu_sample, args.cpu_threads) if args.cpu_sample > 0 else None
 
-    line = {
-        "metric": "2-simplicial attn fwd TFLOP/s (%MFMA peak) + molecules/s, GEOM-Drugs shape",
-        "value": round(tflops, 3),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded, BASELINE.json configs[1])",
-        "config": {
-            "workload": "GEOM-Drugs-like 2-simplicial attention fwd (configs[1])",
-            "batch": B, "heads": H, "tokens_padded": N, "head_dim": D,
-            "valid_atoms": atoms, "valid_gflop": round(flops / 1e9, 4),
-        },
-        "pct_mfma_peak": round(100.0 * tflops / BF16_DENSE_PEAK_TFLOPS, 3),
-        "molecules_per_s": round(B / (ms_per_step * 1e-3), 1),
-        "atoms_per_s": round(atoms / (ms_per_step * 1e-3), 1),
-        "wall_s": round(wall, 4),
-        "roofline": {
-            "bound": "mfma",
-            "achieved": round(achieved, 3),
-            "peak": BF16_DENSE_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_DENSE_PEAK_TFLOPS, 5),
-            "traffic": committed_traffic("simplicial_fwd_geom"),
+    line = _line(
+        "2-simplicial attn fwd TFLOP/s (%MFMA peak) + molecules/s, GEOM-Drugs shape", round(tflops, 3), "TFLOP/s",
+        ms_per_step, args, "bf16", "synthetic (seeded, BASELINE.json configs[1])",
+        {"workload": "GEOM-Drugs-like 2-simplicial attention fwd (configs[1])", "batch": B, "heads": H,
+         "tokens_padded": N, "head_dim": D, "valid_atoms": atoms, "valid_gflop": round(flops / 1e9, 4)},
+        pct_mfma_peak=round(100.0 * tflops / BF16_DENSE_PEAK_TFLOPS, 3),
+        molecules_per_s=round(B / (ms_per_step * 1e-3), 1),
+        atoms_per_s=round(atoms / (ms_per_step * 1e-3), 1),
+        wall_s=round(wall, 4),
+        roofline={
+            "bound": "mfma", "achieved": round(achieved, 3), "peak": BF16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_DENSE_PEAK_TFLOPS, 5), "traffic": committed_traffic("simplicial_fwd_geom"),
             "kernel": "mf_simplicial_fwd launch: simplicial_pair_kernel<bf16, 64, pair_valid=0>",
-            "kernel_ms": round(kernel_ms, 5),
-            "kernel_mean_ms": round(kernel_mean_ms, 5),
+            "kernel_ms": round(kernel_ms, 5), "kernel_ms_source": "HIP events around replays of a 20-launch graph",
+            "single_launch_event_ms": round(single_ms, 5),
         },
-        "cpu_baseline": cpu,
-    }
+        cpu_baseline=cpu,
+        extra=extra,
+    )
     print(json.dumps(line), flush=True)
     return 0
 

@@ -133,3 +133,45 @@ def radius_workload(seed: int = 3, *, cells: int = 8, atoms: int = 512, heads: i
     lattice = torch.cat([lengths.log(), angles.cos()], dim=-1)
     q, k, v = (torch.randn(cells, heads, atoms, head_dim, generator=gen) / 8.0 for _ in range(3))
     return RadiusWorkload(frac, lattice, q, k, v, cutoff)
+
+
+@dataclass
+class TrunkWorkload:
+    x: torch.Tensor        # (B, N, d) fp32 token features
+    cond: torch.Tensor     # (B, d) fp32 conditioning embedding
+    coords: torch.Tensor   # (B, N, 3) fp32 coordinates, N(0, 2 A^2)
+    pad_mask: torch.Tensor  # (B, N) bool, True = padding
+    counts: torch.Tensor   # (B,) valid atoms
+    d_model: int
+    heads: int
+    layers: int
+    knn_k: int
+
+    def valid_flops(self) -> dict:
+        """Algorithmic FLOPs over valid atoms (padded rows are not work):
+        simplicial blocks 28 d^2 per token (in_proj 10 d^2, out_proj 2 d^2, MLP 16 d^2) plus 4 H D n^3,
+        local blocks 24 d^2 per token plus 4 H D n (k + 1); ada_ln 12 d^2 per molecule and block."""
+        d, H = self.d_model, self.heads
+        D = d // H
+        n = self.counts.to(torch.int64)
+        tokens = int(n.sum())
+        n_simp = (self.layers + 1) // 2
+        n_local = self.layers // 2
+        linears = n_simp * 28 * d * d * tokens + n_local * 24 * d * d * tokens
+        linears += self.layers * 12 * d * d * int(n.numel())
+        simp = n_simp * 4 * H * D * int((n ** 3).sum())
+        local = n_local * 4 * H * D * int((n * torch.clamp(n, max=self.knn_k + 1)).sum())
+        return {"linears": linears, "simplicial": simp, "local": local, "total": linears + simp + local}
+
+
+def trunk_workload(seed: int = 4, *, batch: int = 64, atoms: int = 181, d_model: int = 512, heads: int = 8,
+                   layers: int = 12, knn_k: int = 32) -> TrunkWorkload:
+    """Config 5: GEOM-Drugs atom counts (as config 2), coordinates ~ N(0, 2 A^2) (as config 3), token features
+    and conditioning ~ N(0, 1)."""
+    gen = torch.Generator().manual_seed(seed)
+    counts = geom_counts(batch, gen, atoms)
+    pad = torch.arange(atoms)[None, :] >= counts[:, None]
+    x = torch.randn(batch, atoms, d_model, generator=gen)
+    cond = torch.randn(batch, d_model, generator=gen)
+    coords = torch.randn(batch, atoms, 3, generator=gen) * math.sqrt(2.0)
+    return TrunkWorkload(x, cond, coords, pad, counts, d_model, heads, layers, knn_k)
