@@ -300,6 +300,41 @@ typedef struct mf_radius_mask_args {
 int mf_radius_mask(const mf_radius_mask_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Pairwise geometry features in one pass, optionally with the cutoff mask. */
+/*                                                                           */
+/* The pair tensors of GeometryFeatures (geometry/adapters.py:12-21) as the  */
+/* adapters compute them:                                                    */
+/*   gram == NULL (NonPeriodicGeometryAdapter.forward, adapters.py:83-125):  */
+/*     delta = x_i - x_j, d2 = (dx*dx + dy*dy) + dz*dz;                      */
+/*   gram != NULL (PeriodicGeometryAdapter.forward, adapters.py:151-212):    */
+/*     coords fractional; delta = (f_i - f_j) + o for the first offset o of  */
+/*     {-r..r}^3 (itertools.product order) minimising d2 = e^T G e, with     */
+/*     d2 evaluated as in mf_radius_mask;                                    */
+/*   d2 = max(d2, 0), dist = sqrt(d2), dist_norm = dist / scale[b].          */
+/* Every output is 0 outside the valid pairs (both atoms valid).  mask_bits, */
+/* when given, are mf_radius_mask's bits for `cutoff` (d2 <= cutoff^2 on    */
+/* valid pairs, i == j included), in its layout.  Replaces the               */
+/* [B, N, N, 27, 3] image tensor of adapters.py:176-189.                     */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_geometry_args {
+  const float* coords;     /* [B, N, 3] fp32 (fractional when periodic)      */
+  const float* gram;       /* [B, 3, 3] fp32 metric, or NULL (non-periodic)  */
+  const float* scale;      /* [B] fp32 normaliser of dist_norm, or NULL      */
+  const uint8_t* pad_mask; /* [B, N] bytes, nonzero = padding, or NULL       */
+  float* pair_delta;       /* [B, N, N, 3] out, or NULL                      */
+  float* pair_dist2;       /* [B, N, N] out, or NULL                         */
+  float* pair_dist;        /* [B, N, N] out, or NULL                         */
+  float* pair_dist_norm;   /* [B, N, N] out (needs scale), or NULL           */
+  uint32_t* mask_bits;     /* [B, N, ceil(N/32)] out, or NULL                */
+  float cutoff;            /* > 0 when mask_bits is given                    */
+  int32_t batch;
+  int32_t atoms;
+  int32_t pbc_radius;      /* 1 or 2 (ignored when gram == NULL)             */
+} mf_geometry_args;
+
+int mf_geometry_features(const mf_geometry_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Local (radius) attention over a neighbour bit mask.                        */
 /*                                                                           */
 /* out[b,h,i] = sum_j softmax_j(scale * q_i . k_j over j with mask[b,i,j]) v_j */

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "mf_knn",
     "mf_knn_mask",
     "mf_radius_mask",
+    "mf_geometry_features",
     "mf_radius_attn",
 )
 
@@ -141,6 +142,13 @@ class MfRadiusMaskArgs(ctypes.Structure):
     ]
 
 
+class MfGeometryArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "coords", "gram", "scale", "pad_mask", "pair_delta", "pair_dist2", "pair_dist", "pair_dist_norm",
+        "mask_bits")] + [("cutoff", ctypes.c_float), ("batch", ctypes.c_int32), ("atoms", ctypes.c_int32),
+                         ("pbc_radius", ctypes.c_int32)]
+
+
 class MfRadiusAttnArgs(ctypes.Structure):
     _fields_ = [
         ("q", ctypes.c_void_p),
@@ -186,6 +194,7 @@ def _load() -> ctypes.CDLL | None:
         ("mf_knn", MfKnnArgs),
         ("mf_knn_mask", MfKnnMaskArgs),
         ("mf_radius_mask", MfRadiusMaskArgs),
+        ("mf_geometry_features", MfGeometryArgs),
         ("mf_radius_attn", MfRadiusAttnArgs),
     ):
         fn = getattr(lib, name, None)

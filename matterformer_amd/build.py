@@ -42,6 +42,7 @@ BASE_FLAGS = [
 PER_FILE_FLAGS = {
     "knn.hip": ["-ffp-contract=off"],
     "radius.hip": ["-ffp-contract=off"],
+    "geometry.hip": ["-ffp-contract=off"],
 }
 
 

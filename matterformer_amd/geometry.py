@@ -1,0 +1,191 @@
+"""Geometry adapters whose pair features come from one HIP pass (mf_geometry_features).
+
+Mirror of ``matterformer.geometry.adapters`` (src/matterformer/geometry/adapters.py): the same class names,
+constructor and forward signatures and the same ``GeometryFeatures`` (:12-21).
+
+  NonPeriodicGeometryAdapter.forward   :83-125
+  PeriodicGeometryAdapter.forward      :151-212 (27 / 125 images, argmin under the lattice metric)
+
+On GPU tensors the pair tensors (delta, d2, d, d_norm) are written by one kernel that evaluates the images
+in registers: the reference's [B, N, N, 27, 3] image tensor (:176-189) is never formed.  ``forward`` can
+also return the cutoff neighbour mask of the same pass (``radius_cutoff=``, in ``extras["radius_mask_bits"]``,
+mf_radius_mask's layout), which local attention and the kNN / radius consumers read.  The per-molecule
+normalisers (rms radius, cell scale) and the lattice conversions are small torch reductions.  CPU tensors take
+the reference's own torch formulation (as the reference does for them).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from itertools import product
+
+import torch
+from torch import nn
+
+from matterformer_amd.geometry_ops import lattice_to_gram
+
+
+@dataclass
+class GeometryFeatures:
+    pair_delta: torch.Tensor
+    pair_dist: torch.Tensor
+    pair_dist2: torch.Tensor
+    pair_dist_norm: torch.Tensor
+    pair_mask: torch.Tensor
+    global_geom: torch.Tensor
+    kind: str
+    extras: dict[str, torch.Tensor] = field(default_factory=dict)
+
+
+def lattice_latent_to_y1(lattice: torch.Tensor, lattice_repr: str = "y1") -> torch.Tensor:
+    """lattice.py:65-91,103-131: the clamped y1 latent (y1) or y1 recovered from the Gram matrix (ltri)."""
+    lat = lattice.float()
+    rep = lattice_repr.lower()
+    if rep == "y1":
+        return torch.cat([lat[:, :3].clamp(min=-5.0, max=5.0), lat[:, 3:].clamp(min=-0.9999, max=0.9999)], dim=-1)
+    if rep == "ltri":
+        gram = lattice_to_gram(lat, "ltri")
+        lengths = torch.sqrt(torch.diagonal(gram, dim1=-2, dim2=-1).clamp_min(1e-8))
+        den_a = (lengths[:, 1] * lengths[:, 2]).clamp_min(1e-8)
+        den_b = (lengths[:, 0] * lengths[:, 2]).clamp_min(1e-8)
+        den_g = (lengths[:, 0] * lengths[:, 1]).clamp_min(1e-8)
+        cos = torch.stack([(gram[:, 1, 2] / den_a), (gram[:, 0, 2] / den_b), (gram[:, 0, 1] / den_g)], dim=-1)
+        return torch.cat([torch.log(lengths.clamp_min(1e-8)), cos.clamp(min=-0.9999, max=0.9999)], dim=-1)
+    raise ValueError(f"Unsupported lattice_repr: {lattice_repr}")
+
+
+class BaseGeometryAdapter(nn.Module):
+    geometry_kind: str = "base"
+
+    @staticmethod
+    def _valid_atom_mask(coords: torch.Tensor, pad_mask: torch.Tensor | None) -> torch.Tensor:
+        B, N = coords.shape[:2]
+        if pad_mask is None:
+            return torch.ones(B, N, device=coords.device, dtype=torch.bool)
+        if pad_mask.shape != (B, N):
+            raise ValueError(f"pad_mask must have shape {(B, N)}, got {tuple(pad_mask.shape)}")
+        return ~pad_mask.bool()
+
+    @staticmethod
+    def _pair_mask_from_valid(valid: torch.Tensor) -> torch.Tensor:
+        return valid[:, :, None] & valid[:, None, :]
+
+    @staticmethod
+    def _masked(t: torch.Tensor, pair_mask: torch.Tensor) -> torch.Tensor:
+        m = pair_mask
+        while m.ndim < t.ndim:
+            m = m.unsqueeze(-1)
+        return torch.where(m, t, torch.zeros_like(t))
+
+    @staticmethod
+    def _hip_features(coords, pad_mask, scale, gram, pbc_radius, radius_cutoff):
+        from matterformer_amd import _native
+
+        B, N, _ = coords.shape
+        dev = coords.device
+        c = coords.float().contiguous()
+        pad = None if pad_mask is None else pad_mask.to(torch.uint8).contiguous()
+        delta = torch.empty(B, N, N, 3, device=dev, dtype=torch.float32)
+        d2 = torch.empty(B, N, N, device=dev, dtype=torch.float32)
+        dist = torch.empty_like(d2)
+        dnorm = torch.empty_like(d2)
+        bits = None
+        if radius_cutoff is not None:
+            bits = torch.empty(B, N, (N + 31) // 32, device=dev, dtype=torch.int32)
+        g = None if gram is None else gram.float().contiguous()
+        sc = scale.float().contiguous()
+        args = _native.MfGeometryArgs(
+            coords=c.data_ptr(), gram=_native.ptr(g), scale=sc.data_ptr(), pad_mask=_native.ptr(pad),
+            pair_delta=delta.data_ptr(), pair_dist2=d2.data_ptr(), pair_dist=dist.data_ptr(),
+            pair_dist_norm=dnorm.data_ptr(), mask_bits=_native.ptr(bits),
+            cutoff=float(radius_cutoff) if radius_cutoff is not None else 0.0, batch=B, atoms=N,
+            pbc_radius=int(pbc_radius))
+        with torch.cuda.device(dev):
+            _native.check(_native.lib().mf_geometry_features(args, _native.current_stream(dev)),
+                          "mf_geometry_features")
+        return delta, dist, d2, dnorm, bits
+
+
+class NonPeriodicGeometryAdapter(BaseGeometryAdapter):
+    geometry_kind = "nonperiodic"
+
+    def forward(self, coords: torch.Tensor, pad_mask: torch.Tensor | None = None,
+                lattice: torch.Tensor | None = None, *, radius_cutoff: float | None = None) -> GeometryFeatures:
+        if coords.ndim != 3 or coords.shape[-1] != 3:
+            raise ValueError(f"coords must have shape (B, N, 3), got {tuple(coords.shape)}")
+        if lattice is not None:
+            raise ValueError("lattice must be None for NonPeriodicGeometryAdapter")
+        coords = coords.float()
+        valid = self._valid_atom_mask(coords, pad_mask)
+        pair_mask = self._pair_mask_from_valid(valid)
+        sq_norm = coords.square().sum(dim=-1)
+        denom = valid.sum(dim=1).clamp_min(1)
+        rms = torch.sqrt(((sq_norm * valid.to(sq_norm.dtype)).sum(dim=1) / denom).clamp_min(1e-8))
+        extras = {"metric": torch.eye(3, device=coords.device, dtype=coords.dtype).expand(coords.shape[0], -1, -1)}
+        if coords.device.type == "cuda":
+            delta, dist, d2, dnorm, bits = self._hip_features(coords, pad_mask, rms.clamp_min(1e-8), None, 0,
+                                                              radius_cutoff)
+            if bits is not None:
+                extras["radius_mask_bits"] = bits
+        else:
+            delta = coords[:, :, None, :] - coords[:, None, :, :]
+            d2 = delta.square().sum(dim=-1).clamp_min(0.0)
+            dist = torch.sqrt(d2)
+            dnorm = dist / rms[:, None, None].clamp_min(1e-8)
+            delta, dist, d2, dnorm = (self._masked(t, pair_mask) for t in (delta, dist, d2, dnorm))
+            if radius_cutoff is not None:
+                extras["radius_mask"] = pair_mask & (d2 <= float(radius_cutoff) ** 2)
+        return GeometryFeatures(pair_delta=delta, pair_dist=dist, pair_dist2=d2, pair_dist_norm=dnorm,
+                                pair_mask=pair_mask, global_geom=rms[:, None], kind=self.geometry_kind, extras=extras)
+
+
+class PeriodicGeometryAdapter(BaseGeometryAdapter):
+    geometry_kind = "periodic"
+
+    def __init__(self, pbc_radius: int = 1, lattice_repr: str = "y1") -> None:
+        super().__init__()
+        if pbc_radius not in {1, 2}:
+            raise ValueError(f"pbc_radius must be 1 or 2, got {pbc_radius}")
+        self.pbc_radius = int(pbc_radius)
+        self.lattice_repr = lattice_repr.lower()
+        offsets = torch.tensor(list(product(range(-self.pbc_radius, self.pbc_radius + 1), repeat=3)),
+                               dtype=torch.float32)
+        self.register_buffer("_pbc_offsets", offsets.view(1, 1, 1, offsets.shape[0], 3), persistent=False)
+
+    def forward(self, coords: torch.Tensor, pad_mask: torch.Tensor | None = None,
+                lattice: torch.Tensor | None = None, *, radius_cutoff: float | None = None) -> GeometryFeatures:
+        if coords.ndim != 3 or coords.shape[-1] != 3:
+            raise ValueError(f"coords must have shape (B, N, 3), got {tuple(coords.shape)}")
+        if lattice is None:
+            raise ValueError("lattice is required for PeriodicGeometryAdapter")
+        if lattice.ndim != 2 or lattice.shape[-1] != 6:
+            raise ValueError(f"lattice must have shape (B, 6), got {tuple(lattice.shape)}")
+        if lattice.shape[0] != coords.shape[0]:
+            raise ValueError(f"lattice batch {lattice.shape[0]} does not match coords batch {coords.shape[0]}")
+        coords = coords.float()
+        lattice = lattice.float()
+        valid = self._valid_atom_mask(coords, pad_mask)
+        pair_mask = self._pair_mask_from_valid(valid)
+        y1 = lattice_latent_to_y1(lattice, self.lattice_repr)
+        gram = lattice_to_gram(lattice, self.lattice_repr)
+        cell_scale = torch.exp(y1[:, :3]).mean(dim=-1).clamp_min(1e-8)
+        extras = {"metric": gram, "cell_scale": cell_scale[:, None]}
+        if coords.device.type == "cuda":
+            delta, dist, d2, dnorm, bits = self._hip_features(coords, pad_mask, cell_scale, gram, self.pbc_radius,
+                                                              radius_cutoff)
+            if bits is not None:
+                extras["radius_mask_bits"] = bits
+        else:
+            delta0 = coords[:, :, None, :] - coords[:, None, :, :]
+            images = delta0[:, :, :, None, :] + self._pbc_offsets.to(coords.device, coords.dtype)
+            d2_images = torch.einsum("bnmki,bij,bnmkj->bnmk", images, gram, images)
+            idx = d2_images.argmin(dim=-1, keepdim=True)
+            d2 = torch.gather(d2_images, -1, idx).squeeze(-1).clamp_min(0.0)
+            delta = torch.gather(images, 3, idx[..., None].expand(-1, -1, -1, 1, 3)).squeeze(3)
+            dist = torch.sqrt(d2)
+            dnorm = dist / cell_scale[:, None, None]
+            delta, dist, d2, dnorm = (self._masked(t, pair_mask) for t in (delta, dist, d2, dnorm))
+            if radius_cutoff is not None:
+                extras["radius_mask"] = pair_mask & (d2 <= float(radius_cutoff) ** 2)
+        return GeometryFeatures(pair_delta=delta, pair_dist=dist, pair_dist2=d2, pair_dist_norm=dnorm,
+                                pair_mask=pair_mask, global_geom=y1, kind=self.geometry_kind, extras=extras)
