@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 4
+#define MF_ABI_VERSION 5
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -363,6 +363,82 @@ typedef struct mf_radius_attn_args {
 } mf_radius_attn_args;
 
 int mf_radius_attn(const mf_radius_attn_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Packed-token glue of the AdaLN trunk.  The valid atoms of a padded batch  */
+/* are the T rows of one [T, C] matrix (row t: atom of molecule mol[t]).     */
+/* All three replace torch expressions of the reference's AdaLNBlock and     */
+/* SimplicialAttention; none has a kernel of its own in the reference.       */
+/*                                                                           */
+/* mf_adaln_rows: the elementwise steps around a block's attention and MLP   */
+/* (transformer.py:296-316, _modulate):                                      */
+/*   y != NULL:     x_out = x + gate[mol] * y                                */
+/*   shift != NULL: h_out = LN(x') * (1 + scale[mol]) + shift[mol],          */
+/*                  x' = x_out if y != NULL else x; LN without affine, eps.  */
+/* Every product and sum rounded to dtype as the torch expressions are; LN  */
+/* statistics in fp32.  x_out may equal x.  channels and mod_stride multiples */
+/* of 8, channels <= 2048, operands 16-byte aligned (else                    */
+/* MF_ERR_UNSUPPORTED).                                                      */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_adaln_rows_args {
+  const void* x;           /* [T, C] residual stream                          */
+  const void* y;           /* [T, C] branch output, or NULL                   */
+  const void* gate;        /* [B, .] row stride mod_stride (with y)           */
+  const void* shift;       /* [B, .] row stride mod_stride, or NULL           */
+  const void* scale;       /* [B, .] row stride mod_stride (with shift)       */
+  const int32_t* mol;      /* [T] molecule of each row                        */
+  void* x_out;             /* [T, C] (with y)                                 */
+  void* h_out;             /* [T, C] (with shift)                             */
+  float eps;
+  int32_t tokens;
+  int32_t channels;
+  int32_t batch;
+  int32_t mod_stride;      /* elements between molecules' gate/shift/scale rows */
+  int32_t dtype;           /* mf_dtype of every tensor                        */
+} mf_adaln_rows_args;
+
+int mf_adaln_rows(const mf_adaln_rows_args* args, void* stream);
+
+/* mf_rows_to_heads: [T, P*H*D] projections (in_proj output, parts q/k/v...) */
+/* -> [P, B, H, W, D], the layout the attention kernels read:                 */
+/*   heads[p, b, h, w, :] = rows[slot[b*W + w], p*H*D + h*D : +D]             */
+/* (zeros where slot is -1); part 0 multiplied by first_part_scale and       */
+/* rounded in the source dtype first (q * head_dim^-1/2, _project_inputs),   */
+/* then converted to dst_dtype.  D multiple of 8, 16-byte aligned operands.  */
+typedef struct mf_rows_to_heads_args {
+  const void* rows;        /* [T, P*H*D] src_dtype                            */
+  const int32_t* slot;     /* [B*W]: source row of (b, w), or -1              */
+  void* heads;             /* [P, B, H, W, D] dst_dtype                       */
+  float first_part_scale;  /* 1 = none                                       */
+  int32_t tokens;
+  int32_t parts;
+  int32_t batch;
+  int32_t heads_count;
+  int32_t width;           /* W: padded atoms per molecule                    */
+  int32_t head_dim;
+  int32_t src_dtype;
+  int32_t dst_dtype;
+} mf_rows_to_heads_args;
+
+int mf_rows_to_heads(const mf_rows_to_heads_args* args, void* stream);
+
+/* mf_heads_to_rows: [B, H, W, D] attention output -> [T, H*D] rows          */
+/* (_merge_heads on the valid atoms): rows[t, h*D + d] = heads[b, h, w, d]   */
+/* with b*W + w = row_index[t]; converted to dst_dtype.                      */
+typedef struct mf_heads_to_rows_args {
+  const void* heads;       /* [B, H, W, D] src_dtype                          */
+  const int32_t* row_index;/* [T]: b*W + w of row t                          */
+  void* rows;              /* [T, H*D] dst_dtype                              */
+  int32_t tokens;
+  int32_t batch;
+  int32_t heads_count;
+  int32_t width;
+  int32_t head_dim;
+  int32_t src_dtype;
+  int32_t dst_dtype;
+} mf_heads_to_rows_args;
+
+int mf_heads_to_rows(const mf_heads_to_rows_args* args, void* stream);
 
 #ifdef __cplusplus
 }

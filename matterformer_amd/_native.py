@@ -44,9 +44,12 @@ EXPORTED_SYMBOLS = (
     "mf_radius_mask",
     "mf_geometry_features",
     "mf_radius_attn",
+    "mf_adaln_rows",
+    "mf_rows_to_heads",
+    "mf_heads_to_rows",
 )
 
-EXPECTED_ABI_VERSION = 4
+EXPECTED_ABI_VERSION = 5
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -168,6 +171,22 @@ class MfRadiusAttnArgs(ctypes.Structure):
     ]
 
 
+class MfAdalnRowsArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("x", "y", "gate", "shift", "scale", "mol", "x_out", "h_out")] + [
+        ("eps", ctypes.c_float)] + [(n, ctypes.c_int32) for n in ("tokens", "channels", "batch", "mod_stride", "dtype")]
+
+
+class MfRowsToHeadsArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("rows", "slot", "heads")] + [("first_part_scale", ctypes.c_float)] + [
+        (n, ctypes.c_int32) for n in ("tokens", "parts", "batch", "heads_count", "width", "head_dim", "src_dtype",
+                                      "dst_dtype")]
+
+
+class MfHeadsToRowsArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("heads", "row_index", "rows")] + [
+        (n, ctypes.c_int32) for n in ("tokens", "batch", "heads_count", "width", "head_dim", "src_dtype", "dst_dtype")]
+
+
 _LIB: ctypes.CDLL | None = None
 _LOAD_ERROR: str | None = None
 
@@ -196,6 +215,9 @@ def _load() -> ctypes.CDLL | None:
         ("mf_radius_mask", MfRadiusMaskArgs),
         ("mf_geometry_features", MfGeometryArgs),
         ("mf_radius_attn", MfRadiusAttnArgs),
+        ("mf_adaln_rows", MfAdalnRowsArgs),
+        ("mf_rows_to_heads", MfRowsToHeadsArgs),
+        ("mf_heads_to_rows", MfHeadsToRowsArgs),
     ):
         fn = getattr(lib, name, None)
         if fn is not None:

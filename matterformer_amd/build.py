@@ -43,6 +43,7 @@ PER_FILE_FLAGS = {
     "knn.hip": ["-ffp-contract=off"],
     "radius.hip": ["-ffp-contract=off"],
     "geometry.hip": ["-ffp-contract=off"],
+    "token_rows.hip": ["-ffp-contract=off"],
 }
 
 

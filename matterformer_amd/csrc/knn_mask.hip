@@ -9,7 +9,7 @@
 //   mask[b, i, j] = valid_i && (j in idx[b, i, :] || (include_self && j == i))
 // Integer work only; two small launches:
 //   words   one thread per (b, i, 32-column word): scans the k indices of row i
-//   blocks  one thread per (b, 64-row block, 64-column block): OR of its words
+//   blocks  one wave per (b, 64-row block, 64-column block): OR of its words
 #include <algorithm>
 
 #include "mf_common.h"
@@ -41,23 +41,27 @@ __global__ void __launch_bounds__(kThreads) words_kernel(const int32_t* __restri
   }
 }
 
+// One wave per (b, 64-row block, 64-column block): lane r ORs the (at most
+// two) words of row 64*bi + r that cover the column block, then one ballot.
 __global__ void __launch_bounds__(kThreads) blocks_kernel(const uint32_t* __restrict__ bits,
                                                           uint8_t* __restrict__ block_mask, int B, int N, int W,
                                                           int NB) {
   const long long total = (long long)B * NB * NB;
-  for (long long t = (long long)blockIdx.x * kThreads + threadIdx.x; t < total;
-       t += (long long)gridDim.x * kThreads) {
+  const int lane = threadIdx.x & 63;
+  for (long long t = (long long)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); t < total;
+       t += (long long)gridDim.x * (kThreads / 64)) {
     const int bj = int(t % NB);
     const int bi = int((t / NB) % NB);
     const long long b = t / ((long long)NB * NB);
-    const int r1 = min(N, 64 * bi + 64);
-    const int w0 = 2 * bj, w1 = min(W, 2 * bj + 2);
+    const int r = 64 * bi + lane;
     uint32_t any = 0;
-    for (int r = 64 * bi; r < r1; ++r) {
+    if (r < N) {
       const uint32_t* row = bits + ((long long)b * N + r) * W;
-      for (int w = w0; w < w1; ++w) any |= row[w];
+      any = row[2 * bj];
+      if (2 * bj + 1 < W) any |= row[2 * bj + 1];
     }
-    block_mask[t] = any != 0 ? 1 : 0;
+    const unsigned long long hit = __ballot(any != 0);
+    if (lane == 0) block_mask[t] = hit != 0 ? 1 : 0;
   }
 }
 
@@ -84,7 +88,7 @@ extern "C" int mf_knn_mask(const mf_knn_mask_args* a, void* stream) {
   MF_HIP_CHECK(hipGetLastError());
   if (a->block_mask) {
     const long long tiles = (long long)B * NB * NB;
-    const int grid2 = int(std::min<long long>((tiles + kThreads - 1) / kThreads, (long long)dev.num_cus * 16));
+    const int grid2 = int(std::min<long long>((tiles + 3) / 4, (long long)dev.num_cus * 16));
     hipLaunchKernelGGL(blocks_kernel, dim3(grid2), dim3(kThreads), 0, s, a->mask_bits, a->block_mask, B, N, W, NB);
     MF_HIP_CHECK(hipGetLastError());
   }

@@ -44,3 +44,79 @@ def test_torch_path_matches_reference_blocks():
     with torch.no_grad():
         out = trunk(x, cond, coords, pad)
     assert valid_rel_err(out.numpy(), z) <= 1e-5
+
+
+def test_token_packing_round_trips():
+    from matterformer_amd.trunk import TokenPacking
+
+    gen = torch.Generator().manual_seed(3)
+    B, N, C, H, D = 3, 7, 10, 2, 8
+    pad = torch.rand(B, N, generator=gen) < 0.4
+    pad[1] = True  # a molecule with no valid atom
+    pad[2, 0] = False
+    p = TokenPacking(pad)
+    valid = [(b, n) for b in range(B) for n in range(N) if not pad[b, n]]
+    W = int((~pad).sum(1).max())
+    assert p.tokens == len(valid) and p.width == W
+    pos = {}
+    for b, n in valid:
+        pos[(b, n)] = sum(1 for m in range(n) if not pad[b, m])
+    assert [(int(m), int(r) % N) for m, r in zip(p.mol, p.rows)] == valid
+    assert [int(q) for q in p.pos] == [pos[v] for v in valid]
+    assert torch.equal(p.compact_pad_mask, torch.arange(W)[None, :] >= (~pad).sum(1)[:, None])
+    x = torch.randn(B, N, C, generator=gen)
+    xp = p.pack(x)
+    assert torch.equal(xp, torch.stack([x[b, n] for b, n in valid]))
+    back = p.unpack(xp)
+    assert torch.equal(back[~pad], x[~pad]) and not back[pad].any()
+    xc = p.compact(x)
+    assert xc.shape == (B, W, C)
+    for b, n in valid:
+        assert torch.equal(xc[b, pos[(b, n)]], x[b, n])
+    assert not xc[p.compact_pad_mask].any()
+    per_mol = torch.randn(B, C, generator=gen)
+    assert torch.equal(p.per_token(per_mol), torch.stack([per_mol[b] for b, _ in valid]))
+    proj = torch.randn(p.tokens, 3 * H * D, generator=gen)
+    heads = p.to_heads(proj, 3, H, D, torch.float64, first_part_scale=0.5)
+    assert heads.shape == (3, B, H, W, D) and heads.dtype == torch.float64
+    for t, (b, n) in enumerate(valid):
+        want = proj[t].view(3, H, D).double().clone()
+        want[0] = (proj[t].view(3, H, D)[0] * 0.5).double()
+        assert torch.equal(heads[:, b, :, pos[(b, n)], :], want)
+    assert not heads.permute(1, 3, 0, 2, 4)[p.compact_pad_mask].any()
+    assert torch.equal(p.from_heads(heads[1]), proj[:, H * D:2 * H * D].double())
+
+
+def test_adaln_rows_torch_expressions():
+    """adaln_rows (CPU path) is transformer.py:296-316's torch expressions on the packed rows."""
+    from matterformer_amd.token_packing import adaln_rows
+    from matterformer_amd.trunk import TokenPacking
+
+    gen = torch.Generator().manual_seed(5)
+    B, N, C = 3, 6, 16
+    pad = torch.rand(B, N, generator=gen) < 0.3
+    p = TokenPacking(pad)
+    for dtype in (torch.float32, torch.bfloat16):
+        x = torch.randn(B, N, C, generator=gen).to(dtype)
+        y = torch.randn(B, N, C, generator=gen).to(dtype)
+        mods = (torch.randn(B, 6 * C, generator=gen) * 0.3).to(dtype)
+        sh, sc, g = mods[:, :C], mods[:, C:2 * C], mods[:, 2 * C:3 * C]
+        xr = x + g[:, None, :] * y
+        hr = torch.nn.functional.layer_norm(xr, (C,), eps=1e-6) * (1.0 + sc[:, None, :]) + sh[:, None, :]
+        xo, h = adaln_rows(p, p.pack(x), p.pack(y), gate=g, shift=sh, scale=sc, eps=1e-6)
+        assert torch.equal(xo, xr[~pad]) and torch.equal(h, hr[~pad])
+        only_h = adaln_rows(p, p.pack(x), shift=sh, scale=sc, eps=1e-6)
+        hx = torch.nn.functional.layer_norm(x, (C,), eps=1e-6) * (1.0 + sc[:, None, :]) + sh[:, None, :]
+        assert torch.equal(only_h, hx[~pad])
+        assert torch.equal(adaln_rows(p, p.pack(x), p.pack(y), gate=g), xr[~pad])
+
+
+def test_torch_path_zeroes_padded_rows():
+    """transformer.py:1298-1316: the trunk output is zero on padded atoms."""
+    z = load()
+    trunk = build_trunk(z, local_impl="torch", simplicial_impl="torch")
+    x, cond, coords, pad = inputs(z)
+    with torch.no_grad():
+        out = trunk(x[:2], cond[:2], coords[:2], pad[:2])
+    assert not out[pad[:2]].any()
+    assert out[~pad[:2]].abs().sum() > 0
