@@ -275,7 +275,7 @@ def measure_knn(cpu_sample: int) -> dict:
         "queries_per_s": round(sc["queries"] / (sc["ms"] * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("knn_c3_scaled"),
-                     "kernel": "mf::knn::knn_block_kernel<16, 1>", "kernel_ms": round(sc["ms"], 5),
+                     "kernel": "mf::knn::knn_code_kernel<16, 1>", "kernel_ms": round(sc["ms"], 5),
                      "algorithmic_bytes": sc["bytes"]},
         "cpu_baseline": cpu,
     }

@@ -116,6 +116,58 @@ def test_knn_scaled_batch_properties(cuda):
     np.testing.assert_array_equal(dist[sample].cpu().numpy(), rdist)
 
 
+def _near_tie_molecules(B, N, seed):
+    """Atom 0 of every molecule has a shell of 40 atoms whose squared distances lie within 2^-18 of 1 (below
+    the 2^-16 resolution of the 32-bit key codes), and two exact duplicates of atom 5; the rest are random."""
+    gen = torch.Generator().manual_seed(seed)
+    coords = torch.randn(B, N, 3, generator=gen, dtype=torch.float64) * math.sqrt(2.0)
+    dirs = torch.randn(B, 40, 3, generator=gen, dtype=torch.float64)
+    dirs = dirs / dirs.norm(dim=-1, keepdim=True)
+    radius = torch.sqrt(1.0 + torch.rand(B, 40, 1, generator=gen, dtype=torch.float64) * 2.0 ** -18)
+    coords[:, 0] = 0.0
+    coords[:, 1:41] = dirs * radius
+    coords[:, 41] = coords[:, 5]
+    coords[:, 42] = coords[:, 5]
+    return coords.float()
+
+
+@pytest.mark.parametrize("B,k", [(6, 16), (6, 10), (6, 8), (1500, 16)])
+def test_knn_near_ties_match_oracle(cuda, B, k):
+    """Squared distances that agree to 2^-18 and duplicate atoms: the code-key kernel (molecules of <= 256
+    atoms) must detect every shared code at the k-th position and still return the oracle's lists bit for
+    bit.  B=1500 runs the 32-bit code kernel (one lane per query), B=6 the 64-bit block kernel (sixteen)."""
+    print(f"knn near ties B={B} k={k}", flush=True)
+    N = 181
+    coords = _near_tie_molecules(B, N, 77 + k)
+    idx, dist = knn_graph(coords.to(cuda), k)
+    torch.cuda.synchronize()
+    rows = list(range(B)) if B <= 8 else list(range(0, B, 97))
+    ridx, rdist = oracle_knn(coords[rows].numpy(), k)
+    np.testing.assert_array_equal(idx[rows].cpu().numpy(), ridx)
+    np.testing.assert_array_equal(dist[rows].cpu().numpy().view(np.uint32), rdist.view(np.uint32))
+
+
+@pytest.mark.parametrize("B,N,k,pad_kind,excl", [(1500, 181, 16, "holes", False), (7200, 37, 8, "tail", True),
+                                                  (1100, 256, 12, None, True), (2700, 100, 16, "holes", True)])
+def test_knn_code_kernel_matches_oracle(cuda, B, N, k, pad_kind, excl):
+    """Batches of >= 262144 queries take the code kernel (one lane per query, molecules of <= 256 atoms,
+    queries flattened across molecules); every 53rd molecule against the oracle, bit for bit."""
+    print(f"knn code kernel B={B} N={N} k={k} pad={pad_kind} exclude_self={excl}", flush=True)
+    gen = torch.Generator().manual_seed(2000 + N + k)
+    coords = torch.randn(B, N, 3, generator=gen) * math.sqrt(2.0)
+    pad = None
+    if pad_kind == "tail":
+        pad = torch.arange(N)[None, :] >= torch.randint(1, N + 1, (B, 1), generator=gen)
+    elif pad_kind == "holes":
+        pad = torch.rand(B, N, generator=gen) < 0.2
+    idx, dist = knn_graph(coords.to(cuda), k, None if pad is None else pad.to(cuda), exclude_self=excl)
+    torch.cuda.synchronize()
+    rows = list(range(0, B, 53)) + [B - 1]
+    ridx, rdist = oracle_knn(coords[rows].numpy(), k, None if pad is None else pad[rows].numpy(), exclude_self=excl)
+    np.testing.assert_array_equal(idx[rows].cpu().numpy(), ridx)
+    np.testing.assert_array_equal(dist[rows].cpu().numpy().view(np.uint32), rdist.view(np.uint32))
+
+
 # ----------------------------------------------------------------------------- radius mask
 
 def _cells(B, seed, lo=8.0, hi=12.0, amin=80.0, amax=100.0):
