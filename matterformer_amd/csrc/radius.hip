@@ -246,8 +246,17 @@ __global__ void __launch_bounds__(256) radius_mask_kernel(Params p) {
   // (d2(i, j) and d2(j, i) are the same fp32 value: e negates exactly and the
   // image set is symmetric), so the workgroup also writes tile (tj, ti).
   // Row ti of the triangle starts at index ti NT - ti (ti - 1) / 2.
-  const int b = blockIdx.y;
-  const long long nt = p.NT, t = blockIdx.x;
+  // XCD-aware order: consecutive workgroups land on different XCDs (linear
+  // id % 8), so the logical unit is remapped to give each XCD whole cells;
+  // a cell's row pieces (its tiles and their mirrors write 8- and 4-byte
+  // pieces of shared 64-byte rows) then merge in one L2 before they reach
+  // HBM.
+  const long long tiles = (long long)p.NT * (p.NT + 1) / 2;
+  const long long grid = (long long)gridDim.x;
+  const long long unit = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
+  if (unit >= tiles * p.B) return;  // grid padding (whole workgroup)
+  const int b = int(unit / tiles);
+  const long long nt = p.NT, t = unit - (long long)b * tiles;
   auto row_start = [nt](long long r) { return r * nt - r * (r - 1) / 2; };
   const double q = double(2 * nt + 1);
   long long r0 = static_cast<long long>((q - sqrt(q * q - 8.0 * double(t))) * 0.5);
@@ -385,7 +394,8 @@ __global__ void __launch_bounds__(256) radius_mask_kernel(Params p) {
 
 template <int BLOCK, int MODE>
 int launch(const Params& p, hipStream_t stream) {
-  const dim3 grid(p.NT * (p.NT + 1) / 2, p.B);
+  const long long units = (long long)p.NT * (p.NT + 1) / 2 * p.B;
+  const dim3 grid(unsigned((units + 7) / 8 * 8));  // a multiple of 8 (one share per XCD)
   hipLaunchKernelGGL((radius_mask_kernel<BLOCK, MODE>), grid, dim3(256), 0, stream, p);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
@@ -418,7 +428,7 @@ extern "C" int mf_radius_mask(const mf_radius_mask_args* a, void* stream) {
   const long long nb = (a->atoms + a->block - 1) / a->block;
   const int tile = a->block < 64 ? 64 : a->block;
   const long long nt = (a->atoms + tile - 1) / tile;
-  if (a->batch > 65535 || nt * (nt + 1) / 2 > 0x7fffffffLL)
+  if (a->batch > 65535 || nt * (nt + 1) / 2 * a->batch > 0x7ffffff0LL)
     return fail(MF_ERR_UNSUPPORTED, "mf_radius_mask: batch or atom count too large");
   radius::Params p{a->coords, a->gram, a->pad_mask, a->mask_bits, a->block_mask,
                    a->cutoff * a->cutoff, a->batch, a->atoms, (a->atoms + 31) / 32, static_cast<int>(nb),
