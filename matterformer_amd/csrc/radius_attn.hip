@@ -327,6 +327,18 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
 // ---------------------------------------------------------------------------
 constexpr int kThreads2 = 512;
 
+// ds_read_b64_tr_b16 (gfx950): four 16-bit elements, transposed across each
+// group of 16 lanes (see the V^T operand read below).  p must be 8-byte
+// aligned LDS.
+template <typename T>
+__device__ __forceinline__ auto read_tr16(const T* p) {
+  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T Op4;
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4*)(reinterpret_cast<uintptr_t>(p)));
+  return __builtin_bit_cast(Op4, v);
+}
+
 // POS: scale > 0.  The running maximum is then taken over the unscaled
 // masked logits (scaling preserves the order) and p = exp2(s scale - m) is
 // one fma per logit.
@@ -335,7 +347,6 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
   using Op8 = typename Ops<T>::Op8;
   typedef __attribute__((__vector_size__(4 * sizeof(T)))) T Op4;
   constexpr int KS = D + 8;         // K row stride in LDS (elements)
-  constexpr int VS = kTile + 8;     // V^T row stride in LDS (elements)
   constexpr int DK = D / 32;        // K steps of S^T
   constexpr int ND = D / 16;        // d tiles of O^T
   constexpr int CPR = D / 8;        // 16-byte chunks per row
@@ -345,7 +356,7 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
   static_assert(4 * 64 * CW * 4 <= int(sizeof(T)) * 2 * 2 * kTile * KS, "combine area");
 
   __shared__ __attribute__((aligned(16))) T Ks[2][2][kTile * KS];  // [buffer][stream]
-  __shared__ __attribute__((aligned(16))) T VT[2][2][D * VS];
+  __shared__ __attribute__((aligned(16))) T Vs[2][2][kTile * KS];  // V row-major, read transposed
   __shared__ int s_tiles[2][kMaxTiles / 2];  // active tiles of each parity, in order
   __shared__ int s_ntiles[2];
 
@@ -398,20 +409,17 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
   const int nsteps = max(s_ntiles[0], s_ntiles[1]);
   const int* tiles = s_tiles[kh];
 
-  // register staging of this stream's tile of a step (as in the kernel above;
-  // branch-free loads, rows past N zeroed where stored)
-  // chunk t of a thread: K row c / CPR, columns 8 (c % CPR); V row c % 64,
-  // columns 8 (c / 64) (c = ht + 256 t); offsets within a tile, once
-  int krow[CPT], kgo[CPT], vrow_[CPT], vgo[CPT], kso[CPT], vso[CPT];
+  // register staging of this stream's tile of a step (branch-free loads,
+  // rows past N zeroed where stored): chunk t of a thread is row c / CPR,
+  // columns 8 (c % CPR) (c = ht + 256 t) of both K and V, which are stored
+  // row-major alike; offsets within a tile, once
+  int krow[CPT], kgo[CPT], kso[CPT];
 #pragma unroll
   for (int t = 0; t < CPT; ++t) {
     const int c = ht + t * 256;
     krow[t] = c / CPR;
     kgo[t] = krow[t] * D + (c % CPR) * 8;
-    vrow_[t] = c % kTile;
-    vgo[t] = vrow_[t] * D + (c / kTile) * 8;
     kso[t] = krow[t] * KS + (c % CPR) * 8;
-    vso[t] = (c / kTile) * 8 * VS + vrow_[t];
   }
   struct Stage {
     Op8 k[CPT], v[CPT];
@@ -436,39 +444,37 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
 #pragma unroll
       for (int t = 0; t < CPT; ++t) {
         st.k[t] = *reinterpret_cast<const Op8*>(kb + kgo[t]);
-        st.v[t] = *reinterpret_cast<const Op8*>(vb + vgo[t]);
+        st.v[t] = *reinterpret_cast<const Op8*>(vb + kgo[t]);
       }
     } else {
       // rows past N read row N - 1 (zeroed when stored)
 #pragma unroll
       for (int t = 0; t < CPT; ++t) {
-        st.k[t] = *reinterpret_cast<const Op8*>(gk + size_t(min(key0 + krow[t], N - 1)) * D + (kgo[t] - krow[t] * D));
-        st.v[t] = *reinterpret_cast<const Op8*>(gv + size_t(min(key0 + vrow_[t], N - 1)) * D + (vgo[t] - vrow_[t] * D));
+        const size_t off = size_t(min(key0 + krow[t], N - 1)) * D + (kgo[t] - krow[t] * D);
+        st.k[t] = *reinterpret_cast<const Op8*>(gk + off);
+        st.v[t] = *reinterpret_cast<const Op8*>(gv + off);
       }
     }
   };
   auto store_tile = [&](const Stage& st, int buf) {
     T* kd = Ks[buf][kh];
-    T* vd = VT[buf][kh];
+    T* vd = Vs[buf][kh];
     if (st.full) {
 #pragma unroll
       for (int t = 0; t < CPT; ++t) {
         *reinterpret_cast<Op8*>(kd + kso[t]) = st.k[t];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vd[vso[t] + e * VS] = st.v[t][e];
+        *reinterpret_cast<Op8*>(vd + kso[t]) = st.v[t];
       }
     } else {
 #pragma unroll
       for (int t = 0; t < CPT; ++t) {
-        Op8 kz = st.k[t];
+        Op8 kz = st.k[t], vz = st.v[t];
         if (st.key0 + krow[t] >= N) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) kz[e] = T(0.0f);
+          for (int e = 0; e < 8; ++e) kz[e] = vz[e] = T(0.0f);
         }
         *reinterpret_cast<Op8*>(kd + kso[t]) = kz;
-        const bool vok = st.key0 + vrow_[t] < N;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vd[vso[t] + e * VS] = vok ? st.v[t][e] : T(0.0f);
+        *reinterpret_cast<Op8*>(vd + kso[t]) = vz;
       }
     }
   };
@@ -492,7 +498,7 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
     const int buf = s & 1;
     if (s < ntiles) {
       const T* Kt = Ks[buf][kh];
-      const T* VTt = VT[buf][kh];
+      const T* Vt = Vs[buf][kh];
       float sv[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
@@ -551,13 +557,20 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
         }
       }
       l += psum;
+      // V^T operands straight from the row-major tile: within each group of
+      // 16 lanes, ds_read_b64_tr_b16 hands lane 4a + c element c of the
+      // 8-byte pieces addressed by lanes 4e + a (e = 0..3).  Lane 4e + a
+      // addresses key 32 pr + 4 g + e (+16 for the second read), columns
+      // 16 nd + 4a .. +3, so lane r16 receives V[keys 32 pr + 4 g + 0..3]
+      // [d = 16 nd + r16]: the key order of the P^T operand.
+      const T* vt0 = Vt + (4 * g + (r16 >> 2)) * KS + 4 * (r16 & 3);
 #pragma unroll
       for (int nd = 0; nd < ND; ++nd) {
 #pragma unroll
         for (int pr = 0; pr < 2; ++pr) {
-          const T* vrow = VTt + (16 * nd + r16) * VS + 32 * pr + 4 * g;
-          const Op4 lo = *reinterpret_cast<const Op4*>(vrow);
-          const Op4 hi = *reinterpret_cast<const Op4*>(vrow + 16);
+          const T* vp = vt0 + 32 * pr * KS + 16 * nd;
+          const Op4 lo = read_tr16<T>(vp);
+          const Op4 hi = read_tr16<T>(vp + 16 * KS);
           const Op8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
           acc[nd] = Ops<T>::mma(a, pb[pr], acc[nd]);
         }
