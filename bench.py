@@ -326,6 +326,39 @@ def measure_radius(cpu_sample: int) -> dict:
     }
 
 
+def measure_geometry() -> dict:
+    """The one-pass geometry features (mf_geometry_features behind the mirrored adapters): configs[3]'s
+    periodic cells (27 images, with the 6 A cutoff bits) and configs[1]'s GEOM molecules (non-periodic),
+    graph-replayed, against the HBM roofline of the pair tensors they write (delta, d2, d, d_norm in fp32,
+    plus the bits)."""
+    import torch
+
+    from matterformer_amd.geometry import NonPeriodicGeometryAdapter, PeriodicGeometryAdapter
+    from matterformer_amd.workloads import radius_workload, simplicial_workload
+
+    dev = torch.device("cuda", 0)
+    rw = radius_workload()
+    frac, lat = rw.frac.to(dev), rw.lattice.to(dev)
+    sw = simplicial_workload("geom")
+    N = sw.q.shape[2]
+    pad = (torch.arange(N)[None, :] >= sw.counts[:, None]).to(dev)
+    coords = (torch.randn(pad.shape[0], N, 3, generator=torch.Generator().manual_seed(5)) * 2.0 ** 0.5).to(dev)
+    cases = (("c4_periodic_cells", PeriodicGeometryAdapter(pbc_radius=1).to(dev), (frac, None, lat),
+              {"radius_cutoff": rw.cutoff}),
+             ("c2_geom_molecules", NonPeriodicGeometryAdapter().to(dev), (coords, pad), {}))
+    res = {}
+    with torch.no_grad():
+        for name, adapter, args, kw in cases:
+            B, n = args[0].shape[:2]
+            ms = _graph_ms(lambda: adapter(*args, **kw), per_graph=10, replays=5)  # noqa: B023
+            nbytes = B * n * n * 6 * 4 + (B * n * ((n + 31) // 32) * 4 if kw else 0)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            res[name] = {"ms": round(ms, 5), "batch": B, "atoms": n, "output_bytes": nbytes,
+                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                      "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    return res
+
+
 def measure_trunk() -> dict:
     """12-layer alternating trunk forward, bf16 weights and activations, 64 GEOM molecules."""
     import torch
@@ -569,6 +602,7 @@ def main() -> int:
         extra["knn"] = measure_knn(args.cpu_sample)
         extra["radius"] = measure_radius(args.cpu_sample)
         extra["c5_trunk"] = measure_trunk()
+        extra["geometry_features"] = measure_geometry()
 
     cpu = cpu_baseline(w, args.cpu_sample, args.cpu_threads) if args.cpu_sample > 0 else None
 
