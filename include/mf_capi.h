@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 5
+#define MF_ABI_VERSION 6
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -439,6 +439,49 @@ typedef struct mf_heads_to_rows_args {
 } mf_heads_to_rows_args;
 
 int mf_heads_to_rows(const mf_heads_to_rows_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Factorized simplicial geometry bias from the adapters' pair features      */
+/* (SimplicialGeometryBias._compute_factorized_terms, transformer.py:702-717, */
+/* with the MLPs of :566-584 and the rbf of :637-640):                        */
+/*   spoke x_s = [delta (3), rbf(d_norm) (R)],  pair x_p = rbf(d_norm),       */
+/*   rbf_r(x)  = exp(-gamma (x - c_r)^2),                                     */
+/*   u = MLP_u(x_s), v = MLP_v(x_s), w = MLP_w(x_p),                          */
+/*   MLP(x)    = W2 SiLU(W1 x + b1) + b2   (H outputs),                       */
+/* written as [B, H, N, N] fp32 with the diagonal and the pairs outside      */
+/* pair_mask zero.  W1 [hidden, F] row-major (F = 3 + R or R), W2 [H, hidden]. */
+/* fp32 throughout (fp32 MFMA).  R <= 29, hidden a multiple of 16 <= 256,    */
+/* H <= 16.                                                                   */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_pair_mlp_args {
+  const float* pair_delta;      /* [B, N, N, 3]                               */
+  const float* pair_dist_norm;  /* [B, N, N]                                  */
+  const uint8_t* pair_mask;     /* [B, N, N] bytes, nonzero = valid pair      */
+  const float* rbf_centers;     /* [R]                                        */
+  float rbf_gamma;
+  const float* u_w1;            /* [hidden, 3 + R] */
+  const float* u_b1;            /* [hidden]        */
+  const float* u_w2;            /* [H, hidden]     */
+  const float* u_b2;            /* [H]             */
+  const float* v_w1;
+  const float* v_b1;
+  const float* v_w2;
+  const float* v_b2;
+  const float* w_w1;            /* [hidden, R]     */
+  const float* w_b1;
+  const float* w_w2;
+  const float* w_b2;
+  float* u_out;                 /* [B, H, N, N]    */
+  float* v_out;
+  float* w_out;
+  int32_t batch;
+  int32_t atoms;
+  int32_t rbf;
+  int32_t hidden;
+  int32_t heads;
+} mf_pair_mlp_args;
+
+int mf_pair_mlp_bias(const mf_pair_mlp_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -47,9 +47,10 @@ EXPORTED_SYMBOLS = (
     "mf_adaln_rows",
     "mf_rows_to_heads",
     "mf_heads_to_rows",
+    "mf_pair_mlp_bias",
 )
 
-EXPECTED_ABI_VERSION = 5
+EXPECTED_ABI_VERSION = 6
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -187,6 +188,13 @@ class MfHeadsToRowsArgs(ctypes.Structure):
         (n, ctypes.c_int32) for n in ("tokens", "batch", "heads_count", "width", "head_dim", "src_dtype", "dst_dtype")]
 
 
+class MfPairMlpArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("pair_delta", "pair_dist_norm", "pair_mask", "rbf_centers")] + [
+        ("rbf_gamma", ctypes.c_float)] + [(f"{m}_{t}", ctypes.c_void_p) for m in "uvw" for t in ("w1", "b1", "w2", "b2")] + [
+        (n, ctypes.c_void_p) for n in ("u_out", "v_out", "w_out")] + [
+        (n, ctypes.c_int32) for n in ("batch", "atoms", "rbf", "hidden", "heads")]
+
+
 _LIB: ctypes.CDLL | None = None
 _LOAD_ERROR: str | None = None
 
@@ -218,6 +226,7 @@ def _load() -> ctypes.CDLL | None:
         ("mf_adaln_rows", MfAdalnRowsArgs),
         ("mf_rows_to_heads", MfRowsToHeadsArgs),
         ("mf_heads_to_rows", MfHeadsToRowsArgs),
+        ("mf_pair_mlp_bias", MfPairMlpArgs),
     ):
         fn = getattr(lib, name, None)
         if fn is not None:

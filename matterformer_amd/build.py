@@ -44,6 +44,7 @@ PER_FILE_FLAGS = {
     "radius.hip": ["-ffp-contract=off"],
     "geometry.hip": ["-ffp-contract=off"],
     "token_rows.hip": ["-ffp-contract=off"],
+    "pair_mlp.hip": ["-ffp-contract=off"],
 }
 
 

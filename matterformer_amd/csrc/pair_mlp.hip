@@ -1,0 +1,272 @@
+// Factorized simplicial geometry bias in one pass (mf_pair_mlp_bias) on
+// gfx950: the three pairwise MLPs of SimplicialGeometryBias
+// (src/matterformer/models/transformer.py:566-584,702-717)
+//
+//   u = MLP_u([delta, rbf(d_norm)]),  v = MLP_v([delta, rbf(d_norm)]),
+//   w = MLP_w(rbf(d_norm)),           MLP = Linear -> SiLU -> Linear (H outputs),
+//   rbf_r(x) = exp(-gamma (x - c_r)^2)                       (:637-640)
+//
+// written per head as [B, H, N, N] with the diagonal and the pairs outside
+// the geometry pair mask zero (:711-717).  The reference materialises the
+// [B, N, N, F] features and the [B, N, N, hidden] activations of each MLP;
+// here one wave takes 16 pairs (molecule b, row i, columns j0..j0+15) and
+// keeps everything in registers:
+//
+//   layer 1  C1[h][p] = b1[h] + sum_f W1[h][f] X[p][f]    fp32 MFMA 16x16x4,
+//            M = 16 hidden units, N = 16 pairs, K = 4 features per step;
+//            lane (g, r16) computes features g, g+4, ... of pair r16 itself
+//   SiLU     on the accumulators
+//   layer 2  C2[o][p] = b2[o] + sum_h W2[o][h] SiLU(C1[h][p])
+//            the layer-1 accumulators ARE the layer-2 B operands: lane
+//            (g, r16) holds hidden units 16 t + 4 g + r of pair r16, so the
+//            K step (t, r) takes h = 16 t + 4 g + r with W2 read in the
+//            same order
+//
+// The weights of the three MLPs are staged in LDS once per workgroup (rows
+// padded to an odd stride).  Chunks with no valid pair are written as zeros
+// without any arithmetic.  fp32 throughout; this file is built without FMA
+// contraction so the rbf features round as torch's expression does.
+#include <algorithm>
+#include <cmath>
+
+#include "mf_common.h"
+
+namespace mf {
+namespace pmlp {
+
+constexpr int kThreads = 256;
+constexpr int kMaxHidden = 256;
+constexpr int kMaxHeads = 16;
+constexpr int kMaxRbf = 29;  // spoke features 3 + R <= 32
+
+struct Params {
+  const float* delta;
+  const float* dnorm;
+  const uint8_t* mask;
+  const float* centers;
+  float neg_gamma;
+  const float* w1[3];
+  const float* b1[3];
+  const float* w2[3];
+  const float* b2[3];
+  float* out[3];
+  int B, N, R, hidden, heads, chunks;
+};
+
+__device__ __forceinline__ mf_f32x4 mma(float a, float b, mf_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// K4: 4-wide K steps of layer 1 for the spoke (u, v) and pair (w) features.
+template <int KS, int KP>
+__global__ void __launch_bounds__(kThreads, 2) pair_mlp_kernel(Params p) {
+  extern __shared__ float lds[];
+  const int hidden = p.hidden, H = p.heads;
+  const int HT = hidden / 16;
+  // per MLP m: W1 [hidden][s1] (K padded with zeros), b1 [hidden], W2 [16][s2] (rows >= H zero), b2 [16]
+  const int s1s = 4 * KS + 1, s1p = 4 * KP + 1, s2 = hidden + 1;
+  int off[3][4];
+  {
+    int o = 0;
+    for (int m = 0; m < 3; ++m) {
+      const int s1 = m < 2 ? s1s : s1p;
+      off[m][0] = o;
+      o += hidden * s1;
+      off[m][1] = o;
+      o += hidden;
+      off[m][2] = o;
+      o += 16 * s2;
+      off[m][3] = o;
+      o += 16;
+    }
+  }
+  const int tid = threadIdx.x;
+  for (int m = 0; m < 3; ++m) {
+    const int fin = m < 2 ? 3 + p.R : p.R;  // true input width
+    const int s1 = m < 2 ? s1s : s1p;
+    const int kw = 4 * (m < 2 ? KS : KP);
+    for (int e = tid; e < hidden * kw; e += kThreads) {
+      const int h = e / kw, f = e - h * kw;
+      lds[off[m][0] + h * s1 + f] = f < fin ? p.w1[m][h * fin + f] : 0.0f;
+    }
+    for (int e = tid; e < hidden; e += kThreads) lds[off[m][1] + e] = p.b1[m][e];
+    for (int e = tid; e < 16 * hidden; e += kThreads) {
+      const int o = e / hidden, h = e - o * hidden;
+      lds[off[m][2] + o * s2 + h] = o < H ? p.w2[m][o * hidden + h] : 0.0f;
+    }
+    for (int e = tid; e < 16; e += kThreads) lds[off[m][3] + e] = e < H ? p.b2[m][e] : 0.0f;
+  }
+  __syncthreads();
+
+  const int lane = tid & 63, g = lane >> 4, r16 = lane & 15;
+  const int N = p.N;
+  const long long units = (long long)p.B * N * p.chunks;
+  const size_t plane = size_t(N) * N;
+  for (long long u = (long long)blockIdx.x * (kThreads / 64) + (tid >> 6); u < units;
+       u += (long long)gridDim.x * (kThreads / 64)) {
+    const int jc = int(u % p.chunks);
+    const long long row = u / p.chunks;  // b * N + i
+    const int i = int(row % N);
+    const int b = int(row / N);
+    const int j = jc * 16 + r16;
+    const bool in = j < N;
+    const size_t pair = size_t(row) * N + (in ? j : 0);
+    const bool valid = in && j != i && p.mask[pair] != 0;
+    const unsigned long long any = __ballot(valid);
+    // output element (o, b, i, j): ((b * H + o) * N + i) * N + j
+    const size_t obase = size_t(b) * H * plane + size_t(i) * N + j;
+    if (any == 0ull) {
+      if (in && g == 0) {
+        for (int m = 0; m < 3; ++m)
+          for (int o = 0; o < H; ++o) p.out[m][obase + size_t(o) * plane] = 0.0f;
+      }
+      continue;
+    }
+    // features of pair r16: lane g takes f = g, g + 4, ...
+    float xs[KS], xp[KP];
+    const float dn = in ? p.dnorm[pair] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      const int f = 4 * t + g;
+      float v = 0.0f;
+      if (f < 3) {
+        v = in ? p.delta[3 * pair + f] : 0.0f;
+      } else if (f < 3 + p.R) {
+        const float d = dn - p.centers[f - 3];
+        const float sq = d * d;
+        v = expf(p.neg_gamma * sq);
+      }
+      xs[t] = v;
+    }
+#pragma unroll
+    for (int t = 0; t < KP; ++t) {
+      const int f = 4 * t + g;
+      float v = 0.0f;
+      if (f < p.R) {
+        const float d = dn - p.centers[f];
+        const float sq = d * d;
+        v = expf(p.neg_gamma * sq);
+      }
+      xp[t] = v;
+    }
+    for (int m = 0; m < 3; ++m) {
+      const float* W1 = lds + off[m][0];
+      const float* B1 = lds + off[m][1];
+      const float* W2 = lds + off[m][2];
+      const float* B2 = lds + off[m][3];
+      const int s1 = m < 2 ? s1s : s1p;
+      mf_f32x4 o2;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o2[r] = B2[4 * g + r];
+      for (int ht = 0; ht < HT; ++ht) {
+        mf_f32x4 c1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) c1[r] = B1[16 * ht + 4 * g + r];
+        const float* wrow = W1 + (16 * ht + r16) * s1 + g;
+        if (m < 2) {
+#pragma unroll
+          for (int t = 0; t < KS; ++t) c1 = mma(wrow[4 * t], xs[t], c1);
+        } else {
+#pragma unroll
+          for (int t = 0; t < KP; ++t) c1 = mma(wrow[4 * t], xp[t], c1);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = c1[r];
+          const float e = expf(-x);
+          const float den = 1.0f + e;
+          const float act = x / den;  // SiLU
+          o2 = mma(W2[r16 * s2 + 16 * ht + 4 * g + r], act, o2);
+        }
+      }
+      if (in) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int o = 4 * g + r;
+          if (o < H) p.out[m][obase + size_t(o) * plane] = valid ? o2[r] : 0.0f;
+        }
+      }
+    }
+  }
+}
+
+size_t lds_bytes(int ks, int kp, int hidden) {
+  const size_t s2 = size_t(hidden) + 1;
+  size_t floats = 0;
+  for (int m = 0; m < 3; ++m) {
+    const size_t s1 = 4 * size_t(m < 2 ? ks : kp) + 1;
+    floats += size_t(hidden) * s1 + hidden + 16 * s2 + 16;
+  }
+  return floats * sizeof(float);
+}
+
+template <int KS, int KP>
+int launch(const Params& p, int num_cus, hipStream_t s) {
+  const size_t lds = lds_bytes(KS, KP, p.hidden);
+  // dynamic LDS above 64 KB needs the attribute (set once per kernel, thread-safe static init)
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(pair_mlp_kernel<KS, KP>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  MF_HIP_CHECK(attr);
+  const long long units = (long long)p.B * p.N * p.chunks;
+  const int grid = int(std::min<long long>((units + 3) / 4, (long long)num_cus * 2));
+  hipLaunchKernelGGL((pair_mlp_kernel<KS, KP>), dim3(grid), dim3(kThreads), lds, s, p);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
+
+}  // namespace pmlp
+}  // namespace mf
+
+extern "C" int mf_pair_mlp_bias(const mf_pair_mlp_args* a, void* stream) {
+  using namespace mf;
+  using namespace mf::pmlp;
+  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias: args is NULL");
+  if (!a->pair_delta || !a->pair_dist_norm || !a->pair_mask || !a->rbf_centers)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias: feature pointers must be non-NULL");
+  const float* const w1[3] = {a->u_w1, a->v_w1, a->w_w1};
+  const float* const b1[3] = {a->u_b1, a->v_b1, a->w_b1};
+  const float* const w2[3] = {a->u_w2, a->v_w2, a->w_w2};
+  const float* const b2[3] = {a->u_b2, a->v_b2, a->w_b2};
+  float* const out[3] = {a->u_out, a->v_out, a->w_out};
+  for (int m = 0; m < 3; ++m)
+    if (!w1[m] || !b1[m] || !w2[m] || !b2[m] || !out[m])
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias: every weight, bias and output must be non-NULL");
+  if (a->batch < 0 || a->atoms < 0) return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias: bad sizes");
+  if (a->rbf < 1 || a->rbf > kMaxRbf)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: rbf features must be in [1, 29]");
+  if (a->hidden < 16 || a->hidden > kMaxHidden || a->hidden % 16 != 0)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: hidden must be a multiple of 16 in [16, 256]");
+  if (a->heads < 1 || a->heads > kMaxHeads)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: heads must be in [1, 16]");
+  if (!std::isfinite(a->rbf_gamma)) return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias: gamma must be finite");
+  if (a->batch == 0 || a->atoms == 0) return MF_OK;
+  DeviceInfo dev;
+  int st = device_info(&dev);
+  if (st != MF_OK) return st;
+  Params p{};
+  p.delta = a->pair_delta;
+  p.dnorm = a->pair_dist_norm;
+  p.mask = a->pair_mask;
+  p.centers = a->rbf_centers;
+  p.neg_gamma = -a->rbf_gamma;
+  for (int m = 0; m < 3; ++m) {
+    p.w1[m] = w1[m];
+    p.b1[m] = b1[m];
+    p.w2[m] = w2[m];
+    p.b2[m] = b2[m];
+    p.out[m] = out[m];
+  }
+  p.B = a->batch;
+  p.N = a->atoms;
+  p.R = a->rbf;
+  p.hidden = a->hidden;
+  p.heads = a->heads;
+  p.chunks = (a->atoms + 15) / 16;
+  const int ks = (3 + a->rbf + 3) / 4, kp = (a->rbf + 3) / 4;
+  if (lds_bytes(ks, kp, a->hidden) > size_t(dev.max_lds_per_block))
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: weights exceed the LDS of a workgroup");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // spoke K steps (3 + R features) and pair K steps (R features)
+  if (ks <= 5 && kp <= 4) return launch<5, 4>(p, dev.num_cus, s);
+  return launch<8, 8>(p, dev.num_cus, s);
+}

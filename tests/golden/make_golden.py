@@ -160,8 +160,37 @@ def trunk_case(transformer, geometry) -> None:
     )
 
 
+def geometry_bias_case(transformer, geometry) -> None:
+    """SimplicialGeometryBias (transformer.py:516-996) on the reference adapter's features, by the procedure of
+    tests/geometry_bias_fixture.py: the low-rank case (factorized u, v, w + angle and message factors) and the
+    dense angle-residual case."""
+    sys.path.insert(0, str(HERE.parent))
+    import geometry_bias_fixture as fx
+
+    coords, pad, sigma = fx.inputs()
+    feats = geometry.NonPeriodicGeometryAdapter()(coords, pad_mask=pad)
+    arrays = dict(coords=coords.numpy(), pad_mask=pad.numpy(), sigma=sigma.numpy(),
+                  pair_delta=feats.pair_delta.numpy(), pair_dist=feats.pair_dist.numpy(),
+                  pair_dist2=feats.pair_dist2.numpy(), pair_dist_norm=feats.pair_dist_norm.numpy(),
+                  pair_mask=feats.pair_mask.numpy(), global_geom=feats.global_geom.numpy())
+    for case in fx.CASES:
+        module, result = fx.build(transformer.SimplicialGeometryBias, case, feats, pad, sigma)
+        for k, v in fx.outputs(result).items():
+            arrays[f"{case}_{k}"] = v
+        arrays[f"{case}_param_checks"] = fx.param_checks(module)
+        arrays[f"{case}_param_names"] = np.array(list(module.state_dict().keys()))
+    np.savez_compressed(fx.GOLDEN, **arrays)
+
+
 def main(reference_root: str) -> None:
     sys.path.insert(0, str(Path(reference_root) / "src"))
+    if len(sys.argv) > 2 and sys.argv[2] == "geometry_bias":
+        import matterformer.geometry.adapters as geometry  # noqa: E402
+        import matterformer.models.transformer as transformer  # noqa: E402
+
+        geometry_bias_case(transformer, geometry)
+        print("wrote the geometry-bias fixture to", HERE)
+        return
     if len(sys.argv) > 2 and sys.argv[2] == "trunk":
         import matterformer.geometry.adapters as geometry  # noqa: E402
         import matterformer.models.transformer as transformer  # noqa: E402

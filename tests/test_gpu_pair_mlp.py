@@ -1,0 +1,120 @@
+"""mf_pair_mlp_bias (the factorized geometry-bias MLPs in one pass) against SimplicialGeometryBias's torch
+formulation: the reference-fixture module and a configs[1]-sized batch.  Bar: fp32 MFMA against the fp32 torch
+GEMMs, max |difference| <= 1e-5 relative to the largest |term| per head (measured ~1e-6); the diagonal and the
+invalid pairs exactly zero."""
+
+import numpy as np
+import pytest
+import torch
+
+import geometry_bias_fixture as fx
+from matterformer_amd import pair_mlp
+from matterformer_amd.geometry import GeometryFeatures, NonPeriodicGeometryAdapter
+from matterformer_amd.geometry_bias import SimplicialGeometryBias
+from test_geometry_bias import _features
+
+pytestmark = pytest.mark.gpu
+
+
+def _to(feats, dev):
+    return GeometryFeatures(pair_delta=feats.pair_delta.to(dev), pair_dist=feats.pair_dist.to(dev),
+                            pair_dist2=feats.pair_dist2.to(dev), pair_dist_norm=feats.pair_dist_norm.to(dev),
+                            pair_mask=feats.pair_mask.to(dev), global_geom=feats.global_geom.to(dev), kind=feats.kind,
+                            extras={k: v.to(dev) for k, v in feats.extras.items()})
+
+
+def _check(got, want, mask):
+    for g, w in zip(got, want):
+        g, w = g.cpu().double(), w.cpu().double()
+        scale = w.abs().amax(dim=(-2, -1), keepdim=True).clamp_min(1e-30)
+        err = ((g - w).abs() / scale).max().item()
+        assert err <= 1e-5, err
+        n = g.shape[-1]
+        assert not g[..., torch.arange(n), torch.arange(n)].any()
+        assert not g.permute(0, 2, 3, 1)[~mask.cpu()].any()
+
+
+def test_fixture_module_on_gpu_matches_torch(cuda):
+    z = np.load(fx.GOLDEN)
+    feats = _features(z)
+    module, _ = fx.build(SimplicialGeometryBias, "lowrank", feats, torch.from_numpy(z["pad_mask"]),
+                         torch.from_numpy(z["sigma"]))
+    want = module._compute_factorized_terms(feats)  # CPU: torch formulation
+    module = module.to(cuda)
+    gfe = _to(feats, cuda)
+    with torch.no_grad():
+        assert pair_mlp.serves(module, gfe)
+        got = module._compute_factorized_terms(gfe)
+    torch.cuda.synchronize()
+    _check(got, want, feats.pair_mask)
+    np.testing.assert_allclose(got[0].cpu().numpy(), z["lowrank_u"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("B,N,hidden,H,R", [(64, 181, 128, 8, 16), (5, 37, 64, 4, 29), (3, 20, 16, 16, 1)])
+def test_configs_sized_batch_matches_torch(cuda, B, N, hidden, H, R):
+    print(f"pair mlp B={B} N={N} hidden={hidden} H={H} R={R}", flush=True)
+    gen = torch.Generator().manual_seed(B + N)
+    counts = torch.randint(max(2, N // 4), N + 1, (B,), generator=gen)
+    pad = torch.arange(N)[None, :] >= counts[:, None]
+    coords = torch.randn(B, N, 3, generator=gen) * 1.4
+    torch.manual_seed(7)
+    module = SimplicialGeometryBias(H, edge_bias_hidden_dim=hidden, edge_bias_n_rbf=R)
+    feats = NonPeriodicGeometryAdapter()(coords, pad_mask=pad)
+    module._compute_factorized_terms(feats)  # materialise the LazyLinear layers
+    with torch.no_grad():
+        for mlp in (module.spoke_bias_u_mlp, module.spoke_bias_v_mlp, module.pair_bias_w_mlp):
+            mlp[2].weight.copy_(torch.randn(mlp[2].weight.shape, generator=gen) * 0.2)
+            mlp[2].bias.copy_(torch.randn(mlp[2].bias.shape, generator=gen) * 0.2)
+    sub = slice(0, min(B, 6))  # the torch reference on the CPU for a slice of the batch
+    want = [t[sub] for t in module._compute_factorized_terms(
+        GeometryFeatures(**{k: (getattr(feats, k)[sub] if k not in ("kind", "extras") else getattr(feats, k))
+                            for k in ("pair_delta", "pair_dist", "pair_dist2", "pair_dist_norm", "pair_mask",
+                                      "global_geom", "kind", "extras")}))]
+    module = module.to(cuda)
+    gfe = NonPeriodicGeometryAdapter()(coords.to(cuda), pad_mask=pad.to(cuda))
+    with torch.no_grad():
+        got = module._compute_factorized_terms(gfe)
+    torch.cuda.synchronize()
+    _check([t[sub] for t in got], want, feats.pair_mask[sub])
+    assert all(torch.isfinite(t).all() for t in got)
+
+
+def test_grad_calls_take_the_torch_path(cuda):
+    z = np.load(fx.GOLDEN)
+    feats = _to(_features(z), cuda)
+    torch.manual_seed(0)
+    module = SimplicialGeometryBias(4, edge_bias_hidden_dim=16).to(cuda)
+    module._compute_factorized_terms(feats)
+    assert not pair_mlp.serves(module, feats)  # grad enabled, parameters require grad
+    with torch.no_grad():
+        assert pair_mlp.serves(module, feats)
+    u, v, w = module._compute_factorized_terms(feats)
+    assert u.requires_grad  # autograd followed the torch formulation
+
+
+def test_bias_feeds_hip_attention(cuda):
+    """build_structured_bias_inputs on the GPU (kernel u, v, w) into SimplicialAttention's HIP path, against the
+    same module on the CPU (torch u, v, w, torch attention)."""
+    from matterformer_amd.simplicial_attention import SimplicialAttention
+
+    z = np.load(fx.GOLDEN)
+    feats = _features(z)
+    pad, sigma = torch.from_numpy(z["pad_mask"]), torch.from_numpy(z["sigma"])
+    module, _ = fx.build(SimplicialGeometryBias, "lowrank", feats, pad, sigma)
+    module.mode = "factorized"  # only u, v, w for this comparison
+    module.message_mode = "none"
+    torch.manual_seed(3)
+    attn = SimplicialAttention(32, fx.H, precision="ieee_fp32")
+    x = torch.randn(fx.B, fx.N, 32)
+    with torch.no_grad():
+        fb, _, _, _, mask = module.build_structured_bias_inputs(feats, coords_len=fx.N, pad_mask=pad, sigma=sigma)
+        want = attn(x, attention_mask=mask, factorized_bias=fb)
+        module, attn = module.to(cuda), attn.to(cuda)
+        fbg, _, _, _, maskg = module.build_structured_bias_inputs(_to(feats, cuda), coords_len=fx.N,
+                                                                  pad_mask=pad.to(cuda), sigma=sigma.to(cuda))
+        got = attn(x.to(cuda), attention_mask=maskg, factorized_bias=fbg)
+    torch.cuda.synchronize()
+    assert attn._last_impl_used == "triton"
+    valid = ~pad
+    rel = float((got.cpu()[valid] - want[valid]).norm() / want[valid].norm())
+    assert rel <= 1e-4, rel
