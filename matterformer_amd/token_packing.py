@@ -61,6 +61,9 @@ class TokenPacking:
         slot[self.compact_rows] = torch.arange(self.tokens, dtype=torch.int32, device=self.device)
         self.slot32 = slot
         self.compact_pad_mask = torch.arange(self.width, device=self.device)[None, :] >= counts[:, None]
+        atom_index = torch.zeros(self.batch * self.width, dtype=torch.long, device=self.device)
+        atom_index[self.compact_rows] = self.rows - self.mol * self.atoms
+        self.atom_index = atom_index.view(self.batch, self.width)  # atom at each compact position (0 past count)
 
     # -- (B, N, ...) <-> packed rows -------------------------------------------------------------------------
     def pack(self, x: torch.Tensor) -> torch.Tensor:
@@ -83,6 +86,21 @@ class TokenPacking:
         out = t.new_zeros((self.batch * self.width,) + tail)
         out[self.compact_rows] = t.reshape((self.batch * self.atoms,) + tail).index_select(0, self.rows)
         return out.view((self.batch, self.width) + tail)
+
+    def compact_dims(self, t: torch.Tensor, *dims: int) -> torch.Tensor:
+        """Atom axes ``dims`` of a (B, ...) tensor (bias terms, pair masks, gates) from N to the compact width W,
+        each molecule's valid atoms first; positions past a molecule's count are zero (False)."""
+        B, W = self.batch, self.width
+        keep_all = ~self.compact_pad_mask
+        for dim in dims:
+            shape = [1] * t.ndim
+            shape[0], shape[dim] = B, W
+            full = list(t.shape)
+            full[dim] = W
+            t = t.gather(dim, self.atom_index.view(shape).expand(full))
+            keep = keep_all.view(shape)
+            t = t & keep if t.dtype == torch.bool else t.masked_fill(~keep, 0)
+        return t
 
     # -- packed rows <-> compact head layout -----------------------------------------------------------------
     def to_heads(self, xp: torch.Tensor, parts: int, heads: int, head_dim: int, dtype: torch.dtype,

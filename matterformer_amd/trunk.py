@@ -140,16 +140,23 @@ class KnnLocalAttention(nn.Module):
         self.attn = nn.MultiheadAttention(d_model, n_heads, dropout=dropout, batch_first=True)
         self._last_impl_used = "torch"
 
-    def _use_hip(self, h: torch.Tensor) -> bool:
-        if self.impl == "torch" or h.device.type != "cuda":
-            if self.impl == "triton":
-                raise RuntimeError("the HIP local attention requires GPU tensors")
-            return False
+    def _hip_unavailable_reason(self, h: torch.Tensor) -> str | None:
+        if h.device.type != "cuda":
+            return "the HIP local attention requires GPU tensors"
         if self.training and self.attn.dropout > 0.0:
-            if self.impl == "triton":
-                raise RuntimeError("the HIP local attention does not support attention dropout in training mode")
+            return "the HIP local attention does not support attention dropout in training mode"
+        head_dim = self.attn.embed_dim // self.attn.num_heads
+        if head_dim not in (32, 64, 128):
+            return f"the HIP local attention supports head_dim 32, 64 or 128, got {head_dim}"
+        return None
+
+    def _use_hip(self, h: torch.Tensor) -> bool:
+        if self.impl == "torch":
             return False
-        return True
+        reason = self._hip_unavailable_reason(h)
+        if reason is not None and self.impl == "triton":
+            raise RuntimeError(reason)
+        return reason is None
 
     def forward(self, h: torch.Tensor, mask: KnnLocalMask, pad_mask: torch.Tensor | None = None) -> torch.Tensor:
         if self._use_hip(h):
@@ -205,8 +212,48 @@ class KnnLocalAttention(nn.Module):
         return out
 
 
+class SimplicialTerms:
+    """The simplicial blocks' shared inputs: attention mask and the optional logit / message terms (the
+    reference trunk builds them once per forward, transformer.py:1261-1296)."""
+
+    def __init__(self, attention_mask: SimplicialAttentionMask | None, factorized_bias=None, angle_residual=None,
+                 message_residual=None, logit_bias_fn=None) -> None:
+        self.attention_mask = attention_mask
+        self.factorized_bias = factorized_bias
+        self.angle_residual = angle_residual
+        self.message_residual = message_residual
+        self.logit_bias_fn = logit_bias_fn
+
+    def block_kwargs(self) -> dict:
+        return dict(simplicial_attention_mask=self.attention_mask, simplicial_factorized_bias=self.factorized_bias,
+                    simplicial_angle_residual=self.angle_residual, simplicial_message_residual=self.message_residual,
+                    simplicial_logit_bias_fn=self.logit_bias_fn)
+
+    def compact(self, packing: TokenPacking) -> "SimplicialTerms":
+        """Every term in the packing's compact layout (atom axes N -> W)."""
+        if self.logit_bias_fn is not None:
+            raise RuntimeError("a dense logit_bias_fn cannot be packed")
+        from matterformer_amd.simplicial_types import (SimplicialFactorizedBias, SimplicialLowRankAngleResidual,
+                                                       SimplicialLowRankMessageResidual)
+
+        c = packing.compact_dims
+        m = self.attention_mask
+        mask = SimplicialAttentionMask(query_valid=c(m.query_valid, 1), pair_key_valid=c(m.pair_key_valid, 1),
+                                       pair_valid=None if m.pair_valid is None else c(m.pair_valid, 1, 2))
+        fb = self.factorized_bias
+        if fb is not None:
+            fb = SimplicialFactorizedBias(u=c(fb.u, 2, 3), v=c(fb.v, 2, 3), w=c(fb.w, 2, 3), gate=c(fb.gate, 2))
+        ang = self.angle_residual
+        if ang is not None:
+            ang = SimplicialLowRankAngleResidual(left=c(ang.left, 2, 3), right=c(ang.right, 2, 3), gate=c(ang.gate, 2))
+        msg = self.message_residual
+        if msg is not None:
+            msg = SimplicialLowRankMessageResidual(left=c(msg.left, 2, 3), right=c(msg.right, 2, 3))
+        return SimplicialTerms(mask, fb, ang, msg)
+
+
 def _simplicial_packed(attn: SimplicialAttention, hp: torch.Tensor, packing: TokenPacking,
-                       attention_mask: SimplicialAttentionMask, factorized_bias=None) -> torch.Tensor:
+                       terms: SimplicialTerms) -> torch.Tensor:
     """SimplicialAttention.forward's HIP branch on packed rows: in_proj and out_proj on (T, C); q scaled and
     content-gated in the projection dtype as in _project_inputs / _content_query; the core on the padded
     head layout."""
@@ -217,9 +264,10 @@ def _simplicial_packed(attn: SimplicialAttention, hp: torch.Tensor, packing: Tok
     parts = packing.to_heads(attn.in_proj(hp), 5, attn.num_heads, attn.head_dim, dtype,
                              first_part_scale=attn.scale)
     q = parts[0] if on else attn._content_query(parts[0])
-    out = attn._forward_triton(q, parts[1], parts[2], parts[3], parts[4], attention_mask=attention_mask,
-                               factorized_bias=factorized_bias, angle_residual=None, message_residual=None,
-                               message_basis=None)
+    msg = terms.message_residual
+    out = attn._forward_triton(q, parts[1], parts[2], parts[3], parts[4], attention_mask=terms.attention_mask,
+                               factorized_bias=terms.factorized_bias, angle_residual=terms.angle_residual,
+                               message_residual=msg, message_basis=attn.message_basis if msg is not None else None)
     return attn.out_proj(packing.from_heads(out, hp.dtype))
 
 
@@ -276,7 +324,8 @@ class AdaLNBlock(nn.Module):
     def forward(self, x: torch.Tensor, cond_emb: torch.Tensor | None, pad_mask: torch.Tensor | None = None, *,
                 knn_mask: KnnLocalMask | None = None,
                 simplicial_attention_mask: SimplicialAttentionMask | None = None,
-                simplicial_factorized_bias=None) -> torch.Tensor:
+                simplicial_factorized_bias=None, simplicial_angle_residual=None, simplicial_message_residual=None,
+                simplicial_logit_bias_fn=None) -> torch.Tensor:
         if self.use_adaln_conditioning:
             if cond_emb is None or cond_emb.ndim != 2 or cond_emb.shape[-1] != x.shape[-1]:
                 raise ValueError(f"cond_emb must have shape (B, {x.shape[-1]})")
@@ -290,7 +339,8 @@ class AdaLNBlock(nn.Module):
             attn_out = self.attn(h, knn_mask, pad_mask)
         else:
             attn_out = self.attn(h, key_padding_mask=pad_mask, attention_mask=simplicial_attention_mask,
-                                 factorized_bias=simplicial_factorized_bias)
+                                 factorized_bias=simplicial_factorized_bias, angle_residual=simplicial_angle_residual,
+                                 message_residual=simplicial_message_residual, logit_bias_fn=simplicial_logit_bias_fn)
         if self.use_adaln_conditioning:
             x = x + gate_msa[:, None, :] * attn_out
             h = _modulate(self.norm2(x), shift_mlp, scale_mlp)
@@ -305,31 +355,27 @@ class AdaLNBlock(nn.Module):
         return self.ada_ln(cond_emb).contiguous()
 
     def _attention_packed(self, h: torch.Tensor, packing: TokenPacking, knn_mask: KnnLocalMask | None,
-                          simplicial_attention_mask: SimplicialAttentionMask | None,
-                          simplicial_factorized_bias=None) -> torch.Tensor:
+                          terms: "SimplicialTerms | None") -> torch.Tensor:
         if self.attn_type == "knn_local":
             if knn_mask is None:
                 raise ValueError("a knn_local block needs knn_mask")
             return self.attn.forward_packed(h, knn_mask, packing)
-        if simplicial_attention_mask is None:
+        if terms is None or terms.attention_mask is None:
             raise ValueError("a packed simplicial block needs the attention mask of the compact batch")
-        return _simplicial_packed(self.attn, h, packing, simplicial_attention_mask, simplicial_factorized_bias)
+        return _simplicial_packed(self.attn, h, packing, terms)
 
     def forward_packed(self, xp: torch.Tensor, cond_emb: torch.Tensor | None, packing: TokenPacking, *,
-                       knn_mask: KnnLocalMask | None = None,
-                       simplicial_attention_mask: SimplicialAttentionMask | None = None,
-                       simplicial_factorized_bias=None) -> torch.Tensor:
-        """forward on the valid rows (T, C) of a batch (TokenPacking); masks in the packing's compact layout.
-        The same operations in the same dtypes as forward."""
+                       knn_mask: KnnLocalMask | None = None, terms: "SimplicialTerms | None" = None) -> torch.Tensor:
+        """forward on the valid rows (T, C) of a batch (TokenPacking); masks and simplicial terms in the packing's
+        compact layout.  The same operations in the same dtypes as forward."""
         if not self.use_adaln_conditioning:
             h = self.norm1(xp)
-            xp = xp + self._attention_packed(h, packing, knn_mask, simplicial_attention_mask,
-                                             simplicial_factorized_bias)
+            xp = xp + self._attention_packed(h, packing, knn_mask, terms)
             return xp + self.mlp(self.norm2(xp))
         C = xp.shape[-1]
         mods = self._mods(cond_emb, packing.batch)
         h = adaln_rows(packing, xp, shift=mods[:, :C], scale=mods[:, C:2 * C], eps=self.norm1.eps)
-        a = self._attention_packed(h, packing, knn_mask, simplicial_attention_mask, simplicial_factorized_bias)
+        a = self._attention_packed(h, packing, knn_mask, terms)
         xp, h = adaln_rows(packing, xp, a, gate=mods[:, 2 * C:3 * C], shift=mods[:, 3 * C:4 * C],
                            scale=mods[:, 4 * C:5 * C], eps=self.norm2.eps)
         return adaln_rows(packing, xp, self.mlp(h), gate=mods[:, 5 * C:])
@@ -340,10 +386,15 @@ class AlternatingTrunk(nn.Module):
 
     def __init__(self, d_model: int = 512, n_heads: int = 8, n_layers: int = 12, *, mlp_ratio: float = 4.0,
                  knn_k: int = 32, schedule: list[str] | None = None, simplicial_impl: str = "auto",
-                 simplicial_precision: str = "bf16_tc", local_impl: str = "auto", eps: float = 1e-6,
-                 use_adaln_conditioning: bool = True, pack_tokens: bool = True) -> None:
+                 simplicial_precision: str = "bf16_tc", simplicial_message_mode: str = "none",
+                 simplicial_message_rank: int = 16, simplicial_content_logits: str = "on", local_impl: str = "auto",
+                 eps: float = 1e-6, use_adaln_conditioning: bool = True, geometry_adapter: nn.Module | None = None,
+                 simplicial_geometry_bias: nn.Module | None = None, pack_tokens: bool = True) -> None:
         super().__init__()
         self.pack_tokens = bool(pack_tokens)
+        # registered before the blocks, as in TransformerTrunk.__init__ (transformer.py:1137-1139)
+        self.geometry_adapter = geometry_adapter
+        self.simplicial_geometry_bias = simplicial_geometry_bias
         if schedule is None:
             schedule = ["simplicial" if layer % 2 == 0 else "knn_local" for layer in range(n_layers)]
         if len(schedule) != n_layers:
@@ -352,53 +403,85 @@ class AlternatingTrunk(nn.Module):
         self.schedule = list(schedule)
         self.blocks = nn.ModuleList([
             AdaLNBlock(d_model, n_heads, mlp_ratio=mlp_ratio, eps=eps, attn_type=t, simplicial_impl=simplicial_impl,
-                       simplicial_precision=simplicial_precision, local_impl=local_impl,
+                       simplicial_precision=simplicial_precision, simplicial_message_mode=simplicial_message_mode,
+                       simplicial_message_rank=simplicial_message_rank,
+                       simplicial_content_logits=simplicial_content_logits, local_impl=local_impl,
                        use_adaln_conditioning=use_adaln_conditioning)
             for t in self.schedule])
 
     def _use_hip(self, x: torch.Tensor) -> bool:
         local = [b.attn for b in self.blocks if b.attn_type == "knn_local"]
-        return x.device.type == "cuda" and any(a.impl != "torch" for a in local)
+        return x.device.type == "cuda" and any(a.impl != "torch" and a._hip_unavailable_reason(x) is None
+                                               for a in local)
 
-    def packable(self, x: torch.Tensor) -> bool:
-        """True when every block would run its HIP kernels on x, which the packed forward requires."""
+    def packable(self, x: torch.Tensor, terms: SimplicialTerms | None = None) -> bool:
+        """True when every block would run its HIP kernels on x (with the simplicial terms of this call), which
+        the packed forward requires."""
         if not self.pack_tokens or x.device.type != "cuda":
             return False
+        t = terms or SimplicialTerms(None)
         for block in self.blocks:
             a = block.attn
             if a.impl == "torch":
                 return False
             if block.attn_type == "knn_local":
-                if a.training and a.attn.dropout > 0.0:
+                if a._hip_unavailable_reason(x) is not None:
                     return False
-            elif a._triton_unavailable_reason(x=x, factorized_bias=None, angle_residual=None, message_residual=None,
-                                              message_basis=None, logit_bias_fn=None, return_attn=False) is not None:
+            elif a._triton_unavailable_reason(
+                    x=x, factorized_bias=t.factorized_bias, angle_residual=t.angle_residual,
+                    message_residual=t.message_residual,
+                    message_basis=a.message_basis if t.message_residual is not None else None,
+                    logit_bias_fn=t.logit_bias_fn, return_attn=False) is not None:
                 return False
         return True
 
+    def simplicial_terms(self, coords: torch.Tensor, pad_mask: torch.Tensor | None = None,
+                         lattice: torch.Tensor | None = None, sigma: torch.Tensor | None = None
+                         ) -> SimplicialTerms | None:
+        """The geometry features and the simplicial blocks' bias / residual terms and attention mask, once per
+        forward (TransformerTrunk.forward, transformer.py:1246-1296); None without a geometry adapter."""
+        if self.geometry_adapter is None:
+            return None
+        geom = self.geometry_adapter(coords=coords, pad_mask=pad_mask, lattice=lattice)
+        B, N = coords.shape[:2]
+        if self.simplicial_geometry_bias is not None:
+            fb, fn, ang, msg, mask = self.simplicial_geometry_bias.build_structured_bias_inputs(
+                geom_features=geom, coords_len=N, pad_mask=pad_mask, seq_len=N, sigma=sigma)
+            return SimplicialTerms(mask, fb, ang, msg, fn)
+        from matterformer_amd.geometry_bias import build_simplicial_attention_mask
+
+        mask = build_simplicial_attention_mask(coords_len=N, seq_len=N, batch_size=B, device=coords.device,
+                                               pad_mask=pad_mask, geom_pair_mask=geom.pair_mask)
+        return SimplicialTerms(mask)
+
     def forward(self, x: torch.Tensor, cond_emb: torch.Tensor | None, coords: torch.Tensor,
-                pad_mask: torch.Tensor | None = None, *, packing: TokenPacking | None = None) -> torch.Tensor:
-        """x (B, N, C) -> (B, N, C), padded rows zero.  ``packing`` (TokenPacking(pad_mask)) may be passed in,
-        e.g. to capture the forward in a HIP graph; otherwise a GPU call with a pad_mask builds it."""
+                pad_mask: torch.Tensor | None = None, *, lattice: torch.Tensor | None = None,
+                sigma: torch.Tensor | None = None, packing: TokenPacking | None = None) -> torch.Tensor:
+        """x (B, N, C) -> (B, N, C), padded rows zero.  With a geometry adapter (and a SimplicialGeometryBias)
+        the simplicial blocks get the geometry attention mask and bias terms of (coords, lattice, sigma).
+        ``packing`` (TokenPacking(pad_mask)) may be passed in, e.g. to capture the forward in a HIP graph;
+        otherwise a GPU call with a pad_mask builds it."""
         if pad_mask is not None:
             pad_mask = pad_mask.bool()
+        terms = self.simplicial_terms(coords, pad_mask, lattice, sigma)
         if packing is not None:
             if pad_mask is None or (packing.batch, packing.atoms) != tuple(pad_mask.shape):
                 raise ValueError("packing must be built from this call's pad_mask")
-            if not self.packable(x):
+            if not self.packable(x, terms):
                 raise RuntimeError("the packed forward needs every block on its HIP kernels")
-        elif pad_mask is not None and self.packable(x):
+        elif pad_mask is not None and self.packable(x, terms):
             packing = TokenPacking(pad_mask)
         if packing is not None:
-            return self._forward_packed(x, cond_emb, coords, packing)
+            return self._forward_packed(x, cond_emb, coords, packing, terms)
         mask = None
         if "knn_local" in self.schedule:
             mask = build_knn_mask(coords, self.knn_k, pad_mask, use_hip=self._use_hip(x))
+        kwargs = terms.block_kwargs() if terms is not None else {}
         # transformer.py:1298-1316: padded atoms are zeroed before every block and in the output
         for block in self.blocks:
             if pad_mask is not None:
                 x = x.masked_fill(pad_mask[..., None], 0.0)
-            x = block(x, cond_emb, pad_mask, knn_mask=mask)
+            x = block(x, cond_emb, pad_mask, knn_mask=mask, **kwargs)
         if pad_mask is not None:
             x = x.masked_fill(pad_mask[..., None], 0.0)
         return x
@@ -418,7 +501,7 @@ class AlternatingTrunk(nn.Module):
         return list(out.split(lins[0].weight.shape[0], dim=1))
 
     def _forward_packed(self, x: torch.Tensor, cond_emb: torch.Tensor | None, coords: torch.Tensor,
-                        packing: TokenPacking) -> torch.Tensor:
+                        packing: TokenPacking, terms: SimplicialTerms | None = None) -> torch.Tensor:
         """The blocks on the valid rows; attention masks and kNN lists in the compact layout (each molecule's
         valid atoms first, width = its largest count).  With adaLN, one mf_adaln_rows pass joins each
         residual to the next LayerNorm + modulation, the last block's MLP residual to the next block's norm1."""
@@ -427,11 +510,15 @@ class AlternatingTrunk(nn.Module):
         mask = None
         if "knn_local" in self.schedule:
             mask = build_knn_mask(packing.compact(coords.float()), self.knn_k, cpad, use_hip=True)
-        smask = coerce_attention_mask(None, key_padding_mask=cpad, batch_size=B, num_tokens=W, device=x.device)
+        if terms is not None:
+            terms = terms.compact(packing)
+        else:
+            terms = SimplicialTerms(coerce_attention_mask(None, key_padding_mask=cpad, batch_size=B, num_tokens=W,
+                                                          device=x.device))
         xp = packing.pack(x)
         if not all(blk.use_adaln_conditioning for blk in self.blocks):
             for block in self.blocks:
-                xp = block.forward_packed(xp, cond_emb, packing, knn_mask=mask, simplicial_attention_mask=smask)
+                xp = block.forward_packed(xp, cond_emb, packing, knn_mask=mask, terms=terms)
             return packing.unpack(xp)
         C = xp.shape[-1]
         mods = self._all_mods(cond_emb, B)
@@ -439,7 +526,7 @@ class AlternatingTrunk(nn.Module):
         h = adaln_rows(packing, xp, shift=mods[0][:, :C], scale=mods[0][:, C:2 * C], eps=blocks[0].norm1.eps)
         for layer, blk in enumerate(blocks):
             m = mods[layer]
-            a = blk._attention_packed(h, packing, mask, smask)
+            a = blk._attention_packed(h, packing, mask, terms)
             xp, h = adaln_rows(packing, xp, a, gate=m[:, 2 * C:3 * C], shift=m[:, 3 * C:4 * C],
                                scale=m[:, 4 * C:5 * C], eps=blk.norm2.eps, inplace=layer > 0)
             y = blk.mlp(h)

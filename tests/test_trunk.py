@@ -120,3 +120,68 @@ def test_torch_path_zeroes_padded_rows():
         out = trunk(x[:2], cond[:2], coords[:2], pad[:2])
     assert not out[pad[:2]].any()
     assert out[~pad[:2]].abs().sum() > 0
+
+
+def test_compact_dims_and_terms_follow_the_packing():
+    """TokenPacking.compact_dims moves atom axes N -> W (valid atoms first, zero / False past the count), on
+    every named axis; SimplicialTerms.compact applies it to the mask and each term."""
+    from matterformer_amd.simplicial_types import (SimplicialAttentionMask, SimplicialFactorizedBias,
+                                                   SimplicialLowRankAngleResidual)
+    from matterformer_amd.trunk import SimplicialTerms, TokenPacking
+
+    gen = torch.Generator().manual_seed(9)
+    B, H, N, R = 3, 2, 6, 3
+    pad = torch.rand(B, N, generator=gen) < 0.4
+    pad[0] = False
+    p = TokenPacking(pad)
+    W = p.width
+    idx = [[n for n in range(N) if not pad[b, n]] for b in range(B)]
+    u = torch.randn(B, H, N, N, generator=gen)
+    got = p.compact_dims(u, 2, 3)
+    assert got.shape == (B, H, W, W)
+    for b in range(B):
+        c = len(idx[b])
+        want = torch.zeros(H, W, W)
+        want[:, :c, :c] = u[b][:, idx[b]][:, :, idx[b]]
+        assert torch.equal(got[b], want)
+    pv = torch.rand(B, N, N, generator=gen) < 0.7
+    gpv = p.compact_dims(pv, 1, 2)
+    for b in range(B):
+        c = len(idx[b])
+        assert torch.equal(gpv[b, :c, :c], pv[b][idx[b]][:, idx[b]])
+        assert not gpv[b, c:].any() and not gpv[b, :, c:].any()
+    left = torch.randn(B, H, N, N, R, generator=gen)
+    gate = torch.rand(B, H, 1, generator=gen).expand(B, H, N)
+    mask = SimplicialAttentionMask(query_valid=~pad, pair_key_valid=~pad, pair_valid=pv)
+    terms = SimplicialTerms(mask, SimplicialFactorizedBias(u=u, v=u * 2, w=-u, gate=gate),
+                            SimplicialLowRankAngleResidual(left=left, right=left * 3, gate=gate))
+    ct = terms.compact(p)
+    assert torch.equal(ct.attention_mask.query_valid, ~p.compact_pad_mask)
+    assert torch.equal(ct.attention_mask.pair_valid, gpv)
+    assert torch.equal(ct.factorized_bias.w, -got)
+    assert torch.equal(ct.factorized_bias.gate, gate[:, :, :W] * (~p.compact_pad_mask)[:, None, :])
+    assert ct.angle_residual.left.shape == (B, H, W, W, R)
+    assert torch.equal(ct.angle_residual.right, p.compact_dims(left * 3, 2, 3))
+
+
+def test_geometry_trunk_valid_rows_ignore_padded_atoms():
+    """With a geometry adapter and SimplicialGeometryBias (angle_low_rank + low-rank message), the torch
+    trunk's valid rows do not depend on the padded atoms' features or coordinates, padded rows are zero, and
+    the bias terms do reach the output."""
+    from trunk_fixture import geometry_inputs, geometry_trunk
+
+    trunk = geometry_trunk()
+    x, cond, coords, pad, sigma = geometry_inputs()
+    with torch.no_grad():
+        out = trunk(x, cond, coords, pad, sigma=sigma)
+        x2, c2 = x.clone(), coords.clone()
+        x2[pad] = 7.0
+        c2[pad] = -3.0
+        out2 = trunk(x2, cond, c2, pad, sigma=sigma)
+        for prm in trunk.simplicial_geometry_bias.spoke_bias_u_mlp.parameters():
+            prm.data.mul_(2.0)
+        out3 = trunk(x, cond, coords, pad, sigma=sigma)
+    assert all(b.attn._last_impl_used == "torch" for b in trunk.blocks if b.attn_type == "simplicial")
+    assert not out[pad].any() and not out2[pad].any()
+    torch.testing.assert_close(out2[~pad], out[~pad], rtol=1e-5, atol=1e-5)
+    assert float((out3 - out)[~pad].abs().max()) > 1e-3
