@@ -359,6 +359,44 @@ def measure_geometry() -> dict:
     return res
 
 
+def measure_pair_mlp() -> dict:
+    """The factorized geometry bias (SimplicialGeometryBias's u, v, w pairwise MLPs, mf_pair_mlp_bias) on
+    configs[1]'s GEOM molecules: hidden 128, 16 rbf, 8 heads, from the non-periodic adapter's features;
+    graph-replayed kernel time against the HBM roofline of its fp32 outputs (3 x [B, H, N, N]) and inputs."""
+    import torch
+
+    from matterformer_amd import pair_mlp
+    from matterformer_amd.geometry import NonPeriodicGeometryAdapter
+    from matterformer_amd.geometry_bias import SimplicialGeometryBias
+    from matterformer_amd.workloads import simplicial_workload
+
+    dev = torch.device("cuda", 0)
+    sw = simplicial_workload("geom")
+    B, H, N = sw.q.shape[0], sw.q.shape[1], sw.q.shape[2]
+    pad = torch.arange(N)[None, :] >= sw.counts[:, None]
+    coords = torch.randn(B, N, 3, generator=torch.Generator().manual_seed(5)) * 2.0 ** 0.5
+    torch.manual_seed(6)
+    module = SimplicialGeometryBias(H, mode="factorized", edge_bias_hidden_dim=128, edge_bias_n_rbf=16)
+    with torch.no_grad():
+        feats = NonPeriodicGeometryAdapter()(coords[:1], pad[:1])
+        module._compute_factorized_terms(feats)  # materialises the LazyLinear layers (CPU, torch formulation)
+        module = module.to(dev)
+        feats = NonPeriodicGeometryAdapter().to(dev)(coords.to(dev), pad.to(dev))
+        if not pair_mlp.serves(module, feats):
+            raise RuntimeError("mf_pair_mlp_bias does not serve the bench configuration")
+        ms = _graph_ms(lambda: pair_mlp.factorized_terms(module, feats), per_graph=10, replays=5)
+    hidden = 128
+    valid = int((sw.counts.long() ** 2 - sw.counts.long()).sum())
+    nbytes = 3 * B * H * N * N * 4 + B * N * N * (4 * 4 + 1)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    flops = valid * 2 * (2 * (19 * hidden + hidden * H) + (16 * hidden + hidden * H))
+    return {"ms": round(ms, 5), "batch": B, "atoms": N, "heads": H, "hidden": hidden, "rbf": 16,
+            "valid_pairs": valid, "bytes": nbytes, "valid_gflop": round(flops / 1e9, 3),
+            "valid_tflops_fp32": round(flops / (ms * 1e-3) / 1e12, 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def measure_trunk() -> dict:
     """12-layer alternating trunk forward, bf16 weights and activations, 64 GEOM molecules."""
     import torch
@@ -603,6 +641,7 @@ def main() -> int:
         extra["radius"] = measure_radius(args.cpu_sample)
         extra["c5_trunk"] = measure_trunk()
         extra["geometry_features"] = measure_geometry()
+        extra["pair_mlp_bias"] = measure_pair_mlp()
 
     cpu = cpu_baseline(w, args.cpu_sample, args.cpu_threads) if args.cpu_sample > 0 else None
 

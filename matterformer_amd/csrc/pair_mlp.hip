@@ -9,8 +9,9 @@
 // written per head as [B, H, N, N] with the diagonal and the pairs outside
 // the geometry pair mask zero (:711-717).  The reference materialises the
 // [B, N, N, F] features and the [B, N, N, hidden] activations of each MLP;
-// here one wave takes 16 pairs (molecule b, row i, columns j0..j0+15) and
-// keeps everything in registers:
+// here one wave takes a (molecule b, row i, 64-column group) unit, writes
+// the zeros of its invalid pairs, and for each 16-column chunk with a valid
+// pair runs the 16 pairs (b, i, j0..j0+15) with everything in registers:
 //
 //   layer 1  C1[h][p] = b1[h] + sum_f W1[h][f] X[p][f]    fp32 MFMA 16x16x4,
 //            M = 16 hidden units, N = 16 pairs, K = 4 features per step;
@@ -23,9 +24,9 @@
 //            same order
 //
 // The weights of the three MLPs are staged in LDS once per workgroup (rows
-// padded to an odd stride).  Chunks with no valid pair are written as zeros
-// without any arithmetic.  fp32 throughout; this file is built without FMA
-// contraction so the rbf features round as torch's expression does.
+// padded to an odd stride).  fp32 throughout; the exponentials (rbf features,
+// SiLU) use the hardware exp2 and reciprocal, a few ulp, well inside the
+// rounding of the fp32 sums around them.
 #include <algorithm>
 #include <cmath>
 
@@ -34,7 +35,7 @@
 namespace mf {
 namespace pmlp {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;  // 8 waves share one copy of the weights
 constexpr int kMaxHidden = 256;
 constexpr int kMaxHeads = 16;
 constexpr int kMaxRbf = 29;  // spoke features 3 + R <= 32
@@ -50,16 +51,66 @@ struct Params {
   const float* w2[3];
   const float* b2[3];
   float* out[3];
-  int B, N, R, hidden, heads, chunks;
+  int B, N, R, hidden, heads, groups;
 };
 
 __device__ __forceinline__ mf_f32x4 mma(float a, float b, mf_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// SiLU x / (1 + e^-x) with the hardware exp2 and reciprocal (about 2 ulp; the fp32 MFMA sums around it carry
+// more): e^-x overflows to inf for x < -88, giving -0 as torch's SiLU does
+__device__ __forceinline__ float silu(float x) {
+  const float e = __builtin_amdgcn_exp2f(x * -1.44269504088896341f);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// One MLP over the 16 pairs of a chunk: layer 1 (K steps of 4 features, x[t] = feature 4 t + g of pair r16),
+// SiLU, layer 2; lane (g, r16) returns outputs 4 g .. 4 g + 3 of pair r16.  Two 16-unit hidden slices are
+// in flight at a time so one slice's SiLU overlaps the other's MFMA chain.
+template <int K>
+__device__ __forceinline__ mf_f32x4 mlp16(const float (&x)[K], const float* W1, const float* B1, const float* W2,
+                                          const float* B2, int s1, int s2, int HT, int g, int r16) {
+  mf_f32x4 o2;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) o2[r] = B2[4 * g + r];
+  const float* w2row = W2 + r16 * s2 + 4 * g;
+  int ht = 0;
+  for (; ht + 2 <= HT; ht += 2) {
+    mf_f32x4 ca, cb;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ca[r] = B1[16 * ht + 4 * g + r];
+      cb[r] = B1[16 * ht + 16 + 4 * g + r];
+    }
+    const float* wa = W1 + (16 * ht + r16) * s1 + g;
+    const float* wb = wa + 16 * s1;
+#pragma unroll
+    for (int t = 0; t < K; ++t) {
+      ca = mma(wa[4 * t], x[t], ca);
+      cb = mma(wb[4 * t], x[t], cb);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o2 = mma(w2row[16 * ht + r], silu(ca[r]), o2);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o2 = mma(w2row[16 * ht + 16 + r], silu(cb[r]), o2);
+  }
+  if (ht < HT) {
+    mf_f32x4 ca;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ca[r] = B1[16 * ht + 4 * g + r];
+    const float* wa = W1 + (16 * ht + r16) * s1 + g;
+#pragma unroll
+    for (int t = 0; t < K; ++t) ca = mma(wa[4 * t], x[t], ca);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o2 = mma(w2row[16 * ht + r], silu(ca[r]), o2);
+  }
+  return o2;
+}
+
 // K4: 4-wide K steps of layer 1 for the spoke (u, v) and pair (w) features.
 template <int KS, int KP>
-__global__ void __launch_bounds__(kThreads, 2) pair_mlp_kernel(Params p) {
+__global__ void __launch_bounds__(kThreads, 4) pair_mlp_kernel(Params p) {
   extern __shared__ float lds[];
   const int hidden = p.hidden, H = p.heads;
   const int HT = hidden / 16;
@@ -99,94 +150,104 @@ __global__ void __launch_bounds__(kThreads, 2) pair_mlp_kernel(Params p) {
   __syncthreads();
 
   const int lane = tid & 63, g = lane >> 4, r16 = lane & 15;
-  const int N = p.N;
-  const long long units = (long long)p.B * N * p.chunks;
+  const int N = p.N, B = p.B;
   const size_t plane = size_t(N) * N;
-  for (long long u = (long long)blockIdx.x * (kThreads / 64) + (tid >> 6); u < units;
-       u += (long long)gridDim.x * (kThreads / 64)) {
-    const int jc = int(u % p.chunks);
-    const long long row = u / p.chunks;  // b * N + i
-    const int i = int(row % N);
-    const int b = int(row / N);
-    const int j = jc * 16 + r16;
-    const bool in = j < N;
-    const size_t pair = size_t(row) * N + (in ? j : 0);
-    const bool valid = in && j != i && p.mask[pair] != 0;
-    const unsigned long long any = __ballot(valid);
+  // the rbf centres of this lane's features (lane g computes features g, g + 4, ... of its pair)
+  const float kexp = p.neg_gamma * 1.44269504088896341f;  // exp(-gamma s) = exp2(kexp s)
+  float cs[KS], cp[KP];
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const int f = 4 * t + g;
+    cs[t] = (f >= 3 && f < 3 + p.R) ? p.centers[f - 3] : 0.0f;
+  }
+#pragma unroll
+  for (int t = 0; t < KP; ++t) {
+    const int f = 4 * t + g;
+    cp[t] = f < p.R ? p.centers[f] : 0.0f;
+  }
+  // unit u = (cg * N + i) * B + b: molecule b, row i, 64-column group cg.  Each lane owns one pair (b, i, j)
+  // of the unit and writes the zeros of all outputs when the pair is invalid (256-byte row pieces per
+  // store); the 16-column chunks with a valid pair then run the MLPs and write their valid pairs.  Waves
+  // take units round-robin, the next unit's (cg, i, b) following by carries (wave-uniform scalar
+  // arithmetic), and its pair-mask byte is fetched one unit ahead.
+  const int nwaves = gridDim.x * (kThreads / 64);
+  const int db = nwaves % B, di = (nwaves / B) % N, dc = (nwaves / B) / N;
+  int b, i, cg;
+  {
+    const int u0 = blockIdx.x * (kThreads / 64) + (tid >> 6);
+    b = u0 % B;
+    i = (u0 / B) % N;
+    cg = (u0 / B) / N;
+  }
+  auto mask_byte = [&](int bb, int ii, int cc) -> unsigned {
+    const int j = cc * 64 + lane;
+    if (cc >= p.groups || j >= N) return 0u;
+    return p.mask[(size_t(bb) * N + ii) * N + j];
+  };
+  unsigned mbyte = mask_byte(b, i, cg);
+  while (cg < p.groups) {
+    int nb = b + db;
+    int carry = nb >= B;
+    nb -= carry ? B : 0;
+    int ni = i + di + carry;
+    carry = ni >= N;
+    ni -= carry ? N : 0;
+    const int ncg = cg + dc + carry;
+    const unsigned next = mask_byte(nb, ni, ncg);
+
+    const size_t prow = (size_t(b) * N + i) * N;
     // output element (o, b, i, j): ((b * H + o) * N + i) * N + j
-    const size_t obase = size_t(b) * H * plane + size_t(i) * N + j;
-    if (any == 0ull) {
-      if (in && g == 0) {
-        for (int m = 0; m < 3; ++m)
-          for (int o = 0; o < H; ++o) p.out[m][obase + size_t(o) * plane] = 0.0f;
+    const size_t obase = size_t(b) * H * plane + size_t(i) * N;
+    const int j = cg * 64 + lane;
+    const bool in = j < N;
+    const bool valid = in && j != i && mbyte != 0u;
+    if (in && !valid) {
+      for (int m = 0; m < 3; ++m) {
+        float* dst = p.out[m] + obase + j;
+        for (int o = 0; o < H; ++o) dst[size_t(o) * plane] = 0.0f;
       }
-      continue;
     }
-    // features of pair r16: lane g takes f = g, g + 4, ...
-    float xs[KS], xp[KP];
-    const float dn = in ? p.dnorm[pair] : 0.0f;
+    const unsigned long long bal = __ballot(valid);
+    for (int c = 0; c < 4; ++c) {
+      const unsigned bits = unsigned(bal >> (16 * c)) & 0xffffu;
+      if (bits == 0u) continue;  // wave-uniform
+      const int jc = cg * 64 + 16 * c + r16;
+      const bool jvalid = (bits >> r16) & 1u;
+      const size_t pair = prow + (jvalid ? jc : 0);
+      const float dn = jvalid ? p.dnorm[pair] : 0.0f;
+      float xs[KS], xp[KP];
 #pragma unroll
-    for (int t = 0; t < KS; ++t) {
-      const int f = 4 * t + g;
-      float v = 0.0f;
-      if (f < 3) {
-        v = in ? p.delta[3 * pair + f] : 0.0f;
-      } else if (f < 3 + p.R) {
-        const float d = dn - p.centers[f - 3];
-        const float sq = d * d;
-        v = expf(p.neg_gamma * sq);
+      for (int t = 0; t < KS; ++t) {
+        const int f = 4 * t + g;
+        const float d = dn - cs[t];
+        const float rbf = __builtin_amdgcn_exp2f(kexp * (d * d));
+        xs[t] = f < 3 ? (jvalid ? p.delta[3 * pair + f] : 0.0f) : (f < 3 + p.R ? rbf : 0.0f);
       }
-      xs[t] = v;
-    }
 #pragma unroll
-    for (int t = 0; t < KP; ++t) {
-      const int f = 4 * t + g;
-      float v = 0.0f;
-      if (f < p.R) {
-        const float d = dn - p.centers[f];
-        const float sq = d * d;
-        v = expf(p.neg_gamma * sq);
+      for (int t = 0; t < KP; ++t) {
+        const int f = 4 * t + g;
+        const float d = dn - cp[t];
+        xp[t] = f < p.R ? __builtin_amdgcn_exp2f(kexp * (d * d)) : 0.0f;
       }
-      xp[t] = v;
-    }
-    for (int m = 0; m < 3; ++m) {
-      const float* W1 = lds + off[m][0];
-      const float* B1 = lds + off[m][1];
-      const float* W2 = lds + off[m][2];
-      const float* B2 = lds + off[m][3];
-      const int s1 = m < 2 ? s1s : s1p;
-      mf_f32x4 o2;
+      for (int m = 0; m < 3; ++m) {
+        const mf_f32x4 o2 = m < 2 ? mlp16<KS>(xs, lds + off[m][0], lds + off[m][1], lds + off[m][2],
+                                               lds + off[m][3], s1s, s2, HT, g, r16)
+                                  : mlp16<KP>(xp, lds + off[m][0], lds + off[m][1], lds + off[m][2],
+                                              lds + off[m][3], s1p, s2, HT, g, r16);
+        if (jvalid) {
+          float* dst = p.out[m] + obase + jc;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o2[r] = B2[4 * g + r];
-      for (int ht = 0; ht < HT; ++ht) {
-        mf_f32x4 c1;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) c1[r] = B1[16 * ht + 4 * g + r];
-        const float* wrow = W1 + (16 * ht + r16) * s1 + g;
-        if (m < 2) {
-#pragma unroll
-          for (int t = 0; t < KS; ++t) c1 = mma(wrow[4 * t], xs[t], c1);
-        } else {
-#pragma unroll
-          for (int t = 0; t < KP; ++t) c1 = mma(wrow[4 * t], xp[t], c1);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float x = c1[r];
-          const float e = expf(-x);
-          const float den = 1.0f + e;
-          const float act = x / den;  // SiLU
-          o2 = mma(W2[r16 * s2 + 16 * ht + 4 * g + r], act, o2);
-        }
-      }
-      if (in) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int o = 4 * g + r;
-          if (o < H) p.out[m][obase + size_t(o) * plane] = valid ? o2[r] : 0.0f;
+          for (int r = 0; r < 4; ++r) {
+            const int o = 4 * g + r;
+            if (o < H) dst[size_t(o) * plane] = o2[r];
+          }
         }
       }
     }
+    b = nb;
+    i = ni;
+    cg = ncg;
+    mbyte = next;
   }
 }
 
@@ -207,8 +268,8 @@ int launch(const Params& p, int num_cus, hipStream_t s) {
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(pair_mlp_kernel<KS, KP>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   MF_HIP_CHECK(attr);
-  const long long units = (long long)p.B * p.N * p.chunks;
-  const int grid = int(std::min<long long>((units + 3) / 4, (long long)num_cus * 2));
+  const long long units = (long long)p.B * p.N * p.groups;
+  const int grid = int(std::min<long long>((units + 7) / 8, (long long)num_cus * 2));
   hipLaunchKernelGGL((pair_mlp_kernel<KS, KP>), dim3(grid), dim3(kThreads), lds, s, p);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
@@ -261,7 +322,9 @@ extern "C" int mf_pair_mlp_bias(const mf_pair_mlp_args* a, void* stream) {
   p.R = a->rbf;
   p.hidden = a->hidden;
   p.heads = a->heads;
-  p.chunks = (a->atoms + 15) / 16;
+  p.groups = (a->atoms + 63) / 64;
+  if ((long long)a->batch * a->atoms * (p.groups + 1) > 0x7fffffffLL)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: batch * atoms * ceil(atoms / 64) must stay below 2^31");
   const int ks = (3 + a->rbf + 3) / 4, kp = (a->rbf + 3) / 4;
   if (lds_bytes(ks, kp, a->hidden) > size_t(dev.max_lds_per_block))
     return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: weights exceed the LDS of a workgroup");
