@@ -563,14 +563,15 @@ def measure_simplicial_extras(lib, w, wd) -> dict:
                          "kernel_ms": round(bwd_ms, 5), "note": "eager call incl. zero-fills and casts"},
     }
 
-    # factorized bias (bf16), the default trunk's call: general kernel
+    # factorized bias (bf16), the default trunk's call: the pair kernel with the bias K step
     bias = [(torch.randn(B, H, N, N, generator=gen) * 0.5).to(dev, torch.bfloat16) for _ in range(3)] + \
            [torch.randn(B, H, N, generator=gen).to(dev, torch.bfloat16)]
     bias_step = _simplicial_call(lib, ops, wd.query_valid, wd.pair_key_valid, _native.MF_DTYPE_BF16, "bf16_tc",
                                  out=out, bias=bias)
     bias_ms = _graph_ms(bias_step)
     res["bias_fwd"] = {"ms": round(bias_ms, 5), "tflops": round(fwd_flops / (bias_ms * 1e-3) / 1e12, 3),
-                       "kernel": "mf::simplicial::simplicial_fwd_kernel<bf16, 64, 1> (factorized bias, bf16)"}
+                       "kernel": "mf::spair::simplicial_pair_kernel<bf16, 64, pair_valid=0, bias=1> "
+                                 "(factorized bias, bf16)"}
 
     # C1: QM9 fp32
     c1 = simplicial_workload("qm9").to(dev)

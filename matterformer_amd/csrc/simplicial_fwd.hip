@@ -960,16 +960,19 @@ static int simplicial_fwd_impl(const mf_simplicial_fwd_args* a, void* stream) {
   st = check_extras(a);
   if (st != MF_OK) return st;
   size_t lds = 0;
-  if (has_extras(a)) {
-    // the optional terms run on the general kernel
+  const bool outputs_aligned = reinterpret_cast<uintptr_t>(a->out) % 16 == 0 &&
+                               reinterpret_cast<uintptr_t>(a->out_f32) % 16 == 0;
+  const bool pair_ok = uses_fast(a->head_dim, a->dtype) && operands_aligned(a) && outputs_aligned &&
+                       simplicial_pair_serves(a->tokens, a->head_dim, a->dtype);
+  // the factorized bias alone runs in the pair kernel; the angle and message terms (and the bias on
+  // other shapes) run on the general kernel
+  const bool bias_only = a->bias_u != nullptr && a->angle_left == nullptr && a->message_left == nullptr;
+  if (has_extras(a) && !(bias_only && pair_ok)) {
     st = check_shape(a->batch, a->heads, a->tokens, a->head_dim, a->dtype, has_pv, &lds);
     if (st != MF_OK) return st;
     return launch_general(a, lds, dev.num_cus, 0, /*zero_rows=*/true, s);
   }
-  const bool outputs_aligned = reinterpret_cast<uintptr_t>(a->out) % 16 == 0 &&
-                               reinterpret_cast<uintptr_t>(a->out_f32) % 16 == 0;
-  if (uses_fast(a->head_dim, a->dtype) && operands_aligned(a) && outputs_aligned &&
-      simplicial_pair_serves(a->tokens, a->head_dim, a->dtype)) {
+  if (pair_ok) {
     // the pair-flash kernel: one launch per slice of molecules (the slices
     // share the claim counter at the start of the workspace, in stream order)
     const uint64_t need = simplicial_pair_workspace_bytes(a->batch, a->tokens) +

@@ -93,6 +93,13 @@ struct Params {
   float* lse;
   unsigned int* counter;  // claims of this launch (0 at launch start and end)
   int B, H, N, D;
+  // factorized bias S[j,k] += gate_i (u_ij + v_ik + w_jk): u, v, w [B*H, N, N] and gate [B*H, N] in
+  // bias_dtype (the BIAS instantiations only)
+  const void* bu;
+  const void* bv;
+  const void* bw;
+  const void* bg;
+  int bias_dtype;
 };
 
 // The claim counter in the caller's workspace (its own 128-byte line).  It
@@ -146,6 +153,18 @@ struct Lay {
   static constexpr int kRed = 0;
   static constexpr int kRedL = kRed + kWaves * kMaxQ * RS * 4;
   static_assert(kRedL + kWaves * kMaxQ * 4 <= kQ, "reduction area must fit in the K/V staging area");
+  // BIAS instantiations, after the above: fp16 bias operands of the unit's (j block, k block)
+  //   BU [kCap][kMaxQ]     c_i u_ij (row j, query i)
+  //   BW [kCap][kCap]      w_jk
+  //   BV [kMaxQ][kVS]      c_i v_ik at half k + 2 (halves 0, 1 and past the keys read as masked)
+  //   BG float [kMaxQ]     c_i = log2(e) 2^E gate_i; then per-query |u|, |v| maxima and the block |w| maximum
+  static constexpr int kVS = kCap + 16;
+  static constexpr int kBU = (kTotal + 15) & ~15;
+  static constexpr int kBW = kBU + kCap * kMaxQ * 2;
+  static constexpr int kBV = kBW + kCap * kCap * 2;
+  static constexpr int kBG = kBV + kMaxQ * kVS * 2;
+  static constexpr int kBMax = kBG + kMaxQ * 4;  // float [2][kMaxQ] |u|, |v| maxima, then |w|
+  static constexpr int kTotalBias = kBMax + (2 * kMaxQ + 1) * 4;
 };
 
 // ---------------------------------------------------------------------------
@@ -394,7 +413,13 @@ __device__ __forceinline__ uint32_t pv_mask(uint32_t bits4, int s) {
 }
 
 // The first QT of the MQ query tiles held in registers are in use.
-template <int DP, int QT, int MODE, bool HAS_PV, int MQ>
+//
+// BIAS: GEMM1 gets one more 32-wide K step per (row, query tile) whose
+// operands carry the factorized bias in log2 units (c_i = log2(e) 2^E gate_i):
+//   A[pair p][K]: K = 0 -> 1, K = 1 -> w[j][k0 + p], K = 2 + t -> (p == t), t < 16
+//   B[K][i]     : K = 0 -> c_i u[i][j], K = 1 -> c_i, K = 2 + t -> c_i v[i][k0 + t]
+// so the accumulator gains c_i (u_ij + w_jk + v_ik) for pair (j, k0 + p).
+template <int DP, int QT, int MODE, bool HAS_PV, bool BIAS, int MQ>
 __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, int nkk,
                                           const uint4 (&qop)[MQ][DP / 32], const float (&negm)[MQ], float sc,
                                           mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
@@ -416,6 +441,35 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
   const bool odd = (nkj & 1) != 0;
   constexpr uint32_t kOne2 = 0x3c003c00u;  // fp16 (1, 1)
   const mf_f32x4 zero4 = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  // BIAS: the constant part of the A operand (lane (g, r16) holds A[p = r16][K = 8g .. 8g + 7]), the
+  // mask of the B halves that carry v (K in [2, 18)), and c_i as fp16 per query tile
+  uint4 onehot{0u, 0u, 0u, 0u}, vmask{0u, 0u, 0u, 0u};
+  uint32_t cgh[MQ];
+  const unsigned char* BU = smem + Lay<DP>::kBU;
+  const unsigned char* BW = smem + Lay<DP>::kBW;
+  const unsigned char* BV = smem + Lay<DP>::kBV;
+  if constexpr (BIAS) {
+    uint32_t oh[4], vm[4];
+#pragma unroll
+    for (int h2 = 0; h2 < 4; ++h2) {
+      uint32_t o = 0u, m = 0u;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int K = 8 * g + 2 * h2 + e;
+        const bool one = K == 0 || (K >= 2 && K < 18 && r16 == K - 2);
+        o |= (one ? 0x3c00u : 0u) << (16 * e);
+        m |= (K >= 2 && K < 18 ? 0xffffu : 0u) << (16 * e);
+      }
+      oh[h2] = o;
+      vm[h2] = m;
+    }
+    onehot = uint4{oh[0], oh[1], oh[2], oh[3]};
+    vmask = uint4{vm[0], vm[1], vm[2], vm[3]};
+    const float* cg = reinterpret_cast<const float*>(smem + Lay<DP>::kBG);
+#pragma unroll
+    for (int qt = 0; qt < MQ; ++qt)
+      cgh[qt] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(cg[16 * qt + r16])));
+  }
   while (it < it1) {
     const int kt = it / njp;
     int jp = it - kt * njp;
@@ -448,6 +502,15 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
         const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
         v2p[dt][0] = __builtin_amdgcn_perm(rv[1][dt >> 1], rv[0][dt >> 1], sel);
         v2p[dt][1] = __builtin_amdgcn_perm(rv[3][dt >> 1], rv[2][dt >> 1], sel);
+      }
+    }
+    uint4 bvop[MQ];
+    if constexpr (BIAS) {
+      // halves k0 + 8g .. k0 + 8g + 7 of the query's BV row are K = 8g .. 8g + 7 (v at k + 2)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const uint4 t = *reinterpret_cast<const uint4*>(BV + ((16 * qt + r16) * Lay<DP>::kVS + k0 + 8 * g) * 2);
+        bvop[qt] = uint4{t.x & vmask.x, t.y & vmask.y, t.z & vmask.z, t.w & vmask.w};
       }
     }
     const int kvalid = nkk - (k0 + 4 * g);  // keys 4g + r valid for r < kvalid
@@ -504,6 +567,23 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
         for (int c = 1; c < NCH; ++c) {
           sa[qt] = mfma(wa[c], qop[qt][c], sa[qt]);
           sb[qt] = mfma(wb[c], qop[qt][c], sb[qt]);
+        }
+      }
+      if constexpr (BIAS) {
+        // rows j0, j0 + 1: w of the lane's pair into A (K = 1), c_i u_ij into B (K = 0), both on the g = 0
+        // lanes (the padding row j0 + 1 = nkj reads zeros)
+        const uint32_t w_a = *reinterpret_cast<const uint16_t*>(BW + (j0 * kCap + k0 + r16) * 2);
+        const uint32_t w_b = *reinterpret_cast<const uint16_t*>(BW + ((j0 + 1) * kCap + k0 + r16) * 2);
+        const uint4 ab_a{g == 0 ? (0x3c00u | (w_a << 16)) : onehot.x, onehot.y, onehot.z, onehot.w};
+        const uint4 ab_b{g == 0 ? (0x3c00u | (w_b << 16)) : onehot.x, onehot.y, onehot.z, onehot.w};
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const uint32_t u_a = *reinterpret_cast<const uint16_t*>(BU + (j0 * kMaxQ + 16 * qt + r16) * 2);
+          const uint32_t u_b = *reinterpret_cast<const uint16_t*>(BU + ((j0 + 1) * kMaxQ + 16 * qt + r16) * 2);
+          const uint4 bb_a{g == 0 ? (u_a | (cgh[qt] << 16)) : bvop[qt].x, bvop[qt].y, bvop[qt].z, bvop[qt].w};
+          const uint4 bb_b{g == 0 ? (u_b | (cgh[qt] << 16)) : bvop[qt].x, bvop[qt].y, bvop[qt].z, bvop[qt].w};
+          sa[qt] = mfma(ab_a, bb_a, sa[qt]);
+          sb[qt] = mfma(ab_b, bb_b, sb[qt]);
         }
       }
       if constexpr (MODE == kMax) {
@@ -571,15 +651,15 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
 }
 
 // pair_loop for the runtime tile count nqt (1 .. MQ)
-template <int DP, int MODE, bool HAS_PV, int MQ>
+template <int DP, int MODE, bool HAS_PV, bool BIAS, int MQ>
 __device__ __forceinline__ void pair_loop_n(int nqt, const unsigned char* smem, int nkj, int nkk,
                                             const uint4 (&qop)[MQ][DP / 32], const float (&negm)[MQ], float sc,
                                             mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
                                             int g, int r16) {
   static_assert(MQ == 3, "three query tiles");
-  if (nqt == 1) pair_loop<DP, 1, MODE, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
-  else if (nqt == 2) pair_loop<DP, 2, MODE, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
-  else pair_loop<DP, 3, MODE, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+  if (nqt == 1) pair_loop<DP, 1, MODE, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+  else if (nqt == 2) pair_loop<DP, 2, MODE, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+  else pair_loop<DP, 3, MODE, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
 }
 
 // ---------------------------------------------------------------------------
@@ -616,7 +696,18 @@ __device__ __forceinline__ void zero_padded_share(const Params& p, const uint32_
   }
 }
 
-template <typename T, int DP, bool HAS_PV, bool MULTI>
+// An element of a bias tensor as float.
+__device__ __forceinline__ float bias_at(const void* t, size_t idx, int dtype) {
+  if (dtype == MF_DTYPE_F32) return static_cast<const float*>(t)[idx];
+  if (dtype == MF_DTYPE_BF16) return float(static_cast<const __bf16*>(t)[idx]);
+  return float(static_cast<const _Float16*>(t)[idx]);
+}
+// fp16 bits of x, saturated to the finite range
+__device__ __forceinline__ uint16_t half_bits_sat(float x) {
+  return __builtin_bit_cast(uint16_t, _Float16(fminf(fmaxf(x, -65504.0f), 65504.0f)));
+}
+
+template <typename T, int DP, bool HAS_PV, bool MULTI, bool BIAS>
 __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, int b, int h, int nk, int q0, int nqg,
                                           bool kpre, bool qpre, bool zero_share) {
   constexpr int QT = kMaxQ / 16;       // query tiles held in registers
@@ -800,6 +891,107 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   __syncthreads();
   const int s1 = scal[0], s2 = scal[1], t1 = scal[2], t2 = scal[3], sq = scal[4], E = scal[5];
 
+  // ---- factorized bias (BIAS): c_i, then the fp16 operands of a block ------
+  float* cgf = reinterpret_cast<float*>(smem + Ly::kBG);
+  float* bmax = reinterpret_cast<float*>(smem + Ly::kBMax);  // max |u|, |v|, |w| of the unit's staged values
+  // (j block, k block): BU[j][i] = c_i u_ij, BW[j][k] = w_jk, BV[i][k + 2] = c_i v_ik over the staged rows,
+  // zero past the valid keys and queries
+  auto stage_bias = [&](int jc, int kc) {
+    uint16_t* BU = reinterpret_cast<uint16_t*>(smem + Ly::kBU);
+    uint16_t* BW = reinterpret_cast<uint16_t*>(smem + Ly::kBW);
+    uint16_t* BV = reinterpret_cast<uint16_t*>(smem + Ly::kBV);
+    const int j0 = jc * kCap, k0 = kc * kCap;
+    const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
+    const int rj = round16(nkj), rk = round16(nkk);
+    const int dt = p.bias_dtype;
+    float mu = 0.0f, mv = 0.0f, mw = 0.0f;
+    // sets [rows][cols] with the key index fastest (consecutive threads read consecutive keys); kB loads
+    // per thread are issued before their conversions and stores
+    constexpr int kB = 8;
+    // U: rows = queries, cols = rows j of the j block -> BU[j][qi] = c_qi u[qa][ka_j]
+    for (int base = tid; base < kMaxQ * rj; base += kB * kThreads) {
+      float val[kB];
+#pragma unroll
+      for (int t = 0; t < kB; ++t) {
+        const int e = base + t * kThreads;
+        const int qi = e / rj, j = e - qi * rj;
+        const bool ok = e < kMaxQ * rj && j < nkj && qi < nqg;
+        const int qa = ok ? (qpre ? q0 + qi : int(qidx[q0 + qi])) : 0;
+        val[t] = ok ? bias_at(p.bu, (size_t(bh) * N + qa) * N + key_atom(j0 + j), dt) : 0.0f;
+      }
+#pragma unroll
+      for (int t = 0; t < kB; ++t) {
+        const int e = base + t * kThreads;
+        if (e >= kMaxQ * rj) break;
+        const int qi = e / rj, j = e - qi * rj;
+        mu = fmaxf(mu, fabsf(val[t]));
+        BU[j * kMaxQ + qi] = half_bits_sat(cgf[qi] * val[t]);
+      }
+    }
+    // V: rows = queries, cols = keys of the k block -> BV[qi][k + 2] = c_qi v[qa][ka_k]
+    for (int base = tid; base < kMaxQ * rk; base += kB * kThreads) {
+      float val[kB];
+#pragma unroll
+      for (int t = 0; t < kB; ++t) {
+        const int e = base + t * kThreads;
+        const int qi = e / rk, k = e - qi * rk;
+        const bool ok = e < kMaxQ * rk && k < nkk && qi < nqg;
+        const int qa = ok ? (qpre ? q0 + qi : int(qidx[q0 + qi])) : 0;
+        val[t] = ok ? bias_at(p.bv, (size_t(bh) * N + qa) * N + key_atom(k0 + k), dt) : 0.0f;
+      }
+#pragma unroll
+      for (int t = 0; t < kB; ++t) {
+        const int e = base + t * kThreads;
+        if (e >= kMaxQ * rk) break;
+        const int qi = e / rk, k = e - qi * rk;
+        mv = fmaxf(mv, fabsf(val[t]));
+        BV[qi * Ly::kVS + k + 2] = half_bits_sat(cgf[qi] * val[t]);
+      }
+    }
+    // W: rows j of the j block, cols = keys of the k block -> BW[j][k] = w[ka_j][ka_k]
+    for (int base = tid; base < rj * rk; base += kB * kThreads) {
+      float val[kB];
+#pragma unroll
+      for (int t = 0; t < kB; ++t) {
+        const int e = base + t * kThreads;
+        const int j = e / rk, k = e - j * rk;
+        const bool ok = e < rj * rk && j < nkj && k < nkk;
+        val[t] = ok ? bias_at(p.bw, (size_t(bh) * N + key_atom(j0 + j)) * N + key_atom(k0 + k), dt) : 0.0f;
+      }
+#pragma unroll
+      for (int t = 0; t < kB; ++t) {
+        const int e = base + t * kThreads;
+        if (e >= rj * rk) break;
+        const int j = e / rk, k = e - j * rk;
+        mw = fmaxf(mw, fabsf(val[t]));
+        BW[j * kCap + k] = half_bits_sat(val[t]);
+      }
+    }
+    // magnitudes: float order equals bit order
+    atomicMax(reinterpret_cast<unsigned int*>(bmax + 0), __float_as_uint(mu));
+    atomicMax(reinterpret_cast<unsigned int*>(bmax + 1), __float_as_uint(mv));
+    atomicMax(reinterpret_cast<unsigned int*>(bmax + 2), __float_as_uint(mw));
+  };
+  if constexpr (BIAS) {
+    for (int qi = tid; qi < kMaxQ; qi += kThreads) {
+      float c = 0.0f;
+      if (qi < nqg) {
+        const int qa = qpre ? q0 + qi : int(qidx[q0 + qi]);
+        c = ldexpf(bias_at(p.bg, size_t(bh) * N + qa, p.bias_dtype) * kLog2e, E);
+      }
+      cgf[qi] = c;
+    }
+    if (tid < 3) bmax[tid] = 0.0f;
+    __syncthreads();
+    if constexpr (!MULTI) {
+      stage_bias(0, 0);
+      __syncthreads();
+    } else {
+      if (tid == 0) scal[6] = 1;  // blocks stage their bias one pair at a time: two passes, exact maxima
+    }
+  }
+  const float bias_mag = BIAS ? bmax[0] + bmax[1] + bmax[2] : 0.0f;
+
   // ---- phase B: query rows, bounds ---------------------------------------
   {
     unsigned char* Qs = smem + Ly::kQ;
@@ -824,6 +1016,9 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       if (row < 16 * QT) *reinterpret_cast<uint4*>(Qs + row * RB + e0 * 2) = uint4{w[0], w[1], w[2], w[3]};
       // |S| bound of the row: the CPR lanes of a row are consecutive
       ub = __uint_as_float(group_reduce<CPR>(__float_as_uint(ub), AddF32{}));
+      if constexpr (BIAS) {
+        if (row < nqg) ub += fabsf(cgf[row]) * bias_mag;
+      }
       if (row < nqg && cc == 0 && !(ub <= kBoundLimit)) atomicOr(&scal[6], 1);
     }
   }
@@ -890,6 +1085,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       for (int i = 0; i < MAXC; ++i)
         if ((tid + kThreads * i) / CPR < rk) store_v(V2s, t[i], (tid + kThreads * i) / CPR, t2);
     }
+    if constexpr (BIAS && MULTI) stage_bias(jc, kc);
     if constexpr (HAS_PV) {
       // bits of pair_valid for rows j of the j block and keys k of the k block
       uint32_t* pvb = reinterpret_cast<uint32_t*>(smem + Ly::kPV);
@@ -958,11 +1154,11 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     slow = scal[6] != 0;
     load_qop();
     if (!slow) {
-      pair_loop_n<DP, kFast, HAS_PV>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+      pair_loop_n<DP, kFast, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
     } else {
-      pair_loop_n<DP, kMax, HAS_PV>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+      pair_loop_n<DP, kMax, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
       finish_max();
-      pair_loop_n<DP, kSlow, HAS_PV>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+      pair_loop_n<DP, kSlow, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
     }
   } else if (MULTI && nch > 1) {
     __syncthreads();
@@ -975,11 +1171,11 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
           __syncthreads();
           const int nkj = min(kCap, nk - jc * kCap), nkk = min(kCap, nk - kc * kCap);
           if (pass == 0)
-            pair_loop<DP, 1, kMax, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+            pair_loop<DP, 1, kMax, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
           else if (slow)
-            pair_loop<DP, 1, kSlow, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+            pair_loop<DP, 1, kSlow, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
           else
-            pair_loop<DP, 1, kFast, HAS_PV>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+            pair_loop<DP, 1, kFast, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
           __syncthreads();
         }
       }
@@ -1239,7 +1435,7 @@ __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* 
 
 // One unit (molecule b, head h, query group g): index lists of non-prefix
 // masks and the attention of the group's queries.  Ends with a barrier.
-template <typename T, int DP, bool HAS_PV>
+template <typename T, int DP, bool HAS_PV, bool BIAS>
 __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, int b, int h, int g, bool zero_share) {
   using Ly = Lay<DP>;
   const int tid = threadIdx.x;
@@ -1258,8 +1454,8 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
       if (wave == 1 && !qpre) write_ranks(p.qv + size_t(b) * p.N, p.N, qidx, lane);
       __syncthreads();
     }
-    if (nk > kCap) unit_body<T, DP, HAS_PV, true>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
-    else unit_body<T, DP, HAS_PV, false>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
+    if (nk > kCap) unit_body<T, DP, HAS_PV, true, BIAS>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
+    else unit_body<T, DP, HAS_PV, false, BIAS>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
   }
   __syncthreads();
 }
@@ -1272,8 +1468,9 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
 // first; after that a workgroup that
 // finishes a unit claims the next position with one device-scope atomic, so
 // the workgroups that finish first take the longest remaining units.
-template <typename T, int DP, bool HAS_PV>
-__global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) {
+// BIAS: one workgroup per CU (its bias operands take another ~59 KB of LDS).
+template <typename T, int DP, bool HAS_PV, bool BIAS>
+__global__ void __launch_bounds__(kThreads, BIAS ? 1 : 2) simplicial_pair_kernel(Params p) {
   using Ly = Lay<DP>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + Ly::kInfo);
@@ -1283,7 +1480,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
   __shared__ int s_first;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int B = p.B, H = p.H;
+  const int B = p.B;
   const int G = gridDim.x;
   const int wg = blockIdx.x;
 
@@ -1314,7 +1511,7 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
     const uint32_t info = s_info[b];
     const int ng = num_groups(info_nk(info), info_nq(info));
     const int h = div_small(i, ng);
-    run_unit<T, DP, HAS_PV>(p, smem, b, h, i - h * ng, pos == wg);  // ends with a barrier: cl->next is read
+    run_unit<T, DP, HAS_PV, BIAS>(p, smem, b, h, i - h * ng, pos == wg);  // ends with a barrier: cl->next is read
     if (tid == 0) {
       if (cl->claimed) {
         cl->claimed = 0;  // the unit claimed the next position
@@ -1329,11 +1526,11 @@ __global__ void __launch_bounds__(kThreads, 2) simplicial_pair_kernel(Params p) 
   }
 }
 
-template <typename T, int DP, bool HAS_PV>
+template <typename T, int DP, bool HAS_PV, bool BIAS>
 int launch(const Params& prm, int num_cus, hipStream_t stream) {
-  const int grid = std::max(8, 2 * num_cus);  // 2 workgroups per CU
-  auto kern = simplicial_pair_kernel<T, DP, HAS_PV>;
-  const size_t lds = Lay<DP>::kTotal;
+  const int grid = std::max(8, (BIAS ? 1 : 2) * num_cus);  // 2 workgroups per CU (1 with the bias)
+  auto kern = simplicial_pair_kernel<T, DP, HAS_PV, BIAS>;
+  const size_t lds = BIAS ? Lay<DP>::kTotalBias : Lay<DP>::kTotal;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
     MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1371,21 +1568,36 @@ int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* claims, int nu
     return fail(MF_ERR_INVALID_ARGUMENT, "simplicial pair launch: batch slice too large");
   if (!simplicial_pair_serves(a->tokens, a->head_dim, a->dtype))
     return fail(MF_ERR_UNSUPPORTED, "simplicial pair launch: unsupported shape");
+  if (a->angle_left != nullptr || a->message_left != nullptr)
+    return fail(MF_ERR_UNSUPPORTED, "simplicial pair launch: angle and message terms run on the general kernel");
   Params prm{};
   prm.q = a->q; prm.k1 = a->k1; prm.v1 = a->v1; prm.k2 = a->k2; prm.v2 = a->v2;
   prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
   prm.out = a->out; prm.out_f32 = a->out_f32; prm.lse = a->lse;
   prm.B = a->batch; prm.H = a->heads; prm.N = a->tokens; prm.D = a->head_dim;
   prm.counter = static_cast<unsigned int*>(claims);
+  prm.bu = a->bias_u; prm.bv = a->bias_v; prm.bw = a->bias_w; prm.bg = a->bias_gate;
+  prm.bias_dtype = a->bias_dtype;
   const int g = num_cus;
   const bool pv = a->pair_valid != nullptr;
   const bool bf = a->dtype == MF_DTYPE_BF16;
+  const bool bias = a->bias_u != nullptr;
+  auto go = [&](auto tag, auto dp, auto has_pv) {
+    using T = decltype(tag);
+    constexpr int DP = decltype(dp)::value;
+    constexpr bool PV = decltype(has_pv)::value;
+    return bias ? launch<T, DP, PV, true>(prm, g, stream) : launch<T, DP, PV, false>(prm, g, stream);
+  };
+  using I32 = std::integral_constant<int, 32>;
+  using I64 = std::integral_constant<int, 64>;
+  using PV1 = std::true_type;
+  using PV0 = std::false_type;
   if (a->head_dim <= 32) {
-    if (bf) return pv ? launch<__bf16, 32, true>(prm, g, stream) : launch<__bf16, 32, false>(prm, g, stream);
-    return pv ? launch<_Float16, 32, true>(prm, g, stream) : launch<_Float16, 32, false>(prm, g, stream);
+    if (bf) return pv ? go(__bf16{}, I32{}, PV1{}) : go(__bf16{}, I32{}, PV0{});
+    return pv ? go(_Float16{}, I32{}, PV1{}) : go(_Float16{}, I32{}, PV0{});
   }
-  if (bf) return pv ? launch<__bf16, 64, true>(prm, g, stream) : launch<__bf16, 64, false>(prm, g, stream);
-  return pv ? launch<_Float16, 64, true>(prm, g, stream) : launch<_Float16, 64, false>(prm, g, stream);
+  if (bf) return pv ? go(__bf16{}, I64{}, PV1{}) : go(__bf16{}, I64{}, PV0{});
+  return pv ? go(_Float16{}, I64{}, PV1{}) : go(_Float16{}, I64{}, PV0{});
 }
 
 }  // namespace mf

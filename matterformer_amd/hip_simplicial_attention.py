@@ -229,7 +229,8 @@ def hip_simplicial_attention_forward(
                           message_left, message_right, message_basis)
 
     lib = _native.lib()
-    ws_bytes = 0 if ext.present else lib.mf_simplicial_fwd_workspace_size(B, H, N, D, _native.dtype_code(cdt))
+    # (the factorized bias alone runs in the pair kernel and uses the workspace too)
+    ws_bytes = lib.mf_simplicial_fwd_workspace_size(B, H, N, D, _native.dtype_code(cdt))
     ws = _native.workspace(ws_bytes, q.device)
     args = _native.MfSimplicialFwdArgs(
         q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(),

@@ -167,6 +167,22 @@ def test_16bit_terms_match_fp64(cuda, shape, terms, dtype):
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
 
 
+@pytest.mark.parametrize("shape", [(3, 2, 45, 64, [45, 30, 7], [(1, 2)], 0.1), (2, 1, 130, 64, [130, 77], None, 0.0)],
+                         ids=["one_block", "key_blocks"])
+def test_16bit_large_bias_takes_two_passes(cuda, shape):
+    """Bias terms of several units in log2 units (beyond the one-pass bound): the exact two-pass maxima,
+    every valid query row against float64."""
+    B, H, N, D, counts, holes, drop = shape
+    case = random_simplicial(B, H, N, D, seed=N + 11, counts=counts, holes=holes, pair_drop=drop,
+                            std=logit_std(D))
+    tm = make_terms(B, H, N, D, seed=N + 12, scale=6.0)
+    out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc")
+    ref, ref_lse = oracle(case, tm, torch.bfloat16)
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+    assert row_errors(out32.cpu().numpy(), ref, case[5]).max() <= 6e-2
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
 def test_fp32_bias_with_bf16_operands(cuda):
     """The module passes the bias in its own dtype: fp32 bias with bf16 operands."""
     case = random_simplicial(2, 2, 40, 64, seed=3, counts=[40, 21], std=logit_std(64))
