@@ -450,6 +450,58 @@ def measure_trunk() -> dict:
                       "per-token work on the valid atoms (TokenPacking)"}
 
 
+def measure_trunk_geometry() -> dict:
+    """configs[4] with the geometry terms: the trunk of measure_trunk plus a NonPeriodicGeometryAdapter and a
+    SimplicialGeometryBias (factorized, hidden 128, 16 rbf; fp32 modules, output layers drawn N(0, 0.3^2) so
+    the bias is not zero) whose features, u/v/w MLPs (mf_pair_mlp_bias) and noise gate run once per forward
+    on the packing's compact layout and feed the six simplicial blocks through the pair kernel's bias K step."""
+    import torch
+
+    from matterformer_amd.geometry import NonPeriodicGeometryAdapter
+    from matterformer_amd.geometry_bias import SimplicialGeometryBias
+    from matterformer_amd.trunk import AlternatingTrunk, TokenPacking
+    from matterformer_amd.workloads import trunk_workload
+
+    dev = torch.device("cuda", 0)
+    w = trunk_workload()
+    torch.manual_seed(4)
+    bias = SimplicialGeometryBias(w.heads, mode="factorized", edge_bias_hidden_dim=128, edge_bias_n_rbf=16)
+    trunk = AlternatingTrunk(w.d_model, w.heads, w.layers, knn_k=w.knn_k,
+                             geometry_adapter=NonPeriodicGeometryAdapter(), simplicial_geometry_bias=bias)
+    x, cond = w.x.to(dev, torch.bfloat16), w.cond.to(dev, torch.bfloat16)
+    coords, pad = w.coords.to(dev), w.pad_mask.to(dev)
+    gen = torch.Generator().manual_seed(105)
+    sigma = (torch.rand(w.x.shape[0], generator=gen) * 2.0 + 0.05).to(dev)
+    with torch.no_grad():
+        # materialises the LazyLinear layers (CPU, torch formulation)
+        bias._compute_factorized_terms(NonPeriodicGeometryAdapter()(w.coords[:1], w.pad_mask[:1]))
+        for name, prm in bias.named_parameters():
+            if name.endswith(".2.weight") or name.endswith(".2.bias"):
+                prm.data.copy_(torch.randn(prm.shape, generator=gen) * 0.3)
+    trunk.blocks.to(dev).to(torch.bfloat16)
+    trunk.geometry_adapter.to(dev)
+    bias.to(dev)
+    trunk.eval()
+    for blk in trunk.blocks:
+        lin = blk.ada_ln[-1]
+        lin.weight.data.copy_((torch.randn(lin.weight.shape, generator=gen) * 0.05).to(lin.weight.dtype))
+        lin.bias.data.copy_((torch.randn(lin.bias.shape, generator=gen) * 0.05).to(lin.bias.dtype))
+    packing = TokenPacking(pad)
+
+    def step():
+        with torch.no_grad():
+            trunk(x, cond, coords, pad, sigma=sigma, packing=packing)
+
+    stream = torch.cuda.current_stream()
+    eager_ms, _ = timed_loop(stream, step, 10, 3)
+    ms = graph_times(stream, step, per_graph=1, replays=20)
+    return {"ms": round(ms, 4), "molecules_per_s": round(w.x.shape[0] / (ms * 1e-3), 1),
+            "eager_ms": round(eager_ms, 4),
+            "ms_source": "HIP events around replays of the packed forward captured in one HIP graph",
+            "config": "the c5_trunk configuration plus NonPeriodicGeometryAdapter + SimplicialGeometryBias "
+                      "(factorized, fp32), sigma U[0.05, 2.05), terms on the compact layout"}
+
+
 def _line(metric, value, unit, ms, args, dtype, data, config, **more):
     line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -641,6 +693,7 @@ def main() -> int:
         extra["knn"] = measure_knn(args.cpu_sample)
         extra["radius"] = measure_radius(args.cpu_sample)
         extra["c5_trunk"] = measure_trunk()
+        extra["c5_trunk_geometry"] = measure_trunk_geometry()
         extra["geometry_features"] = measure_geometry()
         extra["pair_mlp_bias"] = measure_pair_mlp()
 

@@ -463,16 +463,19 @@ class AlternatingTrunk(nn.Module):
         otherwise a GPU call with a pad_mask builds it."""
         if pad_mask is not None:
             pad_mask = pad_mask.bool()
-        terms = self.simplicial_terms(coords, pad_mask, lattice, sigma)
-        if packing is not None:
-            if pad_mask is None or (packing.batch, packing.atoms) != tuple(pad_mask.shape):
-                raise ValueError("packing must be built from this call's pad_mask")
-            if not self.packable(x, terms):
+        if packing is not None and (pad_mask is None or (packing.batch, packing.atoms) != tuple(pad_mask.shape)):
+            raise ValueError("packing must be built from this call's pad_mask")
+        explicit = packing is not None
+        if pad_mask is not None and (explicit or self.packable(x)):
+            # the packed forward: geometry features and simplicial terms straight on the compact layout
+            # (each molecule's valid atoms first, width W), which is what the packed blocks read
+            packing = packing if explicit else TokenPacking(pad_mask)
+            cterms = self.simplicial_terms(packing.compact(coords), packing.compact_pad_mask, lattice, sigma)
+            if self.packable(x, cterms):
+                return self._forward_packed(x, cond_emb, coords, packing, cterms)
+            if explicit:
                 raise RuntimeError("the packed forward needs every block on its HIP kernels")
-        elif pad_mask is not None and self.packable(x, terms):
-            packing = TokenPacking(pad_mask)
-        if packing is not None:
-            return self._forward_packed(x, cond_emb, coords, packing, terms)
+        terms = self.simplicial_terms(coords, pad_mask, lattice, sigma)
         mask = None
         if "knn_local" in self.schedule:
             mask = build_knn_mask(coords, self.knn_k, pad_mask, use_hip=self._use_hip(x))
@@ -502,6 +505,7 @@ class AlternatingTrunk(nn.Module):
 
     def _forward_packed(self, x: torch.Tensor, cond_emb: torch.Tensor | None, coords: torch.Tensor,
                         packing: TokenPacking, terms: SimplicialTerms | None = None) -> torch.Tensor:
+        """``terms``: the simplicial terms on the packing's compact layout (or None: key padding only)."""
         """The blocks on the valid rows; attention masks and kNN lists in the compact layout (each molecule's
         valid atoms first, width = its largest count).  With adaLN, one mf_adaln_rows pass joins each
         residual to the next LayerNorm + modulation, the last block's MLP residual to the next block's norm1."""
@@ -510,9 +514,7 @@ class AlternatingTrunk(nn.Module):
         mask = None
         if "knn_local" in self.schedule:
             mask = build_knn_mask(packing.compact(coords.float()), self.knn_k, cpad, use_hip=True)
-        if terms is not None:
-            terms = terms.compact(packing)
-        else:
+        if terms is None:
             terms = SimplicialTerms(coerce_attention_mask(None, key_padding_mask=cpad, batch_size=B, num_tokens=W,
                                                           device=x.device))
         xp = packing.pack(x)
