@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 6
+#define MF_ABI_VERSION 7
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -319,7 +319,8 @@ int mf_radius_mask(const mf_radius_mask_args* args, void* stream);
 typedef struct mf_geometry_args {
   const float* coords;     /* [B, N, 3] fp32 (fractional when periodic)      */
   const float* gram;       /* [B, 3, 3] fp32 metric, or NULL (non-periodic)  */
-  const float* scale;      /* [B] fp32 normaliser of dist_norm, or NULL      */
+  float* scale;            /* [B] fp32 normaliser of dist_norm, or NULL; read
+                              (MF_SCALE_GIVEN) or written first (MF_SCALE_RMS) */
   const uint8_t* pad_mask; /* [B, N] bytes, nonzero = padding, or NULL       */
   float* pair_delta;       /* [B, N, N, 3] out, or NULL                      */
   float* pair_dist2;       /* [B, N, N] out, or NULL                         */
@@ -330,7 +331,16 @@ typedef struct mf_geometry_args {
   int32_t batch;
   int32_t atoms;
   int32_t pbc_radius;      /* 1 or 2 (ignored when gram == NULL)             */
+  /* ABI 7: the adapter's small steps in the same call                        */
+  uint8_t* pair_mask;      /* [B, N, N] out: 1 on valid pairs, or NULL       */
+  int32_t scale_mode;      /* MF_SCALE_GIVEN: read `scale`; MF_SCALE_RMS:
+                              write the root-mean-square |x| of each molecule's
+                              valid atoms (the non-periodic adapter's radius,
+                              adapters.py:116-118) into `scale`, then use it */
 } mf_geometry_args;
+
+#define MF_SCALE_GIVEN 0
+#define MF_SCALE_RMS 1
 
 int mf_geometry_features(const mf_geometry_args* args, void* stream);
 

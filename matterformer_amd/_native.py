@@ -50,7 +50,7 @@ EXPORTED_SYMBOLS = (
     "mf_pair_mlp_bias",
 )
 
-EXPECTED_ABI_VERSION = 6
+EXPECTED_ABI_VERSION = 7
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -150,7 +150,12 @@ class MfGeometryArgs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "coords", "gram", "scale", "pad_mask", "pair_delta", "pair_dist2", "pair_dist", "pair_dist_norm",
         "mask_bits")] + [("cutoff", ctypes.c_float), ("batch", ctypes.c_int32), ("atoms", ctypes.c_int32),
-                         ("pbc_radius", ctypes.c_int32)]
+                         ("pbc_radius", ctypes.c_int32), ("pair_mask", ctypes.c_void_p),
+                         ("scale_mode", ctypes.c_int32)]
+
+
+MF_SCALE_GIVEN = 0
+MF_SCALE_RMS = 1
 
 
 class MfRadiusAttnArgs(ctypes.Structure):

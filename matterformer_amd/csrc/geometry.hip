@@ -39,6 +39,7 @@ struct Params {
   const float* gram;
   const float* scale;
   const uint8_t* pad;
+  uint8_t* pmask;
   float* delta;
   float* d2;
   float* dist;
@@ -94,6 +95,47 @@ __device__ __forceinline__ float min_image(float d0, float d1, float d2v, const 
   return best;
 }
 
+// The non-periodic adapter's radius (adapters.py:116-118): one workgroup per
+// molecule, sqrt(max(sum over valid atoms of |x|^2 / max(count, 1), 1e-8)),
+// at least 1e-8.  |x|^2 = (x x + y y) + z z as square().sum(-1) rounds it.
+__global__ void __launch_bounds__(kThreads) rms_kernel(const float* coords, const uint8_t* pad, float* scale, int N) {
+  __shared__ float s_sum[kWavesPerBlock];
+  __shared__ int s_cnt[kWavesPerBlock];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float sum = 0.0f;
+  int cnt = 0;
+  for (int a = tid; a < N; a += kThreads) {
+    const size_t r = size_t(b) * N + a;
+    if (pad != nullptr && pad[r] != 0) continue;
+    const float x = coords[3 * r + 0], y = coords[3 * r + 1], z = coords[3 * r + 2];
+    const float xx = x * x;
+    const float yy = y * y;
+    const float zz = z * z;
+    const float s2 = xx + yy;
+    sum += s2 + zz;
+    ++cnt;
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    sum += __shfl_xor(sum, off, 64);
+    cnt += __shfl_xor(cnt, off, 64);
+  }
+  if (lane == 0) {
+    s_sum[wave] = sum;
+    s_cnt[wave] = cnt;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.0f;
+    int c = 0;
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+      t += s_sum[w];
+      c += s_cnt[w];
+    }
+    const float mean = t / float(c > 0 ? c : 1);
+    scale[b] = fmaxf(sqrtf(fmaxf(mean, 1e-8f)), 1e-8f);
+  }
+}
+
 template <int R>  // R = 0: non-periodic
 __global__ void __launch_bounds__(kThreads) features_kernel(Params p) {
   const int lane = threadIdx.x & 63;
@@ -139,6 +181,7 @@ __global__ void __launch_bounds__(kThreads) features_kernel(Params p) {
       if (p.d2) p.d2[o] = ok ? dd : 0.0f;
       if (p.dist) p.dist[o] = ok ? d : 0.0f;
       if (p.dnorm) p.dnorm[o] = ok ? d / p.scale[b] : 0.0f;
+      if (p.pmask) p.pmask[o] = ok ? 1 : 0;
     }
     if (p.bits) {
       const unsigned long long m = __ballot(ok && dd <= p.rc2);
@@ -160,6 +203,11 @@ extern "C" int mf_geometry_features(const mf_geometry_args* a, void* stream) {
     return fail(MF_ERR_INVALID_ARGUMENT, "mf_geometry_features: batch and atoms must be non-negative");
   if (a->pair_dist_norm && !a->scale)
     return fail(MF_ERR_INVALID_ARGUMENT, "mf_geometry_features: pair_dist_norm needs scale");
+  if (a->scale_mode != MF_SCALE_GIVEN && a->scale_mode != MF_SCALE_RMS)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_geometry_features: unknown scale_mode");
+  if (a->scale_mode == MF_SCALE_RMS && (!a->scale || a->gram))
+    return fail(MF_ERR_INVALID_ARGUMENT,
+                "mf_geometry_features: MF_SCALE_RMS needs a scale buffer and no gram (non-periodic)");
   if (a->mask_bits && !(a->cutoff > 0.0f))
     return fail(MF_ERR_INVALID_ARGUMENT, "mf_geometry_features: mask_bits needs a positive cutoff");
   if (a->gram && a->pbc_radius != 1 && a->pbc_radius != 2)
@@ -169,13 +217,18 @@ extern "C" int mf_geometry_features(const mf_geometry_args* a, void* stream) {
   int st = device_info(&dev);
   if (st != MF_OK) return st;
   Params p{};
-  p.coords = a->coords; p.gram = a->gram; p.scale = a->scale; p.pad = a->pad_mask;
+  p.coords = a->coords; p.gram = a->gram; p.scale = a->scale; p.pad = a->pad_mask; p.pmask = a->pair_mask;
   p.delta = a->pair_delta; p.d2 = a->pair_dist2; p.dist = a->pair_dist; p.dnorm = a->pair_dist_norm;
   p.bits = a->mask_bits; p.rc2 = a->cutoff * a->cutoff;
   p.B = a->batch; p.N = a->atoms; p.W = (a->atoms + 31) / 32; p.chunks = (a->atoms + 63) / 64;
   const long long units = (long long)p.B * p.N * p.chunks;
   const int grid = int(std::min<long long>((units + kWavesPerBlock - 1) / kWavesPerBlock, (long long)dev.num_cus * 32));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->scale_mode == MF_SCALE_RMS) {
+    hipLaunchKernelGGL(rms_kernel, dim3(a->batch), dim3(kThreads), 0, s, a->coords, a->pad_mask, a->scale,
+                       a->atoms);
+    MF_HIP_CHECK(hipGetLastError());
+  }
   if (a->gram == nullptr) hipLaunchKernelGGL(features_kernel<0>, dim3(grid), dim3(kThreads), 0, s, p);
   else if (a->pbc_radius == 1) hipLaunchKernelGGL(features_kernel<1>, dim3(grid), dim3(kThreads), 0, s, p);
   else hipLaunchKernelGGL(features_kernel<2>, dim3(grid), dim3(kThreads), 0, s, p);

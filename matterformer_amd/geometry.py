@@ -54,6 +54,19 @@ def lattice_latent_to_y1(lattice: torch.Tensor, lattice_repr: str = "y1") -> tor
     raise ValueError(f"Unsupported lattice_repr: {lattice_repr}")
 
 
+_METRICS: dict = {}
+
+
+def _identity_metric(batch: int, device: torch.device) -> torch.Tensor:
+    """torch.eye(3) expanded over the batch (the non-periodic adapter's metric), one 3x3 tensor per device."""
+    key = (device.type, device.index)
+    eye = _METRICS.get(key)
+    if eye is None:
+        eye = torch.eye(3, device=device, dtype=torch.float32)
+        _METRICS[key] = eye
+    return eye.expand(batch, -1, -1)
+
+
 class BaseGeometryAdapter(nn.Module):
     geometry_kind: str = "base"
 
@@ -79,31 +92,37 @@ class BaseGeometryAdapter(nn.Module):
 
     @staticmethod
     def _hip_features(coords, pad_mask, scale, gram, pbc_radius, radius_cutoff):
+        """One mf_geometry_features call: the pair tensors, the valid-pair mask and (scale None: the
+        non-periodic rms radius, computed in the same call) the normaliser."""
         from matterformer_amd import _native
 
         B, N, _ = coords.shape
         dev = coords.device
         c = coords.float().contiguous()
-        pad = None if pad_mask is None else pad_mask.to(torch.uint8).contiguous()
+        # a bool mask is read as its bytes (0 / 1)
+        pad = None if pad_mask is None else pad_mask.to(torch.bool).contiguous()
         delta = torch.empty(B, N, N, 3, device=dev, dtype=torch.float32)
         d2 = torch.empty(B, N, N, device=dev, dtype=torch.float32)
         dist = torch.empty_like(d2)
         dnorm = torch.empty_like(d2)
+        pair_mask = torch.empty(B, N, N, device=dev, dtype=torch.uint8)
         bits = None
         if radius_cutoff is not None:
             bits = torch.empty(B, N, (N + 31) // 32, device=dev, dtype=torch.int32)
         g = None if gram is None else gram.float().contiguous()
-        sc = scale.float().contiguous()
+        rms_mode = scale is None
+        sc = torch.empty(B, device=dev, dtype=torch.float32) if rms_mode else scale.float().contiguous()
         args = _native.MfGeometryArgs(
             coords=c.data_ptr(), gram=_native.ptr(g), scale=sc.data_ptr(), pad_mask=_native.ptr(pad),
             pair_delta=delta.data_ptr(), pair_dist2=d2.data_ptr(), pair_dist=dist.data_ptr(),
             pair_dist_norm=dnorm.data_ptr(), mask_bits=_native.ptr(bits),
             cutoff=float(radius_cutoff) if radius_cutoff is not None else 0.0, batch=B, atoms=N,
-            pbc_radius=int(pbc_radius))
+            pbc_radius=int(pbc_radius), pair_mask=pair_mask.data_ptr(),
+            scale_mode=_native.MF_SCALE_RMS if rms_mode else _native.MF_SCALE_GIVEN)
         with torch.cuda.device(dev):
             _native.check(_native.lib().mf_geometry_features(args, _native.current_stream(dev)),
                           "mf_geometry_features")
-        return delta, dist, d2, dnorm, bits
+        return delta, dist, d2, dnorm, bits, pair_mask.view(torch.bool), sc
 
 
 class NonPeriodicGeometryAdapter(BaseGeometryAdapter):
@@ -116,18 +135,21 @@ class NonPeriodicGeometryAdapter(BaseGeometryAdapter):
         if lattice is not None:
             raise ValueError("lattice must be None for NonPeriodicGeometryAdapter")
         coords = coords.float()
-        valid = self._valid_atom_mask(coords, pad_mask)
-        pair_mask = self._pair_mask_from_valid(valid)
-        sq_norm = coords.square().sum(dim=-1)
-        denom = valid.sum(dim=1).clamp_min(1)
-        rms = torch.sqrt(((sq_norm * valid.to(sq_norm.dtype)).sum(dim=1) / denom).clamp_min(1e-8))
-        extras = {"metric": torch.eye(3, device=coords.device, dtype=coords.dtype).expand(coords.shape[0], -1, -1)}
+        extras = {"metric": _identity_metric(coords.shape[0], coords.device)}
         if coords.device.type == "cuda":
-            delta, dist, d2, dnorm, bits = self._hip_features(coords, pad_mask, rms.clamp_min(1e-8), None, 0,
-                                                              radius_cutoff)
+            if pad_mask is not None and pad_mask.shape != coords.shape[:2]:
+                raise ValueError(f"pad_mask must have shape {tuple(coords.shape[:2])}, got {tuple(pad_mask.shape)}")
+            # one call: rms radius, pair tensors and the valid-pair mask
+            delta, dist, d2, dnorm, bits, pair_mask, rms = self._hip_features(coords, pad_mask, None, None, 0,
+                                                                              radius_cutoff)
             if bits is not None:
                 extras["radius_mask_bits"] = bits
         else:
+            valid = self._valid_atom_mask(coords, pad_mask)
+            pair_mask = self._pair_mask_from_valid(valid)
+            sq_norm = coords.square().sum(dim=-1)
+            denom = valid.sum(dim=1).clamp_min(1)
+            rms = torch.sqrt(((sq_norm * valid.to(sq_norm.dtype)).sum(dim=1) / denom).clamp_min(1e-8))
             delta = coords[:, :, None, :] - coords[:, None, :, :]
             d2 = delta.square().sum(dim=-1).clamp_min(0.0)
             dist = torch.sqrt(d2)
@@ -164,18 +186,20 @@ class PeriodicGeometryAdapter(BaseGeometryAdapter):
             raise ValueError(f"lattice batch {lattice.shape[0]} does not match coords batch {coords.shape[0]}")
         coords = coords.float()
         lattice = lattice.float()
-        valid = self._valid_atom_mask(coords, pad_mask)
-        pair_mask = self._pair_mask_from_valid(valid)
         y1 = lattice_latent_to_y1(lattice, self.lattice_repr)
         gram = lattice_to_gram(lattice, self.lattice_repr)
         cell_scale = torch.exp(y1[:, :3]).mean(dim=-1).clamp_min(1e-8)
         extras = {"metric": gram, "cell_scale": cell_scale[:, None]}
         if coords.device.type == "cuda":
-            delta, dist, d2, dnorm, bits = self._hip_features(coords, pad_mask, cell_scale, gram, self.pbc_radius,
-                                                              radius_cutoff)
+            if pad_mask is not None and pad_mask.shape != coords.shape[:2]:
+                raise ValueError(f"pad_mask must have shape {tuple(coords.shape[:2])}, got {tuple(pad_mask.shape)}")
+            delta, dist, d2, dnorm, bits, pair_mask, _ = self._hip_features(coords, pad_mask, cell_scale, gram,
+                                                                            self.pbc_radius, radius_cutoff)
             if bits is not None:
                 extras["radius_mask_bits"] = bits
         else:
+            valid = self._valid_atom_mask(coords, pad_mask)
+            pair_mask = self._pair_mask_from_valid(valid)
             delta0 = coords[:, :, None, :] - coords[:, None, :, :]
             images = delta0[:, :, :, None, :] + self._pbc_offsets.to(coords.device, coords.dtype)
             d2_images = torch.einsum("bnmki,bij,bnmkj->bnmk", images, gram, images)
