@@ -609,9 +609,10 @@ def measure_simplicial_extras(lib, w, wd) -> dict:
         "molecules_per_s": round(B / ((train_ms + bwd_ms) * 1e-3), 1),
         "valid_gflop": round(4 * fwd_flops / 1e9, 3),
         "bwd_roofline": {"bound": "mfma", "achieved": round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 3),
-                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 5),
-                         "kernel": "mf::sbwd::simplicial_bwd_kernel<64> (fp32 MFMA, deterministic)",
+                         "peak": BF16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 5),
+                         "kernel": "mf::sbwd::simplicial_bwd_kernel<64, role, bf16 MFMA> x 3 roles "
+                                   "(deterministic, no atomics)",
                          "kernel_ms": round(bwd_ms, 5), "note": "eager call incl. zero-fills and casts"},
     }
 

@@ -83,6 +83,19 @@ __device__ __forceinline__ float group16_sum(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ds_read_b64_tr_b16 (gfx950): four 16-bit elements, transposed within each
+// group of 16 lanes: lane 4a + c receives element c of the 8-byte pieces
+// addressed by lanes 4e + a of its group, e = 0..3 in order.  p must be
+// 8-byte aligned LDS.
+template <typename T>
+__device__ __forceinline__ auto read_tr16(const T* p) {
+  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T Op4;
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4*)(reinterpret_cast<uintptr_t>(p)));
+  return __builtin_bit_cast(Op4, v);
+}
+
 // Element traits: 16-bit types use the K=32 MFMA (8 K-elements per lane),
 // fp32 uses the K=4 MFMA (1 K-element per lane).  Both produce the same
 // 16x16 fp32 accumulator layout: lane l holds C[4*(l>>4)+r][l&15], r=0..3.

@@ -327,18 +327,6 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
 // ---------------------------------------------------------------------------
 constexpr int kThreads2 = 512;
 
-// ds_read_b64_tr_b16 (gfx950): four 16-bit elements, transposed across each
-// group of 16 lanes (see the V^T operand read below).  p must be 8-byte
-// aligned LDS.
-template <typename T>
-__device__ __forceinline__ auto read_tr16(const T* p) {
-  typedef __attribute__((__vector_size__(4 * sizeof(T)))) T Op4;
-  typedef short s4 __attribute__((ext_vector_type(4)));
-  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s4*)(reinterpret_cast<uintptr_t>(p)));
-  return __builtin_bit_cast(Op4, v);
-}
-
 // POS: scale > 0.  The running maximum is then taken over the unscaled
 // masked logits (scaling preserves the order) and p = exp2(s scale - m) is
 // one fma per logit.

@@ -21,12 +21,16 @@
 //   J    j       i      k       K2 . (k1_j (.) Q[i])       V2 . (v1_j (.) GO[i])    dS: Q (.) K2 -> dk1_j, P: GO (.) V2 -> dv1_j
 //   K    k       i      j       K1 . (k2_k (.) Q[i])       V1 . (v2_k (.) GO[i])    dS: Q (.) K1 -> dk2_k, P: GO (.) V1 -> dv2_k
 //
-// One workgroup per (b, h, block of outer indices, role); each wave owns one
-// outer index for the whole launch, so every gradient element is written by
-// one wave after sums in a fixed order: no atomics, bitwise reproducible.
+// One launch per role, OB workgroups per (b, h); workgroup ob takes the outer indices
+// (it OB + ob) kWaves + wave, one per wave and iteration it, so every
+// gradient element is written by one wave after sums in a fixed order: no
+// atomics, bitwise reproducible.  OB is sized on the host to fill the device
+// (no workgroup lands wholly past the valid atoms of small molecules); the
+// key columns, staged per 64-column block, stay in LDS across iterations when
+// a molecule has at most 64 valid keys.
 //
-// Per wave: for each 64-column block (keys, staged fp32 in LDS as C_S and
-// C_P, shared by the waves) and each 16-row tile (rows read from L2, 4
+// Per wave: for each 64-column block (keys, staged in LDS as C_S and C_P,
+// shared by the waves) and each 16-row tile (rows read from L2, 4
 // consecutive d per lane):
 //   GEMM1   S^T[c][r]  = sum_d C_S[c][d] (oS (.) R_S[r])[d]   fp32 MFMA 16x16x4
 //   GEMM1'  dP^T[c][r] = sum_d C_P[c][d] (oP (.) R_P[r])[d]
@@ -34,10 +38,27 @@
 //   GEMM2   C2a[d][r] += sum_c C_S[c][d] dS[r][c]  (and C2b with C_P and P)
 //   out_o[d] += R[r][d] C2[d][r]   (fp32, the row values already in registers)
 // The accumulator layout of GEMM1 (lane = row r, 4 consecutive columns per
-// lane group) is the B-operand layout GEMM2 needs, as in the forward.  The
-// K index of the fp32 MFMA is mapped to d = 16 t + 4 g + e so that each lane
-// reads 4 consecutive d of a row (one 16-byte load) for 4 MFMA steps.
-// 16-bit inputs are widened to fp32 on load; all products and sums are fp32.
+// lane group) is the B-operand layout GEMM2 needs, as in the forward.
+//
+// Two arithmetic paths share everything but the two GEMMs:
+//   fp32 inputs: fp32 MFMA 16x16x4, all products and sums fp32.  The K index
+//     is mapped to d = 16 t + 4 g + e so that each lane reads 4 consecutive
+//     d of a row (one 16-byte load) for 4 MFMA steps.
+//   bf16 inputs: bf16 MFMA 16x16x32 with fp32 accumulation, at the
+//     reference backward's precision (triton_simplicial_attention.py:546-551
+//     rounds only the score products q (.) k to the input type; its dP and
+//     dS / P contractions, :611-645, are fp32).  Columns and rows are staged
+//     as bf16 (exact).  The GEMM1 B operand is the fp32 product oS (.) R
+//     rounded to bf16 for S, and carried as bf16 hi + lo (x = hi + lo to
+//     about 16 bits, two MFMAs) for dP; 8 consecutive d = 32 s + 8 g .. +7
+//     per lane.  GEMM2 takes dS and P, again as hi + lo, as its B operand
+//     straight from the GEMM1 accumulators of two column tiles, and
+//     C_S^T / C_P^T as its A operand through transposed LDS reads
+//     (ds_read_b64_tr_b16) of the row-major columns.  Softmax, dS and every
+//     sum stay fp32.  Lane (g, r16) holds d = 32 (t >> 1) + 8 g + 4 (t & 1)
+//     + e of tile t: the same d for its GEMM1 operands, its GEMM2 outputs
+//     and its row values.
+//   fp16 inputs take the fp32 path (fp16 columns are not exact in bf16).
 #include <algorithm>
 #include <cmath>
 
@@ -51,13 +72,44 @@ constexpr int kRoleJ = 1;
 constexpr int kRoleK = 2;
 constexpr int kCols = 64;  // staged key columns per block
 
-template <int DP>
+template <int DP, bool M16>
 struct Shape {
-  static constexpr int kWaves = DP >= 128 ? 4 : 8;  // D = 128 needs the whole register file per wave
+  // fp32: D = 128 needs the whole register file per wave.  16-bit: 4 waves
+  // at about 240 VGPRs put two workgroups on each CU, so that one's global
+  // loads overlap the other's arithmetic.
+  static constexpr int kWaves = (M16 || DP >= 128) ? 4 : 8;
+  static constexpr int kMinBlocks = (M16 && DP < 128) ? 2 : 1;  // workgroups per CU the registers must allow
   static constexpr int kThreads = kWaves * 64;
   static constexpr int NT = DP / 16;   // 16-wide d tiles
-  static constexpr int D4 = DP + 4;    // LDS row stride (floats) of the staged columns
+  static constexpr int D4 = DP + 4;    // LDS row stride (floats) of the staged fp32 columns
+  static constexpr int KS = DP + 8;    // LDS row stride (bf16) of the staged 16-bit columns
 };
+
+// First d of the 4 that lane group g holds in d tile t (see the header).
+template <bool M16>
+__device__ __forceinline__ int dof(int t, int g) {
+  return M16 ? 32 * (t >> 1) + 8 * g + 4 * (t & 1) : 16 * t + 4 * g;
+}
+
+__device__ __forceinline__ mf_bf16x8 pack_bf16(const float4& lo, const float4& hi) {
+  mf_bf16x8 r;
+  r[0] = __bf16(lo.x); r[1] = __bf16(lo.y); r[2] = __bf16(lo.z); r[3] = __bf16(lo.w);
+  r[4] = __bf16(hi.x); r[5] = __bf16(hi.y); r[6] = __bf16(hi.z); r[7] = __bf16(hi.w);
+  return r;
+}
+
+__device__ __forceinline__ float4 bf16_lo(const mf_bf16x8& v) {
+  return float4{float(v[0]), float(v[1]), float(v[2]), float(v[3])};
+}
+__device__ __forceinline__ float4 bf16_hi(const mf_bf16x8& v) {
+  return float4{float(v[4]), float(v[5]), float(v[6]), float(v[7])};
+}
+
+__device__ __forceinline__ float4 mul4(const float4& a, const float4& b) {
+  return float4{a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w};
+}
+
+
 
 struct Params {
   const void* q;
@@ -88,19 +140,22 @@ struct Params {
   int B, H, N, D;
   int dtype, gdtype;
   int NP;       // N rounded up to 64: LDS list capacity
-  int OB;       // outer blocks per (b, h): ceil(N / waves)
-  int vec;      // q/k/v/go rows 4-element loads are aligned (D % 4 == 0, aligned bases)
+  int OB;       // workgroups per (b, h, role)
+  int vec;      // q/k/v/go/out rows 4-element loads are aligned (D % 4 == 0, aligned bases)
 };
 
 // LDS layout (bytes), shared by host sizing and device carving.
-template <int DP>
+template <int DP, bool M16>
 struct Lay {
-  static size_t __host__ __device__ cols() { return size_t(2) * kCols * Shape<DP>::D4 * 4; }
+  // staged tiles: fp32 C_S, C_P (64 columns); 16-bit: bf16 C_S, C_P and R_S, R_P (64 rows)
+  static size_t __host__ __device__ cols() {
+    return M16 ? size_t(4) * kCols * Shape<DP, M16>::KS * 2 : size_t(2) * kCols * Shape<DP, M16>::D4 * 4;
+  }
   static size_t __host__ __device__ bytes(int NP, bool has_pv, bool has_bias) {
     size_t s = cols();
-    s += size_t(NP) * 4 * 3;                                  // kidx, qidx, delta
+    s += size_t(NP) * 4 * 4;                                  // kidx, qidx, delta, lse2
     if (has_pv) s += size_t(NP) * 2 * 4;                      // 64 column bits per row
-    if (has_bias) s += size_t(Shape<DP>::kWaves) * (NP + kCols) * 4;  // per-wave row / column sums
+    if (has_bias) s += size_t(Shape<DP, M16>::kWaves) * (NP + kCols) * 4;  // per-wave row / column sums
     s += 16;                                                  // counts
     return s;
   }
@@ -155,25 +210,31 @@ __device__ __forceinline__ int compact(const uint8_t* m, int N, int* dst, int la
   return count;
 }
 
-template <int DP, int ROLE>
+template <int DP, int ROLE, bool M16, bool BIAS>
 __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, int bh, int ob) {
-  using S = Shape<DP>;
+  using S = Shape<DP, M16>;
   constexpr int kWaves = S::kWaves;
   constexpr int kThreads = S::kThreads;
   constexpr int NT = S::NT;
   constexpr int D4 = S::D4;
+  constexpr int KS = S::KS;
   const int N = p.N, D = p.D, NP = p.NP;
   const int b = bh / p.H;
   const bool has_pv = p.pv != nullptr;
-  const bool has_bias = p.u != nullptr;
+  constexpr bool has_bias = BIAS;
   const bool vec = p.vec != 0;
 
-  float* CS = reinterpret_cast<float*>(smem);
+  float* CS = reinterpret_cast<float*>(smem);  // fp32 columns (fp32 path)
   float* CP = CS + kCols * D4;
-  int* kidx = reinterpret_cast<int*>(CP + kCols * D4);
+  __bf16* CS16 = reinterpret_cast<__bf16*>(smem);  // bf16 columns and rows (16-bit path)
+  __bf16* CP16 = CS16 + kCols * KS;
+  __bf16* RS16 = CP16 + kCols * KS;
+  __bf16* RP16 = RS16 + kCols * KS;
+  int* kidx = reinterpret_cast<int*>(smem + Lay<DP, M16>::cols());
   int* qidx = kidx + NP;
-  float* delta = reinterpret_cast<float*>(qidx + NP);
-  uint32_t* pvb = reinterpret_cast<uint32_t*>(delta + NP);
+  float* delta = reinterpret_cast<float*>(qidx + NP);  // go . out of each valid query (roles J, K)
+  float* lse2q = delta + NP;                           // lse log2 e of each valid query (roles J, K)
+  uint32_t* pvb = reinterpret_cast<uint32_t*>(lse2q + NP);
   float* wrow = reinterpret_cast<float*>(pvb + (has_pv ? 2 * NP : 0));
   float* wcol = wrow + (has_bias ? kWaves * NP : 0);
   int* counts = reinterpret_cast<int*>(wcol + (has_bias ? kWaves * kCols : 0));
@@ -211,31 +272,51 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
   const void* t_cp = ROLE == kRoleK ? p.v1 : p.v2;   // columns, dP side
   const size_t rbase = size_t(bh) * N;               // first row of (b, h)
 
-  // ---- delta_i = go_i . out_i of every valid query (rows of roles J / K) ----
+  // ---- delta_i = go_i . out_i and lse_i log2 e of every valid query (rows of roles J / K) ----
+  // CH consecutive lanes share a query, 8 d each, summed in a fixed order.
   if constexpr (ROLE != kRoleQ) {
-    for (int r = wave; r < nq; r += kWaves) {
-      const size_t row = rbase + qidx[r];
+    constexpr int CH = DP / 8;
+    for (int u0 = 0; u0 < nq * CH; u0 += kThreads) {
+      const int u = u0 + tid;
+      const int r = u / CH;
+      const int d0 = (u - r * CH) * 8;
+      const bool ok = u < nq * CH;
       float s = 0.0f;
-      for (int d = lane; d < D; d += 64) s += ld1(p.go, row * D + d, p.gdtype) * p.out[row * D + d];
-      s = wave_sum(s);
-      if (lane == 0) delta[r] = s;
+      if (ok) {
+        const size_t row = rbase + qidx[r];
+        const float4 g0 = ld4(p.go, row, d0, D, p.gdtype, vec), g1 = ld4(p.go, row, d0 + 4, D, p.gdtype, vec);
+        const float4 o0 = ld4(p.out, row, d0, D, MF_DTYPE_F32, vec);
+        const float4 o1 = ld4(p.out, row, d0 + 4, D, MF_DTYPE_F32, vec);
+        s = g0.x * o0.x;
+        s = fmaf(g0.y, o0.y, s); s = fmaf(g0.z, o0.z, s); s = fmaf(g0.w, o0.w, s);
+        s = fmaf(g1.x, o1.x, s); s = fmaf(g1.y, o1.y, s); s = fmaf(g1.z, o1.z, s); s = fmaf(g1.w, o1.w, s);
+      }
+#pragma unroll
+      for (int off = 1; off < CH; off <<= 1) s += __shfl_xor(s, off, 64);
+      if (ok && d0 == 0) {
+        delta[r] = s;
+        lse2q[r] = p.lse[rbase + qidx[r]] * kLog2e;
+      }
     }
   }
 
-  // ---- this wave's outer index ----
-  const int ol = ob * kWaves + wave;
+  // ---- the workgroup's outer indices: (it * OB + ob) * kWaves + wave, it = 0 .. n_it - 1 ----
+  // With one column block (nk <= kCols) the block is staged once for all iterations.
+  const int n_it = (n_outer - ob * kWaves + kWaves * p.OB - 1) / (kWaves * p.OB);
+  for (int it = 0; it < n_it; ++it) {
+  const int ol = (it * p.OB + ob) * kWaves + wave;
   const bool active = ol < n_outer;
   const int oo = active ? outer_list[ol] : 0;
   const size_t orow = rbase + oo;
-  float4 oS[NT], oP[NT];  // outer vectors at d = 16 t + 4 g + e (oS carries log2 e)
+  float4 oS[NT], oP[NT];  // outer vectors at d = dof(t, g) + e (oS carries log2 e)
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     oS[t] = float4{0.f, 0.f, 0.f, 0.f};
     oP[t] = float4{0.f, 0.f, 0.f, 0.f};
     if (active) {
-      const float4 a = ld4(t_os, orow, 16 * t + 4 * g, D, p.dtype, vec);
+      const float4 a = ld4(t_os, orow, dof<M16>(t, g), D, p.dtype, vec);
       oS[t] = float4{a.x * kLog2e, a.y * kLog2e, a.z * kLog2e, a.w * kLog2e};
-      oP[t] = ld4(t_op, orow, 16 * t + 4 * g, D, dt_op, vec);
+      oP[t] = ld4(t_op, orow, dof<M16>(t, g), D, dt_op, vec);
     }
   }
   float lse2_o = 0.0f, delta_o = 0.0f, gate_o = 0.0f;
@@ -259,24 +340,49 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
     }
   float gacc = 0.0f;  // role Q: dgate partial
 
-  const int n_rt = (n_rows + 15) / 16;
-  for (int cb0 = 0; cb0 < nk; cb0 += kCols) {
-    __syncthreads();  // the previous block's LDS reads are done
-    // stage the column block (fp32, zero past nk and past D)
-    constexpr int CPR = DP / 4;  // float4 chunks per row
-    for (int u = tid; u < kCols * CPR; u += kThreads) {
-      const int c = u / CPR;
-      const int d0 = (u - c * CPR) * 4;
-      float4 a = float4{0.f, 0.f, 0.f, 0.f}, bb = a;
-      if (cb0 + c < nk) {
-        const size_t row = rbase + kidx[cb0 + c];
-        a = ld4(t_cs, row, d0, D, p.dtype, vec);
-        bb = ld4(t_cp, row, d0, D, p.dtype, vec);
+  const int ncb = (nk + kCols - 1) / kCols;
+  const int nrb = M16 ? (n_rows + kCols - 1) / kCols : 1;  // 16-bit: rows staged in 64-row blocks
+  for (int cbi = 0; cbi < ncb; ++cbi) {
+  const int cb0 = cbi * kCols;
+  const int ncols = min(kCols, nk - cb0);
+  for (int rbi = 0; rbi < nrb; ++rbi) {
+    const int rb0 = rbi * kCols;
+    const bool stage = rbi == 0 && (it == 0 || ncb > 1);             // the column block
+    const bool stage_r = M16 && (nrb > 1 || (it == 0 && cbi == 0));  // the row block
+    if (stage || stage_r) __syncthreads();  // the previous contents' LDS reads are done
+    // stage the column block (fp32 or bf16, zero past nk and past D)
+    if (!stage) {
+    } else if constexpr (M16) {
+      constexpr int CPR = DP / 8;  // 8-element chunks per row
+      for (int u = tid; u < kCols * CPR; u += kThreads) {
+        const int c = u / CPR;
+        const int d0 = (u - c * CPR) * 8;
+        const float4 z = float4{0.f, 0.f, 0.f, 0.f};
+        mf_bf16x8 a = pack_bf16(z, z), bb = a;
+        if (cb0 + c < nk) {
+          const size_t row = rbase + kidx[cb0 + c];
+          a = pack_bf16(ld4(t_cs, row, d0, D, p.dtype, vec), ld4(t_cs, row, d0 + 4, D, p.dtype, vec));
+          bb = pack_bf16(ld4(t_cp, row, d0, D, p.dtype, vec), ld4(t_cp, row, d0 + 4, D, p.dtype, vec));
+        }
+        *reinterpret_cast<mf_bf16x8*>(CS16 + c * KS + d0) = a;
+        *reinterpret_cast<mf_bf16x8*>(CP16 + c * KS + d0) = bb;
       }
-      *reinterpret_cast<float4*>(CS + c * D4 + d0) = a;
-      *reinterpret_cast<float4*>(CP + c * D4 + d0) = bb;
+    } else {
+      constexpr int CPR = DP / 4;  // float4 chunks per row
+      for (int u = tid; u < kCols * CPR; u += kThreads) {
+        const int c = u / CPR;
+        const int d0 = (u - c * CPR) * 4;
+        float4 a = float4{0.f, 0.f, 0.f, 0.f}, bb = a;
+        if (cb0 + c < nk) {
+          const size_t row = rbase + kidx[cb0 + c];
+          a = ld4(t_cs, row, d0, D, p.dtype, vec);
+          bb = ld4(t_cp, row, d0, D, p.dtype, vec);
+        }
+        *reinterpret_cast<float4*>(CS + c * D4 + d0) = a;
+        *reinterpret_cast<float4*>(CP + c * D4 + d0) = bb;
+      }
     }
-    if (has_pv) {
+    if (stage && has_pv) {
       // bits of the block's 64 columns for every compacted key x:
       //   roles Q, J: pair_valid[x][column]; role K: pair_valid[column][x]
       const uint8_t* pvm = p.pv + size_t(b) * N * N;
@@ -294,16 +400,35 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
         pvb[2 * x + wd] = bits;
       }
     }
-    if (has_bias) {
+    if constexpr (M16) {
+      // stage the row block (bf16, zero past n_rows and past D)
+      if (stage_r) {
+        constexpr int CPR = DP / 8;
+        for (int u = tid; u < kCols * CPR; u += kThreads) {
+          const int c = u / CPR;
+          const int d0 = (u - c * CPR) * 8;
+          const float4 z = float4{0.f, 0.f, 0.f, 0.f};
+          mf_bf16x8 a = pack_bf16(z, z), bb = a;
+          if (rb0 + c < n_rows) {
+            const size_t row = rbase + row_list[rb0 + c];
+            a = pack_bf16(ld4(t_rs, row, d0, D, p.dtype, vec), ld4(t_rs, row, d0 + 4, D, p.dtype, vec));
+            bb = pack_bf16(ld4(t_rp, row, d0, D, dt_rp, vec), ld4(t_rp, row, d0 + 4, D, dt_rp, vec));
+          }
+          *reinterpret_cast<mf_bf16x8*>(RS16 + c * KS + d0) = a;
+          *reinterpret_cast<mf_bf16x8*>(RP16 + c * KS + d0) = bb;
+        }
+      }
+    }
+    // per-wave bias sums (only this wave touches them: no barrier needed)
+    if (has_bias && rbi == 0) {
       for (int u = lane; u < kCols; u += 64) wcol[wave * kCols + u] = 0.0f;
-      if (cb0 == 0)
+      if (cbi == 0)
         for (int u = lane; u < NP; u += 64) wrow[wave * NP + u] = 0.0f;
     }
-    __syncthreads();
+    if (stage || stage_r) __syncthreads();
     if (!active) continue;
 
     // column-tile validity of this block
-    const int ncols = min(kCols, nk - cb0);
     const int nkt = (ncols + 15) / 16;
     uint32_t pv_outer[2] = {0xffffffffu, 0xffffffffu};
     if constexpr (ROLE != kRoleQ) {
@@ -314,21 +439,36 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
     }
     const float gq_o = gate_o * kLog2e;
 
+    const int n_rt = M16 ? (min(kCols, n_rows - rb0) + 15) / 16 : (n_rows + 15) / 16;
     for (int rt = 0; rt < n_rt; ++rt) {
-      const int row = rt * 16 + r16;
+      const int row = rb0 + rt * 16 + r16;  // compacted row index
       const bool row_ok = row < n_rows;
       const size_t rrow = rbase + (row_ok ? row_list[row] : 0);
       const int ro = row_ok ? row_list[row] : 0;
-      float4 rs[NT], rp[NT];  // raw row values at d = 16 t + 4 g + e
+      float4 rs[NT], rp[NT];  // row values at d = dof(t, g) + e
+      if constexpr (M16) {
+        const __bf16* rsp = RS16 + (rt * 16 + r16) * KS + 8 * g;
+        const __bf16* rpp = RP16 + (rt * 16 + r16) * KS + 8 * g;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        rs[t] = row_ok ? ld4(t_rs, rrow, 16 * t + 4 * g, D, p.dtype, vec) : float4{0.f, 0.f, 0.f, 0.f};
-        rp[t] = row_ok ? ld4(t_rp, rrow, 16 * t + 4 * g, D, dt_rp, vec) : float4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < NT / 2; ++s) {
+          const mf_bf16x8 a = *reinterpret_cast<const mf_bf16x8*>(rsp + 32 * s);
+          const mf_bf16x8 bb = *reinterpret_cast<const mf_bf16x8*>(rpp + 32 * s);
+          rs[2 * s] = bf16_lo(a);
+          rs[2 * s + 1] = bf16_hi(a);
+          rp[2 * s] = bf16_lo(bb);
+          rp[2 * s + 1] = bf16_hi(bb);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          rs[t] = row_ok ? ld4(t_rs, rrow, dof<M16>(t, g), D, p.dtype, vec) : float4{0.f, 0.f, 0.f, 0.f};
+          rp[t] = row_ok ? ld4(t_rp, rrow, dof<M16>(t, g), D, dt_rp, vec) : float4{0.f, 0.f, 0.f, 0.f};
+        }
       }
       // per-row softmax state: the query's lse (log2) and delta
       float lse2_r = lse2_o, delta_r = delta_o, gate_r = gate_o, gq_r = gq_o;
       if constexpr (ROLE != kRoleQ) {
-        lse2_r = row_ok ? p.lse[rrow] * kLog2e : 0.0f;
+        lse2_r = row_ok ? lse2q[row] : 0.0f;
         delta_r = row_ok ? delta[row] : 0.0f;
         if (has_bias) {
           gate_r = row_ok ? ld1(p.gate, rrow, p.bias_dtype) : 0.0f;
@@ -352,6 +492,32 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
 
       // GEMM1 (S^T) and GEMM1' (dP^T): lane holds row r16 and columns 16 kt + 4 g + r
       mf_f32x4 sv[4], dv[4];
+      if constexpr (M16) {
+        // B operands: row r16, d = 32 s + 8 g .. +7, products rounded to bf16
+        constexpr int NS = DP / 32;
+        mf_bf16x8 bs[NS], bp[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          bs[s] = pack_bf16(mul4(rs[2 * s], oS[2 * s]), mul4(rs[2 * s + 1], oS[2 * s + 1]));
+          bp[s] = pack_bf16(mul4(rp[2 * s], oP[2 * s]), mul4(rp[2 * s + 1], oP[2 * s + 1]));
+        }
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          sv[kt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+          dv[kt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+          if (kt < nkt) {
+            const __bf16* cs = CS16 + (kt * 16 + r16) * KS + 8 * g;
+            const __bf16* cp = CP16 + (kt * 16 + r16) * KS + 8 * g;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+              const mf_bf16x8 as = *reinterpret_cast<const mf_bf16x8*>(cs + 32 * s);
+              const mf_bf16x8 ap = *reinterpret_cast<const mf_bf16x8*>(cp + 32 * s);
+              sv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as, bs[s], sv[kt], 0, 0, 0);
+              dv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap, bp[s], dv[kt], 0, 0, 0);
+            }
+          }
+        }
+      } else {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         sv[kt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -370,6 +536,7 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
             }
           }
         }
+      }
       }
 
       // P, dS (sv <- dS, dv <- P) and the bias sums
@@ -433,6 +600,49 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
       }
 
       // GEMM2: C2a[d][r] = sum_c C_S[c][d] dS[r][c];  C2b[d][r] = sum_c C_P[c][d] P[r][c] (roles J, K)
+      if constexpr (M16) {
+        // K step pr covers columns 32 pr .. +31; k slot 8 g + j is column
+        // 32 pr + 4 g + j (j < 4, tile 2 pr) or 32 pr + 16 + 4 g + j - 4
+        // (tile 2 pr + 1): the columns this lane holds in sv / dv.  The A
+        // operand rows of lane (g, r16) are d = dof(t, r16 >> 2) + (r16 & 3):
+        // lane 4 e + a of group g addresses column 32 pr + 4 g + e (+16),
+        // d = 32 s + 8 a + 4 h .. +3, and read_tr16 hands lane 4 a + c the
+        // four columns' element c.
+        mf_bf16x8 ps[2], pp[2];
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          ps[pr] = pack_bf16(float4{sv[2 * pr][0], sv[2 * pr][1], sv[2 * pr][2], sv[2 * pr][3]},
+                             float4{sv[2 * pr + 1][0], sv[2 * pr + 1][1], sv[2 * pr + 1][2], sv[2 * pr + 1][3]});
+          pp[pr] = pack_bf16(float4{dv[2 * pr][0], dv[2 * pr][1], dv[2 * pr][2], dv[2 * pr][3]},
+                             float4{dv[2 * pr + 1][0], dv[2 * pr + 1][1], dv[2 * pr + 1][2], dv[2 * pr + 1][3]});
+        }
+        const int tr_off = (4 * g + (r16 >> 2)) * KS + 8 * (r16 & 3);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int toff = tr_off + 32 * (t >> 1) + 4 * (t & 1);
+          mf_f32x4 ca = mf_f32x4{0.f, 0.f, 0.f, 0.f}, cb = ca;
+#pragma unroll
+          for (int pr = 0; pr < 2; ++pr) {
+            if (2 * pr >= nkt) continue;
+            const __bf16* pa = CS16 + toff + 32 * pr * KS;
+            const mf_bf16x8 aa = __builtin_shufflevector(read_tr16(pa), read_tr16(pa + 16 * KS), 0, 1, 2, 3, 4, 5, 6, 7);
+            ca = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aa, ps[pr], ca, 0, 0, 0);
+            if constexpr (ROLE != kRoleQ) {
+              const __bf16* pb = CP16 + toff + 32 * pr * KS;
+              const mf_bf16x8 ab =
+                  __builtin_shufflevector(read_tr16(pb), read_tr16(pb + 16 * KS), 0, 1, 2, 3, 4, 5, 6, 7);
+              cb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, pp[pr], cb, 0, 0, 0);
+            }
+          }
+          // out_o[d] += R[r][d] C2[d][r]: ca[r] is d = dof(t, g) + r of row r16, as is rs[t]
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc_a[t][r] = fmaf(f4(rs[t], r), ca[r], acc_a[t][r]);
+            if constexpr (ROLE != kRoleQ) acc_b[t][r] = fmaf(f4(rp[t], r), cb[r], acc_b[t][r]);
+          }
+        }
+        continue;
+      }
       mf_f32x4 c2a[NT], c2b[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -465,9 +675,10 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
       }
     }
 
+  }  // rbi
     // column sums of this block are complete: dv_bias (role Q) and dw (role J)
     if constexpr (ROLE != kRoleK) {
-      if (has_bias) {
+      if (has_bias && active) {
         for (int c = lane; c < ncols; c += 64) {
           const size_t dst = orow * N + kidx[cb0 + c];
           if constexpr (ROLE == kRoleQ) {
@@ -479,7 +690,7 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
       }
     }
   }
-  if (!active) return;
+  if (!active) continue;  // uniform over the wave
 
   // ---- write the outer index's rows: sum over the 16 row lanes of each group ----
 #pragma unroll
@@ -491,11 +702,11 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
     }
   float* out_a = ROLE == kRoleQ ? p.dq : (ROLE == kRoleJ ? p.dk1 : p.dk2);
   float* out_b = ROLE == kRoleQ ? nullptr : (ROLE == kRoleJ ? p.dv1 : p.dv2);
-  // lane (g, r16) writes d = 16 t + 4 g + (r16 & 3) for the tiles t with (t & 3) == r16 >> 2
+  // lane (g, r16) writes d = dof(t, g) + (r16 & 3) for the tiles t with (t & 3) == r16 >> 2
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if ((t & 3) != (r16 >> 2)) continue;
-    const int d = 16 * t + 4 * g + (r16 & 3);
+    const int d = dof<M16>(t, g) + (r16 & 3);
     if (d >= D) continue;
     float va = 0.0f, vb = 0.0f;
 #pragma unroll
@@ -515,21 +726,21 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
         for (int row = lane; row < nk; row += 64) p.du[orow * N + kidx[row]] = gate_o * wrow[wave * NP + row];
     }
   }
+  }  // it
 }
 
-template <int DP>
-__global__ void __launch_bounds__(Shape<DP>::kThreads) simplicial_bwd_kernel(Params p) {
+// One kernel per role: each gets its own register allocation.
+template <int DP, int ROLE, bool M16, bool BIAS>
+__global__ void __launch_bounds__((Shape<DP, M16>::kThreads), (Shape<DP, M16>::kMinBlocks)) simplicial_bwd_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int bh = blockIdx.x / p.OB;
   const int ob = blockIdx.x - bh * p.OB;
-  if (blockIdx.y == kRoleQ) run_role<DP, kRoleQ>(p, smem, bh, ob);
-  else if (blockIdx.y == kRoleJ) run_role<DP, kRoleJ>(p, smem, bh, ob);
-  else run_role<DP, kRoleK>(p, smem, bh, ob);
+  run_role<DP, ROLE, M16, BIAS>(p, smem, bh, ob);
 }
 
-template <int DP>
+template <int DP, bool M16>
 int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
-  const size_t lds = Lay<DP>::bytes(prm.NP, has_pv, has_bias);
+  const size_t lds = Lay<DP, M16>::bytes(prm.NP, has_pv, has_bias);
   DeviceInfo dev;
   int st = device_info(&dev);
   if (st != MF_OK) return st;
@@ -537,18 +748,29 @@ int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
     return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: tokens=" + std::to_string(prm.N) + " needs " +
                                         std::to_string(lds) + " bytes of LDS per workgroup, the device offers " +
                                         std::to_string(dev.max_lds_per_block));
-  auto kern = simplicial_bwd_kernel<DP>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_set = true;
+  using Kern = void (*)(Params);
+  const Kern kerns[2][3] = {
+      {simplicial_bwd_kernel<DP, kRoleQ, M16, false>, simplicial_bwd_kernel<DP, kRoleJ, M16, false>,
+       simplicial_bwd_kernel<DP, kRoleK, M16, false>},
+      {simplicial_bwd_kernel<DP, kRoleQ, M16, true>, simplicial_bwd_kernel<DP, kRoleJ, M16, true>,
+       simplicial_bwd_kernel<DP, kRoleK, M16, true>}};
+  static bool attr_set[2] = {false, false};
+  if (!attr_set[has_bias]) {
+    for (Kern k : kerns[has_bias])
+      MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set[has_bias] = true;
   }
-  prm.OB = (prm.N + Shape<DP>::kWaves - 1) / Shape<DP>::kWaves;
-  const long long blocks = (long long)prm.B * prm.H * prm.OB;
+  // about 8 workgroups per CU in each role's launch, at most one per kWaves outer indices
+  const long long bh = (long long)prm.B * prm.H;
+  const long long want = (8LL * dev.num_cus + bh - 1) / bh;
+  prm.OB = int(std::max(1LL, std::min<long long>(want, (prm.N + Shape<DP, M16>::kWaves - 1) / Shape<DP, M16>::kWaves)));
+  const long long blocks = bh * prm.OB;
   if (blocks > 0x7fffffffLL) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: grid too large");
-  hipLaunchKernelGGL(kern, dim3(unsigned(blocks), 3), dim3(Shape<DP>::kThreads), lds, stream, prm);
-  MF_HIP_CHECK(hipGetLastError());
+  for (Kern k : kerns[has_bias]) {
+    hipLaunchKernelGGL(k, dim3(unsigned(blocks)), dim3(Shape<DP, M16>::kThreads), lds, stream, prm);
+    MF_HIP_CHECK(hipGetLastError());
+  }
   return MF_OK;
 }
 
@@ -599,12 +821,18 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   for (const void* ptr : {a->q, a->k1, a->v1, a->k2, a->v2})
     vec = vec && reinterpret_cast<uintptr_t>(ptr) % esz == 0;
   vec = vec && reinterpret_cast<uintptr_t>(a->grad_out) % (a->grad_dtype == MF_DTYPE_F32 ? 16 : 8) == 0;
+  vec = vec && reinterpret_cast<uintptr_t>(a->out) % 16 == 0;
   prm.vec = vec ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool has_pv = a->pair_valid != nullptr;
   const int D = a->head_dim;
-  if (D <= 16) return launch<16>(prm, has_pv, has_bias, s);
-  if (D <= 32) return launch<32>(prm, has_pv, has_bias, s);
-  if (D <= 64) return launch<64>(prm, has_pv, has_bias, s);
-  return launch<128>(prm, has_pv, has_bias, s);
+  if (a->dtype == MF_DTYPE_BF16) {  // bf16 inputs: bf16 MFMA (K steps of 32 d); fp16 takes the fp32 path
+    if (D <= 32) return launch<32, true>(prm, has_pv, has_bias, s);
+    if (D <= 64) return launch<64, true>(prm, has_pv, has_bias, s);
+    return launch<128, true>(prm, has_pv, has_bias, s);
+  }
+  if (D <= 16) return launch<16, false>(prm, has_pv, has_bias, s);
+  if (D <= 32) return launch<32, false>(prm, has_pv, has_bias, s);
+  if (D <= 64) return launch<64, false>(prm, has_pv, has_bias, s);
+  return launch<128, false>(prm, has_pv, has_bias, s);
 }

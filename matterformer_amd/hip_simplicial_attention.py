@@ -292,9 +292,11 @@ def hip_simplicial_attention_backward(
 ):
     """Returns the 15-tuple of triton_simplicial_attention.py:963-979 (None for grads not needed or absent).
 
-    Without low-rank angle / message terms the gradients come from one launch
-    of the deterministic HIP kernel ``mf_simplicial_bwd`` (fp32 arithmetic,
-    bitwise reproducible).  Calls with angle or message terms, and shapes
+    Without low-rank angle / message terms the gradients come from the
+    deterministic HIP entry point ``mf_simplicial_bwd`` (bitwise reproducible;
+    bf16 MFMA for bf16 operands, rounding only the score products to bf16 as
+    the reference's backward rounds them to the input type; fp32 MFMA for
+    fp32 and fp16 operands).  Calls with angle or message terms, and shapes
     beyond that kernel's LDS capacity (the library reports them), recompute
     the forward with the fp32-core torch path on the same device and take its
     autograd gradients -- the reference's own ``debug_torch_backward`` route
