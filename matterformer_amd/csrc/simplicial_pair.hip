@@ -354,36 +354,6 @@ __device__ __forceinline__ int div_small(int i, int d) {
   return int((float(i) + 0.5f) * __builtin_amdgcn_rcpf(float(d)));
 }
 
-// The aligned dword at window offset base + 4 lane of a mask row (0 past the
-// row).  A dword that starts inside [row - off, row + N) stays on the row's
-// pages.
-__device__ __forceinline__ uint32_t load_window(const uint8_t* row, int N, int base, int lane, int& off) {
-  off = int(reinterpret_cast<uintptr_t>(row) & 3u);
-  const uint8_t* astart = row - off;  // pointer arithmetic keeps the global address space
-  const int boff = base + 4 * lane;
-  return boff < off + N ? *reinterpret_cast<const uint32_t*>(astart + boff) : 0u;
-}
-
-// Bytes of a window dword that belong to the row: lane l holds atoms
-// 4 l + e - off (e = 0..3) of window `base`; keep those in [0, N).
-__device__ __forceinline__ uint32_t window_keep(int base, int off, int N, int lane) {
-  const int t0 = base + 4 * lane - off;  // atom of byte 0
-  const int lo = min(max(-t0, 0), 4), hi = min(max(t0 + 4 - N, 0), 4);
-  if (lo + hi >= 4) return 0u;
-  return (0xffffffffu << (8 * lo)) & (0xffffffffu >> (8 * hi));
-}
-
-// Valid (nonzero) bytes of one window added to `count`; the last valid atom
-// so far in `last` (t0 = atom of byte 0 of lane 0).
-__device__ __forceinline__ void scan_window(uint32_t w, int t0, int& count, int& last) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const unsigned long long bal = __ballot(((w >> (8 * e)) & 0xffu) != 0u);
-    count += __popcll(bal);
-    if (bal) last = max(last, t0 + 4 * (63 - __builtin_clzll(bal)) + e);
-  }
-}
-
 // dst[r] = the atom of valid rank r in a mask row (one wave).
 __device__ __forceinline__ void write_ranks(const uint8_t* row, int N, uint16_t* dst, int lane) {
   const unsigned long long below = (1ull << lane) - 1ull;
@@ -748,15 +718,19 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   const int nch = (nk + kCap - 1) / kCap;
   auto key_atom = [&](int rank) { return kpre ? rank : int(kidx[rank]); };
   auto round16 = [](int n) { return (n + 15) & ~15; };
+  // chunk slots that hold a staged row (the rest of the MAXC are skipped by a
+  // scalar branch, not issued under an empty exec mask): all of them for key
+  // blocks, else those of the valid rows rounded up to 16
+  const int nI = MULTI ? MAXC : __builtin_amdgcn_readfirstlane((round16(nk) * CPR + kThreads - 1) / kThreads);
   // rows [row0, row0 + nrows) of the compacted keys; rows up to the next
   // multiple of 16 read as zero
   auto load_set = [&](const T* base, int row0, int nrows, uint4 (&arr)[MAXC]) {
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
       const int row = (tid + kThreads * i) / CPR;
-      arr[i] = (row < nrows && col_ok)
-                   ? *reinterpret_cast<const uint4*>(base + size_t(key_atom(row0 + row)) * D + e0)
-                   : uint4{0u, 0u, 0u, 0u};
+      arr[i] = uint4{0u, 0u, 0u, 0u};
+      if (i < nI && row < nrows && col_ok)
+        arr[i] = *reinterpret_cast<const uint4*>(base + size_t(key_atom(row0 + row)) * D + e0);
     }
   };
   uint4 rk1[MAXC], rk2[MAXC], rv1[MAXC], rv2[MAXC], rq[MAXQC];
@@ -779,6 +753,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   auto acc_max = [&]() {
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
+      if (i >= nI) break;
       const uint32_t a1[4] = {rk1[i].x, rk1[i].y, rk1[i].z, rk1[i].w};
       const uint32_t a2[4] = {rk2[i].x, rk2[i].y, rk2[i].z, rk2[i].w};
 #pragma unroll
@@ -1053,6 +1028,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       // the rows loaded in phase A
 #pragma unroll
       for (int i = 0; i < MAXC; ++i) {
+        if (i >= nI) break;
         const int row = (tid + kThreads * i) / CPR;
         if (row < rj) {
           store_k(K1s, rk1[i], row, s1);
@@ -1252,106 +1228,80 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 // ---------------------------------------------------------------------------
 // schedule: every workgroup derives the same unit list from the masks
 // ---------------------------------------------------------------------------
-// 16-byte chunks of the global byte range [src, src + nbytes) into LDS at
-// dst, starting from the chunk that holds src (returns src's offset in it).
-// A 16-byte aligned chunk that starts inside the range stays on the range's
-// pages.
-__device__ __forceinline__ int copy_bytes_to_lds(const uint8_t* src, int nbytes, unsigned char* dst, int wave,
-                                                 int lane) {
-  const int off = int(reinterpret_cast<uintptr_t>(src) & 15u);
-  const uint8_t* a0 = src - off;
-  const int nchunks = (off + nbytes + 15) >> 4;
-  for (int c0 = wave * 64; c0 < nchunks; c0 += kWaves * 64) {
-    if (c0 + lane < nchunks)
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(a0 + 16 * (c0 + lane)),
-                                       (__attribute__((address_space(3))) void*)(dst + 16 * c0), 16, 0, 0);
-  }
-  return off;
-}
-
 // Nonzero bytes of a dword as bit 7 of each byte: ((x & 0x7f) + 0x7f) | x.
 __device__ __forceinline__ uint32_t nz_bytes(uint32_t x) { return (((x & 0x7f7f7f7fu) + 0x7f7f7f7fu) | x) & 0x80808080u; }
 
 // Those of bytes [lo, hi) of a 16-byte chunk (dword j covers bytes 4j..4j+3).
-template <bool PARTIAL>
 __device__ __forceinline__ uint32_t nz_chunk_word(uint32_t x, int j, int lo, int hi) {
-  uint32_t nz = nz_bytes(x);
-  if constexpr (PARTIAL) {
-    const int l = min(max(lo - 4 * j, 0), 4), h = min(max(4 * j + 4 - hi, 0), 4);
-    nz = (l + h >= 4) ? 0u : nz & (0xffffffffu << (8 * l)) & (0xffffffffu >> (8 * h));
-  }
-  return nz;
+  const int l = min(max(lo - 4 * j, 0), 4), h = min(max(4 * j + 4 - hi, 0), 4);
+  return (l + h >= 4) ? 0u : nz_bytes(x) & (0xffffffffu << (8 * l)) & (0xffffffffu >> (8 * h));
 }
 
-// Valid bytes [lo, hi) of the 16-byte chunk at LDS byte c folded into a
-// count; lastc = c when the chunk has one (the last such chunk wins).
-template <bool PARTIAL>
-__device__ __forceinline__ void fold_chunk(const unsigned char* buf, int c, int lo, int hi, int& count, int& lastc) {
-  const uint4 v = *reinterpret_cast<const uint4*>(buf + c);
-  const uint32_t n0 = nz_chunk_word<PARTIAL>(v.x, 0, lo, hi), n1 = nz_chunk_word<PARTIAL>(v.y, 1, lo, hi);
-  const uint32_t n2 = nz_chunk_word<PARTIAL>(v.z, 2, lo, hi), n3 = nz_chunk_word<PARTIAL>(v.w, 3, lo, hi);
-  count += __popc(n0) + __popc(n1) + __popc(n2) + __popc(n3);
-  if ((n0 | n1 | n2 | n3) != 0u) lastc = c;
-}
-
-// Valid count and last valid index of bytes [a, b) of the mask row that
-// starts at LDS byte s of buf (16-byte chunks; the first and last are
-// partial).  The last valid byte is found once, in the last chunk that has
-// one.
-__device__ __forceinline__ void scan_segment(const unsigned char* buf, int s, int a, int b, int& count, int& last) {
-  if (a >= b) return;
-  const int begin = s + a, end = s + b;
-  int c = begin & ~15;
+// Valid (nonzero) byte count and last valid index of bytes [a, e) of a mask
+// row in global memory.  The bytes are read as the 16-byte aligned chunks
+// that hold them, eight loads in flight; an aligned chunk that holds a byte of
+// the row lies on that byte's page.  The last valid byte is located once, in
+// the last chunk that has one.
+__device__ __forceinline__ void scan_row_global(const uint8_t* row, int a, int e, int& count, int& last) {
+  if (a >= e) return;
+  const uint8_t* begin = row + a;
+  const int off = int(reinterpret_cast<uintptr_t>(begin) & 15u);
+  const uint8_t* c0 = begin - off;  // pointer arithmetic keeps the global address space
+  const int span = off + (e - a);   // bytes from c0 to the end of the segment
+  const int nch = (span + 15) >> 4;
   int lastc = -1;
-  fold_chunk<true>(buf, c, begin - c, end - c, count, lastc);
-#pragma unroll 2
-  for (c += 16; c + 16 <= end; c += 16) fold_chunk<false>(buf, c, 0, 16, count, lastc);
-  if (c < end) fold_chunk<true>(buf, c, 0, end - c, count, lastc);
-  if (lastc >= 0) {
-    const uint4 v = *reinterpret_cast<const uint4*>(buf + lastc);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    const int lo = begin - lastc, hi = end - lastc;
-    int l = -1;
+  uint32_t lw[4] = {0u, 0u, 0u, 0u};
+  for (int c = 0; c < nch; c += 8) {
+    uint4 v[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t nz = nz_chunk_word<true>(w[j], j, lo, hi);
-      if (nz) l = 4 * j + ((31 - __clz(nz)) >> 3);
+    for (int t = 0; t < 8; ++t)
+      v[t] = c + t < nch ? *reinterpret_cast<const uint4*>(c0 + 16 * (c + t)) : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int ci = c + t;
+      const int lo = ci == 0 ? off : 0;
+      const int hi = min(16, span - 16 * ci);  // <= 0 past the segment: nothing kept
+      const uint32_t n0 = nz_chunk_word(v[t].x, 0, lo, hi), n1 = nz_chunk_word(v[t].y, 1, lo, hi);
+      const uint32_t n2 = nz_chunk_word(v[t].z, 2, lo, hi), n3 = nz_chunk_word(v[t].w, 3, lo, hi);
+      count += __popc(n0) + __popc(n1) + __popc(n2) + __popc(n3);
+      if ((n0 | n1 | n2 | n3) != 0u) {
+        lastc = ci;
+        lw[0] = n0; lw[1] = n1; lw[2] = n2; lw[3] = n3;
+      }
     }
-    last = lastc - s + l;
+  }
+  if (lastc >= 0) {
+    int l = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (lw[j]) l = 4 * j + ((31 - __clz(lw[j])) >> 3);
+    last = a + 16 * lastc + l - off;
   }
 }
 
-// Valid key / query counts and prefix flags of every molecule into s_info.
-// The masks of a chunk of molecules are copied into the staging area (two
-// halves of SB bytes, global -> LDS loads that need no registers); then TPR
-// adjacent threads scan one row (key rows 0..cb-1, query rows cb..2cb-1),
-// each a segment of it, and the segment counts meet over lanes.
+// Valid key / query counts and prefix flags of every molecule into s_info,
+// straight from the byte masks in global memory.  Rows are taken in passes of
+// whole molecules (row 2m: key mask of molecule m, row 2m + 1: its query
+// mask); TPR adjacent threads scan one row, each a segment of it, and the
+// segment counts meet over lanes.
 template <int DP>
-__device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem, uint32_t* s_info, int wave,
-                                           int lane) {
-  constexpr int SB = Lay<DP>::kQ / 2;
+__device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem, uint32_t* s_info) {
   const int tid = threadIdx.x;
   const int B = p.B, N = p.N;
-  const int cmax = min((SB - 32) / N, kThreads / 2);  // molecules per chunk (slack: alignment)
-  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP>::kQ);  // [2 cmax] counts, then last indices
+  const int rows = 2 * B;
+  // threads per row: a power of two, <= 8, with rows * tpr <= kThreads when rows allow
+  const int tpr = rows > kThreads / 2 ? 1 : rows > kThreads / 4 ? 2 : rows > kThreads / 8 ? 4 : 8;
+  const int rpp = kThreads / tpr;  // rows per pass (even)
+  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP>::kQ);  // [rpp] counts, then [rpp] last indices
   static_assert(kMaxQ * Lay<DP>::RB >= kThreads * 2 * 4, "row results must fit in the query staging area");
-  for (int b0 = 0; b0 < B; b0 += cmax) {
-    const int cb = min(cmax, B - b0);
-    const int ok = copy_bytes_to_lds(p.pkv + size_t(b0) * N, cb * N, smem, wave, lane);
-    const int oq = copy_bytes_to_lds(p.qv + size_t(b0) * N, cb * N, smem + SB, wave, lane);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies have landed
-    __syncthreads();
-    const int rows = 2 * cb;
-    // threads per row: a power of two, <= 8, tpr * rows <= kThreads (rows <= 2 cmax <= kThreads)
-    const int tpr = rows > kThreads / 2 ? 1 : rows > kThreads / 4 ? 2 : rows > kThreads / 8 ? 4 : 8;
-    const int r = tid / tpr, sg = tid & (tpr - 1);
+  const int seg = (N + tpr - 1) / tpr;
+  for (int r0 = 0; r0 < rows; r0 += rpp) {
+    const int r = r0 + tid / tpr, sg = tid & (tpr - 1);
     int cnt = 0, last = -1;
     if (r < rows) {
-      const bool key = r < cb;
-      const int m = key ? r : r - cb;
-      const int seg = (N + tpr - 1) / tpr;
-      const int a = sg * seg;
-      scan_segment(key ? smem : smem + SB, (key ? ok : oq) + m * N, a, min(N, a + seg), cnt, last);
+      const uint8_t* row = ((r & 1) ? p.qv : p.pkv) + size_t(r >> 1) * N;
+      const int a = min(N, sg * seg);
+      scan_row_global(row, a, min(N, a + seg), cnt, last);
     }
     // the tpr threads of a row are adjacent lanes of one wave (all active)
     if (tpr >= 2) {
@@ -1367,20 +1317,20 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
       last = int(MaxI32{}(uint32_t(last), dpp_peer<0x141>(uint32_t(last))));
     }
     if (r < rows && sg == 0) {
-      s_cnt[r] = cnt;
-      s_cnt[2 * cmax + r] = last;
+      s_cnt[r - r0] = cnt;
+      s_cnt[rpp + r - r0] = last;
     }
     __syncthreads();
-    for (int m = tid; m < cb; m += kThreads) {
-      const int ck = min(s_cnt[m], N), cq = min(s_cnt[cb + m], N);
-      const int lk = s_cnt[2 * cmax + m], lq = s_cnt[2 * cmax + cb + m];
-      s_info[b0 + m] =
+    const int m0 = r0 >> 1;
+    for (int m = tid; m < rpp / 2 && m0 + m < B; m += kThreads) {
+      const int ck = min(s_cnt[2 * m], N), cq = min(s_cnt[2 * m + 1], N);
+      const int lk = s_cnt[rpp + 2 * m], lq = s_cnt[rpp + 2 * m + 1];
+      s_info[m0 + m] =
           uint32_t(ck) | (uint32_t(cq) << 11) | (lk + 1 == ck ? kKPre : 0u) | (lq + 1 == cq ? kQPre : 0u);
     }
     __syncthreads();
   }
 }
-
 
 // s_order[rank] = molecule, s_pre[rank] = its first list position
 // (s_pre[B] = attention units in the list), molecules longest first (cost
@@ -1412,6 +1362,7 @@ __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* 
     int rank = 0, pre = 0;
     // pairs part, part + 4, ...: two per 16-byte read
     const uint4* c4 = reinterpret_cast<const uint4*>(s_cu);
+#pragma unroll 8
     for (int o = 2 * part; o < B4; o += 8) {
       const uint4 v = c4[o >> 1];  // pairs o, o + 1
       const bool f0 = v.x > cb || (v.x == cb && o < b);
@@ -1485,7 +1436,7 @@ __global__ void __launch_bounds__(kThreads, BIAS ? 1 : 2) simplicial_pair_kernel
   const int wg = blockIdx.x;
 
   if (tid == 0) cl->claimed = 0;
-  scan_masks<DP>(p, smem, s_info, wave, lane);  // ends with a barrier
+  scan_masks<DP>(p, smem, s_info);  // ends with a barrier
   rank_molecules(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
   const int total = s_pre[B];
 
