@@ -879,73 +879,114 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
     const int rj = round16(nkj), rk = round16(nkk);
     const int dt = p.bias_dtype;
-    float mu = 0.0f, mv = 0.0f, mw = 0.0f;
-    // sets [rows][cols] with the key index fastest (consecutive threads read consecutive keys); kB loads
-    // per thread are issued before their conversions and stores
-    constexpr int kB = 8;
-    // U: rows = queries, cols = rows j of the j block -> BU[j][qi] = c_qi u[qa][ka_j]
-    for (int base = tid; base < kMaxQ * rj; base += kB * kThreads) {
-      float val[kB];
+    float mx[3] = {0.0f, 0.0f, 0.0f};  // max |u|, |v|, |w| of the staged values
+    // Each set is taken a row per wave (rows wave, wave + kWaves, ...) with the lanes along the
+    // columns (lane, lane + 64), so a wave's loads of a row are one coalesced run; kRB rows of a
+    // wave are loaded before any is converted and stored.  Rows and columns past the valid
+    // queries / keys are stored as zero.
+    //   set 0 (U): rows = queries qi < kMaxQ, columns j < rj:  BU[j][qi]     = c_qi u[qa][ka(j0 + j)]
+    //   set 1 (V): rows = queries qi,          columns k < rk:  BV[qi][k + 2] = c_qi v[qa][ka(k0 + k)]
+    //   set 2 (W): rows j < rj,                columns k < rk:  BW[j][k]      = w[ka(j0 + j)][ka(k0 + k)]
+    // The first kRB rows of every set (all of U and V, and W up to 48 rows) are loaded before
+    // anything is stored, so the common case pays one round trip to memory.
+    constexpr int kRB = kMaxQ / kWaves;
+    auto set_shape = [&](auto set_tag, int& R, int& C, int& rvalid, int& cvalid, int& cbase, const void*& src) {
+      constexpr int SET = decltype(set_tag)::value;
+      R = SET == 2 ? rj : kMaxQ;
+      C = SET == 0 ? rj : rk;
+      rvalid = SET == 2 ? nkj : nqg;
+      cvalid = SET == 0 ? nkj : nkk;
+      cbase = SET == 0 ? j0 : k0;
+      src = SET == 0 ? p.bu : (SET == 1 ? p.bv : p.bw);
+    };
+    // Loads without branches: a lane's two column atoms are found once, each row's atom once
+    // (wave-uniform), out-of-range rows and columns read a clamped valid element (zeroed when
+    // stored, so no use follows a load and a wave's loads of a batch are in flight together),
+    // and the element width is one uniform choice for the whole batch.
+    auto load_rows = [&](auto set_tag, int r0, uint32_t (&val)[kRB][2]) {
+      constexpr int SET = decltype(set_tag)::value;
+      int R, C, rvalid, cvalid, cbase;
+      const void* src;
+      set_shape(set_tag, R, C, rvalid, cvalid, cbase, src);
 #pragma unroll
-      for (int t = 0; t < kB; ++t) {
-        const int e = base + t * kThreads;
-        const int qi = e / rj, j = e - qi * rj;
-        const bool ok = e < kMaxQ * rj && j < nkj && qi < nqg;
-        const int qa = ok ? (qpre ? q0 + qi : int(qidx[q0 + qi])) : 0;
-        val[t] = ok ? bias_at(p.bu, (size_t(bh) * N + qa) * N + key_atom(j0 + j), dt) : 0.0f;
-      }
+      for (int t = 0; t < kRB; ++t) val[t][0] = val[t][1] = 0u;
+      if (rvalid <= 0 || cvalid <= 0) return;
+      const bool two = C > 64;  // a second column per lane (wave-uniform)
+      int ca[2];
 #pragma unroll
-      for (int t = 0; t < kB; ++t) {
-        const int e = base + t * kThreads;
-        if (e >= kMaxQ * rj) break;
-        const int qi = e / rj, j = e - qi * rj;
-        mu = fmaxf(mu, fabsf(val[t]));
-        BU[j * kMaxQ + qi] = half_bits_sat(cgf[qi] * val[t]);
+      for (int s = 0; s < 2; ++s) ca[s] = key_atom(cbase + min(lane + 64 * s, cvalid - 1));
+      int ra[kRB];  // row atoms, all found before any load is issued
+#pragma unroll
+      for (int t = 0; t < kRB; ++t) {
+        const int rc = min(r0 + kWaves * t, rvalid - 1);
+        ra[t] = SET == 2 ? key_atom(j0 + rc) : (qpre ? q0 + rc : int(qidx[q0 + rc]));
       }
+      auto batch = [&](auto wide_tag) {
+        constexpr bool WIDE = decltype(wide_tag)::value;
+#pragma unroll
+        for (int t = 0; t < kRB; ++t) {
+          const size_t rowbase = (size_t(bh) * N + ra[t]) * N;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            if (s == 1 && !two) continue;  // wave-uniform
+            if constexpr (WIDE) val[t][s] = static_cast<const uint32_t*>(src)[rowbase + ca[s]];
+            else val[t][s] = static_cast<const uint16_t*>(src)[rowbase + ca[s]];
+          }
+        }
+      };
+      if (dt == MF_DTYPE_F32) batch(std::true_type{});
+      else batch(std::false_type{});
+    };
+    auto store_rows = [&](auto set_tag, int r0, const uint32_t (&val)[kRB][2]) {
+      constexpr int SET = decltype(set_tag)::value;
+      int R, C, rvalid, cvalid, cbase;
+      const void* src;
+      set_shape(set_tag, R, C, rvalid, cvalid, cbase, src);
+#pragma unroll
+      for (int t = 0; t < kRB; ++t) {
+        const int r = r0 + kWaves * t;
+        if (r >= R) break;  // wave-uniform
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const int c = lane + 64 * s;
+          if (c >= C) continue;
+          const uint32_t raw = val[t][s];
+          const float x = !(r < rvalid && c < cvalid) ? 0.0f
+                          : dt == MF_DTYPE_F32         ? __uint_as_float(raw)
+                          : dt == MF_DTYPE_BF16        ? __uint_as_float(raw << 16)
+                                                       : float(__builtin_bit_cast(_Float16, uint16_t(raw)));
+          mx[SET] = fmaxf(mx[SET], fabsf(x));
+          if constexpr (SET == 0) BU[c * kMaxQ + r] = half_bits_sat(cgf[r] * x);
+          else if constexpr (SET == 1) BV[r * Ly::kVS + c + 2] = half_bits_sat(cgf[r] * x);
+          else BW[r * kCap + c] = half_bits_sat(x);
+        }
+      }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    {
+      uint32_t vu[kRB][2], vv[kRB][2], vw[kRB][2];
+      load_rows(S0{}, wave, vu);
+      load_rows(S1{}, wave, vv);
+      load_rows(S2{}, wave, vw);
+      store_rows(S0{}, wave, vu);
+      store_rows(S1{}, wave, vv);
+      store_rows(S2{}, wave, vw);
     }
-    // V: rows = queries, cols = keys of the k block -> BV[qi][k + 2] = c_qi v[qa][ka_k]
-    for (int base = tid; base < kMaxQ * rk; base += kB * kThreads) {
-      float val[kB];
-#pragma unroll
-      for (int t = 0; t < kB; ++t) {
-        const int e = base + t * kThreads;
-        const int qi = e / rk, k = e - qi * rk;
-        const bool ok = e < kMaxQ * rk && k < nkk && qi < nqg;
-        const int qa = ok ? (qpre ? q0 + qi : int(qidx[q0 + qi])) : 0;
-        val[t] = ok ? bias_at(p.bv, (size_t(bh) * N + qa) * N + key_atom(k0 + k), dt) : 0.0f;
-      }
-#pragma unroll
-      for (int t = 0; t < kB; ++t) {
-        const int e = base + t * kThreads;
-        if (e >= kMaxQ * rk) break;
-        const int qi = e / rk, k = e - qi * rk;
-        mv = fmaxf(mv, fabsf(val[t]));
-        BV[qi * Ly::kVS + k + 2] = half_bits_sat(cgf[qi] * val[t]);
-      }
+    // W rows past the first batch (more than 48 staged keys)
+    for (int r0 = wave + kWaves * kRB; r0 < rj; r0 += kWaves * kRB) {
+      uint32_t vw[kRB][2];
+      load_rows(S2{}, r0, vw);
+      store_rows(S2{}, r0, vw);
     }
-    // W: rows j of the j block, cols = keys of the k block -> BW[j][k] = w[ka_j][ka_k]
-    for (int base = tid; base < rj * rk; base += kB * kThreads) {
-      float val[kB];
+    // maxima over the wave, then one LDS atomic per wave and set (float order equals bit order for
+    // magnitudes)
 #pragma unroll
-      for (int t = 0; t < kB; ++t) {
-        const int e = base + t * kThreads;
-        const int j = e / rk, k = e - j * rk;
-        const bool ok = e < rj * rk && j < nkj && k < nkk;
-        val[t] = ok ? bias_at(p.bw, (size_t(bh) * N + key_atom(j0 + j)) * N + key_atom(k0 + k), dt) : 0.0f;
-      }
-#pragma unroll
-      for (int t = 0; t < kB; ++t) {
-        const int e = base + t * kThreads;
-        if (e >= rj * rk) break;
-        const int j = e / rk, k = e - j * rk;
-        mw = fmaxf(mw, fabsf(val[t]));
-        BW[j * kCap + k] = half_bits_sat(val[t]);
-      }
+    for (int e = 0; e < 3; ++e) {
+      const uint32_t m = group_reduce<64>(__float_as_uint(mx[e]), MaxF32{});
+      if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(bmax + e), m);
     }
-    // magnitudes: float order equals bit order
-    atomicMax(reinterpret_cast<unsigned int*>(bmax + 0), __float_as_uint(mu));
-    atomicMax(reinterpret_cast<unsigned int*>(bmax + 1), __float_as_uint(mv));
-    atomicMax(reinterpret_cast<unsigned int*>(bmax + 2), __float_as_uint(mw));
   };
   if constexpr (BIAS) {
     for (int qi = tid; qi < kMaxQ; qi += kThreads) {
