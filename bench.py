@@ -26,13 +26,19 @@ Prints ONE JSON line.  Also reports:
                 the training-state forward (fp32 out + lse), forward + backward
                 (mf_simplicial_bwd), C2 with a factorized bias, C1 (fp32),
                 C3 kNN (and its HBM-sized scaled batch), C4 radius mask +
-                attention, and the configs[4] trunk forward (molecules/s).
+                attention, the configs[4] trunk forward (molecules/s), and the
+                SimplicialAttention module on C2's batch (in_proj -> attention
+                -> out_proj, eager, forward and train step).
 
 Other entry modes (one JSON line each, not the headline):
   --workload knn          kNN top-16 at B=32 and scaled to
                           B=32*1024 for the HBM roofline;
   --workload radius       radius mask + radius attention (configs[3]);
   --workload trunk        the configs[4] trunk forward;
+  --workload module       the TwoSimplicialAttention module (in_proj -> attention ->
+                          out_proj) over the reference harness's grid
+                          (scripts/benchmark_simplicial_attention.py:27-42), forward
+                          and train step, modes none / factorized, impl hip and torch;
   --copy-calibration      a plain device copy of known size, run under
                           rocprofv3 --pmc to scale FETCH_SIZE / WRITE_SIZE.
 """
@@ -63,7 +69,7 @@ def parse_args():
     ap.add_argument("--cpu-sample", type=int, default=64, help="molecules in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="CPU-baseline threads (0 = physical cores, capped by OMP_NUM_THREADS when set)")
-    ap.add_argument("--workload", choices=("simplicial", "knn", "radius", "trunk"), default="simplicial")
+    ap.add_argument("--workload", choices=("simplicial", "knn", "radius", "trunk", "module"), default="simplicial")
     ap.add_argument("--no-extra", action="store_true", help="headline only (skip the extra configurations)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 512 MiB device copy (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -502,6 +508,111 @@ def measure_trunk_geometry() -> dict:
                       "(factorized, fp32), sigma U[0.05, 2.05), terms on the compact layout"}
 
 
+# The reference's module benchmark grid (d_model, heads, tokens, batch): scripts/benchmark_simplicial_attention.py:27-42
+MODULE_GRID = (
+    (512, 8, 24, 256), (512, 8, 32, 128), (512, 8, 48, 64), (512, 8, 64, 32), (512, 8, 96, 16), (512, 8, 128, 8),
+    (512, 8, 192, 4), (768, 12, 24, 256), (768, 12, 32, 128), (768, 12, 48, 64), (768, 12, 64, 32),
+    (768, 12, 96, 16), (768, 12, 128, 8), (768, 12, 192, 4),
+)
+
+
+def _module_case(impl, mode, pass_type, d_model, heads, tokens, batch, *, pad=None, warmup=2, iters=5):
+    """One case run as the reference harness does (scripts/benchmark_simplicial_attention.py:167-259): the
+    module in eval (forward, no_grad) or train mode (out.square().mean() backward), inputs drawn inside every
+    run (randn x and, for mode "factorized", randn u, v, w, gate), host clock around iters runs after warmup.
+    `pad` (True = padding, [batch, tokens]) replaces the all-valid mask of the reference grid."""
+    import torch
+
+    from matterformer_amd.simplicial_attention import TwoSimplicialAttention
+    from matterformer_amd.simplicial_types import SimplicialAttentionMask, SimplicialFactorizedBias
+
+    dev = torch.device("cuda", 0)
+    dt = torch.bfloat16
+    torch.manual_seed(0)
+    attn = TwoSimplicialAttention(dim=d_model, num_heads=heads, chunk_size=min(tokens, 128), dropout=0.0,
+                                  impl=impl, precision="bf16_tc").to(device=dev, dtype=dt)
+    attn.eval() if pass_type == "forward" else attn.train()
+    mask = SimplicialAttentionMask.from_key_padding_mask(pad, batch_size=batch, num_tokens=tokens, device=dev)
+
+    def run_once():
+        rg = pass_type == "train_step"
+        x = torch.randn(batch, tokens, d_model, device=dev, dtype=dt, requires_grad=rg)
+        fb = None
+        if mode == "factorized":
+            fb = SimplicialFactorizedBias(*(torch.randn(batch, heads, tokens, tokens, device=dev, dtype=dt,
+                                                        requires_grad=rg) for _ in range(3)),
+                                          torch.randn(batch, heads, tokens, device=dev, dtype=dt, requires_grad=rg))
+        attn.zero_grad(set_to_none=True)
+        if pass_type == "forward":
+            with torch.no_grad():
+                attn(x, attention_mask=mask, factorized_bias=fb)
+            return
+        attn(x, attention_mask=mask, factorized_bias=fb).square().mean().backward()
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_once()
+    torch.cuda.synchronize()
+    first_ms = (time.perf_counter() - t0) * 1e3
+    for _ in range(warmup):
+        run_once()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        run_once()
+    torch.cuda.synchronize()
+    steady_ms = (time.perf_counter() - t0) * 1e3 / iters
+    return {"impl": impl, "mode": mode, "pass": pass_type, "d_model": d_model, "heads": heads, "tokens": tokens,
+            "batch": batch, "first_ms": round(first_ms, 3), "steady_ms": round(steady_ms, 4),
+            "peak_mem_mib": round(torch.cuda.max_memory_allocated(dev) / 2**20, 1),
+            "last_impl_used": getattr(attn, "_last_impl_used", None)}
+
+
+def measure_module_c2() -> dict:
+    """SimplicialAttention(512, 8) with impl="hip" on C2's batch (64 GEOM molecules padded to 181, their key
+    padding mask): forward and train step, the reference harness's timing (inputs drawn per run)."""
+    from matterformer_amd.workloads import simplicial_workload
+
+    w = simplicial_workload("geom")
+    pad = (~w.pair_key_valid).to("cuda")
+    B, N = pad.shape
+    res = {}
+    for pass_type in ("forward", "train_step"):
+        for mode in ("none", "factorized"):
+            c = _module_case("hip", mode, pass_type, 512, 8, N, B, pad=pad, warmup=3, iters=10)
+            res[f"{pass_type}_{mode}_ms"] = c["steady_ms"]
+            res[f"{pass_type}_{mode}_impl"] = c["last_impl_used"]
+    res["molecules_per_s_forward"] = round(B / (res["forward_none_ms"] * 1e-3), 1)
+    res["config"] = ("TwoSimplicialAttention(dim=512, num_heads=8, impl='hip', bf16_tc), x [64, 181, 512] bf16, "
+                     "C2 key padding mask; per run: randn inputs (and u, v, w, gate for 'factorized'), "
+                     "in_proj -> attention -> out_proj (train step: + backward of out.square().mean())")
+    return res
+
+
+def bench_module(args) -> int:
+    """The reference harness's grid through the mirrored module: impl hip and torch, modes none / factorized,
+    forward and train step (one JSON line; `value` = geometric mean of the hip forward, mode none)."""
+    import math
+
+    cases = []
+    for (d, h, t, b) in MODULE_GRID:
+        for pass_type in ("forward", "train_step"):
+            for mode in ("none", "factorized"):
+                for impl in ("hip", "torch"):
+                    cases.append(_module_case(impl, mode, pass_type, d, h, t, b))
+                    print(json.dumps({"case": cases[-1]}), file=sys.stderr, flush=True)
+    fwd = [c["steady_ms"] for c in cases if c["impl"] == "hip" and c["pass"] == "forward" and c["mode"] == "none"]
+    gm = math.exp(sum(math.log(x) for x in fwd) / len(fwd))
+    line = _line("TwoSimplicialAttention module forward steady ms, reference harness grid (geometric mean)",
+                 round(gm, 4), "ms", gm, args, "bf16", "synthetic (randn per run, as the reference harness)",
+                 {"workload": "scripts/benchmark_simplicial_attention.py grid, bf16_tc, all tokens valid",
+                  "grid": [list(g) for g in MODULE_GRID]}, cases=cases)
+    line["higher_is_better"] = False
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def _line(metric, value, unit, ms, args, dtype, data, config, **more):
     line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -666,6 +777,8 @@ def main() -> int:
         return bench_radius(args)
     if args.workload == "trunk":
         return bench_trunk(args)
+    if args.workload == "module":
+        return bench_module(args)
     dev = torch.device("cuda", 0)
     lib = _native.lib()
 
@@ -697,6 +810,7 @@ def main() -> int:
         extra["c5_trunk_geometry"] = measure_trunk_geometry()
         extra["geometry_features"] = measure_geometry()
         extra["pair_mlp_bias"] = measure_pair_mlp()
+        extra["module_c2"] = measure_module_c2()
 
     cpu = cpu_baseline(w, args.cpu_sample, args.cpu_threads) if args.cpu_sample > 0 else None
 

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 7
+#define MF_ABI_VERSION 8
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -135,6 +135,20 @@ typedef struct mf_simplicial_fwd_args {
   const float* message_right;  /* [B*H, N, N, Rm] fp32                     */
   const float* message_basis;  /* [H, Rm, D] fp32                          */
   int32_t message_rank;        /* Rm, 1..64 when message_left != NULL     */
+  /* ABI 8: strides, in elements, of the [B, H, N, D] operands as
+   * {batch, head, token} (d is unit-stride), for views such as the chunks of
+   * an in_proj output [B, N, 5, H, D] (the reference's _split_heads,
+   * simplicial_attention.py:708-711, without its .contiguous() copies) and an
+   * out that is the merged [B, N, H, D] layout out_proj reads
+   * (_merge_heads).  All three zero: the contiguous [B*H, N, D] layout.
+   * Other strides are taken by the pair kernel only (16-bit operands,
+   * head_dim <= 64 and a multiple of 8, tokens <= 512, no angle or message
+   * term, every stride a multiple of 8 and every base 16-byte aligned);
+   * calls outside that return MF_ERR_UNSUPPORTED.  out_f32 and lse stay
+   * contiguous. */
+  int64_t q_stride[3];   /* of q                                          */
+  int64_t kv_stride[3];  /* shared by k1, v1, k2 and v2                   */
+  int64_t out_stride[3]; /* of out                                        */
 } mf_simplicial_fwd_args;
 
 int mf_simplicial_fwd(const mf_simplicial_fwd_args* args, void* stream);

@@ -50,7 +50,7 @@ EXPORTED_SYMBOLS = (
     "mf_pair_mlp_bias",
 )
 
-EXPECTED_ABI_VERSION = 7
+EXPECTED_ABI_VERSION = 8
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -93,6 +93,9 @@ class MfSimplicialFwdArgs(ctypes.Structure):
         ("message_right", ctypes.c_void_p),
         ("message_basis", ctypes.c_void_p),
         ("message_rank", ctypes.c_int32),
+        ("q_stride", ctypes.c_int64 * 3),
+        ("kv_stride", ctypes.c_int64 * 3),
+        ("out_stride", ctypes.c_int64 * 3),
     ]
 
 

@@ -759,6 +759,19 @@ static bool operands_aligned(const mf_simplicial_fwd_args* a) {
   return true;
 }
 
+// ABI 8 operand strides: any set non-zero means a layout other than the contiguous [B*H, N, D].
+static bool has_strides(const mf_simplicial_fwd_args* a) {
+  for (const int64_t* st : {a->q_stride, a->kv_stride, a->out_stride})
+    if (st[0] != 0 || st[1] != 0 || st[2] != 0) return true;
+  return false;
+}
+
+// Batch stride, in bytes, of a 16-bit operand whose strides are `st` (all zero: contiguous).
+static size_t batch_stride_bytes(const int64_t* st, const mf_simplicial_fwd_args* a) {
+  if (st[0] == 0 && st[1] == 0 && st[2] == 0) return size_t(a->heads) * a->tokens * a->head_dim * 2;
+  return size_t(st[0]) * 2;
+}
+
 extern "C" int mf_simplicial_fwd_supported(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
                                            int32_t dtype) {
   if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0)
@@ -967,6 +980,18 @@ static int simplicial_fwd_impl(const mf_simplicial_fwd_args* a, void* stream) {
   // the factorized bias alone runs in the pair kernel; the angle and message terms (and the bias on
   // other shapes) run on the general kernel
   const bool bias_only = a->bias_u != nullptr && a->angle_left == nullptr && a->message_left == nullptr;
+  if (has_strides(a)) {
+    if (!pair_ok || (has_extras(a) && !bias_only))
+      return fail(MF_ERR_UNSUPPORTED,
+                  "mf_simplicial_fwd: operand strides other than the contiguous [B*H, N, D] layout are taken by "
+                  "the pair kernel only (16-bit operands, head_dim <= 64 and a multiple of 8, tokens <= 512, "
+                  "16-byte aligned bases, no angle or message term)");
+    for (const int64_t* st3 : {a->q_stride, a->kv_stride, a->out_stride})
+      for (int i = 0; i < 3; ++i)
+        if (st3[i] < 0 || st3[i] % 8 != 0)
+          return fail(MF_ERR_INVALID_ARGUMENT,
+                      "mf_simplicial_fwd: operand strides must be non-negative multiples of 8 elements");
+  }
   if (has_extras(a) && !(bias_only && pair_ok)) {
     st = check_shape(a->batch, a->heads, a->tokens, a->head_dim, a->dtype, has_pv, &lds);
     if (st != MF_OK) return st;
@@ -985,21 +1010,31 @@ static int simplicial_fwd_impl(const mf_simplicial_fwd_args* a, void* stream) {
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_fwd: workspace must be 16-byte aligned");
     const int slice = simplicial_pair_max_batch(a->tokens);
     const size_t row = size_t(a->heads) * a->tokens;
-    const size_t elem = row * a->head_dim * 2;
+    const size_t qb = batch_stride_bytes(a->q_stride, a), kvb = batch_stride_bytes(a->kv_stride, a);
+    const size_t ob = batch_stride_bytes(a->out_stride, a);
     for (int b0 = 0; b0 < a->batch; b0 += slice) {
       mf_simplicial_fwd_args sub = *a;
       sub.batch = std::min(slice, a->batch - b0);
-      sub.q = static_cast<const char*>(a->q) + b0 * elem;
-      sub.k1 = static_cast<const char*>(a->k1) + b0 * elem;
-      sub.v1 = static_cast<const char*>(a->v1) + b0 * elem;
-      sub.k2 = static_cast<const char*>(a->k2) + b0 * elem;
-      sub.v2 = static_cast<const char*>(a->v2) + b0 * elem;
+      sub.q = static_cast<const char*>(a->q) + b0 * qb;
+      sub.k1 = static_cast<const char*>(a->k1) + b0 * kvb;
+      sub.v1 = static_cast<const char*>(a->v1) + b0 * kvb;
+      sub.k2 = static_cast<const char*>(a->k2) + b0 * kvb;
+      sub.v2 = static_cast<const char*>(a->v2) + b0 * kvb;
       sub.query_valid = a->query_valid + size_t(b0) * a->tokens;
       sub.pair_key_valid = a->pair_key_valid + size_t(b0) * a->tokens;
       if (a->pair_valid) sub.pair_valid = a->pair_valid + size_t(b0) * a->tokens * a->tokens;
-      if (a->out) sub.out = static_cast<char*>(a->out) + b0 * elem;
+      if (a->out) sub.out = static_cast<char*>(a->out) + b0 * ob;
       if (a->out_f32) sub.out_f32 = a->out_f32 + b0 * row * a->head_dim;
       if (a->lse) sub.lse = a->lse + b0 * row;
+      if (a->bias_u) {
+        // [B*H, N, N] and [B*H, N] in bias_dtype: the slice's molecules
+        const size_t be = a->bias_dtype == MF_DTYPE_F32 ? 4 : 2;
+        const size_t pairs = row * a->tokens * be;
+        sub.bias_u = static_cast<const char*>(a->bias_u) + b0 * pairs;
+        sub.bias_v = static_cast<const char*>(a->bias_v) + b0 * pairs;
+        sub.bias_w = static_cast<const char*>(a->bias_w) + b0 * pairs;
+        sub.bias_gate = static_cast<const char*>(a->bias_gate) + b0 * row * be;
+      }
       st = simplicial_pair_launch(&sub, a->workspace, dev.num_cus, s);
       if (st != MF_OK) return st;
     }

@@ -100,6 +100,11 @@ struct Params {
   const void* bw;
   const void* bg;
   int bias_dtype;
+  // element strides {batch, head, token} of q, of k1 / v1 / k2 / v2, and of out (d is unit-stride);
+  // the contiguous [B*H, N, D] layout unless the caller passed others
+  long long qs_b, qs_h, qs_n;
+  long long ks_b, ks_h, ks_n;
+  long long os_b, os_h, os_n;
 };
 
 // The claim counter in the caller's workspace (its own 128-byte line).  It
@@ -646,16 +651,17 @@ __device__ __forceinline__ void zero_padded_share(const Params& p, const uint32_
   const int N = p.N, D = p.D, H = p.H;
   const int cpr = D / 8;
   for (int bh = w; bh < p.B * H; bh += G) {
-    const int b = bh / H;
+    const int b = bh / H, h = bh - b * H;
     const uint32_t info = s_info[b];
     const bool qpre = (info & kQPre) != 0;
     const int i0 = qpre ? info_nq(info) : 0;  // rows below are valid
     const uint8_t* qrow = p.qv + size_t(b) * N;
+    T* orow0 = p.out ? static_cast<T*>(p.out) + b * p.os_b + h * p.os_h : nullptr;
     for (int u = int(threadIdx.x); u < (N - i0) * CPR; u += kThreads) {
       const int i = i0 + u / CPR, cc = u % CPR;
       if (cc >= cpr || (!qpre && qrow[i] != 0)) continue;
       const size_t row = size_t(bh) * N + i;
-      if (p.out) reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row * D)[cc] = uint4{0u, 0u, 0u, 0u};
+      if (p.out) reinterpret_cast<uint4*>(orow0 + i * p.os_n)[cc] = uint4{0u, 0u, 0u, 0u};
       if (p.out_f32) {
         float4* o = reinterpret_cast<float4*>(p.out_f32 + row * D + cc * 8);
         o[0] = float4{0.f, 0.f, 0.f, 0.f};
@@ -700,11 +706,11 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   float* gmax = reinterpret_cast<float*>(smem + Ly::kG);
   int* scal = reinterpret_cast<int*>(smem + Ly::kScal);
   float* s_m = reinterpret_cast<float*>(smem + Ly::kM);
-  const T* gq = static_cast<const T*>(p.q) + size_t(bh) * N * D;
-  const T* gk1 = static_cast<const T*>(p.k1) + size_t(bh) * N * D;
-  const T* gk2 = static_cast<const T*>(p.k2) + size_t(bh) * N * D;
-  const T* gv1 = static_cast<const T*>(p.v1) + size_t(bh) * N * D;
-  const T* gv2 = static_cast<const T*>(p.v2) + size_t(bh) * N * D;
+  const T* gq = static_cast<const T*>(p.q) + b * p.qs_b + h * p.qs_h;
+  const T* gk1 = static_cast<const T*>(p.k1) + b * p.ks_b + h * p.ks_h;
+  const T* gk2 = static_cast<const T*>(p.k2) + b * p.ks_b + h * p.ks_h;
+  const T* gv1 = static_cast<const T*>(p.v1) + b * p.ks_b + h * p.ks_h;
+  const T* gv2 = static_cast<const T*>(p.v2) + b * p.ks_b + h * p.ks_h;
 
   // staging map: 16-byte chunk u = tid + kThreads i of a row set is row
   // u / CPR, columns 8 cc .. 8 cc + 7 with cc = tid % CPR for every i; only
@@ -730,7 +736,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       const int row = (tid + kThreads * i) / CPR;
       arr[i] = uint4{0u, 0u, 0u, 0u};
       if (i < nI && row < nrows && col_ok)
-        arr[i] = *reinterpret_cast<const uint4*>(base + size_t(key_atom(row0 + row)) * D + e0);
+        arr[i] = *reinterpret_cast<const uint4*>(base + key_atom(row0 + row) * p.ks_n + e0);
     }
   };
   uint4 rk1[MAXC], rk2[MAXC], rv1[MAXC], rv2[MAXC], rq[MAXQC];
@@ -774,7 +780,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     for (int i = 0; i < MAXQC; ++i) {
       const int row = (tid + kThreads * i) / CPR;
       rq[i] = (row < nqg && col_ok)
-                  ? *reinterpret_cast<const uint4*>(gq + size_t(qpre ? q0 + row : int(qidx[q0 + row])) * D + e0)
+                  ? *reinterpret_cast<const uint4*>(gq + (qpre ? q0 + row : int(qidx[q0 + row])) * p.qs_n + e0)
                   : uint4{0u, 0u, 0u, 0u};
     }
   }
@@ -1250,7 +1256,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         const T lo = T(o[2 * e]), hi = T(o[2 * e + 1]);
         w[e] = uint32_t(__builtin_bit_cast(uint16_t, lo)) | (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
       }
-      *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + row * D + c8) = uint4{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + b * p.os_b + h * p.os_h + atom * p.os_n + c8) =
+          uint4{w[0], w[1], w[2], w[3]};
     }
     if (p.out_f32) {
       float4* dst = reinterpret_cast<float4*>(p.out_f32 + row * D + c8);
@@ -1570,6 +1577,16 @@ int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* claims, int nu
   prm.counter = static_cast<unsigned int*>(claims);
   prm.bu = a->bias_u; prm.bv = a->bias_v; prm.bw = a->bias_w; prm.bg = a->bias_gate;
   prm.bias_dtype = a->bias_dtype;
+  const long long cb = (long long)a->heads * a->tokens * a->head_dim, ch = (long long)a->tokens * a->head_dim;
+  auto strides = [&](const int64_t* st, long long& sb, long long& sh, long long& sn) {
+    const bool dflt = st[0] == 0 && st[1] == 0 && st[2] == 0;
+    sb = dflt ? cb : st[0];
+    sh = dflt ? ch : st[1];
+    sn = dflt ? a->head_dim : st[2];
+  };
+  strides(a->q_stride, prm.qs_b, prm.qs_h, prm.qs_n);
+  strides(a->kv_stride, prm.ks_b, prm.ks_h, prm.ks_n);
+  strides(a->out_stride, prm.os_b, prm.os_h, prm.os_n);
   const int g = num_cus;
   const bool pv = a->pair_valid != nullptr;
   const bool bf = a->dtype == MF_DTYPE_BF16;

@@ -23,6 +23,8 @@ ran.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from matterformer_amd import _native
@@ -164,6 +166,29 @@ def _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, angle_left, angle_right, 
     return ext
 
 
+def _operand_views(q, k1, v1, k2, v2, cdt, low_rank: bool):
+    """The (q, k/v) {batch, head, token} element strides when the five [B, H, N, D] operands can be read
+    in place by the pair kernel (views such as the chunks of an in_proj output), else None (the operands
+    are then copied to the contiguous layout).  The pair kernel takes 16-bit operands already in the
+    compute dtype, head_dim <= 64 and a multiple of 8, tokens <= 512, no angle or message term, unit-stride
+    d, strides that are multiples of 8 elements and 16-byte aligned bases; k1, v1, k2 and v2 share strides."""
+    B, H, N, D = q.shape
+    if low_rank or cdt not in (torch.float16, torch.bfloat16) or D % 8 != 0 or D > 64 or N > 512:
+        return None
+    ts = (q, k1, v1, k2, v2)
+    if all(t.is_contiguous() for t in ts):
+        return None
+    if any(t.dtype != cdt or t.stride(3) != 1 or t.data_ptr() % 16 != 0 for t in ts):
+        return None
+    qs = tuple(q.stride()[:3])
+    kvs = tuple(k1.stride()[:3])
+    if any(tuple(t.stride()[:3]) != kvs for t in (v1, k2, v2)):
+        return None
+    if any(x < 0 or x % 8 != 0 for x in qs + kvs):
+        return None
+    return qs, kvs
+
+
 def hip_simplicial_attention_forward(
     q: torch.Tensor,
     k1: torch.Tensor,
@@ -213,13 +238,26 @@ def hip_simplicial_attention_forward(
         raise RuntimeError(f"the HIP backend only supports float16/bfloat16/float32 inputs, got {q.dtype}")
 
     cdt = _compute_dtype(q.dtype, precision)
-    ops = [t.to(device=q.device, dtype=cdt).contiguous() for t in (q, k1, v1, k2, v2)]
+    views = _operand_views(q, k1, v1, k2, v2, cdt, angle_left is not None or message_left is not None)
+    if views is not None:
+        ops = [q, k1, v1, k2, v2]
+        q_stride, kv_stride = views
+    else:
+        ops = [t.to(device=q.device, dtype=cdt).contiguous() for t in (q, k1, v1, k2, v2)]
+        q_stride = kv_stride = (0, 0, 0)
     qv = query_valid.to(device=q.device, dtype=torch.bool).contiguous()
     pkv = pair_key_valid.to(device=q.device, dtype=torch.bool).contiguous()
     pv = None if pair_valid is None else pair_valid.to(device=q.device, dtype=torch.bool).contiguous()
 
     out_direct = q.dtype == cdt
-    out = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype) if out_direct else None
+    out_stride = (0, 0, 0)
+    if views is not None:
+        # written in the merged [B, N, H, D] layout that _merge_heads / out_proj read, returned as its
+        # [B, H, N, D] view
+        out = torch.empty((B, N, H, D), device=q.device, dtype=q.dtype).permute(0, 2, 1, 3)
+        out_stride = (N * H * D, D, H * D)
+    else:
+        out = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype) if out_direct else None
     out_f32 = None
     if need_backward_state or not out_direct:
         out_f32 = torch.empty((B, H, N, D), device=q.device, dtype=torch.float32)
@@ -243,6 +281,8 @@ def hip_simplicial_attention_forward(
         workspace=None if ws is None else ws.data_ptr(), workspace_bytes=ws_bytes,
         batch=B, heads=H, tokens=N, head_dim=D,
         dtype=_native.dtype_code(cdt), precision=_native.MF_PREC[precision],
+        q_stride=(ctypes.c_int64 * 3)(*q_stride), kv_stride=(ctypes.c_int64 * 3)(*kv_stride),
+        out_stride=(ctypes.c_int64 * 3)(*out_stride),
         **ext.fields(),
     )
     with torch.cuda.device(q.device):

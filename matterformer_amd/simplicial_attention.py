@@ -360,8 +360,11 @@ class SimplicialAttention(nn.Module):
             ml, mr = message_residual.left.float(), message_residual.right.float()
             mb = message_basis.to(device=q.device, dtype=torch.float32)
         pv = mask.pair_valid.contiguous() if mask.pair_valid is not None else empty_bool
+        # q, k1, v1, k2, v2 stay the head views of the in_proj output (the reference copies them with
+        # .contiguous() here): the launcher reads them in place through their strides when its kernel
+        # can, and makes the copies itself otherwise
         return _TritonTwoSimplicialAttentionFunction.apply(
-            q.contiguous(), k1.contiguous(), v1.contiguous(), k2.contiguous(), v2.contiguous(),
+            q, k1, v1, k2, v2,
             mask.query_valid.contiguous(), mask.pair_key_valid.contiguous(), pv,
             u.contiguous(), vb.contiguous(), w.contiguous(), gate.contiguous(),
             al.contiguous(), ar_.contiguous(), ag.contiguous(),
