@@ -142,8 +142,9 @@ typedef struct mf_simplicial_fwd_args {
    * out that is the merged [B, N, H, D] layout out_proj reads
    * (_merge_heads).  All three zero: the contiguous [B*H, N, D] layout.
    * Other strides are taken by the pair kernel only (16-bit operands,
-   * head_dim <= 64 and a multiple of 8, tokens <= 512, no angle or message
-   * term, every stride a multiple of 8 and every base 16-byte aligned);
+   * head_dim <= 64 and a multiple of 8, tokens <= 512, no pair_valid, no
+   * angle or message term, every stride a multiple of 8 and below 2^31, every
+   * base 16-byte aligned);
    * calls outside that return MF_ERR_UNSUPPORTED.  out_f32 and lse stay
    * contiguous. */
   int64_t q_stride[3];   /* of q                                          */

@@ -981,11 +981,11 @@ static int simplicial_fwd_impl(const mf_simplicial_fwd_args* a, void* stream) {
   // other shapes) run on the general kernel
   const bool bias_only = a->bias_u != nullptr && a->angle_left == nullptr && a->message_left == nullptr;
   if (has_strides(a)) {
-    if (!pair_ok || (has_extras(a) && !bias_only))
+    if (!pair_ok || has_pv || (has_extras(a) && !bias_only))
       return fail(MF_ERR_UNSUPPORTED,
                   "mf_simplicial_fwd: operand strides other than the contiguous [B*H, N, D] layout are taken by "
                   "the pair kernel only (16-bit operands, head_dim <= 64 and a multiple of 8, tokens <= 512, "
-                  "16-byte aligned bases, no angle or message term)");
+                  "16-byte aligned bases, no pair_valid, no angle or message term)");
     for (const int64_t* st3 : {a->q_stride, a->kv_stride, a->out_stride})
       for (int i = 0; i < 3; ++i)
         if (st3[i] < 0 || st3[i] % 8 != 0)

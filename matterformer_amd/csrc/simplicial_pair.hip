@@ -101,10 +101,11 @@ struct Params {
   const void* bg;
   int bias_dtype;
   // element strides {batch, head, token} of q, of k1 / v1 / k2 / v2, and of out (d is unit-stride);
-  // the contiguous [B*H, N, D] layout unless the caller passed others
-  long long qs_b, qs_h, qs_n;
-  long long ks_b, ks_h, ks_n;
-  long long os_b, os_h, os_n;
+  // the contiguous [B*H, N, D] layout unless the caller passed others.  32-bit (the host refuses larger
+  // ones): the kernel is short of scalar registers, and 64-bit strides cost it more spills.
+  int qs_b, qs_h, qs_n;
+  int ks_b, ks_h, ks_n;
+  int os_b, os_h, os_n;
 };
 
 // The claim counter in the caller's workspace (its own 128-byte line).  It
@@ -645,7 +646,7 @@ __device__ __forceinline__ void pair_loop_n(int nqt, const unsigned char* smem, 
 // loop, so the group is kept small).
 // Zero the output rows of the padded queries of the (b, h) pairs w, w + G,
 // ... (a workgroup's share; rows of CPR 16-byte chunks, DP / 8 of them).
-template <typename T, int DP>
+template <typename T, int DP, bool STR>
 __device__ __forceinline__ void zero_padded_share(const Params& p, const uint32_t* s_info, int w, int G) {
   constexpr int CPR = DP / 8;
   const int N = p.N, D = p.D, H = p.H;
@@ -656,12 +657,14 @@ __device__ __forceinline__ void zero_padded_share(const Params& p, const uint32_
     const bool qpre = (info & kQPre) != 0;
     const int i0 = qpre ? info_nq(info) : 0;  // rows below are valid
     const uint8_t* qrow = p.qv + size_t(b) * N;
-    T* orow0 = p.out ? static_cast<T*>(p.out) + b * p.os_b + h * p.os_h : nullptr;
+    T* orow0 = p.out ? static_cast<T*>(p.out) + (STR ? size_t(b) * p.os_b + size_t(h) * p.os_h : size_t(bh) * N * D)
+                     : nullptr;
+    const size_t osn = STR ? size_t(p.os_n) : size_t(D);
     for (int u = int(threadIdx.x); u < (N - i0) * CPR; u += kThreads) {
       const int i = i0 + u / CPR, cc = u % CPR;
       if (cc >= cpr || (!qpre && qrow[i] != 0)) continue;
       const size_t row = size_t(bh) * N + i;
-      if (p.out) reinterpret_cast<uint4*>(orow0 + i * p.os_n)[cc] = uint4{0u, 0u, 0u, 0u};
+      if (p.out) reinterpret_cast<uint4*>(orow0 + size_t(i) * osn)[cc] = uint4{0u, 0u, 0u, 0u};
       if (p.out_f32) {
         float4* o = reinterpret_cast<float4*>(p.out_f32 + row * D + cc * 8);
         o[0] = float4{0.f, 0.f, 0.f, 0.f};
@@ -683,7 +686,7 @@ __device__ __forceinline__ uint16_t half_bits_sat(float x) {
   return __builtin_bit_cast(uint16_t, _Float16(fminf(fmaxf(x, -65504.0f), 65504.0f)));
 }
 
-template <typename T, int DP, bool HAS_PV, bool MULTI, bool BIAS>
+template <typename T, int DP, bool HAS_PV, bool MULTI, bool BIAS, bool STR>
 __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, int b, int h, int nk, int q0, int nqg,
                                           bool kpre, bool qpre, bool zero_share) {
   constexpr int QT = kMaxQ / 16;       // query tiles held in registers
@@ -706,11 +709,15 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   float* gmax = reinterpret_cast<float*>(smem + Ly::kG);
   int* scal = reinterpret_cast<int*>(smem + Ly::kScal);
   float* s_m = reinterpret_cast<float*>(smem + Ly::kM);
-  const T* gq = static_cast<const T*>(p.q) + b * p.qs_b + h * p.qs_h;
-  const T* gk1 = static_cast<const T*>(p.k1) + b * p.ks_b + h * p.ks_h;
-  const T* gk2 = static_cast<const T*>(p.k2) + b * p.ks_b + h * p.ks_h;
-  const T* gv1 = static_cast<const T*>(p.v1) + b * p.ks_b + h * p.ks_h;
-  const T* gv2 = static_cast<const T*>(p.v2) + b * p.ks_b + h * p.ks_h;
+  // operand strides: the caller's (STR) or those of the contiguous [B*H, N, D] layout
+  const size_t qoff = STR ? size_t(b) * p.qs_b + size_t(h) * p.qs_h : size_t(bh) * N * D;
+  const size_t koff = STR ? size_t(b) * p.ks_b + size_t(h) * p.ks_h : size_t(bh) * N * D;
+  const size_t qsn = STR ? size_t(p.qs_n) : size_t(D), ksn = STR ? size_t(p.ks_n) : size_t(D);
+  const T* gq = static_cast<const T*>(p.q) + qoff;
+  const T* gk1 = static_cast<const T*>(p.k1) + koff;
+  const T* gk2 = static_cast<const T*>(p.k2) + koff;
+  const T* gv1 = static_cast<const T*>(p.v1) + koff;
+  const T* gv2 = static_cast<const T*>(p.v2) + koff;
 
   // staging map: 16-byte chunk u = tid + kThreads i of a row set is row
   // u / CPR, columns 8 cc .. 8 cc + 7 with cc = tid % CPR for every i; only
@@ -736,7 +743,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       const int row = (tid + kThreads * i) / CPR;
       arr[i] = uint4{0u, 0u, 0u, 0u};
       if (i < nI && row < nrows && col_ok)
-        arr[i] = *reinterpret_cast<const uint4*>(base + key_atom(row0 + row) * p.ks_n + e0);
+        arr[i] = *reinterpret_cast<const uint4*>(base + size_t(key_atom(row0 + row)) * ksn + e0);
     }
   };
   uint4 rk1[MAXC], rk2[MAXC], rv1[MAXC], rv2[MAXC], rq[MAXQC];
@@ -780,7 +787,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     for (int i = 0; i < MAXQC; ++i) {
       const int row = (tid + kThreads * i) / CPR;
       rq[i] = (row < nqg && col_ok)
-                  ? *reinterpret_cast<const uint4*>(gq + (qpre ? q0 + row : int(qidx[q0 + row])) * p.qs_n + e0)
+                  ? *reinterpret_cast<const uint4*>(gq + size_t(qpre ? q0 + row : int(qidx[q0 + row])) * qsn + e0)
                   : uint4{0u, 0u, 0u, 0u};
     }
   }
@@ -789,10 +796,10 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     load_block(0, 0);
     // the workgroup's share of padded query rows, stored while the loads are
     // in flight (first unit only)
-    if (zero_share) zero_padded_share<T, DP>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
+    if (zero_share) zero_padded_share<T, DP, STR>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
     acc_max();
   } else {
-    if (zero_share) zero_padded_share<T, DP>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
+    if (zero_share) zero_padded_share<T, DP, STR>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
     for (int rc = 0; rc < nch; ++rc) {
       load_block(rc, rc);
       acc_max();
@@ -1256,8 +1263,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         const T lo = T(o[2 * e]), hi = T(o[2 * e + 1]);
         w[e] = uint32_t(__builtin_bit_cast(uint16_t, lo)) | (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
       }
-      *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + b * p.os_b + h * p.os_h + atom * p.os_n + c8) =
-          uint4{w[0], w[1], w[2], w[3]};
+      const size_t orow = STR ? size_t(b) * p.os_b + size_t(h) * p.os_h + size_t(atom) * p.os_n : row * D;
+      *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + orow + c8) = uint4{w[0], w[1], w[2], w[3]};
     }
     if (p.out_f32) {
       float4* dst = reinterpret_cast<float4*>(p.out_f32 + row * D + c8);
@@ -1434,7 +1441,7 @@ __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* 
 
 // One unit (molecule b, head h, query group g): index lists of non-prefix
 // masks and the attention of the group's queries.  Ends with a barrier.
-template <typename T, int DP, bool HAS_PV, bool BIAS>
+template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
 __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, int b, int h, int g, bool zero_share) {
   using Ly = Lay<DP>;
   const int tid = threadIdx.x;
@@ -1453,8 +1460,8 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
       if (wave == 1 && !qpre) write_ranks(p.qv + size_t(b) * p.N, p.N, qidx, lane);
       __syncthreads();
     }
-    if (nk > kCap) unit_body<T, DP, HAS_PV, true, BIAS>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
-    else unit_body<T, DP, HAS_PV, false, BIAS>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
+    if (nk > kCap) unit_body<T, DP, HAS_PV, true, BIAS, STR>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
+    else unit_body<T, DP, HAS_PV, false, BIAS, STR>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
   }
   __syncthreads();
 }
@@ -1468,7 +1475,7 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
 // finishes a unit claims the next position with one device-scope atomic, so
 // the workgroups that finish first take the longest remaining units.
 // BIAS: one workgroup per CU (its bias operands take another ~59 KB of LDS).
-template <typename T, int DP, bool HAS_PV, bool BIAS>
+template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
 __global__ void __launch_bounds__(kThreads, BIAS ? 1 : 2) simplicial_pair_kernel(Params p) {
   using Ly = Lay<DP>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -1490,7 +1497,7 @@ __global__ void __launch_bounds__(kThreads, BIAS ? 1 : 2) simplicial_pair_kernel
 
   // the rows of padded queries: a static share of (b, h) pairs per
   // workgroup, written during its first unit (or at once without one)
-  if (wg >= total) zero_padded_share<T, DP>(p, s_info, wg, G);
+  if (wg >= total) zero_padded_share<T, DP, STR>(p, s_info, wg, G);
   for (int pos = wg; pos < total;) {
     int b, i;  // molecule, unit within it
     if (pos == wg) {
@@ -1510,7 +1517,7 @@ __global__ void __launch_bounds__(kThreads, BIAS ? 1 : 2) simplicial_pair_kernel
     const uint32_t info = s_info[b];
     const int ng = num_groups(info_nk(info), info_nq(info));
     const int h = div_small(i, ng);
-    run_unit<T, DP, HAS_PV, BIAS>(p, smem, b, h, i - h * ng, pos == wg);  // ends with a barrier: cl->next is read
+    run_unit<T, DP, HAS_PV, BIAS, STR>(p, smem, b, h, i - h * ng, pos == wg);  // ends with a barrier: cl->next is read
     if (tid == 0) {
       if (cl->claimed) {
         cl->claimed = 0;  // the unit claimed the next position
@@ -1525,10 +1532,10 @@ __global__ void __launch_bounds__(kThreads, BIAS ? 1 : 2) simplicial_pair_kernel
   }
 }
 
-template <typename T, int DP, bool HAS_PV, bool BIAS>
+template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
 int launch(const Params& prm, int num_cus, hipStream_t stream) {
   const int grid = std::max(8, (BIAS ? 1 : 2) * num_cus);  // 2 workgroups per CU (1 with the bias)
-  auto kern = simplicial_pair_kernel<T, DP, HAS_PV, BIAS>;
+  auto kern = simplicial_pair_kernel<T, DP, HAS_PV, BIAS, STR>;
   const size_t lds = BIAS ? Lay<DP>::kTotalBias : Lay<DP>::kTotal;
   static bool attr_set = false;  // per instantiation
   if (!attr_set) {
@@ -1578,24 +1585,39 @@ int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* claims, int nu
   prm.bu = a->bias_u; prm.bv = a->bias_v; prm.bw = a->bias_w; prm.bg = a->bias_gate;
   prm.bias_dtype = a->bias_dtype;
   const long long cb = (long long)a->heads * a->tokens * a->head_dim, ch = (long long)a->tokens * a->head_dim;
-  auto strides = [&](const int64_t* st, long long& sb, long long& sh, long long& sn) {
+  bool fits = true;
+  auto strides = [&](const int64_t* st, int& sb, int& sh, int& sn) {
     const bool dflt = st[0] == 0 && st[1] == 0 && st[2] == 0;
-    sb = dflt ? cb : st[0];
-    sh = dflt ? ch : st[1];
-    sn = dflt ? a->head_dim : st[2];
+    const long long v[3] = {dflt ? cb : st[0], dflt ? ch : st[1], dflt ? a->head_dim : st[2]};
+    for (long long x : v) fits = fits && x <= 0x7fffffffLL;
+    sb = int(v[0]);
+    sh = int(v[1]);
+    sn = int(v[2]);
   };
   strides(a->q_stride, prm.qs_b, prm.qs_h, prm.qs_n);
   strides(a->kv_stride, prm.ks_b, prm.ks_h, prm.ks_n);
   strides(a->out_stride, prm.os_b, prm.os_h, prm.os_n);
+  if (!fits) return fail(MF_ERR_UNSUPPORTED, "simplicial pair launch: operand strides must be below 2^31 elements");
   const int g = num_cus;
   const bool pv = a->pair_valid != nullptr;
   const bool bf = a->dtype == MF_DTYPE_BF16;
   const bool bias = a->bias_u != nullptr;
+  // caller strides: their own instantiations (the contiguous ones keep the shape-derived addressing,
+  // which leaves the kernel's scalar registers as they were); none with pair_valid
+  bool strided = false;
+  for (const int64_t* st : {a->q_stride, a->kv_stride, a->out_stride})
+    strided = strided || st[0] != 0 || st[1] != 0 || st[2] != 0;
+  if (strided && pv)
+    return fail(MF_ERR_UNSUPPORTED, "simplicial pair launch: operand strides are not taken together with pair_valid");
   auto go = [&](auto tag, auto dp, auto has_pv) {
     using T = decltype(tag);
     constexpr int DP = decltype(dp)::value;
     constexpr bool PV = decltype(has_pv)::value;
-    return bias ? launch<T, DP, PV, true>(prm, g, stream) : launch<T, DP, PV, false>(prm, g, stream);
+    if constexpr (!PV) {
+      if (strided)
+        return bias ? launch<T, DP, false, true, true>(prm, g, stream) : launch<T, DP, false, false, true>(prm, g, stream);
+    }
+    return bias ? launch<T, DP, PV, true, false>(prm, g, stream) : launch<T, DP, PV, false, false>(prm, g, stream);
   };
   using I32 = std::integral_constant<int, 32>;
   using I64 = std::integral_constant<int, 64>;

@@ -166,14 +166,15 @@ def _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, angle_left, angle_right, 
     return ext
 
 
-def _operand_views(q, k1, v1, k2, v2, cdt, low_rank: bool):
+def _operand_views(q, k1, v1, k2, v2, cdt, excluded: bool):
     """The (q, k/v) {batch, head, token} element strides when the five [B, H, N, D] operands can be read
     in place by the pair kernel (views such as the chunks of an in_proj output), else None (the operands
     are then copied to the contiguous layout).  The pair kernel takes 16-bit operands already in the
-    compute dtype, head_dim <= 64 and a multiple of 8, tokens <= 512, no angle or message term, unit-stride
-    d, strides that are multiples of 8 elements and 16-byte aligned bases; k1, v1, k2 and v2 share strides."""
+    compute dtype, head_dim <= 64 and a multiple of 8, tokens <= 512, no pair_valid and no angle or message
+    term (`excluded`), unit-stride d, strides that are multiples of 8 elements below 2^31 and 16-byte
+    aligned bases; k1, v1, k2 and v2 share strides."""
     B, H, N, D = q.shape
-    if low_rank or cdt not in (torch.float16, torch.bfloat16) or D % 8 != 0 or D > 64 or N > 512:
+    if excluded or cdt not in (torch.float16, torch.bfloat16) or D % 8 != 0 or D > 64 or N > 512:
         return None
     ts = (q, k1, v1, k2, v2)
     if all(t.is_contiguous() for t in ts):
@@ -184,7 +185,7 @@ def _operand_views(q, k1, v1, k2, v2, cdt, low_rank: bool):
     kvs = tuple(k1.stride()[:3])
     if any(tuple(t.stride()[:3]) != kvs for t in (v1, k2, v2)):
         return None
-    if any(x < 0 or x % 8 != 0 for x in qs + kvs):
+    if any(x < 0 or x % 8 != 0 or x >= 2**31 for x in qs + kvs + (N * H * D, H * D)):
         return None
     return qs, kvs
 
@@ -238,7 +239,8 @@ def hip_simplicial_attention_forward(
         raise RuntimeError(f"the HIP backend only supports float16/bfloat16/float32 inputs, got {q.dtype}")
 
     cdt = _compute_dtype(q.dtype, precision)
-    views = _operand_views(q, k1, v1, k2, v2, cdt, angle_left is not None or message_left is not None)
+    views = _operand_views(q, k1, v1, k2, v2, cdt,
+                           angle_left is not None or message_left is not None or pair_valid is not None)
     if views is not None:
         ops = [q, k1, v1, k2, v2]
         q_stride, kv_stride = views

@@ -197,3 +197,27 @@ def test_bias_batch_slices_read_their_own_molecules():
     for n, b in enumerate(pick):
         err = float(np.linalg.norm(got[n] - ref[n]) / max(np.linalg.norm(ref[n]), 1e-30))
         assert err <= 2e-2, (b, err)
+
+
+def test_views_with_pair_valid_fall_back_to_copies():
+    """Strided operands are not taken together with pair_valid: the launcher copies the views instead, and
+    a direct C-ABI call with both is refused."""
+    B, H, N, D = 2, 4, 33, 64
+    q, k1, v1, k2, v2 = _views(B, H, N, D, torch.bfloat16, seed=17)
+    qv, pkv = _masks(B, N, seed=4)
+    gen = torch.Generator().manual_seed(18)
+    pv = (torch.rand(B, N, N, generator=gen) > 0.3).to(DEV)
+    kw = dict(query_valid=qv, pair_key_valid=pkv, pair_valid=pv, precision="bf16_tc")
+    out_v, lse_v, _ = hip_simplicial_attention_forward(q, k1, v1, k2, v2, **kw)
+    out_c, lse_c, _ = hip_simplicial_attention_forward(*(t.contiguous() for t in (q, k1, v1, k2, v2)), **kw)
+    torch.cuda.synchronize()
+    assert out_v.is_contiguous()  # the copies' contiguous output layout
+    assert torch.equal(out_v, out_c) and torch.equal(lse_v, lse_c)
+
+    qc = q.contiguous()
+    out = torch.empty_like(qc)
+    lib, args, keep = _capi_args(qc, (H * N * D, N * D, D), out, _native.MF_DTYPE_BF16)
+    args.pair_valid = pv.data_ptr()
+    status = lib.mf_simplicial_fwd(args, _native.current_stream(DEV))
+    assert status == _native.MF_ERR_UNSUPPORTED
+    assert b"no pair_valid" in lib.mf_last_error()
