@@ -12,8 +12,8 @@
 // plain attention over nk^2 keys whose tiles are formed on the fly.
 //
 // One launch.  A persistent grid of 2 workgroups per CU; each workgroup
-// first copies every molecule's two byte masks (valid keys, valid queries)
-// into LDS and scans them, ranks the molecules by cost and enumerates the
+// first scans every molecule's two byte masks (valid keys, valid queries)
+// straight from global memory, ranks the molecules by cost and enumerates the
 // units (molecule b, head h, query group g) in that order, longest first --
 // every workgroup derives the same list.  Workgroup w takes position w;
 // after that a workgroup that finishes a unit claims the next position with
