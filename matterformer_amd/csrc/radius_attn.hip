@@ -328,10 +328,17 @@ __global__ void __launch_bounds__(kThreads) radius_attn_kernel(Params p) {
 constexpr int kThreads2 = 512;
 
 // POS: scale > 0.  The running maximum is then taken over the unscaled
-// masked logits (scaling preserves the order) and p = exp2(s scale - m) is
-// one fma per logit.
-template <typename T, int D, bool POS>
-__global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p) {
+// masked logits (scaling preserves the order), p = exp2(s scale - m) is one
+// fma per logit, the mask enters as the logit accumulator's start value and
+// the row sum is an MFMA with a ones operand.
+//
+// QW: 16-query tiles per wave (1 or 2).  A workgroup covers 64 QW queries;
+// with QW = 2 every K and V operand read from LDS feeds two query tiles (half
+// the LDS reads per query), and the workgroup's key tiles are those active in
+// either of its two 64-query block rows (a key tile none of a query's keys
+// are allowed in adds exactly 0 to that query's sums).
+template <typename T, int D, bool POS, int QW>
+__global__ void __launch_bounds__(kThreads2, 3 - QW) radius_attn_pair_kernel(Params p) {
   using Op8 = typename Ops<T>::Op8;
   typedef __attribute__((__vector_size__(4 * sizeof(T)))) T Op4;
   constexpr int KS = D + 8;         // K row stride in LDS (elements)
@@ -340,26 +347,37 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
   constexpr int CPR = D / 8;        // 16-byte chunks per row
   constexpr int CPT = kTile * CPR / 256;  // chunks per thread per tile (256 threads per stream)
   static_assert(CPT >= 1 && (kTile * CPR) % 256 == 0, "staging shape");
-  constexpr int CW = ND * 4 + 2;    // floats per lane in the combine: O^T, m, l
-  static_assert(4 * 64 * CW * 4 <= int(sizeof(T)) * 2 * 2 * kTile * KS, "combine area");
+  static_assert(QW == 1 || QW == 2, "query tiles per wave");
+  constexpr int QT = 64 * QW;       // queries per workgroup
+  constexpr int CW = ND * 4 + 2;    // floats per lane and query tile in the combine: O^T, m, l
+  static_assert(4 * 64 * QW * CW * 4 <= int(sizeof(T)) * 2 * 2 * kTile * KS, "combine area");
 
   __shared__ __attribute__((aligned(16))) T Ks[2][2][kTile * KS];  // [buffer][stream]
   __shared__ __attribute__((aligned(16))) T Vs[2][2][kTile * KS];  // V row-major, read transposed
   __shared__ int s_tiles[2][kMaxTiles / 2];  // active tiles of each parity, in order
   __shared__ int s_ntiles[2];
+  // POS: entry n holds the start of a logit accumulator for mask nibble n
+  // (component r: 0 if bit r is set, else -inf)
+  __shared__ mf_f32x4 s_lut[16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
   const int kh = wave >> 2, qw = wave & 3;  // key stream, query group
   const int ht = tid & 255;                 // thread index within the stream
+  if (POS && tid < 16) {
+    mf_f32x4 e;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e[r] = ((tid >> r) & 1) ? 0.0f : -INFINITY;
+    s_lut[tid] = e;
+  }
   const int G = gridDim.x;
   const int unit = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);  // XCD-aware order
   if (unit >= p.units) return;  // grid padding (whole workgroup)
-  const int NQT = p.NB;
+  const int N = p.N;
+  const int NQT = (N + QT - 1) / QT;
   const int qt = unit % NQT;
   const int h = (unit / NQT) % p.H;
   const int b = unit / (NQT * p.H);
-  const int N = p.N;
   const size_t bh = size_t(b) * p.H + h;
   const T* gq = static_cast<const T*>(p.q) + bh * N * D;
   const T* gk = static_cast<const T*>(p.k) + bh * N * D;
@@ -367,11 +385,14 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
 
   if (wave < 2) {
     // wave e lists the active tiles of parity e: lane l looks at tile 2 (base + l) + e
-    const uint8_t* brow = p.block_mask ? p.block_mask + (size_t(b) * p.NB + qt) * p.NB : nullptr;
+    const int br = qt * QW;  // first 64-query block row of the workgroup
+    const uint8_t* brow = p.block_mask ? p.block_mask + (size_t(b) * p.NB + br) * p.NB : nullptr;
+    const bool two = QW == 2 && br + 1 < p.NB;
     int n = 0;
     for (int base = 0; 2 * base < p.NB; base += 64) {
       const int jt = 2 * (base + lane) + wave;
-      const bool on = jt < p.NB && (!brow || brow[jt] != 0);
+      bool on = jt < p.NB;
+      if (on && brow) on = brow[jt] != 0 || (two && brow[p.NB + jt] != 0);
       const uint64_t bal = __ballot(on);
       if (on) s_tiles[wave][n + __popcll(bal & ((1ull << lane) - 1))] = jt;
       n += __popcll(bal);
@@ -379,18 +400,35 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
     if (lane == 0) s_ntiles[wave] = n;
   }
 
-  const int qi = qt * kTile + qw * 16 + r16;
-  const bool q_in = qi < N;
-  Op8 qb[DK];
+  int qi[QW];
+  bool q_in[QW];
+  Op8 qb[QW][DK];
+  const uint32_t* qbits[QW];
 #pragma unroll
-  for (int kk = 0; kk < DK; ++kk)
-    qb[kk] = *reinterpret_cast<const Op8*>(gq + size_t(min(qi, N - 1)) * D + 32 * kk + 8 * g);
-  const uint32_t* qbits = p.bits + size_t(b) * N * p.W + size_t(q_in ? qi : 0) * p.W;
+  for (int t = 0; t < QW; ++t) {
+    qi[t] = qt * QT + (qw * QW + t) * 16 + r16;
+    q_in[t] = qi[t] < N;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk)
+      qb[t][kk] = *reinterpret_cast<const Op8*>(gq + size_t(min(qi[t], N - 1)) * D + 32 * kk + 8 * g);
+    qbits[t] = p.bits + size_t(b) * N * p.W + size_t(q_in[t] ? qi[t] : 0) * p.W;
+  }
 
-  mf_f32x4 acc[ND];
+  mf_f32x4 acc[QW][ND];
+  float m[QW], l[QW];
+  // POS: every component of lacc[t] is the sum over the keys seen so far
+  mf_f32x4 lacc[QW];
 #pragma unroll
-  for (int nd = 0; nd < ND; ++nd) acc[nd] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.0f;
+  for (int t = 0; t < QW; ++t) {
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd) acc[t][nd] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+    m[t] = -INFINITY;
+    l[t] = 0.0f;
+    lacc[t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  Op8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = T(1.0f);
 
   __syncthreads();
   const int ntiles = s_ntiles[kh];  // this stream's
@@ -411,18 +449,21 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
   }
   struct Stage {
     Op8 k[CPT], v[CPT];
-    uint32_t m0, m1;  // mask words as loaded
-    uint32_t mok;     // bit 0 / 1: m0 / m1 are real words of a real query
-    int key0;         // first key of the tile
-    bool full;        // every key of the tile is < N (uniform)
+    uint32_t m0[QW], m1[QW];  // mask words as loaded
+    uint32_t mok[QW];         // bit 0 / 1: m0 / m1 are real words of a real query
+    int key0;                 // first key of the tile
+    bool full;                // every key of the tile is < N (uniform)
   };
   auto load_tile = [&](int jt, Stage& st) {
     // the words are selected when used (a step later), so that nothing
     // waits for these loads now
     const int w0 = 2 * jt;
-    st.m0 = qbits[min(w0, p.W - 1)];
-    st.m1 = qbits[min(w0 + 1, p.W - 1)];
-    st.mok = (q_in && w0 < p.W ? 1u : 0u) | (q_in && w0 + 1 < p.W ? 2u : 0u);
+#pragma unroll
+    for (int t = 0; t < QW; ++t) {
+      st.m0[t] = qbits[t][min(w0, p.W - 1)];
+      st.m1[t] = qbits[t][min(w0 + 1, p.W - 1)];
+      st.mok[t] = (q_in[t] && w0 < p.W ? 1u : 0u) | (q_in[t] && w0 + 1 < p.W ? 2u : 0u);
+    }
     const int key0 = jt * kTile;
     st.key0 = key0;
     st.full = key0 + kTile <= N;
@@ -471,80 +512,132 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
   // the loads of step s + 1 (issued after the previous step's store) and
   // goes to the other buffer at the end of the step.
   Stage st;
-  uint32_t mw0 = 0u, mw1 = 0u;
+  uint32_t mw0[QW], mw1[QW];
+#pragma unroll
+  for (int t = 0; t < QW; ++t) mw0[t] = mw1[t] = 0u;
+  auto take_words = [&](const Stage& x) {
+#pragma unroll
+    for (int t = 0; t < QW; ++t) {
+      mw0[t] = (x.mok[t] & 1u) ? x.m0[t] : 0u;
+      mw1[t] = (x.mok[t] & 2u) ? x.m1[t] : 0u;
+    }
+  };
   if (nsteps > 0) {
     if (0 < ntiles) {
       load_tile(tiles[0], st);
       store_tile(st, 0);
-      mw0 = (st.mok & 1u) ? st.m0 : 0u;
-      mw1 = (st.mok & 2u) ? st.m1 : 0u;
+      take_words(st);
     }
+    // Every global load issued so far (q, the first tile) is complete here on
+    // every path.  Without this wait the path that skips the first tile
+    // leaves the q loads pending into the loop, and the wait placed before
+    // the loop's first use of q then also waits for the next tile's loads,
+    // at the start of every step.  (vmcnt(0); expcnt and lgkmcnt unchanged.)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     if (1 < ntiles) load_tile(tiles[1], st);
     __syncthreads();
   }
+  const float sc = p.scale_log2;
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s & 1;
     if (s < ntiles) {
       const T* Kt = Ks[buf][kh];
       const T* Vt = Vs[buf][kh];
-      float sv[4][4];
+      float sv[QW][4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        mf_f32x4 c = {0.f, 0.f, 0.f, 0.f};
+        mf_f32x4 c[QW];
+#pragma unroll
+        for (int t = 0; t < QW; ++t) {
+          // key 16 kt + 4 g + r is bit 16 (kt & 1) + r of (word kt / 2) >> 4 g
+          c[t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (POS) c[t] = s_lut[(((kt < 2 ? mw0[t] : mw1[t]) >> (4 * g)) >> (16 * (kt & 1))) & 15u];
+        }
 #pragma unroll
         for (int kk = 0; kk < DK; ++kk) {
           const Op8 a = *reinterpret_cast<const Op8*>(Kt + (16 * kt + r16) * KS + 32 * kk + 8 * g);
-          c = Ops<T>::mma(a, qb[kk], c);
+#pragma unroll
+          for (int t = 0; t < QW; ++t) c[t] = Ops<T>::mma(a, qb[t][kk], c[t]);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sv[kt][r] = c[r];
+        for (int t = 0; t < QW; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sv[t][kt][r] = c[t][r];
       }
-      const float sc = p.scale_log2;
-      float tmax = -INFINITY;
-      // key 16 kt + 4 g + r is bit 16 (kt & 1) + r of (word kt / 2) >> 4 g
-      const uint32_t wa = mw0 >> (4 * g), wb = mw1 >> (4 * g);
+      Op8 pb[QW][2];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int t = 0; t < QW; ++t) {
+        float tmax = -INFINITY;
+        if constexpr (POS) {
+          // this lane's maximum only; the query's (over its 4 lanes) is
+          // formed when some lane of the wave may move its offset
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool allowed = (((kt < 2 ? wa : wb) >> (16 * (kt & 1) + r)) & 1u) != 0u;
-          if constexpr (POS) sv[kt][r] = allowed ? sv[kt][r] : -INFINITY;
-          else sv[kt][r] = allowed ? sv[kt][r] * sc : -INFINITY;
-          tmax = fmaxf(tmax, sv[kt][r]);
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sv[t][kt][r]);
+          tmax *= sc;  // -inf stays -inf
+          if (__ballot(tmax > m[t] + 8.0f) != 0ull) {
+            const auto r16s = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+            tmax = fmaxf(__uint_as_float(r16s[0]), __uint_as_float(r16s[1]));
+            const auto r32s = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+            tmax = fmaxf(__uint_as_float(r32s[0]), __uint_as_float(r32s[1]));
+            const bool grow = tmax > m[t] + 8.0f;  // the same for the 4 lanes of a query
+            const float m_set = grow ? tmax : m[t];
+            const float alpha = grow ? fast_exp2(m[t] - m_set) : 1.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) lacc[t][r] *= alpha;
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[t][nd][r] *= alpha;
+            m[t] = m_set;
+          }
+        } else {
+          const uint32_t wa = mw0[t] >> (4 * g), wb = mw1[t] >> (4 * g);
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const bool allowed = (((kt < 2 ? wa : wb) >> (16 * (kt & 1) + r)) & 1u) != 0u;
+              sv[t][kt][r] = allowed ? sv[t][kt][r] * sc : -INFINITY;
+              tmax = fmaxf(tmax, sv[t][kt][r]);
+            }
+          }
+          const auto r16s = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+          tmax = fmaxf(__uint_as_float(r16s[0]), __uint_as_float(r16s[1]));
+          const auto r32s = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+          tmax = fmaxf(__uint_as_float(r32s[0]), __uint_as_float(r32s[1]));
+          // lazy offset, as in the kernel above
+          const bool grow = tmax > m[t] + 8.0f;
+          if (__ballot(grow) != 0ull) {
+            const float m_set = grow ? tmax : m[t];
+            const float alpha = grow ? fast_exp2(m[t] - m_set) : 1.0f;
+            l[t] *= alpha;
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[t][nd][r] *= alpha;
+            m[t] = m_set;
+          }
+        }
+        const float m_off = m[t] == -INFINITY ? 0.0f : m[t];
+        float psum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pv = POS ? fast_exp2(fmaf(sv[t][kt][r], sc, -m_off)) : fast_exp2(sv[t][kt][r] - m_off);
+            if constexpr (!POS) psum += pv;
+            pb[t][kt >> 1][(kt & 1) * 4 + r] = T(pv);
+          }
+        }
+        if constexpr (POS) {
+          lacc[t] = Ops<T>::mma(ones, pb[t][0], lacc[t]);
+          lacc[t] = Ops<T>::mma(ones, pb[t][1], lacc[t]);
+        } else {
+          l[t] += psum;
         }
       }
-      {
-        const auto r16s = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-        tmax = fmaxf(__uint_as_float(r16s[0]), __uint_as_float(r16s[1]));
-        const auto r32s = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-        tmax = fmaxf(__uint_as_float(r32s[0]), __uint_as_float(r32s[1]));
-      }
-      if constexpr (POS) tmax *= sc;  // -inf stays -inf
-      // lazy offset, as in the kernel above
-      const bool grow = tmax > m + 8.0f;
-      if (__ballot(grow) != 0ull) {
-        const float m_set = grow ? tmax : m;
-        const float alpha = grow ? fast_exp2(m - m_set) : 1.0f;
-        l *= alpha;
-#pragma unroll
-        for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[nd][r] *= alpha;
-        m = m_set;
-      }
-      const float m_off = m == -INFINITY ? 0.0f : m;
-      float psum = 0.0f;
-      Op8 pb[2];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pv = POS ? fast_exp2(fmaf(sv[kt][r], sc, -m_off)) : fast_exp2(sv[kt][r] - m_off);
-          psum += pv;
-          pb[kt >> 1][(kt & 1) * 4 + r] = T(pv);
-        }
-      }
-      l += psum;
       // V^T operands straight from the row-major tile: within each group of
       // 16 lanes, ds_read_b64_tr_b16 hands lane 4a + c element c of the
       // 8-byte pieces addressed by lanes 4e + a (e = 0..3).  Lane 4e + a
@@ -560,58 +653,73 @@ __global__ void __launch_bounds__(kThreads2, 2) radius_attn_pair_kernel(Params p
           const Op4 lo = read_tr16<T>(vp);
           const Op4 hi = read_tr16<T>(vp + 16 * KS);
           const Op8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          acc[nd] = Ops<T>::mma(a, pb[pr], acc[nd]);
+#pragma unroll
+          for (int t = 0; t < QW; ++t) acc[t][nd] = Ops<T>::mma(a, pb[t][pr], acc[t][nd]);
         }
       }
     }
     if (s + 1 < ntiles) {
       store_tile(st, buf ^ 1);
-      mw0 = (st.mok & 1u) ? st.m0 : 0u;
-      mw1 = (st.mok & 2u) ? st.m1 : 0u;
+      take_words(st);
     }
     __syncthreads();
     if (s + 2 < ntiles) load_tile(tiles[s + 2], st);
   }
 
-  // combine the streams: l summed over the 4 key groups g first
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  float* cmb = reinterpret_cast<float*>(&Ks[0][0][0]);  // [query group][lane][CW] (after the last barrier)
+  // combine the streams: l summed over the 4 key groups g first (POS: the
+  // MFMA row sum already holds every key)
+#pragma unroll
+  for (int t = 0; t < QW; ++t) {
+    if constexpr (POS) {
+      l[t] = lacc[t][0];
+    } else {
+      l[t] += __shfl_xor(l[t], 16, 64);
+      l[t] += __shfl_xor(l[t], 32, 64);
+    }
+  }
+  float* cmb = reinterpret_cast<float*>(&Ks[0][0][0]);  // [query group][lane][QW][CW] (after the last barrier)
   if (kh == 1) {
-    float* c = cmb + (qw * 64 + lane) * CW;
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
+    for (int t = 0; t < QW; ++t) {
+      float* c = cmb + ((qw * 64 + lane) * QW + t) * CW;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) c[nd * 4 + r] = acc[nd][r];
-    c[ND * 4] = m;
-    c[ND * 4 + 1] = l;
+      for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) c[nd * 4 + r] = acc[t][nd][r];
+      c[ND * 4] = m[t];
+      c[ND * 4 + 1] = l[t];
+    }
   }
   __syncthreads();
-  if (kh == 1 || !q_in) return;
-  const float* c = cmb + (qw * 64 + lane) * CW;
-  const float m1 = c[ND * 4], l1 = c[ND * 4 + 1];
-  const float M = fmaxf(m, m1);
-  const float a0 = M == -INFINITY ? 0.0f : fast_exp2(m - M);  // 0 for a stream without allowed keys
-  const float a1 = M == -INFINITY ? 0.0f : fast_exp2(m1 - M);
-  const float L = a0 * l + a1 * l1;
-  const bool has = L > 0.0f;
-  const float inv = has ? 1.0f / L : 0.0f;
-  const size_t row = bh * N + qi;
+  if (kh == 1) return;
 #pragma unroll
-  for (int nd = 0; nd < ND; ++nd) {
-    const int d0 = 16 * nd + 4 * g;
-    float o[4];
+  for (int t = 0; t < QW; ++t) {
+    if (!q_in[t]) continue;
+    const float* c = cmb + ((qw * 64 + lane) * QW + t) * CW;
+    const float m1 = c[ND * 4], l1 = c[ND * 4 + 1];
+    const float M = fmaxf(m[t], m1);
+    const float a0 = M == -INFINITY ? 0.0f : fast_exp2(m[t] - M);  // 0 for a stream without allowed keys
+    const float a1 = M == -INFINITY ? 0.0f : fast_exp2(m1 - M);
+    const float L = a0 * l[t] + a1 * l1;
+    const bool has = L > 0.0f;
+    const float inv = has ? 1.0f / L : 0.0f;
+    const size_t row = bh * N + qi[t];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = (a0 * acc[nd][r] + a1 * c[nd * 4 + r]) * inv;
-    if (p.out) {
-      Op4 ov;
+    for (int nd = 0; nd < ND; ++nd) {
+      const int d0 = 16 * nd + 4 * g;
+      float o[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ov[r] = T(o[r]);
-      *reinterpret_cast<Op4*>(static_cast<T*>(p.out) + row * D + d0) = ov;
+      for (int r = 0; r < 4; ++r) o[r] = (a0 * acc[t][nd][r] + a1 * c[nd * 4 + r]) * inv;
+      if (p.out) {
+        Op4 ov;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ov[r] = T(o[r]);
+        *reinterpret_cast<Op4*>(static_cast<T*>(p.out) + row * D + d0) = ov;
+      }
+      if (p.out_f32) *reinterpret_cast<float4*>(p.out_f32 + row * D + d0) = float4{o[0], o[1], o[2], o[3]};
     }
-    if (p.out_f32) *reinterpret_cast<float4*>(p.out_f32 + row * D + d0) = float4{o[0], o[1], o[2], o[3]};
+    if (p.lse && g == 0) p.lse[row] = has ? (M + __log2f(L)) * kLn2 : 0.0f;
   }
-  if (p.lse && g == 0) p.lse[row] = has ? (M + __log2f(L)) * kLn2 : 0.0f;
 }
 
 template <typename T, int D>
@@ -622,13 +730,22 @@ int launch(const Params& p, hipStream_t stream) {
   return MF_OK;
 }
 
+// Two query tiles per wave once a (cell, head) spans more than three 64-query
+// tiles (the 128-query workgroups then waste at most a quarter of a tile's
+// queries to padding) and the launch still has a workgroup per CU.
 template <typename T, int D>
 int launch_pair(const Params& p, hipStream_t stream) {
-  const dim3 grid((p.units + 7) / 8 * 8);
-  if (p.scale_log2 > 0.0f)
-    hipLaunchKernelGGL((radius_attn_pair_kernel<T, D, true>), grid, dim3(kThreads2), 0, stream, p);
-  else
-    hipLaunchKernelGGL((radius_attn_pair_kernel<T, D, false>), grid, dim3(kThreads2), 0, stream, p);
+  const bool wide = p.N > 3 * kTile && (long long)p.B * p.H * ((p.N + 2 * kTile - 1) / (2 * kTile)) >= 256;
+  Params q = p;
+  if (wide) q.units = p.B * p.H * ((p.N + 2 * kTile - 1) / (2 * kTile));
+  const dim3 grid((q.units + 7) / 8 * 8);
+  if (p.scale_log2 > 0.0f) {
+    if (wide) hipLaunchKernelGGL((radius_attn_pair_kernel<T, D, true, 2>), grid, dim3(kThreads2), 0, stream, q);
+    else hipLaunchKernelGGL((radius_attn_pair_kernel<T, D, true, 1>), grid, dim3(kThreads2), 0, stream, q);
+  } else {
+    if (wide) hipLaunchKernelGGL((radius_attn_pair_kernel<T, D, false, 2>), grid, dim3(kThreads2), 0, stream, q);
+    else hipLaunchKernelGGL((radius_attn_pair_kernel<T, D, false, 1>), grid, dim3(kThreads2), 0, stream, q);
+  }
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
 }

@@ -339,6 +339,80 @@ def test_radius_attention_matches_fp64_masked_softmax(cuda, B, H, N, D, dtype, u
     assert terr <= tol, terr
 
 
+@pytest.mark.parametrize("scale", [0.6, -0.3, 0.0])
+def test_radius_attention_moving_offset_and_scale_sign(cuda, scale):
+    """Key norms grow along the row (later key tiles hold larger logits), so the
+    running offset moves several times; scale > 0 runs the table-masked path,
+    scale <= 0 the select-masked one."""
+    print(f"radius_attn moving offset scale={scale}", flush=True)
+    B, H, N, D = 2, 2, 300, 64
+    q, k, v, mask = _attn_case(B, H, N, D, seed=41, density=0.3, empty_rows=2)
+    k = k * (1.0 + torch.arange(N, dtype=torch.float32) / 16.0)[None, None, :, None]
+    bits, blocks = _pack(mask)
+    ops = [t.to(torch.bfloat16) for t in (q, k, v)]
+    out, lse, out32 = radius_attention(*(t.to(cuda) for t in ops), bits.to(cuda), blocks.to(cuda), scale=scale,
+                                       return_lse=True, return_fp32=True)
+    ref, ref_lse = masked_attention_fp64(*(t.double().numpy() for t in ops), mask.numpy(), scale)
+    got = out32.cpu().double().numpy()
+    err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert err <= 2e-2, err
+    rel_lse = np.abs(lse.cpu().numpy() - ref_lse) / np.maximum(1.0, np.abs(ref_lse))
+    assert rel_lse.max() <= 2e-2, rel_lse.max()
+    assert (out32[0, :, -2:] == 0).all() and (lse[0, :, -2:] == 0).all()
+
+
+# Shapes with more than three 64-query tiles and at least 256 workgroups of
+# 128 queries: the launch gives each wave two query tiles.
+WIDE_CASES = [
+    # B, H, N, D, dtype, use_block_mask, empty_rows, scale
+    (4, 16, 450, 64, torch.bfloat16, True, 3, None),
+    (8, 16, 300, 32, torch.float16, False, 0, None),
+    (4, 16, 450, 64, torch.bfloat16, True, 2, -0.2),
+    (4, 16, 257, 64, torch.float16, True, 0, 0.9),
+]
+
+
+@pytest.mark.parametrize("B,H,N,D,dtype,use_blocks,empty,scale", WIDE_CASES)
+def test_radius_attention_two_query_tiles_per_wave(cuda, B, H, N, D, dtype, use_blocks, empty, scale):
+    print(f"radius_attn wide B={B} H={H} N={N} D={D} {dtype} blocks={use_blocks} empty={empty} scale={scale}",
+          flush=True)
+    q, k, v, mask = _attn_case(B, H, N, D, seed=N + D + 7, empty_rows=empty)
+    bits, blocks = _pack(mask)
+    ops = [t.to(dtype) for t in (q, k, v)]
+    sc = D ** -0.5 if scale is None else scale
+    out, lse, out32 = radius_attention(*(t.to(cuda) for t in ops), bits.to(cuda),
+                                       blocks.to(cuda) if use_blocks else None, scale=sc, return_lse=True,
+                                       return_fp32=True)
+    ref, ref_lse = masked_attention_fp64(*(t.double().numpy() for t in ops), mask.numpy(), sc)
+    tol = 2e-2 if dtype == torch.bfloat16 else 5e-3
+    got = out32.cpu().double().numpy()
+    err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert err <= tol, err
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=3e-2, rtol=0)
+    torch.testing.assert_close(out.cpu().float(), out32.cpu().to(dtype).float(), rtol=0, atol=0)
+    if empty:
+        assert (out32[0, :, -empty:] == 0).all() and (lse[0, :, -empty:] == 0).all()
+
+
+def test_radius_attention_two_query_tiles_block_skipping_is_exact(cuda):
+    """A banded mask whose two 64-query block rows of a workgroup differ: the
+    workgroup walks the union of their active tiles, and the result equals the
+    one without a block mask bit for bit."""
+    B, H, N, D = 4, 16, 512, 64
+    q, k, v, _ = _attn_case(B, H, N, D, seed=9)
+    i = torch.arange(N)
+    mask = ((i[:, None] - i[None, :]).abs() <= 40)[None].expand(B, N, N).contiguous()
+    bits, blocks = _pack(mask)
+    assert blocks.float().mean() < 0.5
+    ops = [t.to(torch.bfloat16).to(cuda) for t in (q, k, v)]
+    a = radius_attention(*ops, bits.to(cuda), blocks.to(cuda), return_fp32=True)[1]
+    b = radius_attention(*ops, bits.to(cuda), None, return_fp32=True)[1]
+    assert torch.equal(a, b)
+    ref, _ = masked_attention_fp64(*(t.double().cpu().numpy() for t in ops), mask.numpy(), D ** -0.5)
+    err = np.linalg.norm(a.cpu().double().numpy() - ref) / np.linalg.norm(ref)
+    assert err <= 2e-2, err
+
+
 def test_radius_attention_block_skipping_is_exact(cuda):
     q, k, v, _ = _attn_case(1, 2, 256, 64, seed=5)
     # a banded mask: only tiles near the diagonal are active
