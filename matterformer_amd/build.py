@@ -45,6 +45,11 @@ PER_FILE_FLAGS = {
     "geometry.hip": ["-ffp-contract=off"],
     "token_rows.hip": ["-ffp-contract=off"],
     "pair_mlp.hip": ["-ffp-contract=off"],
+    # The pair kernel's unit claim is one lane's atomicAdd whose result is
+    # needed only after the unit's output is written.  The atomic optimizer
+    # would rewrite it into a wave-wide form that reads the result at once,
+    # so the output phase would wait out the atomic's round trip.
+    "simplicial_pair.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
 }
 
 

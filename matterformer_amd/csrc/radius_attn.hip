@@ -522,21 +522,19 @@ __global__ void __launch_bounds__(kThreads2, 3 - QW) radius_attn_pair_kernel(Par
       mw1[t] = (x.mok[t] & 2u) ? x.m1[t] : 0u;
     }
   };
-  if (nsteps > 0) {
-    if (0 < ntiles) {
-      load_tile(tiles[0], st);
-      store_tile(st, 0);
-      take_words(st);
-    }
-    // Every global load issued so far (q, the first tile) is complete here on
-    // every path.  Without this wait the path that skips the first tile
-    // leaves the q loads pending into the loop, and the wait placed before
-    // the loop's first use of q then also waits for the next tile's loads,
-    // at the start of every step.  (vmcnt(0); expcnt and lgkmcnt unchanged.)
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    if (1 < ntiles) load_tile(tiles[1], st);
-    __syncthreads();
+  if (0 < ntiles) {
+    load_tile(tiles[0], st);
+    store_tile(st, 0);
+    take_words(st);
   }
+  // Every global load issued so far (q, the first tile) is complete here, on
+  // every path.  Were a path to reach the loop with the q loads pending (a
+  // stream without tiles), the wait the compiler places before the loop's
+  // first use of q would also wait for the next tile's loads, at the start
+  // of every step.  (vmcnt(0); expcnt and lgkmcnt unchanged.)
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  if (1 < ntiles) load_tile(tiles[1], st);
+  __syncthreads();
   const float sc = p.scale_log2;
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s & 1;
