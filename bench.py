@@ -326,7 +326,7 @@ def measure_radius(cpu_sample: int) -> dict:
         "attn_valid_gflop": round(w.attention_flops(pairs) / 1e9, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": committed_traffic("radius_attn_c4"),
-                     "kernel": "mf::rattn::radius_attn_pair_kernel<bf16, 64, true>", "kernel_ms": round(attn_ms, 5),
+                     "kernel": "mf::rattn::radius_attn_pair_kernel<bf16, 64, POS=true, QW=2>", "kernel_ms": round(attn_ms, 5),
                      "algorithmic_bytes": attn_bytes},
         "cpu_baseline": cpu,
     }
