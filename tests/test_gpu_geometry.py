@@ -168,6 +168,24 @@ def test_knn_code_kernel_matches_oracle(cuda, B, N, k, pad_kind, excl):
     np.testing.assert_array_equal(dist[rows].cpu().numpy().view(np.uint32), rdist.view(np.uint32))
 
 
+@pytest.mark.parametrize("B,k", [(256, 16), (512, 16), (1024, 16), (256, 8), (512, 8), (1024, 8)])
+def test_knn_block_kernel_lane_counts_match_oracle(cuda, B, k):
+    """On 256 CUs the launcher gives each query 8, 4 or 2 lanes for 46 k, 93 k and 185 k queries (B = 256,
+    512, 1024 molecules of 181 atoms): every lane count's butterfly merge, bit for bit against the oracle on
+    a sample of molecules."""
+    print(f"knn lane counts B={B} k={k}", flush=True)
+    N = 181
+    gen = torch.Generator().manual_seed(3100 + B + k)
+    coords = torch.randn(B, N, 3, generator=gen) * math.sqrt(2.0)
+    pad = torch.rand(B, N, generator=gen) < 0.1
+    idx, dist = knn_graph(coords.to(cuda), k, pad.to(cuda), exclude_self=True)
+    torch.cuda.synchronize()
+    rows = list(range(0, B, 37)) + [B - 1]
+    ridx, rdist = oracle_knn(coords[rows].numpy(), k, pad[rows].numpy(), exclude_self=True)
+    np.testing.assert_array_equal(idx[rows].cpu().numpy(), ridx)
+    np.testing.assert_array_equal(dist[rows].cpu().numpy().view(np.uint32), rdist.view(np.uint32))
+
+
 # ----------------------------------------------------------------------------- radius mask
 
 def _cells(B, seed, lo=8.0, hi=12.0, amin=80.0, amax=100.0):
