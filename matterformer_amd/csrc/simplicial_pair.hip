@@ -736,24 +736,39 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   // blocks, else those of the valid rows rounded up to 16
   const int nI = MULTI ? MAXC : __builtin_amdgcn_readfirstlane((round16(nk) * CPR + kThreads - 1) / kThreads);
   // rows [row0, row0 + nrows) of the compacted keys; rows up to the next
-  // multiple of 16 read as zero
-  auto load_set = [&](const T* base, int row0, int nrows, uint4 (&arr)[MAXC]) {
+  // multiple of 16 read as zero.  The atom indices of a block's slots are
+  // read once (rows clamped into the block) for its key and value sets, so
+  // the loads are not each preceded by an index read and its wait.
+  auto slot_atoms = [&](int row0, int nrows, int (&atom)[MAXC]) {
+    const int rlast = max(nrows - 1, 0);
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i)
+      atom[i] = nrows > 0 ? key_atom(row0 + min((tid + kThreads * i) / CPR, rlast)) : 0;
+  };
+  auto load_set = [&](const T* base, const int (&atom)[MAXC], int nrows, uint4 (&arr)[MAXC]) {
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
       const int row = (tid + kThreads * i) / CPR;
       arr[i] = uint4{0u, 0u, 0u, 0u};
-      if (i < nI && row < nrows && col_ok)
-        arr[i] = *reinterpret_cast<const uint4*>(base + size_t(key_atom(row0 + row)) * ksn + e0);
+      if (i < nI && row < nrows && col_ok) arr[i] = *reinterpret_cast<const uint4*>(base + size_t(atom[i]) * ksn + e0);
     }
   };
   uint4 rk1[MAXC], rk2[MAXC], rv1[MAXC], rv2[MAXC], rq[MAXQC];
   auto load_block = [&](int jc, int kc) {
     const int j0 = jc * kCap, k0 = kc * kCap;
     const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
-    load_set(gk1, j0, nkj, rk1);
-    load_set(gv1, j0, nkj, rv1);
-    load_set(gk2, k0, nkk, rk2);
-    load_set(gv2, k0, nkk, rv2);
+    int aj[MAXC], ak[MAXC];
+    slot_atoms(j0, nkj, aj);
+    if (kc == jc) {
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i) ak[i] = aj[i];
+    } else {
+      slot_atoms(k0, nkk, ak);
+    }
+    load_set(gk1, aj, nkj, rk1);
+    load_set(gv1, aj, nkj, rv1);
+    load_set(gk2, ak, nkk, rk2);
+    load_set(gv2, ak, nkk, rv2);
   };
 
   // ---- phase A: maxima -> scale exponents -------------------------------
@@ -782,13 +797,20 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     }
   };
   {
-    // query rows of the group (rows >= nqg read as zero)
+    // query rows of the group (rows >= nqg read as zero; indices first, as
+    // in load_set)
+    const int qlast = max(nqg - 1, 0);
+    int qatom[MAXQC];
+#pragma unroll
+    for (int i = 0; i < MAXQC; ++i) {
+      const int r = q0 + min((tid + kThreads * i) / CPR, qlast);
+      qatom[i] = nqg > 0 ? (qpre ? r : int(qidx[r])) : 0;
+    }
 #pragma unroll
     for (int i = 0; i < MAXQC; ++i) {
       const int row = (tid + kThreads * i) / CPR;
-      rq[i] = (row < nqg && col_ok)
-                  ? *reinterpret_cast<const uint4*>(gq + size_t(qpre ? q0 + row : int(qidx[q0 + row])) * qsn + e0)
-                  : uint4{0u, 0u, 0u, 0u};
+      rq[i] = uint4{0u, 0u, 0u, 0u};
+      if (row < nqg && col_ok) rq[i] = *reinterpret_cast<const uint4*>(gq + size_t(qatom[i]) * qsn + e0);
     }
   }
   ClaimState* cl = reinterpret_cast<ClaimState*>(smem + Ly::kClaim);
@@ -1098,19 +1120,22 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       // live next to the accumulators
       const int j0 = jc * kCap, k0 = kc * kCap;
       uint4 t[MAXC];
-      load_set(gk1, j0, nkj, t);
+      int aj[MAXC], ak[MAXC];
+      slot_atoms(j0, nkj, aj);
+      slot_atoms(k0, nkk, ak);
+      load_set(gk1, aj, nkj, t);
 #pragma unroll
       for (int i = 0; i < MAXC; ++i)
         if ((tid + kThreads * i) / CPR < rj) store_k(K1s, t[i], (tid + kThreads * i) / CPR, s1);
-      load_set(gv1, j0, nkj, t);
+      load_set(gv1, aj, nkj, t);
 #pragma unroll
       for (int i = 0; i < MAXC; ++i)
         if ((tid + kThreads * i) / CPR < rj) store_v(V1s, t[i], (tid + kThreads * i) / CPR, t1);
-      load_set(gk2, k0, nkk, t);
+      load_set(gk2, ak, nkk, t);
 #pragma unroll
       for (int i = 0; i < MAXC; ++i)
         if ((tid + kThreads * i) / CPR < rk) store_k(K2s, t[i], (tid + kThreads * i) / CPR, s2);
-      load_set(gv2, k0, nkk, t);
+      load_set(gv2, ak, nkk, t);
 #pragma unroll
       for (int i = 0; i < MAXC; ++i)
         if ((tid + kThreads * i) / CPR < rk) store_v(V2s, t[i], (tid + kThreads * i) / CPR, t2);
