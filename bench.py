@@ -722,7 +722,7 @@ def measure_simplicial_extras(lib, w, wd) -> dict:
         "bwd_roofline": {"bound": "mfma", "achieved": round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 3),
                          "peak": BF16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 5),
-                         "kernel": "mf::sbwd::simplicial_bwd_kernel<64, role, bf16 MFMA> x 3 roles "
+                         "kernel": "mf::sbwd::simplicial_bwd_kernel<64, bf16 MFMA>, the 3 roles in one launch "
                                    "(deterministic, no atomics)",
                          "kernel_ms": round(bwd_ms, 5), "note": "eager call incl. zero-fills and casts"},
     }

@@ -21,7 +21,7 @@
 //   J    j       i      k       K2 . (k1_j (.) Q[i])       V2 . (v1_j (.) GO[i])    dS: Q (.) K2 -> dk1_j, P: GO (.) V2 -> dv1_j
 //   K    k       i      j       K1 . (k2_k (.) Q[i])       V1 . (v2_k (.) GO[i])    dS: Q (.) K1 -> dk2_k, P: GO (.) V1 -> dv2_k
 //
-// One launch per role, OB workgroups per (b, h); workgroup ob takes the outer indices
+// One launch for the three roles, OB workgroups per (b, h) and role; workgroup ob takes the outer indices
 // (it OB + ob) kWaves + wave, one per wave and iteration it, so every
 // gradient element is written by one wave after sums in a fixed order: no
 // atomics, bitwise reproducible.  OB is sized on the host to fill the device
@@ -730,12 +730,21 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
 }
 
 // One kernel per role: each gets its own register allocation.
-template <int DP, int ROLE, bool M16, bool BIAS>
+// All three roles in one launch: blocks [r G, (r + 1) G) run role r (G =
+// B H OB).  The roles write disjoint gradients, so they may run
+// concurrently, and one launch lets the uneven blocks of the three roles
+// (work grows with the cube of a molecule's size) fill each other's tails.
+template <int DP, bool M16, bool BIAS>
 __global__ void __launch_bounds__((Shape<DP, M16>::kThreads), (Shape<DP, M16>::kMinBlocks)) simplicial_bwd_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int bh = blockIdx.x / p.OB;
-  const int ob = blockIdx.x - bh * p.OB;
-  run_role<DP, ROLE, M16, BIAS>(p, smem, bh, ob);
+  const int G = p.B * p.H * p.OB;
+  const int role = blockIdx.x / G;
+  const int blk = blockIdx.x - role * G;
+  const int bh = blk / p.OB;
+  const int ob = blk - bh * p.OB;
+  if (role == kRoleQ) run_role<DP, kRoleQ, M16, BIAS>(p, smem, bh, ob);
+  else if (role == kRoleJ) run_role<DP, kRoleJ, M16, BIAS>(p, smem, bh, ob);
+  else run_role<DP, kRoleK, M16, BIAS>(p, smem, bh, ob);
 }
 
 template <int DP, bool M16>
@@ -749,28 +758,21 @@ int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
                                         std::to_string(lds) + " bytes of LDS per workgroup, the device offers " +
                                         std::to_string(dev.max_lds_per_block));
   using Kern = void (*)(Params);
-  const Kern kerns[2][3] = {
-      {simplicial_bwd_kernel<DP, kRoleQ, M16, false>, simplicial_bwd_kernel<DP, kRoleJ, M16, false>,
-       simplicial_bwd_kernel<DP, kRoleK, M16, false>},
-      {simplicial_bwd_kernel<DP, kRoleQ, M16, true>, simplicial_bwd_kernel<DP, kRoleJ, M16, true>,
-       simplicial_bwd_kernel<DP, kRoleK, M16, true>}};
+  const Kern kerns[2] = {simplicial_bwd_kernel<DP, M16, false>, simplicial_bwd_kernel<DP, M16, true>};
   static bool attr_set[2] = {false, false};
   if (!attr_set[has_bias]) {
-    for (Kern k : kerns[has_bias])
-      MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kerns[has_bias]),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr_set[has_bias] = true;
   }
-  // about 8 workgroups per CU in each role's launch, at most one per kWaves outer indices
+  // about 8 workgroups per CU for each role, at most one per kWaves outer indices
   const long long bh = (long long)prm.B * prm.H;
   const long long want = (8LL * dev.num_cus + bh - 1) / bh;
   prm.OB = int(std::max(1LL, std::min<long long>(want, (prm.N + Shape<DP, M16>::kWaves - 1) / Shape<DP, M16>::kWaves)));
-  const long long blocks = bh * prm.OB;
+  const long long blocks = 3 * bh * prm.OB;
   if (blocks > 0x7fffffffLL) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: grid too large");
-  for (Kern k : kerns[has_bias]) {
-    hipLaunchKernelGGL(k, dim3(unsigned(blocks)), dim3(Shape<DP, M16>::kThreads), lds, stream, prm);
-    MF_HIP_CHECK(hipGetLastError());
-  }
+  hipLaunchKernelGGL(kerns[has_bias], dim3(unsigned(blocks)), dim3(Shape<DP, M16>::kThreads), lds, stream, prm);
+  MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
 }
 
