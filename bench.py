@@ -757,8 +757,9 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "every kernel here works per molecule or per cell with no cross-GPU exchange, "
-              "see DESIGN.md for how the path would shard.", file=sys.stderr)
+              "every kernel here works per molecule or per cell with no cross-GPU exchange: data "
+              "parallelism over molecules or cells shards the path without any forward exchange.",
+              file=sys.stderr)
         return 2
 
     import torch
