@@ -349,8 +349,11 @@ __global__ void __launch_bounds__(kThreads2, 3 - QW) radius_attn_pair_kernel(Par
   static_assert(CPT >= 1 && (kTile * CPR) % 256 == 0, "staging shape");
   static_assert(QW == 1 || QW == 2, "query tiles per wave");
   constexpr int QT = 64 * QW;       // queries per workgroup
-  constexpr int CW = ND * 4 + 2;    // floats per lane and query tile in the combine: O^T, m, l
-  static_assert(4 * 64 * QW * CW * 4 <= int(sizeof(T)) * 2 * 2 * kTile * KS, "combine area");
+  // combine area: QW ND planes of O^T (a float4 per lane of the 4 query
+  // groups) and QW planes of (m, l) pairs, consecutive lanes at consecutive
+  // addresses (16- and 8-byte LDS accesses without bank conflicts)
+  constexpr int kCombBytes = QW * ND * 256 * 16 + QW * 256 * 8;
+  static_assert(kCombBytes <= int(sizeof(T)) * 2 * 2 * kTile * KS, "combine area");
 
   __shared__ __attribute__((aligned(16))) T Ks[2][2][kTile * KS];  // [buffer][stream]
   __shared__ __attribute__((aligned(16))) T Vs[2][2][kTile * KS];  // V row-major, read transposed
@@ -675,17 +678,16 @@ __global__ void __launch_bounds__(kThreads2, 3 - QW) radius_attn_pair_kernel(Par
       l[t] += __shfl_xor(l[t], 32, 64);
     }
   }
-  float* cmb = reinterpret_cast<float*>(&Ks[0][0][0]);  // [query group][lane][QW][CW] (after the last barrier)
+  // (after the last barrier: the K tiles are no longer read)
+  mf_f32x4* cmb_o = reinterpret_cast<mf_f32x4*>(&Ks[0][0][0]);  // [QW][ND][4 query groups x 64 lanes]
+  float2* cmb_ml = reinterpret_cast<float2*>(cmb_o + QW * ND * 256);  // [QW][4 x 64]
+  const int slot = qw * 64 + lane;
   if (kh == 1) {
 #pragma unroll
     for (int t = 0; t < QW; ++t) {
-      float* c = cmb + ((qw * 64 + lane) * QW + t) * CW;
 #pragma unroll
-      for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) c[nd * 4 + r] = acc[t][nd][r];
-      c[ND * 4] = m[t];
-      c[ND * 4 + 1] = l[t];
+      for (int nd = 0; nd < ND; ++nd) cmb_o[(t * ND + nd) * 256 + slot] = acc[t][nd];
+      cmb_ml[t * 256 + slot] = float2{m[t], l[t]};
     }
   }
   __syncthreads();
@@ -693,8 +695,8 @@ __global__ void __launch_bounds__(kThreads2, 3 - QW) radius_attn_pair_kernel(Par
 #pragma unroll
   for (int t = 0; t < QW; ++t) {
     if (!q_in[t]) continue;
-    const float* c = cmb + ((qw * 64 + lane) * QW + t) * CW;
-    const float m1 = c[ND * 4], l1 = c[ND * 4 + 1];
+    const float2 ml = cmb_ml[t * 256 + slot];
+    const float m1 = ml.x, l1 = ml.y;
     const float M = fmaxf(m[t], m1);
     const float a0 = M == -INFINITY ? 0.0f : fast_exp2(m[t] - M);  // 0 for a stream without allowed keys
     const float a1 = M == -INFINITY ? 0.0f : fast_exp2(m1 - M);
@@ -705,9 +707,10 @@ __global__ void __launch_bounds__(kThreads2, 3 - QW) radius_attn_pair_kernel(Par
 #pragma unroll
     for (int nd = 0; nd < ND; ++nd) {
       const int d0 = 16 * nd + 4 * g;
+      const mf_f32x4 c1 = cmb_o[(t * ND + nd) * 256 + slot];
       float o[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = (a0 * acc[t][nd][r] + a1 * c[nd * 4 + r]) * inv;
+      for (int r = 0; r < 4; ++r) o[r] = (a0 * acc[t][nd][r] + a1 * c1[r]) * inv;
       if (p.out) {
         Op4 ov;
 #pragma unroll
