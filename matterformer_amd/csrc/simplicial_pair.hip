@@ -754,6 +754,14 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     }
   };
   uint4 rk1[MAXC], rk2[MAXC], rv1[MAXC], rv2[MAXC], rq[MAXQC];
+  // every slot without a branch, for the maxima only: rows clamped into the
+  // block repeat a valid row (maxima unchanged), columns past D read column
+  // 0 and are masked in acc_max.  (Conditional loads joined with zeros would
+  // make the compiler wait for each load in its own branch.)
+  auto load_set_all = [&](const T* base, const int (&atom)[MAXC], uint4 (&arr)[MAXC]) {
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) arr[i] = *reinterpret_cast<const uint4*>(base + size_t(atom[i]) * ksn + (col_ok ? e0 : 0));
+  };
   auto load_block = [&](int jc, int kc) {
     const int j0 = jc * kCap, k0 = kc * kCap;
     const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
@@ -778,6 +786,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   uint32_t gv = 0u, gqm = 0u;  // |V1| (low half) and |V2| (high half) maxima; |q| maxima
 #pragma unroll
   for (int e = 0; e < 4; ++e) c1[e] = c2[e] = 0u;
+  const uint32_t cmask = col_ok ? 0x7fff7fffu : 0u;  // magnitude bits; nothing for columns past D
   auto acc_max = [&]() {
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
@@ -786,11 +795,11 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       const uint32_t a2[4] = {rk2[i].x, rk2[i].y, rk2[i].z, rk2[i].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        c1[e] = pk_max_u16(c1[e], a1[e] & 0x7fff7fffu);
-        c2[e] = pk_max_u16(c2[e], a2[e] & 0x7fff7fffu);
+        c1[e] = pk_max_u16(c1[e], a1[e] & cmask);
+        c2[e] = pk_max_u16(c2[e], a2[e] & cmask);
       }
-      const uint32_t m1 = pk_max_u16(pk_max_u16(rv1[i].x, rv1[i].y), pk_max_u16(rv1[i].z, rv1[i].w)) & 0x7fff7fffu;
-      const uint32_t m2 = pk_max_u16(pk_max_u16(rv2[i].x, rv2[i].y), pk_max_u16(rv2[i].z, rv2[i].w)) & 0x7fff7fffu;
+      const uint32_t m1 = pk_max_u16(pk_max_u16(rv1[i].x, rv1[i].y), pk_max_u16(rv1[i].z, rv1[i].w)) & cmask;
+      const uint32_t m2 = pk_max_u16(pk_max_u16(rv2[i].x, rv2[i].y), pk_max_u16(rv2[i].z, rv2[i].w)) & cmask;
       // low half: |V1|, high half: |V2|
       gv = pk_max_u16(gv, __builtin_amdgcn_perm(m2, m1, 0x07060302u));
       gv = pk_max_u16(gv, __builtin_amdgcn_perm(m2, m1, 0x05040100u));
@@ -823,7 +832,12 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   } else {
     if (zero_share) zero_padded_share<T, DP, STR>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
     for (int rc = 0; rc < nch; ++rc) {
-      load_block(rc, rc);
+      int a[MAXC];
+      slot_atoms(rc * kCap, min(kCap, nk - rc * kCap), a);
+      load_set_all(gk1, a, rk1);
+      load_set_all(gv1, a, rv1);
+      load_set_all(gk2, a, rk2);
+      load_set_all(gv2, a, rv2);
       acc_max();
     }
   }
