@@ -1,7 +1,9 @@
 // Library-wide C-ABI entry points: version, thread-local error string and
 // the cached per-device properties the launchers size their grids with.
 #include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "mf_common.h"
@@ -34,6 +36,19 @@ int device_info(DeviceInfo* out) {
     info.device = dev;
   }
   *out = info;
+  return MF_OK;
+}
+
+int ensure_dynamic_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<std::pair<const void*, int>, int>> done;  // ((kernel, device), bytes)
+  int dev = 0;
+  MF_HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(std::make_pair(kernel, dev), bytes);
+  if (done.count(key)) return MF_OK;
+  MF_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+  done.insert(key);
   return MF_OK;
 }
 

@@ -24,6 +24,11 @@ struct DeviceInfo {
 };
 int device_info(DeviceInfo* out);
 
+// hipFuncSetAttribute(kernel, MaxDynamicSharedMemorySize, bytes) once per
+// (kernel, current device, bytes), under a lock: safe from several host threads
+// and on every device the library runs on.
+int ensure_dynamic_lds(const void* kernel, int bytes);
+
 // Register-resident simplicial kernels for 16-bit operands (simplicial_fast.hip).
 int simplicial_fast_capacity(int head_dim);
 size_t simplicial_fast_workspace_bytes(int batch, int heads, int tokens);

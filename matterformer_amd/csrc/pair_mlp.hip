@@ -264,10 +264,9 @@ size_t lds_bytes(int ks, int kp, int hidden) {
 template <int KS, int KP>
 int launch(const Params& p, int num_cus, hipStream_t s) {
   const size_t lds = lds_bytes(KS, KP, p.hidden);
-  // dynamic LDS above 64 KB needs the attribute (set once per kernel, thread-safe static init)
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(pair_mlp_kernel<KS, KP>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  MF_HIP_CHECK(attr);
+  // dynamic LDS above 64 KB needs the attribute (once per kernel and device)
+  const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(pair_mlp_kernel<KS, KP>), 160 * 1024);
+  if (st != MF_OK) return st;
   const long long units = (long long)p.B * p.N * p.groups;
   const int grid = int(std::min<long long>((units + 7) / 8, (long long)num_cus * 2));
   hipLaunchKernelGGL((pair_mlp_kernel<KS, KP>), dim3(grid), dim3(kThreads), lds, s, p);

@@ -50,8 +50,10 @@
 //     dS / P contractions, :611-645, are fp32).  Columns and rows are staged
 //     as bf16 (exact).  The GEMM1 B operand is the fp32 product oS (.) R
 //     rounded to bf16 for S, and carried as bf16 hi + lo (x = hi + lo to
-//     about 16 bits, two MFMAs) for dP; 8 consecutive d = 32 s + 8 g .. +7
-//     per lane.  GEMM2 takes dS and P, again as hi + lo, as its B operand
+//     about 16 bits, two MFMAs) for dP, whose difference dP - delta cancels
+//     when one pair dominates the softmax; 8 consecutive d = 32 s + 8 g .. +7
+//     per lane.  GEMM2 takes dS and P rounded once to bf16 (their sums over
+//     the columns carry no cancellation) as its B operand
 //     straight from the GEMM1 accumulators of two column tiles, and
 //     C_S^T / C_P^T as its A operand through transposed LDS reads
 //     (ds_read_b64_tr_b16) of the row-major columns.  Softmax, dS and every
@@ -495,11 +497,16 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
       if constexpr (M16) {
         // B operands: row r16, d = 32 s + 8 g .. +7, products rounded to bf16
         constexpr int NS = DP / 32;
-        mf_bf16x8 bs[NS], bp[NS];
+        mf_bf16x8 bs[NS], bp[NS], bpl[NS];
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           bs[s] = pack_bf16(mul4(rs[2 * s], oS[2 * s]), mul4(rs[2 * s + 1], oS[2 * s + 1]));
-          bp[s] = pack_bf16(mul4(rp[2 * s], oP[2 * s]), mul4(rp[2 * s + 1], oP[2 * s + 1]));
+          // dP operand as bf16 hi + lo: dP - delta cancels when one pair dominates the softmax
+          const float4 x0 = mul4(rp[2 * s], oP[2 * s]), x1 = mul4(rp[2 * s + 1], oP[2 * s + 1]);
+          bp[s] = pack_bf16(x0, x1);
+          const float4 h0 = bf16_lo(bp[s]), h1 = bf16_hi(bp[s]);
+          bpl[s] = pack_bf16(float4{x0.x - h0.x, x0.y - h0.y, x0.z - h0.z, x0.w - h0.w},
+                             float4{x1.x - h1.x, x1.y - h1.y, x1.z - h1.z, x1.w - h1.w});
         }
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
@@ -514,6 +521,7 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
               const mf_bf16x8 ap = *reinterpret_cast<const mf_bf16x8*>(cp + 32 * s);
               sv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as, bs[s], sv[kt], 0, 0, 0);
               dv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap, bp[s], dv[kt], 0, 0, 0);
+              dv[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap, bpl[s], dv[kt], 0, 0, 0);
             }
           }
         }
@@ -759,12 +767,8 @@ int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
                                         std::to_string(dev.max_lds_per_block));
   using Kern = void (*)(Params);
   const Kern kerns[2] = {simplicial_bwd_kernel<DP, M16, false>, simplicial_bwd_kernel<DP, M16, true>};
-  static bool attr_set[2] = {false, false};
-  if (!attr_set[has_bias]) {
-    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kerns[has_bias]),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_set[has_bias] = true;
-  }
+  st = ensure_dynamic_lds(reinterpret_cast<const void*>(kerns[has_bias]), 160 * 1024);
+  if (st != MF_OK) return st;
   // about 8 workgroups per CU for each role, at most one per kWaves outer indices
   const long long bh = (long long)prm.B * prm.H;
   const long long want = (8LL * dev.num_cus + bh - 1) / bh;
@@ -828,7 +832,10 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool has_pv = a->pair_valid != nullptr;
   const int D = a->head_dim;
-  if (a->dtype == MF_DTYPE_BF16) {  // bf16 inputs: bf16 MFMA (K steps of 32 d); fp16 takes the fp32 path
+  // bf16 operands and a bf16 grad_out: bf16 MFMA (K steps of 32 d), which stages grad_out rows as bf16 (exact
+  // only for a bf16 grad_out).  Everything else -- fp16 operands, or a grad_out of another dtype -- takes the
+  // fp32 path, which reads every operand in its own dtype.
+  if (a->dtype == MF_DTYPE_BF16 && a->grad_dtype == MF_DTYPE_BF16) {
     if (D <= 32) return launch<32, true>(prm, has_pv, has_bias, s);
     if (D <= 64) return launch<64, true>(prm, has_pv, has_bias, s);
     return launch<128, true>(prm, has_pv, has_bias, s);

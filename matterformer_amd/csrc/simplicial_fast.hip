@@ -1339,12 +1339,8 @@ template <typename T, int DP, int NT, bool HAS_PV, int MODE>
 int launch_main(const Params& prm, int grid, hipStream_t stream) {
   auto kern = simplicial_fast_kernel<T, DP, NT, HAS_PV, MODE>;
   const size_t lds = Layout<T, DP, NT>::kFixed;
-  static bool attr_set = false;  // per instantiation
-  if (!attr_set) {
-    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
-    attr_set = true;
-  }
+  const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), int(lds));
+  if (st != MF_OK) return st;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, prm);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;

@@ -689,12 +689,8 @@ template <typename T, int DP, int EXT>
 int launch(const Params& prm, size_t lds, int grid, hipStream_t stream) {
   auto kern = simplicial_fwd_kernel<T, DP, EXT>;
   constexpr int kThreads = Waves<EXT>::kThreadCount;
-  static bool attr_set = false;  // per instantiation
-  if (!attr_set) {
-    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_set = true;
-  }
+  const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), 160 * 1024);
+  if (st != MF_OK) return st;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, prm);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;

@@ -1576,12 +1576,8 @@ int launch(const Params& prm, int num_cus, hipStream_t stream) {
   const int grid = std::max(8, (BIAS ? 1 : 2) * num_cus);  // 2 workgroups per CU (1 with the bias)
   auto kern = simplicial_pair_kernel<T, DP, HAS_PV, BIAS, STR>;
   const size_t lds = BIAS ? Lay<DP>::kTotalBias : Lay<DP>::kTotal;
-  static bool attr_set = false;  // per instantiation
-  if (!attr_set) {
-    MF_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
-    attr_set = true;
-  }
+  const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), int(lds));
+  if (st != MF_OK) return st;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, prm);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;

@@ -145,6 +145,9 @@ class KnnLocalAttention(nn.Module):
             return "the HIP local attention requires GPU tensors"
         if self.training and self.attn.dropout > 0.0:
             return "the HIP local attention does not support attention dropout in training mode"
+        if torch.is_grad_enabled() and (h.requires_grad or any(p.requires_grad for p in self.attn.parameters())):
+            # mf_radius_attn is a forward kernel with no autograd Function: the torch path keeps the graph
+            return "the HIP local attention has no backward; autograd takes the torch path"
         head_dim = self.attn.embed_dim // self.attn.num_heads
         if head_dim not in (32, 64, 128):
             return f"the HIP local attention supports head_dim 32, 64 or 128, got {head_dim}"
