@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 8
+#define MF_ABI_VERSION 9
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -169,8 +169,20 @@ int mf_simplicial_fwd(const mf_simplicial_fwd_args* args, void* stream);
 /* :929-1204, which accumulates them with atomics).  Every output element is */
 /* written by one wave after sums in a fixed order: two calls on the same    */
 /* inputs give bitwise identical gradients.  Outputs are fp32, written only  */
-/* at valid entries: the caller zero-fills them.  Low-rank angle and message */
-/* terms are not part of this entry point.                                   */
+/* at valid entries: the caller zero-fills them.                            */
+/* With the low-rank terms of mf_simplicial_fwd (angle A_ijk = sum_r         */
+/* AL[i,j,r] AR[i,k,r] added to S as ag_i Ra^-1/2 A; message                 */
+/* c_ir = Rm^-1/2 sum_jk P ML[i,j,r] MR[i,k,r], out_i += sum_r c_ir          */
+/* basis[h,r]), dP gains Rm^-1/2 sum_r dc_ir ML MR with dc_ir = basis[h,r].go_i */
+/* and, with sa = Ra^-1/2, sm = Rm^-1/2:                                     */
+/*   dangle_left[i,j]  = ag_i sa sum_k dS AR[i,k]                            */
+/*   dangle_right[i,k] = ag_i sa sum_j dS AL[i,j]                            */
+/*   dangle_gate[i]    = sa sum_jk dS A_ijk                                  */
+/*   dmessage_left[i,j]  = sm dc_i (.) sum_k P MR[i,k]                       */
+/*   dmessage_right[i,k] = sm dc_i (.) sum_j P ML[i,j]                       */
+/*   dmessage_basis[h,r] = sm sum_(b,i valid) (sum_jk P ML MR)_ir go_i       */
+/* (triton_simplicial_attention.py:488-515,575-782).  Calls with these       */
+/* terms run fp32 arithmetic for every operand dtype.                        */
 /* Replaces triton_simplicial_attention_backward,                            */
 /* triton_simplicial_attention.py:929-1204.                                  */
 /* ------------------------------------------------------------------------ */
@@ -207,9 +219,34 @@ typedef struct mf_simplicial_bwd_args {
   int32_t head_dim;         /* 1..128                                        */
   int32_t dtype;            /* mf_dtype of q, k1, v1, k2, v2                 */
   int32_t reserved;
+  /* Low-rank angle and message terms (ABI 9), laid out as in              */
+  /* mf_simplicial_fwd_args; a group is absent when its first pointer is   */
+  /* NULL.  Their gradients are fp32, zero-filled by the caller, written   */
+  /* only at valid entries; NULL = not wanted.                             */
+  int32_t angle_rank;           /* Ra, 1..64 when angle_left != NULL       */
+  int32_t message_rank;         /* Rm, 1..64 when message_left != NULL     */
+  const float* angle_left;      /* [B*H, N, N, Ra] fp32                    */
+  const float* angle_right;     /* [B*H, N, N, Ra] fp32                    */
+  const float* angle_gate;      /* [B*H, N] fp32                           */
+  const float* message_left;    /* [B*H, N, N, Rm] fp32                    */
+  const float* message_right;   /* [B*H, N, N, Rm] fp32                    */
+  const float* message_basis;   /* [H, Rm, D] fp32                         */
+  float* dangle_left;           /* [B*H, N, N, Ra]                         */
+  float* dangle_right;          /* [B*H, N, N, Ra]                         */
+  float* dangle_gate;           /* [B*H, N]                                */
+  float* dmessage_left;         /* [B*H, N, N, Rm]                         */
+  float* dmessage_right;        /* [B*H, N, N, Rm]                         */
+  float* dmessage_basis;        /* [H, Rm, D]                              */
+  void* workspace;              /* mf_simplicial_bwd_workspace_size() bytes (NULL when 0) */
+  uint64_t workspace_bytes;
 } mf_simplicial_bwd_args;
 
 int mf_simplicial_bwd(const mf_simplicial_bwd_args* args, void* stream);
+
+/* Bytes of workspace mf_simplicial_bwd needs (0 without a message term):   */
+/* per query, the message coefficients dc = basis . go and sum_jk P ML MR.  */
+uint64_t mf_simplicial_bwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens,
+                                          int32_t head_dim, int32_t message_rank);
 
 /* Returns MF_OK when mf_simplicial_fwd can serve this shape on the current
  * device, MF_ERR_UNSUPPORTED (with mf_last_error set) when it cannot. */

@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "mf_simplicial_fwd_workspace_size",
     "mf_simplicial_fwd_noalloc",
     "mf_simplicial_bwd",
+    "mf_simplicial_bwd_workspace_size",
     "mf_knn",
     "mf_knn_mask",
     "mf_radius_mask",
@@ -50,7 +51,7 @@ EXPORTED_SYMBOLS = (
     "mf_pair_mlp_bias",
 )
 
-EXPECTED_ABI_VERSION = 8
+EXPECTED_ABI_VERSION = 9
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -105,7 +106,12 @@ class MfSimplicialBwdArgs(ctypes.Structure):
         "bias_u", "bias_v", "bias_w", "bias_gate")] + \
         [("bias_dtype", ctypes.c_int32), ("grad_dtype", ctypes.c_int32)] + \
         [(n, ctypes.c_void_p) for n in ("dq", "dk1", "dv1", "dk2", "dv2", "du", "dv_bias", "dw", "dgate")] + \
-        [(n, ctypes.c_int32) for n in ("batch", "heads", "tokens", "head_dim", "dtype", "reserved")]
+        [(n, ctypes.c_int32) for n in ("batch", "heads", "tokens", "head_dim", "dtype", "reserved",
+                                       "angle_rank", "message_rank")] + \
+        [(n, ctypes.c_void_p) for n in (
+            "angle_left", "angle_right", "angle_gate", "message_left", "message_right", "message_basis",
+            "dangle_left", "dangle_right", "dangle_gate", "dmessage_left", "dmessage_right", "dmessage_basis",
+            "workspace")] + [("workspace_bytes", ctypes.c_uint64)]
 
 
 class MfKnnArgs(ctypes.Structure):
@@ -244,6 +250,8 @@ def _load() -> ctypes.CDLL | None:
     lib.mf_simplicial_fwd_supported.restype = ctypes.c_int
     lib.mf_simplicial_fwd_workspace_size.argtypes = [ctypes.c_int32] * 5
     lib.mf_simplicial_fwd_workspace_size.restype = ctypes.c_uint64
+    lib.mf_simplicial_bwd_workspace_size.argtypes = [ctypes.c_int32] * 5
+    lib.mf_simplicial_bwd_workspace_size.restype = ctypes.c_uint64
     version = lib.mf_abi_version()
     if version != EXPECTED_ABI_VERSION:
         _LOAD_ERROR = f"{path} has ABI version {version}, expected {EXPECTED_ABI_VERSION}"

@@ -61,6 +61,23 @@
 //     + e of tile t: the same d for its GEMM1 operands, its GEMM2 outputs
 //     and its row values.
 //   fp16 inputs take the fp32 path (fp16 columns are not exact in bf16).
+//
+// Low-rank angle and message terms (LR instantiations, fp32 path, 4 waves):
+// every pair (i, j, k) a lane evaluates gains the rank dot products of its
+// query's factors, A = sum_r AL[i,j,r] AR[i,k,r] into S and
+// M = sum_r dc_ir ML[i,j,r] MR[i,k,r] into dP (dc_ir = basis[h,r] . go_i,
+// written to the workspace by a pre-pass).  One factor of each dot depends
+// on the lane's row and the outer index only and is read once per rank
+// chunk; the other is read per column:
+//   role Q (i = o):  row AL[o,j=row], ML[o,row];  column AR[o,k=col], MR[o,col]
+//   role J (j = o):  row AL[i=row,o], ML[row,o];  column AR[row,k=col], MR[row,col]
+//   role K (k = o):  row AR[i=row,o], MR[row,o];  column AL[row,j=col], ML[row,col]
+// All gradients of these terms are indexed by the query i, so ownership
+// still decides who writes them: role Q sums dangle_left[o,row] and
+// dmessage_left[o,row] over its columns, role K dangle_right[row,o] and
+// dmessage_right[row,o]; each wave adds its column blocks' sums in order.
+// Role Q also forms sum_jk P ML MR per query (per-row partials in LDS) for
+// dmessage_basis, which a post-pass reduces over the batch in a fixed order.
 #include <algorithm>
 #include <cmath>
 
@@ -74,12 +91,12 @@ constexpr int kRoleJ = 1;
 constexpr int kRoleK = 2;
 constexpr int kCols = 64;  // staged key columns per block
 
-template <int DP, bool M16>
+template <int DP, bool M16, bool LR = false>
 struct Shape {
-  // fp32: D = 128 needs the whole register file per wave.  16-bit: 4 waves
-  // at about 240 VGPRs put two workgroups on each CU, so that one's global
-  // loads overlap the other's arithmetic.
-  static constexpr int kWaves = (M16 || DP >= 128) ? 4 : 8;
+  // fp32: D = 128 needs the whole register file per wave, as do the rank
+  // terms (LR).  16-bit: 4 waves at about 240 VGPRs put two workgroups on
+  // each CU, so that one's global loads overlap the other's arithmetic.
+  static constexpr int kWaves = (M16 || DP >= 128 || LR) ? 4 : 8;
   static constexpr int kMinBlocks = (M16 && DP < 128) ? 2 : 1;  // workgroups per CU the registers must allow
   static constexpr int kThreads = kWaves * 64;
   static constexpr int NT = DP / 16;   // 16-wide d tiles
@@ -144,21 +161,39 @@ struct Params {
   int NP;       // N rounded up to 64: LDS list capacity
   int OB;       // workgroups per (b, h, role)
   int vec;      // q/k/v/go/out rows 4-element loads are aligned (D % 4 == 0, aligned bases)
+  // low-rank terms (LR instantiations): factors [B*H, N, N, R] fp32, gates [B*H, N], basis [H, Rm, D]
+  const float* al;
+  const float* ar;
+  const float* ag;
+  const float* ml;
+  const float* mr;
+  const float* mb;
+  int Ra, Rm, RmP;      // ranks; Rm rounded up to 4
+  float a_scale, m_scale;
+  int lr_vec;           // rank rows are 16-byte aligned (R % 4 == 0, aligned bases): float4 reads
+  float* dal;
+  float* dar;
+  float* dag;
+  float* dml;
+  float* dmr;
+  float* dc;            // workspace [B*H, N, Rm]: basis[h] . go_i (message)
+  float* coeff;         // workspace [B*H, N, Rm]: sum_jk P ML MR of each valid query (message)
 };
 
 // LDS layout (bytes), shared by host sizing and device carving.
-template <int DP, bool M16>
+template <int DP, bool M16, bool LR = false>
 struct Lay {
   // staged tiles: fp32 C_S, C_P (64 columns); 16-bit: bf16 C_S, C_P and R_S, R_P (64 rows)
   static size_t __host__ __device__ cols() {
     return M16 ? size_t(4) * kCols * Shape<DP, M16>::KS * 2 : size_t(2) * kCols * Shape<DP, M16>::D4 * 4;
   }
-  static size_t __host__ __device__ bytes(int NP, bool has_pv, bool has_bias) {
+  static size_t __host__ __device__ bytes(int NP, bool has_pv, bool has_bias, int RmP = 0) {
     size_t s = cols();
     s += size_t(NP) * 4 * 4;                                  // kidx, qidx, delta, lse2
     if (has_pv) s += size_t(NP) * 2 * 4;                      // 64 column bits per row
-    if (has_bias) s += size_t(Shape<DP, M16>::kWaves) * (NP + kCols) * 4;  // per-wave row / column sums
+    if (has_bias) s += size_t(Shape<DP, M16, LR>::kWaves) * (NP + kCols) * 4;  // per-wave row / column sums
     s += 16;                                                  // counts
+    s += size_t(Shape<DP, M16, LR>::kWaves) * 16 * RmP * 4;   // LR: per-wave, per-row sum_jk P ML MR partials
     return s;
   }
 };
@@ -212,9 +247,29 @@ __device__ __forceinline__ int compact(const uint8_t* m, int N, int* dst, int la
   return count;
 }
 
-template <int DP, int ROLE, bool M16, bool BIAS>
+// Elements r0 .. r0 + 3 of a rank row (rem = R - r0 >= 1 of them valid, the
+// rest 0); one 16-byte read when the rows are aligned and R % 4 == 0.
+__device__ __forceinline__ float4 ld_r4(const float* p, int rem, int vec) {
+  if (vec) return *reinterpret_cast<const float4*>(p);
+  float4 r = float4{p[0], 0.f, 0.f, 0.f};
+  if (rem > 1) r.y = p[1];
+  if (rem > 2) r.z = p[2];
+  if (rem > 3) r.w = p[3];
+  return r;
+}
+
+// x + its partners in the other three 16-lane groups (lanes l ^ 16, l ^ 32), in a fixed order
+__device__ __forceinline__ float4 sum_groups4(float4 v) {
+  v.x += __shfl_xor(v.x, 16, 64); v.y += __shfl_xor(v.y, 16, 64);
+  v.z += __shfl_xor(v.z, 16, 64); v.w += __shfl_xor(v.w, 16, 64);
+  v.x += __shfl_xor(v.x, 32, 64); v.y += __shfl_xor(v.y, 32, 64);
+  v.z += __shfl_xor(v.z, 32, 64); v.w += __shfl_xor(v.w, 32, 64);
+  return v;
+}
+
+template <int DP, int ROLE, bool M16, bool BIAS, bool LR>
 __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, int bh, int ob) {
-  using S = Shape<DP, M16>;
+  using S = Shape<DP, M16, LR>;
   constexpr int kWaves = S::kWaves;
   constexpr int kThreads = S::kThreads;
   constexpr int NT = S::NT;
@@ -240,6 +295,7 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
   float* wrow = reinterpret_cast<float*>(pvb + (has_pv ? 2 * NP : 0));
   float* wcol = wrow + (has_bias ? kWaves * NP : 0);
   int* counts = reinterpret_cast<int*>(wcol + (has_bias ? kWaves * kCols : 0));
+  float* coeffL = reinterpret_cast<float*>(counts + 4);  // LR: [kWaves][16][RmP] per-row sum_jk P ML MR partials
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -341,6 +397,11 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
       acc_b[t][r] = 0.0f;
     }
   float gacc = 0.0f;  // role Q: dgate partial
+  float gacc_a = 0.0f;  // role Q (LR): dangle_gate partial
+  if constexpr (LR && ROLE == kRoleQ) {
+    if (p.ml && p.coeff)
+      for (int u = lane; u < 16 * p.RmP; u += 64) coeffL[wave * 16 * p.RmP + u] = 0.0f;
+  }
 
   const int ncb = (nk + kCols - 1) / kCols;
   const int nrb = M16 ? (n_rows + kCols - 1) / kCols : 1;  // 16-bit: rows staged in 64-row blocks
@@ -547,6 +608,57 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
       }
       }
 
+      // ---- low-rank terms of the lane's 16 pairs (LR): A into S, M into dP ----
+      // column x of the lane: kt = x >> 2, r = x & 3, block column 16 kt + 4 g + r
+      float la[16], lm[16];
+      int catom[16];
+      uint32_t cokm = 0u;  // bit x: column x is a valid key
+      size_t qrow = 0;     // the query of the lane's pairs (row of [B*H, N])
+      float agl2 = 0.0f;   // ag_i Ra^-1/2 log2(e)
+      if constexpr (LR) {
+        qrow = ROLE == kRoleQ ? orow : rrow;
+        const int rowkey = ROLE == kRoleQ ? ro : oo;  // Q: j = row; J: j = o; K: k = o
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+          const int c = (x >> 2) * 16 + 4 * g + (x & 3);
+          cokm |= ((x >> 2) < nkt && cb0 + c < nk) ? (1u << x) : 0u;
+          catom[x] = kidx[min(cb0 + c, nk - 1)];
+          la[x] = 0.0f;
+          lm[x] = 0.0f;
+        }
+        const size_t rowoff = qrow * N + rowkey;  // [.., N, N, R] row of the row-constant factor
+        const size_t coloff = qrow * N;           // + the column atom
+        if (p.al) {
+          agl2 = p.ag[qrow] * p.a_scale * kLog2e;
+          const float* rowp = (ROLE == kRoleK ? p.ar : p.al) + rowoff * p.Ra;
+          const float* colp = (ROLE == kRoleK ? p.al : p.ar) + coloff * p.Ra;
+          for (int c0 = 0; c0 < p.Ra; c0 += 4) {
+            const float4 rv = row_ok ? ld_r4(rowp + c0, p.Ra - c0, p.lr_vec) : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int x = 0; x < 16; ++x) {
+              if (!((cokm >> x) & 1u)) continue;
+              const float4 cv = ld_r4(colp + size_t(catom[x]) * p.Ra + c0, p.Ra - c0, p.lr_vec);
+              la[x] = fmaf(rv.w, cv.w, fmaf(rv.z, cv.z, fmaf(rv.y, cv.y, fmaf(rv.x, cv.x, la[x]))));
+            }
+          }
+        }
+        if (p.ml) {
+          const float* rowp = (ROLE == kRoleK ? p.mr : p.ml) + rowoff * p.Rm;
+          const float* colp = (ROLE == kRoleK ? p.ml : p.mr) + coloff * p.Rm;
+          const float* dcp = p.dc + qrow * p.Rm;
+          for (int c0 = 0; c0 < p.Rm; c0 += 4) {
+            float4 rv = float4{0.f, 0.f, 0.f, 0.f};
+            if (row_ok) rv = mul4(ld_r4(rowp + c0, p.Rm - c0, p.lr_vec), ld_r4(dcp + c0, p.Rm - c0, p.lr_vec));
+#pragma unroll
+            for (int x = 0; x < 16; ++x) {
+              if (!((cokm >> x) & 1u)) continue;
+              const float4 cv = ld_r4(colp + size_t(catom[x]) * p.Rm + c0, p.Rm - c0, p.lr_vec);
+              lm[x] = fmaf(rv.w, cv.w, fmaf(rv.z, cv.z, fmaf(rv.y, cv.y, fmaf(rv.x, cv.x, lm[x]))));
+            }
+          }
+        }
+      }
+
       // P, dS (sv <- dS, dv <- P) and the bias sums
       float rowsum = 0.0f;
 #pragma unroll
@@ -574,13 +686,19 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
             base = (bias_row + be) + bc;
             s2 = fmaf(gq_r, base, s2);
           }
+          float dpv = dv[kt][r];
+          if constexpr (LR) {
+            if (p.al) s2 = fmaf(agl2, la[kt * 4 + r], s2);
+            if (p.ml) dpv = fmaf(p.m_scale, lm[kt * 4 + r], dpv);
+          }
           const float pe = ok ? fast_exp2(s2 - lse2_r) : 0.0f;
-          const float ds = pe * (dv[kt][r] - delta_r);
+          const float ds = pe * (dpv - delta_r);
           sv[kt][r] = ds;
           dv[kt][r] = pe;
           if constexpr (ROLE == kRoleQ) {
             rowsum += ds;
             gacc = fmaf(ds, base, gacc);
+            if constexpr (LR) gacc_a = fmaf(ds, la[kt * 4 + r], gacc_a);
           }
         }
       }
@@ -604,6 +722,78 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
               x += __shfl_xor(x, 8, 64);
               if (r16 == 0) wcol[wave * kCols + kt * 16 + 4 * g + r] += x;
             }
+        }
+      }
+
+      // ---- gradients of the low-rank terms (LR): role Q sums over its columns k into dangle_left[o][row],
+      // dmessage_left[o][row] (and the row's sum_k P ML MR partial), role K over its columns j into
+      // dangle_right[row][o], dmessage_right[row][o]; each (query, key) entry is one lane's, added per
+      // column block in block order ----
+      if constexpr (LR && ROLE != kRoleJ) {
+        const size_t dstoff = ROLE == kRoleQ ? qrow * N + ro : qrow * N + oo;
+        const size_t coloff = qrow * N;
+        float* dA = ROLE == kRoleQ ? p.dal : p.dar;
+        if (p.al && dA) {
+          const float* colp = (ROLE == kRoleK ? p.al : p.ar) + coloff * p.Ra;
+          const float gs = p.ag[qrow] * p.a_scale;
+          for (int c0 = 0; c0 < p.Ra; c0 += 4) {
+            float4 t = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int x = 0; x < 16; ++x) {
+              if (!((cokm >> x) & 1u)) continue;
+              const float4 cv = ld_r4(colp + size_t(catom[x]) * p.Ra + c0, p.Ra - c0, p.lr_vec);
+              const float d = sv[x >> 2][x & 3];
+              t = float4{fmaf(d, cv.x, t.x), fmaf(d, cv.y, t.y), fmaf(d, cv.z, t.z), fmaf(d, cv.w, t.w)};
+            }
+            t = sum_groups4(t);
+            if (g == 0 && row_ok) {
+              float* dst = dA + dstoff * p.Ra + c0;
+              const int rem = min(4, p.Ra - c0);
+              dst[0] = fmaf(gs, t.x, dst[0]);
+              if (rem > 1) dst[1] = fmaf(gs, t.y, dst[1]);
+              if (rem > 2) dst[2] = fmaf(gs, t.z, dst[2]);
+              if (rem > 3) dst[3] = fmaf(gs, t.w, dst[3]);
+            }
+          }
+        }
+        float* dM = ROLE == kRoleQ ? p.dml : p.dmr;
+        const bool want_m = dM != nullptr || (ROLE == kRoleQ && p.coeff != nullptr);
+        if (p.ml && want_m) {
+          const float* colp = (ROLE == kRoleK ? p.ml : p.mr) + coloff * p.Rm;
+          const float* dcp = p.dc + qrow * p.Rm;
+          const float* mlrow = p.ml + (qrow * N + ro) * p.Rm;  // role Q: ML[o][row]
+          for (int c0 = 0; c0 < p.Rm; c0 += 4) {
+            float4 t = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int x = 0; x < 16; ++x) {
+              if (!((cokm >> x) & 1u)) continue;
+              const float4 cv = ld_r4(colp + size_t(catom[x]) * p.Rm + c0, p.Rm - c0, p.lr_vec);
+              const float pe = dv[x >> 2][x & 3];
+              t = float4{fmaf(pe, cv.x, t.x), fmaf(pe, cv.y, t.y), fmaf(pe, cv.z, t.z), fmaf(pe, cv.w, t.w)};
+            }
+            t = sum_groups4(t);
+            if (g == 0 && row_ok) {
+              const int rem = min(4, p.Rm - c0);
+              if (dM) {
+                const float4 dcv = ld_r4(dcp + c0, rem, p.lr_vec);
+                float* dst = dM + dstoff * p.Rm + c0;
+                dst[0] = fmaf(p.m_scale * dcv.x, t.x, dst[0]);
+                if (rem > 1) dst[1] = fmaf(p.m_scale * dcv.y, t.y, dst[1]);
+                if (rem > 2) dst[2] = fmaf(p.m_scale * dcv.z, t.z, dst[2]);
+                if (rem > 3) dst[3] = fmaf(p.m_scale * dcv.w, t.w, dst[3]);
+              }
+              if constexpr (ROLE == kRoleQ) {
+                if (p.coeff) {
+                  const float4 mv = ld_r4(mlrow + c0, rem, p.lr_vec);
+                  float* cl = coeffL + (wave * 16 + r16) * p.RmP + c0;
+                  cl[0] = fmaf(mv.x, t.x, cl[0]);
+                  cl[1] = fmaf(mv.y, t.y, cl[1]);
+                  cl[2] = fmaf(mv.z, t.z, cl[2]);
+                  cl[3] = fmaf(mv.w, t.w, cl[3]);
+                }
+              }
+            }
+          }
         }
       }
 
@@ -726,6 +916,20 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
     if (out_a) out_a[orow * D + d] = va;
     if (out_b) out_b[orow * D + d] = vb;
   }
+  if constexpr (LR && ROLE == kRoleQ) {
+    if (p.al && p.dag) {
+      const float dg = wave_sum(gacc_a);
+      if (lane == 0) p.dag[orow] = p.a_scale * dg;
+    }
+    if (p.ml && p.coeff) {
+      __builtin_amdgcn_wave_barrier();  // the row lanes' partials (LDS, this wave's own) are written
+      for (int r = lane; r < p.Rm; r += 64) {
+        float c = 0.0f;
+        for (int x = 0; x < 16; ++x) c += coeffL[(wave * 16 + x) * p.RmP + r];
+        p.coeff[orow * p.Rm + r] = c;
+      }
+    }
+  }
   if constexpr (ROLE == kRoleQ) {
     if (has_bias) {
       const float dg = wave_sum(gacc);
@@ -742,22 +946,66 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
 // B H OB).  The roles write disjoint gradients, so they may run
 // concurrently, and one launch lets the uneven blocks of the three roles
 // (work grows with the cube of a molecule's size) fill each other's tails.
-template <int DP, bool M16, bool BIAS>
-__global__ void __launch_bounds__((Shape<DP, M16>::kThreads), (Shape<DP, M16>::kMinBlocks)) simplicial_bwd_kernel(Params p) {
+template <int DP, bool M16, bool BIAS, bool LR>
+__global__ void __launch_bounds__((Shape<DP, M16, LR>::kThreads), (Shape<DP, M16, LR>::kMinBlocks)) simplicial_bwd_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int G = p.B * p.H * p.OB;
   const int role = blockIdx.x / G;
   const int blk = blockIdx.x - role * G;
   const int bh = blk / p.OB;
   const int ob = blk - bh * p.OB;
-  if (role == kRoleQ) run_role<DP, kRoleQ, M16, BIAS>(p, smem, bh, ob);
-  else if (role == kRoleJ) run_role<DP, kRoleJ, M16, BIAS>(p, smem, bh, ob);
-  else run_role<DP, kRoleK, M16, BIAS>(p, smem, bh, ob);
+  if (role == kRoleQ) run_role<DP, kRoleQ, M16, BIAS, LR>(p, smem, bh, ob);
+  else if (role == kRoleJ) run_role<DP, kRoleJ, M16, BIAS, LR>(p, smem, bh, ob);
+  else run_role<DP, kRoleK, M16, BIAS, LR>(p, smem, bh, ob);
 }
 
-template <int DP, bool M16>
+// dc[row][r] = basis[h][r] . go[row] for every row of [B*H, N] (message term), and coeff[row][r] = 0:
+// one thread per (row, r).
+__global__ void __launch_bounds__(256) lr_dc_kernel(Params p) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long total = (long long)p.B * p.H * p.N * p.Rm;
+  if (idx >= total) return;
+  const int r = int(idx % p.Rm);
+  const long long row = idx / p.Rm;
+  const int h = int((row / p.N) % p.H);
+  const float* bs = p.mb + (size_t(h) * p.Rm + r) * p.D;
+  float acc = 0.0f;
+  for (int d = 0; d < p.D; ++d) acc = fmaf(bs[d], ld1(p.go, size_t(row) * p.D + d, p.gdtype), acc);
+  p.dc[idx] = acc;
+  // the per-query coefficients start at 0: queries of a molecule without valid keys get no role-Q wave
+  if (p.coeff) p.coeff[idx] = 0.0f;
+}
+
+// dbasis[h][r][d] = Rm^-1/2 sum over valid (b, i) of coeff[b,h,i][r] go[b,h,i][d]: one workgroup per (h, r);
+// thread t takes d = t % 64 (+ 64 per pass) and every fourth (b, i); the four partial sums meet in a fixed order.
+__global__ void __launch_bounds__(256) lr_dbasis_kernel(Params p, float* dmb) {
+  __shared__ float part[256];
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int t = threadIdx.x;
+  const int dl = t & 63, q4 = t >> 6;
+  const int BN = p.B * p.N;
+  for (int d0 = 0; d0 < p.D; d0 += 64) {
+    const int d = d0 + dl;
+    float acc = 0.0f;
+    if (d < p.D) {
+      for (int u = q4; u < BN; u += 4) {
+        const int b = u / p.N, i = u - b * p.N;
+        if (!p.qv[u]) continue;
+        const size_t row = (size_t(b) * p.H + h) * p.N + i;
+        acc = fmaf(p.coeff[row * p.Rm + r], ld1(p.go, row * p.D + d, p.gdtype), acc);
+      }
+    }
+    part[t] = acc;
+    __syncthreads();
+    if (q4 == 0 && d < p.D)
+      dmb[(size_t(h) * p.Rm + r) * p.D + d] = p.m_scale * (((part[dl] + part[64 + dl]) + part[128 + dl]) + part[192 + dl]);
+    __syncthreads();
+  }
+}
+
+template <int DP, bool M16, bool LR = false>
 int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
-  const size_t lds = Lay<DP, M16>::bytes(prm.NP, has_pv, has_bias);
+  const size_t lds = Lay<DP, M16, LR>::bytes(prm.NP, has_pv, has_bias, (LR && prm.ml && prm.coeff) ? prm.RmP : 0);
   DeviceInfo dev;
   int st = device_info(&dev);
   if (st != MF_OK) return st;
@@ -766,16 +1014,17 @@ int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
                                         std::to_string(lds) + " bytes of LDS per workgroup, the device offers " +
                                         std::to_string(dev.max_lds_per_block));
   using Kern = void (*)(Params);
-  const Kern kerns[2] = {simplicial_bwd_kernel<DP, M16, false>, simplicial_bwd_kernel<DP, M16, true>};
+  const Kern kerns[2] = {simplicial_bwd_kernel<DP, M16, false, LR>, simplicial_bwd_kernel<DP, M16, true, LR>};
   st = ensure_dynamic_lds(reinterpret_cast<const void*>(kerns[has_bias]), 160 * 1024);
   if (st != MF_OK) return st;
   // about 8 workgroups per CU for each role, at most one per kWaves outer indices
   const long long bh = (long long)prm.B * prm.H;
   const long long want = (8LL * dev.num_cus + bh - 1) / bh;
-  prm.OB = int(std::max(1LL, std::min<long long>(want, (prm.N + Shape<DP, M16>::kWaves - 1) / Shape<DP, M16>::kWaves)));
+  constexpr int kW = Shape<DP, M16, LR>::kWaves;
+  prm.OB = int(std::max(1LL, std::min<long long>(want, (prm.N + kW - 1) / kW)));
   const long long blocks = 3 * bh * prm.OB;
   if (blocks > 0x7fffffffLL) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: grid too large");
-  hipLaunchKernelGGL(kerns[has_bias], dim3(unsigned(blocks)), dim3(Shape<DP, M16>::kThreads), lds, stream, prm);
+  hipLaunchKernelGGL(kerns[has_bias], dim3(unsigned(blocks)), dim3(Shape<DP, M16, LR>::kThreads), lds, stream, prm);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
 }
@@ -808,6 +1057,30 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   } else if (a->du || a->dv_bias || a->dw || a->dgate) {
     return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: bias gradients requested without a bias");
   }
+  const bool has_angle = a->angle_left != nullptr;
+  const bool has_msg = a->message_left != nullptr;
+  if (has_angle) {
+    if (!a->angle_right || !a->angle_gate)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: angle_left, angle_right and angle_gate go together");
+    if (a->angle_rank < 1 || a->angle_rank > 64)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: angle_rank must be in 1..64, got " + std::to_string(a->angle_rank));
+  } else if (a->dangle_left || a->dangle_right || a->dangle_gate) {
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: angle gradients requested without an angle term");
+  }
+  if (has_msg) {
+    if (!a->message_right || !a->message_basis)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: message_left, message_right and message_basis go together");
+    if (a->message_rank < 1 || a->message_rank > 64)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: message_rank must be in 1..64, got " + std::to_string(a->message_rank));
+    const uint64_t need = mf_simplicial_bwd_workspace_size(a->batch, a->heads, a->tokens, a->head_dim, a->message_rank);
+    if (a->workspace == nullptr || a->workspace_bytes < need)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: the message term needs " + std::to_string(need) +
+                                               " bytes of workspace (mf_simplicial_bwd_workspace_size)");
+    if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: workspace must be 16-byte aligned");
+  } else if (a->dmessage_left || a->dmessage_right || a->dmessage_basis) {
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: message gradients requested without a message term");
+  }
   Params prm{};
   prm.q = a->q; prm.k1 = a->k1; prm.v1 = a->v1; prm.k2 = a->k2; prm.v2 = a->v2; prm.go = a->grad_out;
   prm.out = a->out; prm.lse = a->lse;
@@ -832,6 +1105,46 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool has_pv = a->pair_valid != nullptr;
   const int D = a->head_dim;
+  if (has_angle || has_msg) {
+    // the rank terms: fp32 arithmetic (the fp32 path) for every operand dtype, 4 waves per workgroup
+    bool lv = true;
+    if (has_angle) {
+      prm.al = a->angle_left; prm.ar = a->angle_right; prm.ag = a->angle_gate;
+      prm.Ra = a->angle_rank;
+      prm.a_scale = 1.0f / std::sqrt(float(a->angle_rank));
+      prm.dal = a->dangle_left; prm.dar = a->dangle_right; prm.dag = a->dangle_gate;
+      lv = lv && a->angle_rank % 4 == 0;
+      for (const void* ptr : {(const void*)a->angle_left, (const void*)a->angle_right})
+        lv = lv && reinterpret_cast<uintptr_t>(ptr) % 16 == 0;
+    }
+    if (has_msg) {
+      prm.ml = a->message_left; prm.mr = a->message_right; prm.mb = a->message_basis;
+      prm.Rm = a->message_rank;
+      prm.RmP = (a->message_rank + 3) / 4 * 4;
+      prm.m_scale = 1.0f / std::sqrt(float(a->message_rank));
+      prm.dml = a->dmessage_left; prm.dmr = a->dmessage_right;
+      prm.dc = static_cast<float*>(a->workspace);
+      prm.coeff = a->dmessage_basis ? prm.dc + size_t(a->batch) * a->heads * a->tokens * a->message_rank : nullptr;
+      lv = lv && a->message_rank % 4 == 0;
+      for (const void* ptr : {(const void*)a->message_left, (const void*)a->message_right})
+        lv = lv && reinterpret_cast<uintptr_t>(ptr) % 16 == 0;
+      const long long total = (long long)a->batch * a->heads * a->tokens * a->message_rank;
+      hipLaunchKernelGGL(lr_dc_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, prm);
+      MF_HIP_CHECK(hipGetLastError());
+    }
+    prm.lr_vec = lv ? 1 : 0;
+    int st;
+    if (D <= 32) st = launch<32, false, true>(prm, has_pv, has_bias, s);
+    else if (D <= 64) st = launch<64, false, true>(prm, has_pv, has_bias, s);
+    else st = launch<128, false, true>(prm, has_pv, has_bias, s);
+    if (st != MF_OK) return st;
+    if (has_msg && a->dmessage_basis) {
+      hipLaunchKernelGGL(lr_dbasis_kernel, dim3(unsigned(a->heads), unsigned(a->message_rank)), dim3(256), 0, s, prm,
+                         a->dmessage_basis);
+      MF_HIP_CHECK(hipGetLastError());
+    }
+    return MF_OK;
+  }
   // bf16 operands and a bf16 grad_out: bf16 MFMA (K steps of 32 d), which stages grad_out rows as bf16 (exact
   // only for a bf16 grad_out).  Everything else -- fp16 operands, or a grad_out of another dtype -- takes the
   // fp32 path, which reads every operand in its own dtype.
@@ -844,4 +1157,12 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   if (D <= 32) return launch<32, false>(prm, has_pv, has_bias, s);
   if (D <= 64) return launch<64, false>(prm, has_pv, has_bias, s);
   return launch<128, false>(prm, has_pv, has_bias, s);
+}
+
+extern "C" uint64_t mf_simplicial_bwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                                                     int32_t message_rank) {
+  (void)head_dim;
+  if (batch <= 0 || heads <= 0 || tokens <= 0 || message_rank <= 0) return 0;
+  // dc and the per-query coefficients, [B*H, N, Rm] fp32 each
+  return 2ull * uint64_t(batch) * uint64_t(heads) * uint64_t(tokens) * uint64_t(message_rank) * 4ull;
 }

@@ -334,15 +334,17 @@ def hip_simplicial_attention_backward(
 ):
     """Returns the 15-tuple of triton_simplicial_attention.py:963-979 (None for grads not needed or absent).
 
-    Without low-rank angle / message terms the gradients come from the
-    deterministic HIP entry point ``mf_simplicial_bwd`` (bitwise reproducible;
-    bf16 MFMA for bf16 operands, rounding only the score products to bf16 as
-    the reference's backward rounds them to the input type; fp32 MFMA for
-    fp32 and fp16 operands).  Calls with angle or message terms, and shapes
-    beyond that kernel's LDS capacity (the library reports them), recompute
-    the forward with the fp32-core torch path on the same device and take its
-    autograd gradients -- the reference's own ``debug_torch_backward`` route
-    (simplicial_attention.py:454-552).  ``last_backward_impl`` records which
+    The gradients come from the deterministic HIP entry point ``mf_simplicial_bwd``
+    (bitwise reproducible; bf16 MFMA for bf16 operands without angle / message
+    terms, rounding the score products to bf16 as the reference's backward rounds
+    them to the input type and carrying the value products as bf16 hi + lo; fp32
+    MFMA for fp32 and fp16 operands and for every call with low-rank angle or
+    message terms, whose gradients -- dangle_left/right/gate, dmessage_left/right/
+    basis, triton_simplicial_attention.py:488-515,575-782 -- the kernel computes
+    too).  Shapes beyond that kernel's LDS capacity (the library reports them)
+    recompute the forward with the fp32-core torch path on the same device and
+    take its autograd gradients -- the reference's own ``debug_torch_backward``
+    route (simplicial_attention.py:454-552).  ``last_backward_impl`` records which
     of the two ran ("hip" or "torch_recompute").
     """
     global last_backward_impl
@@ -350,13 +352,12 @@ def hip_simplicial_attention_backward(
                  need_dangle_left=need_dangle_left, need_dangle_right=need_dangle_right,
                  need_dangle_gate=need_dangle_gate, need_dmessage_left=need_dmessage_left,
                  need_dmessage_right=need_dmessage_right, need_dmessage_basis=need_dmessage_basis)
-    has_low_rank = angle_left is not None or message_left is not None
-    if not has_low_rank:
-        result = _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_key_valid, pair_valid,
-                                  u, v_bias, w, gate, flags)
-        if result is not None:
-            last_backward_impl = "hip"
-            return result
+    result = _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_key_valid, pair_valid,
+                              u, v_bias, w, gate, angle_left, angle_right, angle_gate, message_left, message_right,
+                              message_basis, flags)
+    if result is not None:
+        last_backward_impl = "hip"
+        return result
     last_backward_impl = "torch_recompute"
     return _recompute_backward(grad_out, q, k1, v1, k2, v2, query_valid=query_valid,
                                pair_key_valid=pair_key_valid, pair_valid=pair_valid, u=u, v_bias=v_bias, w=w,
@@ -369,7 +370,8 @@ last_backward_impl: str | None = None
 
 
 def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_key_valid, pair_valid,
-                     u, v_bias, w, gate, flags):
+                     u, v_bias, w, gate, angle_left, angle_right, angle_gate, message_left, message_right,
+                     message_basis, flags):
     """mf_simplicial_bwd; None when the library reports the shape as beyond its capacity."""
     if not HIP_AVAILABLE:
         raise RuntimeError(f"HIP simplicial attention is unavailable: {_native.load_error()}")
@@ -391,7 +393,8 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
     pv = None if pair_valid is None else pair_valid.to(device=dev, dtype=torch.bool).contiguous()
     if tuple(qv.shape) != (B, N) or tuple(pkv.shape) != (B, N) or (pv is not None and tuple(pv.shape) != (B, N, N)):
         raise ValueError("query_valid / pair_key_valid must be (B, N) and pair_valid (B, N, N)")
-    ext = _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, None, None, None, None, None, None)
+    ext = _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, angle_left, angle_right, angle_gate,
+                          message_left, message_right, message_basis)
     grads = [torch.zeros(B, H, N, D, device=dev, dtype=torch.float32) for _ in range(5)]
     bias_grads = [None] * 4
     if ext.bias is not None:
@@ -399,6 +402,26 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
                                              ("need_dw", (B, H, N, N)), ("need_dgate", (B, H, N)))):
             if flags[name]:
                 bias_grads[idx] = torch.zeros(shape, device=dev, dtype=torch.float32)
+    # low-rank gradients: (dangle_left, dangle_right, dangle_gate), (dmessage_left, dmessage_right, dmessage_basis)
+    lr_grads: list[torch.Tensor | None] = [None] * 6
+    if ext.angle is not None:
+        ra = int(ext.angle[0].shape[-1])
+        for idx, (name, shape) in enumerate((("need_dangle_left", (B, H, N, N, ra)),
+                                             ("need_dangle_right", (B, H, N, N, ra)),
+                                             ("need_dangle_gate", (B, H, N)))):
+            if flags[name]:
+                lr_grads[idx] = torch.zeros(shape, device=dev, dtype=torch.float32)
+    workspace = None
+    rm = 0
+    if ext.message is not None:
+        rm = int(ext.message[0].shape[-1])
+        for idx, (name, shape) in enumerate((("need_dmessage_left", (B, H, N, N, rm)),
+                                             ("need_dmessage_right", (B, H, N, N, rm)),
+                                             ("need_dmessage_basis", (H, rm, D)))):
+            if flags[name]:
+                lr_grads[3 + idx] = torch.zeros(shape, device=dev, dtype=torch.float32)
+        nbytes = int(_native.lib().mf_simplicial_bwd_workspace_size(B, H, N, D, rm))
+        workspace = torch.empty(nbytes, device=dev, dtype=torch.uint8)
     f = ext.fields()
     args = _native.MfSimplicialBwdArgs(
         q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(), k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
@@ -409,7 +432,15 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
         dq=grads[0].data_ptr(), dk1=grads[1].data_ptr(), dv1=grads[2].data_ptr(), dk2=grads[3].data_ptr(),
         dv2=grads[4].data_ptr(), du=_native.ptr(bias_grads[0]), dv_bias=_native.ptr(bias_grads[1]),
         dw=_native.ptr(bias_grads[2]), dgate=_native.ptr(bias_grads[3]),
-        batch=B, heads=H, tokens=N, head_dim=D, dtype=_native.dtype_code(dt), reserved=0)
+        batch=B, heads=H, tokens=N, head_dim=D, dtype=_native.dtype_code(dt), reserved=0,
+        angle_rank=f.get("angle_rank", 0), message_rank=f.get("message_rank", 0),
+        angle_left=f.get("angle_left"), angle_right=f.get("angle_right"), angle_gate=f.get("angle_gate"),
+        message_left=f.get("message_left"), message_right=f.get("message_right"),
+        message_basis=f.get("message_basis"),
+        dangle_left=_native.ptr(lr_grads[0]), dangle_right=_native.ptr(lr_grads[1]),
+        dangle_gate=_native.ptr(lr_grads[2]), dmessage_left=_native.ptr(lr_grads[3]),
+        dmessage_right=_native.ptr(lr_grads[4]), dmessage_basis=_native.ptr(lr_grads[5]),
+        workspace=_native.ptr(workspace), workspace_bytes=0 if workspace is None else workspace.numel())
     lib = _native.lib()
     with torch.cuda.device(dev):
         status = lib.mf_simplicial_bwd(args, _native.current_stream(dev))
@@ -422,6 +453,9 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
         for idx, src in enumerate((u, v_bias, w, gate)):
             if bias_grads[idx] is not None:
                 optional[idx] = bias_grads[idx].to(src.dtype)
+    for idx, src in enumerate((angle_left, angle_right, angle_gate, message_left, message_right, message_basis)):
+        if lr_grads[idx] is not None:
+            optional[4 + idx] = lr_grads[idx].to(src.dtype)
     return (*core, *optional)
 
 

@@ -16,7 +16,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "mf_capi.h"
 
 def declared_functions() -> list[str]:
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mf_[a-z0-9_]+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*|uint64_t)\s+(mf_[a-z0-9_]+)\s*\(", text, flags=re.M)))
 
 
 def test_library_is_built_and_loads():
@@ -86,3 +86,68 @@ def test_geometry_entry_points_validate_sizes_before_any_device_call():
     assert "float16/bfloat16" in _native.last_error()
     t.dtype, t.head_dim = _native.MF_DTYPE_BF16, 48
     assert lib.mf_radius_attn(t, None) == _native.MF_ERR_UNSUPPORTED and "head_dim" in _native.last_error()
+
+
+STRUCTS = {
+    "mf_simplicial_fwd_args": _native.MfSimplicialFwdArgs,
+    "mf_simplicial_bwd_args": _native.MfSimplicialBwdArgs,
+    "mf_knn_args": _native.MfKnnArgs,
+    "mf_knn_mask_args": _native.MfKnnMaskArgs,
+    "mf_radius_mask_args": _native.MfRadiusMaskArgs,
+    "mf_geometry_args": _native.MfGeometryArgs,
+    "mf_radius_attn_args": _native.MfRadiusAttnArgs,
+    "mf_adaln_rows_args": _native.MfAdalnRowsArgs,
+    "mf_rows_to_heads_args": _native.MfRowsToHeadsArgs,
+    "mf_heads_to_rows_args": _native.MfHeadsToRowsArgs,
+    "mf_pair_mlp_args": _native.MfPairMlpArgs,
+}
+
+
+def test_ctypes_structs_match_the_header_layout(tmp_path):
+    """Every argument struct of the ctypes binding has the C compiler's size and field offsets (gcc on the
+    header itself), so a field added on one side only fails here, not as a wrong pointer on the GPU."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "mf_capi.h"', "int main(void) {"]
+    for cname, py in STRUCTS.items():
+        lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for fname, *_ in py._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        cname, fname, val = line.split()
+        got[(cname, fname)] = int(val)
+    for cname, py in STRUCTS.items():
+        assert got[(cname, "sizeof")] == ctypes.sizeof(py), cname
+        for fname, *_ in py._fields_:
+            assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
+
+
+def test_backward_low_rank_arguments_are_validated_before_any_device_call():
+    lib = _native.lib()
+    fake = 1 << 20  # never dereferenced: every call below fails validation first
+    a = _native.MfSimplicialBwdArgs(q=fake, k1=fake, v1=fake, k2=fake, v2=fake, grad_out=fake, out=fake, lse=fake,
+                                    query_valid=fake, pair_key_valid=fake, batch=2, heads=2, tokens=8, head_dim=16,
+                                    dtype=_native.MF_DTYPE_F32, grad_dtype=_native.MF_DTYPE_F32)
+    a.dangle_left = fake
+    assert lib.mf_simplicial_bwd(a, None) == _native.MF_ERR_INVALID_ARGUMENT
+    assert "without an angle term" in _native.last_error()
+    a.dangle_left = None
+    a.angle_left, a.angle_right, a.angle_gate, a.angle_rank = fake, fake, fake, 65
+    assert lib.mf_simplicial_bwd(a, None) == _native.MF_ERR_INVALID_ARGUMENT and "angle_rank" in _native.last_error()
+    a.angle_left = None
+    a.message_left, a.message_right, a.message_basis, a.message_rank = fake, fake, fake, 8
+    need = lib.mf_simplicial_bwd_workspace_size(2, 2, 8, 16, 8)
+    assert need == 2 * 2 * 2 * 8 * 8 * 4
+    assert lib.mf_simplicial_bwd_workspace_size(2, 2, 8, 16, 0) == 0
+    a.workspace, a.workspace_bytes = fake, need - 4
+    assert lib.mf_simplicial_bwd(a, None) == _native.MF_ERR_INVALID_ARGUMENT and "workspace" in _native.last_error()

@@ -228,8 +228,8 @@ def test_only_requested_bias_gradients_are_returned(cuda):
     assert res[5] is None and res[7] is None and res[6] is not None and res[8] is not None
 
 
-def test_low_rank_terms_use_the_recompute(cuda):
-    """Angle / message gradients are not in the kernel: the backward takes the fp32-core recompute."""
+def test_low_rank_terms_run_on_the_kernel(cuda):
+    """Angle / message gradients come from mf_simplicial_bwd, not from a torch recompute."""
     B, H, N, D = 1, 2, 6, 8
     q, k1, v1, k2, v2 = (torch.randn(B, H, N, D, device=cuda) for _ in range(5))
     ones = torch.ones(B, N, dtype=torch.bool, device=cuda)
@@ -241,5 +241,5 @@ def test_low_rank_terms_use_the_recompute(cuda):
     res = hip_simplicial_attention_backward(torch.randn_like(q), q, k1, v1, k2, v2, out32, lse, query_valid=ones,
                                             pair_key_valid=ones, pair_valid=None, angle_left=al, angle_right=ar,
                                             angle_gate=ag, precision="ieee_fp32")
-    assert hsa.last_backward_impl == "torch_recompute"
+    assert hsa.last_backward_impl == "hip"
     assert res[9] is not None and res[11] is not None

@@ -125,8 +125,8 @@ def test_packed_trunk_matches_padded_and_graph_replays(cuda):
     trunk = build_trunk(z).to(cuda).to(torch.bfloat16).eval()
     x, cond, coords, pad = inputs(z)
     x, cond, coords, pad = x.to(cuda, torch.bfloat16), cond.to(cuda, torch.bfloat16), coords.to(cuda), pad.to(cuda)
-    assert trunk.packable(x)
-    with torch.no_grad():
+    with torch.no_grad():  # under autograd the kNN-local blocks take the torch path, so nothing packs
+        assert trunk.packable(x)
         packed = trunk(x, cond, coords, pad)
         trunk.pack_tokens = False
         padded = trunk(x, cond, coords, pad)
@@ -178,9 +178,9 @@ def test_geometry_trunk_packed_hip_matches_cpu(cuda, mode, message, precision):
         want = trunk(x, cond, coords, pad, sigma=sigma)
     trunk = trunk.to(cuda)
     x, cond, coords, pad, sigma = (t.to(cuda) for t in (x, cond, coords, pad, sigma))
-    terms = trunk.simplicial_terms(coords, pad, sigma=sigma)
-    assert trunk.packable(x, terms)
     with torch.no_grad():
+        terms = trunk.simplicial_terms(coords, pad, sigma=sigma)
+        assert trunk.packable(x, terms)
         packed = trunk(x, cond, coords, pad, sigma=sigma)
         trunk.pack_tokens = False
         padded = trunk(x, cond, coords, pad, sigma=sigma)
