@@ -823,11 +823,89 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     }
   }
   ClaimState* cl = reinterpret_cast<ClaimState*>(smem + Ly::kClaim);
+  // K rows: row-major fp16 scaled by 2^sc_exp
+  auto store_k = [&](unsigned char* dst, const uint4& v, int row, int sc_exp) {
+    float f[8];
+    uint32_t w[4];
+    unpack8<T>(v, f);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = pack_h2(ldexpf(f[2 * e], sc_exp), ldexpf(f[2 * e + 1], sc_exp));
+    *reinterpret_cast<uint4*>(dst + row * RB + e0 * 2) = uint4{w[0], w[1], w[2], w[3]};
+  };
+  // V rows: [row][r16][dt]: column d = 16 dt + r16 at half r16 ND + dt
+  auto store_v = [&](unsigned char* dst, const uint4& v, int row, int sc_exp) {
+    float f[8];
+    unpack8<T>(v, f);
+    unsigned char* a = dst + row * RB + ((8 * (cc & 1)) * ND + (cc >> 1)) * 2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      *reinterpret_cast<_Float16*>(a + e * ND * 2) = _Float16(ldexpf(f[e], sc_exp));
+  };
+  // bits of pair_valid for rows j of the j block and keys k of the k block
+  auto stage_pv = [&](int jc, int kc) {
+    uint32_t* pvb = reinterpret_cast<uint32_t*>(smem + Ly::kPV);
+    const uint8_t* gpv = p.pv + size_t(b) * N * N;
+    const int j0 = jc * kCap, k0 = kc * kCap;
+    const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
+    for (int u = tid; u < kCap * (kCap / 32); u += kThreads) {
+      const int jl = u / (kCap / 32), wd = u % (kCap / 32);
+      uint32_t bits = 0;
+      if (jl < nkj) {
+        const uint8_t* prow = gpv + size_t(key_atom(j0 + jl)) * N;
+        for (int t = 0; t < 32; ++t) {
+          const int kl = wd * 32 + t;
+          if (kl < nkk && prow[key_atom(k0 + kl)] != 0) bits |= 1u << t;
+        }
+      }
+      pvb[u] = bits;
+    }
+  };
+  // GUESS: the unit is staged with unit scales (K, V as they are, Q as q log2(e)) straight from the loads,
+  // before the maxima are known; after the one barrier every wave checks the maxima against the range in
+  // which unit scales give the results of the normalised scales (every staged value, product and P stays
+  // a normal fp16 number, and fp16 rounding is scale-invariant there) and against a looser |S| bound,
+  // max_i ||q'_i||_1 max|K1| max|K2|.  A unit outside it is staged again the normalised way.
+  constexpr bool GUESS = !MULTI && !BIAS;
+  float ql1 = 0.0f;  // GUESS: the largest ||q'_i||_1 of this wave's query rows
   if constexpr (!MULTI) {
     load_block(0, 0);
     // the workgroup's share of padded query rows, stored while the loads are
     // in flight (first unit only)
     if (zero_share) zero_padded_share<T, DP, STR>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
+    if constexpr (GUESS) {
+      const int rj = round16(nk);
+#pragma unroll
+      for (int i = 0; i < MAXC; ++i) {
+        if (i >= nI) break;
+        const int row = (tid + kThreads * i) / CPR;
+        if (row < rj) {
+          store_k(smem + Ly::kK1, rk1[i], row, 0);
+          store_v(smem + Ly::kV1, rv1[i], row, 0);
+          store_k(smem + Ly::kK2, rk2[i], row, 0);
+          store_v(smem + Ly::kV2, rv2[i], row, 0);
+        }
+      }
+      if constexpr (HAS_PV) stage_pv(0, 0);
+      unsigned char* Qs = smem + Ly::kQ;
+#pragma unroll
+      for (int i = 0; i < MAXQC; ++i) {
+        const int row = (tid + kThreads * i) / CPR;
+        float f[8];
+        unpack8<T>(rq[i], f);
+        float l1 = 0.0f;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          f[e] *= kLog2e;
+          l1 += fabsf(f[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = pack_h2(f[2 * e], f[2 * e + 1]);
+        if (row < kMaxQ) *reinterpret_cast<uint4*>(Qs + row * RB + e0 * 2) = uint4{w[0], w[1], w[2], w[3]};
+        l1 = __uint_as_float(group_reduce<CPR>(__float_as_uint(l1), AddF32{}));
+        ql1 = fmaxf(ql1, row < nqg ? l1 : 0.0f);
+      }
+    }
     acc_max();
   } else {
     if (zero_share) zero_padded_share<T, DP, STR>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
@@ -853,6 +931,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     }
     gv = group_reduce<64>(gv, PkMaxU16{});
     gqm = group_reduce<64>(gqm, PkMaxU16{});
+    if constexpr (GUESS) ql1 = __uint_as_float(group_reduce<64>(__float_as_uint(ql1), MaxF32{}));
     uint32_t* colw = reinterpret_cast<uint32_t*>(colmax);  // [kWaves][2][DP / 2] packed pairs
     if (lane < CPR) {
 #pragma unroll
@@ -865,10 +944,45 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       uint32_t* gw = reinterpret_cast<uint32_t*>(gmax);
       gw[wave * 4 + 0] = gv;
       gw[wave * 4 + 1] = gqm;
+      gw[wave * 4 + 2] = __float_as_uint(ql1);
     }
   }
   __syncthreads();
-  if (wave == 0) {
+  // GUESS: every wave combines the partials (the same values in every wave, so every wave takes the same
+  // branch) and keeps the unit-scale staging when it is valid
+  bool staged = false;
+  if constexpr (GUESS) {
+    const uint32_t* colw = reinterpret_cast<const uint32_t*>(colmax);
+    const uint32_t* gw = reinterpret_cast<const uint32_t*>(gmax);
+    float m1 = 0.0f, m2 = 0.0f;
+    if (lane < DP) {
+      uint32_t w1 = 0u, w2 = 0u;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        w1 = max(w1, (colw[(w * 2 + 0) * (DP / 2) + lane / 2] >> (16 * (lane & 1))) & 0xffffu);
+        w2 = max(w2, (colw[(w * 2 + 1) * (DP / 2) + lane / 2] >> (16 * (lane & 1))) & 0xffffu);
+      }
+      m1 = mag_to_float<T>(w1);
+      m2 = mag_to_float<T>(w2);
+    }
+    const float a1 = __uint_as_float(group_reduce<64>(__float_as_uint(m1), MaxF32{}));
+    const float a2 = __uint_as_float(group_reduce<64>(__float_as_uint(m2), MaxF32{}));
+    uint32_t v = 0u, qm = 0u;
+    float qn = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      v = pk_max_u16(v, gw[w * 4 + 0]);
+      qm = pk_max_u16(qm, gw[w * 4 + 1]);
+      qn = fmaxf(qn, __uint_as_float(gw[w * 4 + 2]));
+    }
+    const float b1 = mag_to_float<T>(v & 0xffffu), b2 = mag_to_float<T>(v >> 16);
+    const float bq = fmaxf(mag_to_float<T>(qm & 0xffffu), mag_to_float<T>(qm >> 16));
+    // unit scale is the normalised one up to a factor 2^s, |s| <= 3, for every operand
+    auto in_range = [](float a) { return a == 0.0f || (a >= 0.125f && a < 16.0f); };
+    staged = in_range(a1) && in_range(a2) && in_range(b1) && in_range(b2) && bq * kLog2e < kQLimit &&
+             qn * (a1 * a2) <= kBoundLimit;
+  }
+  if (!staged && wave == 0) {
     const uint32_t* colw = reinterpret_cast<const uint32_t*>(colmax);
     float m1 = 0.0f, m2 = 0.0f;
     if (lane < DP) {
@@ -912,8 +1026,9 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       scal[6] = E != 0 ? 1 : 0;  // two-pass flag (queries add theirs)
     }
   }
-  __syncthreads();
-  const int s1 = scal[0], s2 = scal[1], t1 = scal[2], t2 = scal[3], sq = scal[4], E = scal[5];
+  if (!staged) __syncthreads();
+  const int s1 = staged ? 0 : scal[0], s2 = staged ? 0 : scal[1], t1 = staged ? 0 : scal[2];
+  const int t2 = staged ? 0 : scal[3], sq = staged ? 0 : scal[4], E = staged ? 0 : scal[5];
 
   // ---- factorized bias (BIAS): c_i, then the fp16 operands of a block ------
   float* cgf = reinterpret_cast<float*>(smem + Ly::kBG);
@@ -1058,7 +1173,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   const float bias_mag = BIAS ? bmax[0] + bmax[1] + bmax[2] : 0.0f;
 
   // ---- phase B: query rows, bounds ---------------------------------------
-  {
+  if (!staged) {
     unsigned char* Qs = smem + Ly::kQ;
     const float4 mlo = *reinterpret_cast<const float4*>(mn + e0);
     const float4 mhi = *reinterpret_cast<const float4*>(mn + e0 + 4);
@@ -1096,24 +1211,6 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     unsigned char* V2s = smem + Ly::kV2;
     const int nkj = min(kCap, nk - jc * kCap), nkk = min(kCap, nk - kc * kCap);
     const int rj = round16(nkj), rk = round16(nkk);
-    // K rows: row-major fp16
-    auto store_k = [&](unsigned char* dst, const uint4& v, int row, int sc_exp) {
-      float f[8];
-      uint32_t w[4];
-      unpack8<T>(v, f);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = pack_h2(ldexpf(f[2 * e], sc_exp), ldexpf(f[2 * e + 1], sc_exp));
-      *reinterpret_cast<uint4*>(dst + row * RB + e0 * 2) = uint4{w[0], w[1], w[2], w[3]};
-    };
-    // V rows: [row][r16][dt]: column d = 16 dt + r16 at half r16 ND + dt
-    auto store_v = [&](unsigned char* dst, const uint4& v, int row, int sc_exp) {
-      float f[8];
-      unpack8<T>(v, f);
-      unsigned char* a = dst + row * RB + ((8 * (cc & 1)) * ND + (cc >> 1)) * 2;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<_Float16*>(a + e * ND * 2) = _Float16(ldexpf(f[e], sc_exp));
-    };
     if constexpr (!MULTI) {
       // the rows loaded in phase A
 #pragma unroll
@@ -1155,24 +1252,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         if ((tid + kThreads * i) / CPR < rk) store_v(V2s, t[i], (tid + kThreads * i) / CPR, t2);
     }
     if constexpr (BIAS && MULTI) stage_bias(jc, kc);
-    if constexpr (HAS_PV) {
-      // bits of pair_valid for rows j of the j block and keys k of the k block
-      uint32_t* pvb = reinterpret_cast<uint32_t*>(smem + Ly::kPV);
-      const uint8_t* gpv = p.pv + size_t(b) * N * N;
-      const int j0 = jc * kCap, k0 = kc * kCap;
-      for (int u = tid; u < kCap * (kCap / 32); u += kThreads) {
-        const int jl = u / (kCap / 32), wd = u % (kCap / 32);
-        uint32_t bits = 0;
-        if (jl < nkj) {
-          const uint8_t* prow = gpv + size_t(key_atom(j0 + jl)) * N;
-          for (int t = 0; t < 32; ++t) {
-            const int kl = wd * 32 + t;
-            if (kl < nkk && prow[key_atom(k0 + kl)] != 0) bits |= 1u << t;
-          }
-        }
-        pvb[u] = bits;
-      }
-    }
+    if constexpr (HAS_PV) stage_pv(jc, kc);
   };
 
   // ---- phase C: pair loop -------------------------------------------------
@@ -1218,9 +1298,11 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   };
   bool slow = false;
   if (!MULTI && nch == 1) {
-    store_block(0, 0);
-    __syncthreads();
-    slow = scal[6] != 0;
+    if (!staged) {
+      store_block(0, 0);
+      __syncthreads();
+      slow = scal[6] != 0;
+    }
     load_qop();
     if (!slow) {
       pair_loop_n<DP, kFast, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
