@@ -65,8 +65,14 @@
 namespace mf {
 namespace spair {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
+// Waves per workgroup W: 4 with two workgroups per CU, 8 with one (the bias
+// instantiations, whose extra LDS allows one workgroup per CU: 8 waves keep
+// two waves on every SIMD, which the pair loop needs to overlap MFMA and VALU).
+template <bool BIAS>
+struct Waves {
+  static constexpr int kCount = BIAS ? 8 : 4;
+};
+constexpr int kRedWaves = 4;          // partial-output slots of the final reduction
 constexpr int kCap = 128;             // keys per staged block (one row per 2 threads)
 constexpr int kMaxQ = 48;             // queries per unit
 constexpr int kMaxBatch = 256;        // molecules per launch
@@ -128,9 +134,10 @@ __device__ __forceinline__ int claimed_position(unsigned int* counter, unsigned 
   return int(gridDim.x) + int(ticket);
 }
 
-// LDS layout (bytes) for padded head dim DP.
-template <int DP>
+// LDS layout (bytes) for padded head dim DP and W waves.
+template <int DP, int W>
 struct Lay {
+  static constexpr int kWaves = W;
   static constexpr int RB = DP * 2;  // bytes per staged fp16 row
   static constexpr int kK1 = 0;
   static constexpr int kK2 = kK1 + kCap * RB;
@@ -153,12 +160,13 @@ struct Lay {
   static constexpr int kM = kScal + 8 * 4;      // float [kMaxQ] two-pass maxima (log2 units)
   static constexpr int kClaim = kM + kMaxQ * 4;  // ClaimState
   static constexpr int kTotal = kClaim + int(sizeof(ClaimState));
-  // after the pair loop: per-wave partial outputs float [kWaves][kMaxQ][RS]
-  // and denominators float [kWaves][kMaxQ], over K1s .. V2s
+  // after the pair loop: partial outputs float [kRedWaves][kMaxQ][RS] and
+  // denominators float [kRedWaves][kMaxQ], over K1s .. V2s (with 8 waves,
+  // waves 4..7 add theirs into waves 0..3 through the same area first)
   static constexpr int RS = DP + 4;
   static constexpr int kRed = 0;
-  static constexpr int kRedL = kRed + kWaves * kMaxQ * RS * 4;
-  static_assert(kRedL + kWaves * kMaxQ * 4 <= kQ, "reduction area must fit in the K/V staging area");
+  static constexpr int kRedL = kRed + kRedWaves * kMaxQ * RS * 4;
+  static_assert(kRedL + kRedWaves * kMaxQ * 4 <= kQ, "reduction area must fit in the K/V staging area");
   // BIAS instantiations, after the above: fp16 bias operands of the unit's (j block, k block)
   //   BU [kCap][kMaxQ]     c_i u_ij (row j, query i)
   //   BW [kCap][kCap]      w_jk
@@ -400,7 +408,8 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
                                           const uint4 (&qop)[MQ][DP / 32], const float (&negm)[MQ], float sc,
                                           mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
                                           int g, int r16) {
-  using Ly = Lay<DP>;
+  constexpr int W = Waves<BIAS>::kCount;
+  using Ly = Lay<DP, W>;
   constexpr int RB = Ly::RB;
   constexpr int NCH = Shape<DP>::NCH;
   constexpr int ND = Shape<DP>::ND;
@@ -412,8 +421,8 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
   const int nkt = (nkk + 15) >> 4;
   const int njp = (nkj + 1) >> 1;
   const int total = nkt * njp;
-  int it = (wave * total) >> 2;
-  const int it1 = ((wave + 1) * total) >> 2;
+  int it = (wave * total) / W;
+  const int it1 = ((wave + 1) * total) / W;
   const bool odd = (nkj & 1) != 0;
   constexpr uint32_t kOne2 = 0x3c003c00u;  // fp16 (1, 1)
   const mf_f32x4 zero4 = mf_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -421,9 +430,9 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
   // mask of the B halves that carry v (K in [2, 18)), and c_i as fp16 per query tile
   uint4 onehot{0u, 0u, 0u, 0u}, vmask{0u, 0u, 0u, 0u};
   uint32_t cgh[MQ];
-  const unsigned char* BU = smem + Lay<DP>::kBU;
-  const unsigned char* BW = smem + Lay<DP>::kBW;
-  const unsigned char* BV = smem + Lay<DP>::kBV;
+  const unsigned char* BU = smem + Ly::kBU;
+  const unsigned char* BW = smem + Ly::kBW;
+  const unsigned char* BV = smem + Ly::kBV;
   if constexpr (BIAS) {
     uint32_t oh[4], vm[4];
 #pragma unroll
@@ -441,7 +450,7 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
     }
     onehot = uint4{oh[0], oh[1], oh[2], oh[3]};
     vmask = uint4{vm[0], vm[1], vm[2], vm[3]};
-    const float* cg = reinterpret_cast<const float*>(smem + Lay<DP>::kBG);
+    const float* cg = reinterpret_cast<const float*>(smem + Ly::kBG);
 #pragma unroll
     for (int qt = 0; qt < MQ; ++qt)
       cgh[qt] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(cg[16 * qt + r16])));
@@ -485,7 +494,7 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
       // halves k0 + 8g .. k0 + 8g + 7 of the query's BV row are K = 8g .. 8g + 7 (v at k + 2)
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
-        const uint4 t = *reinterpret_cast<const uint4*>(BV + ((16 * qt + r16) * Lay<DP>::kVS + k0 + 8 * g) * 2);
+        const uint4 t = *reinterpret_cast<const uint4*>(BV + ((16 * qt + r16) * Ly::kVS + k0 + 8 * g) * 2);
         bvop[qt] = uint4{t.x & vmask.x, t.y & vmask.y, t.z & vmask.z, t.w & vmask.w};
       }
     }
@@ -646,8 +655,9 @@ __device__ __forceinline__ void pair_loop_n(int nqt, const unsigned char* smem, 
 // loop, so the group is kept small).
 // Zero the output rows of the padded queries of the (b, h) pairs w, w + G,
 // ... (a workgroup's share; rows of CPR 16-byte chunks, DP / 8 of them).
-template <typename T, int DP, bool STR>
+template <typename T, int DP, bool STR, int W>
 __device__ __forceinline__ void zero_padded_share(const Params& p, const uint32_t* s_info, int w, int G) {
+  constexpr int kThreads = W * 64;
   constexpr int CPR = DP / 8;
   const int N = p.N, D = p.D, H = p.H;
   const int cpr = D / 8;
@@ -691,7 +701,9 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
                                           bool kpre, bool qpre, bool zero_share) {
   constexpr int QT = kMaxQ / 16;       // query tiles held in registers
   const int nqt = (nqg + 15) >> 4;     // query tiles in use
-  using Ly = Lay<DP>;
+  constexpr int kWaves = Waves<BIAS>::kCount;
+  constexpr int kThreads = kWaves * 64;
+  using Ly = Lay<DP, kWaves>;
   constexpr int RB = Ly::RB;
   constexpr int NCH = Shape<DP>::NCH;
   constexpr int ND = Shape<DP>::ND;
@@ -871,7 +883,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     load_block(0, 0);
     // the workgroup's share of padded query rows, stored while the loads are
     // in flight (first unit only)
-    if (zero_share) zero_padded_share<T, DP, STR>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
+    if (zero_share) zero_padded_share<T, DP, STR, Waves<BIAS>::kCount>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
     if constexpr (GUESS) {
       const int rj = round16(nk);
 #pragma unroll
@@ -908,7 +920,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     }
     acc_max();
   } else {
-    if (zero_share) zero_padded_share<T, DP, STR>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
+    if (zero_share) zero_padded_share<T, DP, STR, Waves<BIAS>::kCount>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
     for (int rc = 0; rc < nch; ++rc) {
       int a[MAXC];
       slot_atoms(rc * kCap, min(kCap, nk - rc * kCap), a);
@@ -1344,14 +1356,39 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   __syncthreads();  // every wave is done with K/V (the reduction area aliases them)
   float* red = reinterpret_cast<float*>(smem + Ly::kRed);
   float* redl = reinterpret_cast<float*>(smem + Ly::kRedL);
+  // kRedWaves slots: with 8 waves, wave w + 4 hands its partials to wave w first
+  const int slot = wave & (kRedWaves - 1);
+  auto put_partials = [&]() {
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    if (qt >= nqt) continue;
+    for (int qt = 0; qt < QT; ++qt) {
+      if (qt >= nqt) continue;
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-      *reinterpret_cast<mf_f32x4*>(red + (wave * kMaxQ + 16 * qt + r16) * Ly::RS + 16 * dt + 4 * g) = O[dt][qt];
-    if (g == 0) redl[wave * kMaxQ + 16 * qt + r16] = L[qt][0];
+      for (int dt = 0; dt < ND; ++dt)
+        *reinterpret_cast<mf_f32x4*>(red + (slot * kMaxQ + 16 * qt + r16) * Ly::RS + 16 * dt + 4 * g) = O[dt][qt];
+      if (g == 0) redl[slot * kMaxQ + 16 * qt + r16] = L[qt][0];
+    }
+  };
+  if constexpr (kWaves > kRedWaves) {
+    static_assert(kWaves == 2 * kRedWaves, "two waves per reduction slot");
+    if (wave >= kRedWaves) put_partials();
+    __syncthreads();
+    if (wave < kRedWaves) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        if (qt >= nqt) continue;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+          const mf_f32x4 o2 =
+              *reinterpret_cast<const mf_f32x4*>(red + (slot * kMaxQ + 16 * qt + r16) * Ly::RS + 16 * dt + 4 * g);
+          O[dt][qt] += o2;
+        }
+        // every lane of a query column holds the same denominator in L[qt][0..3]
+        L[qt][0] += redl[slot * kMaxQ + 16 * qt + r16];
+      }
+    }
+    __syncthreads();
   }
+  if (wave < kRedWaves) put_partials();
   __syncthreads();
   constexpr int CPQ = DP / 8;  // 8-column chunks per query
   const float oscale = ldexpf(1.0f, -(t1 + t2));
@@ -1364,7 +1401,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kRedWaves; ++w) {
       l += redl[w * kMaxQ + i];
       const float4 lo = *reinterpret_cast<const float4*>(red + (w * kMaxQ + i) * Ly::RS + c8);
       const float4 hi = *reinterpret_cast<const float4*>(red + (w * kMaxQ + i) * Ly::RS + c8 + 4);
@@ -1460,16 +1497,17 @@ __device__ __forceinline__ void scan_row_global(const uint8_t* row, int a, int e
 // whole molecules (row 2m: key mask of molecule m, row 2m + 1: its query
 // mask); TPR adjacent threads scan one row, each a segment of it, and the
 // segment counts meet over lanes.
-template <int DP>
+template <int DP, int W>
 __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem, uint32_t* s_info) {
+  constexpr int kThreads = W * 64;
   const int tid = threadIdx.x;
   const int B = p.B, N = p.N;
   const int rows = 2 * B;
   // threads per row: a power of two, <= 8, with rows * tpr <= kThreads when rows allow
   const int tpr = rows > kThreads / 2 ? 1 : rows > kThreads / 4 ? 2 : rows > kThreads / 8 ? 4 : 8;
   const int rpp = kThreads / tpr;  // rows per pass (even)
-  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP>::kQ);  // [rpp] counts, then [rpp] last indices
-  static_assert(kMaxQ * Lay<DP>::RB >= kThreads * 2 * 4, "row results must fit in the query staging area");
+  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP, W>::kK2);  // [rpp] counts, then [rpp] last indices
+  static_assert(kCap * Lay<DP, W>::RB >= kThreads * 2 * 4, "row results must fit in the K2 staging area");
   const int seg = (N + tpr - 1) / tpr;
   for (int r0 = 0; r0 < rows; r0 += rpp) {
     const int r = r0 + tid / tpr, sg = tid & (tpr - 1);
@@ -1516,8 +1554,10 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
 // every 4th pair.  s_cu holds the pairs (over the staging area).  The
 // molecule whose positions hold position w (when w < s_pre[B]) writes
 // *s_first = b | (w - its first position) << 16.
+template <int W>
 __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* s_info, uint16_t* s_order, int* s_pre,
                                                uint2* s_cu, int w, int* s_first) {
+  constexpr int kThreads = W * 64;
   const int tid = threadIdx.x;
   const int B = p.B, H = p.H;
   const int B4 = (B + 3) & ~3;
@@ -1564,7 +1604,7 @@ __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* 
 // masks and the attention of the group's queries.  Ends with a barrier.
 template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
 __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, int b, int h, int g, bool zero_share) {
-  using Ly = Lay<DP>;
+  using Ly = Lay<DP, Waves<BIAS>::kCount>;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const uint32_t info = reinterpret_cast<const uint32_t*>(smem + Ly::kInfo)[b];
@@ -1597,8 +1637,9 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
 // the workgroups that finish first take the longest remaining units.
 // BIAS: one workgroup per CU (its bias operands take another ~59 KB of LDS).
 template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
-__global__ void __launch_bounds__(kThreads, BIAS ? 1 : 2) simplicial_pair_kernel(Params p) {
-  using Ly = Lay<DP>;
+__global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, BIAS ? 1 : 2) simplicial_pair_kernel(Params p) {
+  constexpr int W = Waves<BIAS>::kCount;
+  using Ly = Lay<DP, W>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + Ly::kInfo);
   int* s_pre = reinterpret_cast<int*>(smem + Ly::kPre);
@@ -1612,13 +1653,13 @@ __global__ void __launch_bounds__(kThreads, BIAS ? 1 : 2) simplicial_pair_kernel
   const int wg = blockIdx.x;
 
   if (tid == 0) cl->claimed = 0;
-  scan_masks<DP>(p, smem, s_info);  // ends with a barrier
-  rank_molecules(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
+  scan_masks<DP, W>(p, smem, s_info);  // ends with a barrier
+  rank_molecules<W>(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
   const int total = s_pre[B];
 
   // the rows of padded queries: a static share of (b, h) pairs per
   // workgroup, written during its first unit (or at once without one)
-  if (wg >= total) zero_padded_share<T, DP, STR>(p, s_info, wg, G);
+  if (wg >= total) zero_padded_share<T, DP, STR, Waves<BIAS>::kCount>(p, s_info, wg, G);
   for (int pos = wg; pos < total;) {
     int b, i;  // molecule, unit within it
     if (pos == wg) {
@@ -1657,10 +1698,11 @@ template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
 int launch(const Params& prm, int num_cus, hipStream_t stream) {
   const int grid = std::max(8, (BIAS ? 1 : 2) * num_cus);  // 2 workgroups per CU (1 with the bias)
   auto kern = simplicial_pair_kernel<T, DP, HAS_PV, BIAS, STR>;
-  const size_t lds = BIAS ? Lay<DP>::kTotalBias : Lay<DP>::kTotal;
+  constexpr int W = Waves<BIAS>::kCount;
+  const size_t lds = BIAS ? Lay<DP, W>::kTotalBias : Lay<DP, W>::kTotal;
   const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), int(lds));
   if (st != MF_OK) return st;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, prm);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(W * 64), lds, stream, prm);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
 }
