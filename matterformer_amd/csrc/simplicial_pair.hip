@@ -71,6 +71,9 @@ namespace spair {
 template <bool BIAS>
 struct Waves {
   static constexpr int kCount = BIAS ? 8 : 4;
+  // queries per unit: 3 tiles; 2 with the bias, whose operands leave no room for a third at 256
+  // registers per wave
+  static constexpr int kGroup = BIAS ? 32 : 48;
 };
 constexpr int kRedWaves = 4;          // partial-output slots of the final reduction
 constexpr int kCap = 128;             // keys per staged block (one row per 2 threads)
@@ -350,16 +353,19 @@ __device__ __forceinline__ int info_nk(uint32_t w) { return int(w & 0x7ffu); }
 __device__ __forceinline__ int info_nq(uint32_t w) { return int((w >> 11) & 0x7ffu); }
 
 // Query groups of a molecule with nk valid keys and nq valid queries: one
-// group of up to 48, else groups of 32; molecules with more than kCap keys
-// (taken in key blocks) use groups of 16, one query tile.
+// group of up to GQ (48, or 32 with the bias), else groups of 32; molecules
+// with more than kCap keys (taken in key blocks) use groups of 16, one query
+// tile.
+template <int GQ>
 __device__ __forceinline__ int group_size(int nk, int nq) {
   if (nk > kCap) return 16;
-  return nq <= kMaxQ ? kMaxQ : 32;
+  return nq <= GQ ? GQ : 32;
 }
+template <int GQ>
 __device__ __forceinline__ int num_groups(int nk, int nq) {
   if (nq <= 0) return 0;
   if (nk > kCap) return (nq + 15) >> 4;
-  return nq <= kMaxQ ? 1 : (nq + 31) >> 5;
+  return nq <= GQ ? 1 : (nq + 31) >> 5;
 }
 
 // i / d for 0 <= i, d and i + d < 2^21: (i + 1/2) / d is at least 1/(2d)
@@ -641,10 +647,10 @@ __device__ __forceinline__ void pair_loop_n(int nqt, const unsigned char* smem, 
                                             const uint4 (&qop)[MQ][DP / 32], const float (&negm)[MQ], float sc,
                                             mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
                                             int g, int r16) {
-  static_assert(MQ == 3, "three query tiles");
+  static_assert(MQ == 2 || MQ == 3, "two or three query tiles");
   if (nqt == 1) pair_loop<DP, 1, MODE, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
-  else if (nqt == 2) pair_loop<DP, 2, MODE, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
-  else pair_loop<DP, 3, MODE, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+  else if (MQ == 2 || nqt == 2) pair_loop<DP, 2, MODE, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+  else pair_loop<DP, MQ, MODE, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
 }
 
 // ---------------------------------------------------------------------------
@@ -699,7 +705,8 @@ __device__ __forceinline__ uint16_t half_bits_sat(float x) {
 template <typename T, int DP, bool HAS_PV, bool MULTI, bool BIAS, bool STR>
 __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, int b, int h, int nk, int q0, int nqg,
                                           bool kpre, bool qpre, bool zero_share) {
-  constexpr int QT = kMaxQ / 16;       // query tiles held in registers
+  constexpr int GQ = Waves<BIAS>::kGroup;
+  constexpr int QT = GQ / 16;          // query tiles held in registers
   const int nqt = (nqg + 15) >> 4;     // query tiles in use
   constexpr int kWaves = Waves<BIAS>::kCount;
   constexpr int kThreads = kWaves * 64;
@@ -834,6 +841,142 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       if (row < nqg && col_ok) rq[i] = *reinterpret_cast<const uint4*>(gq + size_t(qatom[i]) * qsn + e0);
     }
   }
+  // ---- factorized bias (BIAS): c_i, then the fp16 operands of a block ------
+  float* cgf = reinterpret_cast<float*>(smem + Ly::kBG);
+  float* bmax = reinterpret_cast<float*>(smem + Ly::kBMax);  // max |u|, |v|, |w| of the unit's staged values
+  // (j block, k block): BU[j][i] = c_i u_ij, BW[j][k] = w_jk, BV[i][k + 2] = c_i v_ik over the staged rows,
+  // zero past the valid keys and queries
+  auto stage_bias = [&](int jc, int kc, int cE) {
+    uint16_t* BU = reinterpret_cast<uint16_t*>(smem + Ly::kBU);
+    uint16_t* BW = reinterpret_cast<uint16_t*>(smem + Ly::kBW);
+    uint16_t* BV = reinterpret_cast<uint16_t*>(smem + Ly::kBV);
+    const int j0 = jc * kCap, k0 = kc * kCap;
+    const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
+    const int rj = round16(nkj), rk = round16(nkk);
+    const int dt = p.bias_dtype;
+    float mx[3] = {0.0f, 0.0f, 0.0f};  // max |u|, |v|, |w| of the staged values
+    // Each set is taken a row per wave (rows wave, wave + kWaves, ...) with the lanes along the
+    // columns (lane, lane + 64), so a wave's loads of a row are one coalesced run; kRB rows of a
+    // wave are loaded before any is converted and stored.  Rows and columns past the valid
+    // queries / keys are stored as zero.
+    //   set 0 (U): rows = queries qi < kMaxQ, columns j < rj:  BU[j][qi]     = c_qi u[qa][ka(j0 + j)]
+    //   set 1 (V): rows = queries qi,          columns k < rk:  BV[qi][k + 2] = c_qi v[qa][ka(k0 + k)]
+    //   set 2 (W): rows j < rj,                columns k < rk:  BW[j][k]      = w[ka(j0 + j)][ka(k0 + k)]
+    // The first kRB rows of every set (all of U and V, and W up to 48 rows) and the gates of the
+    // wave's query rows are loaded before anything is stored, so the common case pays one round
+    // trip to memory; c_i = log2(e) 2^cE gate_i is formed in registers (and stored to BG).
+    constexpr int kRB = GQ / kWaves;
+    auto set_shape = [&](auto set_tag, int& R, int& C, int& rvalid, int& cvalid, int& cbase, const void*& src) {
+      constexpr int SET = decltype(set_tag)::value;
+      R = SET == 2 ? rj : GQ;
+      C = SET == 0 ? rj : rk;
+      rvalid = SET == 2 ? nkj : nqg;
+      cvalid = SET == 0 ? nkj : nkk;
+      cbase = SET == 0 ? j0 : k0;
+      src = SET == 0 ? p.bu : (SET == 1 ? p.bv : p.bw);
+    };
+    // Loads without branches: a lane's two column atoms are found once, each row's atom once
+    // (wave-uniform), out-of-range rows and columns read a clamped valid element (zeroed when
+    // stored, so no use follows a load and a wave's loads of a batch are in flight together),
+    // and the element width is one uniform choice for the whole batch.
+    auto load_rows = [&](auto set_tag, int r0, uint32_t (&val)[kRB][2]) {
+      constexpr int SET = decltype(set_tag)::value;
+      int R, C, rvalid, cvalid, cbase;
+      const void* src;
+      set_shape(set_tag, R, C, rvalid, cvalid, cbase, src);
+#pragma unroll
+      for (int t = 0; t < kRB; ++t) val[t][0] = val[t][1] = 0u;
+      if (rvalid <= 0 || cvalid <= 0) return;
+      const bool two = C > 64;  // a second column per lane (wave-uniform)
+      int ca[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) ca[s] = key_atom(cbase + min(lane + 64 * s, cvalid - 1));
+      int ra[kRB];  // row atoms, all found before any load is issued
+#pragma unroll
+      for (int t = 0; t < kRB; ++t) {
+        const int rc = min(r0 + kWaves * t, rvalid - 1);
+        ra[t] = SET == 2 ? key_atom(j0 + rc) : (qpre ? q0 + rc : int(qidx[q0 + rc]));
+      }
+      auto batch = [&](auto wide_tag) {
+        constexpr bool WIDE = decltype(wide_tag)::value;
+#pragma unroll
+        for (int t = 0; t < kRB; ++t) {
+          const size_t rowbase = (size_t(bh) * N + ra[t]) * N;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            if (s == 1 && !two) continue;  // wave-uniform
+            if constexpr (WIDE) val[t][s] = static_cast<const uint32_t*>(src)[rowbase + ca[s]];
+            else val[t][s] = static_cast<const uint16_t*>(src)[rowbase + ca[s]];
+          }
+        }
+      };
+      if (dt == MF_DTYPE_F32) batch(std::true_type{});
+      else batch(std::false_type{});
+    };
+    auto store_rows = [&](auto set_tag, int r0, const uint32_t (&val)[kRB][2], const float (&crow)[kRB]) {
+      constexpr int SET = decltype(set_tag)::value;
+      int R, C, rvalid, cvalid, cbase;
+      const void* src;
+      set_shape(set_tag, R, C, rvalid, cvalid, cbase, src);
+#pragma unroll
+      for (int t = 0; t < kRB; ++t) {
+        const int r = r0 + kWaves * t;
+        if (r >= R) break;  // wave-uniform
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const int c = lane + 64 * s;
+          if (c >= C) continue;
+          const uint32_t raw = val[t][s];
+          const float x = !(r < rvalid && c < cvalid) ? 0.0f
+                          : dt == MF_DTYPE_F32         ? __uint_as_float(raw)
+                          : dt == MF_DTYPE_BF16        ? __uint_as_float(raw << 16)
+                                                       : float(__builtin_bit_cast(_Float16, uint16_t(raw)));
+          mx[SET] = fmaxf(mx[SET], fabsf(x));
+          if constexpr (SET == 0) BU[c * kMaxQ + r] = half_bits_sat(crow[t] * x);
+          else if constexpr (SET == 1) BV[r * Ly::kVS + c + 2] = half_bits_sat(crow[t] * x);
+          else BW[r * kCap + c] = half_bits_sat(x);
+        }
+      }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    const float kNoRow[kRB] = {};
+    {
+      uint32_t vu[kRB][2], vv[kRB][2], vw[kRB][2];
+      float crow[kRB];
+      load_rows(S0{}, wave, vu);
+      load_rows(S1{}, wave, vv);
+      load_rows(S2{}, wave, vw);
+#pragma unroll
+      for (int t = 0; t < kRB; ++t) {  // the gates of query rows wave + kWaves t (wave-uniform loads)
+        const int r = wave + kWaves * t;
+        const int rc = min(r, max(nqg - 1, 0));
+        const int qa = qpre ? q0 + rc : int(qidx[q0 + rc]);
+        const float gte = bias_at(p.bg, size_t(bh) * N + qa, dt);
+        crow[t] = r < nqg ? ldexpf(gte * kLog2e, cE) : 0.0f;
+      }
+      store_rows(S0{}, wave, vu, crow);
+      store_rows(S1{}, wave, vv, crow);
+      store_rows(S2{}, wave, vw, kNoRow);
+      if (lane == 0) {
+#pragma unroll
+        for (int t = 0; t < kRB; ++t) cgf[wave + kWaves * t] = crow[t];
+      }
+    }
+    // W rows past the first batch (more than 48 staged keys)
+    for (int r0 = wave + kWaves * kRB; r0 < rj; r0 += kWaves * kRB) {
+      uint32_t vw[kRB][2];
+      load_rows(S2{}, r0, vw);
+      store_rows(S2{}, r0, vw, kNoRow);
+    }
+    // maxima over the wave, into this wave's slots (float order equals bit order for magnitudes)
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+      const uint32_t m = group_reduce<64>(__float_as_uint(mx[e]), MaxF32{});
+      if (lane == 0) bmax[wave * 3 + e] = __uint_as_float(m);
+    }
+  };
   ClaimState* cl = reinterpret_cast<ClaimState*>(smem + Ly::kClaim);
   // K rows: row-major fp16 scaled by 2^sc_exp
   auto store_k = [&](unsigned char* dst, const uint4& v, int row, int sc_exp) {
@@ -884,6 +1027,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     // the workgroup's share of padded query rows, stored while the loads are
     // in flight (first unit only)
     if (zero_share) zero_padded_share<T, DP, STR, Waves<BIAS>::kCount>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
+    // the bias operands, loaded while the key rows are in flight (query scale exponent E = 0 assumed)
+    if constexpr (BIAS) stage_bias(0, 0, 0);
     if constexpr (GUESS) {
       const int rj = round16(nk);
 #pragma unroll
@@ -1042,147 +1187,27 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   const int s1 = staged ? 0 : scal[0], s2 = staged ? 0 : scal[1], t1 = staged ? 0 : scal[2];
   const int t2 = staged ? 0 : scal[3], sq = staged ? 0 : scal[4], E = staged ? 0 : scal[5];
 
-  // ---- factorized bias (BIAS): c_i, then the fp16 operands of a block ------
-  float* cgf = reinterpret_cast<float*>(smem + Ly::kBG);
-  float* bmax = reinterpret_cast<float*>(smem + Ly::kBMax);  // max |u|, |v|, |w| of the unit's staged values
-  // (j block, k block): BU[j][i] = c_i u_ij, BW[j][k] = w_jk, BV[i][k + 2] = c_i v_ik over the staged rows,
-  // zero past the valid keys and queries
-  auto stage_bias = [&](int jc, int kc) {
-    uint16_t* BU = reinterpret_cast<uint16_t*>(smem + Ly::kBU);
-    uint16_t* BW = reinterpret_cast<uint16_t*>(smem + Ly::kBW);
-    uint16_t* BV = reinterpret_cast<uint16_t*>(smem + Ly::kBV);
-    const int j0 = jc * kCap, k0 = kc * kCap;
-    const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
-    const int rj = round16(nkj), rk = round16(nkk);
-    const int dt = p.bias_dtype;
-    float mx[3] = {0.0f, 0.0f, 0.0f};  // max |u|, |v|, |w| of the staged values
-    // Each set is taken a row per wave (rows wave, wave + kWaves, ...) with the lanes along the
-    // columns (lane, lane + 64), so a wave's loads of a row are one coalesced run; kRB rows of a
-    // wave are loaded before any is converted and stored.  Rows and columns past the valid
-    // queries / keys are stored as zero.
-    //   set 0 (U): rows = queries qi < kMaxQ, columns j < rj:  BU[j][qi]     = c_qi u[qa][ka(j0 + j)]
-    //   set 1 (V): rows = queries qi,          columns k < rk:  BV[qi][k + 2] = c_qi v[qa][ka(k0 + k)]
-    //   set 2 (W): rows j < rj,                columns k < rk:  BW[j][k]      = w[ka(j0 + j)][ka(k0 + k)]
-    // The first kRB rows of every set (all of U and V, and W up to 48 rows) are loaded before
-    // anything is stored, so the common case pays one round trip to memory.
-    constexpr int kRB = kMaxQ / kWaves;
-    auto set_shape = [&](auto set_tag, int& R, int& C, int& rvalid, int& cvalid, int& cbase, const void*& src) {
-      constexpr int SET = decltype(set_tag)::value;
-      R = SET == 2 ? rj : kMaxQ;
-      C = SET == 0 ? rj : rk;
-      rvalid = SET == 2 ? nkj : nqg;
-      cvalid = SET == 0 ? nkj : nkk;
-      cbase = SET == 0 ? j0 : k0;
-      src = SET == 0 ? p.bu : (SET == 1 ? p.bv : p.bw);
-    };
-    // Loads without branches: a lane's two column atoms are found once, each row's atom once
-    // (wave-uniform), out-of-range rows and columns read a clamped valid element (zeroed when
-    // stored, so no use follows a load and a wave's loads of a batch are in flight together),
-    // and the element width is one uniform choice for the whole batch.
-    auto load_rows = [&](auto set_tag, int r0, uint32_t (&val)[kRB][2]) {
-      constexpr int SET = decltype(set_tag)::value;
-      int R, C, rvalid, cvalid, cbase;
-      const void* src;
-      set_shape(set_tag, R, C, rvalid, cvalid, cbase, src);
-#pragma unroll
-      for (int t = 0; t < kRB; ++t) val[t][0] = val[t][1] = 0u;
-      if (rvalid <= 0 || cvalid <= 0) return;
-      const bool two = C > 64;  // a second column per lane (wave-uniform)
-      int ca[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) ca[s] = key_atom(cbase + min(lane + 64 * s, cvalid - 1));
-      int ra[kRB];  // row atoms, all found before any load is issued
-#pragma unroll
-      for (int t = 0; t < kRB; ++t) {
-        const int rc = min(r0 + kWaves * t, rvalid - 1);
-        ra[t] = SET == 2 ? key_atom(j0 + rc) : (qpre ? q0 + rc : int(qidx[q0 + rc]));
-      }
-      auto batch = [&](auto wide_tag) {
-        constexpr bool WIDE = decltype(wide_tag)::value;
-#pragma unroll
-        for (int t = 0; t < kRB; ++t) {
-          const size_t rowbase = (size_t(bh) * N + ra[t]) * N;
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            if (s == 1 && !two) continue;  // wave-uniform
-            if constexpr (WIDE) val[t][s] = static_cast<const uint32_t*>(src)[rowbase + ca[s]];
-            else val[t][s] = static_cast<const uint16_t*>(src)[rowbase + ca[s]];
-          }
-        }
-      };
-      if (dt == MF_DTYPE_F32) batch(std::true_type{});
-      else batch(std::false_type{});
-    };
-    auto store_rows = [&](auto set_tag, int r0, const uint32_t (&val)[kRB][2]) {
-      constexpr int SET = decltype(set_tag)::value;
-      int R, C, rvalid, cvalid, cbase;
-      const void* src;
-      set_shape(set_tag, R, C, rvalid, cvalid, cbase, src);
-#pragma unroll
-      for (int t = 0; t < kRB; ++t) {
-        const int r = r0 + kWaves * t;
-        if (r >= R) break;  // wave-uniform
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int c = lane + 64 * s;
-          if (c >= C) continue;
-          const uint32_t raw = val[t][s];
-          const float x = !(r < rvalid && c < cvalid) ? 0.0f
-                          : dt == MF_DTYPE_F32         ? __uint_as_float(raw)
-                          : dt == MF_DTYPE_BF16        ? __uint_as_float(raw << 16)
-                                                       : float(__builtin_bit_cast(_Float16, uint16_t(raw)));
-          mx[SET] = fmaxf(mx[SET], fabsf(x));
-          if constexpr (SET == 0) BU[c * kMaxQ + r] = half_bits_sat(cgf[r] * x);
-          else if constexpr (SET == 1) BV[r * Ly::kVS + c + 2] = half_bits_sat(cgf[r] * x);
-          else BW[r * kCap + c] = half_bits_sat(x);
-        }
-      }
-    };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    {
-      uint32_t vu[kRB][2], vv[kRB][2], vw[kRB][2];
-      load_rows(S0{}, wave, vu);
-      load_rows(S1{}, wave, vv);
-      load_rows(S2{}, wave, vw);
-      store_rows(S0{}, wave, vu);
-      store_rows(S1{}, wave, vv);
-      store_rows(S2{}, wave, vw);
-    }
-    // W rows past the first batch (more than 48 staged keys)
-    for (int r0 = wave + kWaves * kRB; r0 < rj; r0 += kWaves * kRB) {
-      uint32_t vw[kRB][2];
-      load_rows(S2{}, r0, vw);
-      store_rows(S2{}, r0, vw);
-    }
-    // maxima over the wave, then one LDS atomic per wave and set (float order equals bit order for
-    // magnitudes)
-#pragma unroll
-    for (int e = 0; e < 3; ++e) {
-      const uint32_t m = group_reduce<64>(__float_as_uint(mx[e]), MaxF32{});
-      if (lane == 0) atomicMax(reinterpret_cast<unsigned int*>(bmax + e), m);
-    }
-  };
   if constexpr (BIAS) {
-    for (int qi = tid; qi < kMaxQ; qi += kThreads) {
-      float c = 0.0f;
-      if (qi < nqg) {
-        const int qa = qpre ? q0 + qi : int(qidx[q0 + qi]);
-        c = ldexpf(bias_at(p.bg, size_t(bh) * N + qa, p.bias_dtype) * kLog2e, E);
-      }
-      cgf[qi] = c;
-    }
-    if (tid < 3) bmax[tid] = 0.0f;
-    __syncthreads();
     if constexpr (!MULTI) {
-      stage_bias(0, 0);
-      __syncthreads();
+      // staged with the key rows assuming E = 0; a query scale of its own (E != 0, rare) restages
+      if (E != 0) {
+        __syncthreads();
+        stage_bias(0, 0, E);
+        __syncthreads();
+      }
     } else {
       if (tid == 0) scal[6] = 1;  // blocks stage their bias one pair at a time: two passes, exact maxima
     }
   }
-  const float bias_mag = BIAS ? bmax[0] + bmax[1] + bmax[2] : 0.0f;
+  float bias_mag = 0.0f;
+  if constexpr (BIAS) {
+    float m3[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+      for (int e = 0; e < 3; ++e) m3[e] = fmaxf(m3[e], bmax[w * 3 + e]);
+    bias_mag = m3[0] + m3[1] + m3[2];
+  }
 
   // ---- phase B: query rows, bounds ---------------------------------------
   if (!staged) {
@@ -1263,7 +1288,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       for (int i = 0; i < MAXC; ++i)
         if ((tid + kThreads * i) / CPR < rk) store_v(V2s, t[i], (tid + kThreads * i) / CPR, t2);
     }
-    if constexpr (BIAS && MULTI) stage_bias(jc, kc);
+    if constexpr (BIAS && MULTI) stage_bias(jc, kc, E);
     if constexpr (HAS_PV) stage_pv(jc, kc);
   };
 
@@ -1554,7 +1579,7 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
 // every 4th pair.  s_cu holds the pairs (over the staging area).  The
 // molecule whose positions hold position w (when w < s_pre[B]) writes
 // *s_first = b | (w - its first position) << 16.
-template <int W>
+template <int W, int GQ>
 __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* s_info, uint16_t* s_order, int* s_pre,
                                                uint2* s_cu, int w, int* s_first) {
   constexpr int kThreads = W * 64;
@@ -1567,7 +1592,7 @@ __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* 
       const uint32_t w = s_info[b];
       const int nk = info_nk(w), nq = info_nq(w);
       cu.x = uint32_t(nk * nk) * uint32_t((nq + 15) / 16);
-      cu.y = uint32_t(H * num_groups(nk, nq));
+      cu.y = uint32_t(H * num_groups<GQ>(nk, nq));
     }
     s_cu[b] = cu;
   }
@@ -1610,7 +1635,7 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
   const uint32_t info = reinterpret_cast<const uint32_t*>(smem + Ly::kInfo)[b];
   const int nk = info_nk(info), nq = info_nq(info);
   const bool kpre = (info & kKPre) != 0, qpre = (info & kQPre) != 0;
-  const int gs = group_size(nk, nq);
+  const int gs = group_size<Waves<BIAS>::kGroup>(nk, nq);
   const int q0 = gs * g;
   const int nqg = min(gs, nq - q0);
   if (nqg > 0) {
@@ -1654,7 +1679,7 @@ __global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, BIAS ? 1 : 2) simpli
 
   if (tid == 0) cl->claimed = 0;
   scan_masks<DP, W>(p, smem, s_info);  // ends with a barrier
-  rank_molecules<W>(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
+  rank_molecules<W, Waves<BIAS>::kGroup>(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
   const int total = s_pre[B];
 
   // the rows of padded queries: a static share of (b, h) pairs per
@@ -1677,7 +1702,7 @@ __global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, BIAS ? 1 : 2) simpli
       i = pos - s_pre[lo];
     }
     const uint32_t info = s_info[b];
-    const int ng = num_groups(info_nk(info), info_nq(info));
+    const int ng = num_groups<Waves<BIAS>::kGroup>(info_nk(info), info_nq(info));
     const int h = div_small(i, ng);
     run_unit<T, DP, HAS_PV, BIAS, STR>(p, smem, b, h, i - h * ng, pos == wg);  // ends with a barrier: cl->next is read
     if (tid == 0) {
