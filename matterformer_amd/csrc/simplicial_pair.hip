@@ -329,6 +329,9 @@ struct AddI32 {
 struct MaxI32 {
   __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return uint32_t(max(int(a), int(b))); }
 };
+struct MinI32 {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return uint32_t(min(int(a), int(b))); }
+};
 
 // |x| from the 16-bit pattern of x with the sign cleared
 template <typename T>
@@ -948,12 +951,27 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       load_rows(S0{}, wave, vu);
       load_rows(S1{}, wave, vv);
       load_rows(S2{}, wave, vw);
+      // the gates of query rows wave + kWaves t: all loaded (one uniform width) before any is used
+      uint32_t graw[kRB];
+      int gidx[kRB];
 #pragma unroll
-      for (int t = 0; t < kRB; ++t) {  // the gates of query rows wave + kWaves t (wave-uniform loads)
+      for (int t = 0; t < kRB; ++t) {
+        const int rc = min(wave + kWaves * t, max(nqg - 1, 0));
+        gidx[t] = qpre ? q0 + rc : int(qidx[q0 + rc]);
+      }
+      if (dt == MF_DTYPE_F32) {
+#pragma unroll
+        for (int t = 0; t < kRB; ++t) graw[t] = static_cast<const uint32_t*>(p.bg)[size_t(bh) * N + gidx[t]];
+      } else {
+#pragma unroll
+        for (int t = 0; t < kRB; ++t) graw[t] = static_cast<const uint16_t*>(p.bg)[size_t(bh) * N + gidx[t]];
+      }
+#pragma unroll
+      for (int t = 0; t < kRB; ++t) {
         const int r = wave + kWaves * t;
-        const int rc = min(r, max(nqg - 1, 0));
-        const int qa = qpre ? q0 + rc : int(qidx[q0 + rc]);
-        const float gte = bias_at(p.bg, size_t(bh) * N + qa, dt);
+        const float gte = dt == MF_DTYPE_F32 ? __uint_as_float(graw[t])
+                          : dt == MF_DTYPE_BF16 ? __uint_as_float(graw[t] << 16)
+                                                : float(__builtin_bit_cast(_Float16, uint16_t(graw[t])));
         crow[t] = r < nqg ? ldexpf(gte * kLog2e, cE) : 0.0f;
       }
       store_rows(S0{}, wave, vu, crow);
@@ -1469,51 +1487,71 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 // Nonzero bytes of a dword as bit 7 of each byte: ((x & 0x7f) + 0x7f) | x.
 __device__ __forceinline__ uint32_t nz_bytes(uint32_t x) { return (((x & 0x7f7f7f7fu) + 0x7f7f7f7fu) | x) & 0x80808080u; }
 
-// Those of bytes [lo, hi) of a 16-byte chunk (dword j covers bytes 4j..4j+3).
-__device__ __forceinline__ uint32_t nz_chunk_word(uint32_t x, int j, int lo, int hi) {
-  const int l = min(max(lo - 4 * j, 0), 4), h = min(max(4 * j + 4 - hi, 0), 4);
-  return (l + h >= 4) ? 0u : nz_bytes(x) & (0xffffffffu << (8 * l)) & (0xffffffffu >> (8 * h));
+// Bit 7 of each byte in [lo, hi) of a 16-byte chunk (dword j covers bytes 4j..4j+3).
+__device__ __forceinline__ uint4 chunk_bytes(int lo, int hi) {
+  uint32_t m[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int l = min(max(lo - 4 * j, 0), 4), h = min(max(hi - 4 * j, 0), 4);
+    m[j] = h <= l ? 0u : (0x80808080u & (0xffffffffu << (8 * l)) & (0xffffffffu >> (8 * (4 - h))));
+  }
+  return uint4{m[0], m[1], m[2], m[3]};
 }
 
-// Valid (nonzero) byte count and last valid index of bytes [a, e) of a mask
-// row in global memory.  The bytes are read as the 16-byte aligned chunks
-// that hold them, eight loads in flight; an aligned chunk that holds a byte of
-// the row lies on that byte's page.  The last valid byte is located once, in
-// the last chunk that has one.
-__device__ __forceinline__ void scan_row_global(const uint8_t* row, int a, int e, int& count, int& last) {
+// Valid (nonzero) byte count of bytes [a, e) of a mask row in global memory,
+// and the index of the first zero byte among them (e if none).  The bytes are
+// read as the 16-byte aligned chunks that hold them, eight loads in flight; an
+// aligned chunk that holds a byte of the row lies on that byte's page.  Every
+// chunk is counted whole; the bytes of the first chunk before a are masked
+// there (a compile-time slot), and those of the last chunk from e on are read
+// again once and taken off.  The first zero is looked for from a on; one past
+// e is clamped to e.
+__device__ __forceinline__ void scan_row_global(const uint8_t* row, int a, int e, int& count, int& firstzero) {
+  firstzero = e;
   if (a >= e) return;
   const uint8_t* begin = row + a;
   const int off = int(reinterpret_cast<uintptr_t>(begin) & 15u);
   const uint8_t* c0 = begin - off;  // pointer arithmetic keeps the global address space
   const int span = off + (e - a);   // bytes from c0 to the end of the segment
   const int nch = (span + 15) >> 4;
-  int lastc = -1;
-  uint32_t lw[4] = {0u, 0u, 0u, 0u};
+  const uint4 keep0 = chunk_bytes(off, 16);
+  int cnt = 0, zc = -1;
+  uint32_t zw[4] = {0u, 0u, 0u, 0u};
   for (int c = 0; c < nch; c += 8) {
     uint4 v[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t)
       v[t] = c + t < nch ? *reinterpret_cast<const uint4*>(c0 + 16 * (c + t)) : uint4{0u, 0u, 0u, 0u};
+    const uint4 m0 = c == 0 ? keep0 : uint4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const int ci = c + t;
-      const int lo = ci == 0 ? off : 0;
-      const int hi = min(16, span - 16 * ci);  // <= 0 past the segment: nothing kept
-      const uint32_t n0 = nz_chunk_word(v[t].x, 0, lo, hi), n1 = nz_chunk_word(v[t].y, 1, lo, hi);
-      const uint32_t n2 = nz_chunk_word(v[t].z, 2, lo, hi), n3 = nz_chunk_word(v[t].w, 3, lo, hi);
-      count += __popc(n0) + __popc(n1) + __popc(n2) + __popc(n3);
-      if ((n0 | n1 | n2 | n3) != 0u) {
-        lastc = ci;
-        lw[0] = n0; lw[1] = n1; lw[2] = n2; lw[3] = n3;
+      uint32_t n0 = nz_bytes(v[t].x), n1 = nz_bytes(v[t].y), n2 = nz_bytes(v[t].z), n3 = nz_bytes(v[t].w);
+      uint32_t z0 = n0 ^ 0x80808080u, z1 = n1 ^ 0x80808080u, z2 = n2 ^ 0x80808080u, z3 = n3 ^ 0x80808080u;
+      if (t == 0) {
+        n0 &= m0.x; n1 &= m0.y; n2 &= m0.z; n3 &= m0.w;
+        z0 &= m0.x; z1 &= m0.y; z2 &= m0.z; z3 &= m0.w;
+      }
+      cnt += __popc(n0) + __popc(n1) + __popc(n2) + __popc(n3);
+      if (zc < 0 && (z0 | z1 | z2 | z3) != 0u) {
+        zc = c + t;
+        zw[0] = z0; zw[1] = z1; zw[2] = z2; zw[3] = z3;
       }
     }
   }
-  if (lastc >= 0) {
-    int l = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (lw[j]) l = 4 * j + ((31 - __clz(lw[j])) >> 3);
-    last = a + 16 * lastc + l - off;
+  if (span & 15) {  // bytes e .. of the last chunk
+    const uint4 vl = *reinterpret_cast<const uint4*>(c0 + 16 * (nch - 1));
+    uint4 ml = chunk_bytes(span & 15, 16);
+    if (nch == 1) ml = uint4{ml.x & keep0.x, ml.y & keep0.y, ml.z & keep0.z, ml.w & keep0.w};
+    cnt -= __popc(nz_bytes(vl.x) & ml.x) + __popc(nz_bytes(vl.y) & ml.y) + __popc(nz_bytes(vl.z) & ml.z) +
+           __popc(nz_bytes(vl.w) & ml.w);
+  }
+  count += cnt;
+  if (zc >= 0) {
+    int pos = 12 + (__builtin_ctz(zw[3] | 0x80000000u) >> 3);
+    if (zw[2]) pos = 8 + (__builtin_ctz(zw[2]) >> 3);
+    if (zw[1]) pos = 4 + (__builtin_ctz(zw[1]) >> 3);
+    if (zw[0]) pos = __builtin_ctz(zw[0]) >> 3;
+    firstzero = min(e, a - off + 16 * zc + pos);
   }
 }
 
@@ -1531,12 +1569,12 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
   // threads per row: a power of two, <= 8, with rows * tpr <= kThreads when rows allow
   const int tpr = rows > kThreads / 2 ? 1 : rows > kThreads / 4 ? 2 : rows > kThreads / 8 ? 4 : 8;
   const int rpp = kThreads / tpr;  // rows per pass (even)
-  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP, W>::kK2);  // [rpp] counts, then [rpp] last indices
+  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP, W>::kK2);  // [rpp] counts, then [rpp] first zeros
   static_assert(kCap * Lay<DP, W>::RB >= kThreads * 2 * 4, "row results must fit in the K2 staging area");
   const int seg = (N + tpr - 1) / tpr;
   for (int r0 = 0; r0 < rows; r0 += rpp) {
     const int r = r0 + tid / tpr, sg = tid & (tpr - 1);
-    int cnt = 0, last = -1;
+    int cnt = 0, last = N;  // count and first zero byte of the row
     if (r < rows) {
       const uint8_t* row = ((r & 1) ? p.qv : p.pkv) + size_t(r >> 1) * N;
       const int a = min(N, sg * seg);
@@ -1545,15 +1583,15 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
     // the tpr threads of a row are adjacent lanes of one wave (all active)
     if (tpr >= 2) {
       cnt = int(AddI32{}(uint32_t(cnt), dpp_peer<0xB1>(uint32_t(cnt))));
-      last = int(MaxI32{}(uint32_t(last), dpp_peer<0xB1>(uint32_t(last))));
+      last = int(MinI32{}(uint32_t(last), dpp_peer<0xB1>(uint32_t(last))));
     }
     if (tpr >= 4) {
       cnt = int(AddI32{}(uint32_t(cnt), dpp_peer<0x4E>(uint32_t(cnt))));
-      last = int(MaxI32{}(uint32_t(last), dpp_peer<0x4E>(uint32_t(last))));
+      last = int(MinI32{}(uint32_t(last), dpp_peer<0x4E>(uint32_t(last))));
     }
     if (tpr >= 8) {
       cnt = int(AddI32{}(uint32_t(cnt), dpp_peer<0x141>(uint32_t(cnt))));
-      last = int(MaxI32{}(uint32_t(last), dpp_peer<0x141>(uint32_t(last))));
+      last = int(MinI32{}(uint32_t(last), dpp_peer<0x141>(uint32_t(last))));
     }
     if (r < rows && sg == 0) {
       s_cnt[r - r0] = cnt;
@@ -1563,9 +1601,9 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
     const int m0 = r0 >> 1;
     for (int m = tid; m < rpp / 2 && m0 + m < B; m += kThreads) {
       const int ck = min(s_cnt[2 * m], N), cq = min(s_cnt[2 * m + 1], N);
-      const int lk = s_cnt[rpp + 2 * m], lq = s_cnt[rpp + 2 * m + 1];
-      s_info[m0 + m] =
-          uint32_t(ck) | (uint32_t(cq) << 11) | (lk + 1 == ck ? kKPre : 0u) | (lq + 1 == cq ? kQPre : 0u);
+      // the valid bytes are the prefix 0 .. n - 1 exactly when the first zero byte is byte n
+      const int zk = s_cnt[rpp + 2 * m], zq = s_cnt[rpp + 2 * m + 1];
+      s_info[m0 + m] = uint32_t(ck) | (uint32_t(cq) << 11) | (zk == ck ? kKPre : 0u) | (zq == cq ? kQPre : 0u);
     }
     __syncthreads();
   }
