@@ -8,8 +8,10 @@ reference's bias + angle + message fixture (tests/test_oracle_simplicial.py).
 Tolerances as for the plain forward: fp32 operands with ieee_fp32 precision
 1e-4 (the reference's own parity bar, tests/test_simplicial_attention.py:1017),
 16-bit operands normwise relative error <= 2e-2 against float64 on the same
-16-bit-rounded inputs, and additionally every valid query row within 6e-2 of
-its own norm, so a few wrong rows cannot hide in the normwise figure.
+16-bit-rounded inputs, and additionally every valid query row within 3e-2 of
+its own norm, so a few wrong rows cannot hide in the normwise figure (the
+worst row measured over every case here is 2.1e-2, bf16 with the low-rank
+message term at N = 130; fp16 cases stay below 3e-3).
 """
 
 from pathlib import Path
@@ -104,6 +106,10 @@ def logit_std(D):
     return (4.0 / D) ** (1.0 / 6.0)
 
 
+# every valid query row within this fraction of its own norm (16-bit operands)
+ROW_BAR = 3e-2
+
+
 def test_reference_golden_bias_angle_message(cuda):
     z = np.load(GOLDEN / "simplicial_fp32_bias_angle_message.npz")
     t = {k: torch.from_numpy(z[k]).to(cuda) for k in z.files if z[k].ndim > 0}
@@ -163,7 +169,9 @@ def test_16bit_terms_match_fp64(cuda, shape, terms, dtype):
     assert out.dtype == dtype
     assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-2
-    assert row_errors(out32.cpu().numpy(), ref, case[5]).max() <= 6e-2
+    worst = row_errors(out32.cpu().numpy(), ref, case[5]).max()
+    print(f"worst row {worst:.3e}", flush=True)
+    assert worst <= ROW_BAR
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
 
 
@@ -179,8 +187,48 @@ def test_16bit_large_bias_takes_two_passes(cuda, shape):
     out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc")
     ref, ref_lse = oracle(case, tm, torch.bfloat16)
     assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
-    assert row_errors(out32.cpu().numpy(), ref, case[5]).max() <= 6e-2
+    worst = row_errors(out32.cpu().numpy(), ref, case[5]).max()
+    print(f"worst row {worst:.3e}", flush=True)
+    assert worst <= ROW_BAR
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
+def test_16bit_masking_scale_bias(cuda):
+    """A masking-style bias: u_ij = -1e4 on a random 30 % of (query, key) pairs, the rest N(0, 0.5^2), gates
+    1 + N(0, 0.1^2).  c_i u_ij ~ -1.4e4 (log2 units) is staged as fp16 without saturating and drives those
+    pairs' P to 0 exactly as exp(-1e4) does in float64; the exact two-pass maxima are taken over the rest.
+    Bar: 2e-2 normwise and every valid row within the row bar of its norm."""
+    B, H, N, D = 2, 2, 37, 64
+    case = random_simplicial(B, H, N, D, seed=41, counts=[37, 23], std=logit_std(D))
+    tm = make_terms(B, H, N, D, seed=42)
+    gen = torch.Generator().manual_seed(43)
+    u = tm["bias"][0]
+    u[torch.rand(u.shape, generator=gen) < 0.3] = -1e4
+    tm["bias"][3] = 1.0 + 0.1 * torch.randn(B, H, N, generator=gen)
+    out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc")
+    ref, ref_lse = oracle(case, tm, torch.bfloat16)
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+    worst = row_errors(out32.cpu().numpy(), ref, case[5]).max()
+    print(f"masking-scale bias: worst row {worst:.3e}", flush=True)
+    assert worst <= ROW_BAR
+
+
+def test_16bit_dominant_pair_bias_near_fp16_limit(cuda):
+    """One key pair per molecule made dominant by w_jk = 2e4 (gate 1: c w ~ 2.9e4 log2 units, below the fp16
+    limit of 65504 the staged products saturate at): every valid query's output is v1_j (.) v2_k of that pair,
+    as in float64.  Bar: 2e-2 normwise and the row bar per valid row."""
+    B, H, N, D = 2, 2, 29, 64
+    case = random_simplicial(B, H, N, D, seed=44, counts=[29, 17], std=logit_std(D))
+    tm = make_terms(B, H, N, D, seed=45)
+    tm["bias"][2][0, :, 3, 5] = 2e4
+    tm["bias"][2][1, :, 11, 2] = 2e4
+    tm["bias"][3] = torch.ones(B, H, N)
+    out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc")
+    ref, ref_lse = oracle(case, tm, torch.bfloat16)
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+    worst = row_errors(out32.cpu().numpy(), ref, case[5]).max()
+    print(f"dominant pair bias: worst row {worst:.3e}", flush=True)
+    assert worst <= ROW_BAR
 
 
 def test_fp32_bias_with_bf16_operands(cuda):
@@ -223,7 +271,9 @@ def test_geom_config_with_bias_whole_batch(cuda):
     out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc")
     ref, ref_lse = oracle(case, tm, torch.bfloat16)
     assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
-    assert row_errors(out32.cpu().numpy(), ref, w.query_valid).max() <= 6e-2
+    worst = row_errors(out32.cpu().numpy(), ref, w.query_valid).max()
+    print(f"config 2 with bias: worst row {worst:.3e}", flush=True)
+    assert worst <= ROW_BAR
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
 
 

@@ -333,7 +333,9 @@ def test_geom_config_every_molecule_per_row(cuda):
     rows = w.query_valid[:, None, :].expand(-1, w.shape[1], -1).numpy()
     diff = np.linalg.norm(got - ref, axis=-1)[rows]
     norm = np.linalg.norm(ref, axis=-1)[rows]
-    assert (diff / norm).max() <= 6e-2, (diff / norm).max()
+    print(f"config 2: worst row {(diff / norm).max():.3e}, median {np.median(diff / norm):.3e}", flush=True)
+    # measured worst row 6.2e-4 (median 3.1e-4): the bar is five times the worst
+    assert (diff / norm).max() <= 3e-3, (diff / norm).max()
     for b in range(w.shape[0]):
         assert rel_err(got[b], ref[b]) <= 2e-2, b
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
