@@ -44,6 +44,19 @@ int simplicial_pair_max_batch(int tokens);
 size_t simplicial_pair_workspace_bytes(int batch, int tokens);
 int simplicial_pair_launch(const mf_simplicial_fwd_args* a, void* claims, int num_cus, hipStream_t stream);
 
+// Pair-formulation backward for bf16 operands (simplicial_pair_bwd.hip): it
+// serves every molecule with at most simplicial_pair_bwd_max_tokens() valid
+// queries and keys and leaves the others untouched.
+// It needs simplicial_pair_bwd_workspace_bytes() of 256-byte aligned
+// workspace (a plan of units, served flags, atom lists and partial
+// sums); after a launch simplicial_pair_bwd_served() points at one int per
+// molecule, nonzero when the pair kernel computed its gradients.
+bool simplicial_pair_bwd_serves(const mf_simplicial_bwd_args* a);
+int simplicial_pair_bwd_max_tokens();
+size_t simplicial_pair_bwd_workspace_bytes(int batch, int heads);
+const int* simplicial_pair_bwd_served(const mf_simplicial_bwd_args* a);
+int simplicial_pair_bwd_launch(const mf_simplicial_bwd_args* a, hipStream_t stream);
+
 #define MF_HIP_CHECK(expr)                                                     \
   do {                                                                         \
     hipError_t mf_err_ = (expr);                                               \

@@ -161,6 +161,7 @@ struct Params {
   int NP;       // N rounded up to 64: LDS list capacity
   int OB;       // workgroups per (b, h, role)
   int vec;      // q/k/v/go/out rows 4-element loads are aligned (D % 4 == 0, aligned bases)
+  const int* served;  // [B] nonzero: the pair kernel computed this molecule's gradients (or NULL)
   // low-rank terms (LR instantiations): factors [B*H, N, N, R] fp32, gates [B*H, N], basis [H, Rm, D]
   const float* al;
   const float* ar;
@@ -277,6 +278,7 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
   constexpr int KS = S::KS;
   const int N = p.N, D = p.D, NP = p.NP;
   const int b = bh / p.H;
+  if (p.served != nullptr && p.served[b] != 0) return;  // the pair kernel's molecule (uniform)
   const bool has_pv = p.pv != nullptr;
   constexpr bool has_bias = BIAS;
   const bool vec = p.vec != 0;
@@ -1034,6 +1036,12 @@ int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
 
 using namespace mf;
 
+// dc and the per-query coefficients of the message term, [B*H, N, Rm] fp32 each
+static uint64_t message_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t message_rank) {
+  if (batch <= 0 || heads <= 0 || tokens <= 0 || message_rank <= 0) return 0;
+  return 2ull * uint64_t(batch) * uint64_t(heads) * uint64_t(tokens) * uint64_t(message_rank) * 4ull;
+}
+
 extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) {
   using namespace mf::sbwd;
   if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: args is NULL");
@@ -1072,7 +1080,7 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: message_left, message_right and message_basis go together");
     if (a->message_rank < 1 || a->message_rank > 64)
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: message_rank must be in 1..64, got " + std::to_string(a->message_rank));
-    const uint64_t need = mf_simplicial_bwd_workspace_size(a->batch, a->heads, a->tokens, a->head_dim, a->message_rank);
+    const uint64_t need = message_workspace_bytes(a->batch, a->heads, a->tokens, a->message_rank);
     if (a->workspace == nullptr || a->workspace_bytes < need)
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: the message term needs " + std::to_string(need) +
                                                " bytes of workspace (mf_simplicial_bwd_workspace_size)");
@@ -1149,6 +1157,13 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   // only for a bf16 grad_out).  Everything else -- fp16 operands, or a grad_out of another dtype -- takes the
   // fp32 path, which reads every operand in its own dtype.
   if (a->dtype == MF_DTYPE_BF16 && a->grad_dtype == MF_DTYPE_BF16) {
+    // molecules of at most 80 valid atoms take the pair formulation; the ownership kernel below takes the rest
+    if (simplicial_pair_bwd_serves(a)) {
+      const int st = simplicial_pair_bwd_launch(a, s);
+      if (st != MF_OK) return st;
+      if (a->tokens <= simplicial_pair_bwd_max_tokens()) return MF_OK;
+      prm.served = simplicial_pair_bwd_served(a);
+    }
     if (D <= 32) return launch<32, true>(prm, has_pv, has_bias, s);
     if (D <= 64) return launch<64, true>(prm, has_pv, has_bias, s);
     return launch<128, true>(prm, has_pv, has_bias, s);
@@ -1161,8 +1176,10 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
 
 extern "C" uint64_t mf_simplicial_bwd_workspace_size(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
                                                      int32_t message_rank) {
-  (void)head_dim;
-  if (batch <= 0 || heads <= 0 || tokens <= 0 || message_rank <= 0) return 0;
-  // dc and the per-query coefficients, [B*H, N, Rm] fp32 each
-  return 2ull * uint64_t(batch) * uint64_t(heads) * uint64_t(tokens) * uint64_t(message_rank) * 4ull;
+  if (batch <= 0 || heads <= 0 || tokens <= 0) return 0;
+  // the message term's coefficients, or (head_dim 64) the pair kernel's plan and partial sums; one call uses
+  // at most one of them
+  const uint64_t msg = message_rank > 0 ? message_workspace_bytes(batch, heads, tokens, message_rank) : 0;
+  const uint64_t pair = head_dim == 64 ? uint64_t(simplicial_pair_bwd_workspace_bytes(batch, heads)) : 0;
+  return std::max(msg, pair);
 }

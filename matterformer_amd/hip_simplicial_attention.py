@@ -411,7 +411,6 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
                                              ("need_dangle_gate", (B, H, N)))):
             if flags[name]:
                 lr_grads[idx] = torch.zeros(shape, device=dev, dtype=torch.float32)
-    workspace = None
     rm = 0
     if ext.message is not None:
         rm = int(ext.message[0].shape[-1])
@@ -420,8 +419,9 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
                                              ("need_dmessage_basis", (H, rm, D)))):
             if flags[name]:
                 lr_grads[3 + idx] = torch.zeros(shape, device=dev, dtype=torch.float32)
-        nbytes = int(_native.lib().mf_simplicial_bwd_workspace_size(B, H, N, D, rm))
-        workspace = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    # the message term's coefficients, or the pair kernel's plan and partial sums (bf16, head_dim 64)
+    nbytes = int(_native.lib().mf_simplicial_bwd_workspace_size(B, H, N, D, rm))
+    workspace = torch.empty(nbytes, device=dev, dtype=torch.uint8) if nbytes > 0 else None
     f = ext.fields()
     args = _native.MfSimplicialBwdArgs(
         q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(), k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),

@@ -164,25 +164,29 @@ def test_qm9_config_gradients_whole_batch(cuda):
         np.testing.assert_allclose(g.cpu().numpy(), r, rtol=1e-4, atol=1e-4, err_msg=name)
 
 
-def test_geom_config_gradients_every_molecule(cuda):
-    """Config 2 (bf16, 64 molecules up to 181 atoms) with a factorized bias: the batched HIP gradients of
-    each molecule against float64 autograd over that molecule's atoms, 2e-2 per gradient."""
+@pytest.mark.parametrize("with_bias", [False, True], ids=["nobias", "bias"])
+def test_geom_config_gradients_every_molecule(cuda, with_bias):
+    """Config 2 (bf16, 64 molecules of 10-72 atoms padded to 181), without a bias (the pair-formulation kernel)
+    and with a factorized bias (the ownership kernel): the batched HIP gradients of each molecule against
+    float64 autograd over that molecule's atoms, 2e-2 per gradient."""
     w = simplicial_workload("geom")
     B, H, N, D = w.shape
     gen = torch.Generator().manual_seed(56)
     go = torch.randn(B, H, N, D, generator=gen).to(torch.bfloat16)
     bias = [(torch.randn(B, H, N, N, generator=gen) * 0.5).to(torch.bfloat16) for _ in range(3)] + \
            [torch.randn(B, H, N, generator=gen).to(torch.bfloat16)]
+    if not with_bias:
+        bias = None
     ops_cpu = [t.to(torch.bfloat16) for t in (w.q, w.k1, w.v1, w.k2, w.v2)]
     _, got = hip_grads([t.to(cuda) for t in ops_cpu], w.query_valid.to(cuda), w.pair_key_valid.to(cuda), None,
-                       go.to(cuda), "bf16_tc", bias=[t.to(cuda) for t in bias])
-    got = [g.float().cpu() for g in got]
+                       go.to(cuda), "bf16_tc", bias=None if bias is None else [t.to(cuda) for t in bias])
+    got = [g.float().cpu() for g in got if g is not None]
     worst = {}
     for b in range(B):
         n = int(w.counts[b])
         ones = torch.ones(1, n, dtype=torch.bool)
         sl = [t[b:b + 1, :, :n] for t in ops_cpu]
-        bsl = [t[b:b + 1, :, :n, :n] for t in bias[:3]] + [bias[3][b:b + 1, :, :n]]
+        bsl = None if bias is None else [t[b:b + 1, :, :n, :n] for t in bias[:3]] + [bias[3][b:b + 1, :, :n]]
         _, ref = fp64_grads(sl, ones, ones, None, go[b:b + 1, :, :n], bias=bsl)
         for idx, (name, r) in enumerate(zip(GRAD_NAMES, ref)):
             g = got[idx][b:b + 1, :, :n]
@@ -196,20 +200,24 @@ def test_geom_config_gradients_every_molecule(cuda):
     print("worst per-molecule relative error:", {k: f"{v:.2e}" for k, v in worst.items()}, flush=True)
 
 
-def test_backward_is_bitwise_deterministic(cuda):
-    """Two backward calls on the same inputs (config-2 sized, bias) give identical bits."""
+@pytest.mark.parametrize("with_bias", [False, True], ids=["nobias", "bias"])
+def test_backward_is_bitwise_deterministic(cuda, with_bias):
+    """Two backward calls on the same inputs (config-2 sized, with and without a bias) give identical bits."""
     w = simplicial_workload("geom", batch=16)
     B, H, N, D = w.shape
     gen = torch.Generator().manual_seed(57)
     go = torch.randn(B, H, N, D, generator=gen).to(torch.bfloat16).to(cuda)
     bias = [(torch.randn(B, H, N, N, generator=gen) * 0.5).to(torch.bfloat16).to(cuda) for _ in range(3)] + \
            [torch.randn(B, H, N, generator=gen).to(torch.bfloat16).to(cuda)]
+    if not with_bias:
+        bias = None
     ops = [t.to(torch.bfloat16).to(cuda) for t in (w.q, w.k1, w.v1, w.k2, w.v2)]
     qv, pkv = w.query_valid.to(cuda), w.pair_key_valid.to(cuda)
     _, first = hip_grads(ops, qv, pkv, None, go, "bf16_tc", bias=bias)
     _, second = hip_grads(ops, qv, pkv, None, go, "bf16_tc", bias=bias)
     for name, a, b in zip(GRAD_NAMES, first, second):
-        assert torch.equal(a, b), name
+        assert (a is None) == (b is None), name
+        assert a is None or torch.equal(a, b), name
 
 
 def test_only_requested_bias_gradients_are_returned(cuda):
