@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 9
+#define MF_ABI_VERSION 10
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -168,8 +168,13 @@ int mf_simplicial_fwd(const mf_simplicial_fwd_args* args, void* stream);
 /* (the quantities of triton_simplicial_attention.py:332-782 and             */
 /* :929-1204, which accumulates them with atomics).  Every output element is */
 /* written by one wave after sums in a fixed order: two calls on the same    */
-/* inputs give bitwise identical gradients.  Outputs are fp32, written only  */
-/* at valid entries: the caller zero-fills them.                            */
+/* inputs give bitwise identical gradients.  dq, dk1, dv1, dk2 and dv2 are  */
+/* fp32 (grads_dtype MF_DTYPE_F32), written only at valid entries, the      */
+/* caller zero-filling them; or (ABI 10) bf16 when grads_dtype, dtype and   */
+/* grad_dtype are all MF_DTYPE_BF16, no low-rank term is given, head_dim is */
+/* a multiple of 8, tokens <= 4096 and the buffers are 16-byte aligned: then */
+/* every row is written (zeros at padded queries and keys) and the caller   */
+/* needs no fill.  Bias gradients stay fp32, zero-filled by the caller.     */
 /* With the low-rank terms of mf_simplicial_fwd (angle A_ijk = sum_r         */
 /* AL[i,j,r] AR[i,k,r] added to S as ag_i Ra^-1/2 A; message                 */
 /* c_ir = Rm^-1/2 sum_jk P ML[i,j,r] MR[i,k,r], out_i += sum_r c_ir          */
@@ -204,11 +209,11 @@ typedef struct mf_simplicial_bwd_args {
   const void* bias_gate;
   int32_t bias_dtype;
   int32_t grad_dtype;       /* mf_dtype of grad_out                          */
-  float* dq;                /* [B*H, N, D] fp32 each; NULL = not wanted      */
-  float* dk1;
-  float* dv1;
-  float* dk2;
-  float* dv2;
+  void* dq;                 /* [B*H, N, D] each, type `grads_dtype`; NULL = not wanted */
+  void* dk1;
+  void* dv1;
+  void* dk2;
+  void* dv2;
   float* du;                /* [B*H, N, N] fp32 each (bias only); NULL = not wanted */
   float* dv_bias;
   float* dw;
@@ -218,7 +223,7 @@ typedef struct mf_simplicial_bwd_args {
   int32_t tokens;
   int32_t head_dim;         /* 1..128                                        */
   int32_t dtype;            /* mf_dtype of q, k1, v1, k2, v2                 */
-  int32_t reserved;
+  int32_t grads_dtype;      /* ABI 10: MF_DTYPE_F32 (0) or MF_DTYPE_BF16     */
   /* Low-rank angle and message terms (ABI 9), laid out as in              */
   /* mf_simplicial_fwd_args; a group is absent when its first pointer is   */
   /* NULL.  Their gradients are fp32, zero-filled by the caller, written   */

@@ -51,7 +51,7 @@ EXPORTED_SYMBOLS = (
     "mf_pair_mlp_bias",
 )
 
-EXPECTED_ABI_VERSION = 9
+EXPECTED_ABI_VERSION = 10
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,
@@ -106,7 +106,7 @@ class MfSimplicialBwdArgs(ctypes.Structure):
         "bias_u", "bias_v", "bias_w", "bias_gate")] + \
         [("bias_dtype", ctypes.c_int32), ("grad_dtype", ctypes.c_int32)] + \
         [(n, ctypes.c_void_p) for n in ("dq", "dk1", "dv1", "dk2", "dv2", "du", "dv_bias", "dw", "dgate")] + \
-        [(n, ctypes.c_int32) for n in ("batch", "heads", "tokens", "head_dim", "dtype", "reserved",
+        [(n, ctypes.c_int32) for n in ("batch", "heads", "tokens", "head_dim", "dtype", "grads_dtype",
                                        "angle_rank", "message_rank")] + \
         [(n, ctypes.c_void_p) for n in (
             "angle_left", "angle_right", "angle_gate", "message_left", "message_right", "message_basis",

@@ -55,6 +55,7 @@ bool simplicial_pair_bwd_serves(const mf_simplicial_bwd_args* a);
 int simplicial_pair_bwd_max_tokens();
 size_t simplicial_pair_bwd_workspace_bytes(int batch, int heads);
 const int* simplicial_pair_bwd_served(const mf_simplicial_bwd_args* a);
+const int* simplicial_pair_bwd_unserved_count(const mf_simplicial_bwd_args* a);  // molecules left over
 int simplicial_pair_bwd_launch(const mf_simplicial_bwd_args* a, hipStream_t stream);
 
 #define MF_HIP_CHECK(expr)                                                     \

@@ -147,11 +147,12 @@ struct Params {
   const void* w;
   const void* gate;
   int bias_dtype;
-  float* dq;
-  float* dk1;
-  float* dv1;
-  float* dk2;
-  float* dv2;
+  void* dq;      // gradients, fp32 or (gout16) bf16
+  void* dk1;
+  void* dv1;
+  void* dk2;
+  void* dv2;
+  int gout16;
   float* du;
   float* dvb;
   float* dw;
@@ -162,6 +163,9 @@ struct Params {
   int OB;       // workgroups per (b, h, role)
   int vec;      // q/k/v/go/out rows 4-element loads are aligned (D % 4 == 0, aligned bases)
   const int* served;  // [B] nonzero: the pair kernel computed this molecule's gradients (or NULL)
+  const int* unserved;  // the number of molecules the pair kernel left over (with `served`)
+  int blocks;         // 3 B H OB work blocks; the grid may be smaller and loop over them
+  int served_lds;     // byte offset of the LDS copy of `served` (after the role's layout)
   // low-rank terms (LR instantiations): factors [B*H, N, N, R] fp32, gates [B*H, N], basis [H, Rm, D]
   const float* al;
   const float* ar;
@@ -231,6 +235,12 @@ __device__ __forceinline__ float4 ld4(const void* p, size_t row, int d0, int D, 
   return r;
 }
 
+// One gradient element, fp32 or rounded to bf16.
+__device__ __forceinline__ void store_grad(void* base, size_t i, float v, int bf16) {
+  if (bf16) static_cast<__bf16*>(base)[i] = __bf16(v);
+  else static_cast<float*>(base)[i] = v;
+}
+
 __device__ __forceinline__ float f4(const float4& v, int e) {
   return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
 }
@@ -278,7 +288,6 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
   constexpr int KS = S::KS;
   const int N = p.N, D = p.D, NP = p.NP;
   const int b = bh / p.H;
-  if (p.served != nullptr && p.served[b] != 0) return;  // the pair kernel's molecule (uniform)
   const bool has_pv = p.pv != nullptr;
   constexpr bool has_bias = BIAS;
   const bool vec = p.vec != 0;
@@ -900,8 +909,8 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
       acc_a[t][r] = group16_sum(acc_a[t][r]);
       if constexpr (ROLE != kRoleQ) acc_b[t][r] = group16_sum(acc_b[t][r]);
     }
-  float* out_a = ROLE == kRoleQ ? p.dq : (ROLE == kRoleJ ? p.dk1 : p.dk2);
-  float* out_b = ROLE == kRoleQ ? nullptr : (ROLE == kRoleJ ? p.dv1 : p.dv2);
+  void* out_a = ROLE == kRoleQ ? p.dq : (ROLE == kRoleJ ? p.dk1 : p.dk2);
+  void* out_b = ROLE == kRoleQ ? nullptr : (ROLE == kRoleJ ? p.dv1 : p.dv2);
   // lane (g, r16) writes d = dof(t, g) + (r16 & 3) for the tiles t with (t & 3) == r16 >> 2
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -915,8 +924,8 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
         va = acc_a[t][r];
         vb = acc_b[t][r];
       }
-    if (out_a) out_a[orow * D + d] = va;
-    if (out_b) out_b[orow * D + d] = vb;
+    if (out_a) store_grad(out_a, orow * D + d, va, p.gout16);
+    if (out_b) store_grad(out_b, orow * D + d, vb, p.gout16);
   }
   if constexpr (LR && ROLE == kRoleQ) {
     if (p.al && p.dag) {
@@ -951,14 +960,25 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
 template <int DP, bool M16, bool BIAS, bool LR>
 __global__ void __launch_bounds__((Shape<DP, M16, LR>::kThreads), (Shape<DP, M16, LR>::kMinBlocks)) simplicial_bwd_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  if (p.served != nullptr && *p.unserved == 0) return;  // the pair kernel served every molecule
   const int G = p.B * p.H * p.OB;
-  const int role = blockIdx.x / G;
-  const int blk = blockIdx.x - role * G;
-  const int bh = blk / p.OB;
-  const int ob = blk - bh * p.OB;
-  if (role == kRoleQ) run_role<DP, kRoleQ, M16, BIAS, LR>(p, smem, bh, ob);
-  else if (role == kRoleJ) run_role<DP, kRoleJ, M16, BIAS, LR>(p, smem, bh, ob);
-  else run_role<DP, kRoleK, M16, BIAS, LR>(p, smem, bh, ob);
+  const int* served = reinterpret_cast<const int*>(smem + p.served_lds);
+  if (p.served != nullptr) {
+    for (int i = threadIdx.x; i < p.B; i += Shape<DP, M16, LR>::kThreads)
+      const_cast<int*>(served)[i] = p.served[i];
+    __syncthreads();
+  }
+  for (int w = blockIdx.x; w < p.blocks; w += gridDim.x) {
+    const int role = w / G;
+    const int blk = w - role * G;
+    const int bh = blk / p.OB;
+    const int ob = blk - bh * p.OB;
+    if (p.served != nullptr && served[bh / p.H] != 0) continue;  // uniform: the pair kernel's molecule
+    if (w != int(blockIdx.x)) __syncthreads();  // the previous block's LDS reads are done
+    if (role == kRoleQ) run_role<DP, kRoleQ, M16, BIAS, LR>(p, smem, bh, ob);
+    else if (role == kRoleJ) run_role<DP, kRoleJ, M16, BIAS, LR>(p, smem, bh, ob);
+    else run_role<DP, kRoleK, M16, BIAS, LR>(p, smem, bh, ob);
+  }
 }
 
 // dc[row][r] = basis[h][r] . go[row] for every row of [B*H, N] (message term), and coeff[row][r] = 0:
@@ -1005,9 +1025,52 @@ __global__ void __launch_bounds__(256) lr_dbasis_kernel(Params p, float* dmb) {
   }
 }
 
+// 16-bit gradients are written in full: zeros at every row the kernels do not write -- padded queries (dq) and
+// keys (dk1, dv1, dk2, dv2), and every row of a molecule without a valid query or key.  One workgroup per
+// (molecule, head): the two mask rows are read once into LDS, then 16-byte stores of zeros.
+constexpr int kZeroMaxN = 4096;
+__global__ void __launch_bounds__(256) zero_rows_kernel(Params p) {
+  __shared__ uint8_t s_q[kZeroMaxN], s_k[kZeroMaxN];
+  __shared__ int s_cnt[2];
+  const int bh = blockIdx.x;
+  const int b = bh / p.H;
+  const int N = p.N, D = p.D;
+  const int tid = threadIdx.x;
+  if (tid < 2) s_cnt[tid] = 0;
+  __syncthreads();
+  int cq = 0, ck = 0;
+  for (int t = tid; t < N; t += 256) {
+    const uint8_t q = p.qv[size_t(b) * N + t] != 0, k = p.pkv[size_t(b) * N + t] != 0;
+    s_q[t] = q;
+    s_k[t] = k;
+    cq += q;
+    ck += k;
+  }
+  if (cq) atomicAdd(&s_cnt[0], cq);
+  if (ck) atomicAdd(&s_cnt[1], ck);
+  __syncthreads();
+  const bool empty = s_cnt[0] == 0 || s_cnt[1] == 0;
+  const int C = D / 8;  // 16-byte chunks per row (D % 8 == 0 on this path)
+  const size_t base = size_t(bh) * N * C;
+  const uint4 z{0u, 0u, 0u, 0u};
+  for (int u = tid; u < N * C; u += 256) {
+    const int row = u / C;
+    if (empty || !s_q[row]) static_cast<uint4*>(p.dq)[base + u] = z;
+    if (empty || !s_k[row]) {
+      static_cast<uint4*>(p.dk1)[base + u] = z;
+      static_cast<uint4*>(p.dv1)[base + u] = z;
+      static_cast<uint4*>(p.dk2)[base + u] = z;
+      static_cast<uint4*>(p.dv2)[base + u] = z;
+    }
+  }
+}
+
 template <int DP, bool M16, bool LR = false>
 int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
-  const size_t lds = Lay<DP, M16, LR>::bytes(prm.NP, has_pv, has_bias, (LR && prm.ml && prm.coeff) ? prm.RmP : 0);
+  size_t lds = Lay<DP, M16, LR>::bytes(prm.NP, has_pv, has_bias, (LR && prm.ml && prm.coeff) ? prm.RmP : 0);
+  lds = (lds + 15) & ~size_t(15);
+  prm.served_lds = int(lds);
+  if (prm.served != nullptr) lds += size_t(prm.B) * 4;
   DeviceInfo dev;
   int st = device_info(&dev);
   if (st != MF_OK) return st;
@@ -1026,7 +1089,10 @@ int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
   prm.OB = int(std::max(1LL, std::min<long long>(want, (prm.N + kW - 1) / kW)));
   const long long blocks = 3 * bh * prm.OB;
   if (blocks > 0x7fffffffLL) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: grid too large");
-  hipLaunchKernelGGL(kerns[has_bias], dim3(unsigned(blocks)), dim3(Shape<DP, M16, LR>::kThreads), lds, stream, prm);
+  prm.blocks = int(blocks);
+  // after the pair kernel most blocks are skipped: a grid of a few workgroups per CU loops over them
+  const long long grid = prm.served != nullptr ? std::min<long long>(blocks, 2LL * dev.num_cus) : blocks;
+  hipLaunchKernelGGL(kerns[has_bias], dim3(unsigned(grid)), dim3(Shape<DP, M16, LR>::kThreads), lds, stream, prm);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
 }
@@ -1089,7 +1155,22 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   } else if (a->dmessage_left || a->dmessage_right || a->dmessage_basis) {
     return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: message gradients requested without a message term");
   }
+  const bool gout16 = a->grads_dtype == MF_DTYPE_BF16;
+  if (a->grads_dtype != MF_DTYPE_F32 && !gout16)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: grads_dtype must be MF_DTYPE_F32 or MF_DTYPE_BF16");
+  if (gout16) {
+    if (a->dtype != MF_DTYPE_BF16 || a->grad_dtype != MF_DTYPE_BF16 || has_angle || has_msg)
+      return fail(MF_ERR_INVALID_ARGUMENT,
+                  "mf_simplicial_bwd: bf16 gradients need bf16 operands and grad_out and no low-rank term");
+    if (!a->dq || !a->dk1 || !a->dv1 || !a->dk2 || !a->dv2 || a->head_dim % 8 != 0 || a->tokens > kZeroMaxN)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: bf16 gradients need all five of dq, dk1, dv1, dk2, "
+                                           "dv2, a head_dim that is a multiple of 8 and at most 4096 tokens");
+    for (const void* ptr : {a->dq, a->dk1, a->dv1, a->dk2, a->dv2})
+      if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
+        return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: bf16 gradient buffers must be 16-byte aligned");
+  }
   Params prm{};
+  prm.gout16 = gout16 ? 1 : 0;
   prm.q = a->q; prm.k1 = a->k1; prm.v1 = a->v1; prm.k2 = a->k2; prm.v2 = a->v2; prm.go = a->grad_out;
   prm.out = a->out; prm.lse = a->lse;
   prm.qv = a->query_valid; prm.pkv = a->pair_key_valid; prm.pv = a->pair_valid;
@@ -1156,6 +1237,10 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   // bf16 operands and a bf16 grad_out: bf16 MFMA (K steps of 32 d), which stages grad_out rows as bf16 (exact
   // only for a bf16 grad_out).  Everything else -- fp16 operands, or a grad_out of another dtype -- takes the
   // fp32 path, which reads every operand in its own dtype.
+  if (gout16) {
+    hipLaunchKernelGGL(zero_rows_kernel, dim3(unsigned(a->batch * a->heads)), dim3(256), 0, s, prm);
+    MF_HIP_CHECK(hipGetLastError());
+  }
   if (a->dtype == MF_DTYPE_BF16 && a->grad_dtype == MF_DTYPE_BF16) {
     // molecules of at most 80 valid atoms take the pair formulation; the ownership kernel below takes the rest
     if (simplicial_pair_bwd_serves(a)) {
@@ -1163,6 +1248,7 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
       if (st != MF_OK) return st;
       if (a->tokens <= simplicial_pair_bwd_max_tokens()) return MF_OK;
       prm.served = simplicial_pair_bwd_served(a);
+      prm.unserved = simplicial_pair_bwd_unserved_count(a);
     }
     if (D <= 32) return launch<32, true>(prm, has_pv, has_bias, s);
     if (D <= 64) return launch<64, true>(prm, has_pv, has_bias, s);

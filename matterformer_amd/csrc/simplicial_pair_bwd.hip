@@ -40,9 +40,9 @@
 // than 40 valid keys run as two units that take alternate key pairs
 // (jp = part, part + 2, ...), the others as one.  Workgroup w runs unit w.
 // The two halves of a molecule own their dk1 / dv1 rows and hold partial
-// sums of dq, dk2 and dv2: part 0 writes its partials to the gradient rows,
-// part 1 to its slab of the workspace, and a third launch writes part 0 +
-// part 1 in that order.  (Handing the sums over inside the kernel would need
+// sums of dq, dk2 and dv2: part 0 writes its partials to the fp32 gradient
+// rows (to its own slab of the workspace when the gradients are bf16), part 1
+// to its slab, and a third launch writes part 0 + part 1 in that order.  (Handing the sums over inside the kernel would need
 // a device-scope release and acquire per half, which on this part write back
 // and invalidate the whole L2 of the XCD and held each workgroup's CU for
 // tens of microseconds.)
@@ -92,16 +92,17 @@ struct Params {
   const uint8_t* qv;
   const uint8_t* pkv;
   const uint8_t* pv;
-  float* dq;
-  float* dk1;
-  float* dv1;
-  float* dk2;
-  float* dv2;
+  void* dq;               // gradients, fp32 or (gout16) bf16
+  void* dk1;
+  void* dv1;
+  void* dk2;
+  void* dv2;
+  int gout16;
   const int* total;       // plan: units in the list
   const uint32_t* units;  // plan: (b H + h) << 1 | part, longest first
   const int2* counts;     // plan: [B] valid keys, valid queries
   const uint16_t* lists;  // plan: [B][2][kMaxN] their atoms
-  float* slab;            // [B*H][3][kMaxN][DP] part 1's partial dq, dk2, dv2 (compacted rows)
+  float* slab;            // [B*H][2 parts][3][kMaxN][DP] partial dq, dk2, dv2 of split molecules (compacted rows)
   int H, N;
 };
 
@@ -120,12 +121,12 @@ struct Ws {
   size_t units, served, counts, lists, slab, bytes;
   Ws(int B, int H) {
     const size_t bh = size_t(B) * H;
-    units = 16;
+    units = 16;  // [0, 4): units in the list, [4, 8): molecules the pair kernel does not serve
     served = units + ((bh * 2 * 4 + 15) & ~size_t(15));
     counts = served + ((size_t(B) * 4 + 15) & ~size_t(15));
     lists = counts + size_t(B) * 8;
     slab = (lists + size_t(B) * 2 * kMaxN * 2 + 255) & ~size_t(255);
-    bytes = slab + bh * 3 * kMaxN * DP * 4;
+    bytes = slab + bh * 2 * 3 * kMaxN * DP * 4;
   }
 };
 constexpr int kPlanThreads = 1024;
@@ -135,7 +136,7 @@ constexpr int kMaxTokens = 512;  // mask rows the plan reads in one pass of 8 x 
 struct PlanParams {
   const uint8_t* qv;
   const uint8_t* pkv;
-  int* total;
+  int* total;       // total[0] units, total[1] unserved molecules
   uint32_t* units;
   int* served;
   int2* counts;     // [B] (valid keys, valid queries)
@@ -169,6 +170,14 @@ typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 mf_f16x4
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 mf_bf16x2;
+
+// One gradient element, fp32 or rounded to bf16.
+__device__ __forceinline__ void store_grad(void* base, size_t i, float v, int bf16) {
+  if (bf16) static_cast<__bf16*>(base)[i] = __bf16(v);
+  else static_cast<float*>(base)[i] = v;
+}
 
 // Largest magnitude of eight bf16 (as the 15-bit pattern: for positive values bit order is value order).
 __device__ __forceinline__ uint32_t absmax_bits8(const uint4 r) {
@@ -206,6 +215,14 @@ __device__ __forceinline__ mf_f16x8 cat8(const mf_f16x4 a, const mf_f16x4 b) {
 
 __device__ __forceinline__ mf_f32x4 mma(const mf_f16x8& a, const mf_f16x8& b, const mf_f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Workgroup barrier that orders LDS accesses only: unlike __syncthreads() it does not wait for this thread's
+// outstanding global stores (no workgroup reads back what these kernels store to global memory).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // DPP lane moves within rows of 16 (VALU, no LDS): quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
@@ -251,7 +268,7 @@ __global__ void __launch_bounds__(kPlanThreads) pair_bwd_plan(PlanParams pp) {
   __shared__ uint32_t s_cost[kMaxPlanBatch];
   __shared__ int s_units[kMaxPlanBatch];
   __shared__ int s_count[2 * kMaxPlanBatch];
-  __shared__ int s_total;
+  __shared__ int s_total, s_unserved;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int B = pp.B, H = pp.H, N = pp.N;
   constexpr int kRows = 4;
@@ -287,17 +304,21 @@ __global__ void __launch_bounds__(kPlanThreads) pair_bwd_plan(PlanParams pp) {
       if (lane == 0) s_count[r] = count;
     }
   }
-  if (tid == 0) s_total = 0;
-  __syncthreads();
+  if (tid == 0) {
+    s_total = 0;
+    s_unserved = 0;
+  }
+  lds_barrier();
   for (int b = tid; b < B; b += kPlanThreads) {
     const int nk = s_count[2 * b], nq = s_count[2 * b + 1];
     const bool served = nk > 0 && nq > 0 && nk <= kMaxN && nq <= kMaxN;
     s_cost[b] = served ? unit_cost(nk, nq) : 0u;
     s_units[b] = served ? H * parts_of(nk) : 0;
     pp.served[b] = served ? 1 : 0;
+    if (!served && nk > 0 && nq > 0) atomicAdd(&s_unserved, 1);
     pp.counts[b] = int2{nk, nq};
   }
-  __syncthreads();
+  lds_barrier();
   // rank: kTpm threads per molecule, each over every kTpm-th other molecule, partial sums added over the
   // thread group (adjacent lanes) by shuffles
   const int tpm = B >= kPlanThreads ? 1 : (B > kPlanThreads / 2 ? 2 : (B > kPlanThreads / 4 ? 4 : (B > kPlanThreads / 8 ? 8 : 16)));
@@ -318,8 +339,11 @@ __global__ void __launch_bounds__(kPlanThreads) pair_bwd_plan(PlanParams pp) {
       atomicAdd(&s_total, s_units[b]);
     }
   }
-  __syncthreads();
-  if (tid == 0) *pp.total = s_total;
+  lds_barrier();
+  if (tid == 0) {
+    pp.total[0] = s_total;
+    pp.total[1] = s_unserved;
+  }
 }
 
 // The unit's main loop (key tiles x key pairs x the NQT query tiles), its dk1 / dv1 rows, dq, and for a split
@@ -333,8 +357,10 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   const int g = lane >> 4;
   const int r16 = lane & 15;
   const size_t rbase = size_t(bh) * p.N;
-  float* slab = p.slab + size_t(bh) * 3 * kMaxN * DP;
-  const bool to_slab = part == 1;
+  // split molecules: part 1's partial dq, dk2, dv2 go to its slab, and part 0's too when the gradients are
+  // 16-bit (fp32 ones hold part 0's partials in the gradient rows until the combine launch)
+  const bool to_slab = parts == 2 && (part == 1 || p.gout16 != 0);
+  float* slab = p.slab + (size_t(bh) * 2 + part) * 3 * kMaxN * DP;
   _Float16* Qs = reinterpret_cast<_Float16*>(smem + Lay::rows);
   _Float16* Gs = Qs + kMaxN * KS;
   _Float16* K1s = Gs + kMaxN * KS;
@@ -590,7 +616,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
           sl[16 * DP + (4 * g + r) * DP + 16 * dt + r16] = dv2a[dt][r];
         }
     }
-    __syncthreads();
+    lds_barrier();
     for (int u = tid; u < kSlot; u += kThreads) {
       const int which = u / (16 * DP);
       const int kk = (u / DP) % 16;
@@ -601,20 +627,20 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         s += slot[3 * kSlot + u];
         s *= which ? con[kFDv2] : con[kFDk2];
         if (to_slab) slab[size_t(1 + which) * kMaxN * DP + (k0 + kk) * DP + d] = s;
-        else (which ? p.dv2 : p.dk2)[(rbase + kidx[k0 + kk]) * DP + d] = s;
+        else store_grad(which ? p.dv2 : p.dk2, (rbase + kidx[k0 + kk]) * DP + d, s, p.gout16);
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   // ---- dk1 / dv1 rows of the unit's keys j (key pairs jp = j / 2 with jp % parts == part) ----
   for (int u = tid; u < nk * DP; u += kThreads) {
     if (((u / DP) >> 1) % parts != part) continue;
     const size_t o = (rbase + kidx[u / DP]) * DP + (u % DP);
-    p.dk1[o] = dk1a[u] * con[kFDk1];
-    p.dv1[o] = dv1a[u] * con[kFDv1];
+    store_grad(p.dk1, o, dk1a[u] * con[kFDk1], p.gout16);
+    store_grad(p.dv1, o, dv1a[u] * con[kFDv1], p.gout16);
   }
-  __syncthreads();  // rows and acc1 are free for the dq partials
+  lds_barrier();  // rows and acc1 are free for the dq partials
   // ---- dq: the four waves' partials in wave order ----
   float* dqs = reinterpret_cast<float*>(smem);
 #pragma unroll
@@ -625,14 +651,14 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       for (int r = 0; r < 4; ++r)
         dqs[(wave * kMaxN + qt * 16 + 4 * g + r) * DP + 16 * dt + r16] = dqa[qt][dt][r];
   }
-  __syncthreads();
+  lds_barrier();
   for (int u = tid; u < nq * DP; u += kThreads) {
     float s = dqs[u] + dqs[kMaxN * DP + u];
     s += dqs[2 * kMaxN * DP + u];
     s += dqs[3 * kMaxN * DP + u];
     s *= con[kFDq];
     if (to_slab) slab[u] = s;
-    else p.dq[(rbase + qidx[u / DP]) * DP + (u % DP)] = s;
+    else store_grad(p.dq, (rbase + qidx[u / DP]) * DP + (u % DP), s, p.gout16);
   }
 }
 
@@ -662,7 +688,7 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
     const int at = tid < kMaxN ? tid : tid - kMaxN;
     if (at < (tid < kMaxN ? nk : nq)) (tid < kMaxN ? kidx : qidx)[at] = p.lists[size_t(b) * 2 * kMaxN + tid];
   }
-  __syncthreads();
+  lds_barrier();
   const int parts = parts_of(nk);
   const size_t rbase = size_t(bh) * N;
   // ---- stage q, go, k1, k2, v1, v2 rows (compacted, zero past the counts) as fp16 scaled by 2^-e per operand
@@ -725,7 +751,7 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
       mx[tt] = wave_max_u32(mx[tt]);
       if (lane == 0) red[wave * 8 + tt] = mx[tt];
     }
-    __syncthreads();
+    lds_barrier();
     int ex[6];
 #pragma unroll
     for (int tt = 0; tt < 6; ++tt)
@@ -788,7 +814,7 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
     }
   }
   for (int u = tid; u < 2 * kMaxN * DP / 4; u += kThreads) reinterpret_cast<float4*>(dk1a)[u] = float4{0.f, 0.f, 0.f, 0.f};
-  __syncthreads();
+  lds_barrier();
 
   switch ((nq + 15) / 16) {
     case 1: unit_body<1>(p, smem, nq, nk, part, parts, bh, has_pv); break;
@@ -799,9 +825,9 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
   }
 }
 
-// Split molecules: part 0's partial dq, dk2, dv2 are in the gradient rows, part 1's in its slab; write
-// part 0 + part 1 (in that order).  One workgroup per (molecule, head); a separate launch, so the stream
-// orders it after both halves without any cross-workgroup fence.
+// Split molecules: part 0's partial dq, dk2, dv2 are in the fp32 gradient rows (or, 16-bit gradients, in its
+// slab), part 1's in its slab; write part 0 + part 1 (in that order).  One workgroup per (molecule, head); a
+// separate launch, so the stream orders it after both halves without any cross-workgroup fence.
 __global__ void __launch_bounds__(kThreads) pair_bwd_combine(Params p) {
   const int bh = blockIdx.x;
   const int b = bh / p.H;
@@ -809,13 +835,16 @@ __global__ void __launch_bounds__(kThreads) pair_bwd_combine(Params p) {
   const int nk = nkq.x, nq = nkq.y;
   if (nk <= 0 || nq <= 0 || nk > kMaxN || nq > kMaxN || parts_of(nk) == 1) return;
   const size_t rbase = size_t(bh) * p.N;
-  const float* slab = p.slab + size_t(bh) * 3 * kMaxN * DP;
+  const float* slab0 = p.slab + size_t(bh) * 2 * 3 * kMaxN * DP;
+  const float* slab = slab0 + 3 * kMaxN * DP;  // part 1
   const uint16_t* lists = p.lists + size_t(b) * 2 * kMaxN;
+  const bool g16 = p.gout16 != 0;
   // rows: dq of the nq queries, then dk2 and dv2 of the nk keys, 16 float4 each; 8 per thread at a time
   const int nrows = nq + 2 * nk;
   for (int u0 = 0; u0 < nrows * 16; u0 += 8 * kThreads) {
     float4 a[8], c[8];
-    float* dst[8];
+    size_t dst[8];
+    void* base[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int u = min(u0 + int(threadIdx.x) + kThreads * i, nrows * 16 - 1);  // clamped: no branch around loads
@@ -823,14 +852,25 @@ __global__ void __launch_bounds__(kThreads) pair_bwd_combine(Params p) {
       const int which = row < nq ? 0 : (row < nq + nk ? 1 : 2);
       const int rr = which == 0 ? row : (which == 1 ? row - nq : row - nq - nk);
       const int idx = which == 0 ? lists[kMaxN + rr] : lists[rr];
-      dst[i] = (which == 0 ? p.dq : (which == 1 ? p.dk2 : p.dv2)) + (rbase + idx) * DP + 4 * q4;
-      a[i] = *reinterpret_cast<const float4*>(dst[i]);
-      c[i] = *reinterpret_cast<const float4*>(slab + size_t(which) * kMaxN * DP + rr * DP + 4 * q4);
+      base[i] = which == 0 ? p.dq : (which == 1 ? p.dk2 : p.dv2);
+      dst[i] = (rbase + idx) * DP + 4 * q4;
+      const size_t so = size_t(which) * kMaxN * DP + rr * DP + 4 * q4;
+      a[i] = g16 ? *reinterpret_cast<const float4*>(slab0 + so)
+                 : *reinterpret_cast<const float4*>(static_cast<const float*>(base[i]) + dst[i]);
+      c[i] = *reinterpret_cast<const float4*>(slab + so);
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (u0 + int(threadIdx.x) + kThreads * i < nrows * 16)
-        *reinterpret_cast<float4*>(dst[i]) = float4{a[i].x + c[i].x, a[i].y + c[i].y, a[i].z + c[i].z, a[i].w + c[i].w};
+    for (int i = 0; i < 8; ++i) {
+      if (u0 + int(threadIdx.x) + kThreads * i >= nrows * 16) continue;
+      const float4 v{a[i].x + c[i].x, a[i].y + c[i].y, a[i].z + c[i].z, a[i].w + c[i].w};
+      if (g16) {
+        const uint2 w{__builtin_bit_cast(uint32_t, mf_bf16x2{__bf16(v.x), __bf16(v.y)}),
+                      __builtin_bit_cast(uint32_t, mf_bf16x2{__bf16(v.z), __bf16(v.w)})};
+        *reinterpret_cast<uint2*>(static_cast<__bf16*>(base[i]) + dst[i]) = w;
+      } else {
+        *reinterpret_cast<float4*>(static_cast<float*>(base[i]) + dst[i]) = v;
+      }
+    }
   }
 }
 
@@ -860,6 +900,10 @@ size_t simplicial_pair_bwd_workspace_bytes(int batch, int heads) {
 const int* simplicial_pair_bwd_served(const mf_simplicial_bwd_args* a) {
   const pbwd::Ws ws(a->batch, a->heads);
   return reinterpret_cast<const int*>(static_cast<const unsigned char*>(a->workspace) + ws.served);
+}
+
+const int* simplicial_pair_bwd_unserved_count(const mf_simplicial_bwd_args* a) {
+  return static_cast<const int*>(a->workspace) + 1;
 }
 
 int simplicial_pair_bwd_launch(const mf_simplicial_bwd_args* a, hipStream_t stream) {
@@ -896,6 +940,7 @@ int simplicial_pair_bwd_launch(const mf_simplicial_bwd_args* a, hipStream_t stre
   p.pkv = a->pair_key_valid;
   p.pv = a->pair_valid;
   p.dq = a->dq; p.dk1 = a->dk1; p.dv1 = a->dv1; p.dk2 = a->dk2; p.dv2 = a->dv2;
+  p.gout16 = a->grads_dtype == MF_DTYPE_BF16 ? 1 : 0;
   p.H = a->heads;
   p.N = a->tokens;
   DeviceInfo dev;

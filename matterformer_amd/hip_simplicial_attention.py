@@ -395,7 +395,14 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
         raise ValueError("query_valid / pair_key_valid must be (B, N) and pair_valid (B, N, N)")
     ext = _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, angle_left, angle_right, angle_gate,
                           message_left, message_right, message_basis)
-    grads = [torch.zeros(B, H, N, D, device=dev, dtype=torch.float32) for _ in range(5)]
+    # bf16 operands, grad_out and leaves, no low-rank term: the library writes every row of bf16 gradients
+    # (no fill, no cast); otherwise fp32 gradients, zero-filled here and cast to the leaves' dtypes
+    g16 = (dt == torch.bfloat16 and gdt == torch.bfloat16 and ext.angle is None and ext.message is None
+           and D % 8 == 0 and N <= 4096 and all(t.dtype == torch.bfloat16 for t in (q, k1, v1, k2, v2)))
+    if g16:
+        grads = [torch.empty(B, H, N, D, device=dev, dtype=torch.bfloat16) for _ in range(5)]
+    else:
+        grads = [torch.zeros(B, H, N, D, device=dev, dtype=torch.float32) for _ in range(5)]
     bias_grads = [None] * 4
     if ext.bias is not None:
         for idx, (name, shape) in enumerate((("need_du", (B, H, N, N)), ("need_dv_bias", (B, H, N, N)),
@@ -432,7 +439,8 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
         dq=grads[0].data_ptr(), dk1=grads[1].data_ptr(), dv1=grads[2].data_ptr(), dk2=grads[3].data_ptr(),
         dv2=grads[4].data_ptr(), du=_native.ptr(bias_grads[0]), dv_bias=_native.ptr(bias_grads[1]),
         dw=_native.ptr(bias_grads[2]), dgate=_native.ptr(bias_grads[3]),
-        batch=B, heads=H, tokens=N, head_dim=D, dtype=_native.dtype_code(dt), reserved=0,
+        batch=B, heads=H, tokens=N, head_dim=D, dtype=_native.dtype_code(dt),
+        grads_dtype=_native.dtype_code(torch.bfloat16 if g16 else torch.float32),
         angle_rank=f.get("angle_rank", 0), message_rank=f.get("message_rank", 0),
         angle_left=f.get("angle_left"), angle_right=f.get("angle_right"), angle_gate=f.get("angle_gate"),
         message_left=f.get("message_left"), message_right=f.get("message_right"),
@@ -447,7 +455,7 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
     if status == _native.MF_ERR_UNSUPPORTED:
         return None
     _native.check(status, "mf_simplicial_bwd")
-    core = [g.to(t.dtype) for g, t in zip(grads, (q, k1, v1, k2, v2))]
+    core = grads if g16 else [g.to(t.dtype) for g, t in zip(grads, (q, k1, v1, k2, v2))]
     optional = [None] * 10
     if ext.bias is not None:
         for idx, src in enumerate((u, v_bias, w, gate)):

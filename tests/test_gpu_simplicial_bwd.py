@@ -251,3 +251,64 @@ def test_low_rank_terms_run_on_the_kernel(cuda):
                                             angle_gate=ag, precision="ieee_fp32")
     assert hsa.last_backward_impl == "hip"
     assert res[9] is not None and res[11] is not None
+
+
+def _abi_bwd(ops, go, out32, lse, qv, pkv, grads_dtype):
+    """mf_simplicial_bwd through the C ABI; gradient buffers filled with NaN (bf16) or zeros (fp32, the
+    caller's fill that the fp32 contract asks for)."""
+    from matterformer_amd import _native
+
+    B, H, N, D = ops[0].shape
+    dev = ops[0].device
+    lib = _native.lib()
+    nbytes = int(lib.mf_simplicial_bwd_workspace_size(B, H, N, D, 0))
+    ws = torch.empty(max(nbytes, 16), device=dev, dtype=torch.uint8)
+    if grads_dtype == torch.bfloat16:
+        grads = [torch.full((B, H, N, D), float("nan"), device=dev, dtype=torch.bfloat16) for _ in range(5)]
+    else:
+        grads = [torch.zeros(B, H, N, D, device=dev) for _ in range(5)]
+    qb, pb = qv.to(torch.bool).contiguous(), pkv.to(torch.bool).contiguous()
+    args = _native.MfSimplicialBwdArgs(
+        q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(), k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
+        grad_out=go.data_ptr(), out=out32.data_ptr(), lse=lse.float().contiguous().data_ptr(),
+        query_valid=qb.data_ptr(), pair_key_valid=pb.data_ptr(), pair_valid=None,
+        grad_dtype=_native.dtype_code(torch.bfloat16), dq=grads[0].data_ptr(), dk1=grads[1].data_ptr(),
+        dv1=grads[2].data_ptr(), dk2=grads[3].data_ptr(), dv2=grads[4].data_ptr(), batch=B, heads=H, tokens=N,
+        head_dim=D, dtype=_native.dtype_code(torch.bfloat16), grads_dtype=_native.dtype_code(grads_dtype),
+        workspace=ws.data_ptr(), workspace_bytes=nbytes)
+    with torch.cuda.device(dev):
+        _native.check(lib.mf_simplicial_bwd(args, _native.current_stream(dev)), "mf_simplicial_bwd")
+    torch.cuda.synchronize()
+    return grads
+
+
+@pytest.mark.parametrize("counts", [[70, 41, 0, 12], [150, 64, 1, 33]], ids=["pair_only", "with_ownership"])
+def test_bf16_gradients_written_in_full(cuda, counts):
+    """grads_dtype bf16: every row of the five gradients is written (buffers start as NaN; padded rows and a
+    molecule without valid queries come back 0), and the values are the fp32-gradient call's rounded to bf16
+    (both paths form the same fp32 sums).  The second case has a 150-atom molecule (ownership kernel) beside
+    pair-kernel molecules, one of them split in two halves."""
+    B, H, N, D = len(counts), 2, max(counts) + 3, 64
+    case = random_simplicial(B, H, N, D, seed=71, counts=counts, std=logit_std(D))
+    q, k1, v1, k2, v2, qv, pkv, pv = case
+    qv = qv.clone()
+    qv[2] = False  # molecule 2: keys but no valid query
+    gen = torch.Generator().manual_seed(72)
+    go = torch.randn(B, H, N, D, generator=gen).to(torch.bfloat16).to(cuda)
+    ops = [t.to(torch.bfloat16).to(cuda).contiguous() for t in (q, k1, v1, k2, v2)]
+    qv, pkv = qv.to(cuda), pkv.to(cuda)
+    out, lse, out32 = hip_simplicial_attention_forward(*ops, query_valid=qv, pair_key_valid=pkv, pair_valid=None,
+                                                       precision="bf16_tc")
+    g16 = _abi_bwd(ops, go, out32, lse, qv, pkv, torch.bfloat16)
+    g32 = _abi_bwd(ops, go, out32, lse, qv, pkv, torch.float32)
+    for name, a, r in zip(GRAD_NAMES, g16, g32):
+        assert not torch.isnan(a).any(), name
+        assert torch.equal(a, r.to(torch.bfloat16)), name
+    # padded rows, and every row of molecule 2, are zero
+    qvc, pkvc = qv.cpu(), pkv.cpu()
+    for b in range(B):
+        rows_q = ~qvc[b] if b != 2 else torch.ones(N, dtype=torch.bool)
+        rows_k = ~pkvc[b] if b != 2 else torch.ones(N, dtype=torch.bool)
+        assert not g16[0][b][:, rows_q.to(cuda)].any()
+        for g in g16[1:]:
+            assert not g[b][:, rows_k.to(cuda)].any()
