@@ -713,7 +713,8 @@ def measure_simplicial_extras(lib, w, wd) -> dict:
                                           pair_key_valid=wd.pair_key_valid, pair_valid=None, precision="bf16_tc")
 
     bwd_step()
-    bwd_ms, _ = timed_loop(torch.cuda.current_stream(), bwd_step, 10, 2)
+    bwd_eager_ms, _ = timed_loop(torch.cuda.current_stream(), bwd_step, 10, 2)
+    bwd_ms = _graph_ms(bwd_step, per_graph=10, replays=5)
     bwd_flops = 3 * fwd_flops  # dP, dq, dk1, dk2, dv1, dv2: 12 D n^3 per head against the forward's 4 D n^3
     res["fwd_bwd"] = {
         "fwd_ms": round(train_ms, 5), "bwd_ms": round(bwd_ms, 5), "ms": round(train_ms + bwd_ms, 5),
@@ -722,9 +723,12 @@ def measure_simplicial_extras(lib, w, wd) -> dict:
         "bwd_roofline": {"bound": "mfma", "achieved": round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 3),
                          "peak": BF16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 5),
-                         "kernel": "mf::sbwd::simplicial_bwd_kernel<64, bf16 MFMA>, the 3 roles in one launch "
-                                   "(deterministic, no atomics)",
-                         "kernel_ms": round(bwd_ms, 5), "note": "eager call incl. zero-fills and casts"},
+                         "kernel": "mf::pbwd::pair_bwd_kernel (pairs as keys, fp16 operands, LPT plan, large "
+                                   "molecules in two halves) with its plan, combine and zero-rows launches; "
+                                   "deterministic, no atomics",
+                         "kernel_ms": round(bwd_ms, 5),
+                         "note": "hip_simplicial_attention_backward graph-replayed, bf16 gradients written by the "
+                                 "kernels (no fill, no cast); eager call " + f"{bwd_eager_ms:.4f} ms"},
     }
 
     # factorized bias (bf16), the default trunk's call: the pair kernel with the bias K step

@@ -269,6 +269,29 @@ __device__ __forceinline__ float4 ld_r4(const float* p, int rem, int vec) {
   return r;
 }
 
+// DPP moves within 16-lane rows (VALU, no LDS): quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __uint_as_float(uint32_t(__builtin_amdgcn_update_dpp(0, int(__float_as_uint(v)), CTRL, 0xf, 0xf, false)));
+}
+
+// Sum over each 16-lane row, in every lane of the row (pairs, quads, halves, rows).
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f<0xb1>(x);
+  x += dpp_f<0x4e>(x);
+  x += dpp_f<0x141>(x);
+  return x + dpp_f<0x140>(x);
+}
+
+// Sum over the four 16-lane rows, (r0 + r2) + (r1 + r3) in every lane: the gfx950 lane swaps.
+__device__ __forceinline__ float rows4_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // x + its partners in the other three 16-lane groups (lanes l ^ 16, l ^ 32), in a fixed order
 __device__ __forceinline__ float4 sum_groups4(float4 v) {
   v.x += __shfl_xor(v.x, 16, 64); v.y += __shfl_xor(v.y, 16, 64);
@@ -683,7 +706,7 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
           float base = 0.0f;
           if (has_bias && ok) {
             const int co = kidx[cb0 + c];
-            float be = 0.0f, bc = 0.0f;  // terms of (row, col) and of (outer, col)
+            float be, bc;  // terms of (row, col) and of (outer, col)
             if constexpr (ROLE == kRoleQ) {
               bc = ld1(p.vb, orow * N + co, p.bias_dtype);            // v[i=o][k=c]
               be = ld1(p.w, (rbase + ro) * N + co, p.bias_dtype);     // w[j=r][k=c]
@@ -717,8 +740,7 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
       // bias sums: role Q du (row sums) and dv (column sums), role J dw (column sums of gate_r dS)
       if (has_bias) {
         if constexpr (ROLE == kRoleQ) {
-          rowsum += __shfl_xor(rowsum, 16, 64);
-          rowsum += __shfl_xor(rowsum, 32, 64);
+          rowsum = rows4_sum(rowsum);
           if (g == 0 && row_ok) wrow[wave * NP + row] += rowsum;
         }
         if constexpr (ROLE != kRoleK) {
@@ -727,10 +749,7 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               float x = ROLE == kRoleQ ? sv[kt][r] : gate_r * sv[kt][r];
-              x += __shfl_xor(x, 1, 64);
-              x += __shfl_xor(x, 2, 64);
-              x += __shfl_xor(x, 4, 64);
-              x += __shfl_xor(x, 8, 64);
+              x = row16_sum(x);
               if (r16 == 0) wcol[wave * kCols + kt * 16 + 4 * g + r] += x;
             }
         }
