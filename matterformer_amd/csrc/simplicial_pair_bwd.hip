@@ -102,7 +102,22 @@ struct Params {
   const uint32_t* units;  // plan: (b H + h) << 1 | part, longest first
   const int2* counts;     // plan: [B] valid keys, valid queries
   const uint16_t* lists;  // plan: [B][2][kMaxN] their atoms
-  float* slab;            // [B*H][2 parts][3][kMaxN][DP] partial dq, dk2, dv2 of split molecules (compacted rows)
+  float* slab;            // [B*H][2 parts][5][kMaxN][DP] partial dq, dk2, dv2 of split molecules and (bias)
+                          // the dk1, dv1 sums of the unit's keys (compacted rows)
+  // factorized bias (BIAS kernels): S += gate_i (u_ij + v_ik + w_jk), u / v / w [B*H, N, N], gate [B*H, N]
+  // bf16; gradients fp32 (NULL = not wanted)
+  const uint16_t* bu;
+  const uint16_t* bv;
+  const uint16_t* bw;
+  const uint16_t* bg;
+  float* du;
+  float* dvb;
+  float* dw;
+  float* dgate;
+  float* dupart;          // [B*H][kMaxN / 16 key tiles][kMaxN i][kMaxN j] per-key-tile sums over k of dS 2^-es
+  float* dvbpart;         // [B*H][2 parts][kMaxN k][kMaxN i] sums over the part's j of dS 2^-es
+  float* dgpart;          // [B*H][2 parts][kMaxN i] sums over the part's (j, k) of dS 2^-es (u + v + w)
+  float* fds;             // [B*H] 2^es of the unit (dS is carried as dS 2^-es)
   int H, N;
 };
 
@@ -118,7 +133,7 @@ __device__ __forceinline__ uint32_t unit_cost(int nk, int nq) {
 
 // Workspace of the pair path (16-byte aligned regions).
 struct Ws {
-  size_t units, served, counts, lists, slab, bytes;
+  size_t units, served, counts, lists, slab, dupart, dvbpart, dgpart, fds, bytes;
   Ws(int B, int H) {
     const size_t bh = size_t(B) * H;
     units = 16;  // [0, 4): units in the list, [4, 8): molecules the pair kernel does not serve
@@ -126,7 +141,11 @@ struct Ws {
     counts = served + ((size_t(B) * 4 + 15) & ~size_t(15));
     lists = counts + size_t(B) * 8;
     slab = (lists + size_t(B) * 2 * kMaxN * 2 + 255) & ~size_t(255);
-    bytes = slab + bh * 2 * 3 * kMaxN * DP * 4;
+    dupart = slab + bh * 2 * 5 * kMaxN * DP * 4;
+    dvbpart = dupart + bh * (kMaxN / 16) * kMaxN * kMaxN * 4;
+    dgpart = dvbpart + bh * 2 * kMaxN * kMaxN * 4;
+    fds = dgpart + bh * 2 * kMaxN * 4;
+    bytes = fds + bh * 4;
   }
 };
 constexpr int kPlanThreads = 1024;
@@ -144,31 +163,44 @@ struct PlanParams {
   int B, H, N;
 };
 
-// LDS layout (bytes)
+// LDS layout (bytes).  BIAS: no dk1 / dv1 sums (they run in the workspace) but the bias terms u^T [j][i],
+// v^T [k][i] (bf16 as given) and the gates.
+constexpr int KU = kMaxN + 8;  // bf16 row stride of u^T, v^T (176 B)
+template <bool BIAS>
 struct Lay {
-  static constexpr size_t rows = 0;                                       // q, go, k1, k2, v1, v2: [80][KS] fp16
-  static constexpr size_t acc1 = rows + size_t(6) * kMaxN * KS * 2;       // dk1, dv1 of the wave's j: [2][80][64] f32
-  static constexpr size_t slot = acc1 + size_t(2) * kMaxN * DP * 4;       // [4 waves][kSlot] f32
-  static constexpr size_t scr = slot + size_t(kWaves) * kSlot * 4;        // [4 waves][2][32][SS] fp16
-  static constexpr size_t lse2 = scr + size_t(kWaves) * 2 * 32 * SS * 2;  // [80] f32
-  static constexpr size_t dlt = lse2 + kMaxN * 4;                         // [80] f32
-  static constexpr size_t pvb = dlt + kMaxN * 4;                          // [80][3] u32 pair bits
-  static constexpr size_t kidx = pvb + kMaxN * 3 * 4;                     // [80] i32
-  static constexpr size_t qidx = kidx + kMaxN * 4;                        // [80] i32
-  static constexpr size_t cnt = qidx + kMaxN * 4;                         // [4] i32
-  static constexpr size_t red = cnt + 16;                                 // [4 waves][8] u32 operand maxima
-  static constexpr size_t con = red + kWaves * 8 * 4;                     // [8] f32 unit constants (kC*)
+  static constexpr size_t rows = 0;                                            // q, go, k1, k2, v1, v2: [80][KS] fp16
+  static constexpr size_t acc1 = rows + size_t(6) * kMaxN * KS * 2;            // dk1, dv1 of the wave's j: [2][80][64] f32
+  static constexpr size_t slot = acc1 + (BIAS ? 0 : size_t(2) * kMaxN * DP * 4);  // [4 waves][kSlot] f32
+  static constexpr size_t dvb = slot + size_t(kWaves) * kSlot * 4;             // BIAS: [4 waves][5][16 k][16 i] f32
+  static constexpr size_t scr = dvb + (BIAS ? size_t(kWaves) * NT * 256 * 4 : 0);  // [4 waves][2][32][SS] fp16
+  static constexpr size_t ut = scr + size_t(kWaves) * 2 * 32 * SS * 2;         // BIAS: [80][KU] bf16
+  static constexpr size_t vt = ut + (BIAS ? size_t(kMaxN) * KU * 2 : 0);      // BIAS: [80][KU] bf16
+  static constexpr size_t gt = vt + (BIAS ? size_t(kMaxN) * KU * 2 : 0);      // BIAS: [2][80] f32 gate, gate log2 e
+  static constexpr size_t lse2 = gt + (BIAS ? 2 * kMaxN * 4 : 0);              // [80] f32
+  static constexpr size_t dlt = lse2 + kMaxN * 4;                              // [80] f32
+  static constexpr size_t pvb = dlt + kMaxN * 4;                               // [80][3] u32 pair bits
+  static constexpr size_t kidx = pvb + kMaxN * 3 * 4;                          // [80] i32
+  static constexpr size_t qidx = kidx + kMaxN * 4;                             // [80] i32
+  static constexpr size_t cnt = qidx + kMaxN * 4;                              // [4] i32
+  static constexpr size_t red = cnt + 16;                                      // [4 waves][8] u32 operand maxima
+  static constexpr size_t con = red + kWaves * 8 * 4;                          // [8] f32 unit constants (kC*)
   static constexpr size_t bytes = con + 8 * 4;
-  static_assert(size_t(kWaves) * kMaxN * DP * 4 <= slot, "dq partials reuse rows + acc1");
+  static_assert(bytes <= 160 * 1024, "one workgroup per CU");
+  // BIAS passes of at most 3 query tiles: the four waves' dq partials in slot + dvb
+  static_assert(!BIAS || size_t(kWaves) * 48 * DP * 4 <= scr - slot, "dq partials of a pass fit slot + dvb");
+  static_assert(size_t(kWaves) * kMaxN * DP * 4 <= scr, "dq partials reuse rows + acc1 / slot");
+  static_assert(size_t(kMaxN) * 16 <= size_t(kSlot), "a wave's dv_bias partials of a key tile fit its slot");
+  static_assert(48 * 4 <= 2 * 32 * SS * 2, "a wave's dgate partials of a pass fit its scratch");
 };
 
 // Unit constants in LDS: S log2 e = S_c cS; dS 2^-es = P (dP_c cP - delta 2^-es); the written gradients are
 // the accumulated sums times fDq, fDk1, fDk2, fDv1, fDv2.
-enum { kCS = 0, kCP, kFDq, kFDk1, kFDk2, kFDv1, kFDv2 };
+enum { kCS = 0, kCP, kFDq, kFDk1, kFDk2, kFDv1, kFDv2, kFDs };
 
 typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 mf_f16x4;
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_u16(uint16_t w) { return __uint_as_float(uint32_t(w) << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 mf_bf16x2;
@@ -250,6 +282,12 @@ __device__ __forceinline__ float sum8(float x) {
   x += __uint_as_float(dpp<kDppXor1>(__float_as_uint(x)));
   x += __uint_as_float(dpp<kDppXor2>(__float_as_uint(x)));
   return x + __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(x)));
+}
+
+// Sum over each 16-lane row, in every lane of the row.
+__device__ __forceinline__ float row16_sum(float x) {
+  x = sum8(x);
+  return x + __uint_as_float(dpp<kDppMirror>(__float_as_uint(x)));
 }
 
 // Sum over the four 16-lane groups, (g0 + g2) + (g1 + g3) in every lane: the gfx950 lane swaps (VALU, no LDS).
@@ -346,11 +384,16 @@ __global__ void __launch_bounds__(kPlanThreads) pair_bwd_plan(PlanParams pp) {
   }
 }
 
-// The unit's main loop (key tiles x key pairs x the NQT query tiles), its dk1 / dv1 rows, dq, and for a split
-// molecule the combination of the two halves.  LDS as staged by the kernel.
-template <int NQT>
+// The unit's main loop (key tiles x key pairs x NQT query tiles from tile qt0), its dk1 / dv1 rows, dq, and
+// for a split molecule the combination of the two halves.  LDS as staged by the kernel.  A unit may run its
+// query tiles in passes (first .. last): every key-side sum is linear in the queries, so a later pass adds to
+// what the earlier ones left (dk2 / dv2 partials in the unit's slab rows, the dk1 / dv1 sums and dw in the
+// workspace, each read back by the thread that wrote it); dq and the query-side bias sums belong to the pass.
+template <int NQT, bool BIAS>
 __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, int nq, int nk, int part, int parts,
-                                          int bh, bool has_pv) {
+                                          int bh, bool has_pv, int qt0, bool first, bool last) {
+  using Ly = Lay<BIAS>;
+  const int q0 = qt0 * 16;
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = wave_id();
@@ -360,28 +403,44 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   // split molecules: part 1's partial dq, dk2, dv2 go to its slab, and part 0's too when the gradients are
   // 16-bit (fp32 ones hold part 0's partials in the gradient rows until the combine launch)
   const bool to_slab = parts == 2 && (part == 1 || p.gout16 != 0);
-  float* slab = p.slab + (size_t(bh) * 2 + part) * 3 * kMaxN * DP;
-  _Float16* Qs = reinterpret_cast<_Float16*>(smem + Lay::rows);
+  float* slab = p.slab + (size_t(bh) * 2 + part) * 5 * kMaxN * DP;
+  _Float16* Qs = reinterpret_cast<_Float16*>(smem + Ly::rows);
   _Float16* Gs = Qs + kMaxN * KS;
   _Float16* K1s = Gs + kMaxN * KS;
   _Float16* K2s = K1s + kMaxN * KS;
   _Float16* V1s = K2s + kMaxN * KS;
   _Float16* V2s = V1s + kMaxN * KS;
-  float* dk1a = reinterpret_cast<float*>(smem + Lay::acc1);
+  float* dk1a = reinterpret_cast<float*>(smem + Ly::acc1);
   float* dv1a = dk1a + kMaxN * DP;
-  float* slot = reinterpret_cast<float*>(smem + Lay::slot);
-  _Float16* scr = reinterpret_cast<_Float16*>(smem + Lay::scr) + wave * 2 * 32 * SS;
-  const float* con = reinterpret_cast<const float*>(smem + Lay::con);
+  float* slot = reinterpret_cast<float*>(smem + Ly::slot);
+  _Float16* scr = reinterpret_cast<_Float16*>(smem + Ly::scr) + wave * 2 * 32 * SS;
+  const float* con = reinterpret_cast<const float*>(smem + Ly::con);
   const float cS = con[kCS], cP = con[kCP];
-  const float* lse2 = reinterpret_cast<const float*>(smem + Lay::lse2);
-  const float* dlt = reinterpret_cast<const float*>(smem + Lay::dlt);
-  const uint32_t* pvb = reinterpret_cast<const uint32_t*>(smem + Lay::pvb);
-  const int* kidx = reinterpret_cast<const int*>(smem + Lay::kidx);
-  const int* qidx = reinterpret_cast<const int*>(smem + Lay::qidx);
-  int* cnt = reinterpret_cast<int*>(smem + Lay::cnt);
+  const float* lse2 = reinterpret_cast<const float*>(smem + Ly::lse2) + q0;  // the pass's queries
+  const float* dlt = reinterpret_cast<const float*>(smem + Ly::dlt) + q0;
+  const _Float16* Qp = Qs + q0 * KS;
+  const _Float16* Gp = Gs + q0 * KS;
+  const uint32_t* pvb = reinterpret_cast<const uint32_t*>(smem + Ly::pvb);
+  const int* kidx = reinterpret_cast<const int*>(smem + Ly::kidx);
+  const int* qidx = reinterpret_cast<const int*>(smem + Ly::qidx);
+  // BIAS: the staged bias terms, and the dk1 / dv1 sums of the unit's keys in the workspace (slab rows 3, 4)
+  const uint16_t* uT = reinterpret_cast<const uint16_t*>(smem + Ly::ut) + q0;
+  const uint16_t* vT = reinterpret_cast<const uint16_t*>(smem + Ly::vt) + q0;
+  const float* cg = reinterpret_cast<const float*>(smem + Ly::gt) + q0;
+  float* sk1 = slab + 3 * kMaxN * DP;
+  float* sv1 = slab + 4 * kMaxN * DP;
+  const int N = p.N;
+  // BIAS: the B operand that sums dS over the keys of each j of a pair tile (column c = pair j index)
+  const mf_f16x8 jsum = r16 == (g >> 1) ? mf_f16x8{1, 1, 1, 1, 1, 1, 1, 1} : mf_f16x8{0, 0, 0, 0, 0, 0, 0, 0};
 
   const int nkt = (nk + 15) / 16;
   const int njp = (nk + 1) / 2;
+  // BIAS: dgate partial of queries qt 16 + 4 g + r over the lane's (j, k)
+  float accg[NQT][4];
+#pragma unroll
+  for (int t = 0; t < NQT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) accg[t][r] = 0.0f;
 
   mf_f32x4 dqa[NQT][4];
 #pragma unroll
@@ -401,12 +460,10 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     // keys k0 + 8 (g & 1) + e at d = 16 dt + r16: the dq B operand (transposed reads; lane 4 e' + a of a group
     // addresses row e' (+4), columns 4 a .. 4 a + 3)
     mf_f16x8 kcol[4];
-    // keys k0 + 4 g + r at d = 16 dt + r16: the dk1 / dv1 sums
+    // keys k0 + 4 g + r at d = 16 dt + r16: the dk1 / dv1 sums (BIAS: read in each pair tile's epilogue, which
+    // leaves the registers to the bias sums)
     float kk2[4][4], kv2[4][4];
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const _Float16* pc = K2s + (k0 + 8 * (g & 1) + (r16 >> 2)) * KS + 16 * dt + 4 * (r16 & 3);
-      kcol[dt] = cat8(read_tr16(pc), read_tr16(pc + 4 * KS));
+    auto read_kv2 = [&](int dt) {
       const int roff = (k0 + 4 * g + (r16 >> 2)) * KS + 16 * dt + 4 * (r16 & 3);
       const auto a4 = read_tr16(K2s + roff);
       const auto b4 = read_tr16(V2s + roff);
@@ -415,6 +472,19 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         kk2[dt][r] = float(a4[r]);
         kv2[dt][r] = float(b4[r]);
       }
+    };
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const _Float16* pc = K2s + (k0 + 8 * (g & 1) + (r16 >> 2)) * KS + 16 * dt + 4 * (r16 & 3);
+      kcol[dt] = cat8(read_tr16(pc), read_tr16(pc + 4 * KS));
+      if constexpr (!BIAS) read_kv2(dt);
+    }
+    // BIAS: this wave's dv_bias partials of the key tile (LDS, [qt][key r16][query 4 g + r])
+    float* dvl = reinterpret_cast<float*>(smem + Ly::dvb) + wave * NT * 256;
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt)
+        *reinterpret_cast<float4*>(dvl + (qt * 16 + r16) * 16 + 4 * g) = float4{0.f, 0.f, 0.f, 0.f};
     }
     mf_f32x4 dk2a[4], dv2a[4];  // key k0 + 4 g + r, d = 16 dt + r16
 #pragma unroll
@@ -426,6 +496,13 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 
     for (int jp = part + parts * wave; jp < njp; jp += parts * kWaves) {
       const int ja = 2 * jp;
+      // BIAS: w of pairs (ja + jn, k0 + r16) (clamped indices, unconditional loads), and dw partials
+      float wv[2] = {0.0f, 0.0f}, dwa[2] = {0.0f, 0.0f};
+      if constexpr (BIAS) {
+        const int kc = kidx[min(k0 + r16, nk - 1)];
+#pragma unroll
+        for (int jn = 0; jn < 2; ++jn) wv[jn] = bf_u16(p.bw[(rbase + kidx[min(ja + jn, nk - 1)]) * N + kc]);
+      }
       // the epilogue's LDS operands, read now so that their latency hides under the query loop:
       // k1 / v1 of j = ja + jn at d = 16 dt + r16, and the dk1 / dv1 sums of j so far
       _Float16 k1h[2][4];
@@ -435,11 +512,30 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           k1h[jn][dt] = K1s[(ja + jn) * KS + 16 * dt + r16];
-          k1p[jn][dt] = float(k1h[jn][dt]);
-          v1p[jn][dt] = float(V1s[(ja + jn) * KS + 16 * dt + r16]);
-          d1k[jn][dt] = dk1a[(ja + jn) * DP + 16 * dt + r16];
-          d1v[jn][dt] = dv1a[(ja + jn) * DP + 16 * dt + r16];
+          if constexpr (!BIAS) {
+            k1p[jn][dt] = float(k1h[jn][dt]);
+            v1p[jn][dt] = float(V1s[(ja + jn) * KS + 16 * dt + r16]);
+          }
+          if constexpr (BIAS) {
+            d1k[jn][dt] = sk1[(ja + jn) * DP + 16 * dt + r16];
+            d1v[jn][dt] = sv1[(ja + jn) * DP + 16 * dt + r16];
+          } else {
+            d1k[jn][dt] = dk1a[(ja + jn) * DP + 16 * dt + r16];
+            d1v[jn][dt] = dv1a[(ja + jn) * DP + 16 * dt + r16];
+          }
         }
+      if constexpr (BIAS) {  // the workspace rows hold sums only after the first key tile (read back by the
+                             // g = 0 lanes that wrote them: the same thread, so in order)
+        if (kt == 0 && first) {
+#pragma unroll
+          for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+              d1k[jn][dt] = 0.0f;
+              d1v[jn][dt] = 0.0f;
+            }
+        }
+      }
       // ---- the pair tile's operands: W, Z (hi, lo) of pairs (ja + jn, k0 + r16), d = 32 s + 8 g + e ----
       mf_f16x8 wb[2][2], zh[2][2], zl[2][2];
 #pragma unroll
@@ -491,8 +587,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 #pragma unroll
           for (int h = 0; h < NH; ++h) {
             const int qt = qb + h;
-            const mf_f16x8 aq = *reinterpret_cast<const mf_f16x8*>(Qs + (qt * 16 + r16) * KS + 32 * s + 8 * g);
-            const mf_f16x8 ag = *reinterpret_cast<const mf_f16x8*>(Gs + (qt * 16 + r16) * KS + 32 * s + 8 * g);
+            const mf_f16x8 aq = *reinterpret_cast<const mf_f16x8*>(Qp + (qt * 16 + r16) * KS + 32 * s + 8 * g);
+            const mf_f16x8 ag = *reinterpret_cast<const mf_f16x8*>(Gp + (qt * 16 + r16) * KS + 32 * s + 8 * g);
 #pragma unroll
             for (int jn = 0; jn < 2; ++jn) {
               sacc[h][jn] = mma(aq, wb[jn][s], sacc[h][jn]);
@@ -518,14 +614,50 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
           const float4 dl = *reinterpret_cast<const float4*>(dlt + qt * 16 + 4 * g);
           const float l2v[4] = {l2.x, l2.y, l2.z, l2.w};
           const float dlv[4] = {dl.x, dl.y, dl.z, dl.w};
+          // BIAS: gate_i (u_ij + v_ik + w_jk) of the lane's queries and pairs (natural units)
+          float cl[4] = {0.f, 0.f, 0.f, 0.f}, base[2][4];
+          if constexpr (BIAS) {
+            // (the offset is opaque to the compiler, so these loads stay here instead of being hoisted out of
+            // the loops into registers held throughout)
+            int qo = qt * 16 + 4 * g;
+            asm volatile("" : "+v"(qo));
+            const float4 l4 = *reinterpret_cast<const float4*>(cg + kMaxN + qo);
+            cl[0] = l4.x; cl[1] = l4.y; cl[2] = l4.z; cl[3] = l4.w;
+            const uint2 v4 = *reinterpret_cast<const uint2*>(vT + (k0 + r16) * KU + qo);
+            const float vv[4] = {bf_lo(v4.x), bf_hi(v4.x), bf_lo(v4.y), bf_hi(v4.y)};
+#pragma unroll
+            for (int jn = 0; jn < 2; ++jn) {
+              const uint2 u4 = *reinterpret_cast<const uint2*>(uT + (ja + jn) * KU + qo);
+              const float uu[4] = {bf_lo(u4.x), bf_hi(u4.x), bf_lo(u4.y), bf_hi(u4.y)};
+#pragma unroll
+              for (int r = 0; r < 4; ++r) base[jn][r] = (uu[r] + vv[r]) + wv[jn];
+            }
+          }
 #pragma unroll
           for (int jn = 0; jn < 2; ++jn)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const float pp = pok[jn] ? fast_exp2(fmaf(sacc[h][jn][r], cS, -l2v[r])) : 0.0f;
+              float s2 = fmaf(sacc[h][jn][r], cS, -l2v[r]);
+              if constexpr (BIAS) s2 = fmaf(cl[r], base[jn][r], s2);
+              const float pp = pok[jn] ? fast_exp2(s2) : 0.0f;
               pvv[h][jn][r] = pp;
               dsv[h][jn][r] = pp * fmaf(pacc[h][jn][r], cP, -dlv[r]);
+              if constexpr (BIAS) {
+                accg[qt][r] = fmaf(dsv[h][jn][r], base[jn][r], accg[qt][r]);
+                dwa[jn] = fmaf(cl[r], dsv[h][jn][r], dwa[jn]);
+              }
             }
+          if constexpr (BIAS) {
+            int vo = (qt * 16 + r16) * 16 + 4 * g;
+            asm volatile("" : "+v"(vo));
+            float4* pv = reinterpret_cast<float4*>(dvl + vo);
+            float4 a = *pv;
+            a.x += dsv[h][0][0] + dsv[h][1][0];
+            a.y += dsv[h][0][1] + dsv[h][1][1];
+            a.z += dsv[h][0][2] + dsv[h][1][2];
+            a.w += dsv[h][0][3] + dsv[h][1][3];
+            *pv = a;
+          }
           // dS [pair (jn, key)][query] into slot h of the wave's scratch
 #pragma unroll
           for (int jn = 0; jn < 2; ++jn) {
@@ -547,6 +679,22 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         for (int h = 0; h < NH; ++h)
 #pragma unroll
           for (int dt = 0; dt < 4; ++dt) dqa[qb + h][dt] = mma(ads[h], wc[dt], dqa[qb + h][dt]);
+        // BIAS: du partial of (query, j) over the tile's 16 keys: column c < 2 of dS x jsum is the sum for
+        // j = ja + c (lanes r16 < 2), written once per key tile
+        if constexpr (BIAS) {
+          if (p.du != nullptr) {
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+              const mf_f32x4 su = mma(ads[h], jsum, mf_f32x4{0.f, 0.f, 0.f, 0.f});
+              if (r16 < 2) {
+                float* dst = p.dupart + ((size_t(bh) * (kMaxN / 16) + kt) * kMaxN + q0 + (qb + h) * 16 + 4 * g) * kMaxN +
+                             ja + r16;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dst[r * kMaxN] = su[r];
+              }
+            }
+          }
+        }
         // G^T and H^T: A = dS^T / P^T of the two query tiles as the lane holds them (K slot 4 h + r is query
         // (qb + h) 16 + 4 g + r), B = q / go at those queries and d = 16 dt + r16 (transposed reads)
         mf_f16x8 dsb[2], pb[2];
@@ -568,8 +716,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           const int off = (qb * 16 + 4 * g + (r16 >> 2)) * KS + 16 * dt + 4 * (r16 & 3);
-          const mf_f16x8 bq = cat8(read_tr16(Qs + off), read_tr16(Qs + off + off2));
-          const mf_f16x8 bg = cat8(read_tr16(Gs + off), read_tr16(Gs + off + off2));
+          const mf_f16x8 bq = cat8(read_tr16(Qp + off), read_tr16(Qp + off + off2));
+          const mf_f16x8 bg = cat8(read_tr16(Gp + off), read_tr16(Gp + off + off2));
 #pragma unroll
           for (int jn = 0; jn < 2; ++jn) {
             gt[jn][dt] = mma(dsb[jn], bq, gt[jn][dt]);
@@ -578,7 +726,32 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         }
       }
 
+      // BIAS: dw of the pair tile (sum over the four query groups; each pair belongs to one wave of one unit)
+      if constexpr (BIAS) {
+        if (p.dw != nullptr) {
+          const float fds = con[kFDs] * (1.0f / kLog2e);  // dwa holds sums of gate log2 e dS 2^-es
+#pragma unroll
+          for (int jn = 0; jn < 2; ++jn) {
+            const float x = sum_groups(dwa[jn]) * fds;
+            if (g == 0 && ja + jn < nk && kvalid) {
+              float* o = p.dw + (rbase + kidx[ja + jn]) * N + kidx[k0 + r16];
+              *o = first ? x : *o + x;
+            }
+          }
+        }
+      }
       // ---- the pair tile's key-side gradients ----
+      if constexpr (BIAS) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) read_kv2(dt);
+#pragma unroll
+        for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            k1p[jn][dt] = float(k1h[jn][dt]);
+            v1p[jn][dt] = float(V1s[(ja + jn) * KS + 16 * dt + r16]);
+          }
+      }
 #pragma unroll
       for (int jn = 0; jn < 2; ++jn) {
         const int j = ja + jn;
@@ -598,8 +771,19 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
           x = sum_groups(x);
           y = sum_groups(y);
           if (g == 0) {  // rows of j belong to this wave
-            dk1a[j * DP + 16 * dt + r16] = d1k[jn][dt] + x;
-            dv1a[j * DP + 16 * dt + r16] = d1v[jn][dt] + y;
+            if constexpr (BIAS) {
+              if (kt + 1 < nkt || !last) {
+                sk1[j * DP + 16 * dt + r16] = d1k[jn][dt] + x;
+                sv1[j * DP + 16 * dt + r16] = d1v[jn][dt] + y;
+              } else {  // the last key tile: the gradient rows
+                const size_t o = (rbase + kidx[j]) * DP + 16 * dt + r16;
+                store_grad(p.dk1, o, (d1k[jn][dt] + x) * con[kFDk1], p.gout16);
+                store_grad(p.dv1, o, (d1v[jn][dt] + y) * con[kFDv1], p.gout16);
+              }
+            } else {
+              dk1a[j * DP + 16 * dt + r16] = d1k[jn][dt] + x;
+              dv1a[j * DP + 16 * dt + r16] = d1v[jn][dt] + y;
+            }
           }
         }
       }
@@ -626,43 +810,84 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         s += slot[2 * kSlot + u];
         s += slot[3 * kSlot + u];
         s *= which ? con[kFDv2] : con[kFDk2];
-        if (to_slab) slab[size_t(1 + which) * kMaxN * DP + (k0 + kk) * DP + d] = s;
+        float* ps = slab + size_t(1 + which) * kMaxN * DP + (k0 + kk) * DP + d;
+        if (!first) s += *ps;  // an earlier pass's partial (this thread wrote it)
+        if (to_slab || !last) *ps = s;
         else store_grad(which ? p.dv2 : p.dk2, (rbase + kidx[k0 + kk]) * DP + d, s, p.gout16);
+      }
+    }
+    // BIAS: dv_bias partial of the key tile (sum over the part's j), the four waves' partials in wave order
+    if constexpr (BIAS) {
+      if (p.dvb != nullptr) {
+        const float* dv0 = reinterpret_cast<const float*>(smem + Ly::dvb);
+        for (int u = tid; u < NQT * 256; u += kThreads) {
+          const int i = q0 + (u / 256) * 16 + u % 16, kk = (u / 16) % 16;
+          if (i < nq && k0 + kk < nk)
+            p.dvbpart[((size_t(bh) * 2 + part) * kMaxN + k0 + kk) * kMaxN + i] =
+                ((dv0[u] + dv0[NT * 256 + u]) + dv0[2 * NT * 256 + u]) + dv0[3 * NT * 256 + u];
+        }
       }
     }
     lds_barrier();
   }
 
-  // ---- dk1 / dv1 rows of the unit's keys j (key pairs jp = j / 2 with jp % parts == part) ----
-  for (int u = tid; u < nk * DP; u += kThreads) {
-    if (((u / DP) >> 1) % parts != part) continue;
-    const size_t o = (rbase + kidx[u / DP]) * DP + (u % DP);
-    store_grad(p.dk1, o, dk1a[u] * con[kFDk1], p.gout16);
-    store_grad(p.dv1, o, dv1a[u] * con[kFDv1], p.gout16);
+  if constexpr (BIAS) {
+    // dgate partials of the pass: sums over each lane's keys into the wave's own scratch (other waves may still
+    // be using theirs), then the four waves in order
+    float* gs = reinterpret_cast<float*>(scr);
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = row16_sum(accg[qt][r]);
+        if (r16 == 0) gs[qt * 16 + 4 * g + r] = x;
+      }
+  } else {
+    // ---- dk1 / dv1 rows of the unit's keys j (key pairs jp = j / 2 with jp % parts == part) ----
+    for (int u = tid; u < nk * DP; u += kThreads) {
+      if (((u / DP) >> 1) % parts != part) continue;
+      const size_t o = (rbase + kidx[u / DP]) * DP + (u % DP);
+      store_grad(p.dk1, o, dk1a[u] * con[kFDk1], p.gout16);
+      store_grad(p.dv1, o, dv1a[u] * con[kFDv1], p.gout16);
+    }
   }
   lds_barrier();  // rows and acc1 are free for the dq partials
+  if constexpr (BIAS) {
+    if (p.dgate != nullptr) {
+      const float* gs = reinterpret_cast<const float*>(smem + Ly::scr);
+      constexpr int kW = 2 * 32 * SS / 2;  // floats per wave's scratch
+      for (int i = tid; i < min(nq - q0, NQT * 16); i += kThreads)
+        p.dgpart[(size_t(bh) * 2 + part) * kMaxN + q0 + i] =
+            ((gs[i] + gs[kW + i]) + gs[2 * kW + i]) + gs[3 * kW + i];
+    }
+  }
   // ---- dq: the four waves' partials in wave order ----
-  float* dqs = reinterpret_cast<float*>(smem);
+  // (BIAS: in slot + dvb, since a later pass still needs the rows)
+  float* dqs = reinterpret_cast<float*>(smem + (BIAS ? Ly::slot : 0));
+  constexpr int kDqs = NQT * 16 * DP;  // one wave's partials
 #pragma unroll
   for (int qt = 0; qt < NQT; ++qt) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        dqs[(wave * kMaxN + qt * 16 + 4 * g + r) * DP + 16 * dt + r16] = dqa[qt][dt][r];
+        dqs[wave * kDqs + (qt * 16 + 4 * g + r) * DP + 16 * dt + r16] = dqa[qt][dt][r];
   }
   lds_barrier();
-  for (int u = tid; u < nq * DP; u += kThreads) {
-    float s = dqs[u] + dqs[kMaxN * DP + u];
-    s += dqs[2 * kMaxN * DP + u];
-    s += dqs[3 * kMaxN * DP + u];
+  for (int u = tid; u < min(nq - q0, NQT * 16) * DP; u += kThreads) {
+    float s = dqs[u] + dqs[kDqs + u];
+    s += dqs[2 * kDqs + u];
+    s += dqs[3 * kDqs + u];
     s *= con[kFDq];
-    if (to_slab) slab[u] = s;
-    else store_grad(p.dq, (rbase + qidx[u / DP]) * DP + (u % DP), s, p.gout16);
+    if (to_slab) slab[q0 * DP + u] = s;
+    else store_grad(p.dq, (rbase + qidx[q0 + u / DP]) * DP + (u % DP), s, p.gout16);
   }
+  if (!last) lds_barrier();  // slot, dvb and the scratch are the next pass's
 }
 
+template <bool BIAS>
 __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
+  using Lk = Lay<BIAS>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   if (int(blockIdx.x) >= *p.total) return;
   const uint32_t unit = p.units[blockIdx.x];
@@ -671,15 +896,14 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
   const int b = bh / p.H;
   const int N = p.N;
   const int tid = threadIdx.x;
-  _Float16* Qs = reinterpret_cast<_Float16*>(smem + Lay::rows);  // q, go, k1, k2, v1, v2 rows in this order
+  _Float16* Qs = reinterpret_cast<_Float16*>(smem + Lk::rows);  // q, go, k1, k2, v1, v2 rows in this order
   const int lane = lane_id();
   const int wave = wave_id();
-  float* dk1a = reinterpret_cast<float*>(smem + Lay::acc1);  // dk1 then dv1 sums
-  float* lse2 = reinterpret_cast<float*>(smem + Lay::lse2);
-  float* dlt = reinterpret_cast<float*>(smem + Lay::dlt);
-  uint32_t* pvb = reinterpret_cast<uint32_t*>(smem + Lay::pvb);
-  int* kidx = reinterpret_cast<int*>(smem + Lay::kidx);
-  int* qidx = reinterpret_cast<int*>(smem + Lay::qidx);
+  float* lse2 = reinterpret_cast<float*>(smem + Lk::lse2);
+  float* dlt = reinterpret_cast<float*>(smem + Lk::dlt);
+  uint32_t* pvb = reinterpret_cast<uint32_t*>(smem + Lk::pvb);
+  int* kidx = reinterpret_cast<int*>(smem + Lk::kidx);
+  int* qidx = reinterpret_cast<int*>(smem + Lk::qidx);
 
   // ---- valid keys and queries of molecule b, from the plan (which lists only molecules with 1 .. kMaxN) ----
   const int2 nkq = p.counts[b];
@@ -745,7 +969,7 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
 #pragma unroll
       for (int tt = 0; tt < 6; ++tt) mx[tt] = t == tt ? max(mx[tt], m) : mx[tt];
     }
-    uint32_t* red = reinterpret_cast<uint32_t*>(smem + Lay::red);
+    uint32_t* red = reinterpret_cast<uint32_t*>(smem + Lk::red);
 #pragma unroll
     for (int tt = 0; tt < 6; ++tt) {
       mx[tt] = wave_max_u32(mx[tt]);
@@ -770,7 +994,7 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
       *reinterpret_cast<uint4*>(Qs + size_t(t) * kMaxN * KS + rr * KS + 8 * c) = to_f16x8(buf[i], ldexpf(1.0f, -e));
     }
     if (tid == 0) {
-      float* con = reinterpret_cast<float*>(smem + Lay::con);
+      float* con = reinterpret_cast<float*>(smem + Lk::con);
       con[kCS] = ldexpf(kLog2e, ex[0] + ex[2] + ex[3]);
       con[kCP] = ldexpf(1.0f, ex[1] + ex[4] + ex[5] - es);
       con[kFDq] = ldexpf(1.0f, es + ex[2] + ex[3]);
@@ -778,6 +1002,8 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
       con[kFDk2] = ldexpf(1.0f, ex[2] + es + ex[0]);
       con[kFDv1] = ldexpf(1.0f, ex[5] + ex[1]);
       con[kFDv2] = ldexpf(1.0f, ex[4] + ex[1]);
+      con[kFDs] = ldexpf(1.0f, es);
+      if (BIAS && part == 0) p.fds[bh] = con[kFDs];
     }
     const float dscale = ldexpf(1.0f, -es);
 #pragma unroll
@@ -813,15 +1039,66 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
       pvb[u] = bits;
     }
   }
-  for (int u = tid; u < 2 * kMaxN * DP / 4; u += kThreads) reinterpret_cast<float4*>(dk1a)[u] = float4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (BIAS) {
+    // ---- u^T [j][i] = u[i][j] and v^T [k][i] = v[i][k] of the compacted atoms (bf16 as given, zero past the
+    // counts), the gates and gate log2 e (zero past nq).  Loads from clamped indices, then the selects. ----
+    uint16_t* ut = reinterpret_cast<uint16_t*>(smem + Lk::ut);
+    uint16_t* vt = reinterpret_cast<uint16_t*>(smem + Lk::vt);
+    float* cgs = reinterpret_cast<float*>(smem + Lk::gt);
+    constexpr int kPer = 5;
+    static_assert(kMaxN * kMaxN % (kThreads * kPer) == 0, "whole passes");
+    for (int u0 = 0; u0 < kMaxN * kMaxN; u0 += kThreads * kPer) {
+      uint16_t a[kPer], c[kPer];
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) {
+        const int u = u0 + tid + kThreads * t;
+        const int i = u / kMaxN, j = u % kMaxN;
+        const size_t o = (rbase + qidx[min(i, nq - 1)]) * N + kidx[min(j, nk - 1)];
+        a[t] = p.bu[o];
+        c[t] = p.bv[o];
+      }
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) {
+        const int u = u0 + tid + kThreads * t;
+        const int i = u / kMaxN, j = u % kMaxN;
+        const bool ok = i < nq && j < nk;
+        ut[j * KU + i] = ok ? a[t] : uint16_t(0);
+        vt[j * KU + i] = ok ? c[t] : uint16_t(0);
+      }
+    }
+    if (tid < kMaxN) {
+      const float gv = bf_u16(p.bg[rbase + qidx[min(tid, nq - 1)]]);
+      cgs[tid] = tid < nq ? gv : 0.0f;
+      cgs[kMaxN + tid] = tid < nq ? gv * kLog2e : 0.0f;
+    }
+  } else {
+    for (int u = tid; u < 2 * kMaxN * DP / 4; u += kThreads)
+      reinterpret_cast<float4*>(smem + Lk::acc1)[u] = float4{0.f, 0.f, 0.f, 0.f};
+  }
   lds_barrier();
 
-  switch ((nq + 15) / 16) {
-    case 1: unit_body<1>(p, smem, nq, nk, part, parts, bh, has_pv); break;
-    case 2: unit_body<2>(p, smem, nq, nk, part, parts, bh, has_pv); break;
-    case 3: unit_body<3>(p, smem, nq, nk, part, parts, bh, has_pv); break;
-    case 4: unit_body<4>(p, smem, nq, nk, part, parts, bh, has_pv); break;
-    default: unit_body<NT>(p, smem, nq, nk, part, parts, bh, has_pv); break;
+  if constexpr (BIAS) {  // at most three query tiles per pass (the bias sums leave no registers for more)
+    switch ((nq + 15) / 16) {
+      case 1: unit_body<1, true>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, true); break;
+      case 2: unit_body<2, true>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, true); break;
+      case 3: unit_body<3, true>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, true); break;
+      case 4:
+        unit_body<2, true>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, false);
+        unit_body<2, true>(p, smem, nq, nk, part, parts, bh, has_pv, 2, false, true);
+        break;
+      default:
+        unit_body<3, true>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, false);
+        unit_body<2, true>(p, smem, nq, nk, part, parts, bh, has_pv, 3, false, true);
+        break;
+    }
+  } else {
+    switch ((nq + 15) / 16) {
+      case 1: unit_body<1, false>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, true); break;
+      case 2: unit_body<2, false>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, true); break;
+      case 3: unit_body<3, false>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, true); break;
+      case 4: unit_body<4, false>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, true); break;
+      default: unit_body<NT, false>(p, smem, nq, nk, part, parts, bh, has_pv, 0, true, true); break;
+    }
   }
 }
 
@@ -835,8 +1112,8 @@ __global__ void __launch_bounds__(kThreads) pair_bwd_combine(Params p) {
   const int nk = nkq.x, nq = nkq.y;
   if (nk <= 0 || nq <= 0 || nk > kMaxN || nq > kMaxN || parts_of(nk) == 1) return;
   const size_t rbase = size_t(bh) * p.N;
-  const float* slab0 = p.slab + size_t(bh) * 2 * 3 * kMaxN * DP;
-  const float* slab = slab0 + 3 * kMaxN * DP;  // part 1
+  const float* slab0 = p.slab + size_t(bh) * 2 * 5 * kMaxN * DP;
+  const float* slab = slab0 + 5 * kMaxN * DP;  // part 1
   const uint16_t* lists = p.lists + size_t(b) * 2 * kMaxN;
   const bool g16 = p.gout16 != 0;
   // rows: dq of the nq queries, then dk2 and dv2 of the nk keys, 16 float4 each; 8 per thread at a time
@@ -874,6 +1151,51 @@ __global__ void __launch_bounds__(kThreads) pair_bwd_combine(Params p) {
   }
 }
 
+// The factorized bias gradients of every served molecule from the units' partial sums (dS 2^-es):
+//   du_ij = gate_i 2^es sum_kt dupart[kt][i][j],  dv_ik = gate_i 2^es (part 0 + part 1),
+//   dgate_i = 2^es (part 0 + part 1); dw was written by the units.  One workgroup per (molecule, head).
+__global__ void __launch_bounds__(kThreads) pair_bwd_bias_finish(Params p) {
+  __shared__ float s_gate[kMaxN];
+  __shared__ int s_q[kMaxN], s_k[kMaxN];
+  const int bh = blockIdx.x;
+  const int b = bh / p.H;
+  const int2 nkq = p.counts[b];
+  const int nk = nkq.x, nq = nkq.y;
+  if (nk <= 0 || nq <= 0 || nk > kMaxN || nq > kMaxN) return;
+  const int tid = threadIdx.x;
+  const size_t rbase = size_t(bh) * p.N;
+  const uint16_t* lists = p.lists + size_t(b) * 2 * kMaxN;
+  const float fds = p.fds[bh];
+  const bool two = parts_of(nk) == 2;
+  if (tid < kMaxN) {
+    s_k[tid] = lists[min(tid, nk - 1)];
+    s_q[tid] = lists[kMaxN + min(tid, nq - 1)];
+    s_gate[tid] = bf_u16(p.bg[rbase + lists[kMaxN + min(tid, nq - 1)]]);
+  }
+  __syncthreads();
+  const float* dvp = p.dvbpart + size_t(bh) * 2 * kMaxN * kMaxN;
+  for (int u = tid; u < nq * nk; u += kThreads) {
+    const int i = u / nk, j = u % nk;
+    const size_t o = (rbase + s_q[i]) * p.N + s_k[j];
+    const float c = s_gate[i] * fds;
+    if (p.du != nullptr) {
+      const float* dp = p.dupart + (size_t(bh) * (kMaxN / 16) * kMaxN + i) * kMaxN + j;
+      float s = dp[0];
+      for (int kt = 1; kt * 16 < nk; ++kt) s += dp[size_t(kt) * kMaxN * kMaxN];
+      p.du[o] = c * s;
+    }
+    if (p.dvb != nullptr) {
+      float s = dvp[j * kMaxN + i];
+      if (two) s += dvp[kMaxN * kMaxN + j * kMaxN + i];
+      p.dvb[o] = c * s;
+    }
+  }
+  if (p.dgate != nullptr) {
+    const float* gp = p.dgpart + size_t(bh) * 2 * kMaxN;
+    for (int i = tid; i < nq; i += kThreads) p.dgate[rbase + s_q[i]] = fds * (two ? gp[i] + gp[kMaxN + i] : gp[i]);
+  }
+}
+
 }  // namespace pbwd
 
 bool simplicial_pair_bwd_serves(const mf_simplicial_bwd_args* a) {
@@ -882,7 +1204,10 @@ bool simplicial_pair_bwd_serves(const mf_simplicial_bwd_args* a) {
       reinterpret_cast<uintptr_t>(a->workspace) % 256 != 0 ||
       a->workspace_bytes < pbwd::Ws(a->batch, a->heads).bytes)
     return false;
-  if (a->bias_u != nullptr || a->angle_left != nullptr || a->message_left != nullptr) return false;
+  if (a->angle_left != nullptr || a->message_left != nullptr) return false;
+  if (a->bias_u != nullptr) {  // bf16 bias terms (staged as they are)
+    if (a->bias_dtype != MF_DTYPE_BF16 || !a->bias_v || !a->bias_w || !a->bias_gate) return false;
+  }
   if (!a->dq || !a->dk1 || !a->dv1 || !a->dk2 || !a->dv2) return false;
   for (const void* ptr : {(const void*)a->q, (const void*)a->k1, (const void*)a->v1, (const void*)a->k2,
                           (const void*)a->v2, (const void*)a->grad_out, (const void*)a->out})
@@ -941,24 +1266,47 @@ int simplicial_pair_bwd_launch(const mf_simplicial_bwd_args* a, hipStream_t stre
   p.pv = a->pair_valid;
   p.dq = a->dq; p.dk1 = a->dk1; p.dv1 = a->dv1; p.dk2 = a->dk2; p.dv2 = a->dv2;
   p.gout16 = a->grads_dtype == MF_DTYPE_BF16 ? 1 : 0;
+  const bool bias = a->bias_u != nullptr;
+  if (bias) {
+    p.bu = static_cast<const uint16_t*>(a->bias_u);
+    p.bv = static_cast<const uint16_t*>(a->bias_v);
+    p.bw = static_cast<const uint16_t*>(a->bias_w);
+    p.bg = static_cast<const uint16_t*>(a->bias_gate);
+    p.du = a->du;
+    p.dvb = a->dv_bias;
+    p.dw = a->dw;
+    p.dgate = a->dgate;
+    p.dupart = reinterpret_cast<float*>(wsp + ws.dupart);
+    p.dvbpart = reinterpret_cast<float*>(wsp + ws.dvbpart);
+    p.dgpart = reinterpret_cast<float*>(wsp + ws.dgpart);
+    p.fds = reinterpret_cast<float*>(wsp + ws.fds);
+  }
   p.H = a->heads;
   p.N = a->tokens;
   DeviceInfo dev;
   int st = device_info(&dev);
   if (st != MF_OK) return st;
-  if (Lay::bytes > size_t(dev.max_lds_per_block))
-    return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: the pair kernel needs " + std::to_string(Lay::bytes) +
+  const size_t lds = bias ? Lay<true>::bytes : Lay<false>::bytes;
+  const void* kern = bias ? reinterpret_cast<const void*>(pair_bwd_kernel<true>)
+                          : reinterpret_cast<const void*>(pair_bwd_kernel<false>);
+  if (lds > size_t(dev.max_lds_per_block))
+    return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: the pair kernel needs " + std::to_string(lds) +
                                         " bytes of LDS per workgroup");
-  st = ensure_dynamic_lds(reinterpret_cast<const void*>(pair_bwd_kernel), int(Lay::bytes));
+  st = ensure_dynamic_lds(kern, int(lds));
   if (st != MF_OK) return st;
   const long long blocks = 2LL * a->batch * a->heads;  // the most units a plan can list
   if (blocks > 0x7fffffffLL) return fail(MF_ERR_UNSUPPORTED, "mf_simplicial_bwd: grid too large");
   hipLaunchKernelGGL(pair_bwd_plan, dim3(1), dim3(kPlanThreads), 0, stream, pp);
   MF_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(pair_bwd_kernel, dim3(unsigned(blocks)), dim3(kThreads), Lay::bytes, stream, p);
+  if (bias) hipLaunchKernelGGL(pair_bwd_kernel<true>, dim3(unsigned(blocks)), dim3(kThreads), lds, stream, p);
+  else hipLaunchKernelGGL(pair_bwd_kernel<false>, dim3(unsigned(blocks)), dim3(kThreads), lds, stream, p);
   MF_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(pair_bwd_combine, dim3(unsigned(a->batch * a->heads)), dim3(kThreads), 0, stream, p);
   MF_HIP_CHECK(hipGetLastError());
+  if (bias) {
+    hipLaunchKernelGGL(pair_bwd_bias_finish, dim3(unsigned(a->batch * a->heads)), dim3(kThreads), 0, stream, p);
+    MF_HIP_CHECK(hipGetLastError());
+  }
   return MF_OK;
 }
 

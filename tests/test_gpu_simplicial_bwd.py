@@ -253,9 +253,10 @@ def test_low_rank_terms_run_on_the_kernel(cuda):
     assert res[9] is not None and res[11] is not None
 
 
-def _abi_bwd(ops, go, out32, lse, qv, pkv, grads_dtype):
+def _abi_bwd(ops, go, out32, lse, qv, pkv, grads_dtype, bias=None):
     """mf_simplicial_bwd through the C ABI; gradient buffers filled with NaN (bf16) or zeros (fp32, the
-    caller's fill that the fp32 contract asks for)."""
+    caller's fill that the fp32 contract asks for); with a bf16 factorized bias also du, dv_bias, dw, dgate
+    (fp32, zero-filled)."""
     from matterformer_amd import _native
 
     B, H, N, D = ops[0].shape
@@ -268,6 +269,14 @@ def _abi_bwd(ops, go, out32, lse, qv, pkv, grads_dtype):
     else:
         grads = [torch.zeros(B, H, N, D, device=dev) for _ in range(5)]
     qb, pb = qv.to(torch.bool).contiguous(), pkv.to(torch.bool).contiguous()
+    extra = {}
+    if bias is not None:
+        bgrads = [torch.zeros(B, H, N, N, device=dev) for _ in range(3)] + [torch.zeros(B, H, N, device=dev)]
+        extra = dict(bias_u=bias[0].data_ptr(), bias_v=bias[1].data_ptr(), bias_w=bias[2].data_ptr(),
+                     bias_gate=bias[3].data_ptr(), bias_dtype=_native.dtype_code(bias[0].dtype),
+                     du=bgrads[0].data_ptr(), dv_bias=bgrads[1].data_ptr(), dw=bgrads[2].data_ptr(),
+                     dgate=bgrads[3].data_ptr())
+        grads = grads + bgrads
     args = _native.MfSimplicialBwdArgs(
         q=ops[0].data_ptr(), k1=ops[1].data_ptr(), v1=ops[2].data_ptr(), k2=ops[3].data_ptr(), v2=ops[4].data_ptr(),
         grad_out=go.data_ptr(), out=out32.data_ptr(), lse=lse.float().contiguous().data_ptr(),
@@ -275,19 +284,21 @@ def _abi_bwd(ops, go, out32, lse, qv, pkv, grads_dtype):
         grad_dtype=_native.dtype_code(torch.bfloat16), dq=grads[0].data_ptr(), dk1=grads[1].data_ptr(),
         dv1=grads[2].data_ptr(), dk2=grads[3].data_ptr(), dv2=grads[4].data_ptr(), batch=B, heads=H, tokens=N,
         head_dim=D, dtype=_native.dtype_code(torch.bfloat16), grads_dtype=_native.dtype_code(grads_dtype),
-        workspace=ws.data_ptr(), workspace_bytes=nbytes)
+        workspace=ws.data_ptr(), workspace_bytes=nbytes, **extra)
     with torch.cuda.device(dev):
         _native.check(lib.mf_simplicial_bwd(args, _native.current_stream(dev)), "mf_simplicial_bwd")
     torch.cuda.synchronize()
     return grads
 
 
+@pytest.mark.parametrize("with_bias", [False, True], ids=["nobias", "bias"])
 @pytest.mark.parametrize("counts", [[70, 41, 0, 12], [150, 64, 1, 33]], ids=["pair_only", "with_ownership"])
-def test_bf16_gradients_written_in_full(cuda, counts):
+def test_bf16_gradients_written_in_full(cuda, counts, with_bias):
     """grads_dtype bf16: every row of the five gradients is written (buffers start as NaN; padded rows and a
     molecule without valid queries come back 0), and the values are the fp32-gradient call's rounded to bf16
-    (both paths form the same fp32 sums).  The second case has a 150-atom molecule (ownership kernel) beside
-    pair-kernel molecules, one of them split in two halves."""
+    (both paths form the same fp32 sums); the fp32 bias gradients of the two calls are identical.  The second
+    case has a 150-atom molecule (ownership kernel) beside pair-kernel molecules, one of them split in two
+    halves; the 70-atom molecule runs its query tiles in two passes when there is a bias."""
     B, H, N, D = len(counts), 2, max(counts) + 3, 64
     case = random_simplicial(B, H, N, D, seed=71, counts=counts, std=logit_std(D))
     q, k1, v1, k2, v2, qv, pkv, pv = case
@@ -297,18 +308,51 @@ def test_bf16_gradients_written_in_full(cuda, counts):
     go = torch.randn(B, H, N, D, generator=gen).to(torch.bfloat16).to(cuda)
     ops = [t.to(torch.bfloat16).to(cuda).contiguous() for t in (q, k1, v1, k2, v2)]
     qv, pkv = qv.to(cuda), pkv.to(cuda)
+    bias, kw = None, {}
+    if with_bias:
+        bias = [(torch.randn(B, H, N, N, generator=gen) * 0.5).to(torch.bfloat16).to(cuda) for _ in range(3)] + \
+               [torch.randn(B, H, N, generator=gen).to(torch.bfloat16).to(cuda)]
+        kw = dict(u=bias[0], v_bias=bias[1], w=bias[2], gate=bias[3])
     out, lse, out32 = hip_simplicial_attention_forward(*ops, query_valid=qv, pair_key_valid=pkv, pair_valid=None,
-                                                       precision="bf16_tc")
-    g16 = _abi_bwd(ops, go, out32, lse, qv, pkv, torch.bfloat16)
-    g32 = _abi_bwd(ops, go, out32, lse, qv, pkv, torch.float32)
-    for name, a, r in zip(GRAD_NAMES, g16, g32):
+                                                       precision="bf16_tc", **kw)
+    g16 = _abi_bwd(ops, go, out32, lse, qv, pkv, torch.bfloat16, bias=bias)
+    g32 = _abi_bwd(ops, go, out32, lse, qv, pkv, torch.float32, bias=bias)
+    for name, a, r in zip(GRAD_NAMES, g16[:5], g32[:5]):
         assert not torch.isnan(a).any(), name
         assert torch.equal(a, r.to(torch.bfloat16)), name
+    for name, a, r in zip(GRAD_NAMES[5:], g16[5:], g32[5:]):
+        assert torch.equal(a, r), name
     # padded rows, and every row of molecule 2, are zero
     qvc, pkvc = qv.cpu(), pkv.cpu()
     for b in range(B):
         rows_q = ~qvc[b] if b != 2 else torch.ones(N, dtype=torch.bool)
         rows_k = ~pkvc[b] if b != 2 else torch.ones(N, dtype=torch.bool)
         assert not g16[0][b][:, rows_q.to(cuda)].any()
-        for g in g16[1:]:
+        for g in g16[1:5]:
             assert not g[b][:, rows_k.to(cuda)].any()
+
+
+def test_pair_path_bias_gradients_with_masking_scale_terms(cuda):
+    """bf16 operands, pair formulation with a factorized bias whose w carries -30000 on a fifth of the pairs
+    (positive gates: those pairs' P underflows to 0, as under an additive mask) beside ordinary terms; one
+    molecule of 70 atoms (split in two halves, query tiles in two passes) and one of 41.  Every gradient
+    against float64 autograd on the same rounded inputs, 2e-2."""
+    B, H, N, D = 2, 2, 70, 64
+    case = random_simplicial(B, H, N, D, seed=81, counts=[70, 41], std=logit_std(D))
+    q, k1, v1, k2, v2, qv, pkv, pv = case
+    gen = torch.Generator().manual_seed(82)
+    go = torch.randn(B, H, N, D, generator=gen).to(torch.bfloat16)
+    u, v, w = (torch.randn(B, H, N, N, generator=gen) * 0.5 for _ in range(3))
+    w[torch.rand(B, H, N, N, generator=gen) < 0.2] = -30000.0
+    gate = torch.rand(B, H, N, generator=gen) + 0.5
+    bias = [t.to(torch.bfloat16) for t in (u, v, w, gate)]
+    ops_cpu = [t.to(torch.bfloat16) for t in (q, k1, v1, k2, v2)]
+    _, got = hip_grads([t.to(cuda) for t in ops_cpu], qv.to(cuda), pkv.to(cuda), None, go.to(cuda), "bf16_tc",
+                       bias=[t.to(cuda) for t in bias])
+    _, ref = fp64_grads(ops_cpu, qv, pkv, None, go, bias=bias)
+    errs = {}
+    for name, g, r in zip(GRAD_NAMES, got, ref):
+        errs[name] = rel_err(g.float().cpu().numpy(), r)
+    print("relative errors:", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    for name, e in errs.items():
+        assert e <= 2e-2, (name, e)
