@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 10
+#define MF_ABI_VERSION 11
 
 typedef enum mf_status {
   MF_OK = 0,
@@ -174,7 +174,10 @@ int mf_simplicial_fwd(const mf_simplicial_fwd_args* args, void* stream);
 /* grad_dtype are all MF_DTYPE_BF16, no low-rank term is given, head_dim is */
 /* a multiple of 8, tokens <= 4096 and the buffers are 16-byte aligned: then */
 /* every row is written (zeros at padded queries and keys) and the caller   */
-/* needs no fill.  Bias gradients stay fp32, zero-filled by the caller.     */
+/* needs no fill.  The bias gradients follow (ABI 11): fp32, zero-filled   */
+/* by the caller and written at valid entries, with grads_dtype F32; bf16,  */
+/* every element written (zeros where an index is padded), with grads_dtype */
+/* BF16 (16-byte aligned buffers).                                          */
 /* With the low-rank terms of mf_simplicial_fwd (angle A_ijk = sum_r         */
 /* AL[i,j,r] AR[i,k,r] added to S as ag_i Ra^-1/2 A; message                 */
 /* c_ir = Rm^-1/2 sum_jk P ML[i,j,r] MR[i,k,r], out_i += sum_r c_ir          */
@@ -214,10 +217,10 @@ typedef struct mf_simplicial_bwd_args {
   void* dv1;
   void* dk2;
   void* dv2;
-  float* du;                /* [B*H, N, N] fp32 each (bias only); NULL = not wanted */
-  float* dv_bias;
-  float* dw;
-  float* dgate;             /* [B*H, N] fp32                                  */
+  void* du;                 /* [B*H, N, N] each, type `grads_dtype` (bias only); NULL = not wanted */
+  void* dv_bias;
+  void* dw;
+  void* dgate;              /* [B*H, N], type `grads_dtype`                   */
   int32_t batch;
   int32_t heads;
   int32_t tokens;

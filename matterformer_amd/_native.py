@@ -51,7 +51,7 @@ EXPORTED_SYMBOLS = (
     "mf_pair_mlp_bias",
 )
 
-EXPECTED_ABI_VERSION = 10
+EXPECTED_ABI_VERSION = 11
 
 _DTYPE_CODE = {
     torch.float32: MF_DTYPE_F32,

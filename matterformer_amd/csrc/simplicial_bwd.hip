@@ -153,10 +153,10 @@ struct Params {
   void* dk2;
   void* dv2;
   int gout16;
-  float* du;
-  float* dvb;
-  float* dw;
-  float* dgate;
+  void* du;      // bias gradients, fp32 or (gout16) bf16
+  void* dvb;
+  void* dw;
+  void* dgate;
   int B, H, N, D;
   int dtype, gdtype;
   int NP;       // N rounded up to 64: LDS list capacity
@@ -910,9 +910,9 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
         for (int c = lane; c < ncols; c += 64) {
           const size_t dst = orow * N + kidx[cb0 + c];
           if constexpr (ROLE == kRoleQ) {
-            if (p.dvb) p.dvb[dst] = gate_o * wcol[wave * kCols + c];
+            if (p.dvb) store_grad(p.dvb, dst, gate_o * wcol[wave * kCols + c], p.gout16);
           } else {
-            if (p.dw) p.dw[dst] = wcol[wave * kCols + c];
+            if (p.dw) store_grad(p.dw, dst, wcol[wave * kCols + c], p.gout16);
           }
         }
       }
@@ -963,9 +963,10 @@ __device__ __forceinline__ void run_role(const Params& p, unsigned char* smem, i
   if constexpr (ROLE == kRoleQ) {
     if (has_bias) {
       const float dg = wave_sum(gacc);
-      if (lane == 0 && p.dgate) p.dgate[orow] = dg;
+      if (lane == 0 && p.dgate) store_grad(p.dgate, orow, dg, p.gout16);
       if (p.du)
-        for (int row = lane; row < nk; row += 64) p.du[orow * N + kidx[row]] = gate_o * wrow[wave * NP + row];
+        for (int row = lane; row < nk; row += 64)
+          store_grad(p.du, orow * N + kidx[row], gate_o * wrow[wave * NP + row], p.gout16);
     }
   }
   }  // it
@@ -1084,6 +1085,23 @@ __global__ void __launch_bounds__(256) zero_rows_kernel(Params p) {
   }
 }
 
+// bf16 bias gradients are written in full: the four tensors are cleared first (one flat pass of 16-byte
+// stores, the last n % 8 elements one by one), then the kernels write every valid entry.
+__global__ void __launch_bounds__(256) zero_bias_kernel(void* du, void* dvb, void* dw, void* dgate, size_t plane,
+                                                        size_t gates) {
+  void* const ptrs[4] = {du, dvb, dw, dgate};
+  const size_t n[4] = {plane, plane, plane, gates};
+  const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (ptrs[t] == nullptr) continue;
+    const size_t chunks = n[t] / 8;
+    for (size_t c = gid; c < chunks; c += stride) static_cast<uint4*>(ptrs[t])[c] = uint4{0u, 0u, 0u, 0u};
+    if (gid < n[t] % 8) static_cast<__bf16*>(ptrs[t])[chunks * 8 + gid] = __bf16(0.0f);
+  }
+}
+
 template <int DP, bool M16, bool LR = false>
 int launch(Params prm, bool has_pv, bool has_bias, hipStream_t stream) {
   size_t lds = Lay<DP, M16, LR>::bytes(prm.NP, has_pv, has_bias, (LR && prm.ml && prm.coeff) ? prm.RmP : 0);
@@ -1184,7 +1202,7 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
     if (!a->dq || !a->dk1 || !a->dv1 || !a->dk2 || !a->dv2 || a->head_dim % 8 != 0 || a->tokens > kZeroMaxN)
       return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: bf16 gradients need all five of dq, dk1, dv1, dk2, "
                                            "dv2, a head_dim that is a multiple of 8 and at most 4096 tokens");
-    for (const void* ptr : {a->dq, a->dk1, a->dv1, a->dk2, a->dv2})
+    for (const void* ptr : {a->dq, a->dk1, a->dv1, a->dk2, a->dv2, a->du, a->dv_bias, a->dw, a->dgate})
       if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
         return fail(MF_ERR_INVALID_ARGUMENT, "mf_simplicial_bwd: bf16 gradient buffers must be 16-byte aligned");
   }
@@ -1259,6 +1277,13 @@ extern "C" int mf_simplicial_bwd(const mf_simplicial_bwd_args* a, void* stream) 
   if (gout16) {
     hipLaunchKernelGGL(zero_rows_kernel, dim3(unsigned(a->batch * a->heads)), dim3(256), 0, s, prm);
     MF_HIP_CHECK(hipGetLastError());
+    if (has_bias && (a->du || a->dv_bias || a->dw || a->dgate)) {
+      const size_t gates = size_t(a->batch) * a->heads * a->tokens, plane = gates * a->tokens;
+      const size_t grid = std::min<size_t>((plane / 8 + 255) / 256, 4096);
+      hipLaunchKernelGGL(zero_bias_kernel, dim3(unsigned(std::max<size_t>(grid, 1))), dim3(256), 0, s, a->du,
+                         a->dv_bias, a->dw, a->dgate, plane, gates);
+      MF_HIP_CHECK(hipGetLastError());
+    }
   }
   if (a->dtype == MF_DTYPE_BF16 && a->grad_dtype == MF_DTYPE_BF16) {
     // molecules of at most 80 valid atoms take the pair formulation; the ownership kernel below takes the rest

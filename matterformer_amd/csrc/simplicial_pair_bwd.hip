@@ -105,17 +105,18 @@ struct Params {
   float* slab;            // [B*H][2 parts][5][kMaxN][DP] partial dq, dk2, dv2 of split molecules and (bias)
                           // the dk1, dv1 sums of the unit's keys (compacted rows)
   // factorized bias (BIAS kernels): S += gate_i (u_ij + v_ik + w_jk), u / v / w [B*H, N, N], gate [B*H, N]
-  // bf16; gradients fp32 (NULL = not wanted)
+  // bf16; gradients fp32 or (gout16) bf16, NULL = not wanted
   const uint16_t* bu;
   const uint16_t* bv;
   const uint16_t* bw;
   const uint16_t* bg;
-  float* du;
-  float* dvb;
-  float* dw;
-  float* dgate;
+  void* du;
+  void* dvb;
+  void* dw;
+  void* dgate;
+  float* dwpart;          // [B*H][kMaxN j][kMaxN k] dw of the earlier query passes (compacted)
   float* dupart;          // [B*H][kMaxN / 16 key tiles][kMaxN i][kMaxN j] per-key-tile sums over k of dS 2^-es
-  float* dvbpart;         // [B*H][2 parts][kMaxN k][kMaxN i] sums over the part's j of dS 2^-es
+  float* dvbpart;         // [B*H][2 parts][kMaxN i][kMaxN k] sums over the part's j of dS 2^-es
   float* dgpart;          // [B*H][2 parts][kMaxN i] sums over the part's (j, k) of dS 2^-es (u + v + w)
   float* fds;             // [B*H] 2^es of the unit (dS is carried as dS 2^-es)
   int H, N;
@@ -133,7 +134,7 @@ __device__ __forceinline__ uint32_t unit_cost(int nk, int nq) {
 
 // Workspace of the pair path (16-byte aligned regions).
 struct Ws {
-  size_t units, served, counts, lists, slab, dupart, dvbpart, dgpart, fds, bytes;
+  size_t units, served, counts, lists, slab, dupart, dvbpart, dgpart, fds, dwpart, bytes;
   Ws(int B, int H) {
     const size_t bh = size_t(B) * H;
     units = 16;  // [0, 4): units in the list, [4, 8): molecules the pair kernel does not serve
@@ -145,7 +146,8 @@ struct Ws {
     dvbpart = dupart + bh * (kMaxN / 16) * kMaxN * kMaxN * 4;
     dgpart = dvbpart + bh * 2 * kMaxN * kMaxN * 4;
     fds = dgpart + bh * 2 * kMaxN * 4;
-    bytes = fds + bh * 4;
+    dwpart = (fds + bh * 4 + 15) & ~size_t(15);
+    bytes = dwpart + bh * kMaxN * kMaxN * 4;
   }
 };
 constexpr int kPlanThreads = 1024;
@@ -732,10 +734,13 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
           const float fds = con[kFDs] * (1.0f / kLog2e);  // dwa holds sums of gate log2 e dS 2^-es
 #pragma unroll
           for (int jn = 0; jn < 2; ++jn) {
-            const float x = sum_groups(dwa[jn]) * fds;
+            float x = sum_groups(dwa[jn]) * fds;
             if (g == 0 && ja + jn < nk && kvalid) {
-              float* o = p.dw + (rbase + kidx[ja + jn]) * N + kidx[k0 + r16];
-              *o = first ? x : *o + x;
+              // earlier passes keep their sum in the workspace (read back by the thread that wrote it)
+              float* o = p.dwpart + (size_t(bh) * kMaxN + ja + jn) * kMaxN + k0 + r16;
+              if (!first) x += *o;
+              if (!last) *o = x;
+              else store_grad(p.dw, (rbase + kidx[ja + jn]) * N + kidx[k0 + r16], x, p.gout16);
             }
           }
         }
@@ -820,11 +825,12 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     if constexpr (BIAS) {
       if (p.dvb != nullptr) {
         const float* dv0 = reinterpret_cast<const float*>(smem + Ly::dvb);
-        for (int u = tid; u < NQT * 256; u += kThreads) {
-          const int i = q0 + (u / 256) * 16 + u % 16, kk = (u / 16) % 16;
+        for (int u = tid; u < NQT * 256; u += kThreads) {  // key fastest: 64-byte runs of the global rows
+          const int kk = u % 16, i16 = (u / 16) % 16, qt = u / 256;
+          const int i = q0 + qt * 16 + i16, l = (qt * 16 + kk) * 16 + i16;
           if (i < nq && k0 + kk < nk)
-            p.dvbpart[((size_t(bh) * 2 + part) * kMaxN + k0 + kk) * kMaxN + i] =
-                ((dv0[u] + dv0[NT * 256 + u]) + dv0[2 * NT * 256 + u]) + dv0[3 * NT * 256 + u];
+            p.dvbpart[((size_t(bh) * 2 + part) * kMaxN + i) * kMaxN + k0 + kk] =
+                ((dv0[l] + dv0[NT * 256 + l]) + dv0[2 * NT * 256 + l]) + dv0[3 * NT * 256 + l];
         }
       }
     }
@@ -1045,7 +1051,7 @@ __global__ void __launch_bounds__(kThreads, 1) pair_bwd_kernel(Params p) {
     uint16_t* ut = reinterpret_cast<uint16_t*>(smem + Lk::ut);
     uint16_t* vt = reinterpret_cast<uint16_t*>(smem + Lk::vt);
     float* cgs = reinterpret_cast<float*>(smem + Lk::gt);
-    constexpr int kPer = 5;
+    constexpr int kPer = 25;  // every load issued before the first LDS store
     static_assert(kMaxN * kMaxN % (kThreads * kPer) == 0, "whole passes");
     for (int u0 = 0; u0 < kMaxN * kMaxN; u0 += kThreads * kPer) {
       uint16_t a[kPer], c[kPer];
@@ -1153,7 +1159,9 @@ __global__ void __launch_bounds__(kThreads) pair_bwd_combine(Params p) {
 
 // The factorized bias gradients of every served molecule from the units' partial sums (dS 2^-es):
 //   du_ij = gate_i 2^es sum_kt dupart[kt][i][j],  dv_ik = gate_i 2^es (part 0 + part 1),
-//   dgate_i = 2^es (part 0 + part 1); dw was written by the units.  One workgroup per (molecule, head).
+//   dgate_i = 2^es (part 0 + part 1); dw was written by the units.  kFinishSplit workgroups per (molecule,
+// head), each thread kFinishBatch entries at a time with every load issued before the first store.
+constexpr int kFinishSplit = 4, kFinishBatch = 4;
 __global__ void __launch_bounds__(kThreads) pair_bwd_bias_finish(Params p) {
   __shared__ float s_gate[kMaxN];
   __shared__ int s_q[kMaxN], s_k[kMaxN];
@@ -1174,25 +1182,39 @@ __global__ void __launch_bounds__(kThreads) pair_bwd_bias_finish(Params p) {
   }
   __syncthreads();
   const float* dvp = p.dvbpart + size_t(bh) * 2 * kMaxN * kMaxN;
-  for (int u = tid; u < nq * nk; u += kThreads) {
-    const int i = u / nk, j = u % nk;
-    const size_t o = (rbase + s_q[i]) * p.N + s_k[j];
-    const float c = s_gate[i] * fds;
-    if (p.du != nullptr) {
-      const float* dp = p.dupart + (size_t(bh) * (kMaxN / 16) * kMaxN + i) * kMaxN + j;
-      float s = dp[0];
-      for (int kt = 1; kt * 16 < nk; ++kt) s += dp[size_t(kt) * kMaxN * kMaxN];
-      p.du[o] = c * s;
+  const float* dup = p.dupart + size_t(bh) * (kMaxN / 16) * kMaxN * kMaxN;
+  const int n = nq * nk, nkt = (nk + 15) / 16;
+  const int step = kThreads * kFinishSplit;
+  for (int u0 = blockIdx.y * kThreads + tid; u0 < n; u0 += kFinishBatch * step) {
+    float su[kFinishBatch], sv[kFinishBatch];
+#pragma unroll
+    for (int t = 0; t < kFinishBatch; ++t) {
+      const int u = min(u0 + t * step, n - 1);  // clamped: loads without branches
+      const int e = (u / nk) * kMaxN + u % nk;
+      su[t] = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < kMaxN / 16; ++kt) {
+        const float x = dup[size_t(kt) * kMaxN * kMaxN + e];
+        su[t] += kt < nkt ? x : 0.0f;  // tiles past nkt hold stale workspace bytes
+      }
+      const float v1 = dvp[kMaxN * kMaxN + e];
+      sv[t] = dvp[e] + (two ? v1 : 0.0f);
     }
-    if (p.dvb != nullptr) {
-      float s = dvp[j * kMaxN + i];
-      if (two) s += dvp[kMaxN * kMaxN + j * kMaxN + i];
-      p.dvb[o] = c * s;
+#pragma unroll
+    for (int t = 0; t < kFinishBatch; ++t) {
+      const int u = u0 + t * step;
+      if (u >= n) break;
+      const int i = u / nk, j = u % nk;
+      const size_t o = (rbase + s_q[i]) * p.N + s_k[j];
+      const float c = s_gate[i] * fds;
+      if (p.du != nullptr) store_grad(p.du, o, c * su[t], p.gout16);
+      if (p.dvb != nullptr) store_grad(p.dvb, o, c * sv[t], p.gout16);
     }
   }
-  if (p.dgate != nullptr) {
+  if (p.dgate != nullptr && blockIdx.y == 0) {
     const float* gp = p.dgpart + size_t(bh) * 2 * kMaxN;
-    for (int i = tid; i < nq; i += kThreads) p.dgate[rbase + s_q[i]] = fds * (two ? gp[i] + gp[kMaxN + i] : gp[i]);
+    for (int i = tid; i < nq; i += kThreads)
+      store_grad(p.dgate, rbase + s_q[i], fds * (two ? gp[i] + gp[kMaxN + i] : gp[i]), p.gout16);
   }
 }
 
@@ -1280,6 +1302,7 @@ int simplicial_pair_bwd_launch(const mf_simplicial_bwd_args* a, hipStream_t stre
     p.dvbpart = reinterpret_cast<float*>(wsp + ws.dvbpart);
     p.dgpart = reinterpret_cast<float*>(wsp + ws.dgpart);
     p.fds = reinterpret_cast<float*>(wsp + ws.fds);
+    p.dwpart = reinterpret_cast<float*>(wsp + ws.dwpart);
   }
   p.H = a->heads;
   p.N = a->tokens;
@@ -1304,7 +1327,8 @@ int simplicial_pair_bwd_launch(const mf_simplicial_bwd_args* a, hipStream_t stre
   hipLaunchKernelGGL(pair_bwd_combine, dim3(unsigned(a->batch * a->heads)), dim3(kThreads), 0, stream, p);
   MF_HIP_CHECK(hipGetLastError());
   if (bias) {
-    hipLaunchKernelGGL(pair_bwd_bias_finish, dim3(unsigned(a->batch * a->heads)), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL(pair_bwd_bias_finish, dim3(unsigned(a->batch * a->heads), kFinishSplit), dim3(kThreads), 0,
+                       stream, p);
     MF_HIP_CHECK(hipGetLastError());
   }
   return MF_OK;

@@ -395,10 +395,12 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
         raise ValueError("query_valid / pair_key_valid must be (B, N) and pair_valid (B, N, N)")
     ext = _prepare_extras(q, B, H, N, D, u, v_bias, w, gate, angle_left, angle_right, angle_gate,
                           message_left, message_right, message_basis)
-    # bf16 operands, grad_out and leaves, no low-rank term: the library writes every row of bf16 gradients
-    # (no fill, no cast); otherwise fp32 gradients, zero-filled here and cast to the leaves' dtypes
+    # bf16 operands, grad_out and leaves (bias terms included), no low-rank term: the library writes every
+    # element of bf16 gradients (no fill, no cast); otherwise fp32 gradients, zero-filled here and cast to the
+    # leaves' dtypes
     g16 = (dt == torch.bfloat16 and gdt == torch.bfloat16 and ext.angle is None and ext.message is None
-           and D % 8 == 0 and N <= 4096 and all(t.dtype == torch.bfloat16 for t in (q, k1, v1, k2, v2)))
+           and D % 8 == 0 and N <= 4096 and all(t.dtype == torch.bfloat16 for t in (q, k1, v1, k2, v2))
+           and (ext.bias is None or all(t.dtype == torch.bfloat16 for t in (u, v_bias, w, gate))))
     if g16:
         grads = [torch.empty(B, H, N, D, device=dev, dtype=torch.bfloat16) for _ in range(5)]
     else:
@@ -408,7 +410,8 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
         for idx, (name, shape) in enumerate((("need_du", (B, H, N, N)), ("need_dv_bias", (B, H, N, N)),
                                              ("need_dw", (B, H, N, N)), ("need_dgate", (B, H, N)))):
             if flags[name]:
-                bias_grads[idx] = torch.zeros(shape, device=dev, dtype=torch.float32)
+                bias_grads[idx] = (torch.empty(shape, device=dev, dtype=torch.bfloat16) if g16 else
+                                   torch.zeros(shape, device=dev, dtype=torch.float32))
     # low-rank gradients: (dangle_left, dangle_right, dangle_gate), (dmessage_left, dmessage_right, dmessage_basis)
     lr_grads: list[torch.Tensor | None] = [None] * 6
     if ext.angle is not None:
@@ -460,7 +463,7 @@ def _kernel_backward(grad_out, q, k1, v1, k2, v2, out, lse, query_valid, pair_ke
     if ext.bias is not None:
         for idx, src in enumerate((u, v_bias, w, gate)):
             if bias_grads[idx] is not None:
-                optional[idx] = bias_grads[idx].to(src.dtype)
+                optional[idx] = bias_grads[idx] if g16 else bias_grads[idx].to(src.dtype)
     for idx, src in enumerate((angle_left, angle_right, angle_gate, message_left, message_right, message_basis)):
         if lr_grads[idx] is not None:
             optional[4 + idx] = lr_grads[idx].to(src.dtype)

@@ -256,7 +256,7 @@ def test_low_rank_terms_run_on_the_kernel(cuda):
 def _abi_bwd(ops, go, out32, lse, qv, pkv, grads_dtype, bias=None):
     """mf_simplicial_bwd through the C ABI; gradient buffers filled with NaN (bf16) or zeros (fp32, the
     caller's fill that the fp32 contract asks for); with a bf16 factorized bias also du, dv_bias, dw, dgate
-    (fp32, zero-filled)."""
+    (the same dtype and fill)."""
     from matterformer_amd import _native
 
     B, H, N, D = ops[0].shape
@@ -271,7 +271,11 @@ def _abi_bwd(ops, go, out32, lse, qv, pkv, grads_dtype, bias=None):
     qb, pb = qv.to(torch.bool).contiguous(), pkv.to(torch.bool).contiguous()
     extra = {}
     if bias is not None:
-        bgrads = [torch.zeros(B, H, N, N, device=dev) for _ in range(3)] + [torch.zeros(B, H, N, device=dev)]
+        if grads_dtype == torch.bfloat16:
+            bgrads = [torch.full(s, float("nan"), device=dev, dtype=torch.bfloat16)
+                      for s in ((B, H, N, N),) * 3 + ((B, H, N),)]
+        else:
+            bgrads = [torch.zeros(B, H, N, N, device=dev) for _ in range(3)] + [torch.zeros(B, H, N, device=dev)]
         extra = dict(bias_u=bias[0].data_ptr(), bias_v=bias[1].data_ptr(), bias_w=bias[2].data_ptr(),
                      bias_gate=bias[3].data_ptr(), bias_dtype=_native.dtype_code(bias[0].dtype),
                      du=bgrads[0].data_ptr(), dv_bias=bgrads[1].data_ptr(), dw=bgrads[2].data_ptr(),
@@ -294,11 +298,11 @@ def _abi_bwd(ops, go, out32, lse, qv, pkv, grads_dtype, bias=None):
 @pytest.mark.parametrize("with_bias", [False, True], ids=["nobias", "bias"])
 @pytest.mark.parametrize("counts", [[70, 41, 0, 12], [150, 64, 1, 33]], ids=["pair_only", "with_ownership"])
 def test_bf16_gradients_written_in_full(cuda, counts, with_bias):
-    """grads_dtype bf16: every row of the five gradients is written (buffers start as NaN; padded rows and a
-    molecule without valid queries come back 0), and the values are the fp32-gradient call's rounded to bf16
-    (both paths form the same fp32 sums); the fp32 bias gradients of the two calls are identical.  The second
-    case has a 150-atom molecule (ownership kernel) beside pair-kernel molecules, one of them split in two
-    halves; the 70-atom molecule runs its query tiles in two passes when there is a bias."""
+    """grads_dtype bf16: every element of the gradients (the bias gradients too) is written (buffers start as
+    NaN; padded rows and entries, and a molecule without valid queries, come back 0), and the values are the
+    fp32-gradient call's rounded to bf16 (both paths form the same fp32 sums).  The second case has a 150-atom
+    molecule (ownership kernel) beside pair-kernel molecules, one of them split in two halves; the 70-atom
+    molecule runs its query tiles in two passes when there is a bias."""
     B, H, N, D = len(counts), 2, max(counts) + 3, 64
     case = random_simplicial(B, H, N, D, seed=71, counts=counts, std=logit_std(D))
     q, k1, v1, k2, v2, qv, pkv, pv = case
@@ -317,11 +321,9 @@ def test_bf16_gradients_written_in_full(cuda, counts, with_bias):
                                                        precision="bf16_tc", **kw)
     g16 = _abi_bwd(ops, go, out32, lse, qv, pkv, torch.bfloat16, bias=bias)
     g32 = _abi_bwd(ops, go, out32, lse, qv, pkv, torch.float32, bias=bias)
-    for name, a, r in zip(GRAD_NAMES, g16[:5], g32[:5]):
+    for name, a, r in zip(GRAD_NAMES, g16, g32):
         assert not torch.isnan(a).any(), name
         assert torch.equal(a, r.to(torch.bfloat16)), name
-    for name, a, r in zip(GRAD_NAMES[5:], g16[5:], g32[5:]):
-        assert torch.equal(a, r), name
     # padded rows, and every row of molecule 2, are zero
     qvc, pkvc = qv.cpu(), pkv.cpu()
     for b in range(B):
@@ -330,6 +332,12 @@ def test_bf16_gradients_written_in_full(cuda, counts, with_bias):
         assert not g16[0][b][:, rows_q.to(cuda)].any()
         for g in g16[1:5]:
             assert not g[b][:, rows_k.to(cuda)].any()
+        if with_bias:  # du, dv_bias at padded (query, key), dw at padded (key, key), dgate at padded queries
+            rq, rk = rows_q.to(cuda), rows_k.to(cuda)
+            for g in g16[5:7]:
+                assert not g[b][:, rq, :].any() and not g[b][:, :, rk].any()
+            assert not g16[7][b][:, rk, :].any() and not g16[7][b][:, :, rk].any()
+            assert not g16[8][b][:, rq].any()
 
 
 def test_pair_path_bias_gradients_with_masking_scale_terms(cuda):
