@@ -740,6 +740,24 @@ def measure_simplicial_extras(lib, w, wd) -> dict:
     res["bias_fwd"] = {"ms": round(bias_ms, 5), "tflops": round(fwd_flops / (bias_ms * 1e-3) / 1e12, 3),
                        "kernel": "mf::spair::simplicial_pair_kernel<bf16, 64, pair_valid=0, bias=1> "
                                  "(factorized bias, bf16)"}
+    # its backward: the bias training state, then mf_simplicial_bwd with the nine gradients
+    bias_state = _simplicial_call(lib, ops, wd.query_valid, wd.pair_key_valid, _native.MF_DTYPE_BF16, "bf16_tc",
+                                  out=out, out_f32=out32, lse=lse, bias=bias)
+    bias_state()
+    torch.cuda.synchronize()
+
+    def bias_bwd_step():
+        hip_simplicial_attention_backward(go, *ops, out32, lse, query_valid=wd.query_valid,
+                                          pair_key_valid=wd.pair_key_valid, pair_valid=None, precision="bf16_tc",
+                                          u=bias[0], v_bias=bias[1], w=bias[2], gate=bias[3])
+
+    bias_bwd_step()
+    bias_bwd_eager_ms, _ = timed_loop(torch.cuda.current_stream(), bias_bwd_step, 10, 2)
+    bias_bwd_ms = _graph_ms(bias_bwd_step, per_graph=10, replays=5)
+    res["bias_bwd"] = {"ms": round(bias_bwd_ms, 5), "eager_ms": round(bias_bwd_eager_ms, 5),
+                       "kernel": "mf::pbwd::pair_bwd_kernel<bias=1> (query tiles in passes of at most three) with "
+                                 "its plan, combine, bias finish and clearing launches; dq, dk1, dv1, dk2, dv2, du, "
+                                 "dv_bias, dw, dgate in bf16, written in full"}
 
     # C1: QM9 fp32
     c1 = simplicial_workload("qm9").to(dev)
