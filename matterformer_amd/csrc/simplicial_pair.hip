@@ -65,18 +65,18 @@
 namespace mf {
 namespace spair {
 
-// Waves per workgroup W: 4 with two workgroups per CU, 8 with one (the bias
-// instantiations, whose extra LDS allows one workgroup per CU: 8 waves keep
-// two waves on every SIMD, which the pair loop needs to overlap MFMA and VALU).
+// Waves per workgroup (4, two workgroups per CU: two waves on every SIMD, which the pair loop needs to
+// overlap MFMA and VALU), queries per unit and keys per staged block.  The bias instantiations stage 64-key
+// blocks, so that their bias operands fit beside a second workgroup's LDS.
 template <bool BIAS>
 struct Waves {
-  static constexpr int kCount = BIAS ? 8 : 4;
+  static constexpr int kCount = 4;
   // queries per unit: 3 tiles; 2 with the bias, whose operands leave no room for a third at 256
   // registers per wave
   static constexpr int kGroup = BIAS ? 32 : 48;
+  static constexpr int kCap = BIAS ? 64 : 128;  // keys per staged block (one row per 2 or 4 threads)
 };
 constexpr int kRedWaves = 4;          // partial-output slots of the final reduction
-constexpr int kCap = 128;             // keys per staged block (one row per 2 threads)
 constexpr int kMaxQ = 48;             // queries per unit
 constexpr int kMaxBatch = 256;        // molecules per launch
 constexpr int kMaxN = 512;            // tokens
@@ -137,10 +137,12 @@ __device__ __forceinline__ int claimed_position(unsigned int* counter, unsigned 
   return int(gridDim.x) + int(ticket);
 }
 
-// LDS layout (bytes) for padded head dim DP and W waves.
-template <int DP, int W>
+// LDS layout (bytes) for padded head dim DP.
+template <int DP, bool BIAS>
 struct Lay {
-  static constexpr int kWaves = W;
+  static constexpr int kWaves = Waves<BIAS>::kCount;
+  static constexpr int kCap = Waves<BIAS>::kCap;
+  static constexpr int RQ = Waves<BIAS>::kGroup;  // query rows of a reduction slot
   static constexpr int RB = DP * 2;  // bytes per staged fp16 row
   static constexpr int kK1 = 0;
   static constexpr int kK2 = kK1 + kCap * RB;
@@ -163,13 +165,13 @@ struct Lay {
   static constexpr int kM = kScal + 8 * 4;      // float [kMaxQ] two-pass maxima (log2 units)
   static constexpr int kClaim = kM + kMaxQ * 4;  // ClaimState
   static constexpr int kTotal = kClaim + int(sizeof(ClaimState));
-  // after the pair loop: partial outputs float [kRedWaves][kMaxQ][RS] and
-  // denominators float [kRedWaves][kMaxQ], over K1s .. V2s (with 8 waves,
-  // waves 4..7 add theirs into waves 0..3 through the same area first)
+  // after the pair loop: partial outputs float [kRedWaves][RQ][RS] and
+  // denominators float [kRedWaves][RQ], over K1s .. V2s, Qs and the pair bits
+  // (none of them is read after the pair loop)
   static constexpr int RS = DP + 4;
   static constexpr int kRed = 0;
-  static constexpr int kRedL = kRed + kRedWaves * kMaxQ * RS * 4;
-  static_assert(kRedL + kRedWaves * kMaxQ * 4 <= kQ, "reduction area must fit in the K/V staging area");
+  static constexpr int kRedL = kRed + kRedWaves * RQ * RS * 4;
+  static_assert(kRedL + kRedWaves * RQ * 4 <= kInfo, "reduction area must fit in the staging area");
   // BIAS instantiations, after the above: fp16 bias operands of the unit's (j block, k block)
   //   BU [kCap][kMaxQ]     c_i u_ij (row j, query i)
   //   BW [kCap][kCap]      w_jk
@@ -359,12 +361,12 @@ __device__ __forceinline__ int info_nq(uint32_t w) { return int((w >> 11) & 0x7f
 // group of up to GQ (48, or 32 with the bias), else groups of 32; molecules
 // with more than kCap keys (taken in key blocks) use groups of 16, one query
 // tile.
-template <int GQ>
+template <int GQ, int kCap>
 __device__ __forceinline__ int group_size(int nk, int nq) {
   if (nk > kCap) return 16;
   return nq <= GQ ? GQ : 32;
 }
-template <int GQ>
+template <int GQ, int kCap>
 __device__ __forceinline__ int num_groups(int nk, int nq) {
   if (nq <= 0) return 0;
   if (nk > kCap) return (nq + 15) >> 4;
@@ -418,7 +420,8 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
                                           mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
                                           int g, int r16) {
   constexpr int W = Waves<BIAS>::kCount;
-  using Ly = Lay<DP, W>;
+  using Ly = Lay<DP, BIAS>;
+  constexpr int kCap = Ly::kCap;
   constexpr int RB = Ly::RB;
   constexpr int NCH = Shape<DP>::NCH;
   constexpr int ND = Shape<DP>::ND;
@@ -713,7 +716,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   const int nqt = (nqg + 15) >> 4;     // query tiles in use
   constexpr int kWaves = Waves<BIAS>::kCount;
   constexpr int kThreads = kWaves * 64;
-  using Ly = Lay<DP, kWaves>;
+  using Ly = Lay<DP, BIAS>;
+  constexpr int kCap = Ly::kCap;
   constexpr int RB = Ly::RB;
   constexpr int NCH = Shape<DP>::NCH;
   constexpr int ND = Shape<DP>::ND;
@@ -865,10 +869,11 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     //   set 0 (U): rows = queries qi < kMaxQ, columns j < rj:  BU[j][qi]     = c_qi u[qa][ka(j0 + j)]
     //   set 1 (V): rows = queries qi,          columns k < rk:  BV[qi][k + 2] = c_qi v[qa][ka(k0 + k)]
     //   set 2 (W): rows j < rj,                columns k < rk:  BW[j][k]      = w[ka(j0 + j)][ka(k0 + k)]
-    // The first kRB rows of every set (all of U and V, and W up to 48 rows) and the gates of the
-    // wave's query rows are loaded before anything is stored, so the common case pays one round
-    // trip to memory; c_i = log2(e) 2^cE gate_i is formed in registers (and stored to BG).
-    constexpr int kRB = GQ / kWaves;
+    // Batches of kRB rows per wave: the U and V rows of a batch, its gates and, in the first batch, the
+    // first W rows are loaded before anything is stored (GQ / (kWaves kRB) round trips for U and V);
+    // c_i = log2(e) 2^cE gate_i is formed in registers (and stored to BG).
+    constexpr int kRB = 4;
+    static_assert(GQ % (kWaves * kRB) == 0, "whole batches of query rows");
     auto set_shape = [&](auto set_tag, int& R, int& C, int& rvalid, int& cvalid, int& cbase, const void*& src) {
       constexpr int SET = decltype(set_tag)::value;
       R = SET == 2 ? rj : GQ;
@@ -890,7 +895,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 #pragma unroll
       for (int t = 0; t < kRB; ++t) val[t][0] = val[t][1] = 0u;
       if (rvalid <= 0 || cvalid <= 0) return;
-      const bool two = C > 64;  // a second column per lane (wave-uniform)
+      const bool two = kCap > 64 && C > 64;  // a second column per lane (wave-uniform; never with 64-key blocks)
       int ca[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) ca[s] = key_atom(cbase + min(lane + 64 * s, cvalid - 1));
@@ -926,7 +931,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         const int r = r0 + kWaves * t;
         if (r >= R) break;  // wave-uniform
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < (kCap > 64 ? 2 : 1); ++s) {
           const int c = lane + 64 * s;
           if (c >= C) continue;
           const uint32_t raw = val[t][s];
@@ -945,18 +950,20 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
     const float kNoRow[kRB] = {};
-    {
+#pragma unroll 1
+    for (int qb = 0; qb < GQ / (kWaves * kRB); ++qb) {
+      const int r0 = wave + kWaves * kRB * qb;
       uint32_t vu[kRB][2], vv[kRB][2], vw[kRB][2];
       float crow[kRB];
-      load_rows(S0{}, wave, vu);
-      load_rows(S1{}, wave, vv);
-      load_rows(S2{}, wave, vw);
+      load_rows(S0{}, r0, vu);
+      load_rows(S1{}, r0, vv);
+      if (qb == 0) load_rows(S2{}, r0, vw);
       // the gates of query rows wave + kWaves t: all loaded (one uniform width) before any is used
       uint32_t graw[kRB];
       int gidx[kRB];
 #pragma unroll
       for (int t = 0; t < kRB; ++t) {
-        const int rc = min(wave + kWaves * t, max(nqg - 1, 0));
+        const int rc = min(r0 + kWaves * t, max(nqg - 1, 0));
         gidx[t] = qpre ? q0 + rc : int(qidx[q0 + rc]);
       }
       if (dt == MF_DTYPE_F32) {
@@ -968,21 +975,21 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       }
 #pragma unroll
       for (int t = 0; t < kRB; ++t) {
-        const int r = wave + kWaves * t;
+        const int r = r0 + kWaves * t;
         const float gte = dt == MF_DTYPE_F32 ? __uint_as_float(graw[t])
                           : dt == MF_DTYPE_BF16 ? __uint_as_float(graw[t] << 16)
                                                 : float(__builtin_bit_cast(_Float16, uint16_t(graw[t])));
         crow[t] = r < nqg ? ldexpf(gte * kLog2e, cE) : 0.0f;
       }
-      store_rows(S0{}, wave, vu, crow);
-      store_rows(S1{}, wave, vv, crow);
-      store_rows(S2{}, wave, vw, kNoRow);
+      store_rows(S0{}, r0, vu, crow);
+      store_rows(S1{}, r0, vv, crow);
+      if (qb == 0) store_rows(S2{}, r0, vw, kNoRow);
       if (lane == 0) {
 #pragma unroll
-        for (int t = 0; t < kRB; ++t) cgf[wave + kWaves * t] = crow[t];
+        for (int t = 0; t < kRB; ++t) cgf[r0 + kWaves * t] = crow[t];
       }
     }
-    // W rows past the first batch (more than 48 staged keys)
+    // W rows past the first batch (more than kWaves kRB staged keys)
     for (int r0 = wave + kWaves * kRB; r0 < rj; r0 += kWaves * kRB) {
       uint32_t vw[kRB][2];
       load_rows(S2{}, r0, vw);
@@ -1407,8 +1414,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       if (qt >= nqt) continue;
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt)
-        *reinterpret_cast<mf_f32x4*>(red + (slot * kMaxQ + 16 * qt + r16) * Ly::RS + 16 * dt + 4 * g) = O[dt][qt];
-      if (g == 0) redl[slot * kMaxQ + 16 * qt + r16] = L[qt][0];
+        *reinterpret_cast<mf_f32x4*>(red + (slot * Ly::RQ + 16 * qt + r16) * Ly::RS + 16 * dt + 4 * g) = O[dt][qt];
+      if (g == 0) redl[slot * Ly::RQ + 16 * qt + r16] = L[qt][0];
     }
   };
   if constexpr (kWaves > kRedWaves) {
@@ -1422,11 +1429,11 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt) {
           const mf_f32x4 o2 =
-              *reinterpret_cast<const mf_f32x4*>(red + (slot * kMaxQ + 16 * qt + r16) * Ly::RS + 16 * dt + 4 * g);
+              *reinterpret_cast<const mf_f32x4*>(red + (slot * Ly::RQ + 16 * qt + r16) * Ly::RS + 16 * dt + 4 * g);
           O[dt][qt] += o2;
         }
         // every lane of a query column holds the same denominator in L[qt][0..3]
-        L[qt][0] += redl[slot * kMaxQ + 16 * qt + r16];
+        L[qt][0] += redl[slot * Ly::RQ + 16 * qt + r16];
       }
     }
     __syncthreads();
@@ -1445,9 +1452,9 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;
 #pragma unroll
     for (int w = 0; w < kRedWaves; ++w) {
-      l += redl[w * kMaxQ + i];
-      const float4 lo = *reinterpret_cast<const float4*>(red + (w * kMaxQ + i) * Ly::RS + c8);
-      const float4 hi = *reinterpret_cast<const float4*>(red + (w * kMaxQ + i) * Ly::RS + c8 + 4);
+      l += redl[w * Ly::RQ + i];
+      const float4 lo = *reinterpret_cast<const float4*>(red + (w * Ly::RQ + i) * Ly::RS + c8);
+      const float4 hi = *reinterpret_cast<const float4*>(red + (w * Ly::RQ + i) * Ly::RS + c8 + 4);
       o[0] += lo.x; o[1] += lo.y; o[2] += lo.z; o[3] += lo.w;
       o[4] += hi.x; o[5] += hi.y; o[6] += hi.z; o[7] += hi.w;
     }
@@ -1560,17 +1567,17 @@ __device__ __forceinline__ void scan_row_global(const uint8_t* row, int a, int e
 // whole molecules (row 2m: key mask of molecule m, row 2m + 1: its query
 // mask); TPR adjacent threads scan one row, each a segment of it, and the
 // segment counts meet over lanes.
-template <int DP, int W>
+template <int DP, bool BIAS>
 __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem, uint32_t* s_info) {
-  constexpr int kThreads = W * 64;
+  constexpr int kThreads = Waves<BIAS>::kCount * 64;
   const int tid = threadIdx.x;
   const int B = p.B, N = p.N;
   const int rows = 2 * B;
   // threads per row: a power of two, <= 8, with rows * tpr <= kThreads when rows allow
   const int tpr = rows > kThreads / 2 ? 1 : rows > kThreads / 4 ? 2 : rows > kThreads / 8 ? 4 : 8;
   const int rpp = kThreads / tpr;  // rows per pass (even)
-  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP, W>::kK2);  // [rpp] counts, then [rpp] first zeros
-  static_assert(kCap * Lay<DP, W>::RB >= kThreads * 2 * 4, "row results must fit in the K2 staging area");
+  int* s_cnt = reinterpret_cast<int*>(smem + Lay<DP, BIAS>::kK2);  // [rpp] counts, then [rpp] first zeros
+  static_assert(Lay<DP, BIAS>::kCap * Lay<DP, BIAS>::RB >= kThreads * 2 * 4, "row results must fit in the K2 staging area");
   const int seg = (N + tpr - 1) / tpr;
   for (int r0 = 0; r0 < rows; r0 += rpp) {
     const int r = r0 + tid / tpr, sg = tid & (tpr - 1);
@@ -1617,7 +1624,7 @@ __device__ __forceinline__ void scan_masks(const Params& p, unsigned char* smem,
 // every 4th pair.  s_cu holds the pairs (over the staging area).  The
 // molecule whose positions hold position w (when w < s_pre[B]) writes
 // *s_first = b | (w - its first position) << 16.
-template <int W, int GQ>
+template <int W, int GQ, int kCap>
 __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* s_info, uint16_t* s_order, int* s_pre,
                                                uint2* s_cu, int w, int* s_first) {
   constexpr int kThreads = W * 64;
@@ -1630,7 +1637,7 @@ __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* 
       const uint32_t w = s_info[b];
       const int nk = info_nk(w), nq = info_nq(w);
       cu.x = uint32_t(nk * nk) * uint32_t((nq + 15) / 16);
-      cu.y = uint32_t(H * num_groups<GQ>(nk, nq));
+      cu.y = uint32_t(H * num_groups<GQ, kCap>(nk, nq));
     }
     s_cu[b] = cu;
   }
@@ -1667,13 +1674,13 @@ __device__ __forceinline__ void rank_molecules(const Params& p, const uint32_t* 
 // masks and the attention of the group's queries.  Ends with a barrier.
 template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
 __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, int b, int h, int g, bool zero_share) {
-  using Ly = Lay<DP, Waves<BIAS>::kCount>;
+  using Ly = Lay<DP, BIAS>;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const uint32_t info = reinterpret_cast<const uint32_t*>(smem + Ly::kInfo)[b];
   const int nk = info_nk(info), nq = info_nq(info);
   const bool kpre = (info & kKPre) != 0, qpre = (info & kQPre) != 0;
-  const int gs = group_size<Waves<BIAS>::kGroup>(nk, nq);
+  const int gs = group_size<Waves<BIAS>::kGroup, Waves<BIAS>::kCap>(nk, nq);
   const int q0 = gs * g;
   const int nqg = min(gs, nq - q0);
   if (nqg > 0) {
@@ -1684,7 +1691,7 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
       if (wave == 1 && !qpre) write_ranks(p.qv + size_t(b) * p.N, p.N, qidx, lane);
       __syncthreads();
     }
-    if (nk > kCap) unit_body<T, DP, HAS_PV, true, BIAS, STR>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
+    if (nk > Waves<BIAS>::kCap) unit_body<T, DP, HAS_PV, true, BIAS, STR>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
     else unit_body<T, DP, HAS_PV, false, BIAS, STR>(p, smem, b, h, nk, q0, nqg, kpre, qpre, zero_share);
   }
   __syncthreads();
@@ -1700,9 +1707,9 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
 // the workgroups that finish first take the longest remaining units.
 // BIAS: one workgroup per CU (its bias operands take another ~59 KB of LDS).
 template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
-__global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, BIAS ? 1 : 2) simplicial_pair_kernel(Params p) {
+__global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, 2) simplicial_pair_kernel(Params p) {
   constexpr int W = Waves<BIAS>::kCount;
-  using Ly = Lay<DP, W>;
+  using Ly = Lay<DP, BIAS>;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   uint32_t* s_info = reinterpret_cast<uint32_t*>(smem + Ly::kInfo);
   int* s_pre = reinterpret_cast<int*>(smem + Ly::kPre);
@@ -1716,8 +1723,8 @@ __global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, BIAS ? 1 : 2) simpli
   const int wg = blockIdx.x;
 
   if (tid == 0) cl->claimed = 0;
-  scan_masks<DP, W>(p, smem, s_info);  // ends with a barrier
-  rank_molecules<W, Waves<BIAS>::kGroup>(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
+  scan_masks<DP, BIAS>(p, smem, s_info);  // ends with a barrier
+  rank_molecules<W, Waves<BIAS>::kGroup, Waves<BIAS>::kCap>(p, s_info, s_order, s_pre, reinterpret_cast<uint2*>(smem), wg, &s_first);
   const int total = s_pre[B];
 
   // the rows of padded queries: a static share of (b, h) pairs per
@@ -1740,7 +1747,7 @@ __global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, BIAS ? 1 : 2) simpli
       i = pos - s_pre[lo];
     }
     const uint32_t info = s_info[b];
-    const int ng = num_groups<Waves<BIAS>::kGroup>(info_nk(info), info_nq(info));
+    const int ng = num_groups<Waves<BIAS>::kGroup, Waves<BIAS>::kCap>(info_nk(info), info_nq(info));
     const int h = div_small(i, ng);
     run_unit<T, DP, HAS_PV, BIAS, STR>(p, smem, b, h, i - h * ng, pos == wg);  // ends with a barrier: cl->next is read
     if (tid == 0) {
@@ -1759,10 +1766,11 @@ __global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, BIAS ? 1 : 2) simpli
 
 template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
 int launch(const Params& prm, int num_cus, hipStream_t stream) {
-  const int grid = std::max(8, (BIAS ? 1 : 2) * num_cus);  // 2 workgroups per CU (1 with the bias)
+  const int grid = std::max(8, 2 * num_cus);  // 2 workgroups per CU
   auto kern = simplicial_pair_kernel<T, DP, HAS_PV, BIAS, STR>;
   constexpr int W = Waves<BIAS>::kCount;
-  const size_t lds = BIAS ? Lay<DP, W>::kTotalBias : Lay<DP, W>::kTotal;
+  const size_t lds = BIAS ? Lay<DP, BIAS>::kTotalBias : Lay<DP, BIAS>::kTotal;
+  static_assert((BIAS ? Lay<DP, BIAS>::kTotalBias : Lay<DP, BIAS>::kTotal) <= 80 * 1024, "two workgroups per CU");
   const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), int(lds));
   if (st != MF_OK) return st;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(W * 64), lds, stream, prm);
