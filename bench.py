@@ -65,7 +65,9 @@ def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # ~70 ms of untimed steps: the GPU reaches its steady-state clocks only after some tens of milliseconds
+    # of work (20 warm-up steps measured 33.7-34.1 us per step, 2000 measured 30.8-30.9 us, same build)
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--cpu-sample", type=int, default=64, help="molecules in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="CPU-baseline threads (0 = physical cores, capped by OMP_NUM_THREADS when set)")
