@@ -405,6 +405,27 @@ typedef struct mf_geometry_args {
 int mf_geometry_features(const mf_geometry_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* The lattice terms of the periodic adapter in one launch (ABI 11).         */
+/*                                                                           */
+/* For a batch of lattice latents [B, 6] fp32 in `lattice_repr`:             */
+/*   gram[b]       = C C^T of the lower-triangular cell C (the metric),      */
+/*                   non-finite entries replaced by 0                        */
+/*                   (lattice_latent_to_gram, geometry/lattice.py:12-59,94-100); */
+/*   y1[b]         = the clamped y1 latent (y1), or y1 recovered from gram   */
+/*                   (ltri) (lattice_latent_to_y1, lattice.py:65-91,103-131); */
+/*   cell_scale[b] = max(mean(exp(y1[b, 0:3])), 1e-8)                        */
+/*                   (PeriodicGeometryAdapter.forward, adapters.py:173-174,192). */
+/* Each output may be NULL.  fp32 throughout, every operation rounded as the */
+/* torch formulation evaluates it.  Replaces the ~27 small torch kernels of  */
+/* those three lines on a [B, 6] tensor.                                      */
+/* ------------------------------------------------------------------------ */
+#define MF_LATTICE_Y1 0
+#define MF_LATTICE_LTRI 1
+
+int mf_lattice_terms(const float* lattice, int32_t batch, int32_t lattice_repr, float* gram, float* y1,
+                     float* cell_scale, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Local (radius) attention over a neighbour bit mask.                        */
 /*                                                                           */
 /* out[b,h,i] = sum_j softmax_j(scale * q_i . k_j over j with mask[b,i,j]) v_j */

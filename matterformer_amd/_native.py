@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "mf_rows_to_heads",
     "mf_heads_to_rows",
     "mf_pair_mlp_bias",
+    "mf_lattice_terms",
 )
 
 EXPECTED_ABI_VERSION = 11
@@ -165,6 +166,8 @@ class MfGeometryArgs(ctypes.Structure):
 
 MF_SCALE_GIVEN = 0
 MF_SCALE_RMS = 1
+MF_LATTICE_Y1 = 0
+MF_LATTICE_LTRI = 1
 
 
 class MfRadiusAttnArgs(ctypes.Structure):
@@ -252,6 +255,10 @@ def _load() -> ctypes.CDLL | None:
     lib.mf_simplicial_fwd_workspace_size.restype = ctypes.c_uint64
     lib.mf_simplicial_bwd_workspace_size.argtypes = [ctypes.c_int32] * 5
     lib.mf_simplicial_bwd_workspace_size.restype = ctypes.c_uint64
+    if getattr(lib, "mf_lattice_terms", None) is not None:
+        lib.mf_lattice_terms.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.mf_lattice_terms.restype = ctypes.c_int
     version = lib.mf_abi_version()
     if version != EXPECTED_ABI_VERSION:
         _LOAD_ERROR = f"{path} has ABI version {version}, expected {EXPECTED_ABI_VERSION}"

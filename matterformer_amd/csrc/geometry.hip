@@ -191,8 +191,98 @@ __global__ void __launch_bounds__(kThreads) features_kernel(Params p) {
   }
 }
 
+// min(max(x, lo), hi) that keeps a NaN, as torch.clamp does
+__device__ __forceinline__ float clampf(float x, float lo, float hi) { return x != x ? x : fminf(fmaxf(x, lo), hi); }
+
+// The lattice terms of one cell per thread (lattice.py:12-131; adapters.py:173-174,192), each operation in
+// the order the torch formulation applies it (this file is built without FMA contraction).
+__global__ void __launch_bounds__(kThreads) lattice_kernel(const float* lat, int B, int repr, float* gram, float* y1,
+                                                           float* cell_scale) {
+  const int b = blockIdx.x * kThreads + threadIdx.x;
+  if (b >= B) return;
+  float l[6];
+#pragma unroll
+  for (int e = 0; e < 6; ++e) l[e] = lat[size_t(b) * 6 + e];
+  float c[3][3] = {{0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}, {0.f, 0.f, 0.f}};
+  if (repr == MF_LATTICE_Y1) {
+    const float l0 = expf(clampf(l[0], -5.0f, 5.0f));
+    const float l1 = expf(clampf(l[1], -5.0f, 5.0f));
+    const float l2 = expf(clampf(l[2], -5.0f, 5.0f));
+    const float ca = clampf(l[3], -0.9999f, 0.9999f);
+    const float cb = clampf(l[4], -0.9999f, 0.9999f);
+    const float cgm = clampf(l[5], -0.9999f, 0.9999f);
+    const float sg = sqrtf(fmaxf(1.0f - cgm * cgm, 1e-8f));
+    c[0][0] = l0;
+    c[1][0] = l1 * cgm;
+    c[1][1] = l1 * sg;
+    c[2][0] = l2 * cb;
+    c[2][1] = (l2 * (ca - cb * cgm)) / sg;
+    const float r = sqrtf((l2 * l2 - c[2][0] * c[2][0]) - c[2][1] * c[2][1]);
+    c[2][2] = r != r ? r : fmaxf(r, 1e-8f);  // clamp_min keeps a NaN
+  } else {
+    c[0][0] = expf(clampf(l[0], -5.0f, 5.0f));
+    c[1][1] = expf(clampf(l[2], -5.0f, 5.0f));
+    c[2][2] = expf(clampf(l[5], -5.0f, 5.0f));
+    c[1][0] = clampf(l[1], -10.0f, 10.0f);
+    c[2][0] = clampf(l[3], -10.0f, 10.0f);
+    c[2][1] = clampf(l[4], -10.0f, 10.0f);
+  }
+  float g[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const float v = (c[i][0] * c[j][0] + c[i][1] * c[j][1]) + c[i][2] * c[j][2];
+      g[i][j] = isfinite(v) ? v : 0.0f;
+    }
+  if (gram) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) gram[size_t(b) * 9 + 3 * i + j] = g[i][j];
+  }
+  float y[6];
+  if (repr == MF_LATTICE_Y1) {
+#pragma unroll
+    for (int e = 0; e < 3; ++e) y[e] = clampf(l[e], -5.0f, 5.0f);
+#pragma unroll
+    for (int e = 3; e < 6; ++e) y[e] = clampf(l[e], -0.9999f, 0.9999f);
+  } else {  // gram_to_y1
+    float len[3];
+#pragma unroll
+    for (int e = 0; e < 3; ++e) len[e] = sqrtf(fmaxf(g[e][e], 1e-8f));
+    const float da = fmaxf(len[1] * len[2], 1e-8f), db = fmaxf(len[0] * len[2], 1e-8f),
+                dg = fmaxf(len[0] * len[1], 1e-8f);
+#pragma unroll
+    for (int e = 0; e < 3; ++e) y[e] = logf(fmaxf(len[e], 1e-8f));
+    y[3] = clampf(g[1][2] / da, -0.9999f, 0.9999f);
+    y[4] = clampf(g[0][2] / db, -0.9999f, 0.9999f);
+    y[5] = clampf(g[0][1] / dg, -0.9999f, 0.9999f);
+  }
+  if (y1) {
+#pragma unroll
+    for (int e = 0; e < 6; ++e) y1[size_t(b) * 6 + e] = y[e];
+  }
+  if (cell_scale) cell_scale[b] = fmaxf(((expf(y[0]) + expf(y[1])) + expf(y[2])) / 3.0f, 1e-8f);
+}
+
 }  // namespace geom
 }  // namespace mf
+
+extern "C" int mf_lattice_terms(const float* lattice, int32_t batch, int32_t lattice_repr, float* gram, float* y1,
+                                float* cell_scale, void* stream) {
+  using namespace mf;
+  using namespace mf::geom;
+  if (batch < 0) return fail(MF_ERR_INVALID_ARGUMENT, "mf_lattice_terms: batch must be non-negative");
+  if (lattice_repr != MF_LATTICE_Y1 && lattice_repr != MF_LATTICE_LTRI)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_lattice_terms: unknown lattice_repr");
+  if (batch == 0) return MF_OK;
+  if (!lattice) return fail(MF_ERR_INVALID_ARGUMENT, "mf_lattice_terms: lattice must be non-NULL");
+  hipLaunchKernelGGL(lattice_kernel, dim3(unsigned((batch + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), lattice, int(batch), int(lattice_repr), gram, y1, cell_scale);
+  MF_HIP_CHECK(hipGetLastError());
+  return MF_OK;
+}
 
 extern "C" int mf_geometry_features(const mf_geometry_args* a, void* stream) {
   using namespace mf;

@@ -22,7 +22,7 @@ from itertools import product
 import torch
 from torch import nn
 
-from matterformer_amd.geometry_ops import lattice_to_gram
+from matterformer_amd.geometry_ops import lattice_terms
 
 
 @dataclass
@@ -39,19 +39,7 @@ class GeometryFeatures:
 
 def lattice_latent_to_y1(lattice: torch.Tensor, lattice_repr: str = "y1") -> torch.Tensor:
     """lattice.py:65-91,103-131: the clamped y1 latent (y1) or y1 recovered from the Gram matrix (ltri)."""
-    lat = lattice.float()
-    rep = lattice_repr.lower()
-    if rep == "y1":
-        return torch.cat([lat[:, :3].clamp(min=-5.0, max=5.0), lat[:, 3:].clamp(min=-0.9999, max=0.9999)], dim=-1)
-    if rep == "ltri":
-        gram = lattice_to_gram(lat, "ltri")
-        lengths = torch.sqrt(torch.diagonal(gram, dim1=-2, dim2=-1).clamp_min(1e-8))
-        den_a = (lengths[:, 1] * lengths[:, 2]).clamp_min(1e-8)
-        den_b = (lengths[:, 0] * lengths[:, 2]).clamp_min(1e-8)
-        den_g = (lengths[:, 0] * lengths[:, 1]).clamp_min(1e-8)
-        cos = torch.stack([(gram[:, 1, 2] / den_a), (gram[:, 0, 2] / den_b), (gram[:, 0, 1] / den_g)], dim=-1)
-        return torch.cat([torch.log(lengths.clamp_min(1e-8)), cos.clamp(min=-0.9999, max=0.9999)], dim=-1)
-    raise ValueError(f"Unsupported lattice_repr: {lattice_repr}")
+    return lattice_terms(lattice, lattice_repr)[1]
 
 
 _METRICS: dict = {}
@@ -186,9 +174,8 @@ class PeriodicGeometryAdapter(BaseGeometryAdapter):
             raise ValueError(f"lattice batch {lattice.shape[0]} does not match coords batch {coords.shape[0]}")
         coords = coords.float()
         lattice = lattice.float()
-        y1 = lattice_latent_to_y1(lattice, self.lattice_repr)
-        gram = lattice_to_gram(lattice, self.lattice_repr)
-        cell_scale = torch.exp(y1[:, :3]).mean(dim=-1).clamp_min(1e-8)
+        # adapters.py:173-174,192 (one mf_lattice_terms launch on the GPU)
+        gram, y1, cell_scale = lattice_terms(lattice, self.lattice_repr)
         extras = {"metric": gram, "cell_scale": cell_scale[:, None]}
         if coords.device.type == "cuda":
             if pad_mask is not None and pad_mask.shape != coords.shape[:2]:

@@ -10,7 +10,9 @@ geometry adapters and attention modules:
                      neighbour list the legacy knn / knn_graph built with
                      cdist + topk (legacy/rapidash_v5/models/rapidash_utils.py:139-193),
                      here with ties ordered by index.
-  lattice_to_gram    lattice_latent_to_gram (src/matterformer/geometry/lattice.py:12-100)
+  lattice_terms      lattice_latent_to_gram, lattice_latent_to_y1 and the periodic adapter's
+                     cell scale (src/matterformer/geometry/lattice.py:12-131, adapters.py:173-192);
+                     lattice_to_gram is its first output.
   radius_mask        minimum-image distance of PeriodicGeometryAdapter.forward
                      (adapters.py:141-149,176-190) or the plain distance
                      (:98-99), thresholded at a cutoff, as bits.
@@ -107,16 +109,12 @@ def knn_mask(idx: torch.Tensor, pad_mask: torch.Tensor | None = None, *, include
     return (bits, blocks) if with_block_mask else bits
 
 
-def lattice_to_gram(lattice: torch.Tensor, lattice_repr: str = "y1") -> torch.Tensor:
-    """Metric G = cell cell^T of a lattice latent (B, 6), as lattice_latent_to_gram
-    (src/matterformer/geometry/lattice.py:12-59,94-100): lower-triangular cell
-    with a along x and b in the xy plane, in fp32."""
-    lat = lattice.float()
-    if lat.ndim != 2 or lat.shape[-1] != 6:
-        raise ValueError(f"lattice must have shape (B, 6), got {tuple(lat.shape)}")
+def _lattice_terms_torch(lat: torch.Tensor, rep: str):
+    """The torch formulation (CPU tensors): lattice_latent_to_gram, lattice_latent_to_y1
+    (src/matterformer/geometry/lattice.py:12-131) and the periodic adapter's cell scale
+    (adapters.py:192)."""
     B = lat.shape[0]
     cell = torch.zeros(B, 3, 3, device=lat.device, dtype=lat.dtype)
-    rep = lattice_repr.lower()
     if rep == "y1":
         lengths = torch.exp(lat[:, :3].clamp(min=-5.0, max=5.0))
         ca, cb, cg = lat[:, 3:].clamp(min=-0.9999, max=0.9999).unbind(dim=-1)
@@ -128,7 +126,7 @@ def lattice_to_gram(lattice: torch.Tensor, lattice_repr: str = "y1") -> torch.Te
         cell[:, 2, 1] = lengths[:, 2] * (ca - cb * cg) / sg
         cell[:, 2, 2] = torch.sqrt(lengths[:, 2].square() - cell[:, 2, 0].square()
                                    - cell[:, 2, 1].square()).clamp_min(1e-8)
-    elif rep == "ltri":
+    else:
         diag = torch.exp(lat[:, [0, 2, 5]].clamp(min=-5.0, max=5.0))
         off = lat[:, [1, 3, 4]].clamp(min=-10.0, max=10.0)
         cell[:, 0, 0] = diag[:, 0]
@@ -137,10 +135,53 @@ def lattice_to_gram(lattice: torch.Tensor, lattice_repr: str = "y1") -> torch.Te
         cell[:, 2, 0] = off[:, 1]
         cell[:, 2, 1] = off[:, 2]
         cell[:, 2, 2] = diag[:, 2]
+    gram = torch.nan_to_num(torch.matmul(cell, cell.transpose(-1, -2)), nan=0.0, posinf=0.0, neginf=0.0)
+    if rep == "y1":
+        y1 = torch.cat([lat[:, :3].clamp(min=-5.0, max=5.0), lat[:, 3:].clamp(min=-0.9999, max=0.9999)], dim=-1)
     else:
+        lengths = torch.sqrt(torch.diagonal(gram, dim1=-2, dim2=-1).clamp_min(1e-8))
+        den_a = (lengths[:, 1] * lengths[:, 2]).clamp_min(1e-8)
+        den_b = (lengths[:, 0] * lengths[:, 2]).clamp_min(1e-8)
+        den_g = (lengths[:, 0] * lengths[:, 1]).clamp_min(1e-8)
+        cos = torch.stack([(gram[:, 1, 2] / den_a), (gram[:, 0, 2] / den_b), (gram[:, 0, 1] / den_g)], dim=-1)
+        y1 = torch.cat([torch.log(lengths.clamp_min(1e-8)), cos.clamp(min=-0.9999, max=0.9999)], dim=-1)
+    cell_scale = torch.exp(y1[:, :3]).mean(dim=-1).clamp_min(1e-8)
+    return gram, y1, cell_scale
+
+
+def lattice_terms(lattice: torch.Tensor, lattice_repr: str = "y1"):
+    """(gram (B, 3, 3), y1 (B, 6), cell_scale (B,)) of lattice latents (B, 6), fp32: the metric
+    C C^T of lattice_latent_to_gram (src/matterformer/geometry/lattice.py:12-59,94-100), the y1
+    latent of lattice_latent_to_y1 (:65-91,103-131) and the periodic adapter's cell scale
+    max(mean(exp(y1[:, :3])), 1e-8) (adapters.py:173-174,192).  CUDA tensors: one
+    mf_lattice_terms launch; CPU tensors: the torch formulation."""
+    lat = lattice.float()
+    if lat.ndim != 2 or lat.shape[-1] != 6:
+        raise ValueError(f"lattice must have shape (B, 6), got {tuple(lat.shape)}")
+    rep = lattice_repr.lower()
+    if rep not in ("y1", "ltri"):
         raise ValueError(f"Unsupported lattice_repr: {lattice_repr}")
-    gram = torch.matmul(cell, cell.transpose(-1, -2))
-    return torch.nan_to_num(gram, nan=0.0, posinf=0.0, neginf=0.0)
+    if lat.device.type != "cuda":
+        return _lattice_terms_torch(lat, rep)
+    dev = lat.device
+    B = lat.shape[0]
+    lat = lat.contiguous()
+    gram = torch.empty(B, 3, 3, device=dev, dtype=torch.float32)
+    y1 = torch.empty(B, 6, device=dev, dtype=torch.float32)
+    scale = torch.empty(B, device=dev, dtype=torch.float32)
+    code = _native.MF_LATTICE_Y1 if rep == "y1" else _native.MF_LATTICE_LTRI
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().mf_lattice_terms(lat.data_ptr(), B, code, gram.data_ptr(), y1.data_ptr(),
+                                                     scale.data_ptr(), _native.current_stream(dev)),
+                      "mf_lattice_terms")
+    return gram, y1, scale
+
+
+def lattice_to_gram(lattice: torch.Tensor, lattice_repr: str = "y1") -> torch.Tensor:
+    """Metric G = cell cell^T of a lattice latent (B, 6), as lattice_latent_to_gram
+    (src/matterformer/geometry/lattice.py:12-59,94-100): lower-triangular cell
+    with a along x and b in the xy plane, in fp32 (non-finite entries 0)."""
+    return lattice_terms(lattice, lattice_repr)[0]
 
 
 def radius_mask(coords: torch.Tensor, cutoff: float, *, gram: torch.Tensor | None = None,

@@ -81,3 +81,49 @@ def test_c4_features_and_mask_in_one_pass(cuda):
     bits, _ = radius_mask(frac, w.cutoff, gram=lattice_to_gram(lat))
     assert torch.equal(f.extras["radius_mask_bits"], bits)
     assert torch.isfinite(f.pair_dist_norm).all()
+
+
+def _lattice_cases(seed: int) -> torch.Tensor:
+    """Lattice latents: ordinary cells, every clamp engaged (log lengths past +-5, cosines past +-1,
+    ltri off-diagonals past +-10) and cells whose third row is degenerate (sqrt of a negative: NaN in the
+    cell, 0 in the metric)."""
+    gen = torch.Generator().manual_seed(seed)
+    lat = torch.cat([torch.rand(64, 3, generator=gen) * 1.5 + 1.8, torch.rand(64, 3, generator=gen) * 0.6 - 0.3],
+                    dim=-1)
+    wild = torch.randn(64, 6, generator=gen) * 8.0
+    degenerate = torch.tensor([[2.0, 2.0, 2.0, 0.9999, -0.9999, 0.9999], [1.0, 1.5, 2.0, -1.0, 1.0, -1.0]])
+    return torch.cat([lat, wild, degenerate])
+
+
+@pytest.mark.parametrize("rep", ["y1", "ltri"])
+def test_lattice_terms_kernel_matches_torch_formulation(cuda, rep):
+    """mf_lattice_terms (gram, y1, cell scale in one launch) against the torch formulation of
+    lattice.py:12-131 / adapters.py:192 on the CPU, and (y1) the metric against the float64 oracle:
+    the kernel evaluates the same fp32 operations in the same order, so only exp / log / sqrt rounding
+    may differ (relative 1e-6); metric entries the torch formulation zeroes (non-finite) are zero."""
+    from matterformer_amd.geometry_ops import _lattice_terms_torch, lattice_terms
+    from oracle.radius import lattice_y1_to_gram
+
+    lat = _lattice_cases(17 if rep == "y1" else 18)
+    g, y1, sc = (t.cpu() for t in lattice_terms(lat.to(cuda), rep))
+    rg, ry1, rsc = _lattice_terms_torch(lat, rep)
+    np.testing.assert_allclose(g.numpy(), rg.numpy(), rtol=1e-6, atol=1e-6)
+    # (ltri: y1[:3] = log |row| is near 0 for rows of length ~1, where one ulp of the length is ~1.2e-7 absolute)
+    np.testing.assert_allclose(y1.numpy(), ry1.numpy(), rtol=1e-6, atol=3e-7)
+    np.testing.assert_allclose(sc.numpy(), rsc.numpy(), rtol=1e-6, atol=0)
+    assert torch.equal(g == 0, rg == 0)
+    assert torch.isfinite(g).all() and torch.isfinite(y1).all() and torch.isfinite(sc).all()
+    if rep == "y1":
+        ordinary = lat[:64].numpy()
+        np.testing.assert_allclose(g[:64].numpy(), lattice_y1_to_gram(ordinary), rtol=2e-6, atol=1e-5)
+
+
+def test_periodic_adapter_lattice_extras_match_cpu(cuda):
+    """The adapter's metric and cell scale (now from mf_lattice_terms) against its CPU formulation."""
+    z = np.load(GOLDEN / "geometry_periodic.npz")
+    frac, lat = torch.from_numpy(z["frac"]), torch.from_numpy(z["lattice_y1"])
+    f = PeriodicGeometryAdapter()(frac.to(cuda), lattice=lat.to(cuda))
+    cpu = PeriodicGeometryAdapter()(frac, lattice=lat)
+    for key in ("metric", "cell_scale"):
+        np.testing.assert_allclose(f.extras[key].cpu().numpy(), cpu.extras[key].numpy(), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(f.global_geom.cpu().numpy(), cpu.global_geom.numpy(), rtol=1e-6, atol=0)
