@@ -574,6 +574,44 @@ typedef struct mf_pair_mlp_args {
 
 int mf_pair_mlp_bias(const mf_pair_mlp_args* args, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Its backward with respect to the MLP weights (ABI 11), the gradients     */
+/* autograd gives SimplicialGeometryBias's u, v, w MLPs (transformer.py:     */
+/* 566-584,702-717) for upstream gradients u_grad, v_grad, w_grad of the     */
+/* masked outputs (pairs outside pair_mask and the diagonal contribute       */
+/* nothing, as the reference's `* mask` makes them):                         */
+/*   dW2 = sum_p dY h^T,  db2 = sum_p dY,  dW1 = sum_p dA x^T,  db1 = sum_p dA, */
+/*   h = SiLU(W1 x + b1),  dA = (W2^T dY) (.) SiLU'(W1 x + b1).               */
+/* `fwd` holds the forward's features and weights (its u_out, v_out, w_out   */
+/* are not used).  The features take no gradient.  fp32 MFMA; every sum in  */
+/* a fixed order (two calls give identical bits).  R <= 28, hidden a         */
+/* multiple of 16 <= 128, H <= 16; the workspace holds per-wave partial sums */
+/* (mf_pair_mlp_bias_bwd_workspace_size(hidden) bytes, no fill needed).      */
+/* ------------------------------------------------------------------------ */
+typedef struct mf_pair_mlp_bwd_args {
+  mf_pair_mlp_args fwd;
+  const float* u_grad;          /* [B, H, N, N] */
+  const float* v_grad;
+  const float* w_grad;
+  float* u_dw1;                 /* [hidden, 3 + R] */
+  float* u_db1;                 /* [hidden]        */
+  float* u_dw2;                 /* [H, hidden]     */
+  float* u_db2;                 /* [H]             */
+  float* v_dw1;
+  float* v_db1;
+  float* v_dw2;
+  float* v_db2;
+  float* w_dw1;                 /* [hidden, R]     */
+  float* w_db1;
+  float* w_dw2;
+  float* w_db2;
+  void* workspace;
+  uint64_t workspace_bytes;
+} mf_pair_mlp_bwd_args;
+
+uint64_t mf_pair_mlp_bias_bwd_workspace_size(int32_t hidden);
+int mf_pair_mlp_bias_bwd(const mf_pair_mlp_bwd_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

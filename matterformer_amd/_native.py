@@ -50,6 +50,8 @@ EXPORTED_SYMBOLS = (
     "mf_heads_to_rows",
     "mf_pair_mlp_bias",
     "mf_lattice_terms",
+    "mf_pair_mlp_bias_bwd",
+    "mf_pair_mlp_bias_bwd_workspace_size",
 )
 
 EXPECTED_ABI_VERSION = 11
@@ -212,6 +214,12 @@ class MfPairMlpArgs(ctypes.Structure):
         (n, ctypes.c_int32) for n in ("batch", "atoms", "rbf", "hidden", "heads")]
 
 
+class MfPairMlpBwdArgs(ctypes.Structure):
+    _fields_ = [("fwd", MfPairMlpArgs)] + [(f"{m}_grad", ctypes.c_void_p) for m in "uvw"] + [
+        (f"{m}_{t}", ctypes.c_void_p) for m in "uvw" for t in ("dw1", "db1", "dw2", "db2")] + [
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64)]
+
+
 _LIB: ctypes.CDLL | None = None
 _LOAD_ERROR: str | None = None
 
@@ -244,6 +252,7 @@ def _load() -> ctypes.CDLL | None:
         ("mf_rows_to_heads", MfRowsToHeadsArgs),
         ("mf_heads_to_rows", MfHeadsToRowsArgs),
         ("mf_pair_mlp_bias", MfPairMlpArgs),
+        ("mf_pair_mlp_bias_bwd", MfPairMlpBwdArgs),
     ):
         fn = getattr(lib, name, None)
         if fn is not None:
@@ -255,6 +264,9 @@ def _load() -> ctypes.CDLL | None:
     lib.mf_simplicial_fwd_workspace_size.restype = ctypes.c_uint64
     lib.mf_simplicial_bwd_workspace_size.argtypes = [ctypes.c_int32] * 5
     lib.mf_simplicial_bwd_workspace_size.restype = ctypes.c_uint64
+    if getattr(lib, "mf_pair_mlp_bias_bwd_workspace_size", None) is not None:
+        lib.mf_pair_mlp_bias_bwd_workspace_size.argtypes = [ctypes.c_int32]
+        lib.mf_pair_mlp_bias_bwd_workspace_size.restype = ctypes.c_uint64
     if getattr(lib, "mf_lattice_terms", None) is not None:
         lib.mf_lattice_terms.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]

@@ -274,6 +274,216 @@ int launch(const Params& p, int num_cus, hipStream_t s) {
   return MF_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Backward (weights): for MLP m over the valid off-diagonal pairs p with upstream gradient dY[o][p]
+// (the gradient of the masked output, transformer.py:702-717, so invalid pairs contribute nothing):
+//   a1 = W1 x + b1,  h = SiLU(a1),  dH = W2^T dY,  dA = dH (.) SiLU'(a1),  SiLU'(a) = s (1 + a (1 - s)),
+//   dW2 += dY h^T,  db2 += dY,  dW1 += dA x^T,  db1 += dA   (db1 as the column of dW1 for a constant-1
+//   feature placed after the last real one).
+// One workgroup of kBwdThreads takes MLP blockIdx.y; its waves take (molecule, row, 64-column group) units
+// as the forward does and, per 16-pair chunk with a valid pair, recompute layer 1 transposed (MFMA 16x16x4
+// fp32, pairs as the rows: lane (g, r16) holds pairs 4 g + r of hidden unit r16), form dH^T the same way,
+// and accumulate dW1^T [f][h] and dW2 [o][h] by MFMA over the pairs (K): accumulator r of h and dA is the B
+// operand of K step r as it is (K index g = pair 4 g + r), so nothing is transposed.  The waves of a workgroup add
+// their sums into LDS in wave order and the workgroup writes them to its workspace slot; a second launch adds
+// the slots in slot order.  Deterministic (no atomics).
+// ---------------------------------------------------------------------------
+constexpr int kBwdThreads = 256;
+constexpr int kBwdWaves = kBwdThreads / 64;
+constexpr int kBwdGroups = 256;     // workgroups per MLP (about three per CU at ~170 registers per lane)
+constexpr int kBwdMaxHidden = 128;  // dW1^T / dW2 accumulators in registers: 2 x HT + HT tiles
+constexpr int kBwdSlots = kBwdGroups;
+
+struct BwdParams {
+  const float* delta;
+  const float* dnorm;
+  const uint8_t* mask;
+  const float* centers;
+  float neg_gamma;
+  const float* w1[3];
+  const float* b1[3];
+  const float* w2[3];
+  const float* gy[3];   // [B, H, N, N] upstream gradients of u, v, w
+  float* dw1[3];        // [hidden, F_m]
+  float* db1[3];        // [hidden]
+  float* dw2[3];        // [H, hidden]
+  float* db2[3];        // [H]
+  float* slots;         // [3][kBwdSlots][48 hidden + 16] per-wave partial sums
+  int B, N, R, hidden, heads, groups;
+};
+
+__host__ __device__ inline size_t bwd_slot_floats(int hidden) { return size_t(48) * hidden + 16; }
+
+template <int KS, int KP>
+__global__ void __launch_bounds__(kBwdThreads) pair_mlp_bwd_kernel(BwdParams p) {
+  extern __shared__ float lds[];
+  const int m = blockIdx.y;
+  constexpr int KMAX = KS > KP ? KS : KP;
+  const int K = m < 2 ? KS : KP;          // layer-1 K steps (features 4 t + g)
+  const int F = m < 2 ? 3 + p.R : p.R;    // true input width; feature F is the constant 1 (db1)
+  const int hidden = p.hidden, H = p.heads, HT = hidden / 16;
+  const int s1 = 4 * K + 1, s2 = hidden + 1;
+  // LDS: W1 [hidden][s1] (columns >= F zero), b1 [hidden], W2 [16][s2] (rows >= H zero), then the
+  // workgroup's sums [48 hidden + 16]
+  float* W1 = lds;
+  float* B1 = W1 + hidden * s1;
+  float* W2 = B1 + hidden;
+  float* red = W2 + 16 * s2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, r16 = lane & 15;
+  for (int e = tid; e < hidden * 4 * K; e += kBwdThreads) {
+    const int h = e / (4 * K), f = e - h * (4 * K);
+    W1[h * s1 + f] = f < F ? p.w1[m][h * F + f] : 0.0f;
+  }
+  for (int e = tid; e < hidden; e += kBwdThreads) B1[e] = p.b1[m][e];
+  for (int e = tid; e < 16 * hidden; e += kBwdThreads) {
+    const int o = e / hidden, h = e - o * hidden;
+    W2[o * s2 + h] = o < H ? p.w2[m][o * hidden + h] : 0.0f;
+  }
+  __syncthreads();
+
+  const int N = p.N, B = p.B;
+  const size_t plane = size_t(N) * N;
+  const float kexp = p.neg_gamma * 1.44269504088896341f;
+  const float* gy = p.gy[m];
+  // features of a pair as the layer-1 A operand (feature 4 t + g) and as the dW1 A operand (feature 16 ft + r16)
+  const int rb0 = m < 2 ? 3 : 0;  // first rbf feature
+  auto feature = [&](size_t pair, float dn, int f) -> float {
+    if (f < rb0) return p.delta[3 * pair + f];
+    if (f < F) {
+      const float d = dn - p.centers[f - rb0];
+      return __builtin_amdgcn_exp2f(kexp * (d * d));
+    }
+    return f == F ? 1.0f : 0.0f;
+  };
+
+  mf_f32x4 aw1[2][kBwdMaxHidden / 16], aw2[kBwdMaxHidden / 16];
+#pragma unroll
+  for (int ht = 0; ht < kBwdMaxHidden / 16; ++ht) {
+    aw1[0][ht] = aw1[1][ht] = aw2[ht] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float adb2 = 0.0f;
+
+  const long long units = (long long)B * N * p.groups;
+  const int nw = gridDim.x * kBwdWaves;
+  for (long long u = (long long)blockIdx.x * kBwdWaves + wave; u < units; u += nw) {
+    const int b = int(u % B);
+    const int i = int((u / B) % N);
+    const int cg = int(u / ((long long)B * N));
+    const int j = cg * 64 + lane;
+    const bool valid = j < N && j != i && p.mask[(size_t(b) * N + i) * N + min(j, N - 1)] != 0;
+    const unsigned long long bal = __ballot(valid);
+    const size_t prow = (size_t(b) * N + i) * N;
+    for (int c = 0; c < 4; ++c) {
+      const unsigned bits = unsigned(bal >> (16 * c)) & 0xffffu;
+      if (bits == 0u) continue;  // wave-uniform
+      const int j0 = cg * 64 + 16 * c;
+      // pair r16 (layer 1, dH): features 4 t + g, upstream gradients of heads 4 s + g
+      const bool v16 = (bits >> r16) & 1u;
+      const size_t pr = prow + (v16 ? j0 + r16 : 0);
+      const float dn16 = v16 ? p.dnorm[pr] : 0.0f;
+      float xf[KMAX];
+#pragma unroll
+      for (int t = 0; t < KMAX; ++t) xf[t] = (t < K && v16) ? feature(pr, dn16, 4 * t + g) : 0.0f;
+      float yb[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int o = 4 * s + g;
+        yb[s] = (v16 && o < H) ? gy[(size_t(b) * H + o) * plane + size_t(i) * N + j0 + r16] : 0.0f;
+      }
+      // pairs 4 g + s (dW1 / dW2 A operands of K step s): features 16 ft + r16, upstream gradient of head r16
+      float xw[4][2], ya[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int q = 4 * g + s;
+        const bool vq = (bits >> q) & 1u;
+        const size_t pq = prow + (vq ? j0 + q : 0);
+        const float dnq = vq ? p.dnorm[pq] : 0.0f;
+#pragma unroll
+        for (int ft = 0; ft < 2; ++ft) xw[s][ft] = vq ? feature(pq, dnq, 16 * ft + r16) : 0.0f;
+        ya[s] = (vq && r16 < H) ? gy[(size_t(b) * H + r16) * plane + size_t(i) * N + j0 + q] : 0.0f;
+        adb2 += ya[s];
+      }
+      for (int ht = 0; ht < HT; ++ht) {
+        // layer 1 and dH, transposed: pairs 4 g + r, hidden unit 16 ht + r16
+        const float bias1 = B1[16 * ht + r16];
+        mf_f32x4 a1 = mf_f32x4{bias1, bias1, bias1, bias1}, dh = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+        const float* wa = W1 + (16 * ht + r16) * s1 + g;
+#pragma unroll
+        for (int t = 0; t < KMAX; ++t)
+          if (t < K) a1 = mma(xf[t], wa[4 * t], a1);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          if (4 * s < H) dh = mma(yb[s], W2[(4 * s + g) * s2 + 16 * ht + r16], dh);
+        float hv[4], dv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float a = a1[r];
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.44269504088896341f));
+          hv[r] = a * sg;
+          dv[r] = dh[r] * (sg * (1.0f + a * (1.0f - sg)));
+        }
+        // K step s: pairs 4 g + s, i.e. accumulator s of h and dA
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          aw1[0][ht] = mma(xw[s][0], dv[s], aw1[0][ht]);
+          aw1[1][ht] = mma(xw[s][1], dv[s], aw1[1][ht]);
+          aw2[ht] = mma(ya[s], hv[s], aw2[ht]);
+        }
+      }
+    }
+  }
+  // the waves' sums added into LDS in wave order: dW1^T [32][hidden] (f = 16 ft + 4 g + r, h = 16 ht + r16),
+  // dW2 [16][hidden] (o = 4 g + r), db2 [16] (over the four lane groups); then the workgroup's slot
+  adb2 += __shfl_xor(adb2, 16, 64);
+  adb2 += __shfl_xor(adb2, 32, 64);
+  for (int w = 0; w < kBwdWaves; ++w) {
+    if (wave == w) {
+      for (int ht = 0; ht < HT; ++ht) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int h = 16 * ht + r16;
+          float* e0 = red + (4 * g + r) * hidden + h;
+          float* e1 = red + (16 + 4 * g + r) * hidden + h;
+          float* e2 = red + (32 + 4 * g + r) * hidden + h;
+          *e0 = w == 0 ? aw1[0][ht][r] : *e0 + aw1[0][ht][r];
+          *e1 = w == 0 ? aw1[1][ht][r] : *e1 + aw1[1][ht][r];
+          *e2 = w == 0 ? aw2[ht][r] : *e2 + aw2[ht][r];
+        }
+      }
+      if (g == 0) red[48 * hidden + r16] = w == 0 ? adb2 : red[48 * hidden + r16] + adb2;
+    }
+    __syncthreads();
+  }
+  const size_t sf = bwd_slot_floats(hidden);
+  float* slot = p.slots + (size_t(m) * kBwdSlots + blockIdx.x) * sf;
+  for (int e = tid; e < int(sf); e += kBwdThreads) slot[e] = red[e];
+}
+
+// The slots added in slot order, then written as dW1 [hidden][F] (column F of the sums: db1), dW2 [H][hidden],
+// db2 [H].
+__global__ void __launch_bounds__(256) pair_mlp_bwd_reduce(BwdParams p) {
+  const int m = blockIdx.y;
+  const int hidden = p.hidden, H = p.heads;
+  const int F = m < 2 ? 3 + p.R : p.R;
+  const size_t sf = bwd_slot_floats(hidden);
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (size_t(e) >= sf) return;
+  const float* src = p.slots + size_t(m) * kBwdSlots * sf + e;
+  float s = 0.0f;
+  for (int w = 0; w < kBwdSlots; ++w) s += src[size_t(w) * sf];
+  if (e < 32 * hidden) {
+    const int f = e / hidden, h = e - f * hidden;
+    if (f < F) p.dw1[m][h * F + f] = s;
+    else if (f == F) p.db1[m][h] = s;
+  } else if (e < 48 * hidden) {
+    const int o = e / hidden - 32, h = e % hidden;
+    if (o < H) p.dw2[m][o * hidden + h] = s;
+  } else {
+    const int o = e - 48 * hidden;
+    if (o < H) p.db2[m][o] = s;
+  }
+}
+
 }  // namespace pmlp
 }  // namespace mf
 
@@ -331,4 +541,78 @@ extern "C" int mf_pair_mlp_bias(const mf_pair_mlp_args* a, void* stream) {
   // spoke K steps (3 + R features) and pair K steps (R features)
   if (ks <= 5 && kp <= 4) return launch<5, 4>(p, dev.num_cus, s);
   return launch<8, 8>(p, dev.num_cus, s);
+}
+
+extern "C" uint64_t mf_pair_mlp_bias_bwd_workspace_size(int32_t hidden) {
+  if (hidden < 16 || hidden > mf::pmlp::kBwdMaxHidden || hidden % 16 != 0) return 0;
+  return uint64_t(3) * mf::pmlp::kBwdSlots * mf::pmlp::bwd_slot_floats(hidden) * sizeof(float);
+}
+
+extern "C" int mf_pair_mlp_bias_bwd(const mf_pair_mlp_bwd_args* a, void* stream) {
+  using namespace mf;
+  using namespace mf::pmlp;
+  if (a == nullptr) return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias_bwd: args is NULL");
+  const mf_pair_mlp_args& f = a->fwd;
+  if (!f.pair_delta || !f.pair_dist_norm || !f.pair_mask || !f.rbf_centers)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias_bwd: feature pointers must be non-NULL");
+  const float* const w1[3] = {f.u_w1, f.v_w1, f.w_w1};
+  const float* const b1[3] = {f.u_b1, f.v_b1, f.w_b1};
+  const float* const w2[3] = {f.u_w2, f.v_w2, f.w_w2};
+  const float* const gy[3] = {a->u_grad, a->v_grad, a->w_grad};
+  float* const dw1[3] = {a->u_dw1, a->v_dw1, a->w_dw1};
+  float* const db1[3] = {a->u_db1, a->v_db1, a->w_db1};
+  float* const dw2[3] = {a->u_dw2, a->v_dw2, a->w_dw2};
+  float* const db2[3] = {a->u_db2, a->v_db2, a->w_db2};
+  for (int m = 0; m < 3; ++m)
+    if (!w1[m] || !b1[m] || !w2[m] || !gy[m] || !dw1[m] || !db1[m] || !dw2[m] || !db2[m])
+      return fail(MF_ERR_INVALID_ARGUMENT,
+                  "mf_pair_mlp_bias_bwd: every weight, upstream gradient and weight gradient must be non-NULL");
+  if (f.batch < 0 || f.atoms < 0) return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias_bwd: bad sizes");
+  if (f.rbf < 1 || f.rbf > kMaxRbf - 1)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias_bwd: rbf features must be in [1, 28]");
+  if (f.hidden < 16 || f.hidden > kBwdMaxHidden || f.hidden % 16 != 0)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias_bwd: hidden must be a multiple of 16 in [16, 128]");
+  if (f.heads < 1 || f.heads > kMaxHeads)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias_bwd: heads must be in [1, 16]");
+  if (!std::isfinite(f.rbf_gamma)) return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias_bwd: gamma must be finite");
+  const uint64_t need = mf_pair_mlp_bias_bwd_workspace_size(f.hidden);
+  if (a->workspace == nullptr || a->workspace_bytes < need)
+    return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias_bwd: workspace smaller than "
+                                         "mf_pair_mlp_bias_bwd_workspace_size(hidden)");
+  if ((long long)f.batch * f.atoms * ((f.atoms + 63) / 64 + 1) > 0x7fffffffLL)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias_bwd: batch * atoms * ceil(atoms / 64) must stay below 2^31");
+  BwdParams p{};
+  p.delta = f.pair_delta;
+  p.dnorm = f.pair_dist_norm;
+  p.mask = f.pair_mask;
+  p.centers = f.rbf_centers;
+  p.neg_gamma = -f.rbf_gamma;
+  for (int m = 0; m < 3; ++m) {
+    p.w1[m] = w1[m]; p.b1[m] = b1[m]; p.w2[m] = w2[m]; p.gy[m] = gy[m];
+    p.dw1[m] = dw1[m]; p.db1[m] = db1[m]; p.dw2[m] = dw2[m]; p.db2[m] = db2[m];
+  }
+  p.slots = static_cast<float*>(a->workspace);
+  p.B = f.batch;
+  p.N = f.atoms;
+  p.R = f.rbf;
+  p.hidden = f.hidden;
+  p.heads = f.heads;
+  p.groups = (f.atoms + 63) / 64;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int ks = (3 + f.rbf + 1 + 3) / 4, kp = (f.rbf + 1 + 3) / 4;  // K steps holding the features (and F)
+  // LDS of the instantiation: W1 rows of 4 KMAX + 1 (the kernel's largest stride), b1, W2, transpose tiles
+  auto go = [&](auto kern, int kmax) -> int {
+    const size_t lds = (size_t(f.hidden) * (4 * kmax + 1) + f.hidden + 16 * size_t(f.hidden + 1) +
+                        bwd_slot_floats(f.hidden)) * sizeof(float);
+    const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), int(lds));
+    if (st != MF_OK) return st;
+    hipLaunchKernelGGL(kern, dim3(kBwdGroups, 3), dim3(kBwdThreads), lds, s, p);
+    MF_HIP_CHECK(hipGetLastError());
+    const int rblocks = int((bwd_slot_floats(f.hidden) + 255) / 256);
+    hipLaunchKernelGGL(pair_mlp_bwd_reduce, dim3(rblocks, 3), dim3(256), 0, s, p);
+    MF_HIP_CHECK(hipGetLastError());
+    return MF_OK;
+  };
+  if (ks <= 5 && kp <= 5) return go(pair_mlp_bwd_kernel<5, 5>, 5);
+  return go(pair_mlp_bwd_kernel<8, 8>, 8);
 }

@@ -1,10 +1,11 @@
 """The factorized geometry-bias MLPs on the GPU: SimplicialGeometryBias._compute_factorized_terms
-(src/matterformer/models/transformer.py:702-717) as one mf_pair_mlp_bias pass over the valid pairs.
+(src/matterformer/models/transformer.py:702-717) as one mf_pair_mlp_bias pass over the valid pairs, and, when
+the MLP weights take gradients, its weight backward as one mf_pair_mlp_bias_bwd pass (an autograd Function).
 
-Used for inference calls (the kernel has no backward): GPU features, fp32 weights and features, materialised
-LazyLinear layers (their first call runs the torch formulation, which draws their weights in the reference's
-order), non-periodic spoke features (no Fourier / global terms), rbf <= 29, hidden a multiple of 16 <= 256,
-heads <= 16.  Everything else takes the torch formulation.
+Served: GPU features, fp32 weights and features, materialised LazyLinear layers (their first call runs the
+torch formulation, which draws their weights in the reference's order), non-periodic spoke features (no
+Fourier / global terms), rbf <= 29, hidden a multiple of 16 <= 256, heads <= 16; under autograd also rbf <= 28,
+hidden <= 128 and features that take no gradient.  Everything else takes the torch formulation.
 """
 
 from __future__ import annotations
@@ -15,21 +16,32 @@ from torch.nn.parameter import UninitializedParameter
 from matterformer_amd import _native
 
 
-def _mlp_parts(mlp):
-    first, act, last = mlp[0], mlp[1], mlp[2]
-    return first, act, last
+def _mlps(module):
+    return module.spoke_bias_u_mlp, module.spoke_bias_v_mlp, module.pair_bias_w_mlp
+
+
+def _weights(module) -> list[torch.Tensor]:
+    """W1, b1, W2, b2 of the u, v, w MLPs, in that order (12 tensors)."""
+    out = []
+    for mlp in _mlps(module):
+        first, last = mlp[0], mlp[2]
+        out += [first.weight, first.bias, last.weight, last.bias]
+    return out
+
+
+def _trains(module, geom_features) -> bool:
+    g = geom_features
+    return torch.is_grad_enabled() and (any(prm.requires_grad for m in _mlps(module) for prm in m.parameters())
+                                        or g.pair_delta.requires_grad or g.pair_dist_norm.requires_grad)
 
 
 def serves(module, geom_features) -> bool:
     g = geom_features
     if g.pair_delta.device.type != "cuda":
         return False
-    mlps = (module.spoke_bias_u_mlp, module.spoke_bias_v_mlp, module.pair_bias_w_mlp)
+    mlps = _mlps(module)
     params = [prm for m in mlps for prm in m.parameters()]
     if any(isinstance(prm, UninitializedParameter) for prm in params):
-        return False
-    if torch.is_grad_enabled() and (any(prm.requires_grad for prm in params) or g.pair_delta.requires_grad
-                                    or g.pair_dist_norm.requires_grad):
         return False
     if module.use_periodic_features and g.kind == "periodic":
         return False
@@ -44,34 +56,98 @@ def serves(module, geom_features) -> bool:
     if mlps[0][0].in_features != 3 + R or mlps[1][0].in_features != 3 + R or mlps[2][0].in_features != R:
         return False
     tensors = [g.pair_delta, g.pair_dist_norm] + params
-    return all(t.dtype == torch.float32 for t in tensors)
+    if not all(t.dtype == torch.float32 for t in tensors):
+        return False
+    if _trains(module, g):
+        # the weight backward: features without gradient, R <= 28, hidden <= 128
+        if g.pair_delta.requires_grad or g.pair_dist_norm.requires_grad:
+            return False
+        return R <= 28 and hidden <= 128
+    return True
+
+
+def _forward_args(module, delta, dnorm, mask, centers, gamma, weights, outs):
+    B, N = delta.shape[:2]
+    fields = {}
+    for idx, name in enumerate("uvw"):
+        for k, key in enumerate(("w1", "b1", "w2", "b2")):
+            fields[f"{name}_{key}"] = weights[4 * idx + k].data_ptr()
+    return _native.MfPairMlpArgs(
+        pair_delta=delta.data_ptr(), pair_dist_norm=dnorm.data_ptr(), pair_mask=mask.data_ptr(),
+        rbf_centers=centers.data_ptr(), rbf_gamma=gamma,
+        u_out=_native.ptr(outs[0]), v_out=_native.ptr(outs[1]), w_out=_native.ptr(outs[2]),
+        batch=B, atoms=N, rbf=int(centers.numel()), hidden=int(weights[0].shape[0]), heads=int(weights[2].shape[0]),
+        **fields)
+
+
+def _inputs(module, geom_features):
+    g = geom_features
+    dev = g.pair_delta.device
+    delta = g.pair_delta.detach().contiguous()
+    dnorm = g.pair_dist_norm.detach().contiguous()
+    mask = g.pair_mask.to(torch.uint8).contiguous()
+    centers = module._edge_rbf_centers.to(device=dev, dtype=torch.float32).contiguous()
+    return delta, dnorm, mask, centers, float(module._edge_rbf_gamma_value)
+
+
+def _run_forward(module, delta, dnorm, mask, centers, gamma, weights):
+    B, N = delta.shape[:2]
+    H = int(weights[2].shape[0])
+    dev = delta.device
+    outs = [torch.empty(B, H, N, N, device=dev, dtype=torch.float32) for _ in range(3)]
+    args = _forward_args(module, delta, dnorm, mask, centers, gamma, weights, outs)
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().mf_pair_mlp_bias(args, _native.current_stream(dev)), "mf_pair_mlp_bias")
+    return outs
+
+
+class _PairMlpFunction(torch.autograd.Function):
+    """u, v, w from mf_pair_mlp_bias; the gradients of the 12 MLP weights from mf_pair_mlp_bias_bwd."""
+
+    @staticmethod
+    def forward(ctx, module, delta, dnorm, mask, centers, gamma, *weights):
+        ws = [w.detach().contiguous() for w in weights]
+        outs = _run_forward(module, delta, dnorm, mask, centers, gamma, ws)
+        ctx.save_for_backward(delta, dnorm, mask, centers, *ws)
+        ctx.gamma = gamma
+        ctx.module = module
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, gu, gv, gw):
+        delta, dnorm, mask, centers, *ws = ctx.saved_tensors
+        dev = delta.device
+        B, N = delta.shape[:2]
+        H = int(ws[2].shape[0])
+        hidden = int(ws[0].shape[0])
+        ups = []
+        for gt in (gu, gv, gw):
+            ups.append(torch.zeros(B, H, N, N, device=dev, dtype=torch.float32) if gt is None
+                       else gt.float().contiguous())
+        grads = [torch.empty_like(w) for w in ws]
+        lib = _native.lib()
+        nbytes = int(lib.mf_pair_mlp_bias_bwd_workspace_size(hidden))
+        workspace = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+        fields = {}
+        for idx, name in enumerate("uvw"):
+            for k, key in enumerate(("dw1", "db1", "dw2", "db2")):
+                fields[f"{name}_{key}"] = grads[4 * idx + k].data_ptr()
+        args = _native.MfPairMlpBwdArgs(
+            fwd=_forward_args(ctx.module, delta, dnorm, mask, centers, ctx.gamma, ws, (None, None, None)),
+            u_grad=ups[0].data_ptr(), v_grad=ups[1].data_ptr(), w_grad=ups[2].data_ptr(),
+            workspace=workspace.data_ptr(), workspace_bytes=nbytes, **fields)
+        with torch.cuda.device(dev):
+            _native.check(lib.mf_pair_mlp_bias_bwd(args, _native.current_stream(dev)), "mf_pair_mlp_bias_bwd")
+        return (None, None, None, None, None, None, *grads)
 
 
 def factorized_terms(module, geom_features):
-    """(u, v, w) [B, H, N, N] fp32, diagonal and invalid pairs zero."""
-    g = geom_features
-    B, N = g.pair_delta.shape[:2]
-    H = module.n_heads
-    dev = g.pair_delta.device
-    delta = g.pair_delta.contiguous()
-    dnorm = g.pair_dist_norm.contiguous()
-    mask = g.pair_mask.to(torch.uint8).contiguous()
-    centers = module._edge_rbf_centers.to(device=dev, dtype=torch.float32).contiguous()
-    gamma = module._edge_rbf_gamma_value
-    outs = [torch.empty(B, H, N, N, device=dev, dtype=torch.float32) for _ in range(3)]
-    keep = [delta, dnorm, mask, centers]
-    fields = {}
-    for name, mlp in zip("uvw", (module.spoke_bias_u_mlp, module.spoke_bias_v_mlp, module.pair_bias_w_mlp)):
-        first, _, last = _mlp_parts(mlp)
-        ts = [first.weight.contiguous(), first.bias.contiguous(), last.weight.contiguous(), last.bias.contiguous()]
-        keep += ts
-        for t, key in zip(ts, ("w1", "b1", "w2", "b2")):
-            fields[f"{name}_{key}"] = t.data_ptr()
-    args = _native.MfPairMlpArgs(
-        pair_delta=delta.data_ptr(), pair_dist_norm=dnorm.data_ptr(), pair_mask=mask.data_ptr(),
-        rbf_centers=centers.data_ptr(), rbf_gamma=gamma, u_out=outs[0].data_ptr(), v_out=outs[1].data_ptr(),
-        w_out=outs[2].data_ptr(), batch=B, atoms=N, rbf=int(centers.numel()), hidden=module.spoke_bias_u_mlp[0].out_features,
-        heads=H, **fields)
-    with torch.cuda.device(dev):
-        _native.check(_native.lib().mf_pair_mlp_bias(args, _native.current_stream(dev)), "mf_pair_mlp_bias")
-    return tuple(outs)
+    """(u, v, w) [B, H, N, N] fp32, diagonal and invalid pairs zero; differentiable in the MLP weights when
+    they take gradients."""
+    delta, dnorm, mask, centers, gamma = _inputs(module, geom_features)
+    weights = _weights(module)
+    if _trains(module, geom_features):
+        return _PairMlpFunction.apply(module, delta, dnorm, mask, centers, gamma, *weights)
+    with torch.no_grad():
+        return tuple(_run_forward(module, delta, dnorm, mask, centers, gamma,
+                                  [w.contiguous() for w in weights]))

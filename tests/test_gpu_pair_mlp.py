@@ -1,7 +1,8 @@
 """mf_pair_mlp_bias (the factorized geometry-bias MLPs in one pass) against SimplicialGeometryBias's torch
 formulation: the reference-fixture module and a configs[1]-sized batch.  Bar: fp32 MFMA against the fp32 torch
 GEMMs, max |difference| <= 1e-5 relative to the largest |term| per head (measured ~1e-6); the diagonal and the
-invalid pairs exactly zero."""
+invalid pairs exactly zero.  Its weight backward (mf_pair_mlp_bias_bwd) against float64 autograd of the torch
+formulation, normwise 2e-5 per gradient, and bitwise repeatable."""
 
 import numpy as np
 import pytest
@@ -79,17 +80,89 @@ def test_configs_sized_batch_matches_torch(cuda, B, N, hidden, H, R):
     assert all(torch.isfinite(t).all() for t in got)
 
 
-def test_grad_calls_take_the_torch_path(cuda):
-    z = np.load(fx.GOLDEN)
-    feats = _to(_features(z), cuda)
-    torch.manual_seed(0)
-    module = SimplicialGeometryBias(4, edge_bias_hidden_dim=16).to(cuda)
-    module._compute_factorized_terms(feats)
-    assert not pair_mlp.serves(module, feats)  # grad enabled, parameters require grad
+def _trained_module(B, N, hidden, H, R, seed):
+    """A SimplicialGeometryBias with materialised, non-zero layers and its non-periodic features (CPU)."""
+    gen = torch.Generator().manual_seed(seed)
+    counts = torch.randint(max(2, N // 3), N + 1, (B,), generator=gen)
+    pad = torch.arange(N)[None, :] >= counts[:, None]
+    coords = torch.randn(B, N, 3, generator=gen) * 1.4
+    torch.manual_seed(seed)
+    module = SimplicialGeometryBias(H, edge_bias_hidden_dim=hidden, edge_bias_n_rbf=R)
+    feats = NonPeriodicGeometryAdapter()(coords, pad_mask=pad)
     with torch.no_grad():
-        assert pair_mlp.serves(module, feats)
+        module._compute_factorized_terms(feats)  # materialise the LazyLinear layers
+        for mlp in (module.spoke_bias_u_mlp, module.spoke_bias_v_mlp, module.pair_bias_w_mlp):
+            mlp[2].weight.copy_(torch.randn(mlp[2].weight.shape, generator=gen) * 0.2)
+            mlp[2].bias.copy_(torch.randn(mlp[2].bias.shape, generator=gen) * 0.2)
+    ups = [torch.randn(B, H, N, N, generator=gen) for _ in range(3)]  # non-zero at invalid pairs too
+    return module, feats, coords, pad, ups
+
+
+def _weight_grads(module, feats, ups):
+    module.zero_grad(set_to_none=True)
     u, v, w = module._compute_factorized_terms(feats)
-    assert u.requires_grad  # autograd followed the torch formulation
+    ((u * ups[0]).sum() + (v * ups[1]).sum() + (w * ups[2]).sum()).backward()
+    return [p.grad.detach().clone() for m in (module.spoke_bias_u_mlp, module.spoke_bias_v_mlp,
+                                              module.pair_bias_w_mlp) for p in (m[0].weight, m[0].bias,
+                                                                               m[2].weight, m[2].bias)]
+
+
+@pytest.mark.parametrize("B,N,hidden,H,R", [(6, 48, 128, 8, 16), (3, 37, 64, 4, 28), (3, 20, 16, 16, 1)])
+def test_weight_gradients_match_float64_autograd(cuda, B, N, hidden, H, R):
+    """mf_pair_mlp_bias_bwd (through the autograd Function) against float64 autograd of the torch
+    formulation on the CPU: the 12 weight gradients of the u, v, w MLPs, normwise relative error <= 2e-5
+    per tensor (fp32 MFMA sums over the valid pairs; upstream gradients non-zero at invalid pairs and on the
+    diagonal, which must contribute nothing)."""
+    import copy
+
+    print(f"pair mlp bwd B={B} N={N} hidden={hidden} H={H} R={R}", flush=True)
+    module, feats, coords, pad, ups = _trained_module(B, N, hidden, H, R, seed=B * 7 + N)
+    ref_module = copy.deepcopy(module).double()
+    feats64 = GeometryFeatures(pair_delta=feats.pair_delta.double(), pair_dist=feats.pair_dist.double(),
+                               pair_dist2=feats.pair_dist2.double(), pair_dist_norm=feats.pair_dist_norm.double(),
+                               pair_mask=feats.pair_mask, global_geom=feats.global_geom.double(), kind=feats.kind,
+                               extras=feats.extras)
+    want = _weight_grads(ref_module, feats64, [t.double() for t in ups])
+    module = module.to(cuda)
+    gfe = NonPeriodicGeometryAdapter()(coords.to(cuda), pad_mask=pad.to(cuda))
+    assert pair_mlp.serves(module, gfe)  # grad enabled: the kernel's autograd Function
+    got = _weight_grads(module, gfe, [t.to(cuda) for t in ups])
+    torch.cuda.synchronize()
+    for k, (g, r) in enumerate(zip(got, want)):
+        g, r = g.cpu().double(), r.double()
+        rel = float((g - r).norm() / r.norm().clamp_min(1e-30))
+        assert rel <= 2e-5, (k, rel)
+
+
+def test_weight_gradients_are_bitwise_deterministic(cuda):
+    module, feats, coords, pad, ups = _trained_module(4, 40, 128, 8, 16, seed=5)
+    module = module.to(cuda)
+    gfe = NonPeriodicGeometryAdapter()(coords.to(cuda), pad_mask=pad.to(cuda))
+    ups = [t.to(cuda) for t in ups]
+    first = _weight_grads(module, gfe, ups)
+    second = _weight_grads(module, gfe, ups)
+    assert all(torch.equal(a, b) for a, b in zip(first, second))
+
+
+def test_grad_calls_outside_the_backward_take_the_torch_path(cuda):
+    """Features that take gradients, or 29 rbf features, under autograd: the torch formulation."""
+    module, feats, coords, pad, ups = _trained_module(2, 20, 16, 4, 16, seed=9)
+    module = module.to(cuda)
+    gfe = NonPeriodicGeometryAdapter()(coords.to(cuda), pad_mask=pad.to(cuda))
+    assert pair_mlp.serves(module, gfe)
+    d = gfe.pair_dist_norm.clone().requires_grad_(True)
+    g2 = GeometryFeatures(pair_delta=gfe.pair_delta, pair_dist=gfe.pair_dist, pair_dist2=gfe.pair_dist2,
+                          pair_dist_norm=d, pair_mask=gfe.pair_mask, global_geom=gfe.global_geom, kind=gfe.kind,
+                          extras=gfe.extras)
+    assert not pair_mlp.serves(module, g2)
+    with torch.no_grad():
+        assert pair_mlp.serves(module, g2)
+    m29, f29, c29, p29, _ = _trained_module(2, 20, 16, 4, 29, seed=10)
+    m29 = m29.to(cuda)
+    g29 = NonPeriodicGeometryAdapter()(c29.to(cuda), pad_mask=p29.to(cuda))
+    assert not pair_mlp.serves(m29, g29)
+    with torch.no_grad():
+        assert pair_mlp.serves(m29, g29)
 
 
 def test_bias_feeds_hip_attention(cuda):
