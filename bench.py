@@ -398,11 +398,38 @@ def measure_pair_mlp() -> dict:
     nbytes = 3 * B * H * N * N * 4 + B * N * N * (4 * 4 + 1)
     gbs = nbytes / (ms * 1e-3) / 1e9
     flops = valid * 2 * (2 * (19 * hidden + hidden * H) + (16 * hidden + hidden * H))
+
+    # a training step through the MLPs: forward, a loss over u, v, w, backward to the 12 weights
+    # (mf_pair_mlp_bias_bwd through the autograd Function), against the same step on the torch formulation
+    gen = torch.Generator().manual_seed(8)
+    ups = [torch.randn(B, H, N, N, generator=gen).to(dev) for _ in range(3)]
+    params = [p for m in (module.spoke_bias_u_mlp, module.spoke_bias_v_mlp, module.pair_bias_w_mlp)
+              for p in m.parameters()]
+
+    def train_kernel():
+        u, v, w = module._compute_factorized_terms(feats)
+        torch.autograd.grad((u * ups[0]).sum() + (v * ups[1]).sum() + (w * ups[2]).sum(), params)
+
+    def train_torch():
+        spoke, pairf = module._build_spoke_features(feats), module._build_pair_features(feats)
+        mask = feats.pair_mask[:, None].float()
+        u, v, w = (module._zero_pairwise_diag(mlp(f).permute(0, 3, 1, 2).contiguous()) * mask
+                   for mlp, f in ((module.spoke_bias_u_mlp, spoke), (module.spoke_bias_v_mlp, spoke),
+                                  (module.pair_bias_w_mlp, pairf)))
+        torch.autograd.grad((u * ups[0]).sum() + (v * ups[1]).sum() + (w * ups[2]).sum(), params)
+
+    if not pair_mlp.serves(module, feats):
+        raise RuntimeError("mf_pair_mlp_bias_bwd does not serve the bench configuration")
+    train_ms, _ = timed_loop(torch.cuda.current_stream(), train_kernel, 10, 3)
+    torch_ms, _ = timed_loop(torch.cuda.current_stream(), train_torch, 3, 1)
     return {"ms": round(ms, 5), "batch": B, "atoms": N, "heads": H, "hidden": hidden, "rbf": 16,
             "valid_pairs": valid, "bytes": nbytes, "valid_gflop": round(flops / 1e9, 3),
             "valid_tflops_fp32": round(flops / (ms * 1e-3) / 1e12, 2),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "train_step_ms": round(train_ms, 4), "train_step_torch_ms": round(torch_ms, 4),
+            "train_step": "forward + loss over u, v, w + backward to the MLP weights (mf_pair_mlp_bias_bwd), "
+                          "eager; torch: the same step on the torch formulation on the GPU"}
 
 
 def measure_trunk() -> dict:
