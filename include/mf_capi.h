@@ -540,9 +540,9 @@ int mf_heads_to_rows(const mf_heads_to_rows_args* args, void* stream);
 /*   u = MLP_u(x_s), v = MLP_v(x_s), w = MLP_w(x_p),                          */
 /*   MLP(x)    = W2 SiLU(W1 x + b1) + b2   (H outputs),                       */
 /* written as [B, H, N, N] fp32 with the diagonal and the pairs outside      */
-/* pair_mask zero.  W1 [hidden, F] row-major (F = 3 + R or R), W2 [H, hidden]. */
-/* fp32 throughout (fp32 MFMA).  R <= 29, hidden a multiple of 16 <= 256,    */
-/* H <= 16.                                                                   */
+/* pair_mask zero.  W1 [hidden, F] row-major (F = 3 + R or R, + the periodic */
+/* features below), W2 [H, hidden].  fp32 throughout (fp32 MFMA).  R <= 29,  */
+/* hidden a multiple of 16 <= 256, H <= 16; periodic spoke features <= 80.  */
 /* ------------------------------------------------------------------------ */
 typedef struct mf_pair_mlp_args {
   const float* pair_delta;      /* [B, N, N, 3]                               */
@@ -570,6 +570,12 @@ typedef struct mf_pair_mlp_args {
   int32_t rbf;
   int32_t hidden;
   int32_t heads;
+  /* ABI 11: the periodic features of use_periodic_features (transformer.py:641-652), forward only: the  */
+  /* spoke input gains, for each delta component c, sin and cos of (2 pi delta_c) freqs[k] (k < n_freqs), */
+  /* then global_geom[b] (6); the pair input gains global_geom[b].  n_freqs = 0 and NULLs: none.          */
+  int32_t n_freqs;
+  const float* freqs;           /* [n_freqs]       */
+  const float* global_geom;     /* [B, 6]          */
 } mf_pair_mlp_args;
 
 int mf_pair_mlp_bias(const mf_pair_mlp_args* args, void* stream);

@@ -211,7 +211,8 @@ class MfPairMlpArgs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ("pair_delta", "pair_dist_norm", "pair_mask", "rbf_centers")] + [
         ("rbf_gamma", ctypes.c_float)] + [(f"{m}_{t}", ctypes.c_void_p) for m in "uvw" for t in ("w1", "b1", "w2", "b2")] + [
         (n, ctypes.c_void_p) for n in ("u_out", "v_out", "w_out")] + [
-        (n, ctypes.c_int32) for n in ("batch", "atoms", "rbf", "hidden", "heads")]
+        (n, ctypes.c_int32) for n in ("batch", "atoms", "rbf", "hidden", "heads")] + [
+        ("n_freqs", ctypes.c_int32), ("freqs", ctypes.c_void_p), ("global_geom", ctypes.c_void_p)]
 
 
 class MfPairMlpBwdArgs(ctypes.Structure):

@@ -52,6 +52,10 @@ struct Params {
   const float* b2[3];
   float* out[3];
   int B, N, R, hidden, heads, groups;
+  // periodic features (PER instantiations): nf Fourier frequencies, the molecule's 6 global features
+  int nf;
+  const float* freqs;
+  const float* glob;
 };
 
 __device__ __forceinline__ mf_f32x4 mma(float a, float b, mf_f32x4 c) {
@@ -108,9 +112,30 @@ __device__ __forceinline__ mf_f32x4 mlp16(const float (&x)[K], const float* W1, 
   return o2;
 }
 
-// K4: 4-wide K steps of layer 1 for the spoke (u, v) and pair (w) features.
-template <int KS, int KP>
-__global__ void __launch_bounds__(kThreads, 4) pair_mlp_kernel(Params p) {
+// Spoke feature f of a pair under PER (transformer.py:641-652; geometry_bias's _periodic_terms): the delta,
+// rbf, then for each delta component c the sines and cosines of (2 pi delta_c) freq_k, then the 6 global
+// features of the molecule.
+__device__ __forceinline__ float periodic_spoke(const Params& p, int f, float d0, float d1, float d2, float rbf,
+                                                int b) {
+  const int fb = 3 + p.R, ff = fb + 6 * p.nf;
+  if (f < 3) return f == 0 ? d0 : (f == 1 ? d1 : d2);
+  if (f < fb) return rbf;
+  if (f < ff) {
+    const int idx = f - fb, c = idx / (2 * p.nf), rem = idx - c * 2 * p.nf;
+    const bool sn = rem < p.nf;
+    const float dc = c == 0 ? d0 : (c == 1 ? d1 : d2);
+    const float arg = (6.28318530717958647692f * dc) * p.freqs[sn ? rem : rem - p.nf];
+    float sv, cv;
+    sincosf(arg, &sv, &cv);
+    return sn ? sv : cv;
+  }
+  if (f < ff + 6) return p.glob[size_t(b) * 6 + (f - ff)];
+  return 0.0f;
+}
+
+// K4: 4-wide K steps of layer 1 for the spoke (u, v) and pair (w) features; PER adds the periodic ones.
+template <int KS, int KP, bool PER>
+__global__ void __launch_bounds__(kThreads, PER ? 1 : 4) pair_mlp_kernel(Params p) {  // PER: ~128 KB of LDS
   extern __shared__ float lds[];
   const int hidden = p.hidden, H = p.heads;
   const int HT = hidden / 16;
@@ -133,7 +158,7 @@ __global__ void __launch_bounds__(kThreads, 4) pair_mlp_kernel(Params p) {
   }
   const int tid = threadIdx.x;
   for (int m = 0; m < 3; ++m) {
-    const int fin = m < 2 ? 3 + p.R : p.R;  // true input width
+    const int fin = m < 2 ? 3 + p.R + (PER ? 6 * p.nf + 6 : 0) : p.R + (PER ? 6 : 0);  // true input width
     const int s1 = m < 2 ? s1s : s1p;
     const int kw = 4 * (m < 2 ? KS : KP);
     for (int e = tid; e < hidden * kw; e += kThreads) {
@@ -216,18 +241,36 @@ __global__ void __launch_bounds__(kThreads, 4) pair_mlp_kernel(Params p) {
       const size_t pair = prow + (jvalid ? jc : 0);
       const float dn = jvalid ? p.dnorm[pair] : 0.0f;
       float xs[KS], xp[KP];
+      if constexpr (PER) {
+        const float d0 = jvalid ? p.delta[3 * pair] : 0.0f;
+        const float d1 = jvalid ? p.delta[3 * pair + 1] : 0.0f;
+        const float d2 = jvalid ? p.delta[3 * pair + 2] : 0.0f;
 #pragma unroll
-      for (int t = 0; t < KS; ++t) {
-        const int f = 4 * t + g;
-        const float d = dn - cs[t];
-        const float rbf = __builtin_amdgcn_exp2f(kexp * (d * d));
-        xs[t] = f < 3 ? (jvalid ? p.delta[3 * pair + f] : 0.0f) : (f < 3 + p.R ? rbf : 0.0f);
-      }
+        for (int t = 0; t < KS; ++t) {
+          const float d = dn - cs[t];
+          xs[t] = periodic_spoke(p, 4 * t + g, d0, d1, d2, __builtin_amdgcn_exp2f(kexp * (d * d)), b);
+        }
 #pragma unroll
-      for (int t = 0; t < KP; ++t) {
-        const int f = 4 * t + g;
-        const float d = dn - cp[t];
-        xp[t] = f < p.R ? __builtin_amdgcn_exp2f(kexp * (d * d)) : 0.0f;
+        for (int t = 0; t < KP; ++t) {
+          const int f = 4 * t + g;
+          const float d = dn - cp[t];
+          xp[t] = f < p.R ? __builtin_amdgcn_exp2f(kexp * (d * d))
+                          : (f < p.R + 6 ? p.glob[size_t(b) * 6 + (f - p.R)] : 0.0f);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+          const int f = 4 * t + g;
+          const float d = dn - cs[t];
+          const float rbf = __builtin_amdgcn_exp2f(kexp * (d * d));
+          xs[t] = f < 3 ? (jvalid ? p.delta[3 * pair + f] : 0.0f) : (f < 3 + p.R ? rbf : 0.0f);
+        }
+#pragma unroll
+        for (int t = 0; t < KP; ++t) {
+          const int f = 4 * t + g;
+          const float d = dn - cp[t];
+          xp[t] = f < p.R ? __builtin_amdgcn_exp2f(kexp * (d * d)) : 0.0f;
+        }
       }
       for (int m = 0; m < 3; ++m) {
         const mf_f32x4 o2 = m < 2 ? mlp16<KS>(xs, lds + off[m][0], lds + off[m][1], lds + off[m][2],
@@ -261,15 +304,17 @@ size_t lds_bytes(int ks, int kp, int hidden) {
   return floats * sizeof(float);
 }
 
-template <int KS, int KP>
-int launch(const Params& p, int num_cus, hipStream_t s) {
+template <int KS, int KP, bool PER>
+int launch(const Params& p, int num_cus, int max_lds, hipStream_t s) {
   const size_t lds = lds_bytes(KS, KP, p.hidden);
+  if (lds > size_t(max_lds))
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: weights exceed the LDS of a workgroup");
   // dynamic LDS above 64 KB needs the attribute (once per kernel and device)
-  const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(pair_mlp_kernel<KS, KP>), 160 * 1024);
+  const int st = ensure_dynamic_lds(reinterpret_cast<const void*>(pair_mlp_kernel<KS, KP, PER>), 160 * 1024);
   if (st != MF_OK) return st;
   const long long units = (long long)p.B * p.N * p.groups;
   const int grid = int(std::min<long long>((units + 7) / 8, (long long)num_cus * 2));
-  hipLaunchKernelGGL((pair_mlp_kernel<KS, KP>), dim3(grid), dim3(kThreads), lds, s, p);
+  hipLaunchKernelGGL((pair_mlp_kernel<KS, KP, PER>), dim3(grid), dim3(kThreads), lds, s, p);
   MF_HIP_CHECK(hipGetLastError());
   return MF_OK;
 }
@@ -534,13 +579,26 @@ extern "C" int mf_pair_mlp_bias(const mf_pair_mlp_args* a, void* stream) {
   p.groups = (a->atoms + 63) / 64;
   if ((long long)a->batch * a->atoms * (p.groups + 1) > 0x7fffffffLL)
     return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: batch * atoms * ceil(atoms / 64) must stay below 2^31");
-  const int ks = (3 + a->rbf + 3) / 4, kp = (a->rbf + 3) / 4;
-  if (lds_bytes(ks, kp, a->hidden) > size_t(dev.max_lds_per_block))
-    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: weights exceed the LDS of a workgroup");
+  const bool per = a->n_freqs > 0 || a->global_geom != nullptr;
+  if (per) {
+    if (a->n_freqs < 1 || !a->freqs || !a->global_geom)
+      return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias: periodic features need n_freqs >= 1, freqs and "
+                                           "global_geom");
+    p.nf = a->n_freqs;
+    p.freqs = a->freqs;
+    p.glob = a->global_geom;
+  }
+  // spoke K steps (3 + R features, + 6 n_freqs + 6 periodic) and pair K steps (R, + 6 periodic)
+  const int ks = (3 + a->rbf + (per ? 6 * a->n_freqs + 6 : 0) + 3) / 4, kp = (a->rbf + (per ? 6 : 0) + 3) / 4;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // spoke K steps (3 + R features) and pair K steps (R features)
-  if (ks <= 5 && kp <= 4) return launch<5, 4>(p, dev.num_cus, s);
-  return launch<8, 8>(p, dev.num_cus, s);
+  if (per) {
+    if (ks > 20 || kp > 9)
+      return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias: periodic spoke features must be at most 80 (3 + R + "
+                                      "6 n_freqs + 6) and pair features at most 36");
+    return launch<20, 9, true>(p, dev.num_cus, dev.max_lds_per_block, s);
+  }
+  if (ks <= 5 && kp <= 4) return launch<5, 4, false>(p, dev.num_cus, dev.max_lds_per_block, s);
+  return launch<8, 8, false>(p, dev.num_cus, dev.max_lds_per_block, s);
 }
 
 extern "C" uint64_t mf_pair_mlp_bias_bwd_workspace_size(int32_t hidden) {
@@ -568,6 +626,8 @@ extern "C" int mf_pair_mlp_bias_bwd(const mf_pair_mlp_bwd_args* a, void* stream)
       return fail(MF_ERR_INVALID_ARGUMENT,
                   "mf_pair_mlp_bias_bwd: every weight, upstream gradient and weight gradient must be non-NULL");
   if (f.batch < 0 || f.atoms < 0) return fail(MF_ERR_INVALID_ARGUMENT, "mf_pair_mlp_bias_bwd: bad sizes");
+  if (f.n_freqs != 0 || f.global_geom != nullptr)
+    return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias_bwd: periodic features are forward-only");
   if (f.rbf < 1 || f.rbf > kMaxRbf - 1)
     return fail(MF_ERR_UNSUPPORTED, "mf_pair_mlp_bias_bwd: rbf features must be in [1, 28]");
   if (f.hidden < 16 || f.hidden > kBwdMaxHidden || f.hidden % 16 != 0)

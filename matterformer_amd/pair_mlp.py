@@ -3,9 +3,11 @@
 the MLP weights take gradients, its weight backward as one mf_pair_mlp_bias_bwd pass (an autograd Function).
 
 Served: GPU features, fp32 weights and features, materialised LazyLinear layers (their first call runs the
-torch formulation, which draws their weights in the reference's order), non-periodic spoke features (no
-Fourier / global terms), rbf <= 29, hidden a multiple of 16 <= 256, heads <= 16; under autograd also rbf <= 28,
-hidden <= 128 and features that take no gradient.  Everything else takes the torch formulation.
+torch formulation, which draws their weights in the reference's order), rbf <= 29, hidden a multiple of 16
+<= 256, heads <= 16, and with use_periodic_features on periodic features (Fourier terms of the pair delta and
+the cell's global features, transformer.py:641-652) at most 80 spoke inputs; under autograd also rbf <= 28,
+hidden <= 128, non-periodic features and features that take no gradient.  Everything else takes the torch
+formulation.
 """
 
 from __future__ import annotations
@@ -35,6 +37,10 @@ def _trains(module, geom_features) -> bool:
                                         or g.pair_delta.requires_grad or g.pair_dist_norm.requires_grad)
 
 
+def _periodic(module, geom_features) -> bool:
+    return bool(module.use_periodic_features) and geom_features.kind == "periodic"
+
+
 def serves(module, geom_features) -> bool:
     g = geom_features
     if g.pair_delta.device.type != "cuda":
@@ -42,8 +48,6 @@ def serves(module, geom_features) -> bool:
     mlps = _mlps(module)
     params = [prm for m in mlps for prm in m.parameters()]
     if any(isinstance(prm, UninitializedParameter) for prm in params):
-        return False
-    if module.use_periodic_features and g.kind == "periodic":
         return False
     if not isinstance(mlps[0][1], torch.nn.SiLU):
         return False
@@ -53,22 +57,32 @@ def serves(module, geom_features) -> bool:
         return False
     if any(m[0].out_features != hidden or m[0].bias is None or m[2].bias is None for m in mlps):
         return False
-    if mlps[0][0].in_features != 3 + R or mlps[1][0].in_features != 3 + R or mlps[2][0].in_features != R:
+    per = _periodic(module, g)
+    nf = int(module._edge_freqs.numel()) if per else 0
+    fs, fp = 3 + R + (6 * nf + 6 if per else 0), R + (6 if per else 0)
+    if mlps[0][0].in_features != fs or mlps[1][0].in_features != fs or mlps[2][0].in_features != fp:
+        return False
+    if per and (fs > 80 or fp > 36 or g.global_geom.shape != (g.pair_delta.shape[0], 6)
+                or g.global_geom.dtype != torch.float32):
         return False
     tensors = [g.pair_delta, g.pair_dist_norm] + params
     if not all(t.dtype == torch.float32 for t in tensors):
         return False
     if _trains(module, g):
-        # the weight backward: features without gradient, R <= 28, hidden <= 128
-        if g.pair_delta.requires_grad or g.pair_dist_norm.requires_grad:
+        # the weight backward: non-periodic features without gradient, R <= 28, hidden <= 128
+        if per or g.pair_delta.requires_grad or g.pair_dist_norm.requires_grad:
             return False
         return R <= 28 and hidden <= 128
     return True
 
 
-def _forward_args(module, delta, dnorm, mask, centers, gamma, weights, outs):
+def _forward_args(module, delta, dnorm, mask, centers, gamma, weights, outs, periodic=None):
+    """periodic: None, or (freqs [nf], global_geom [B, 6]) fp32 contiguous."""
     B, N = delta.shape[:2]
     fields = {}
+    if periodic is not None:
+        fields.update(n_freqs=int(periodic[0].numel()), freqs=periodic[0].data_ptr(),
+                      global_geom=periodic[1].data_ptr())
     for idx, name in enumerate("uvw"):
         for k, key in enumerate(("w1", "b1", "w2", "b2")):
             fields[f"{name}_{key}"] = weights[4 * idx + k].data_ptr()
@@ -90,12 +104,12 @@ def _inputs(module, geom_features):
     return delta, dnorm, mask, centers, float(module._edge_rbf_gamma_value)
 
 
-def _run_forward(module, delta, dnorm, mask, centers, gamma, weights):
+def _run_forward(module, delta, dnorm, mask, centers, gamma, weights, periodic=None):
     B, N = delta.shape[:2]
     H = int(weights[2].shape[0])
     dev = delta.device
     outs = [torch.empty(B, H, N, N, device=dev, dtype=torch.float32) for _ in range(3)]
-    args = _forward_args(module, delta, dnorm, mask, centers, gamma, weights, outs)
+    args = _forward_args(module, delta, dnorm, mask, centers, gamma, weights, outs, periodic)
     with torch.cuda.device(dev):
         _native.check(_native.lib().mf_pair_mlp_bias(args, _native.current_stream(dev)), "mf_pair_mlp_bias")
     return outs
@@ -148,6 +162,11 @@ def factorized_terms(module, geom_features):
     weights = _weights(module)
     if _trains(module, geom_features):
         return _PairMlpFunction.apply(module, delta, dnorm, mask, centers, gamma, *weights)
+    periodic = None
+    if _periodic(module, geom_features):
+        dev = delta.device
+        periodic = (module._edge_freqs.to(device=dev, dtype=torch.float32).contiguous(),
+                    geom_features.global_geom.detach().to(device=dev, dtype=torch.float32).contiguous())
     with torch.no_grad():
         return tuple(_run_forward(module, delta, dnorm, mask, centers, gamma,
-                                  [w.contiguous() for w in weights]))
+                                  [w.contiguous() for w in weights], periodic))

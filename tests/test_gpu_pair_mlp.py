@@ -191,3 +191,37 @@ def test_bias_feeds_hip_attention(cuda):
     valid = ~pad
     rel = float((got.cpu()[valid] - want[valid]).norm() / want[valid].norm())
     assert rel <= 1e-4, rel
+
+
+@pytest.mark.parametrize("n_freqs,R", [(8, 16), (2, 5)])
+def test_periodic_features_match_torch(cuda, n_freqs, R):
+    """use_periodic_features on periodic features (the MOF configuration): the spoke MLPs also read the
+    sines / cosines of (2 pi delta_c) freq_k and the cell's 6 global features, the pair MLP the global
+    features (transformer.py:641-652).  The same features on both sides (the CPU adapter's, copied to the
+    GPU); bar as above (sin / cos in fp32 on both sides)."""
+    from matterformer_amd.geometry import PeriodicGeometryAdapter
+
+    gen = torch.Generator().manual_seed(31 + n_freqs)
+    B, N, H = 2, 24, 4
+    frac = torch.rand(B, N, 3, generator=gen)
+    lattice = torch.cat([torch.rand(B, 3, generator=gen) * 0.6 + 2.0, torch.rand(B, 3, generator=gen) * 0.4 - 0.2],
+                        dim=-1)
+    pad = torch.zeros(B, N, dtype=torch.bool)
+    pad[1, 19:] = True
+    feats = PeriodicGeometryAdapter()(frac, pad_mask=pad, lattice=lattice)
+    torch.manual_seed(4)
+    module = SimplicialGeometryBias(H, mode="factorized", edge_bias_hidden_dim=64, edge_bias_n_rbf=R,
+                                    edge_bias_n_freqs=n_freqs, use_periodic_features=True)
+    with torch.no_grad():
+        module._compute_factorized_terms(feats)  # materialise the LazyLinear layers (periodic widths)
+        for mlp in (module.spoke_bias_u_mlp, module.spoke_bias_v_mlp, module.pair_bias_w_mlp):
+            mlp[2].weight.copy_(torch.randn(mlp[2].weight.shape, generator=gen) * 0.2)
+            mlp[2].bias.copy_(torch.randn(mlp[2].bias.shape, generator=gen) * 0.2)
+        want = module._compute_factorized_terms(feats)
+        module = module.to(cuda)
+        gfe = _to(feats, cuda)
+        assert pair_mlp.serves(module, gfe)
+        got = module._compute_factorized_terms(gfe)
+    torch.cuda.synchronize()
+    _check(got, want, feats.pair_mask)
+    assert not pair_mlp.serves(module, gfe)  # under autograd: the torch formulation (no periodic backward)
