@@ -66,18 +66,20 @@ namespace mf {
 namespace spair {
 
 // Waves per workgroup (4, two workgroups per CU: two waves on every SIMD, which the pair loop needs to
-// overlap MFMA and VALU), queries per unit and keys per staged block.  The bias instantiations stage 64-key
-// blocks, so that their bias operands fit beside a second workgroup's LDS.
+// overlap MFMA and VALU), queries per unit and keys per staged block.  The bias instantiations stage 80-key
+// blocks (molecules of up to 80 atoms in one block) with 32 staged query rows, so that their bias operands
+// fit beside a second workgroup's LDS.
 template <bool BIAS>
 struct Waves {
   static constexpr int kCount = 4;
   // queries per unit: 3 tiles; 2 with the bias, whose operands leave no room for a third at 256
   // registers per wave
   static constexpr int kGroup = BIAS ? 32 : 48;
-  static constexpr int kCap = BIAS ? 64 : 128;  // keys per staged block (one row per 2 or 4 threads)
+  static constexpr int kMaxQ = kGroup;          // staged query rows
+  static constexpr int kCap = BIAS ? 80 : 128;  // keys per staged block (a multiple of 16)
+  static constexpr int kPVW = (kCap + 31) / 32;  // pair-valid words per staged row
 };
 constexpr int kRedWaves = 4;          // partial-output slots of the final reduction
-constexpr int kMaxQ = 48;             // queries per unit
 constexpr int kMaxBatch = 256;        // molecules per launch
 constexpr int kMaxN = 512;            // tokens
 constexpr float kBoundLimit = 13.5f;  // fast path bound on |S| (log2 units)
@@ -142,6 +144,8 @@ template <int DP, bool BIAS>
 struct Lay {
   static constexpr int kWaves = Waves<BIAS>::kCount;
   static constexpr int kCap = Waves<BIAS>::kCap;
+  static constexpr int kMaxQ = Waves<BIAS>::kMaxQ;
+  static constexpr int kPVW = Waves<BIAS>::kPVW;
   static constexpr int RQ = Waves<BIAS>::kGroup;  // query rows of a reduction slot
   static constexpr int RB = DP * 2;  // bytes per staged fp16 row
   static constexpr int kK1 = 0;
@@ -149,8 +153,8 @@ struct Lay {
   static constexpr int kV1 = kK2 + kCap * RB;
   static constexpr int kV2 = kV1 + kCap * RB;
   static constexpr int kQ = kV2 + kCap * RB;
-  static constexpr int kPV = kQ + kMaxQ * RB;             // u32 [kCap][kCap / 32] pair-valid bits
-  static constexpr int kInfo = kPV + kCap * (kCap / 32) * 4;  // u32 [kMaxBatch] molecule info
+  static constexpr int kPV = kQ + kMaxQ * RB;             // u32 [kCap][kPVW] pair-valid bits
+  static constexpr int kInfo = kPV + kCap * kPVW * 4;     // u32 [kMaxBatch] molecule info
   static constexpr int kPre = kInfo + kMaxBatch * 4;     // int [kMaxBatch + 4] unit prefix by rank
   static constexpr int kOrder = kPre + (kMaxBatch + 4) * 4;  // u16 [kMaxBatch] molecule of each rank
   static constexpr int kKidx = kOrder + kMaxBatch * 2;   // u16 [kMaxN] valid key atoms
@@ -545,8 +549,8 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
       // valid keys 4g + r of rows j0 (bits_a) and j0 + 1 (bits_b)
       uint32_t bits_a = kmask, bits_b = last_odd ? 0u : kmask;
       if constexpr (HAS_PV) {
-        bits_a &= pvb[j0 * (kCap / 32) + pvword] >> pvshift;
-        bits_b &= pvb[(j0 + 1) * (kCap / 32) + pvword] >> pvshift;
+        bits_a &= pvb[j0 * Ly::kPVW + pvword] >> pvshift;
+        bits_b &= pvb[(j0 + 1) * Ly::kPVW + pvword] >> pvshift;
       }
       // GEMM1 for rows j0 and j0 + 1
       uint4 wa[NCH], wb[NCH];
@@ -575,8 +579,8 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
         const uint4 ab_b{g == 0 ? (0x3c00u | (w_b << 16)) : onehot.x, onehot.y, onehot.z, onehot.w};
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
-          const uint32_t u_a = *reinterpret_cast<const uint16_t*>(BU + (j0 * kMaxQ + 16 * qt + r16) * 2);
-          const uint32_t u_b = *reinterpret_cast<const uint16_t*>(BU + ((j0 + 1) * kMaxQ + 16 * qt + r16) * 2);
+          const uint32_t u_a = *reinterpret_cast<const uint16_t*>(BU + (j0 * Ly::kMaxQ + 16 * qt + r16) * 2);
+          const uint32_t u_b = *reinterpret_cast<const uint16_t*>(BU + ((j0 + 1) * Ly::kMaxQ + 16 * qt + r16) * 2);
           const uint4 bb_a{g == 0 ? (u_a | (cgh[qt] << 16)) : bvop[qt].x, bvop[qt].y, bvop[qt].z, bvop[qt].w};
           const uint4 bb_b{g == 0 ? (u_b | (cgh[qt] << 16)) : bvop[qt].x, bvop[qt].y, bvop[qt].z, bvop[qt].w};
           sa[qt] = mfma(ab_a, bb_a, sa[qt]);
@@ -718,6 +722,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   constexpr int kThreads = kWaves * 64;
   using Ly = Lay<DP, BIAS>;
   constexpr int kCap = Ly::kCap;
+  constexpr int kMaxQ = Ly::kMaxQ;
   constexpr int RB = Ly::RB;
   constexpr int NCH = Shape<DP>::NCH;
   constexpr int ND = Shape<DP>::ND;
@@ -749,7 +754,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   // u / CPR, columns 8 cc .. 8 cc + 7 with cc = tid % CPR for every i; only
   // the rows the pair loop reads (the valid ones rounded up to 16) are staged
   constexpr int CPR = DP / 8;                        // chunks per row
-  constexpr int MAXC = kCap * CPR / kThreads;        // chunks per thread and block
+  constexpr int MAXC = (kCap * CPR + kThreads - 1) / kThreads;  // chunks per thread and block
   constexpr int MAXQC = (kMaxQ * CPR + kThreads - 1) / kThreads;
   const int cc = tid % CPR;
   const int e0 = 8 * cc;
@@ -895,7 +900,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
 #pragma unroll
       for (int t = 0; t < kRB; ++t) val[t][0] = val[t][1] = 0u;
       if (rvalid <= 0 || cvalid <= 0) return;
-      const bool two = kCap > 64 && C > 64;  // a second column per lane (wave-uniform; never with 64-key blocks)
+      const bool two = kCap > 64 && C > 64;  // a second column per lane (wave-uniform)
       int ca[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) ca[s] = key_atom(cbase + min(lane + 64 * s, cvalid - 1));
@@ -1027,8 +1032,8 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     const uint8_t* gpv = p.pv + size_t(b) * N * N;
     const int j0 = jc * kCap, k0 = kc * kCap;
     const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
-    for (int u = tid; u < kCap * (kCap / 32); u += kThreads) {
-      const int jl = u / (kCap / 32), wd = u % (kCap / 32);
+    for (int u = tid; u < kCap * Ly::kPVW; u += kThreads) {
+      const int jl = u / Ly::kPVW, wd = u % Ly::kPVW;
       uint32_t bits = 0;
       if (jl < nkj) {
         const uint8_t* prow = gpv + size_t(key_atom(j0 + jl)) * N;
@@ -1705,7 +1710,7 @@ __device__ __forceinline__ void run_unit(const Params& p, unsigned char* smem, i
 // first; after that a workgroup that
 // finishes a unit claims the next position with one device-scope atomic, so
 // the workgroups that finish first take the longest remaining units.
-// BIAS: one workgroup per CU (its bias operands take another ~59 KB of LDS).
+// BIAS: its bias operands take another ~24 KB of LDS (two workgroups per CU still fit).
 template <typename T, int DP, bool HAS_PV, bool BIAS, bool STR>
 __global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, 2) simplicial_pair_kernel(Params p) {
   constexpr int W = Waves<BIAS>::kCount;

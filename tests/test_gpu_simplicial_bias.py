@@ -128,8 +128,9 @@ SHAPES = [
     # (B, H, N, D, counts, holes, pair_drop)
     (1, 2, 7, 8, [5], None, 0.2),
     (3, 2, 29, 32, [29, 17, 9], [(0, 3)], 0.0),
-    (2, 2, 70, 64, [70, 41], None, 0.1),      # two key chunks
-    (2, 1, 130, 64, [130, 64], [(1, 5)], 0.0),  # three key chunks
+    (2, 2, 70, 64, [70, 41], None, 0.1),      # more than 64 keys in one block
+    (2, 1, 81, 64, [81, 80], [(0, 7)], 0.1),  # a full 80-key block; 81 keys in two blocks (80 + 1)
+    (2, 1, 130, 64, [130, 64], [(1, 5)], 0.0),  # key blocks
     (2, 2, 33, 128, [33, 16], None, 0.0),
     (2, 2, 24, 20, [24, 11], [(1, 5)], 0.0),  # head_dim not a multiple of 8
 ]
