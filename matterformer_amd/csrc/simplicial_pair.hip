@@ -53,8 +53,11 @@
 // n_d = max_k |k2_k[d]|, |S_i[j,k]| <= U_i = sum_d |q'_i[d]| m_d n_d.  When
 // U_i <= kBoundLimit for every query of the unit (and the query scale is
 // representable), P = 2^S lies in [2^-U, 2^U], inside the normal fp16 range,
-// and softmax is invariant to the missing offset.  Otherwise the unit takes
-// two passes: the exact maximum m_i of the valid logits (GEMM1 only), then
+// and softmax is invariant to the missing offset.  Otherwise a single-block
+// unit whose bounds are at most kShiftMax first takes one shifted pass,
+// P = 2^(S - m_i) with m_i = max(U_i - kShiftTop, 0), kept when every shifted
+// query's denominator reaches kMinMass.  Failing that, the unit takes two
+// passes: the exact maximum m_i of the valid logits (GEMM1 only), then
 // P = 2^(S - m_i) with S rescaled to log2 units (the query scale is then
 // normalised on its own: sq = 1 - exponent(max|q'|)).
 #include <cmath>
@@ -84,6 +87,14 @@ constexpr int kMaxBatch = 256;        // molecules per launch
 constexpr int kMaxN = 512;            // tokens
 constexpr float kBoundLimit = 13.5f;  // fast path bound on |S| (log2 units)
 constexpr float kQLimit = 8192.0f;    // fast path bound on max |Qs|
+// Shifted one-pass mode (a unit past the fast-path bound, single key block): query i takes the offset
+// m_i = max(B_i - kShiftTop, 0) from its own bound |S| <= B_i (log2 units), so every 2^(S - m_i) <= 2^14 fits
+// fp16; the pass is kept when every shifted query's denominator reaches kMinMass (then terms lost to fp16
+// underflow, at most one 2^-25 per pair, stay below 2^-10 of it), else the unit reruns the exact two-pass
+// way.  Bounds above kShiftMax (masking-scale terms) go to the two-pass way at once.
+constexpr float kShiftTop = 14.0f;
+constexpr float kShiftMax = 32.0f;
+constexpr float kMinMass = 0.25f;
 
 enum Mode { kFast = 0, kSlow = 1, kMax = 2 };
 
@@ -165,7 +176,7 @@ struct Lay {
   static constexpr int kCol = kQidx + kMaxN * 2;
   static constexpr int kMn = kCol + (kColBytes > kWaves * kMaxQ * 4 ? kColBytes : kWaves * kMaxQ * 4);
   static constexpr int kG = kMn + DP * 4;       // float [kWaves][4] |V1|, |V2|, |q| maxima
-  static constexpr int kScal = kG + kWaves * 4 * 4;  // int [8] scale exponents, slow flag
+  static constexpr int kScal = kG + kWaves * 4 * 4;  // int [8] scale exponents, slow flag, no-shift flag
   static constexpr int kM = kScal + 8 * 4;      // float [kMaxQ] two-pass maxima (log2 units)
   static constexpr int kClaim = kM + kMaxQ * 4;  // ClaimState
   static constexpr int kTotal = kClaim + int(sizeof(ClaimState));
@@ -1211,6 +1222,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       scal[4] = sq;
       scal[5] = E;
       scal[6] = E != 0 ? 1 : 0;  // two-pass flag (queries add theirs)
+      scal[7] = E != 0 ? 1 : 0;  // no shifted one-pass (queries add theirs)
     }
   }
   if (!staged) __syncthreads();
@@ -1267,6 +1279,9 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         if (row < nqg) ub += fabsf(cgf[row]) * bias_mag;
       }
       if (row < nqg && cc == 0 && !(ub <= kBoundLimit)) atomicOr(&scal[6], 1);
+      if (row < nqg && cc == 0 && !(ub <= kShiftMax)) atomicOr(&scal[7], 1);
+      // the query's offset in the shifted one-pass mode (0 for padded rows)
+      if (cc == 0 && row < 16 * QT) s_m[row] = row < nqg ? fmaxf(ub - kShiftTop, 0.0f) : 0.0f;
     }
   }
 
@@ -1374,9 +1389,45 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     if (!slow) {
       pair_loop_n<DP, kFast, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
     } else {
-      pair_loop_n<DP, kMax, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
-      finish_max();
-      pair_loop_n<DP, kSlow, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+      bool exact = staged || scal[7] != 0;
+      if (!exact) {
+        // shifted one pass, then every wave sums the waves' denominators of all queries (the same
+        // values in every wave, so every wave takes the same branch)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) negm[qt] = -s_m[16 * qt + r16];
+        pair_loop_n<DP, kSlow, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+        float* redm = colmax;  // [kWaves][kMaxQ]
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+          if (g == 0) redm[wave * kMaxQ + 16 * qt + r16] = L[qt][0];
+        __syncthreads();
+        bool low = false;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          float l = 0.0f;
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) l += redm[w * kMaxQ + 16 * qt + r16];
+          const int q = 16 * qt + r16;
+          low |= q < nqg && s_m[q] > 0.0f && !(l >= kMinMass);
+        }
+        exact = __any(low);
+        if (exact) {
+          __syncthreads();  // every wave has read the denominators before finish_max reuses the area
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            L[qt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+            mloc[qt] = -INFINITY;
+            negm[qt] = 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) O[dt][qt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      }
+      if (exact) {
+        pair_loop_n<DP, kMax, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+        finish_max();
+        pair_loop_n<DP, kSlow, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+      }
     }
   } else if (MULTI && nch > 1) {
     __syncthreads();

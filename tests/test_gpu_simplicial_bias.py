@@ -232,6 +232,48 @@ def test_16bit_dominant_pair_bias_near_fp16_limit(cuda):
     assert worst <= ROW_BAR
 
 
+def _small_logit_case(B, H, N, D, seed, counts):
+    """q scaled by 0.1, so that the logit bound of a query is about 9 log2 units and the bias decides whether
+    a unit stays within the one-pass bound (13.5), takes the shifted one pass (bound <= 32) or neither."""
+    case = list(random_simplicial(B, H, N, D, seed=seed, counts=counts, std=logit_std(D)))
+    case[0] = case[0] * 0.1
+    return tuple(case)
+
+
+def test_16bit_shifted_one_pass_matches_fp64(cuda):
+    """Bias N(0, 0.5^2), gates N(0, 1): queries with large gates put their units past the one-pass bound but
+    below the shifted pass's cap; the shifted pass (offset max(B_i - 14, 0) per query) keeps them.  Every
+    valid query row against float64, and the lse, which carries each query's offset."""
+    B, H, N, D = 3, 4, 45, 64
+    case = _small_logit_case(B, H, N, D, 47, [45, 33, 12])
+    tm = make_terms(B, H, N, D, seed=48)
+    out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc")
+    ref, ref_lse = oracle(case, tm, torch.bfloat16)
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+    worst = row_errors(out32.cpu().numpy(), ref, case[5]).max()
+    print(f"shifted one pass: worst row {worst:.3e}", flush=True)
+    assert worst <= ROW_BAR
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
+def test_16bit_shifted_pass_falls_back_when_its_denominators_underflow(cuda):
+    """u = -12 on every pair, v = w = 0, gate 1: c u = -17.3 log2 units, so each query's bound (~26) is past
+    the one-pass bound and below the shifted pass's cap, but the bound's offset leaves every 2^(S - m_i) near
+    2^-21: the denominators stay far below the pass's floor and the unit reruns the exact two-pass way.  The
+    constant cancels in the softmax; output and lse against float64."""
+    B, H, N, D = 2, 2, 41, 64
+    case = _small_logit_case(B, H, N, D, 46, [41, 26])
+    tm = {"bias": [torch.full((B, H, N, N), -12.0), torch.zeros(B, H, N, N), torch.zeros(B, H, N, N),
+                   torch.ones(B, H, N)]}
+    out, lse, out32 = run(case, tm, cuda, torch.bfloat16, "bf16_tc")
+    ref, ref_lse = oracle(case, tm, torch.bfloat16)
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+    worst = row_errors(out32.cpu().numpy(), ref, case[5]).max()
+    print(f"shifted pass fallback: worst row {worst:.3e}", flush=True)
+    assert worst <= ROW_BAR
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
 def test_fp32_bias_with_bf16_operands(cuda):
     """The module passes the bias in its own dtype: fp32 bias with bf16 operands."""
     case = random_simplicial(2, 2, 40, 64, seed=3, counts=[40, 21], std=logit_std(64))
