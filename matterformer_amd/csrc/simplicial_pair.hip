@@ -91,9 +91,10 @@ constexpr float kQLimit = 8192.0f;    // fast path bound on max |Qs|
 // m_i = max(B_i - kShiftTop, 0) from its own bound |S| <= B_i (log2 units), so every 2^(S - m_i) <= 2^14 fits
 // fp16; the pass is kept when every shifted query's denominator reaches kMinMass (then terms lost to fp16
 // underflow, at most one 2^-25 per pair, stay below 2^-10 of it), else the unit reruns the exact two-pass
-// way.  Bounds above kShiftMax (masking-scale terms) go to the two-pass way at once.
+// way.  Bounds above kShiftMax (large or masking-scale terms, whose shifted pass mostly fails and costs a
+// pass) go to the two-pass way at once.
 constexpr float kShiftTop = 14.0f;
-constexpr float kShiftMax = 32.0f;
+constexpr float kShiftMax = 24.0f;
 constexpr float kMinMass = 0.25f;
 
 enum Mode { kFast = 0, kSlow = 1, kMax = 2 };
