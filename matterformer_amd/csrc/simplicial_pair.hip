@@ -1774,7 +1774,7 @@ __global__ void __launch_bounds__(Waves<BIAS>::kCount * 64, 2) simplicial_pair_k
   ClaimState* cl = reinterpret_cast<ClaimState*>(smem + Ly::kClaim);
   __shared__ int s_first;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
   const int B = p.B;
   const int G = gridDim.x;
   const int wg = blockIdx.x;

@@ -87,6 +87,22 @@ def test_16bit_matches_fp64_oracle(cuda, shape, dtype):
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("D, qscale", [(64, 0.2), (32, 0.3)], ids=["D64", "D32"])
+def test_16bit_shifted_one_pass_matches_fp64(cuda, dtype, D, qscale):
+    """q scaled so that each query's logit bound sum_d |q_d| max|k1_d| max|k2_d| is about 18 log2 units:
+    past the one-pass bound (13.5) and within the shifted pass's cap (24), whose per-query offset
+    max(bound - 14, 0) keeps every 2^(S - m) below 2^14.  Output and lse (which carries the offset)
+    against float64."""
+    case = list(random_simplicial(3, 2, 41, D, seed=D + 5, counts=[41, 30, 9], std=logit_std(D)))
+    case[0] = case[0] * qscale
+    out, lse, out32 = run_hip(tuple(case), cuda, dtype)
+    ref, ref_lse = oracle64(tuple(case), dtype)
+    assert rel_err(out32.cpu().numpy(), ref) <= 2e-2
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-2
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=2e-2, atol=5e-2)
+
+
 def test_16bit_ieee_precision_upcasts(cuda):
     case = random_simplicial(2, 2, 21, 16, seed=3, counts=[21, 8])
     out, lse, out32 = run_hip(case, cuda, torch.bfloat16, precision="ieee_fp32")
