@@ -56,10 +56,13 @@
 // and softmax is invariant to the missing offset.  Otherwise a single-block
 // unit whose bounds are at most kShiftMax first takes one shifted pass,
 // P = 2^(S - m_i) with m_i = max(U_i - kShiftTop, 0), kept when every shifted
-// query's denominator reaches kMinMass.  Failing that, the unit takes two
-// passes: the exact maximum m_i of the valid logits (GEMM1 only), then
-// P = 2^(S - m_i) with S rescaled to log2 units (the query scale is then
-// normalised on its own: sq = 1 - exponent(max|q'|)).
+// query's denominator reaches kMinMass.  Failing that, the unit takes the
+// exact offsets: two passes, the maximum m_i of the valid logits (GEMM1
+// only), then P = 2^(S - m_i) with S rescaled to log2 units (the query scale
+// is then normalised on its own: sq = 1 - exponent(max|q'|)); with the bias,
+// one pass whose offsets follow the running maxima (O and L rescaled when a
+// tile's maximum passes the offset by more than kOnlineSlack), the waves'
+// partials moved to the largest of their offsets at the end.
 #include <cmath>
 #include <type_traits>
 
@@ -90,14 +93,18 @@ constexpr float kQLimit = 8192.0f;    // fast path bound on max |Qs|
 // Shifted one-pass mode (a unit past the fast-path bound, single key block): query i takes the offset
 // m_i = max(B_i - kShiftTop, 0) from its own bound |S| <= B_i (log2 units), so every 2^(S - m_i) <= 2^14 fits
 // fp16; the pass is kept when every shifted query's denominator reaches kMinMass (then terms lost to fp16
-// underflow, at most one 2^-25 per pair, stay below 2^-10 of it), else the unit reruns the exact two-pass
-// way.  Bounds above kShiftMax (large or masking-scale terms, whose shifted pass mostly fails and costs a
-// pass) go to the two-pass way at once.
+// underflow, at most one 2^-25 per pair, stay below 2^-10 of it), else the unit reruns the exact way.
+// Bounds above kShiftMax (large or masking-scale terms, whose shifted pass mostly fails and costs a pass) go
+// to the exact way at once.  The exact way: the maximum of the valid logits, then the main pass (a max pass
+// and a pass with those offsets); the bias instantiations take one pass with running offsets (kOnline).
 constexpr float kShiftTop = 14.0f;
 constexpr float kShiftMax = 24.0f;
 constexpr float kMinMass = 0.25f;
 
-enum Mode { kFast = 0, kSlow = 1, kMax = 2 };
+// kOnline: one pass with a running offset per query (raised, with the query's O and L rescaled, when a tile's
+// maximum passes it by more than kOnlineSlack), for units that need the exact offsets
+enum Mode { kFast = 0, kSlow = 1, kMax = 2, kOnline = 3 };
+constexpr float kOnlineSlack = 8.0f;
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f2_t __attribute__((ext_vector_type(2)));
@@ -432,7 +439,7 @@ __device__ __forceinline__ uint32_t pv_mask(uint32_t bits4, int s) {
 // so the accumulator gains c_i (u_ij + w_jk + v_ik) for pair (j, k0 + p).
 template <int DP, int QT, int MODE, bool HAS_PV, bool BIAS, int MQ>
 __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, int nkk,
-                                          const uint4 (&qop)[MQ][DP / 32], const float (&negm)[MQ], float sc,
+                                          const uint4 (&qop)[MQ][DP / 32], float (&negm)[MQ], float sc,
                                           mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
                                           int g, int r16) {
   constexpr int W = Waves<BIAS>::kCount;
@@ -613,6 +620,31 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
           }
         }
       } else {
+        if constexpr (MODE == kOnline) {
+          // the running offset of each query (mloc, log2 units; negm = -mloc): the tile's maximum over the
+          // valid logits of the query's four lane groups; when it passes the offset by more than the slack
+          // the offset moves to it and the query's O and L are rescaled (2^-inf = 0 on the first move)
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            float t = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              t = fmaxf(t, ((bits_a >> r) & 1u) ? sa[qt][r] : -INFINITY);
+              t = fmaxf(t, ((bits_b >> r) & 1u) ? sb[qt][r] : -INFINITY);
+            }
+            t = __uint_as_float(swap32_op(swap16_op(__float_as_uint(t), MaxF32{}), MaxF32{})) * sc;
+            const bool up = t > mloc[qt] + kOnlineSlack;
+            if (__any(up)) {
+              const float mn = up ? t : mloc[qt];
+              const float f = up ? __builtin_amdgcn_exp2f(mloc[qt] - mn) : 1.0f;
+#pragma unroll
+              for (int dt = 0; dt < ND; ++dt) O[dt][qt] *= f;
+              L[qt] *= f;
+              mloc[qt] = mn;
+              negm[qt] = -mn;
+            }
+          }
+        }
         // Z^T operands: d = 16 dt + r16, keys 4g + r of row j0 (halves
         // 0..3) and of row j0 + 1 (halves 4..7)
         uint4 z[ND];
@@ -644,7 +676,7 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
           pop[qt] = uint4{pack_h2(ea[0], ea[1]), pack_h2(ea[2], ea[3]), pack_h2(eb[0], eb[1]), pack_h2(eb[2], eb[3])};
           // two-pass mode: padded pairs have S = 0, so 2^(0 - m) may exceed
           // the fp16 range; they and the pairs pair_valid clears get P = 0
-          if constexpr (HAS_PV || MODE == kSlow) {
+          if constexpr (HAS_PV || MODE == kSlow || MODE == kOnline) {
             pop[qt].x &= pv_mask(bits_a, 0);
             pop[qt].y &= pv_mask(bits_a, 1);
             pop[qt].z &= pv_mask(bits_b, 0);
@@ -666,7 +698,7 @@ __device__ __forceinline__ void pair_loop(const unsigned char* smem, int nkj, in
 // pair_loop for the runtime tile count nqt (1 .. MQ)
 template <int DP, int MODE, bool HAS_PV, bool BIAS, int MQ>
 __device__ __forceinline__ void pair_loop_n(int nqt, const unsigned char* smem, int nkj, int nkk,
-                                            const uint4 (&qop)[MQ][DP / 32], const float (&negm)[MQ], float sc,
+                                            const uint4 (&qop)[MQ][DP / 32], float (&negm)[MQ], float sc,
                                             mf_f32x4 (&O)[DP / 16][MQ], mf_f32x4 (&L)[MQ], float (&mloc)[MQ], int wave,
                                             int g, int r16) {
   static_assert(MQ == 2 || MQ == 3, "two or three query tiles");
@@ -1424,10 +1456,36 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
           }
         }
       }
-      if (exact) {
+      if (exact && !BIAS) {
         pair_loop_n<DP, kMax, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
         finish_max();
         pair_loop_n<DP, kSlow, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+      } else if (exact) {
+        // (the bias instantiations) one pass with running offsets (mloc = -inf, negm = +inf until a query's
+        // first valid logit), then every wave moves its partial O and L to the queries' common offset, the
+        // largest of the waves'
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          mloc[qt] = -INFINITY;
+          negm[qt] = INFINITY;
+        }
+        pair_loop_n<DP, kOnline, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
+        float* redm = colmax;  // [kWaves][kMaxQ]
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+          if (g == 0) redm[wave * kMaxQ + 16 * qt + r16] = mloc[qt];
+        __syncthreads();
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          float m = -INFINITY;
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) m = fmaxf(m, redm[w * kMaxQ + 16 * qt + r16]);
+          const float f = mloc[qt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mloc[qt] - m);
+#pragma unroll
+          for (int dt = 0; dt < ND; ++dt) O[dt][qt] *= f;
+          L[qt] *= f;
+          if (wave == 0 && g == 0) s_m[16 * qt + r16] = m == -INFINITY ? 0.0f : m;
+        }
       }
     }
   } else if (MULTI && nch > 1) {

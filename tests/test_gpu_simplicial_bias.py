@@ -178,9 +178,10 @@ def test_16bit_terms_match_fp64(cuda, shape, terms, dtype):
 
 @pytest.mark.parametrize("shape", [(3, 2, 45, 64, [45, 30, 7], [(1, 2)], 0.1), (2, 1, 130, 64, [130, 77], None, 0.0)],
                          ids=["one_block", "key_blocks"])
-def test_16bit_large_bias_takes_two_passes(cuda, shape):
-    """Bias terms of several units in log2 units (beyond the one-pass bound): the exact two-pass maxima,
-    every valid query row against float64."""
+def test_16bit_large_bias_takes_exact_offsets(cuda, shape):
+    """Bias terms of several units in log2 units (beyond the one-pass bound and the shifted pass's cap): exact
+    offsets (running maxima in one key block, two passes over key blocks), every valid query row against
+    float64."""
     B, H, N, D, counts, holes, drop = shape
     case = random_simplicial(B, H, N, D, seed=N + 11, counts=counts, holes=holes, pair_drop=drop,
                             std=logit_std(D))
@@ -197,7 +198,7 @@ def test_16bit_large_bias_takes_two_passes(cuda, shape):
 def test_16bit_masking_scale_bias(cuda):
     """A masking-style bias: u_ij = -1e4 on a random 30 % of (query, key) pairs, the rest N(0, 0.5^2), gates
     1 + N(0, 0.1^2).  c_i u_ij ~ -1.4e4 (log2 units) is staged as fp16 without saturating and drives those
-    pairs' P to 0 exactly as exp(-1e4) does in float64; the exact two-pass maxima are taken over the rest.
+    pairs' P to 0 exactly as exp(-1e4) does in float64; the exact offsets are taken over the rest.
     Bar: 2e-2 normwise and every valid row within the row bar of its norm."""
     B, H, N, D = 2, 2, 37, 64
     case = random_simplicial(B, H, N, D, seed=41, counts=[37, 23], std=logit_std(D))
@@ -260,7 +261,7 @@ def test_16bit_shifted_one_pass_matches_fp64(cuda):
 def test_16bit_shifted_pass_falls_back_when_its_denominators_underflow(cuda):
     """u = -10 on every pair, v = w = 0, gate 1: c u = -14.4 log2 units, so each query's bound (~19) is past
     the one-pass bound and below the shifted pass's cap, but the bound's offset leaves every 2^(S - m_i) near
-    2^-19: the denominators stay far below the pass's floor and the unit reruns the exact two-pass way.  The
+    2^-19: the denominators stay far below the pass's floor and the unit reruns with exact offsets.  The
     constant cancels in the softmax; output and lse against float64."""
     B, H, N, D = 2, 2, 41, 64
     case = _small_logit_case(B, H, N, D, 46, [41, 26])
