@@ -1271,7 +1271,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         __syncthreads();
       }
     } else {
-      if (tid == 0) scal[6] = 1;  // blocks stage their bias one pair at a time: two passes, exact maxima
+      if (tid == 0) scal[6] = 1;  // blocks stage their bias one pair at a time: exact offsets (online pass)
     }
   }
   float bias_mag = 0.0f;
@@ -1411,6 +1411,33 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
       if (wave == 0 && g == 0) s_m[16 * qt + r16] = m;
     }
   };
+  // after a kOnline pass: every wave moves its partial O and L to the queries' common offset, the largest of
+  // the waves' running offsets, which becomes the lse offset
+  auto combine_online = [&]() {
+    float* redm = colmax;  // [kWaves][kMaxQ]
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+      if (g == 0) redm[wave * kMaxQ + 16 * qt + r16] = mloc[qt];
+    __syncthreads();
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) m = fmaxf(m, redm[w * kMaxQ + 16 * qt + r16]);
+      const float f = mloc[qt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mloc[qt] - m);
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) O[dt][qt] *= f;
+      L[qt] *= f;
+      if (wave == 0 && g == 0) s_m[16 * qt + r16] = m == -INFINITY ? 0.0f : m;
+    }
+  };
+  auto start_online = [&]() {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      mloc[qt] = -INFINITY;
+      negm[qt] = INFINITY;
+    }
+  };
   bool slow = false;
   if (!MULTI && nch == 1) {
     if (!staged) {
@@ -1462,32 +1489,28 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         pair_loop_n<DP, kSlow, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
       } else if (exact) {
         // (the bias instantiations) one pass with running offsets (mloc = -inf, negm = +inf until a query's
-        // first valid logit), then every wave moves its partial O and L to the queries' common offset, the
-        // largest of the waves'
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          mloc[qt] = -INFINITY;
-          negm[qt] = INFINITY;
-        }
+        // first valid logit), then the waves' common offsets
+        start_online();
         pair_loop_n<DP, kOnline, HAS_PV, BIAS>(nqt, smem, nk, nk, qop, negm, sc, O, L, mloc, wave, g, r16);
-        float* redm = colmax;  // [kWaves][kMaxQ]
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-          if (g == 0) redm[wave * kMaxQ + 16 * qt + r16] = mloc[qt];
-        __syncthreads();
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          float m = -INFINITY;
-#pragma unroll
-          for (int w = 0; w < kWaves; ++w) m = fmaxf(m, redm[w * kMaxQ + 16 * qt + r16]);
-          const float f = mloc[qt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mloc[qt] - m);
-#pragma unroll
-          for (int dt = 0; dt < ND; ++dt) O[dt][qt] *= f;
-          L[qt] *= f;
-          if (wave == 0 && g == 0) s_m[16 * qt + r16] = m == -INFINITY ? 0.0f : m;
-        }
+        combine_online();
       }
     }
+  } else if (MULTI && nch > 1 && BIAS) {
+    // the bias key-block path (always exact offsets): one pass over the block pairs with running offsets
+    __syncthreads();
+    slow = true;
+    load_qop();
+    start_online();
+    for (int jc = 0; jc < nch; ++jc) {
+      for (int kc = 0; kc < nch; ++kc) {
+        store_block(jc, kc);
+        __syncthreads();
+        const int nkj = min(kCap, nk - jc * kCap), nkk = min(kCap, nk - kc * kCap);
+        pair_loop<DP, 1, kOnline, HAS_PV, BIAS>(smem, nkj, nkk, qop, negm, sc, O, L, mloc, wave, g, r16);
+        __syncthreads();
+      }
+    }
+    combine_online();
   } else if (MULTI && nch > 1) {
     __syncthreads();
     slow = scal[6] != 0;
