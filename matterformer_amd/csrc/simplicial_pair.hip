@@ -1472,7 +1472,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         }
         exact = __any(low);
         if (exact) {
-          __syncthreads();  // every wave has read the denominators before finish_max reuses the area
+          __syncthreads();  // every wave has read the denominators before the exact way reuses the area
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {
             L[qt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
