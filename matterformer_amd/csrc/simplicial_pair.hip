@@ -1098,6 +1098,10 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
   float ql1 = 0.0f;  // GUESS: the largest ||q'_i||_1 of this wave's query rows
   if constexpr (!MULTI) {
     load_block(0, 0);
+    // without the bias: the pair-valid bits of the unit's one block, while the key rows are in flight (with
+    // the bias they are staged with the block, after the bias: staged here, their waits held up the bias
+    // loads)
+    if constexpr (HAS_PV && !BIAS) stage_pv(0, 0);
     // the workgroup's share of padded query rows, stored while the loads are
     // in flight (first unit only)
     if (zero_share) zero_padded_share<T, DP, STR, Waves<BIAS>::kCount>(p, reinterpret_cast<const uint32_t*>(smem + Ly::kInfo), blockIdx.x, gridDim.x);
@@ -1116,7 +1120,6 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
           store_v(smem + Ly::kV2, rv2[i], row, 0);
         }
       }
-      if constexpr (HAS_PV) stage_pv(0, 0);
       unsigned char* Qs = smem + Ly::kQ;
 #pragma unroll
       for (int i = 0; i < MAXQC; ++i) {
@@ -1367,7 +1370,7 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
         if ((tid + kThreads * i) / CPR < rk) store_v(V2s, t[i], (tid + kThreads * i) / CPR, t2);
     }
     if constexpr (BIAS && MULTI) stage_bias(jc, kc, E);
-    if constexpr (HAS_PV) stage_pv(jc, kc);
+    if constexpr (HAS_PV && (MULTI || BIAS)) stage_pv(jc, kc);
   };
 
   // ---- phase C: pair loop -------------------------------------------------
