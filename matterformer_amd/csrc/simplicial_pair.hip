@@ -1076,14 +1076,20 @@ __device__ __forceinline__ void unit_body(const Params& p, unsigned char* smem, 
     const uint8_t* gpv = p.pv + size_t(b) * N * N;
     const int j0 = jc * kCap, k0 = kc * kCap;
     const int nkj = min(kCap, nk - j0), nkk = min(kCap, nk - k0);
+    // a word's bytes are loaded 16 at a time without branches (columns past the block read its last key,
+    // and are masked afterwards), so each 16 loads are in flight together
     for (int u = tid; u < kCap * Ly::kPVW; u += kThreads) {
       const int jl = u / Ly::kPVW, wd = u % Ly::kPVW;
       uint32_t bits = 0;
-      if (jl < nkj) {
+      if (jl < nkj && nkk > 0) {
         const uint8_t* prow = gpv + size_t(key_atom(j0 + jl)) * N;
-        for (int t = 0; t < 32; ++t) {
-          const int kl = wd * 32 + t;
-          if (kl < nkk && prow[key_atom(k0 + kl)] != 0) bits |= 1u << t;
+#pragma unroll 1
+        for (int h = 0; h < 32; h += 16) {
+          uint8_t v[16];
+#pragma unroll
+          for (int t = 0; t < 16; ++t) v[t] = prow[key_atom(k0 + min(wd * 32 + h + t, nkk - 1))];
+#pragma unroll
+          for (int t = 0; t < 16; ++t) bits |= (wd * 32 + h + t < nkk && v[t] != 0) ? 1u << (h + t) : 0u;
         }
       }
       pvb[u] = bits;
